@@ -1,0 +1,142 @@
+/*
+ * chebykan.h -- C-ABI of the MI355X (gfx950) ChebyKAN layer hot path.
+ *
+ * The reference (0xEodum/KAN) is pure Python on torch; this boundary replaces
+ * the torch op sequences its ChebyKAN layer executes.  Each entry point names
+ * the reference code it stands in for.  No torch or C++ types cross it: plain
+ * device pointers, sizes and a hipStream_t passed as void*.
+ *
+ * Conventions
+ *   - All pointers are device pointers unless stated; all launches are
+ *     stream-ordered on `stream` (a hipStream_t) and never synchronise the host.
+ *   - x, y, dy, dx and t are row-major fp32.  Coefficients C are [in, out, D]
+ *     row-major (D = degree + 1), fp32 or bf16, the layout of the reference's
+ *     `cheby_coeffs` parameter (kan/layers/chebykan.py:48-51).
+ *   - Every call returns a ckan_status; on failure ckan_last_error() returns a
+ *     thread-local message.  Argument checks happen on the host before any
+ *     launch, so an invalid call launches nothing.
+ *   - Workspaces are caller-allocated.  A forward workspace must be zero-filled
+ *     once before its first use (ckan_workspace_init); every call leaves its
+ *     split-K counters back at zero.  Calls that share one workspace must not
+ *     overlap in time.
+ */
+#ifndef CHEBYKAN_H
+#define CHEBYKAN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum ckan_status {
+  CKAN_OK = 0,
+  CKAN_ERR_INVALID_ARG = 1,   /* bad shape, null pointer, size mismatch  */
+  CKAN_ERR_UNSUPPORTED = 2,   /* valid request this build does not serve */
+  CKAN_ERR_WORKSPACE = 3,     /* workspace smaller than required          */
+  CKAN_ERR_HIP = 4            /* a HIP runtime call or launch failed      */
+} ckan_status;
+
+typedef enum ckan_compute {
+  CKAN_COMPUTE_FP32 = 0,      /* fp32 MFMA (v_mfma_f32_32x32x2_f32)                 */
+  CKAN_COMPUTE_BF16 = 1       /* bf16 MFMA, fp32 accumulate (v_mfma_f32_32x32x16_bf16) */
+} ckan_compute;
+
+typedef enum ckan_dtype {
+  CKAN_DTYPE_F32 = 0,
+  CKAN_DTYPE_BF16 = 1
+} ckan_dtype;
+
+/* Problem descriptor: one ChebyKANLayer(in_dim, out_dim, degree) applied to a
+ * batch of `batch` rows (kan/layers/chebykan.py:21-22,64). */
+typedef struct ckan_desc {
+  int64_t batch;        /* B: rows of x after x.view(-1, in_dim)          */
+  int32_t in_dim;       /* I                                               */
+  int32_t out_dim;      /* O                                               */
+  int32_t degree;       /* deg; D = deg + 1 coefficients per (i, o)        */
+  int32_t compute;      /* ckan_compute                                    */
+  int32_t coeff_dtype;  /* ckan_dtype of C passed to ckan_pack_coeffs      */
+  int32_t reserved;     /* must be 0                                       */
+} ckan_desc;
+
+/* ---- sizes (host only, no device work) ---------------------------------- */
+
+/* Bytes of the packed-coefficient buffer written by ckan_pack_coeffs. */
+size_t ckan_packed_bytes(const ckan_desc* desc);
+/* Elements (fp32) of the tanh cache written by ckan_forward and read by
+ * ckan_backward: tanh(x) as [B, in_pad] with zero padding columns. */
+size_t ckan_tcache_elems(const ckan_desc* desc);
+/* Bytes of forward / backward workspace. */
+size_t ckan_fwd_workspace_bytes(const ckan_desc* desc);
+size_t ckan_bwd_workspace_bytes(const ckan_desc* desc, int need_dx, int need_dcoeffs);
+
+/* Zero-fill a workspace on `stream` with a fill kernel (no hipMemset). */
+int ckan_workspace_init(void* ws, size_t ws_bytes, void* stream);
+
+/* ---- layer operators ---------------------------------------------------- */
+
+/* Re-lays C [in, out, D] out into the MFMA operand layouts used by the
+ * forward and input-gradient contractions, in the compute precision, and the
+ * per-output bias sum_i C[i, o, 0] (the T_0 = 1 term).
+ * Replaces: the coefficient permute/reshape/clone inside
+ * torch.einsum('bid,iod->bo') (kan/basis/chebyshev.py:101). */
+int ckan_pack_coeffs(const ckan_desc* desc, const void* coeffs, void* packed, void* stream);
+
+/* y[b, o] = sum_{i, d} T_d(tanh x[b, i]) C[i, o, d]; also writes t = tanh(x)
+ * into t_cache (ckan_tcache_elems floats) for the backward.
+ * Replaces: ChebyshevBasis.forward (kan/basis/chebyshev.py:80-101): tanh
+ * (:78), closed-form basis (:130-145) and the einsum (:101). */
+int ckan_forward(const ckan_desc* desc, const float* x, const void* packed, float* y,
+                 float* t_cache, void* ws, size_t ws_bytes, void* stream);
+
+/* Gradients of the forward for upstream gradient dy [B, out]:
+ *   dx[b, i]    = (1 - t^2) sum_{o, d} dy[b, o] C[i, o, d] d U_{d-1}(t)   (dx may be NULL)
+ *   dC[i, o, d] = sum_b T_d(t[b, i]) dy[b, o]                            (dcoeffs may be NULL)
+ * With accumulate != 0, dC is added to the existing contents of dcoeffs
+ * (torch AccumulateGrad semantics); otherwise it is overwritten.
+ * Replaces: torch autograd through kan/basis/chebyshev.py:78,101,136-145
+ * (BmmBackward0 x2, CosBackward0, MulBackward0, AcosBackward0, TanhBackward0).
+ * Divergence: for |x| >= 9.0108, where fp32 tanh(x) == +-1, the reference
+ * yields NaN in dx (acos'(+-1) = -inf); this returns the finite analytic value. */
+int ckan_backward(const ckan_desc* desc, const float* t_cache, const void* packed,
+                  const float* dy, float* dx, float* dcoeffs, int accumulate,
+                  void* ws, size_t ws_bytes, void* stream);
+
+/* out[n, d] = T_d(t[n]) for d = 0..degree (fp32).  Replaces
+ * ChebyshevBasis.basis_functions (kan/basis/chebyshev.py:103-172). */
+int ckan_basis(const float* t, int64_t n, int32_t degree, float* out, void* stream);
+/* d_t[n] = sum_d g[n, d] d U_{d-1}(t[n]): backward of ckan_basis. */
+int ckan_basis_backward(const float* t, const float* g, int64_t n, int32_t degree,
+                        float* dt, void* stream);
+
+/* ---- optimizers (in place, fp32) ---------------------------------------- */
+
+/* p -= lr * (g + weight_decay * p).  Replaces torch.optim.SGD.step without
+ * momentum (torch/optim/sgd.py, used by configs 2 and 4). */
+int ckan_sgd_step(float* p, const float* g, int64_t n, float lr, float weight_decay,
+                  void* stream);
+
+/* Adam in torch's single-tensor order (torch/optim/adam.py; README.md:59,66):
+ *   g' = g + wd p;  m = lerp(m, g', 1 - b1);  v = b2 v + (1 - b2) g'^2;
+ *   p -= (lr / (1 - b1^step)) * m / (sqrt(v) / sqrt(1 - b2^step) + eps).
+ * `step` is the step count after increment (1 on the first call). */
+int ckan_adam_step(float* p, const float* g, float* m, float* v, int64_t n, int64_t step,
+                   double lr, double beta1, double beta2, double eps, double weight_decay,
+                   void* stream);
+
+/* ---- diagnostics --------------------------------------------------------- */
+
+const char* ckan_last_error(void);
+const char* ckan_version(void);
+/* Per-kernel HIP-event timing on the launch stream (off by default). */
+int ckan_profile_enable(int on);
+/* Writes "name count total_ms\n" lines (synchronises on the recorded events)
+ * and clears the records.  Returns the number of bytes needed. */
+size_t ckan_profile_report(char* buf, size_t len);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CHEBYKAN_H */

@@ -1,0 +1,138 @@
+"""ctypes binding of the C-ABI in include/chebykan.h.
+
+The library is the in-tree ``kan_amd/libckan_gfx950.so`` built by
+``kan_amd.build``.  torch is imported first so that the HIP runtime the
+library resolves (soname libamdhip64.so.7) is the one torch already loaded;
+streams and device pointers handed over from torch are then valid in it.
+There is no fallback: if the library is missing or cannot be loaded, every
+entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch  # noqa: F401  (must be loaded before the HIP library)
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libckan_gfx950.so")
+
+CKAN_OK = 0
+CKAN_ERR_INVALID_ARG = 1
+CKAN_ERR_UNSUPPORTED = 2
+CKAN_ERR_WORKSPACE = 3
+CKAN_ERR_HIP = 4
+
+CKAN_COMPUTE_FP32 = 0
+CKAN_COMPUTE_BF16 = 1
+CKAN_DTYPE_F32 = 0
+CKAN_DTYPE_BF16 = 1
+
+
+class CkanDesc(ctypes.Structure):
+    _fields_ = [
+        ("batch", ctypes.c_int64),
+        ("in_dim", ctypes.c_int32),
+        ("out_dim", ctypes.c_int32),
+        ("degree", ctypes.c_int32),
+        ("compute", ctypes.c_int32),
+        ("coeff_dtype", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+    ]
+
+
+class CkanError(RuntimeError):
+    """Raised when a C-ABI call returns a non-zero ckan_status."""
+
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"[ckan status {code}] {msg}")
+        self.code = code
+
+
+_vp = ctypes.c_void_p
+_sz = ctypes.c_size_t
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int32
+_f32 = ctypes.c_float
+_f64 = ctypes.c_double
+_pdesc = ctypes.POINTER(CkanDesc)
+
+# name -> (restype, argtypes); every function declared in include/chebykan.h
+SIGNATURES = {
+    "ckan_packed_bytes": (_sz, [_pdesc]),
+    "ckan_tcache_elems": (_sz, [_pdesc]),
+    "ckan_fwd_workspace_bytes": (_sz, [_pdesc]),
+    "ckan_bwd_workspace_bytes": (_sz, [_pdesc, ctypes.c_int, ctypes.c_int]),
+    "ckan_workspace_init": (ctypes.c_int, [_vp, _sz, _vp]),
+    "ckan_pack_coeffs": (ctypes.c_int, [_pdesc, _vp, _vp, _vp]),
+    "ckan_forward": (ctypes.c_int, [_pdesc, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "ckan_backward": (ctypes.c_int, [_pdesc, _vp, _vp, _vp, _vp, _vp, ctypes.c_int, _vp, _sz, _vp]),
+    "ckan_basis": (ctypes.c_int, [_vp, _i64, _i32, _vp, _vp]),
+    "ckan_basis_backward": (ctypes.c_int, [_vp, _vp, _i64, _i32, _vp, _vp]),
+    "ckan_sgd_step": (ctypes.c_int, [_vp, _vp, _i64, _f32, _f32, _vp]),
+    "ckan_adam_step": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _f64, _f64, _f64, _f64, _f64, _vp]),
+    "ckan_last_error": (ctypes.c_char_p, []),
+    "ckan_version": (ctypes.c_char_p, []),
+    "ckan_profile_enable": (ctypes.c_int, [ctypes.c_int]),
+    "ckan_profile_report": (_sz, [ctypes.c_char_p, _sz]),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+def load():
+    """Load (once) and return the C-ABI library; raises if it is absent."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"kan_amd: HIP library {LIB_PATH} is not built; run `python -m kan_amd.build`")
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+def check(rc: int) -> None:
+    if rc != CKAN_OK:
+        msg = load().ckan_last_error().decode(errors="replace")
+        raise CkanError(rc, msg)
+
+
+def make_desc(batch: int, in_dim: int, out_dim: int, degree: int, compute: int,
+              coeff_dtype: int) -> CkanDesc:
+    return CkanDesc(int(batch), int(in_dim), int(out_dim), int(degree), int(compute),
+                    int(coeff_dtype), 0)
+
+
+def stream_ptr(device: torch.device) -> int:
+    """hipStream_t of torch's current stream on `device`."""
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def ptr(t) -> int:
+    return 0 if t is None else t.data_ptr()
+
+
+def profile_enable(on: bool) -> None:
+    check(load().ckan_profile_enable(1 if on else 0))
+
+
+def profile_report() -> dict:
+    """{kernel name: (launch count, total ms)} of the launches since the last report."""
+    lib = load()
+    buf = ctypes.create_string_buffer(1 << 16)  # the report clears the records: call once
+    lib.ckan_profile_report(buf, len(buf))
+    out = {}
+    for line in buf.value.decode().splitlines():
+        name, cnt, ms = line.split()
+        out[name] = (int(cnt), float(ms))
+    return out

@@ -1,0 +1,334 @@
+// C-ABI entry points (include/chebykan.h): argument checks on the host,
+// workspace carving, kernel sequencing on the caller's stream, and optional
+// per-kernel HIP-event timing.
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/chebykan.h"
+#include "ckan_kernels.hpp"
+
+using namespace ckan;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(CKAN_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+  return CKAN_OK;
+}
+
+// ---- per-kernel event timing ------------------------------------------------
+struct ProfRec {
+  const char* name;
+  hipEvent_t a, b;
+};
+std::mutex g_prof_mu;
+bool g_prof_on = false;
+std::vector<ProfRec> g_prof;
+
+struct ProfScope {
+  ProfRec rec{};
+  bool on;
+  hipStream_t s;
+  ProfScope(const char* name, hipStream_t st) : s(st) {
+    {
+      std::lock_guard<std::mutex> lk(g_prof_mu);
+      on = g_prof_on;
+    }
+    if (!on) return;
+    rec.name = name;
+    if (hipEventCreate(&rec.a) != hipSuccess || hipEventCreate(&rec.b) != hipSuccess) {
+      on = false;
+      return;
+    }
+    hipEventRecord(rec.a, s);
+  }
+  ~ProfScope() {
+    if (!on) return;
+    hipEventRecord(rec.b, s);
+    std::lock_guard<std::mutex> lk(g_prof_mu);
+    g_prof.push_back(rec);
+  }
+};
+
+int validate_desc(const ckan_desc* d) {
+  if (!d) return fail(CKAN_ERR_INVALID_ARG, "desc is NULL");
+  if (d->batch < 0) return fail(CKAN_ERR_INVALID_ARG, "batch must be >= 0 (got %lld)", (long long)d->batch);
+  if (d->in_dim < 1) return fail(CKAN_ERR_INVALID_ARG, "in_dim must be >= 1 (got %d)", d->in_dim);
+  if (d->out_dim < 1) return fail(CKAN_ERR_INVALID_ARG, "out_dim must be >= 1 (got %d)", d->out_dim);
+  if (d->degree < 0) return fail(CKAN_ERR_INVALID_ARG, "degree must be >= 0 (got %d)", d->degree);
+  if (d->degree > 16)
+    return fail(CKAN_ERR_UNSUPPORTED, "degree %d > 16 is not supported by this build", d->degree);
+  if (d->compute != CKAN_COMPUTE_FP32 && d->compute != CKAN_COMPUTE_BF16)
+    return fail(CKAN_ERR_INVALID_ARG, "unknown compute mode %d", d->compute);
+  if (d->coeff_dtype != CKAN_DTYPE_F32 && d->coeff_dtype != CKAN_DTYPE_BF16)
+    return fail(CKAN_ERR_INVALID_ARG, "unknown coefficient dtype %d", d->coeff_dtype);
+  if (d->reserved != 0) return fail(CKAN_ERR_INVALID_ARG, "reserved field must be 0");
+  // Index arithmetic inside the kernels uses 64-bit offsets; bound the
+  // 32-bit grid dimensions.
+  if (d->in_dim > (1 << 20) || d->out_dim > (1 << 20))
+    return fail(CKAN_ERR_UNSUPPORTED, "in_dim/out_dim above 2^20 are not supported");
+  if (d->batch > ((int64_t)1 << 34))
+    return fail(CKAN_ERR_UNSUPPORTED, "batch above 2^34 rows is not supported");
+  return CKAN_OK;
+}
+
+Plan plan_of(const ckan_desc* d) {
+  return make_plan(d->batch, d->in_dim, d->out_dim, d->degree, d->compute == CKAN_COMPUTE_BF16);
+}
+
+inline bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
+
+}  // namespace
+
+extern "C" {
+
+const char* ckan_last_error(void) { return g_err.c_str(); }
+
+const char* ckan_version(void) { return "kan_amd-chebykan 0.1.0 (gfx950)"; }
+
+size_t ckan_packed_bytes(const ckan_desc* desc) {
+  if (validate_desc(desc) != CKAN_OK) return 0;
+  return packed_bytes(plan_of(desc));
+}
+
+size_t ckan_tcache_elems(const ckan_desc* desc) {
+  if (validate_desc(desc) != CKAN_OK) return 0;
+  const Plan p = plan_of(desc);
+  return (size_t)p.B * p.I_sg;
+}
+
+size_t ckan_fwd_workspace_bytes(const ckan_desc* desc) {
+  if (validate_desc(desc) != CKAN_OK) return 0;
+  const Plan p = plan_of(desc);
+  if (p.B == 0) return 0;
+  return fwd_ws_bytes(p, choose_fwd(p));
+}
+
+size_t ckan_bwd_workspace_bytes(const ckan_desc* desc, int need_dx, int need_dcoeffs) {
+  if (validate_desc(desc) != CKAN_OK) return 0;
+  const Plan p = plan_of(desc);
+  return bwd_layout(p, need_dx != 0, need_dcoeffs != 0).total;
+}
+
+int ckan_workspace_init(void* ws, size_t ws_bytes, void* stream) {
+  if (ws_bytes == 0) return CKAN_OK;
+  if (!ws) return fail(CKAN_ERR_INVALID_ARG, "workspace is NULL");
+  if (!aligned16(ws) || (ws_bytes & 15))
+    return fail(CKAN_ERR_INVALID_ARG, "workspace must be 16-byte aligned and sized");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  ProfScope ps("zero", s);
+  launch_zero(ws, ws_bytes, s);
+  return check_launch("workspace_init");
+}
+
+int ckan_pack_coeffs(const ckan_desc* desc, const void* coeffs, void* packed, void* stream) {
+  int rc = validate_desc(desc);
+  if (rc) return rc;
+  if (!coeffs || !packed) return fail(CKAN_ERR_INVALID_ARG, "coeffs/packed is NULL");
+  if (!aligned16(packed)) return fail(CKAN_ERR_INVALID_ARG, "packed buffer must be 16-byte aligned");
+  const Plan p = plan_of(desc);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  ProfScope ps("pack", s);
+  launch_pack(coeffs, desc->coeff_dtype == CKAN_DTYPE_BF16, packed, p, s);
+  return check_launch("pack_coeffs");
+}
+
+int ckan_forward(const ckan_desc* desc, const float* x, const void* packed, float* y,
+                 float* t_cache, void* ws, size_t ws_bytes, void* stream) {
+  int rc = validate_desc(desc);
+  if (rc) return rc;
+  const Plan p = plan_of(desc);
+  if (p.B == 0) return CKAN_OK;
+  if (!x || !packed || !y || !t_cache)
+    return fail(CKAN_ERR_INVALID_ARG, "x/packed/y/t_cache is NULL");
+  if (!aligned16(packed) || !aligned16(t_cache))
+    return fail(CKAN_ERR_INVALID_ARG, "packed and t_cache must be 16-byte aligned");
+  const FwdChoice c = choose_fwd(p);
+  const size_t need = fwd_ws_bytes(p, c);
+  if (ws_bytes < need)
+    return fail(CKAN_ERR_WORKSPACE, "forward workspace too small: %zu < %zu bytes", ws_bytes, need);
+  if (need && !ws) return fail(CKAN_ERR_INVALID_ARG, "workspace is NULL");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  {
+    ProfScope ps("tanh", s);
+    launch_tanh(x, t_cache, p, s);
+  }
+  if ((rc = check_launch("tanh"))) return rc;
+  {
+    ProfScope ps("fwd_gemm", s);
+    launch_fwd_gemm(t_cache, packed, y, ws, p, c, s);
+  }
+  return check_launch("fwd_gemm");
+}
+
+int ckan_backward(const ckan_desc* desc, const float* t_cache, const void* packed,
+                  const float* dy, float* dx, float* dcoeffs, int accumulate, void* ws,
+                  size_t ws_bytes, void* stream) {
+  int rc = validate_desc(desc);
+  if (rc) return rc;
+  const Plan p = plan_of(desc);
+  const bool need_dx = dx != nullptr, need_dc = dcoeffs != nullptr;
+  if (!need_dx && !need_dc) return CKAN_OK;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (p.B == 0) {
+    // empty batch: dC = 0 (or unchanged when accumulating), dx is empty
+    if (need_dc && !accumulate) {
+      launch_zero_f32(dcoeffs, (int64_t)p.I * p.O * p.D, s);
+      return check_launch("zero dcoeffs");
+    }
+    return CKAN_OK;
+  }
+  if (!t_cache || !dy || (need_dx && !packed))
+    return fail(CKAN_ERR_INVALID_ARG, "t_cache/dy/packed is NULL");
+  if (need_dx && !aligned16(packed)) return fail(CKAN_ERR_INVALID_ARG, "packed must be 16-byte aligned");
+  const BwdLayout L = bwd_layout(p, need_dx, need_dc);
+  if (ws_bytes < L.total)
+    return fail(CKAN_ERR_WORKSPACE, "backward workspace too small: %zu < %zu bytes", ws_bytes, L.total);
+  if (!ws || !aligned16(ws)) return fail(CKAN_ERR_INVALID_ARG, "workspace is NULL or misaligned");
+  char* w = reinterpret_cast<char*>(ws);
+  void* dYx = w + L.dyx_off;
+  void* dYc = w + L.dyc_off;
+  float* colsum = reinterpret_cast<float*>(w + L.colsum_off);
+  float* part = reinterpret_cast<float*>(w + L.part_off);
+  {
+    ProfScope ps("prep_dy", s);
+    launch_prep_dy(dy, dYx, dYc, colsum, p, need_dx, need_dc, s);
+  }
+  if ((rc = check_launch("prep_dy"))) return rc;
+  if (need_dx) {
+    ProfScope ps("dx_gemm", s);
+    launch_dx_gemm(dYx, packed, t_cache, dx, p, s);
+  }
+  if ((rc = check_launch("dx_gemm"))) return rc;
+  if (need_dc) {
+    {
+      ProfScope ps("dc_gemm", s);
+      launch_dc_gemm(dYc, t_cache, part, p, L, s);
+    }
+    if ((rc = check_launch("dc_gemm"))) return rc;
+    {
+      ProfScope ps("dc_finalize", s);
+      launch_dc_finalize(part, L.dc_splits, colsum, dcoeffs, accumulate != 0, p, s);
+    }
+    if ((rc = check_launch("dc_finalize"))) return rc;
+  }
+  return CKAN_OK;
+}
+
+int ckan_basis(const float* t, int64_t n, int32_t degree, float* out, void* stream) {
+  if (n < 0 || degree < 0) return fail(CKAN_ERR_INVALID_ARG, "n and degree must be >= 0");
+  if (n == 0) return CKAN_OK;
+  if (!t || !out) return fail(CKAN_ERR_INVALID_ARG, "t/out is NULL");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  ProfScope ps("basis", s);
+  launch_basis(t, n, degree, out, s);
+  return check_launch("basis");
+}
+
+int ckan_basis_backward(const float* t, const float* g, int64_t n, int32_t degree, float* dt,
+                        void* stream) {
+  if (n < 0 || degree < 0) return fail(CKAN_ERR_INVALID_ARG, "n and degree must be >= 0");
+  if (n == 0) return CKAN_OK;
+  if (!t || !g || !dt) return fail(CKAN_ERR_INVALID_ARG, "t/g/dt is NULL");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  ProfScope ps("basis_bwd", s);
+  launch_basis_bwd(t, g, n, degree, dt, s);
+  return check_launch("basis_backward");
+}
+
+int ckan_sgd_step(float* p, const float* g, int64_t n, float lr, float weight_decay,
+                  void* stream) {
+  if (n < 0) return fail(CKAN_ERR_INVALID_ARG, "n must be >= 0");
+  if (n == 0) return CKAN_OK;
+  if (!p || !g) return fail(CKAN_ERR_INVALID_ARG, "p/g is NULL");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  ProfScope ps("sgd", s);
+  launch_sgd(p, g, n, lr, weight_decay, s);
+  return check_launch("sgd_step");
+}
+
+int ckan_adam_step(float* p, const float* g, float* m, float* v, int64_t n, int64_t step,
+                   double lr, double beta1, double beta2, double eps, double weight_decay,
+                   void* stream) {
+  if (n < 0) return fail(CKAN_ERR_INVALID_ARG, "n must be >= 0");
+  if (step < 1) return fail(CKAN_ERR_INVALID_ARG, "step must be >= 1 (got %lld)", (long long)step);
+  if (!(beta1 >= 0.0 && beta1 < 1.0) || !(beta2 >= 0.0 && beta2 < 1.0))
+    return fail(CKAN_ERR_INVALID_ARG, "betas must lie in [0, 1)");
+  if (n == 0) return CKAN_OK;
+  if (!p || !g || !m || !v) return fail(CKAN_ERR_INVALID_ARG, "p/g/m/v is NULL");
+  const double bc1 = 1.0 - pow(beta1, (double)step);
+  const double bc2 = 1.0 - pow(beta2, (double)step);
+  const double step_size = lr / bc1;
+  const double bc2_sqrt = sqrt(bc2);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  ProfScope ps("adam", s);
+  launch_adam(p, g, m, v, n, (float)(1.0 - beta1), (float)beta2, (float)(1.0 - beta2),
+              (float)bc2_sqrt, (float)eps, (float)(-step_size), (float)weight_decay, s);
+  return check_launch("adam_step");
+}
+
+int ckan_profile_enable(int on) {
+  std::lock_guard<std::mutex> lk(g_prof_mu);
+  g_prof_on = on != 0;
+  return CKAN_OK;
+}
+
+size_t ckan_profile_report(char* buf, size_t len) {
+  std::vector<ProfRec> recs;
+  {
+    std::lock_guard<std::mutex> lk(g_prof_mu);
+    recs.swap(g_prof);
+  }
+  std::vector<std::string> names;
+  std::vector<double> tot;
+  std::vector<long> cnt;
+  for (auto& r : recs) {
+    float ms = 0.0f;
+    if (hipEventSynchronize(r.b) == hipSuccess) hipEventElapsedTime(&ms, r.a, r.b);
+    hipEventDestroy(r.a);
+    hipEventDestroy(r.b);
+    size_t k = 0;
+    for (; k < names.size(); ++k)
+      if (names[k] == r.name) break;
+    if (k == names.size()) {
+      names.push_back(r.name);
+      tot.push_back(0.0);
+      cnt.push_back(0);
+    }
+    tot[k] += ms;
+    cnt[k] += 1;
+  }
+  std::string out;
+  char line[160];
+  for (size_t k = 0; k < names.size(); ++k) {
+    snprintf(line, sizeof(line), "%s %ld %.6f\n", names[k].c_str(), cnt[k], tot[k]);
+    out += line;
+  }
+  if (buf && len) {
+    const size_t n = out.size() < len - 1 ? out.size() : len - 1;
+    memcpy(buf, out.data(), n);
+    buf[n] = 0;
+  }
+  return out.size() + 1;
+}
+
+}  // extern "C"

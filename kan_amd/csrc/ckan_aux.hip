@@ -1,0 +1,391 @@
+// Bandwidth-bound kernels around the three MFMA contractions: the tanh cache,
+// coefficient packing, the dy re-layout, the dC finalisation, the optimizers
+// and the materialised basis.  All are HBM-bound elementwise or re-layout
+// passes; each moves its bytes once with coalesced accesses.
+#include "ckan_kernels.hpp"
+
+namespace ckan {
+
+// t[b, i] = tanh(x[b, i]) for i < I, 0 for I <= i < I_sg.  Row pitch I_sg.
+// Replaces torch.tanh (kan/basis/chebyshev.py:78).
+__global__ void __launch_bounds__(256)
+k_tanh(const float* __restrict__ x, float* __restrict__ t, int64_t B, int I, int I_sg) {
+  const int64_t n4 = B * (int64_t)(I_sg / 4);
+  const bool vec = (I % 4) == 0;
+  for (int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; q < n4;
+       q += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t b = q / (I_sg / 4);
+    const int i = (int)(q - b * (I_sg / 4)) * 4;
+    f32x4_t v;
+    if (vec && i < I) {
+      v = *reinterpret_cast<const f32x4_t*>(x + b * I + i);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] = (i + j < I) ? x[b * I + i + j] : 0.0f;
+    }
+    f32x4_t r;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) r[j] = (i + j < I) ? tanhf(v[j]) : 0.0f;
+    *reinterpret_cast<f32x4_t*>(t + b * I_sg + i) = r;
+  }
+}
+
+template <typename CT> __device__ __forceinline__ float to_f32(CT v);
+template <> __device__ __forceinline__ float to_f32<float>(float v) { return v; }
+template <> __device__ __forceinline__ float to_f32<uint16_t>(uint16_t v) {
+  return __uint_as_float(((unsigned)v) << 16);
+}
+
+// Packs C [I, O, D] into
+//   Cf: forward B operand, [NBf][KB][64][8]   (columns o, reduction (i, d>=1))
+//   Cb: dX B operand,      [NIB*P][KBx][64][8] (columns (input block, d), reduction o)
+//   bias_part[ib][o] = sum_{i in block ib} C[i, o, 0]
+// One block per (32 inputs, 32 outputs) tile, staged through LDS so the
+// global read of C is one contiguous run of 32*D values per input.
+template <int P, bool BF, typename CT>
+__global__ void __launch_bounds__(256)
+k_pack(const CT* __restrict__ C, typename Elem<BF>::type* __restrict__ Cf,
+       typename Elem<BF>::type* __restrict__ Cb, float* __restrict__ bias_part, Plan p) {
+  using G = FwdGroup<P>;
+  __shared__ float tile[32 * 32 * 17];
+  const int tid = threadIdx.x;
+  const int ib = blockIdx.x, ob = blockIdx.y;
+  const int i0 = ib * 32, o0 = ob * 32;
+  const int D = p.D;
+  const int n = 32 * 32 * D;
+  for (int idx = tid; idx < n; idx += 256) {
+    const int il = idx / (32 * D);
+    const int rem = idx - il * 32 * D;
+    const int ol = rem / D;
+    const int i = i0 + il, o = o0 + ol;
+    float v = 0.0f;
+    if (i < p.I && o < p.O) v = to_f32<CT>(C[((size_t)i * p.O + o0) * D + rem]);
+    tile[idx] = v;
+  }
+  __syncthreads();
+
+  if (tid < 32 && o0 + tid < p.O32) {
+    float s = 0.0f;
+    for (int il = 0; il < 32; ++il) s += tile[(il * 32 + tid) * D];
+    bias_part[(size_t)ib * p.O32 + o0 + tid] = s;
+  }
+
+  if (ob < p.NBf) {
+    const int kb_base = ib * 2 * P;  // 32 inputs * P values / 16 per k-block
+    for (int item = tid; item < 2 * P * 64; item += 256) {
+      const int kbl = item >> 6, lane = item & 63;
+      const int kb = kb_base + kbl;
+      if (kb >= p.KB) continue;
+      const int ol = lane & 31, g = lane >> 5;
+      const int r = kb / G::SGK, q = kb - r * G::SGK;
+      const int s = q / G::KBG, h = q - s * G::KBG;
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int vv = 8 * h + j;
+        const int u = vv / P, d = vv % P + 1;
+        const int i = r * G::SGI + g * 2 * G::IPG + s * (G::IPG / 2) + u;
+        v[j] = (d <= p.deg) ? tile[((i - i0) * 32 + ol) * D + d] : 0.0f;
+      }
+      store_frag<BF>(Cf + ((size_t)ob * p.KB + kb) * kFragElems, lane, v);
+    }
+  }
+
+  for (int item = tid; item < P * 2 * 64; item += 256) {
+    const int e = item >> 7, rem = item & 127;
+    const int kbl = rem >> 6, lane = rem & 63;
+    const int il = lane & 31, g = lane >> 5;
+    const int kbx = ob * 2 + kbl;
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int ol = 16 * kbl + 8 * g + j;
+      v[j] = (e + 1 <= p.deg) ? tile[(il * 32 + ol) * D + e + 1] : 0.0f;
+    }
+    store_frag<BF>(Cb + ((size_t)(ib * P + e) * p.KBx + kbx) * kFragElems, lane, v);
+  }
+}
+
+// Re-lays dy [B, O] (fp32) into
+//   dYx: dX A operand  [B32/32][KBx][64][8]  (rows b, reduction o)
+//   dYc: dC B operand  [NBf][KBc][64][8]     (columns o, reduction b)
+// and writes colsum_part[bb][o] = sum of dy over rows [256 bb, 256 bb + 256).
+// One block per (256 rows, 32 columns); 32x32 sub-tiles pass through LDS.
+template <bool BF>
+__global__ void __launch_bounds__(256)
+k_prep_dy(const float* __restrict__ dy, typename Elem<BF>::type* __restrict__ dYx,
+          typename Elem<BF>::type* __restrict__ dYc, float* __restrict__ colsum_part,
+          Plan p, int need_dx, int need_dc) {
+  __shared__ float tile[32][33];
+  const int tid = threadIdx.x;
+  const int bb = blockIdx.x, ob = blockIdx.y;
+  const int o0 = ob * 32;
+  const int64_t row_end = p.B32 > p.Bc ? p.B32 : p.Bc;
+  float cs = 0.0f;
+  for (int sub = 0; sub < kPrepRows / 32; ++sub) {
+    const int64_t b0 = (int64_t)bb * kPrepRows + sub * 32;
+    if (b0 >= row_end) break;
+    for (int idx = tid; idx < 1024; idx += 256) {
+      const int r = idx >> 5, c = idx & 31;
+      const int64_t b = b0 + r;
+      const int o = o0 + c;
+      tile[r][c] = (b < p.B && o < p.O) ? dy[b * p.O + o] : 0.0f;
+    }
+    __syncthreads();
+    if (tid < 32) {
+      for (int r = 0; r < 32; ++r) cs += tile[r][tid];
+    }
+    if (tid < 128) {
+      if (need_dx && b0 < p.B32) {
+        const int kbl = tid >> 6, lane = tid & 63;
+        const int r = lane & 31, g = lane >> 5;
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = tile[r][16 * kbl + 8 * g + j];
+        store_frag<BF>(dYx + ((size_t)(b0 / 32) * p.KBx + ob * 2 + kbl) * kFragElems, lane, v);
+      }
+    } else {
+      if (need_dc && ob < p.NBf && b0 < p.Bc) {
+        const int t2 = tid - 128;
+        const int kbl = t2 >> 6, lane = t2 & 63;
+        const int c = lane & 31, g = lane >> 5;
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = tile[16 * kbl + 8 * g + j][c];
+        store_frag<BF>(dYc + ((size_t)ob * p.KBc + b0 / 16 + kbl) * kFragElems, lane, v);
+      }
+    }
+    __syncthreads();
+  }
+  if (need_dc && tid < 32 && o0 + tid < p.O32 && bb < p.NBB)
+    colsum_part[(size_t)bb * p.O32 + o0 + tid] = cs;
+}
+
+// dC[i, o, d] (=|+=) for d = 0: sum_b dy[b, o] (from the colsum partials);
+// for d >= 1: sum over the S split partials part[s][d-1][i][o].
+// One block per (16 inputs, 64 outputs); the tile is transposed through LDS
+// so the write of dC is one contiguous run of 64*D values per input.
+__global__ void __launch_bounds__(256)
+k_dc_finalize(const float* __restrict__ part, int S, const float* __restrict__ colsum_part,
+              float* __restrict__ dC, int accumulate, Plan p) {
+  __shared__ float tile[16 * 64 * 17];
+  __shared__ float cs[64];
+  const int tid = threadIdx.x;
+  const int i0 = blockIdx.x * 16, o0 = blockIdx.y * 64;
+  const int D = p.D;
+  if (tid < 64) {
+    const int o = o0 + tid;
+    float s = 0.0f;
+    if (o < p.O)
+      for (int bb = 0; bb < p.NBB; ++bb) s += colsum_part[(size_t)bb * p.O32 + o];
+    cs[tid] = s;
+  }
+  const int nval = 16 * p.deg * 64;
+  for (int idx = tid; idx < nval; idx += 256) {
+    const int il = idx / (p.deg * 64);
+    const int rem = idx - il * p.deg * 64;
+    const int e = rem >> 6, ol = rem & 63;
+    const int i = i0 + il, o = o0 + ol;
+    float v = 0.0f;
+    if (i < p.I && o < p.O) {
+      for (int s = 0; s < S; ++s)
+        v += part[(((size_t)s * p.P + e) * p.I32 + i) * p.O32 + o];
+    }
+    tile[(il * 64 + ol) * D + e + 1] = v;
+  }
+  __syncthreads();
+  for (int idx = tid; idx < 16 * 64; idx += 256) tile[idx * D] = cs[idx & 63];
+  __syncthreads();
+  const int ocount = (p.O - o0) < 64 ? (p.O - o0) : 64;
+  const int nrow = ocount * D;
+  for (int il = 0; il < 16; ++il) {
+    const int i = i0 + il;
+    if (i >= p.I) break;
+    float* dst = dC + ((size_t)i * p.O + o0) * D;
+    const float* src = tile + il * 64 * D;
+    for (int idx = tid; idx < nrow; idx += 256) {
+      const float v = src[idx];
+      dst[idx] = accumulate ? dst[idx] + v : v;
+    }
+  }
+}
+
+__global__ void __launch_bounds__(256)
+k_sgd(float* __restrict__ p, const float* __restrict__ g, int64_t n, float lr, float wd) {
+  for (int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; q < n;
+       q += (int64_t)gridDim.x * blockDim.x) {
+    float gv = g[q];
+    if (wd != 0.0f) gv = gv + wd * p[q];
+    p[q] = p[q] - lr * gv;
+  }
+}
+
+// Adam in torch's single-tensor order; scalars are prepared on the host in
+// double precision and rounded to fp32 as torch does for fp32 tensors.
+__global__ void __launch_bounds__(256)
+k_adam(float* __restrict__ p, const float* __restrict__ g, float* __restrict__ m,
+       float* __restrict__ v, int64_t n, float w1, float beta2, float one_m_beta2,
+       float bc2_sqrt, float eps, float neg_step_size, float wd) {
+  for (int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; q < n;
+       q += (int64_t)gridDim.x * blockDim.x) {
+    float gv = g[q];
+    const float pv = p[q];
+    if (wd != 0.0f) gv = gv + wd * pv;
+    float mv = m[q];
+    // lerp(m, g, w1) as torch computes it for |w1| < 0.5 and otherwise
+    mv = (w1 < 0.5f) ? mv + w1 * (gv - mv) : gv - (gv - mv) * (1.0f - w1);
+    float vv = v[q] * beta2;
+    vv = vv + one_m_beta2 * gv * gv;
+    const float denom = sqrtf(vv) / bc2_sqrt + eps;
+    m[q] = mv;
+    v[q] = vv;
+    p[q] = pv + neg_step_size * (mv / denom);
+  }
+}
+
+// out[q, d] = T_d(t[q]), d = 0..deg.
+__global__ void __launch_bounds__(256)
+k_basis(const float* __restrict__ t, int64_t n, int deg, float* __restrict__ out) {
+  for (int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; q < n;
+       q += (int64_t)gridDim.x * blockDim.x) {
+    const float tv = t[q];
+    float* o = out + q * (deg + 1);
+    o[0] = 1.0f;
+    if (deg >= 1) o[1] = tv;
+    float a = 1.0f, b = tv;
+    const float t2 = tv + tv;
+    for (int d = 2; d <= deg; ++d) {
+      const float c = fmaf(t2, b, -a);
+      o[d] = c;
+      a = b;
+      b = c;
+    }
+  }
+}
+
+// dt[q] = sum_d g[q, d] d U_{d-1}(t[q]).
+__global__ void __launch_bounds__(256)
+k_basis_bwd(const float* __restrict__ t, const float* __restrict__ g, int64_t n, int deg,
+            float* __restrict__ dt) {
+  for (int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; q < n;
+       q += (int64_t)gridDim.x * blockDim.x) {
+    const float tv = t[q];
+    const float t2 = tv + tv;
+    const float* gq = g + q * (deg + 1);
+    float up = 0.0f, u = 1.0f, s = 0.0f;  // U_{-1}, U_0
+    for (int d = 1; d <= deg; ++d) {
+      s = fmaf(gq[d] * (float)d, u, s);
+      const float un = fmaf(t2, u, -up);
+      up = u;
+      u = un;
+    }
+    dt[q] = s;
+  }
+}
+
+__global__ void __launch_bounds__(256) k_zero(u32x4_t* __restrict__ p, int64_t n16) {
+  for (int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; q < n16;
+       q += (int64_t)gridDim.x * blockDim.x)
+    p[q] = u32x4_t{0u, 0u, 0u, 0u};
+}
+
+__global__ void __launch_bounds__(256) k_zero_f32(float* __restrict__ p, int64_t n) {
+  for (int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; q < n;
+       q += (int64_t)gridDim.x * blockDim.x)
+    p[q] = 0.0f;
+}
+
+// ---------------------------------------------------------------------------
+// Host-side launchers
+// ---------------------------------------------------------------------------
+
+static int grid_for(int64_t work, int per_block = 256) {
+  int64_t g = (work + per_block - 1) / per_block;
+  if (g > 65536) g = 65536;
+  if (g < 1) g = 1;
+  return (int)g;
+}
+
+void launch_tanh(const float* x, float* t, const Plan& p, hipStream_t s) {
+  const int64_t n4 = p.B * (p.I_sg / 4);
+  hipLaunchKernelGGL(k_tanh, dim3(grid_for(n4)), dim3(256), 0, s, x, t, p.B, p.I, p.I_sg);
+}
+
+template <int P, bool BF>
+static void launch_pack_t(const void* C, bool c_bf16, void* packed, const Plan& p, hipStream_t s) {
+  typedef typename Elem<BF>::type E;
+  E* Cf = reinterpret_cast<E*>(packed);
+  E* Cb = Cf + packed_cf_elems(p);
+  float* bias = reinterpret_cast<float*>(reinterpret_cast<char*>(packed) + packed_bias_offset(p));
+  dim3 grid(p.NIB, p.O64 / 32);
+  if (c_bf16)
+    hipLaunchKernelGGL((k_pack<P, BF, uint16_t>), grid, dim3(256), 0, s,
+                       reinterpret_cast<const uint16_t*>(C), Cf, Cb, bias, p);
+  else
+    hipLaunchKernelGGL((k_pack<P, BF, float>), grid, dim3(256), 0, s,
+                       reinterpret_cast<const float*>(C), Cf, Cb, bias, p);
+}
+
+void launch_pack(const void* C, bool c_bf16, void* packed, const Plan& p, hipStream_t s) {
+  const bool bf = p.esz == 2;
+  switch (p.P) {
+    case 2: bf ? launch_pack_t<2, true>(C, c_bf16, packed, p, s) : launch_pack_t<2, false>(C, c_bf16, packed, p, s); break;
+    case 4: bf ? launch_pack_t<4, true>(C, c_bf16, packed, p, s) : launch_pack_t<4, false>(C, c_bf16, packed, p, s); break;
+    case 8: bf ? launch_pack_t<8, true>(C, c_bf16, packed, p, s) : launch_pack_t<8, false>(C, c_bf16, packed, p, s); break;
+    default: bf ? launch_pack_t<16, true>(C, c_bf16, packed, p, s) : launch_pack_t<16, false>(C, c_bf16, packed, p, s); break;
+  }
+}
+
+void launch_prep_dy(const float* dy, void* dYx, void* dYc, float* colsum_part, const Plan& p,
+                    bool need_dx, bool need_dc, hipStream_t s) {
+  const int64_t row_end = p.B32 > p.Bc ? p.B32 : p.Bc;
+  dim3 grid((unsigned)ceil_div(row_end, kPrepRows), p.O64 / 32);
+  if (p.esz == 2)
+    hipLaunchKernelGGL((k_prep_dy<true>), grid, dim3(256), 0, s, dy,
+                       reinterpret_cast<uint16_t*>(dYx), reinterpret_cast<uint16_t*>(dYc),
+                       colsum_part, p, (int)need_dx, (int)need_dc);
+  else
+    hipLaunchKernelGGL((k_prep_dy<false>), grid, dim3(256), 0, s, dy,
+                       reinterpret_cast<float*>(dYx), reinterpret_cast<float*>(dYc),
+                       colsum_part, p, (int)need_dx, (int)need_dc);
+}
+
+void launch_dc_finalize(const float* part, int S, const float* colsum_part, float* dC,
+                        bool accumulate, const Plan& p, hipStream_t s) {
+  dim3 grid((unsigned)ceil_div(p.I, 16), (unsigned)ceil_div(p.O, 64));
+  hipLaunchKernelGGL(k_dc_finalize, grid, dim3(256), 0, s, part, S, colsum_part, dC,
+                     (int)accumulate, p);
+}
+
+void launch_sgd(float* p, const float* g, int64_t n, float lr, float wd, hipStream_t s) {
+  hipLaunchKernelGGL(k_sgd, dim3(grid_for(n)), dim3(256), 0, s, p, g, n, lr, wd);
+}
+
+void launch_adam(float* p, const float* g, float* m, float* v, int64_t n, float w1, float beta2,
+                 float one_m_beta2, float bc2_sqrt, float eps, float neg_step, float wd,
+                 hipStream_t s) {
+  hipLaunchKernelGGL(k_adam, dim3(grid_for(n)), dim3(256), 0, s, p, g, m, v, n, w1, beta2,
+                     one_m_beta2, bc2_sqrt, eps, neg_step, wd);
+}
+
+void launch_basis(const float* t, int64_t n, int deg, float* out, hipStream_t s) {
+  hipLaunchKernelGGL(k_basis, dim3(grid_for(n)), dim3(256), 0, s, t, n, deg, out);
+}
+
+void launch_basis_bwd(const float* t, const float* g, int64_t n, int deg, float* dt,
+                      hipStream_t s) {
+  hipLaunchKernelGGL(k_basis_bwd, dim3(grid_for(n)), dim3(256), 0, s, t, g, n, deg, dt);
+}
+
+void launch_zero_f32(float* ptr, int64_t n, hipStream_t s) {
+  if (n > 0) hipLaunchKernelGGL(k_zero_f32, dim3(grid_for(n)), dim3(256), 0, s, ptr, n);
+}
+
+void launch_zero(void* ptr, size_t bytes, hipStream_t s) {
+  const int64_t n16 = (int64_t)(bytes / 16);
+  if (n16 > 0)
+    hipLaunchKernelGGL(k_zero, dim3(grid_for(n16)), dim3(256), 0, s,
+                       reinterpret_cast<u32x4_t*>(ptr), n16);
+}
+
+}  // namespace ckan

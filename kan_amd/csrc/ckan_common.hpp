@@ -1,0 +1,206 @@
+// Shared definitions of the gfx950 ChebyKAN kernels: the layout plan, MFMA
+// fragment helpers and the Chebyshev recurrences.
+//
+// Notation: B rows, I inputs, O outputs, deg the degree, D = deg + 1.
+// The T_0 = 1 term of every contraction is handled apart from the MFMA work
+// (as a per-output bias in the forward, a column sum of dy in dC, and it has
+// no derivative), so the contractions run over T_1..T_P, where P is deg
+// padded to 2, 4, 8 or 16 with zero coefficients.
+//
+// MFMA operand layout ("fragment-major").  One k-block is 16 reduction
+// indices; for v_mfma_f32_32x32x16_bf16 a wave's operand fragment is 64 lanes
+// x 8 values, lane l holding row/column (l % 32) and the 8 reduction slots of
+// half g = l / 32.  The fp32 path runs the same k-block as 8
+// v_mfma_f32_32x32x2_f32, value j of both halves feeding instruction j.
+// Which reduction index sits in slot (g, j) is free as long as both operands
+// agree, so every packed operand is stored as [frag row-block][k-block][lane][8],
+// one contiguous 1 KiB (bf16) / 2 KiB (fp32) run per fragment: a wave loads a
+// fragment with one fully coalesced 16 B (or 32 B) access per lane, and the
+// LDS copy of a fragment is read back without bank conflicts.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ckan {
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+typedef __attribute__((ext_vector_type(16))) float f32x16_t;
+typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+typedef __attribute__((ext_vector_type(4))) unsigned u32x4_t;
+
+constexpr int kFragElems = 512;  // 64 lanes x 8 values
+
+__host__ __device__ constexpr int padded_degree(int deg) {
+  return deg <= 2 ? 2 : deg <= 4 ? 4 : deg <= 8 ? 8 : deg <= 16 ? 16 : -1;
+}
+
+// Forward reduction grouping for padded degree P.  A "group" gives each lane
+// half IPG/2 inputs x P degrees = 8*KBG values (KBG k-blocks); a
+// "super-group" (SG) is 4 groups, SGI inputs, SGK k-blocks, so one lane reads
+// 2*IPG consecutive tanh values per SG with vector loads.
+template <int P> struct FwdGroup {
+  static constexpr int IPG = 2 * (P < 8 ? 8 / P : 1);
+  static constexpr int KBG = P > 8 ? P / 8 : 1;
+  static constexpr int SGI = 4 * IPG;
+  static constexpr int SGK = 4 * KBG;
+  static constexpr int LANE_T = 2 * IPG;  // tanh values a lane reads per SG
+};
+
+__host__ __device__ inline int fwd_sgi(int P) { return 4 * 2 * (P < 8 ? 8 / P : 1); }
+__host__ __device__ inline int fwd_sgk(int P) { return 4 * (P > 8 ? P / 8 : 1); }
+
+inline int64_t round_up(int64_t a, int64_t b) { return (a + b - 1) / b * b; }
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Batch rows per k-block stage of the dC reduction (4 k-blocks of 16 rows).
+constexpr int kDcStageRows = 64;
+// Output columns per k-block stage of the dX reduction.
+constexpr int kDxStageCols = 64;
+// Rows covered by one prep_dy block (colsum partial granularity).
+constexpr int kPrepRows = 256;
+
+struct Plan {
+  int64_t B;       // rows
+  int I, O, deg, D, P;
+  int SGI, SGK;    // forward super-group inputs / k-blocks
+  int I_sg;        // I padded to SGI (tanh-cache row pitch, forward K inputs)
+  int KB;          // forward k-blocks = I_sg * P / 16
+  int O32, NBf;    // O padded to 32; forward N fragments
+  int I32, NIB;    // I padded to 32; input blocks of 32
+  int O64, KBx;    // O padded to 64; dX reduction k-blocks
+  int64_t B32;     // rows padded to 32
+  int64_t Bc, KBc; // rows padded to kDcStageRows; dC reduction k-blocks
+  int NBB;         // prep_dy row blocks (colsum partials)
+  int esz;         // bytes per packed operand element (2 bf16, 4 fp32)
+};
+
+inline Plan make_plan(int64_t B, int I, int O, int deg, bool bf16) {
+  Plan p;
+  p.B = B; p.I = I; p.O = O; p.deg = deg; p.D = deg + 1;
+  p.P = padded_degree(deg);
+  p.SGI = fwd_sgi(p.P);
+  p.SGK = fwd_sgk(p.P);
+  p.I_sg = (int)round_up(I, p.SGI);
+  p.KB = p.I_sg * p.P / 16;
+  p.O32 = (int)round_up(O, 32);
+  p.NBf = p.O32 / 32;
+  p.I32 = (int)round_up(I, 32);
+  p.NIB = p.I32 / 32;
+  p.O64 = (int)round_up(O, kDxStageCols);
+  p.KBx = p.O64 / 16;
+  p.B32 = round_up(B, 32);
+  p.Bc = round_up(B, kDcStageRows);
+  p.KBc = p.Bc / 16;
+  p.NBB = (int)ceil_div(B, kPrepRows);
+  p.esz = bf16 ? 2 : 4;
+  return p;
+}
+
+// ---------------------------------------------------------------------------
+// Device helpers
+// ---------------------------------------------------------------------------
+
+template <bool BF> struct Elem;
+template <> struct Elem<true> { typedef uint16_t type; };
+template <> struct Elem<false> { typedef float type; };
+
+// One lane's share of an MFMA operand fragment for one k-block.
+template <bool BF> struct Frag;
+template <> struct Frag<true> { bf16x8_t v; };
+template <> struct Frag<false> { f32x4_t lo, hi; };
+
+__device__ __forceinline__ Frag<true> make_frag_bf(const float* v) {
+  Frag<true> f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) f.v[j] = (__bf16)v[j];  // v_cvt_pk_bf16_f32, RNE
+  return f;
+}
+
+template <bool BF> __device__ __forceinline__ Frag<BF> make_frag(const float* v);
+template <> __device__ __forceinline__ Frag<true> make_frag<true>(const float* v) {
+  return make_frag_bf(v);
+}
+template <> __device__ __forceinline__ Frag<false> make_frag<false>(const float* v) {
+  Frag<false> f;
+  f.lo = f32x4_t{v[0], v[1], v[2], v[3]};
+  f.hi = f32x4_t{v[4], v[5], v[6], v[7]};
+  return f;
+}
+
+// Load this lane's 8 values of a fragment stored at `base` (fragment start).
+template <bool BF> __device__ __forceinline__ Frag<BF> load_frag(const typename Elem<BF>::type* base, int lane);
+template <> __device__ __forceinline__ Frag<true> load_frag<true>(const uint16_t* base, int lane) {
+  Frag<true> f;
+  f.v = *reinterpret_cast<const bf16x8_t*>(base + lane * 8);
+  return f;
+}
+template <> __device__ __forceinline__ Frag<false> load_frag<false>(const float* base, int lane) {
+  Frag<false> f;
+  const f32x4_t* p = reinterpret_cast<const f32x4_t*>(base + lane * 8);
+  f.lo = p[0];
+  f.hi = p[1];
+  return f;
+}
+
+template <bool BF> __device__ __forceinline__ Frag<BF> zero_frag();
+template <> __device__ __forceinline__ Frag<true> zero_frag<true>() {
+  Frag<true> f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) f.v[j] = (__bf16)0.0f;
+  return f;
+}
+template <> __device__ __forceinline__ Frag<false> zero_frag<false>() {
+  Frag<false> f;
+  f.lo = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  f.hi = f.lo;
+  return f;
+}
+
+// Store 8 values as this lane's share of a fragment at `base`.
+template <bool BF> __device__ __forceinline__ void store_frag(typename Elem<BF>::type* base, int lane, const float* v);
+template <> __device__ __forceinline__ void store_frag<true>(uint16_t* base, int lane, const float* v) {
+  Frag<true> f = make_frag_bf(v);
+  *reinterpret_cast<bf16x8_t*>(base + lane * 8) = f.v;
+}
+template <> __device__ __forceinline__ void store_frag<false>(float* base, int lane, const float* v) {
+  f32x4_t* p = reinterpret_cast<f32x4_t*>(base + lane * 8);
+  p[0] = f32x4_t{v[0], v[1], v[2], v[3]};
+  p[1] = f32x4_t{v[4], v[5], v[6], v[7]};
+}
+
+// acc[32x32] += A_frag(k-block) * B_frag(k-block)
+__device__ __forceinline__ void mma(f32x16_t& acc, const Frag<true>& a, const Frag<true>& b) {
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a.v, b.v, acc, 0, 0, 0);
+}
+__device__ __forceinline__ void mma(f32x16_t& acc, const Frag<false>& a, const Frag<false>& b) {
+  acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.lo[0], b.lo[0], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.lo[1], b.lo[1], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.lo[2], b.lo[2], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.lo[3], b.lo[3], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.hi[0], b.hi[0], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.hi[1], b.hi[1], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.hi[2], b.hi[2], acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.hi[3], b.hi[3], acc, 0, 0, 0);
+}
+
+// Row of accumulator value v (0..15) for lane half g in a 32x32 MFMA result;
+// the column is lane % 32.
+__device__ __forceinline__ int acc_row(int v, int g) { return 8 * (v >> 2) + 4 * g + (v & 3); }
+
+// T_1..T_P of t by the three-term recurrence T_{n+1} = 2 t T_n - T_{n-1}.
+template <int P>
+__device__ __forceinline__ void cheb_T(float t, float* out) {
+  const float t2 = t + t;
+  float a = 1.0f, b = t;
+  out[0] = t;
+#pragma unroll
+  for (int d = 1; d < P; ++d) {
+    const float c = fmaf(t2, b, -a);
+    out[d] = c;
+    a = b;
+    b = c;
+  }
+}
+
+}  // namespace ckan

@@ -1,0 +1,607 @@
+// The three MFMA contractions of the ChebyKAN layer on gfx950.
+//
+//   forward  y[b,o]        = bias[o] + sum_{i,d>=1} T_d(t[b,i]) C[i,o,d]
+//            M = rows, N = outputs, reduction = (input, degree)
+//   dX       dT[b,(i,d)]   = sum_o dy[b,o] C[i,o,d]; dx[b,i] = (1-t^2) sum_d d U_{d-1}(t) dT
+//            M = rows, N = (input, degree), reduction = outputs
+//   dC       dC[i,o,d]     = sum_b T_d(t[b,i]) dy[b,o]
+//            M = (input, degree), N = outputs, reduction = rows
+//
+// The basis T_d(tanh x) never reaches HBM.  In the forward each lane builds
+// its MFMA A fragment in registers from 2*IPG tanh values with the three-term
+// recurrence; in dC the block builds the basis operand once per stage into
+// LDS.  The coefficient operands are pre-packed fragment-major and staged
+// through LDS with a register double buffer (one barrier per stage).
+#include "ckan_kernels.hpp"
+
+namespace ckan {
+
+// ---------------------------------------------------------------------------
+// Forward
+// ---------------------------------------------------------------------------
+// Block = 4 waves arranged WGM x WGN; wave tile NM x NN fragments of 32x32.
+// The reduction runs over super-groups (SG): SGI inputs = SGK k-blocks.
+// With gridDim.z > 1 the SGs are split over blocks; each block writes its
+// partial tile and the last block of a tile (atomic ticket) reduces them in
+// fixed split order and re-arms the ticket.
+template <int P, bool BF, int NM, int NN, int WGM, int WGN>
+__global__ void __launch_bounds__(256)
+k_fwd(const float* __restrict__ tc, const typename Elem<BF>::type* __restrict__ Cf,
+      const float* __restrict__ bias_part, float* __restrict__ y, float* __restrict__ part,
+      unsigned* __restrict__ counters, Plan p, int sg_per_split) {
+  typedef typename Elem<BF>::type E;
+  typedef FwdGroup<P> G;
+  static_assert(WGM * WGN == 4, "4 waves per block");
+  constexpr int BNF = WGN * NN;
+  constexpr int BM = WGM * NM * 32;
+  constexpr int STAGE = BNF * G::SGK * kFragElems;
+  constexpr int CE = 16 / (int)sizeof(E);
+  constexpr int NCHUNK = STAGE / CE;
+  constexpr int CPT = NCHUNK / 256;
+  constexpr int CPN = G::SGK * kFragElems / CE;  // chunks per N fragment
+  static_assert(NCHUNK % 256 == 0, "stage must split evenly over 256 threads");
+  __shared__ __attribute__((aligned(16))) E lds[2 * STAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WGN, wn = wave % WGN;
+  const int g = lane >> 5;
+  const int64_t m_blk = (int64_t)blockIdx.x * BM;
+  const int nb0 = blockIdx.y * BNF;
+  const int nsg = p.I_sg / G::SGI;
+  const int sg0 = blockIdx.z * sg_per_split;
+  const int sg1 = min(nsg, sg0 + sg_per_split);
+
+  const float* trow[NM];
+  bool rvalid[NM];
+#pragma unroll
+  for (int mi = 0; mi < NM; ++mi) {
+    const int64_t r = m_blk + (wm * NM + mi) * 32 + (lane & 31);
+    rvalid[mi] = r < p.B;
+    trow[mi] = tc + (rvalid[mi] ? r : 0) * p.I_sg + g * G::LANE_T;
+  }
+
+  u32x4_t pre[CPT];
+  auto gload = [&](int sg) {
+#pragma unroll
+    for (int q = 0; q < CPT; ++q) {
+      const int c = tid + q * 256;
+      const int nbl = c / CPN, off = c - nbl * CPN;
+      const int nb = nb0 + nbl;
+      if (nb < p.NBf)
+        pre[q] = *reinterpret_cast<const u32x4_t*>(
+            Cf + ((size_t)nb * p.KB + (size_t)sg * G::SGK) * kFragElems + (size_t)off * CE);
+      else
+        pre[q] = u32x4_t{0u, 0u, 0u, 0u};
+    }
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int q = 0; q < CPT; ++q)
+      *reinterpret_cast<u32x4_t*>(lds + buf * STAGE + (tid + q * 256) * CE) = pre[q];
+  };
+
+  f32x16_t acc[NM][NN];
+#pragma unroll
+  for (int mi = 0; mi < NM; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < NN; ++ni)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[mi][ni][v] = 0.0f;
+
+  if (sg0 < sg1) {
+    gload(sg0);
+    lstore(0);
+  }
+  __syncthreads();
+
+  for (int sg = sg0; sg < sg1; ++sg) {
+    const int buf = (sg - sg0) & 1;
+    const bool more = sg + 1 < sg1;
+    if (more) gload(sg + 1);
+
+    Frag<BF> af[NM][G::SGK];
+#pragma unroll
+    for (int mi = 0; mi < NM; ++mi) {
+      float tv[G::LANE_T];
+      if (rvalid[mi]) {
+        const f32x4_t* src = reinterpret_cast<const f32x4_t*>(trow[mi] + (size_t)sg * G::SGI);
+#pragma unroll
+        for (int q = 0; q < G::LANE_T / 4; ++q) {
+          const f32x4_t w = src[q];
+          tv[4 * q + 0] = w[0]; tv[4 * q + 1] = w[1]; tv[4 * q + 2] = w[2]; tv[4 * q + 3] = w[3];
+        }
+      } else {
+#pragma unroll
+        for (int q = 0; q < G::LANE_T; ++q) tv[q] = 0.0f;
+      }
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        float vals[8 * G::KBG];
+#pragma unroll
+        for (int u = 0; u < G::IPG / 2; ++u) cheb_T<P>(tv[s * (G::IPG / 2) + u], vals + u * P);
+#pragma unroll
+        for (int h = 0; h < G::KBG; ++h) af[mi][s * G::KBG + h] = make_frag<BF>(vals + 8 * h);
+      }
+    }
+
+    const E* sb = lds + buf * STAGE;
+#pragma unroll
+    for (int kbl = 0; kbl < G::SGK; ++kbl) {
+#pragma unroll
+      for (int ni = 0; ni < NN; ++ni) {
+        const Frag<BF> bfr = load_frag<BF>(sb + ((wn * NN + ni) * G::SGK + kbl) * kFragElems, lane);
+#pragma unroll
+        for (int mi = 0; mi < NM; ++mi) mma(acc[mi][ni], af[mi][kbl], bfr);
+      }
+    }
+    if (more) lstore(buf ^ 1);
+    __syncthreads();
+  }
+
+  const bool split = gridDim.z > 1;
+  if (!split) {
+#pragma unroll
+    for (int ni = 0; ni < NN; ++ni) {
+      const int o = (nb0 + wn * NN + ni) * 32 + (lane & 31);
+      if (o >= p.O) continue;
+      float bias = 0.0f;
+      for (int ib = 0; ib < p.NIB; ++ib) bias += bias_part[(size_t)ib * p.O32 + o];
+#pragma unroll
+      for (int mi = 0; mi < NM; ++mi) {
+        const int64_t r0 = m_blk + (wm * NM + mi) * 32;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int64_t r = r0 + acc_row(v, g);
+          if (r < p.B) y[r * p.O + o] = acc[mi][ni][v] + bias;
+        }
+      }
+    }
+    return;
+  }
+
+  // split-K: partial tile, then the last block of this tile reduces.
+#pragma unroll
+  for (int ni = 0; ni < NN; ++ni) {
+    const int nb = nb0 + wn * NN + ni;
+    if (nb >= p.NBf) continue;
+    const int o = nb * 32 + (lane & 31);
+#pragma unroll
+    for (int mi = 0; mi < NM; ++mi) {
+      const int64_t r0 = m_blk + (wm * NM + mi) * 32;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int64_t r = r0 + acc_row(v, g);
+        if (r < p.B32)
+          part[((size_t)blockIdx.z * p.B32 + r) * p.O32 + o] = acc[mi][ni][v];
+      }
+    }
+  }
+  __threadfence();
+  __syncthreads();
+  __shared__ unsigned s_last;
+  const unsigned tile_id = blockIdx.y * gridDim.x + blockIdx.x;
+  if (tid == 0) {
+    const unsigned prev = atomicAdd(&counters[tile_id], 1u);
+    s_last = (prev == gridDim.z - 1) ? 1u : 0u;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+  constexpr int BN = BNF * 32;
+  for (int idx = tid; idx < BM * BN; idx += 256) {
+    const int rl = idx / BN, cl = idx - rl * BN;
+    const int64_t r = m_blk + rl;
+    const int o = nb0 * 32 + cl;
+    if (r >= p.B || o >= p.O) continue;
+    float s = 0.0f;
+    for (int ib = 0; ib < p.NIB; ++ib) s += bias_part[(size_t)ib * p.O32 + o];
+    for (unsigned z = 0; z < gridDim.z; ++z) s += part[((size_t)z * p.B32 + r) * p.O32 + o];
+    y[r * p.O + o] = s;
+  }
+  if (tid == 0) counters[tile_id] = 0u;
+}
+
+// ---------------------------------------------------------------------------
+// dX: one block = 4 waves along rows x one input block (32 inputs x P degrees).
+// B fragments (coefficients, all P degrees of the input block) are shared
+// through LDS; A fragments (dy) are per-wave global loads, prefetched a stage
+// ahead.  Epilogue: per (row, input), sum over degrees with d U_{d-1}(t) and
+// the tanh chain factor, all in registers.
+// ---------------------------------------------------------------------------
+template <int P, bool BF, int NM, int KI>
+__global__ void __launch_bounds__(256)
+k_dx(const typename Elem<BF>::type* __restrict__ dYx, const typename Elem<BF>::type* __restrict__ Cb,
+     const float* __restrict__ tc, float* __restrict__ dx, Plan p) {
+  typedef typename Elem<BF>::type E;
+  constexpr int WGM = 4;
+  constexpr int STAGE = P * KI * kFragElems;
+  constexpr int CE = 16 / (int)sizeof(E);
+  constexpr int NCHUNK = STAGE / CE;
+  constexpr int CPT = NCHUNK / 256;
+  constexpr int CPE = KI * kFragElems / CE;  // chunks per degree
+  static_assert(NCHUNK % 256 == 0, "stage must split evenly over 256 threads");
+  __shared__ __attribute__((aligned(16))) E lds[2 * STAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 5;
+  const int ib = blockIdx.y;
+  const int64_t mf0 = (int64_t)blockIdx.x * WGM * NM + wave * NM;  // first 32-row fragment
+  const int64_t nmf = p.B32 / 32;
+  const int nst = p.KBx / KI;
+
+  u32x4_t pre[CPT];
+  auto gload = [&](int st) {
+#pragma unroll
+    for (int q = 0; q < CPT; ++q) {
+      const int c = tid + q * 256;
+      const int e = c / CPE, off = c - e * CPE;
+      pre[q] = *reinterpret_cast<const u32x4_t*>(
+          Cb + ((size_t)(ib * P + e) * p.KBx + (size_t)st * KI) * kFragElems + (size_t)off * CE);
+    }
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int q = 0; q < CPT; ++q)
+      *reinterpret_cast<u32x4_t*>(lds + buf * STAGE + (tid + q * 256) * CE) = pre[q];
+  };
+  Frag<BF> apre[NM][KI];
+  auto aload = [&](int st) {
+#pragma unroll
+    for (int mi = 0; mi < NM; ++mi)
+#pragma unroll
+      for (int k = 0; k < KI; ++k) {
+        const int64_t mf = mf0 + mi;
+        apre[mi][k] = (mf < nmf)
+            ? load_frag<BF>(dYx + ((size_t)mf * p.KBx + (size_t)st * KI + k) * kFragElems, lane)
+            : zero_frag<BF>();
+      }
+  };
+
+  f32x16_t acc[NM][P];
+#pragma unroll
+  for (int mi = 0; mi < NM; ++mi)
+#pragma unroll
+    for (int e = 0; e < P; ++e)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[mi][e][v] = 0.0f;
+
+  gload(0);
+  lstore(0);
+  aload(0);
+  __syncthreads();
+
+  for (int st = 0; st < nst; ++st) {
+    const int buf = st & 1;
+    const bool more = st + 1 < nst;
+    Frag<BF> a[NM][KI];
+#pragma unroll
+    for (int mi = 0; mi < NM; ++mi)
+#pragma unroll
+      for (int k = 0; k < KI; ++k) a[mi][k] = apre[mi][k];
+    if (more) {
+      gload(st + 1);
+      aload(st + 1);
+    }
+    const E* sb = lds + buf * STAGE;
+#pragma unroll
+    for (int k = 0; k < KI; ++k) {
+#pragma unroll
+      for (int e = 0; e < P; ++e) {
+        const Frag<BF> bfr = load_frag<BF>(sb + (e * KI + k) * kFragElems, lane);
+#pragma unroll
+        for (int mi = 0; mi < NM; ++mi) mma(acc[mi][e], a[mi][k], bfr);
+      }
+    }
+    if (more) lstore(buf ^ 1);
+    __syncthreads();
+  }
+
+  const int i = ib * 32 + (lane & 31);
+#pragma unroll
+  for (int mi = 0; mi < NM; ++mi) {
+    const int64_t r0 = (mf0 + mi) * 32;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int64_t r = r0 + acc_row(v, g);
+      const bool ok = r < p.B && i < p.I;
+      const float tv = ok ? tc[r * p.I_sg + i] : 0.0f;
+      const float t2 = tv + tv;
+      float up = 0.0f, u = 1.0f, s = 0.0f;  // U_{-1}, U_0
+#pragma unroll
+      for (int e = 0; e < P; ++e) {
+        s = fmaf(acc[mi][e][v] * (float)(e + 1), u, s);
+        const float un = fmaf(t2, u, -up);
+        up = u;
+        u = un;
+      }
+      if (ok) dx[r * p.I + i] = s * (1.0f - tv * tv);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dC: one block = 4 waves along outputs x one input block (32 inputs x P
+// degrees) x one batch split.  The basis operand (rows = inputs, one fragment
+// per degree) is generated by the block into LDS once per stage of KI
+// k-blocks (16*KI batch rows); the dy operand (columns = outputs) is a
+// per-wave global load prefetched a stage ahead.  Output: fp32 partials
+// part[split][d-1][i][o], reduced by k_dc_finalize.
+// ---------------------------------------------------------------------------
+template <int P, bool BF, int NM, int KI>
+__global__ void __launch_bounds__(256)
+k_dc(const typename Elem<BF>::type* __restrict__ dYc, const float* __restrict__ tc,
+     float* __restrict__ part, Plan p, int st_per_split) {
+  typedef typename Elem<BF>::type E;
+  constexpr int WGM = 4;
+  static_assert(KI * 64 <= 256, "at most one generated lane-slot per thread per stage");
+  constexpr int GEN = KI * 64;  // threads that generate the basis operand
+  constexpr int STAGE = P * KI * kFragElems;
+  __shared__ __attribute__((aligned(16))) E lds[2 * STAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 5;
+  const int ib = blockIdx.y;
+  const int mf0 = blockIdx.x * WGM * NM + wave * NM;  // first 32-output fragment
+  const int nst = (int)(p.KBc / KI);
+  const int st0 = blockIdx.z * st_per_split;
+  const int st1 = min(nst, st0 + st_per_split);
+
+  // generator slot of this thread: k-block kg of the stage, fragment lane ln
+  const int kg = (tid >> 6) % KI, ln = tid & 63;
+  const int gi = ib * 32 + (ln & 31);
+  const bool gvalid = gi < p.I;
+  float tpre[8];
+  auto tload = [&](int st) {
+    const int64_t b0 = ((int64_t)st * KI + kg) * 16 + 8 * (ln >> 5);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int64_t b = b0 + j;
+      tpre[j] = (gvalid && b < p.B) ? tc[b * p.I_sg + gi] : 0.0f;
+    }
+  };
+  auto generate = [&](int buf) {
+    float ta[8], tb[8], t2[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      ta[j] = 1.0f;
+      tb[j] = tpre[j];
+      t2[j] = tpre[j] + tpre[j];
+    }
+    E* dst = lds + buf * STAGE + kg * kFragElems;
+    store_frag<BF>(dst, ln, tb);  // T_1
+#pragma unroll
+    for (int e = 1; e < P; ++e) {
+      float tn[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        tn[j] = fmaf(t2[j], tb[j], -ta[j]);
+        ta[j] = tb[j];
+        tb[j] = tn[j];
+      }
+      store_frag<BF>(dst + e * KI * kFragElems, ln, tn);
+    }
+  };
+  Frag<BF> bpre[NM][KI];
+  auto bload = [&](int st) {
+#pragma unroll
+    for (int mi = 0; mi < NM; ++mi)
+#pragma unroll
+      for (int k = 0; k < KI; ++k) {
+        const int mf = mf0 + mi;
+        bpre[mi][k] = (mf < p.NBf)
+            ? load_frag<BF>(dYc + ((size_t)mf * p.KBc + (size_t)st * KI + k) * kFragElems, lane)
+            : zero_frag<BF>();
+      }
+  };
+
+  f32x16_t acc[P][NM];
+#pragma unroll
+  for (int e = 0; e < P; ++e)
+#pragma unroll
+    for (int mi = 0; mi < NM; ++mi)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[e][mi][v] = 0.0f;
+
+  const bool gen = tid < GEN;
+  if (st0 < st1) {
+    if (gen) {
+      tload(st0);
+      generate(0);
+    }
+    bload(st0);
+  }
+  __syncthreads();
+
+  for (int st = st0; st < st1; ++st) {
+    const int buf = (st - st0) & 1;
+    const bool more = st + 1 < st1;
+    Frag<BF> b[NM][KI];
+#pragma unroll
+    for (int mi = 0; mi < NM; ++mi)
+#pragma unroll
+      for (int k = 0; k < KI; ++k) b[mi][k] = bpre[mi][k];
+    if (more) {
+      if (gen) tload(st + 1);
+      bload(st + 1);
+    }
+    const E* sb = lds + buf * STAGE;
+#pragma unroll
+    for (int k = 0; k < KI; ++k) {
+#pragma unroll
+      for (int e = 0; e < P; ++e) {
+        const Frag<BF> afr = load_frag<BF>(sb + (e * KI + k) * kFragElems, lane);
+#pragma unroll
+        for (int mi = 0; mi < NM; ++mi) mma(acc[e][mi], afr, b[mi][k]);
+      }
+    }
+    if (more && gen) generate(buf ^ 1);
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int mi = 0; mi < NM; ++mi) {
+    const int mf = mf0 + mi;
+    if (mf >= p.NBf) continue;
+    const int o = mf * 32 + (lane & 31);
+#pragma unroll
+    for (int e = 0; e < P; ++e) {
+      float* dst = part + (((size_t)blockIdx.z * p.P + e) * p.I32 + ib * 32) * p.O32 + o;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) dst[(size_t)acc_row(v, g) * p.O32] = acc[e][mi][v];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host-side configuration and launchers
+// ---------------------------------------------------------------------------
+
+// Number of workgroups that fills the chip once: 256 CUs, one 4-wave block each.
+static constexpr int kChipBlocks = 256;
+
+FwdChoice choose_fwd(const Plan& p) {
+  FwdChoice c;
+  if (p.B <= 32) {
+    c.tile = kFwdSmall32; c.bm = 32; c.bnf = 4;
+  } else if (p.B <= 64) {
+    c.tile = kFwdSmall64; c.bm = 64; c.bnf = 4;
+  } else {
+    c.tile = kFwdBig; c.bm = 256; c.bnf = 4;
+  }
+  c.tiles_m = (int)ceil_div(p.B, c.bm);
+  c.tiles_n = (int)ceil_div(p.NBf, c.bnf);
+  const int nsg = p.I_sg / p.SGI;
+  const int64_t tiles = (int64_t)c.tiles_m * c.tiles_n;
+  const int target = (c.tile == kFwdBig) ? kChipBlocks : 2 * kChipBlocks;
+  int splits = 1;
+  if (tiles < target) splits = (int)ceil_div(target, tiles);
+  if (splits > nsg) splits = nsg;
+  if (splits > 64) splits = 64;
+  if (splits < 1) splits = 1;
+  c.sg_per_split = (int)ceil_div(nsg, splits);
+  c.splits = (int)ceil_div(nsg, c.sg_per_split);
+  if (c.splits < 1) c.splits = 1;
+  return c;
+}
+
+template <int P, bool BF>
+static void fwd_dispatch(const float* t, const void* packed, float* y, void* ws, const Plan& p,
+                         const FwdChoice& c, hipStream_t s) {
+  typedef typename Elem<BF>::type E;
+  const E* Cf = reinterpret_cast<const E*>(packed);
+  const float* bias =
+      reinterpret_cast<const float*>(reinterpret_cast<const char*>(packed) + packed_bias_offset(p));
+  unsigned* counters = nullptr;
+  float* part = nullptr;
+  if (c.splits > 1) {
+    counters = reinterpret_cast<unsigned*>(ws);
+    part = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + fwd_counters_bytes(c));
+  }
+  dim3 grid(c.tiles_m, c.tiles_n, c.splits);
+  switch (c.tile) {
+    case kFwdSmall32:
+      hipLaunchKernelGGL((k_fwd<P, BF, 1, 1, 1, 4>), grid, dim3(256), 0, s, t, Cf, bias, y, part,
+                         counters, p, c.sg_per_split);
+      break;
+    case kFwdSmall64:
+      hipLaunchKernelGGL((k_fwd<P, BF, 2, 1, 1, 4>), grid, dim3(256), 0, s, t, Cf, bias, y, part,
+                         counters, p, c.sg_per_split);
+      break;
+    default:
+      hipLaunchKernelGGL((k_fwd<P, BF, 2, 4, 4, 1>), grid, dim3(256), 0, s, t, Cf, bias, y, part,
+                         counters, p, c.sg_per_split);
+      break;
+  }
+}
+
+void launch_fwd_gemm(const float* t, const void* packed, float* y, void* ws, const Plan& p,
+                     const FwdChoice& c, hipStream_t s) {
+  const bool bf = p.esz == 2;
+  switch (p.P) {
+    case 2: bf ? fwd_dispatch<2, true>(t, packed, y, ws, p, c, s) : fwd_dispatch<2, false>(t, packed, y, ws, p, c, s); break;
+    case 4: bf ? fwd_dispatch<4, true>(t, packed, y, ws, p, c, s) : fwd_dispatch<4, false>(t, packed, y, ws, p, c, s); break;
+    case 8: bf ? fwd_dispatch<8, true>(t, packed, y, ws, p, c, s) : fwd_dispatch<8, false>(t, packed, y, ws, p, c, s); break;
+    default: bf ? fwd_dispatch<16, true>(t, packed, y, ws, p, c, s) : fwd_dispatch<16, false>(t, packed, y, ws, p, c, s); break;
+  }
+}
+
+// dX stage depth: 4 k-blocks for bf16; fp32 halves it to bound LDS.
+template <bool BF> struct DxKI { static constexpr int v = BF ? 4 : 2; };
+
+template <int P, bool BF>
+static void dx_dispatch(const void* dYx, const void* packed, const float* t, float* dx,
+                        const Plan& p, hipStream_t s) {
+  typedef typename Elem<BF>::type E;
+  constexpr int NM = BwdTile<P>::NM;
+  const E* Cb = reinterpret_cast<const E*>(packed) + packed_cf_elems(p);
+  dim3 grid((unsigned)ceil_div(p.B32 / 32, 4 * NM), p.NIB);
+  hipLaunchKernelGGL((k_dx<P, BF, NM, DxKI<BF>::v>), grid, dim3(256), 0, s,
+                     reinterpret_cast<const E*>(dYx), Cb, t, dx, p);
+}
+
+void launch_dx_gemm(const void* dYx, const void* packed, const float* t, float* dx,
+                    const Plan& p, hipStream_t s) {
+  const bool bf = p.esz == 2;
+  switch (p.P) {
+    case 2: bf ? dx_dispatch<2, true>(dYx, packed, t, dx, p, s) : dx_dispatch<2, false>(dYx, packed, t, dx, p, s); break;
+    case 4: bf ? dx_dispatch<4, true>(dYx, packed, t, dx, p, s) : dx_dispatch<4, false>(dYx, packed, t, dx, p, s); break;
+    case 8: bf ? dx_dispatch<8, true>(dYx, packed, t, dx, p, s) : dx_dispatch<8, false>(dYx, packed, t, dx, p, s); break;
+    default: bf ? dx_dispatch<16, true>(dYx, packed, t, dx, p, s) : dx_dispatch<16, false>(dYx, packed, t, dx, p, s); break;
+  }
+}
+
+// dC stage depth in k-blocks: 4 for bf16, 2 for fp32 (LDS bound).
+template <bool BF> struct DcKI { static constexpr int v = BF ? 4 : 2; };
+
+BwdLayout bwd_layout(const Plan& p, bool need_dx, bool need_dc) {
+  BwdLayout L;
+  size_t off = 0;
+  L.dyx_off = off;
+  if (need_dx) off += align256((size_t)(p.B32 / 32) * p.KBx * kFragElems * p.esz);
+  L.dyc_off = off;
+  if (need_dc) off += align256((size_t)p.NBf * p.KBc * kFragElems * p.esz);
+  L.colsum_off = off;
+  if (need_dc) off += align256((size_t)p.NBB * p.O32 * sizeof(float));
+  L.part_off = off;
+  L.dc_splits = 1;
+  L.dc_st_per_split = 0;
+  if (need_dc) {
+    const int nm = bwd_nm(p.P);
+    const int64_t tiles = ceil_div(p.NBf, 4 * nm) * (int64_t)p.NIB;
+    const int nst = (int)(p.KBc / (p.esz == 2 ? DcKI<true>::v : DcKI<false>::v));
+    int splits = 1;
+    if (tiles < kChipBlocks) splits = (int)ceil_div(kChipBlocks, tiles);
+    if (splits > nst) splits = nst;
+    if (splits > 64) splits = 64;
+    if (splits < 1) splits = 1;
+    L.dc_st_per_split = (int)ceil_div(nst, splits);
+    L.dc_splits = (int)ceil_div(nst, L.dc_st_per_split);
+    if (L.dc_splits < 1) L.dc_splits = 1;
+    off += align256((size_t)L.dc_splits * p.P * p.I32 * p.O32 * sizeof(float));
+  }
+  L.total = off;
+  return L;
+}
+
+template <int P, bool BF>
+static void dc_dispatch(const void* dYc, const float* t, float* part, const Plan& p,
+                        const BwdLayout& L, hipStream_t s) {
+  typedef typename Elem<BF>::type E;
+  constexpr int NM = BwdTile<P>::NM;
+  dim3 grid((unsigned)ceil_div(p.NBf, 4 * NM), p.NIB, L.dc_splits);
+  hipLaunchKernelGGL((k_dc<P, BF, NM, DcKI<BF>::v>), grid, dim3(256), 0, s,
+                     reinterpret_cast<const E*>(dYc), t, part, p, L.dc_st_per_split);
+}
+
+void launch_dc_gemm(const void* dYc, const float* t, float* part, const Plan& p,
+                    const BwdLayout& L, hipStream_t s) {
+  const bool bf = p.esz == 2;
+  switch (p.P) {
+    case 2: bf ? dc_dispatch<2, true>(dYc, t, part, p, L, s) : dc_dispatch<2, false>(dYc, t, part, p, L, s); break;
+    case 4: bf ? dc_dispatch<4, true>(dYc, t, part, p, L, s) : dc_dispatch<4, false>(dYc, t, part, p, L, s); break;
+    case 8: bf ? dc_dispatch<8, true>(dYc, t, part, p, L, s) : dc_dispatch<8, false>(dYc, t, part, p, L, s); break;
+    default: bf ? dc_dispatch<16, true>(dYc, t, part, p, L, s) : dc_dispatch<16, false>(dYc, t, part, p, L, s); break;
+  }
+}
+
+}  // namespace ckan

@@ -1,0 +1,78 @@
+// Launch interface between the C-ABI host code and the kernels, and the
+// byte layout of the packed-coefficient buffer and the workspaces.
+#pragma once
+
+#include "ckan_common.hpp"
+
+namespace ckan {
+
+inline size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+// ---- packed coefficients: [Cf][Cb][bias partials] -------------------------
+inline size_t packed_cf_elems(const Plan& p) { return (size_t)p.NBf * p.KB * kFragElems; }
+inline size_t packed_cb_elems(const Plan& p) { return (size_t)p.NIB * p.P * p.KBx * kFragElems; }
+inline size_t packed_bias_offset(const Plan& p) {
+  return align256((packed_cf_elems(p) + packed_cb_elems(p)) * p.esz);
+}
+inline size_t packed_bytes(const Plan& p) {
+  return align256(packed_bias_offset(p) + (size_t)p.NIB * p.O32 * sizeof(float));
+}
+
+// ---- forward: tile configuration and split-K -------------------------------
+// Tile shapes (waves along M x waves along N, fragments per wave M x N):
+enum FwdTile { kFwdBig = 0, kFwdSmall32 = 1, kFwdSmall64 = 2 };
+struct FwdChoice {
+  int tile;           // FwdTile
+  int bm, bnf;        // block rows, block N fragments
+  int tiles_m, tiles_n;
+  int splits, sg_per_split;
+};
+FwdChoice choose_fwd(const Plan& p);
+inline size_t fwd_counters_bytes(const FwdChoice& c) {
+  return c.splits > 1 ? align256((size_t)c.tiles_m * c.tiles_n * sizeof(unsigned)) : 0;
+}
+inline size_t fwd_ws_bytes(const Plan& p, const FwdChoice& c) {
+  if (c.splits <= 1) return 0;
+  return fwd_counters_bytes(c) + align256((size_t)c.splits * p.B32 * p.O32 * sizeof(float));
+}
+
+// ---- backward workspace: [dYx][dYc][colsum partials][dC split partials] ----
+struct BwdLayout {
+  size_t dyx_off, dyc_off, colsum_off, part_off, total;
+  int dc_splits, dc_st_per_split;
+};
+BwdLayout bwd_layout(const Plan& p, bool need_dx, bool need_dc);
+
+// ---- launchers -------------------------------------------------------------
+void launch_tanh(const float* x, float* t, const Plan& p, hipStream_t s);
+void launch_pack(const void* C, bool c_bf16, void* packed, const Plan& p, hipStream_t s);
+void launch_prep_dy(const float* dy, void* dYx, void* dYc, float* colsum_part, const Plan& p,
+                    bool need_dx, bool need_dc, hipStream_t s);
+void launch_dc_finalize(const float* part, int S, const float* colsum_part, float* dC,
+                        bool accumulate, const Plan& p, hipStream_t s);
+void launch_fwd_gemm(const float* t, const void* packed, float* y, void* ws, const Plan& p,
+                     const FwdChoice& c, hipStream_t s);
+void launch_dx_gemm(const void* dYx, const void* packed, const float* t, float* dx,
+                    const Plan& p, hipStream_t s);
+void launch_dc_gemm(const void* dYc, const float* t, float* part, const Plan& p,
+                    const BwdLayout& L, hipStream_t s);
+void launch_sgd(float* p, const float* g, int64_t n, float lr, float wd, hipStream_t s);
+void launch_adam(float* p, const float* g, float* m, float* v, int64_t n, float w1, float beta2,
+                 float one_m_beta2, float bc2_sqrt, float eps, float neg_step, float wd,
+                 hipStream_t s);
+void launch_basis(const float* t, int64_t n, int deg, float* out, hipStream_t s);
+void launch_basis_bwd(const float* t, const float* g, int64_t n, int deg, float* dt,
+                      hipStream_t s);
+void launch_zero(void* ptr, size_t bytes, hipStream_t s);
+void launch_zero_f32(float* ptr, int64_t n, hipStream_t s);
+
+// dX / dC tile shapes (fragments per wave along M; 4 waves along M).
+// NM * P = 16 fragments (256 accumulator registers per lane), capped at 4
+// fragments along M so the P = 2 tile does not spill.
+template <int P> struct BwdTile {
+  static constexpr int NM = (16 / P) < 4 ? (16 / P) : 4;
+  static constexpr int WGM = 4;
+};
+inline int bwd_nm(int P) { return (16 / P) < 4 ? (16 / P) : 4; }
+
+}  // namespace ckan

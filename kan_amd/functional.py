@@ -1,0 +1,149 @@
+"""Autograd functions over the C-ABI: the ChebyKAN forward/backward and the
+materialised basis.  Device memory and streams come from torch; all compute
+is the HIP library's.  Tensors on the CPU are rejected: there is no CPU path.
+"""
+from __future__ import annotations
+
+import threading
+
+import torch
+
+from . import _lib
+
+_COMPUTE = {"fp32": _lib.CKAN_COMPUTE_FP32, "bf16": _lib.CKAN_COMPUTE_BF16}
+
+# Forward workspaces hold split-K tickets that must start at zero; the
+# library re-arms them at the end of every call.  One per (device, stream):
+# calls sharing a workspace must not overlap in time.
+_fwd_ws = {}
+_fwd_ws_lock = threading.Lock()
+
+
+def _forward_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    stream = _lib.stream_ptr(device)
+    key = (device.index, stream)
+    with _fwd_ws_lock:
+        ws = _fwd_ws.get(key)
+        if ws is None or ws.numel() < nbytes:
+            ws = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
+            _fwd_ws[key] = ws
+    return ws
+
+
+def _require_device(*tensors) -> None:
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError(
+                "kan_amd ChebyKAN runs only on a ROCm device (MI355X); got a tensor on "
+                f"{t.device}. Move the module and inputs to 'cuda'.")
+
+
+def compute_code(compute: str) -> int:
+    try:
+        return _COMPUTE[compute]
+    except KeyError:
+        raise ValueError(f"compute must be one of {sorted(_COMPUTE)}, got {compute!r}") from None
+
+
+def coeff_code(dtype: torch.dtype) -> int:
+    if dtype == torch.float32:
+        return _lib.CKAN_DTYPE_F32
+    if dtype == torch.bfloat16:
+        return _lib.CKAN_DTYPE_BF16
+    raise RuntimeError(f"kan_amd ChebyKAN supports float32 or bfloat16 coefficients, got {dtype}")
+
+
+class ChebyKANFunction(torch.autograd.Function):
+    """y = einsum('bid,iod->bo', T(tanh x), C) with hand-written HIP backward."""
+
+    @staticmethod
+    def forward(ctx, x: torch.Tensor, coeffs: torch.Tensor, compute: str = "fp32"):
+        _require_device(x, coeffs)
+        if coeffs.dim() != 3:
+            raise RuntimeError(f"coefficients must be [in, out, degree+1], got {tuple(coeffs.shape)}")
+        in_dim, out_dim, dd = coeffs.shape
+        if x.dim() != 2 or x.shape[1] != in_dim:
+            raise RuntimeError(f"x must be [batch, {in_dim}], got {tuple(x.shape)}")
+        lib = _lib.load()
+        dev = x.device
+        x32 = x.contiguous() if x.dtype == torch.float32 else x.float().contiguous()
+        c = coeffs.detach().contiguous()
+        desc = _lib.make_desc(x32.shape[0], in_dim, out_dim, dd - 1, compute_code(compute),
+                              coeff_code(c.dtype))
+        stream = _lib.stream_ptr(dev)
+        packed = torch.empty(lib.ckan_packed_bytes(desc), dtype=torch.uint8, device=dev)
+        _lib.check(lib.ckan_pack_coeffs(desc, c.data_ptr(), packed.data_ptr(), stream))
+        t = torch.empty(lib.ckan_tcache_elems(desc), dtype=torch.float32, device=dev)
+        y = torch.empty(x32.shape[0], out_dim, dtype=torch.float32, device=dev)
+        ws_bytes = lib.ckan_fwd_workspace_bytes(desc)
+        ws = _forward_workspace(dev, ws_bytes) if ws_bytes else None
+        _lib.check(lib.ckan_forward(desc, x32.data_ptr(), packed.data_ptr(), y.data_ptr(),
+                                    t.data_ptr(), _lib.ptr(ws), ws_bytes, stream))
+        ctx.save_for_backward(t, packed)
+        ctx.desc = desc
+        ctx.x_dtype = x.dtype
+        ctx.c_dtype = coeffs.dtype
+        return y
+
+    @staticmethod
+    def backward(ctx, dy: torch.Tensor):
+        t, packed = ctx.saved_tensors
+        desc = ctx.desc
+        need_dx, need_dc = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        if not (need_dx or need_dc):
+            return None, None, None
+        lib = _lib.load()
+        dev = dy.device
+        dy32 = dy.contiguous() if dy.dtype == torch.float32 else dy.float().contiguous()
+        dx = torch.empty(desc.batch, desc.in_dim, dtype=torch.float32, device=dev) if need_dx else None
+        dc = (torch.empty(desc.in_dim, desc.out_dim, desc.degree + 1, dtype=torch.float32, device=dev)
+              if need_dc else None)
+        ws_bytes = lib.ckan_bwd_workspace_bytes(desc, int(need_dx), int(need_dc))
+        ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
+        _lib.check(lib.ckan_backward(desc, t.data_ptr(), packed.data_ptr(), dy32.data_ptr(),
+                                     _lib.ptr(dx), _lib.ptr(dc), 0, ws.data_ptr(), ws_bytes,
+                                     _lib.stream_ptr(dev)))
+        if dx is not None and ctx.x_dtype != torch.float32:
+            dx = dx.to(ctx.x_dtype)
+        if dc is not None and ctx.c_dtype != torch.float32:
+            dc = dc.to(ctx.c_dtype)
+        return dx, dc, None
+
+
+class ChebyshevBasisFunction(torch.autograd.Function):
+    """T_d(t) for d = 0..degree, materialised as [..., degree+1] (fp32)."""
+
+    @staticmethod
+    def forward(ctx, t: torch.Tensor, degree: int):
+        _require_device(t)
+        lib = _lib.load()
+        t32 = t.contiguous() if t.dtype == torch.float32 else t.float().contiguous()
+        out = torch.empty(*t32.shape, degree + 1, dtype=torch.float32, device=t.device)
+        _lib.check(lib.ckan_basis(t32.data_ptr(), t32.numel(), int(degree), out.data_ptr(),
+                                  _lib.stream_ptr(t.device)))
+        ctx.save_for_backward(t32)
+        ctx.degree = degree
+        ctx.t_dtype = t.dtype
+        return out
+
+    @staticmethod
+    def backward(ctx, g: torch.Tensor):
+        (t32,) = ctx.saved_tensors
+        if not ctx.needs_input_grad[0]:
+            return None, None
+        lib = _lib.load()
+        g32 = g.contiguous() if g.dtype == torch.float32 else g.float().contiguous()
+        dt = torch.empty_like(t32)
+        _lib.check(lib.ckan_basis_backward(t32.data_ptr(), g32.data_ptr(), t32.numel(),
+                                           int(ctx.degree), dt.data_ptr(),
+                                           _lib.stream_ptr(t32.device)))
+        return dt.to(ctx.t_dtype), None
+
+
+def chebykan(x: torch.Tensor, coeffs: torch.Tensor, compute: str = "fp32") -> torch.Tensor:
+    """Functional ChebyKAN layer: x [B, in], coeffs [in, out, D] -> y [B, out]."""
+    return ChebyKANFunction.apply(x, coeffs, compute)
+
+
+def chebyshev_basis(t: torch.Tensor, degree: int) -> torch.Tensor:
+    return ChebyshevBasisFunction.apply(t, degree)

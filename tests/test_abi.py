@@ -1,0 +1,136 @@
+"""CPU-side checks of the C-ABI boundary: the library loads, exports every
+function include/chebykan.h declares, and rejects invalid requests on the
+host before any launch (no GPU needed: these calls return before touching
+the HIP runtime)."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from kan_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _header_functions():
+    txt = open(os.path.join(ROOT, "include", "chebykan.h")).read()
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+    return sorted(set(re.findall(r"\b(ckan_[a-z0-9_]+)\s*\(", txt)))
+
+
+def test_library_exports_every_header_symbol():
+    lib = _lib.load()
+    names = _header_functions()
+    assert len(names) >= 15
+    for n in names:
+        assert hasattr(lib, n), n
+        assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
+    assert set(_lib.SIGNATURES) == set(names)
+
+
+def test_version_string():
+    assert b"gfx950" in _lib.load().ckan_version()
+
+
+def _desc(B=8, I=4, O=3, deg=8, compute=0, cdt=0):
+    return _lib.make_desc(B, I, O, deg, compute, cdt)
+
+
+@pytest.mark.parametrize("field,value,code", [
+    ("batch", -1, _lib.CKAN_ERR_INVALID_ARG),
+    ("in_dim", 0, _lib.CKAN_ERR_INVALID_ARG),
+    ("out_dim", 0, _lib.CKAN_ERR_INVALID_ARG),
+    ("degree", -1, _lib.CKAN_ERR_INVALID_ARG),
+    ("degree", 17, _lib.CKAN_ERR_UNSUPPORTED),
+    ("compute", 7, _lib.CKAN_ERR_INVALID_ARG),
+    ("coeff_dtype", 5, _lib.CKAN_ERR_INVALID_ARG),
+    ("reserved", 1, _lib.CKAN_ERR_INVALID_ARG),
+])
+def test_descriptor_validation(field, value, code):
+    lib = _lib.load()
+    d = _desc()
+    setattr(d, field, value)
+    assert lib.ckan_forward(ctypes.byref(d), 1, 1, 1, 1, None, 0, None) == code
+    assert lib.ckan_last_error()
+    assert lib.ckan_packed_bytes(ctypes.byref(d)) == 0
+
+
+def test_null_pointers_rejected_before_launch():
+    lib = _lib.load()
+    d = _desc()
+    assert lib.ckan_forward(None, 1, 1, 1, 1, None, 0, None) == _lib.CKAN_ERR_INVALID_ARG
+    assert lib.ckan_forward(ctypes.byref(d), None, 16, 16, 16, None, 0, None) == _lib.CKAN_ERR_INVALID_ARG
+    assert lib.ckan_pack_coeffs(ctypes.byref(d), None, 16, None) == _lib.CKAN_ERR_INVALID_ARG
+    # misaligned packed buffer
+    assert lib.ckan_pack_coeffs(ctypes.byref(d), 16, 18, None) == _lib.CKAN_ERR_INVALID_ARG
+    assert lib.ckan_adam_step(16, 16, 16, 16, 4, 0, 1e-3, 0.9, 0.999, 1e-8, 0.0, None) == \
+        _lib.CKAN_ERR_INVALID_ARG
+    assert lib.ckan_adam_step(16, 16, 16, 16, 4, 1, 1e-3, 1.5, 0.999, 1e-8, 0.0, None) == \
+        _lib.CKAN_ERR_INVALID_ARG
+    assert lib.ckan_sgd_step(None, None, 4, 0.1, 0.0, None) == _lib.CKAN_ERR_INVALID_ARG
+    assert lib.ckan_basis(None, 4, 3, None, None) == _lib.CKAN_ERR_INVALID_ARG
+
+
+def test_workspace_too_small_is_reported():
+    lib = _lib.load()
+    d = _desc(B=1, I=2048, O=2048, deg=8, compute=1, cdt=1)
+    need = lib.ckan_fwd_workspace_bytes(ctypes.byref(d))
+    assert need > 0  # small batch uses split-K partials
+    rc = lib.ckan_forward(ctypes.byref(d), 16, 16, 16, 16, 16, need - 256, None)
+    assert rc == _lib.CKAN_ERR_WORKSPACE
+    assert b"workspace" in lib.ckan_last_error()
+
+
+def test_empty_calls_are_noops():
+    lib = _lib.load()
+    d = _desc(B=0)
+    assert lib.ckan_forward(ctypes.byref(d), None, None, None, None, None, 0, None) == _lib.CKAN_OK
+    assert lib.ckan_backward(ctypes.byref(d), None, None, None, None, None, 0, None, 0, None) == _lib.CKAN_OK
+    assert lib.ckan_sgd_step(None, None, 0, 0.1, 0.0, None) == _lib.CKAN_OK
+
+
+def test_sizes_are_consistent():
+    lib = _lib.load()
+    d = _desc(B=8192, I=1024, O=1024, deg=8, compute=1)
+    packed = lib.ckan_packed_bytes(ctypes.byref(d))
+    # Cf + Cb in bf16 (2 x 1024*1024*8*2 bytes) plus bias partials
+    assert packed >= 2 * 1024 * 1024 * 8 * 2
+    assert lib.ckan_tcache_elems(ctypes.byref(d)) == 8192 * 1024
+    d32 = _desc(B=8192, I=1024, O=1024, deg=8, compute=0)
+    assert lib.ckan_packed_bytes(ctypes.byref(d32)) >= 2 * packed - 4096 * 1024
+
+
+def test_cpu_tensors_fail_loudly():
+    import kan_amd
+    m = kan_amd.ChebyKANLayer(4, 3, 5)
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        m(torch.randn(2, 4))
+
+
+def test_layer_api_matches_reference_surface():
+    import kan_amd
+    from oracle import chebykan_oracle as orc
+    torch.manual_seed(11)
+    m = kan_amd.ChebyKANLayer(6, 5, 4)
+    c = orc.init_coeffs(6, 5, 4, seed=11)
+    assert torch.equal(m.cheby_coeffs.detach(), c)
+    assert list(m.state_dict()) == ["cheby_coeffs"]
+    assert m.get_coefficients() is m.cheby_coeffs
+    f = m.get_analytical_form()
+    assert f["type"] == "ChebyKANLayer" and f["basis"] == "Chebyshev-4"
+    assert f["coefficients"].shape == (6, 5, 5)
+    assert repr(m) == "ChebyKANLayer(input_dim=6, output_dim=5, degree=4)"
+    assert isinstance(kan_amd.get_layer("chebykan", input_dim=2, output_dim=2, degree=3),
+                      kan_amd.ChebyKANLayer)
+    with pytest.raises(ValueError):
+        kan_amd.get_layer("nope")
+    with pytest.raises(ValueError):
+        kan_amd.get_basis("nope")
+    b = kan_amd.get_basis("chebyshev", degree=3)
+    assert b.name == "Chebyshev-3" and b.domain == (-1, 1)
+    seq = kan_amd.KANSequential(kan_amd.ChebyKANLayer(3, 4, 2), kan_amd.ChebyKANLayer(4, 2, 2))
+    assert len(seq.get_analytical_form()) == 2
+    with pytest.raises(ValueError):
+        kan_amd.ChebyKANLayer(3, 3, 3, compute="fp8")

@@ -1,0 +1,270 @@
+"""GPU parity: the HIP path (through the C-ABI) against the CPU oracle.
+
+Tolerances (norm-wise, ||a - b|| / ||b||):
+  fp32 MFMA path:  1e-5 for y, dx and dC
+  bf16 MFMA path:  2e-2, against the fp32 oracle applied to the same
+                   bf16-rounded coefficients (the reference cannot run bf16
+                   coefficients itself)
+Inputs keep |x| < 9 so the reference's saturation NaN (|x| >= 9.0108) does
+not arise; that divergence is tested separately.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import chebykan_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+FP32_TOL = 1e-5
+BF16_TOL = 2e-2
+
+
+def _rel(a, b):
+    a = a.detach().double().cpu()
+    b = b.detach().double().cpu()
+    n = b.norm().item()
+    return (a - b).norm().item() / (n if n > 0 else 1.0)
+
+
+def _inputs(B, I, O, deg, seed, x_scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(B, I, generator=g) * x_scale
+    c = torch.randn(I, O, deg + 1, generator=g) / (I * (deg + 1))
+    dy = torch.randn(B, O, generator=g)
+    return x, c, dy
+
+
+def _gpu_fwd_bwd(x, c, dy, compute, need_dx=True, need_dc=True):
+    from kan_amd import functional as F
+    xd = x.cuda().requires_grad_(need_dx)
+    cd = c.cuda().requires_grad_(need_dc)
+    y = F.chebykan(xd, cd, compute)
+    y.backward(dy.cuda())
+    torch.cuda.synchronize()
+    return (y.detach().cpu(), xd.grad.cpu() if need_dx else None,
+            cd.grad.cpu() if need_dc else None)
+
+
+SHAPES = [
+    # B, I, O, deg
+    (100, 1, 1, 8),       # config 1
+    (256, 784, 64, 4),    # config 2 layer 1
+    (256, 64, 10, 4),     # config 2 layer 2
+    (64, 33, 17, 0),
+    (7, 3, 5, 1),
+    (65, 31, 33, 2),
+    (300, 40, 70, 3),
+    (33, 100, 100, 5),
+    (129, 64, 96, 7),
+    (512, 256, 256, 8),
+    (96, 48, 40, 9),
+    (200, 72, 50, 15),
+    (256, 128, 64, 16),
+]
+
+
+@pytest.mark.parametrize("B,I,O,deg", SHAPES)
+def test_fp32_forward_backward_parity(B, I, O, deg):
+    print(f"fp32 parity B={B} I={I} O={O} deg={deg}", flush=True)
+    x, c, dy = _inputs(B, I, O, deg, seed=B * 7 + I + deg, x_scale=1.5)
+    y_ref, dx_ref, dc_ref = orc.layer_forward_backward(x, c, dy)
+    y, dx, dc = _gpu_fwd_bwd(x, c, dy, "fp32")
+    assert _rel(y, y_ref) <= FP32_TOL
+    assert _rel(dx, dx_ref) <= FP32_TOL
+    assert _rel(dc, dc_ref) <= FP32_TOL
+
+
+@pytest.mark.parametrize("B,I,O,deg", SHAPES)
+def test_bf16_forward_backward_parity(B, I, O, deg):
+    print(f"bf16 parity B={B} I={I} O={O} deg={deg}", flush=True)
+    x, c, dy = _inputs(B, I, O, deg, seed=B * 5 + O + deg, x_scale=1.5)
+    c_r = c.bfloat16().float()
+    y_ref, dx_ref, dc_ref = orc.layer_forward_backward(x, c_r, dy)
+    y, dx, dc = _gpu_fwd_bwd(x, c_r, dy, "bf16")
+    assert _rel(y, y_ref) <= BF16_TOL
+    assert _rel(dx, dx_ref) <= BF16_TOL
+    assert _rel(dc, dc_ref) <= BF16_TOL
+
+
+def test_fp32_config3_scaled_parity():
+    # config 3 shape with the batch cut to 1024 rows so the CPU oracle is quick
+    print("fp32 parity cfg3 B=1024", flush=True)
+    x, c, dy = _inputs(1024, 1024, 1024, 8, seed=3)
+    y_ref, dx_ref, dc_ref = orc.layer_forward_backward(x, c, dy)
+    y, dx, dc = _gpu_fwd_bwd(x, c, dy, "fp32")
+    assert _rel(y, y_ref) <= FP32_TOL
+    assert _rel(dx, dx_ref) <= FP32_TOL
+    assert _rel(dc, dc_ref) <= FP32_TOL
+
+
+@pytest.mark.parametrize("compute,tol", [("fp32", FP32_TOL), ("bf16", BF16_TOL)])
+def test_config3_full_size_properties(compute, tol):
+    """Full config 3 (B=8192, 1024->1024, deg 8): row-local parity on sampled
+    rows, and the size-independent identity <dC, C> = <dy, y>."""
+    print(f"cfg3 full-size properties {compute}", flush=True)
+    B, I, O, deg = 8192, 1024, 1024, 8
+    g = torch.Generator().manual_seed(33)
+    x = torch.randn(B, I, generator=g)
+    c = torch.randn(I, O, deg + 1, generator=g) / (I * (deg + 1))
+    if compute == "bf16":
+        c = c.bfloat16().float()
+    dy = torch.randn(B, O, generator=g)
+    y, dx, dc = _gpu_fwd_bwd(x, c, dy, compute)
+    rows = torch.arange(0, B, 97)
+    y_ref, dx_ref, _ = orc.layer_forward_backward(x[rows], c, dy[rows], need_dc=False)
+    assert _rel(y[rows], y_ref) <= tol
+    assert _rel(dx[rows], dx_ref) <= tol
+    lhs = (dc.double() * c.double()).sum().item()
+    rhs = (dy.double() * y.double()).sum().item()
+    scale = (dc.double().abs() * c.double().abs()).sum().item()
+    assert abs(lhs - rhs) <= tol * scale
+    # dC columns for a few inputs, from the fp64 definition
+    t = torch.tanh(x.double())
+    for i in (0, 511, 1023):
+        basis = torch.from_numpy(orc.cheb_T_fp64(t[:, i].numpy(), deg))  # [B, D]
+        ref = basis.T @ dy.double()                                      # [D, O]
+        assert _rel(dc[i].T, ref) <= tol
+
+
+@pytest.mark.parametrize("B", [1, 16, 64])
+def test_config5_small_batch_bf16_coeffs(B):
+    """Config 5: 2048 -> 2048, deg 8, bf16 coefficients, B in {1, 16, 64}."""
+    print(f"cfg5 small batch B={B}", flush=True)
+    from kan_amd import functional as F
+    I = O = 2048
+    deg = 8
+    g = torch.Generator().manual_seed(50 + B)
+    x = torch.randn(B, I, generator=g)
+    c = (torch.randn(I, O, deg + 1, generator=g) / (I * (deg + 1))).bfloat16()
+    y = F.chebykan(x.cuda(), c.cuda(), "bf16")
+    torch.cuda.synchronize()
+    y_ref = orc.layer_forward(x, c.float())
+    assert _rel(y.cpu(), y_ref) <= BF16_TOL
+    # repeated calls reuse the split-K tickets; results must not drift
+    y2 = F.chebykan(x.cuda(), c.cuda(), "bf16")
+    torch.cuda.synchronize()
+    assert torch.equal(y.cpu(), y2.cpu())
+
+
+def test_split_k_paths_fp32():
+    # small batches with a long reduction select split-K in the forward and dC
+    for B, I, O, deg in [(1, 512, 96, 8), (20, 300, 64, 4), (48, 1024, 32, 16)]:
+        print(f"split-K B={B} I={I} O={O} deg={deg}", flush=True)
+        x, c, dy = _inputs(B, I, O, deg, seed=B + I)
+        y_ref, dx_ref, dc_ref = orc.layer_forward_backward(x, c, dy)
+        y, dx, dc = _gpu_fwd_bwd(x, c, dy, "fp32")
+        assert _rel(y, y_ref) <= FP32_TOL
+        assert _rel(dx, dx_ref) <= FP32_TOL
+        assert _rel(dc, dc_ref) <= FP32_TOL
+
+
+def test_deterministic_results():
+    x, c, dy = _inputs(512, 128, 128, 8, seed=9)
+    a = _gpu_fwd_bwd(x, c, dy, "bf16")
+    b = _gpu_fwd_bwd(x, c, dy, "bf16")
+    for u, v in zip(a, b):
+        assert torch.equal(u, v)
+
+
+def test_only_coeff_grad_skips_dx():
+    x, c, dy = _inputs(128, 64, 32, 4, seed=4)
+    y_ref, _, dc_ref = orc.layer_forward_backward(x, c, dy, need_dx=False)
+    y, dx, dc = _gpu_fwd_bwd(x, c, dy, "fp32", need_dx=False)
+    assert dx is None
+    assert _rel(dc, dc_ref) <= FP32_TOL
+
+
+def test_saturation_is_finite_and_analytic():
+    """Divergence from the reference by design: for |x| >= 9.0108 the
+    reference's dx is NaN; this path returns the analytic limit."""
+    x = torch.tensor([[0.0], [3.0], [9.5], [-12.0]])
+    c = torch.ones(1, 1, 9)
+    dy = torch.ones(4, 1)
+    _, dx, _ = _gpu_fwd_bwd(x, c, dy, "fp32")
+    dx64, _ = orc.backward_fp64(x.numpy(), c.numpy(), dy.numpy())
+    assert torch.isfinite(dx).all()
+    assert np.allclose(dx.numpy().ravel(), dx64.ravel(), rtol=1e-4, atol=1e-5)
+
+
+def test_layer_module_and_state_dict_roundtrip():
+    import kan_amd
+    torch.manual_seed(2)
+    m = kan_amd.ChebyKANLayer(16, 8, 6).cuda()
+    x = torch.randn(4, 2, 16)  # forward views to [-1, in]
+    y = m(x.cuda())
+    assert y.shape == (8, 8)
+    y_ref = orc.layer_forward(x.reshape(-1, 16), m.cheby_coeffs.detach().cpu())
+    assert _rel(y.detach().cpu(), y_ref) <= FP32_TOL
+    m2 = kan_amd.ChebyKANLayer(16, 8, 6).cuda()
+    m2.load_state_dict(m.state_dict())
+    assert torch.equal(m2(x.cuda()).detach().cpu(), y.detach().cpu())
+
+
+def test_basis_functions_and_backward():
+    import kan_amd
+    b = kan_amd.ChebyshevBasis(degree=7)
+    t = (torch.rand(50, 6) * 2 - 1)
+    out = b.basis_functions(t.cuda()).cpu()
+    assert _rel(out, orc.basis_closed_form(t, 7)) <= 1e-5
+    td = t.cuda().requires_grad_(True)
+    g = torch.randn(50, 6, 8)
+    b.basis_functions(td).backward(g.cuda())
+    tr = t.clone().requires_grad_(True)
+    orc.basis_recurrence(tr, 7).backward(g)
+    assert _rel(td.grad.cpu(), tr.grad) <= 1e-5
+
+
+def test_optimizers_match_torch():
+    from kan_amd import optim
+    g = torch.Generator().manual_seed(8)
+    p0 = torch.randn(1000, generator=g)
+    grads = [torch.randn(1000, generator=g) for _ in range(5)]
+    for wd in (0.0, 0.01):
+        pr = p0.clone().requires_grad_(True)
+        ref = torch.optim.Adam([pr], lr=0.01, weight_decay=wd)
+        pd = p0.cuda().requires_grad_(True)
+        opt = optim.Adam([pd], lr=0.01, weight_decay=wd)
+        for gr in grads:
+            pr.grad = gr.clone()
+            ref.step()
+            pd.grad = gr.cuda()
+            opt.step()
+        assert torch.allclose(pd.detach().cpu(), pr.detach(), rtol=0, atol=1e-6)
+    pr = p0.clone().requires_grad_(True)
+    ref = torch.optim.SGD([pr], lr=0.05)
+    pd = p0.cuda().requires_grad_(True)
+    opt = optim.SGD([pd], lr=0.05)
+    for gr in grads:
+        pr.grad = gr.clone()
+        ref.step()
+        pd.grad = gr.cuda()
+        opt.step()
+    assert torch.allclose(pd.detach().cpu(), pr.detach(), rtol=0, atol=1e-6)
+
+
+def test_config1_training_loop_matches_oracle():
+    """Config 1 (README.md:42-73): 1000 full-batch Adam steps on sin(2 pi x)."""
+    import kan_amd
+    from kan_amd import optim
+    x = torch.linspace(-1, 1, 100).reshape(-1, 1)
+    y = torch.sin(2 * math.pi * x)
+    torch.manual_seed(0)
+    m = kan_amd.ChebyKANLayer(1, 1, 8)
+    c0 = m.cheby_coeffs.detach().clone()
+    m = m.cuda()
+    opt = optim.Adam(m.parameters(), lr=0.01)
+    xd, yd = x.cuda(), y.cuda()
+    losses = []
+    for _ in range(1000):
+        opt.zero_grad()
+        loss = torch.nn.functional.mse_loss(m(xd), yd)
+        loss.backward()
+        opt.step()
+        losses.append(loss.detach())
+    losses = torch.stack(losses).cpu()
+    c_ref, losses_ref = orc.train_steps(x, y, [c0], steps=1000, loss="mse", optimizer="adam", lr=0.01)
+    assert abs(losses[-1].item() - losses_ref[-1]) <= 1e-3 * max(losses_ref[0], 1e-6) + 1e-5
+    assert _rel(m.cheby_coeffs.detach().cpu(), c_ref[0]) <= 1e-3
