@@ -41,32 +41,45 @@ template <> __device__ __forceinline__ float to_f32<uint16_t>(uint16_t v) {
 //   Cb: dX B operand,      [NIB*P][KBx][64][8] (columns (input block, d), reduction o)
 //   bias_part[ib][o] = sum_{i in block ib} C[i, o, 0]
 // One block per (32 inputs, 32 outputs) tile, staged through LDS so the
-// global read of C is one contiguous run of 32*D values per input.
+// global read of C is one contiguous run of 32*D values per input.  The LDS
+// row pitch 32*D+1 is odd, so the column-wise reads of the Cb re-layout hit
+// 32 distinct banks.
 template <int P, bool BF, typename CT>
 __global__ void __launch_bounds__(256)
 k_pack(const CT* __restrict__ C, typename Elem<BF>::type* __restrict__ Cf,
        typename Elem<BF>::type* __restrict__ Cb, float* __restrict__ bias_part, Plan p) {
   using G = FwdGroup<P>;
-  __shared__ float tile[32 * 32 * 17];
+  constexpr int RPMAX = 32 * (P + 1) + 1;
+  __shared__ float tile[32 * RPMAX];
+  __shared__ float bsum[8][32];
   const int tid = threadIdx.x;
   const int ib = blockIdx.x, ob = blockIdx.y;
   const int i0 = ib * 32, o0 = ob * 32;
   const int D = p.D;
-  const int n = 32 * 32 * D;
-  for (int idx = tid; idx < n; idx += 256) {
-    const int il = idx / (32 * D);
-    const int rem = idx - il * 32 * D;
-    const int ol = rem / D;
-    const int i = i0 + il, o = o0 + ol;
-    float v = 0.0f;
-    if (i < p.I && o < p.O) v = to_f32<CT>(C[((size_t)i * p.O + o0) * D + rem]);
-    tile[idx] = v;
+  const int RP = 32 * D + 1;
+  const int ocount = min(32, p.O - o0);  // may be <= 0 for the Cb zero-fill blocks
+  const int nrow = ocount > 0 ? ocount * D : 0;
+#pragma unroll 4
+  for (int il = 0; il < 32; ++il) {
+    const int i = i0 + il;
+    const CT* src = C + ((size_t)i * p.O + o0) * D;
+    for (int k = tid; k < 32 * D; k += 256)
+      tile[il * RP + k] = (i < p.I && k < nrow) ? to_f32<CT>(src[k]) : 0.0f;
   }
   __syncthreads();
 
+  {  // bias partial: 8 groups of 4 inputs, then a fixed-order sum
+    const int ol = tid & 31, grp = tid >> 5;
+    float s = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) s += tile[(grp * 4 + q) * RP + ol * D];
+    bsum[grp][ol] = s;
+  }
+  __syncthreads();
   if (tid < 32 && o0 + tid < p.O32) {
     float s = 0.0f;
-    for (int il = 0; il < 32; ++il) s += tile[(il * 32 + tid) * D];
+#pragma unroll
+    for (int grp = 0; grp < 8; ++grp) s += bsum[grp][tid];
     bias_part[(size_t)ib * p.O32 + o0 + tid] = s;
   }
 
@@ -85,7 +98,7 @@ k_pack(const CT* __restrict__ C, typename Elem<BF>::type* __restrict__ Cf,
         const int vv = 8 * h + j;
         const int u = vv / P, d = vv % P + 1;
         const int i = r * G::SGI + g * 2 * G::IPG + s * (G::IPG / 2) + u;
-        v[j] = (d <= p.deg) ? tile[((i - i0) * 32 + ol) * D + d] : 0.0f;
+        v[j] = (d <= p.deg) ? tile[(i - i0) * RP + ol * D + d] : 0.0f;
       }
       store_frag<BF>(Cf + ((size_t)ob * p.KB + kb) * kFragElems, lane, v);
     }
@@ -100,9 +113,23 @@ k_pack(const CT* __restrict__ C, typename Elem<BF>::type* __restrict__ Cf,
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int ol = 16 * kbl + 8 * g + j;
-      v[j] = (e + 1 <= p.deg) ? tile[(il * 32 + ol) * D + e + 1] : 0.0f;
+      v[j] = (e + 1 <= p.deg) ? tile[il * RP + ol * D + e + 1] : 0.0f;
     }
     store_frag<BF>(Cb + ((size_t)(ib * P + e) * p.KBx + kbx) * kFragElems, lane, v);
+  }
+}
+
+// 8 consecutive values of row b of dy starting at column o (zero outside B x O).
+__device__ __forceinline__ void load_row8(const float* __restrict__ dy, int64_t b, int o,
+                                          const Plan& p, float* v) {
+  if (b < p.B && o + 8 <= p.O && (p.O & 3) == 0) {
+    const f32x4_t* src = reinterpret_cast<const f32x4_t*>(dy + b * p.O + o);
+    const f32x4_t a = src[0], c = src[1];
+    v[0] = a[0]; v[1] = a[1]; v[2] = a[2]; v[3] = a[3];
+    v[4] = c[0]; v[5] = c[1]; v[6] = c[2]; v[7] = c[3];
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = (b < p.B && o + j < p.O) ? dy[b * p.O + o + j] : 0.0f;
   }
 }
 
@@ -110,91 +137,93 @@ k_pack(const CT* __restrict__ C, typename Elem<BF>::type* __restrict__ Cf,
 //   dYx: dX A operand  [B32/32][KBx][64][8]  (rows b, reduction o)
 //   dYc: dC B operand  [NBf][KBc][64][8]     (columns o, reduction b)
 // and writes colsum_part[bb][o] = sum of dy over rows [256 bb, 256 bb + 256).
-// One block per (256 rows, 32 columns); 32x32 sub-tiles pass through LDS.
+// One wave per (32 columns, 256 rows); each fragment lane reads its 8 values
+// straight from dy (a 32-byte row run for dYx, one coalesced 128-byte row
+// segment per value for dYc) and writes one 16- or 32-byte vector.
 template <bool BF>
 __global__ void __launch_bounds__(256)
 k_prep_dy(const float* __restrict__ dy, typename Elem<BF>::type* __restrict__ dYx,
           typename Elem<BF>::type* __restrict__ dYc, float* __restrict__ colsum_part,
-          Plan p, int need_dx, int need_dc) {
-  __shared__ float tile[32][33];
-  const int tid = threadIdx.x;
-  const int bb = blockIdx.x, ob = blockIdx.y;
-  const int o0 = ob * 32;
-  const int64_t row_end = p.B32 > p.Bc ? p.B32 : p.Bc;
-  float cs = 0.0f;
-  for (int sub = 0; sub < kPrepRows / 32; ++sub) {
-    const int64_t b0 = (int64_t)bb * kPrepRows + sub * 32;
-    if (b0 >= row_end) break;
-    for (int idx = tid; idx < 1024; idx += 256) {
-      const int r = idx >> 5, c = idx & 31;
-      const int64_t b = b0 + r;
-      const int o = o0 + c;
-      tile[r][c] = (b < p.B && o < p.O) ? dy[b * p.O + o] : 0.0f;
-    }
-    __syncthreads();
-    if (tid < 32) {
-      for (int r = 0; r < 32; ++r) cs += tile[r][tid];
-    }
-    if (tid < 128) {
-      if (need_dx && b0 < p.B32) {
-        const int kbl = tid >> 6, lane = tid & 63;
-        const int r = lane & 31, g = lane >> 5;
-        float v[8];
+          Plan p, int need_dx, int need_dc, int nob, int nbb) {
+  const int lane = threadIdx.x & 63;
+  const int w = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (w >= nob * nbb) return;
+  const int ob = w % nob, bb = w / nob;
+  const int g = lane >> 5, c = lane & 31;
+  const int64_t r0 = (int64_t)bb * kPrepRows;
+  if (need_dx) {
+    for (int mbl = 0; mbl < kPrepRows / 32; ++mbl) {
+      const int64_t b0 = r0 + mbl * 32;
+      if (b0 >= p.B32) break;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = tile[r][16 * kbl + 8 * g + j];
+      for (int kbl = 0; kbl < 2; ++kbl) {
+        float v[8];
+        load_row8(dy, b0 + c, ob * 32 + 16 * kbl + 8 * g, p, v);
         store_frag<BF>(dYx + ((size_t)(b0 / 32) * p.KBx + ob * 2 + kbl) * kFragElems, lane, v);
       }
-    } else {
-      if (need_dc && ob < p.NBf && b0 < p.Bc) {
-        const int t2 = tid - 128;
-        const int kbl = t2 >> 6, lane = t2 & 63;
-        const int c = lane & 31, g = lane >> 5;
-        float v[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = tile[16 * kbl + 8 * g + j][c];
-        store_frag<BF>(dYc + ((size_t)ob * p.KBc + b0 / 16 + kbl) * kFragElems, lane, v);
-      }
     }
-    __syncthreads();
   }
-  if (need_dc && tid < 32 && o0 + tid < p.O32 && bb < p.NBB)
-    colsum_part[(size_t)bb * p.O32 + o0 + tid] = cs;
+  if (need_dc && ob < p.NBf) {
+    const int o = ob * 32 + c;
+    const bool ocol = o < p.O;
+    float cs = 0.0f;
+    for (int kbl = 0; kbl < kPrepRows / 16; ++kbl) {
+      const int64_t b0 = r0 + kbl * 16;
+      if (b0 >= p.Bc) break;
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int64_t b = b0 + 8 * g + j;
+        v[j] = (ocol && b < p.B) ? dy[b * p.O + o] : 0.0f;
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) cs += v[j];
+      store_frag<BF>(dYc + ((size_t)ob * p.KBc + b0 / 16) * kFragElems, lane, v);
+    }
+    // rows of lane halves interleave in blocks of 8; add the halves in a fixed order
+    const float other = __shfl_xor(cs, 32);
+    if (g == 0 && bb < p.NBB) colsum_part[(size_t)bb * p.O32 + o] = cs + other;
+  }
 }
 
 // dC[i, o, d] (=|+=) for d = 0: sum_b dy[b, o] (from the colsum partials);
 // for d >= 1: sum over the S split partials part[s][d-1][i][o].
 // One block per (16 inputs, 64 outputs); the tile is transposed through LDS
 // so the write of dC is one contiguous run of 64*D values per input.
+template <int P>
 __global__ void __launch_bounds__(256)
 k_dc_finalize(const float* __restrict__ part, int S, const float* __restrict__ colsum_part,
               float* __restrict__ dC, int accumulate, Plan p) {
-  __shared__ float tile[16 * 64 * 17];
-  __shared__ float cs[64];
+  __shared__ float tile[16 * 64 * (P + 1)];
+  __shared__ float csq[4][64];
   const int tid = threadIdx.x;
   const int i0 = blockIdx.x * 16, o0 = blockIdx.y * 64;
   const int D = p.D;
-  if (tid < 64) {
-    const int o = o0 + tid;
+  const int ol = tid & 63, q = tid >> 6;
+  const int o = o0 + ol;
+  {  // column sums: 4 interleaved partial sums per column, then a fixed-order add
     float s = 0.0f;
     if (o < p.O)
-      for (int bb = 0; bb < p.NBB; ++bb) s += colsum_part[(size_t)bb * p.O32 + o];
-    cs[tid] = s;
+      for (int bb = q; bb < p.NBB; bb += 4) s += colsum_part[(size_t)bb * p.O32 + o];
+    csq[q][ol] = s;
   }
-  const int nval = 16 * p.deg * 64;
-  for (int idx = tid; idx < nval; idx += 256) {
-    const int il = idx / (p.deg * 64);
-    const int rem = idx - il * p.deg * 64;
-    const int e = rem >> 6, ol = rem & 63;
-    const int i = i0 + il, o = o0 + ol;
-    float v = 0.0f;
-    if (i < p.I && o < p.O) {
-      for (int s = 0; s < S; ++s)
-        v += part[(((size_t)s * p.P + e) * p.I32 + i) * p.O32 + o];
+  for (int il = 0; il < 16; ++il) {
+    const int i = i0 + il;
+    for (int e = q; e < p.deg; e += 4) {
+      float v = 0.0f;
+      if (i < p.I && o < p.O) {
+        const float* src = part + ((size_t)e * p.I32 + i) * p.O32 + o;
+        const size_t sstride = (size_t)p.P * p.I32 * p.O32;
+        for (int s = 0; s < S; ++s) v += src[s * sstride];
+      }
+      tile[(il * 64 + ol) * D + e + 1] = v;
     }
-    tile[(il * 64 + ol) * D + e + 1] = v;
   }
   __syncthreads();
-  for (int idx = tid; idx < 16 * 64; idx += 256) tile[idx * D] = cs[idx & 63];
+  for (int idx = tid; idx < 16 * 64; idx += 256) {
+    const int c = idx & 63;
+    tile[idx * D] = ((csq[0][c] + csq[1][c]) + csq[2][c]) + csq[3][c];
+  }
   __syncthreads();
   const int ocount = (p.O - o0) < 64 ? (p.O - o0) : 64;
   const int nrow = ocount * D;
@@ -339,22 +368,28 @@ void launch_pack(const void* C, bool c_bf16, void* packed, const Plan& p, hipStr
 void launch_prep_dy(const float* dy, void* dYx, void* dYc, float* colsum_part, const Plan& p,
                     bool need_dx, bool need_dc, hipStream_t s) {
   const int64_t row_end = p.B32 > p.Bc ? p.B32 : p.Bc;
-  dim3 grid((unsigned)ceil_div(row_end, kPrepRows), p.O64 / 32);
+  const int nob = p.O64 / 32;
+  const int nbb = (int)ceil_div(row_end, kPrepRows);
+  dim3 grid((unsigned)ceil_div((int64_t)nob * nbb, 4));
   if (p.esz == 2)
     hipLaunchKernelGGL((k_prep_dy<true>), grid, dim3(256), 0, s, dy,
                        reinterpret_cast<uint16_t*>(dYx), reinterpret_cast<uint16_t*>(dYc),
-                       colsum_part, p, (int)need_dx, (int)need_dc);
+                       colsum_part, p, (int)need_dx, (int)need_dc, nob, nbb);
   else
     hipLaunchKernelGGL((k_prep_dy<false>), grid, dim3(256), 0, s, dy,
                        reinterpret_cast<float*>(dYx), reinterpret_cast<float*>(dYc),
-                       colsum_part, p, (int)need_dx, (int)need_dc);
+                       colsum_part, p, (int)need_dx, (int)need_dc, nob, nbb);
 }
 
 void launch_dc_finalize(const float* part, int S, const float* colsum_part, float* dC,
                         bool accumulate, const Plan& p, hipStream_t s) {
   dim3 grid((unsigned)ceil_div(p.I, 16), (unsigned)ceil_div(p.O, 64));
-  hipLaunchKernelGGL(k_dc_finalize, grid, dim3(256), 0, s, part, S, colsum_part, dC,
-                     (int)accumulate, p);
+  switch (p.P) {
+    case 2: hipLaunchKernelGGL((k_dc_finalize<2>), grid, dim3(256), 0, s, part, S, colsum_part, dC, (int)accumulate, p); break;
+    case 4: hipLaunchKernelGGL((k_dc_finalize<4>), grid, dim3(256), 0, s, part, S, colsum_part, dC, (int)accumulate, p); break;
+    case 8: hipLaunchKernelGGL((k_dc_finalize<8>), grid, dim3(256), 0, s, part, S, colsum_part, dC, (int)accumulate, p); break;
+    default: hipLaunchKernelGGL((k_dc_finalize<16>), grid, dim3(256), 0, s, part, S, colsum_part, dC, (int)accumulate, p); break;
+  }
 }
 
 void launch_sgd(float* p, const float* g, int64_t n, float lr, float wd, hipStream_t s) {

@@ -88,8 +88,21 @@ k_fwd(const float* __restrict__ tc, const typename Elem<BF>::type* __restrict__ 
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[mi][ni][v] = 0.0f;
 
+  // tanh values of the next super-group, prefetched one stage ahead
+  f32x4_t tnext[NM][G::LANE_T / 4];
+  auto tload = [&](int sg) {
+#pragma unroll
+    for (int mi = 0; mi < NM; ++mi) {
+      const f32x4_t* src = reinterpret_cast<const f32x4_t*>(trow[mi] + (size_t)sg * G::SGI);
+#pragma unroll
+      for (int q = 0; q < G::LANE_T / 4; ++q)
+        tnext[mi][q] = rvalid[mi] ? src[q] : f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+
   if (sg0 < sg1) {
     gload(sg0);
+    tload(sg0);
     lstore(0);
   }
   __syncthreads();
@@ -97,22 +110,24 @@ k_fwd(const float* __restrict__ tc, const typename Elem<BF>::type* __restrict__ 
   for (int sg = sg0; sg < sg1; ++sg) {
     const int buf = (sg - sg0) & 1;
     const bool more = sg + 1 < sg1;
-    if (more) gload(sg + 1);
+    f32x4_t tcur[NM][G::LANE_T / 4];
+#pragma unroll
+    for (int mi = 0; mi < NM; ++mi)
+#pragma unroll
+      for (int q = 0; q < G::LANE_T / 4; ++q) tcur[mi][q] = tnext[mi][q];
+    if (more) {
+      gload(sg + 1);
+      tload(sg + 1);
+    }
 
     Frag<BF> af[NM][G::SGK];
 #pragma unroll
     for (int mi = 0; mi < NM; ++mi) {
       float tv[G::LANE_T];
-      if (rvalid[mi]) {
-        const f32x4_t* src = reinterpret_cast<const f32x4_t*>(trow[mi] + (size_t)sg * G::SGI);
 #pragma unroll
-        for (int q = 0; q < G::LANE_T / 4; ++q) {
-          const f32x4_t w = src[q];
-          tv[4 * q + 0] = w[0]; tv[4 * q + 1] = w[1]; tv[4 * q + 2] = w[2]; tv[4 * q + 3] = w[3];
-        }
-      } else {
-#pragma unroll
-        for (int q = 0; q < G::LANE_T; ++q) tv[q] = 0.0f;
+      for (int q = 0; q < G::LANE_T / 4; ++q) {
+        tv[4 * q + 0] = tcur[mi][q][0]; tv[4 * q + 1] = tcur[mi][q][1];
+        tv[4 * q + 2] = tcur[mi][q][2]; tv[4 * q + 3] = tcur[mi][q][3];
       }
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
