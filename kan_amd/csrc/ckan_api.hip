@@ -10,7 +10,7 @@
 #include <string>
 #include <vector>
 
-#include "../../include/chebykan.h"
+#include "chebykan.h"
 #include "ckan_kernels.hpp"
 
 using namespace ckan;

@@ -59,12 +59,39 @@ k_pack(const CT* __restrict__ C, typename Elem<BF>::type* __restrict__ Cf,
   const int RP = 32 * D + 1;
   const int ocount = min(32, p.O - o0);  // may be <= 0 for the Cb zero-fill blocks
   const int nrow = ocount > 0 ? ocount * D : 0;
+  // Each input's run of 32*D values is contiguous in C.  When the run is
+  // 16-byte aligned, every thread issues its float4 loads before any use.
+  const bool vec = sizeof(CT) == 4 && ((size_t)p.O * D) % 4 == 0 && ocount == 32;
+  if (vec) {
+    constexpr int MAXV = (32 * 32 * (P + 1) / 4 + 255) / 256;  // float4 per thread
+    const int nv = 32 * 8 * D;                                   // float4 in the tile
+    f32x4_t buf[MAXV];
+#pragma unroll
+    for (int q = 0; q < MAXV; ++q) {
+      const int v = tid + q * 256;
+      const int il = v / (8 * D), k4 = v - il * (8 * D);
+      const int i = i0 + il;
+      buf[q] = (v < nv && i < p.I)
+          ? *reinterpret_cast<const f32x4_t*>(reinterpret_cast<const float*>(C) + ((size_t)i * p.O + o0) * D + k4 * 4)
+          : f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int q = 0; q < MAXV; ++q) {
+      const int v = tid + q * 256;
+      if (v < nv) {
+        const int il = v / (8 * D), k4 = v - il * (8 * D);
+        float* dst = tile + il * RP + k4 * 4;
+        dst[0] = buf[q][0]; dst[1] = buf[q][1]; dst[2] = buf[q][2]; dst[3] = buf[q][3];
+      }
+    }
+  } else {
 #pragma unroll 4
-  for (int il = 0; il < 32; ++il) {
-    const int i = i0 + il;
-    const CT* src = C + ((size_t)i * p.O + o0) * D;
-    for (int k = tid; k < 32 * D; k += 256)
-      tile[il * RP + k] = (i < p.I && k < nrow) ? to_f32<CT>(src[k]) : 0.0f;
+    for (int il = 0; il < 32; ++il) {
+      const int i = i0 + il;
+      const CT* src = C + ((size_t)i * p.O + o0) * D;
+      for (int k = tid; k < 32 * D; k += 256)
+        tile[il * RP + k] = (i < p.I && k < nrow) ? to_f32<CT>(src[k]) : 0.0f;
+    }
   }
   __syncthreads();
 
@@ -119,6 +146,25 @@ k_pack(const CT* __restrict__ C, typename Elem<BF>::type* __restrict__ Cf,
   }
 }
 
+// out[o] = sum_k part[k][o] for k < nparts (row pitch `pitch`): 4 interleaved
+// partial sums per column keep independent loads in flight; they are added in
+// a fixed order, so the result is deterministic.  Used for the forward bias
+// (sum_i C[i, o, 0] over input blocks) and the dC column sums of dy.
+__global__ void __launch_bounds__(256)
+k_col_reduce(const float* __restrict__ part, int nparts, int pitch, int n, float* __restrict__ out) {
+  __shared__ float q4[4][64];
+  const int ol = threadIdx.x & 63, q = threadIdx.x >> 6;
+  const int o = blockIdx.x * 64 + ol;
+  float s = 0.0f;
+  if (o < n) {
+#pragma unroll 8
+    for (int k = q; k < nparts; k += 4) s += part[(size_t)k * pitch + o];
+  }
+  q4[q][ol] = s;
+  __syncthreads();
+  if (q == 0 && o < n) out[o] = ((q4[0][ol] + q4[1][ol]) + q4[2][ol]) + q4[3][ol];
+}
+
 // 8 consecutive values of row b of dy starting at column o (zero outside B x O).
 __device__ __forceinline__ void load_row8(const float* __restrict__ dy, int64_t b, int o,
                                           const Plan& p, float* v) {
@@ -152,33 +198,41 @@ k_prep_dy(const float* __restrict__ dy, typename Elem<BF>::type* __restrict__ dY
   const int g = lane >> 5, c = lane & 31;
   const int64_t r0 = (int64_t)bb * kPrepRows;
   if (need_dx) {
+    // all loads of the wave's rows first, then the conversions and stores
+    float v[kPrepRows / 32][2][8];
+#pragma unroll
+    for (int mbl = 0; mbl < kPrepRows / 32; ++mbl)
+#pragma unroll
+      for (int kbl = 0; kbl < 2; ++kbl)
+        load_row8(dy, r0 + mbl * 32 + c, ob * 32 + 16 * kbl + 8 * g, p, v[mbl][kbl]);
+#pragma unroll
     for (int mbl = 0; mbl < kPrepRows / 32; ++mbl) {
       const int64_t b0 = r0 + mbl * 32;
-      if (b0 >= p.B32) break;
+      if (b0 < p.B32) {
 #pragma unroll
-      for (int kbl = 0; kbl < 2; ++kbl) {
-        float v[8];
-        load_row8(dy, b0 + c, ob * 32 + 16 * kbl + 8 * g, p, v);
-        store_frag<BF>(dYx + ((size_t)(b0 / 32) * p.KBx + ob * 2 + kbl) * kFragElems, lane, v);
+        for (int kbl = 0; kbl < 2; ++kbl)
+          store_frag<BF>(dYx + ((size_t)(b0 / 32) * p.KBx + ob * 2 + kbl) * kFragElems, lane, v[mbl][kbl]);
       }
     }
   }
   if (need_dc && ob < p.NBf) {
     const int o = ob * 32 + c;
     const bool ocol = o < p.O;
-    float cs = 0.0f;
-    for (int kbl = 0; kbl < kPrepRows / 16; ++kbl) {
-      const int64_t b0 = r0 + kbl * 16;
-      if (b0 >= p.Bc) break;
-      float v[8];
+    float v[kPrepRows / 16][8];
+#pragma unroll
+    for (int kbl = 0; kbl < kPrepRows / 16; ++kbl)
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const int64_t b = b0 + 8 * g + j;
-        v[j] = (ocol && b < p.B) ? dy[b * p.O + o] : 0.0f;
+        const int64_t b = r0 + kbl * 16 + 8 * g + j;
+        v[kbl][j] = (ocol && b < p.B) ? dy[b * p.O + o] : 0.0f;
       }
+    float cs = 0.0f;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) cs += v[j];
-      store_frag<BF>(dYc + ((size_t)ob * p.KBc + b0 / 16) * kFragElems, lane, v);
+    for (int kbl = 0; kbl < kPrepRows / 16; ++kbl) {
+      const int64_t b0 = r0 + kbl * 16;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) cs += v[kbl][j];
+      if (b0 < p.Bc) store_frag<BF>(dYc + ((size_t)ob * p.KBc + b0 / 16) * kFragElems, lane, v[kbl]);
     }
     // rows of lane halves interleave in blocks of 8; add the halves in a fixed order
     const float other = __shfl_xor(cs, 32);
@@ -192,38 +246,33 @@ k_prep_dy(const float* __restrict__ dy, typename Elem<BF>::type* __restrict__ dY
 // so the write of dC is one contiguous run of 64*D values per input.
 template <int P>
 __global__ void __launch_bounds__(256)
-k_dc_finalize(const float* __restrict__ part, int S, const float* __restrict__ colsum_part,
+k_dc_finalize(const float* __restrict__ part, int S, const float* __restrict__ colsum,
               float* __restrict__ dC, int accumulate, Plan p) {
   __shared__ float tile[16 * 64 * (P + 1)];
-  __shared__ float csq[4][64];
+  __shared__ float csq[1][64];
   const int tid = threadIdx.x;
   const int i0 = blockIdx.x * 16, o0 = blockIdx.y * 64;
   const int D = p.D;
   const int ol = tid & 63, q = tid >> 6;
   const int o = o0 + ol;
-  {  // column sums: 4 interleaved partial sums per column, then a fixed-order add
-    float s = 0.0f;
-    if (o < p.O)
-      for (int bb = q; bb < p.NBB; bb += 4) s += colsum_part[(size_t)bb * p.O32 + o];
-    csq[q][ol] = s;
-  }
+  if (tid < 64) csq[0][ol] = (o < p.O) ? colsum[o] : 0.0f;
+  const size_t sstride = (size_t)p.P * p.I32 * p.O32;
+#pragma unroll 4
   for (int il = 0; il < 16; ++il) {
     const int i = i0 + il;
-    for (int e = q; e < p.deg; e += 4) {
+    const bool ok = i < p.I && o < p.O;
+#pragma unroll
+    for (int e = q; e < P; e += 4) {
       float v = 0.0f;
-      if (i < p.I && o < p.O) {
+      if (ok && e < p.deg) {
         const float* src = part + ((size_t)e * p.I32 + i) * p.O32 + o;
-        const size_t sstride = (size_t)p.P * p.I32 * p.O32;
         for (int s = 0; s < S; ++s) v += src[s * sstride];
       }
-      tile[(il * 64 + ol) * D + e + 1] = v;
+      if (e < p.deg) tile[(il * 64 + ol) * D + e + 1] = v;
     }
   }
   __syncthreads();
-  for (int idx = tid; idx < 16 * 64; idx += 256) {
-    const int c = idx & 63;
-    tile[idx * D] = ((csq[0][c] + csq[1][c]) + csq[2][c]) + csq[3][c];
-  }
+  for (int idx = tid; idx < 16 * 64; idx += 256) tile[idx * D] = csq[0][idx & 63];
   __syncthreads();
   const int ocount = (p.O - o0) < 64 ? (p.O - o0) : 64;
   const int nrow = ocount * D;
@@ -357,6 +406,15 @@ static void launch_pack_t(const void* C, bool c_bf16, void* packed, const Plan& 
 
 void launch_pack(const void* C, bool c_bf16, void* packed, const Plan& p, hipStream_t s) {
   const bool bf = p.esz == 2;
+  char* base = reinterpret_cast<char*>(packed);
+  struct Reduce {
+    char* base; const Plan& p; hipStream_t s;
+    ~Reduce() {
+      hipLaunchKernelGGL(k_col_reduce, dim3((unsigned)ceil_div(p.O32, 64)), dim3(256), 0, s,
+                         reinterpret_cast<const float*>(base + packed_bias_offset(p)), p.NIB,
+                         p.O32, p.O32, reinterpret_cast<float*>(base + packed_biasf_offset(p)));
+    }
+  } reduce{base, p, s};
   switch (p.P) {
     case 2: bf ? launch_pack_t<2, true>(C, c_bf16, packed, p, s) : launch_pack_t<2, false>(C, c_bf16, packed, p, s); break;
     case 4: bf ? launch_pack_t<4, true>(C, c_bf16, packed, p, s) : launch_pack_t<4, false>(C, c_bf16, packed, p, s); break;
@@ -381,14 +439,19 @@ void launch_prep_dy(const float* dy, void* dYx, void* dYc, float* colsum_part, c
                        colsum_part, p, (int)need_dx, (int)need_dc, nob, nbb);
 }
 
-void launch_dc_finalize(const float* part, int S, const float* colsum_part, float* dC,
+void launch_dc_finalize(const float* part, int S, float* colsum_part, float* dC,
                         bool accumulate, const Plan& p, hipStream_t s) {
+  // column sums of dy: reduce the per-row-block partials in place into row 0
+  float* colsum = colsum_part + (size_t)p.NBB * p.O32;
+  hipLaunchKernelGGL(k_col_reduce, dim3((unsigned)ceil_div(p.O32, 64)), dim3(256), 0, s,
+                     colsum_part, p.NBB, p.O32, p.O32, colsum);
+  const float* colsum_part_r = colsum;
   dim3 grid((unsigned)ceil_div(p.I, 16), (unsigned)ceil_div(p.O, 64));
   switch (p.P) {
-    case 2: hipLaunchKernelGGL((k_dc_finalize<2>), grid, dim3(256), 0, s, part, S, colsum_part, dC, (int)accumulate, p); break;
-    case 4: hipLaunchKernelGGL((k_dc_finalize<4>), grid, dim3(256), 0, s, part, S, colsum_part, dC, (int)accumulate, p); break;
-    case 8: hipLaunchKernelGGL((k_dc_finalize<8>), grid, dim3(256), 0, s, part, S, colsum_part, dC, (int)accumulate, p); break;
-    default: hipLaunchKernelGGL((k_dc_finalize<16>), grid, dim3(256), 0, s, part, S, colsum_part, dC, (int)accumulate, p); break;
+    case 2: hipLaunchKernelGGL((k_dc_finalize<2>), grid, dim3(256), 0, s, part, S, colsum_part_r, dC, (int)accumulate, p); break;
+    case 4: hipLaunchKernelGGL((k_dc_finalize<4>), grid, dim3(256), 0, s, part, S, colsum_part_r, dC, (int)accumulate, p); break;
+    case 8: hipLaunchKernelGGL((k_dc_finalize<8>), grid, dim3(256), 0, s, part, S, colsum_part_r, dC, (int)accumulate, p); break;
+    default: hipLaunchKernelGGL((k_dc_finalize<16>), grid, dim3(256), 0, s, part, S, colsum_part_r, dC, (int)accumulate, p); break;
   }
 }
 

@@ -57,8 +57,8 @@ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 constexpr int kDcStageRows = 64;
 // Output columns per k-block stage of the dX reduction.
 constexpr int kDxStageCols = 64;
-// Rows covered by one prep_dy block (colsum partial granularity).
-constexpr int kPrepRows = 256;
+// Rows covered by one prep_dy wave (colsum partial granularity).
+constexpr int kPrepRows = 64;
 
 struct Plan {
   int64_t B;       // rows
@@ -182,6 +182,36 @@ __device__ __forceinline__ void mma(f32x16_t& acc, const Frag<false>& a, const F
   acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.hi[1], b.hi[1], acc, 0, 0, 0);
   acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.hi[2], b.hi[2], acc, 0, 0, 0);
   acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.hi[3], b.hi[3], acc, 0, 0, 0);
+}
+
+// ---- pipeline primitives ----------------------------------------------------
+// Wait until at most N vector-memory operations of this wave are in flight
+// (gfx9 s_waitcnt encoding: vmcnt[3:0] | vmcnt[5:4] << 14; expcnt and lgkmcnt
+// left at their maxima so only vmcnt is waited on).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit field");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+// Wait until at most N LDS/scalar-memory operations are in flight.
+template <int N>
+__device__ __forceinline__ void wait_lgkmcnt() {
+  static_assert(N >= 0 && N < 16, "lgkmcnt is a 4-bit field");
+  __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4) | (N << 8));
+}
+// Workgroup execution barrier without the memory fence of __syncthreads():
+// in-flight prefetches stay in flight.  The empty asm keeps the compiler
+// from moving LDS accesses across it.
+__device__ __forceinline__ void block_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+// One 16-byte-per-lane global -> LDS copy (global_load_lds_dwordx4): lane l's
+// 16 bytes from `src` land at lds_base + 16 * l.  `lds_base` must be
+// wave-uniform.
+__device__ __forceinline__ void dma16(const void* src, void* lds_base) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds_base, 16, 0, 0);
 }
 
 // Row of accumulator value v (0..15) for lane half g in a 32x32 MFMA result;

@@ -27,7 +27,7 @@ namespace ckan {
 template <int P, bool BF, int NM, int NN, int WGM, int WGN>
 __global__ void __launch_bounds__(256)
 k_fwd(const float* __restrict__ tc, const typename Elem<BF>::type* __restrict__ Cf,
-      const float* __restrict__ bias_part, float* __restrict__ y, float* __restrict__ part,
+      const float* __restrict__ bias_f, float* __restrict__ y, float* __restrict__ part,
       unsigned* __restrict__ counters, Plan p, int sg_per_split) {
   typedef typename Elem<BF>::type E;
   typedef FwdGroup<P> G;
@@ -159,8 +159,7 @@ k_fwd(const float* __restrict__ tc, const typename Elem<BF>::type* __restrict__ 
     for (int ni = 0; ni < NN; ++ni) {
       const int o = (nb0 + wn * NN + ni) * 32 + (lane & 31);
       if (o >= p.O) continue;
-      float bias = 0.0f;
-      for (int ib = 0; ib < p.NIB; ++ib) bias += bias_part[(size_t)ib * p.O32 + o];
+      const float bias = bias_f[o];
 #pragma unroll
       for (int mi = 0; mi < NM; ++mi) {
         const int64_t r0 = m_blk + (wm * NM + mi) * 32;
@@ -208,8 +207,256 @@ k_fwd(const float* __restrict__ tc, const typename Elem<BF>::type* __restrict__ 
     const int64_t r = m_blk + rl;
     const int o = nb0 * 32 + cl;
     if (r >= p.B || o >= p.O) continue;
-    float s = 0.0f;
-    for (int ib = 0; ib < p.NIB; ++ib) s += bias_part[(size_t)ib * p.O32 + o];
+    float s = bias_f[o];
+    for (unsigned z = 0; z < gridDim.z; ++z) s += part[((size_t)z * p.B32 + r) * p.O32 + o];
+    y[r * p.O + o] = s;
+  }
+  if (tid == 0) counters[tile_id] = 0u;
+}
+
+// ---------------------------------------------------------------------------
+// Forward, large-batch pipeline.  Block tile 256 rows x 128 outputs, 8 waves
+// (2 per SIMD): waves 0-3 ("half 0") take the even super-groups of the
+// reduction and waves 4-7 the odd ones, each half covering the whole tile
+// (4 waves along rows, 2 x 4 fragments each); the two partial tiles are summed
+// through LDS at the end.  Two waves per SIMD let one wave's MFMAs run while
+// the other generates its basis fragments or waits on LDS, within the
+// 256-register budget, without global split-K partials.
+//
+// Each super-group stage (coefficient fragments for 128 outputs and the
+// 256 x SGI tanh tile) is copied global -> LDS by global_load_lds_dwordx4
+// into a ring of NPB stage pairs, issued one pair-iteration ahead; a pair
+// costs one barrier.  Out-of-range rows and output fragments read a clamped
+// in-bounds address; their results are never stored.
+// ---------------------------------------------------------------------------
+template <int P, bool BF>
+struct FwdPipe {
+  typedef typename Elem<BF>::type E;
+  typedef FwdGroup<P> G;
+  static constexpr int NM = 2, NN = 4, BM = 256, BNF = 4, THREADS = 512;
+  static constexpr int B_BYTES = BNF * G::SGK * kFragElems * (int)sizeof(E);
+  static constexpr int T_BYTES = BM * G::SGI * 4;
+  static constexpr int STAGE_BYTES = B_BYTES + T_BYTES;
+  static constexpr int PAIR_BYTES = 2 * STAGE_BYTES;
+  static constexpr int RED_BYTES = BM * BNF * 32 * 4;  // one partial tile, fp32
+  static constexpr int NPB_FIT = (160 * 1024) / PAIR_BYTES;
+  static constexpr int NPB = NPB_FIT > 3 ? 3 : NPB_FIT;
+  static constexpr int RING_BYTES = NPB * PAIR_BYTES;
+  static constexpr int LDS_BYTES = RING_BYTES > RED_BYTES + 16 ? RING_BYTES : RED_BYTES + 16;
+  // dma16 ops per thread per stage (each op moves 512 x 16 bytes per block)
+  static constexpr int B_OPS = B_BYTES / (16 * THREADS);
+  static constexpr int T_OPS = T_BYTES / (16 * THREADS);
+  static constexpr int OPS = 2 * (B_OPS + T_OPS);  // per pair
+  static constexpr bool kOk = NPB >= 2 && LDS_BYTES <= 160 * 1024 && RED_BYTES + 16 <= LDS_BYTES &&
+                              B_BYTES % (16 * THREADS) == 0 && T_BYTES % (16 * THREADS) == 0;
+};
+
+template <int P, bool BF>
+__global__ void __launch_bounds__(512)
+k_fwd_pipe(const float* __restrict__ tc, const typename Elem<BF>::type* __restrict__ Cf,
+           const float* __restrict__ bias_f, float* __restrict__ y, float* __restrict__ part,
+           unsigned* __restrict__ counters, Plan p, int sg_per_split) {
+  typedef FwdPipe<P, BF> K;
+  typedef typename K::E E;
+  typedef typename K::G G;
+  constexpr int NM = K::NM, NN = K::NN, BM = K::BM, BNF = K::BNF, NPB = K::NPB;
+  constexpr int TH = K::THREADS;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int half = wave >> 2, wq = wave & 3;
+  const int g = lane >> 5;
+  const int64_t m_blk = (int64_t)blockIdx.x * BM;
+  const int nb0 = blockIdx.y * BNF;
+  const int nsg = p.I_sg / G::SGI;
+  const int sg0 = blockIdx.z * sg_per_split;
+  const int sg1 = min(nsg, sg0 + sg_per_split);
+  const int npair = (sg1 - sg0 + 1) / 2;
+
+  // stage-invariant DMA source offsets (bytes); chunk c = (q*8 + wave)*64 + lane
+  constexpr int CPF = kFragElems * (int)sizeof(E) / 16;  // 16-byte chunks per fragment
+  const char* cf = reinterpret_cast<const char*>(Cf);
+  size_t boff[K::B_OPS];
+#pragma unroll
+  for (int q = 0; q < K::B_OPS; ++q) {
+    const int c = (q * 8 + wave) * 64 + lane;
+    const int nbl = c / (G::SGK * CPF), off = c - nbl * (G::SGK * CPF);
+    const int nb = min(nb0 + nbl, p.NBf - 1);
+    boff[q] = (size_t)nb * p.KB * kFragElems * sizeof(E) + (size_t)off * 16;
+  }
+  const char* tcb = reinterpret_cast<const char*>(tc);
+  size_t toff[K::T_OPS];
+#pragma unroll
+  for (int q = 0; q < K::T_OPS; ++q) {
+    const int c = (q * 8 + wave) * 64 + lane;
+    const int rl = c / (G::SGI / 4), part4 = c - rl * (G::SGI / 4);
+    int64_t r = m_blk + rl;
+    if (r >= p.B) r = p.B - 1;
+    toff[q] = ((size_t)r * p.I_sg + part4 * 4) * 4;
+  }
+  const size_t b_stride = (size_t)G::SGK * kFragElems * sizeof(E);
+  const size_t t_stride = (size_t)G::SGI * 4;
+
+  // stage `sg` (if it exists) into ring slot `slot` (0 .. 2*NPB-1)
+  auto issue = [&](int sg, int slot) {
+    if (sg >= sg1) return;
+    char* base = smem + slot * K::STAGE_BYTES;
+#pragma unroll
+    for (int q = 0; q < K::B_OPS; ++q)
+      dma16(cf + boff[q] + (size_t)sg * b_stride, base + (q * 8 + wave) * 1024);
+#pragma unroll
+    for (int q = 0; q < K::T_OPS; ++q)
+      dma16(tcb + toff[q] + (size_t)sg * t_stride, base + K::B_BYTES + (q * 8 + wave) * 1024);
+  };
+  auto issue_pair = [&](int j) {
+    const int slot = (j % NPB) * 2;
+    issue(sg0 + 2 * j, slot);
+    issue(sg0 + 2 * j + 1, slot + 1);
+  };
+
+  f32x16_t acc[NM][NN];
+#pragma unroll
+  for (int mi = 0; mi < NM; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < NN; ++ni)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[mi][ni][v] = 0.0f;
+
+  auto compute = [&](int slot) {
+    const char* base = smem + slot * K::STAGE_BYTES;
+    const float* tl = reinterpret_cast<const float*>(base + K::B_BYTES);
+    const E* bl = reinterpret_cast<const E*>(base);
+    float tv[NM][G::LANE_T];
+#pragma unroll
+    for (int mi = 0; mi < NM; ++mi) {
+      const int rl = (wq * NM + mi) * 32 + (lane & 31);
+      const f32x4_t* src = reinterpret_cast<const f32x4_t*>(tl + rl * G::SGI + g * G::LANE_T);
+#pragma unroll
+      for (int q = 0; q < G::LANE_T / 4; ++q) {
+        const f32x4_t w = src[q];
+        tv[mi][4 * q + 0] = w[0]; tv[mi][4 * q + 1] = w[1];
+        tv[mi][4 * q + 2] = w[2]; tv[mi][4 * q + 3] = w[3];
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      Frag<BF> af[NM][G::KBG];
+#pragma unroll
+      for (int mi = 0; mi < NM; ++mi) {
+        float vals[8 * G::KBG];
+#pragma unroll
+        for (int u = 0; u < G::IPG / 2; ++u) cheb_T<P>(tv[mi][s * (G::IPG / 2) + u], vals + u * P);
+#pragma unroll
+        for (int h = 0; h < G::KBG; ++h) af[mi][h] = make_frag<BF>(vals + 8 * h);
+      }
+#pragma unroll
+      for (int h = 0; h < G::KBG; ++h) {
+        const int kbl = s * G::KBG + h;
+#pragma unroll
+        for (int ni = 0; ni < NN; ++ni) {
+          const Frag<BF> bfr = load_frag<BF>(bl + (ni * G::SGK + kbl) * kFragElems, lane);
+#pragma unroll
+          for (int mi = 0; mi < NM; ++mi) mma(acc[mi][ni], af[mi][h], bfr);
+        }
+      }
+    }
+  };
+
+#pragma unroll
+  for (int j = 0; j < NPB - 1; ++j)
+    if (j < npair) issue_pair(j);
+  for (int j = 0; j < npair; ++j) {
+    // pair j has landed once at most (pairs issued after it) * OPS remain;
+    // only the last pair can be a single stage, so near the end wait for all
+    if (j + NPB - 2 < npair - 1) wait_vmcnt<K::OPS * (NPB - 2)>();
+    else wait_vmcnt<0>();
+    block_barrier();
+    if (j + NPB - 1 < npair) issue_pair(j + NPB - 1);
+    if (sg0 + 2 * j + half < sg1) compute((j % NPB) * 2 + half);
+  }
+
+  // sum the two halves' tiles through LDS (the ring is free once all waves
+  // pass the barrier); every barrier below is reached by all 8 waves
+  wait_lgkmcnt<0>();
+  block_barrier();
+  float* red = reinterpret_cast<float*>(smem);
+  if (half == 1) {
+#pragma unroll
+    for (int mi = 0; mi < NM; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < NN; ++ni)
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          red[(((wq * NM + mi) * NN + ni) * 16 + v) * 64 + lane] = acc[mi][ni][v];
+  }
+  __syncthreads();
+  if (half == 0) {
+#pragma unroll
+    for (int mi = 0; mi < NM; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < NN; ++ni)
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          acc[mi][ni][v] += red[(((wq * NM + mi) * NN + ni) * 16 + v) * 64 + lane];
+  }
+
+  const bool split = gridDim.z > 1;
+  if (!split) {
+    if (half != 0) return;
+#pragma unroll
+    for (int ni = 0; ni < NN; ++ni) {
+      const int o = (nb0 + ni) * 32 + (lane & 31);
+      if (o >= p.O) continue;
+      const float bias = bias_f[o];
+#pragma unroll
+      for (int mi = 0; mi < NM; ++mi) {
+        const int64_t r0 = m_blk + (wq * NM + mi) * 32;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int64_t r = r0 + acc_row(v, g);
+          if (r < p.B) y[r * p.O + o] = acc[mi][ni][v] + bias;
+        }
+      }
+    }
+    return;
+  }
+
+  if (half == 0) {
+#pragma unroll
+    for (int ni = 0; ni < NN; ++ni) {
+      const int nb = nb0 + ni;
+      if (nb >= p.NBf) continue;
+      const int o = nb * 32 + (lane & 31);
+#pragma unroll
+      for (int mi = 0; mi < NM; ++mi) {
+        const int64_t r0 = m_blk + (wq * NM + mi) * 32;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int64_t r = r0 + acc_row(v, g);
+          if (r < p.B32) part[((size_t)blockIdx.z * p.B32 + r) * p.O32 + o] = acc[mi][ni][v];
+        }
+      }
+    }
+  }
+  __threadfence();
+  __syncthreads();
+  // the ticket flag lives past the reduction tile in the (now idle) ring
+  unsigned* s_last = reinterpret_cast<unsigned*>(smem + K::RED_BYTES);
+  const unsigned tile_id = blockIdx.y * gridDim.x + blockIdx.x;
+  if (tid == 0) {
+    const unsigned prev = atomicAdd(&counters[tile_id], 1u);
+    *s_last = (prev == gridDim.z - 1) ? 1u : 0u;
+  }
+  __syncthreads();
+  if (!*s_last) return;
+  __threadfence();
+  constexpr int BN = BNF * 32;
+  for (int idx = tid; idx < BM * BN; idx += TH) {
+    const int rl = idx / BN, cl = idx - rl * BN;
+    const int64_t r = m_blk + rl;
+    const int o = nb0 * 32 + cl;
+    if (r >= p.B || o >= p.O) continue;
+    float s = bias_f[o];
     for (unsigned z = 0; z < gridDim.z; ++z) s += part[((size_t)z * p.B32 + r) * p.O32 + o];
     y[r * p.O + o] = s;
   }
@@ -505,7 +752,7 @@ static void fwd_dispatch(const float* t, const void* packed, float* y, void* ws,
   typedef typename Elem<BF>::type E;
   const E* Cf = reinterpret_cast<const E*>(packed);
   const float* bias =
-      reinterpret_cast<const float*>(reinterpret_cast<const char*>(packed) + packed_bias_offset(p));
+      reinterpret_cast<const float*>(reinterpret_cast<const char*>(packed) + packed_biasf_offset(p));
   unsigned* counters = nullptr;
   float* part = nullptr;
   if (c.splits > 1) {
@@ -523,8 +770,21 @@ static void fwd_dispatch(const float* t, const void* packed, float* y, void* ws,
                          counters, p, c.sg_per_split);
       break;
     default:
-      hipLaunchKernelGGL((k_fwd<P, BF, 2, 4, 4, 1>), grid, dim3(256), 0, s, t, Cf, bias, y, part,
+      if constexpr (FwdPipe<P, BF>::kOk) {
+      typedef FwdPipe<P, BF> K;
+      const size_t lds = (size_t)K::LDS_BYTES;
+      static bool attr_set = false;  // one-time raise of the dynamic LDS limit
+      if (!attr_set) {
+        hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fwd_pipe<P, BF>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        attr_set = true;
+      }
+      hipLaunchKernelGGL((k_fwd_pipe<P, BF>), grid, dim3(K::THREADS), lds, s, t, Cf, bias, y, part,
                          counters, p, c.sg_per_split);
+      } else {
+        hipLaunchKernelGGL((k_fwd<P, BF, 2, 4, 4, 1>), grid, dim3(256), 0, s, t, Cf, bias, y,
+                           part, counters, p, c.sg_per_split);
+      }
       break;
   }
 }
@@ -575,8 +835,8 @@ BwdLayout bwd_layout(const Plan& p, bool need_dx, bool need_dc) {
   if (need_dx) off += align256((size_t)(p.B32 / 32) * p.KBx * kFragElems * p.esz);
   L.dyc_off = off;
   if (need_dc) off += align256((size_t)p.NBf * p.KBc * kFragElems * p.esz);
-  L.colsum_off = off;
-  if (need_dc) off += align256((size_t)p.NBB * p.O32 * sizeof(float));
+  L.colsum_off = off;  // NBB partial rows + the reduced row
+  if (need_dc) off += align256((size_t)(p.NBB + 1) * p.O32 * sizeof(float));
   L.part_off = off;
   L.dc_splits = 1;
   L.dc_st_per_split = 0;

@@ -14,8 +14,12 @@ inline size_t packed_cb_elems(const Plan& p) { return (size_t)p.NIB * p.P * p.KB
 inline size_t packed_bias_offset(const Plan& p) {
   return align256((packed_cf_elems(p) + packed_cb_elems(p)) * p.esz);
 }
-inline size_t packed_bytes(const Plan& p) {
+// final per-output bias sum_i C[i, o, 0], reduced from the partials
+inline size_t packed_biasf_offset(const Plan& p) {
   return align256(packed_bias_offset(p) + (size_t)p.NIB * p.O32 * sizeof(float));
+}
+inline size_t packed_bytes(const Plan& p) {
+  return align256(packed_biasf_offset(p) + (size_t)p.O32 * sizeof(float));
 }
 
 // ---- forward: tile configuration and split-K -------------------------------
@@ -48,7 +52,7 @@ void launch_tanh(const float* x, float* t, const Plan& p, hipStream_t s);
 void launch_pack(const void* C, bool c_bf16, void* packed, const Plan& p, hipStream_t s);
 void launch_prep_dy(const float* dy, void* dYx, void* dYc, float* colsum_part, const Plan& p,
                     bool need_dx, bool need_dc, hipStream_t s);
-void launch_dc_finalize(const float* part, int S, const float* colsum_part, float* dC,
+void launch_dc_finalize(const float* part, int S, float* colsum_part, float* dC,
                         bool accumulate, const Plan& p, hipStream_t s);
 void launch_fwd_gemm(const float* t, const void* packed, float* y, void* ws, const Plan& p,
                      const FwdChoice& c, hipStream_t s);
