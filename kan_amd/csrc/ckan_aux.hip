@@ -190,7 +190,7 @@ template <bool BF>
 __global__ void __launch_bounds__(256)
 k_prep_dy(const float* __restrict__ dy, typename Elem<BF>::type* __restrict__ dYx,
           typename Elem<BF>::type* __restrict__ dYc, float* __restrict__ colsum_part,
-          Plan p, int need_dx, int need_dc, int nob, int nbb) {
+          Plan p, int need_dx, int need_dc, int nob, int nbb, int64_t dx_rows) {
   const int lane = threadIdx.x & 63;
   const int w = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (w >= nob * nbb) return;
@@ -208,7 +208,7 @@ k_prep_dy(const float* __restrict__ dy, typename Elem<BF>::type* __restrict__ dY
 #pragma unroll
     for (int mbl = 0; mbl < kPrepRows / 32; ++mbl) {
       const int64_t b0 = r0 + mbl * 32;
-      if (b0 < p.B32) {
+      if (b0 < dx_rows) {
 #pragma unroll
         for (int kbl = 0; kbl < 2; ++kbl)
           store_frag<BF>(dYx + ((size_t)(b0 / 32) * p.KBx + ob * 2 + kbl) * kFragElems, lane, v[mbl][kbl]);
@@ -425,18 +425,20 @@ void launch_pack(const void* C, bool c_bf16, void* packed, const Plan& p, hipStr
 
 void launch_prep_dy(const float* dy, void* dYx, void* dYc, float* colsum_part, const Plan& p,
                     bool need_dx, bool need_dc, hipStream_t s) {
-  const int64_t row_end = p.B32 > p.Bc ? p.B32 : p.Bc;
+  const int64_t dx_rows = need_dx ? dx_row_frags(p) * 32 : 0;  // dYx rows incl. zero padding
+  int64_t row_end = p.B32 > p.Bc ? p.B32 : p.Bc;
+  if (dx_rows > row_end) row_end = dx_rows;
   const int nob = p.O64 / 32;
   const int nbb = (int)ceil_div(row_end, kPrepRows);
   dim3 grid((unsigned)ceil_div((int64_t)nob * nbb, 4));
   if (p.esz == 2)
     hipLaunchKernelGGL((k_prep_dy<true>), grid, dim3(256), 0, s, dy,
                        reinterpret_cast<uint16_t*>(dYx), reinterpret_cast<uint16_t*>(dYc),
-                       colsum_part, p, (int)need_dx, (int)need_dc, nob, nbb);
+                       colsum_part, p, (int)need_dx, (int)need_dc, nob, nbb, dx_rows);
   else
     hipLaunchKernelGGL((k_prep_dy<false>), grid, dim3(256), 0, s, dy,
                        reinterpret_cast<float*>(dYx), reinterpret_cast<float*>(dYc),
-                       colsum_part, p, (int)need_dx, (int)need_dc, nob, nbb);
+                       colsum_part, p, (int)need_dx, (int)need_dc, nob, nbb, dx_rows);
 }
 
 void launch_dc_finalize(const float* part, int S, float* colsum_part, float* dC,

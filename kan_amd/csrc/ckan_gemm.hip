@@ -61,7 +61,7 @@ k_fwd(const float* __restrict__ tc, const typename Elem<BF>::type* __restrict__ 
   }
 
   u32x4_t pre[CPT];
-  auto gload = [&](int sg) {
+  auto gload = [&](int sg) __attribute__((always_inline)) {
 #pragma unroll
     for (int q = 0; q < CPT; ++q) {
       const int c = tid + q * 256;
@@ -74,7 +74,7 @@ k_fwd(const float* __restrict__ tc, const typename Elem<BF>::type* __restrict__ 
         pre[q] = u32x4_t{0u, 0u, 0u, 0u};
     }
   };
-  auto lstore = [&](int buf) {
+  auto lstore = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
     for (int q = 0; q < CPT; ++q)
       *reinterpret_cast<u32x4_t*>(lds + buf * STAGE + (tid + q * 256) * CE) = pre[q];
@@ -90,7 +90,7 @@ k_fwd(const float* __restrict__ tc, const typename Elem<BF>::type* __restrict__ 
 
   // tanh values of the next super-group, prefetched one stage ahead
   f32x4_t tnext[NM][G::LANE_T / 4];
-  auto tload = [&](int sg) {
+  auto tload = [&](int sg) __attribute__((always_inline)) {
 #pragma unroll
     for (int mi = 0; mi < NM; ++mi) {
       const f32x4_t* src = reinterpret_cast<const f32x4_t*>(trow[mi] + (size_t)sg * G::SGI);
@@ -298,7 +298,7 @@ k_fwd_pipe(const float* __restrict__ tc, const typename Elem<BF>::type* __restri
   const size_t t_stride = (size_t)G::SGI * 4;
 
   // stage `sg` (if it exists) into ring slot `slot` (0 .. 2*NPB-1)
-  auto issue = [&](int sg, int slot) {
+  auto issue = [&](int sg, int slot) __attribute__((always_inline)) {
     if (sg >= sg1) return;
     char* base = smem + slot * K::STAGE_BYTES;
 #pragma unroll
@@ -308,7 +308,7 @@ k_fwd_pipe(const float* __restrict__ tc, const typename Elem<BF>::type* __restri
     for (int q = 0; q < K::T_OPS; ++q)
       dma16(tcb + toff[q] + (size_t)sg * t_stride, base + K::B_BYTES + (q * 8 + wave) * 1024);
   };
-  auto issue_pair = [&](int j) {
+  auto issue_pair = [&](int j) __attribute__((always_inline)) {
     const int slot = (j % NPB) * 2;
     issue(sg0 + 2 * j, slot);
     issue(sg0 + 2 * j + 1, slot + 1);
@@ -322,7 +322,7 @@ k_fwd_pipe(const float* __restrict__ tc, const typename Elem<BF>::type* __restri
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[mi][ni][v] = 0.0f;
 
-  auto compute = [&](int slot) {
+  auto compute = [&](int slot) __attribute__((always_inline)) {
     const char* base = smem + slot * K::STAGE_BYTES;
     const float* tl = reinterpret_cast<const float*>(base + K::B_BYTES);
     const E* bl = reinterpret_cast<const E*>(base);
@@ -464,6 +464,159 @@ k_fwd_pipe(const float* __restrict__ tc, const typename Elem<BF>::type* __restri
 }
 
 // ---------------------------------------------------------------------------
+// dX, pipelined.  A block's tile is 256 rows (4 waves x NM fragments) x one
+// input block (32 inputs x P degrees).  Both operands (dy fragments for the
+// wave's rows, coefficient fragments for the input block) are copied
+// global -> LDS by global_load_lds_dwordx4 into a ring of NBUF stages of KI
+// k-blocks (16 outputs each), NBUF-1 stages ahead; each wave reads the next
+// k-block's fragments into registers while its MFMAs run on the current one.
+// The epilogue sums over degrees with d U_{d-1}(t) and the tanh chain factor
+// in registers.
+// ---------------------------------------------------------------------------
+template <int P, bool BF>
+struct DxPipe {
+  typedef typename Elem<BF>::type E;
+  static constexpr int NM = BwdTile<P>::NM, WGM = 4, KI = 2;  // KI even (loop unroll)
+  static constexpr int FB = kFragElems * (int)sizeof(E);  // bytes per fragment
+  static constexpr int A_BYTES = WGM * NM * KI * FB;
+  static constexpr int B_BYTES = P * KI * FB;
+  static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
+  static constexpr int NBUF_FIT = (160 * 1024) / STAGE_BYTES;
+  static constexpr int NBUF = NBUF_FIT > 5 ? 5 : NBUF_FIT;
+  static constexpr int OPS = STAGE_BYTES / 4096;  // dma16 per thread per stage
+  static constexpr int A_OPS = A_BYTES / 4096;
+  static constexpr bool kOk = NBUF >= 3 && STAGE_BYTES % 4096 == 0 && A_BYTES % 4096 == 0 &&
+                              OPS * (NBUF - 2) < 64;
+};
+
+template <int P, bool BF>
+__global__ void __launch_bounds__(256)
+k_dx_pipe(const typename Elem<BF>::type* __restrict__ dYx,
+          const typename Elem<BF>::type* __restrict__ Cb, const float* __restrict__ tc,
+          float* __restrict__ dx, Plan p, int n_rb) {
+  typedef DxPipe<P, BF> K;
+  typedef typename K::E E;
+  constexpr int NM = K::NM, WGM = K::WGM, KI = K::KI, FB = K::FB, NBUF = K::NBUF;
+  constexpr int RUN = KI * FB / 16;  // 16-byte chunks per contiguous fragment run
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 5;
+  const int nst = p.KBx / KI;
+  const int rb = blockIdx.x % n_rb, ib = blockIdx.x / n_rb;
+
+  // per-op source offsets (bytes); dYx rows are padded to whole tiles
+  const char* abase = reinterpret_cast<const char*>(dYx) + (size_t)rb * WGM * NM * p.KBx * FB;
+  const char* bbase = reinterpret_cast<const char*>(Cb) + (size_t)ib * P * p.KBx * FB;
+  uint32_t off[K::OPS];
+#pragma unroll
+  for (int q = 0; q < K::OPS; ++q) {
+    const int c = (q * 4 + wave) * 64 + lane;
+    if (q < K::A_OPS) {
+      const int run = c / RUN, w = c - run * RUN;  // run = wave' * NM + mi
+      off[q] = (uint32_t)(run * p.KBx * FB + w * 16);
+    } else {
+      const int cc = c - K::A_OPS * 256;
+      const int e = cc / RUN, w = cc - e * RUN;
+      off[q] = (uint32_t)(e * p.KBx * FB + w * 16);
+    }
+  }
+  auto issue = [&](int st) __attribute__((always_inline)) {
+    if (st >= nst) return;
+    const size_t sb = (size_t)st * KI * FB;
+    char* dst = smem + (st % NBUF) * K::STAGE_BYTES + wave * 1024;
+#pragma unroll
+    for (int q = 0; q < K::OPS; ++q)
+      dma16((q < K::A_OPS ? abase : bbase) + sb + off[q], dst + q * 4096);
+  };
+
+  struct Regs {
+    Frag<BF> a[NM];
+    Frag<BF> b[P];
+  };
+  auto lds_read = [&](int kb, Regs& R) __attribute__((always_inline)) {
+    const int kk = kb % KI;
+    const char* base = smem + ((kb / KI) % NBUF) * K::STAGE_BYTES;
+#pragma unroll
+    for (int mi = 0; mi < NM; ++mi)
+      R.a[mi] = load_frag<BF>(reinterpret_cast<const E*>(base + ((wave * NM + mi) * KI + kk) * FB), lane);
+#pragma unroll
+    for (int e = 0; e < P; ++e)
+      R.b[e] = load_frag<BF>(reinterpret_cast<const E*>(base + K::A_BYTES + (e * KI + kk) * FB), lane);
+  };
+
+  f32x16_t acc[NM][P];
+#pragma unroll
+  for (int mi = 0; mi < NM; ++mi)
+#pragma unroll
+    for (int e = 0; e < P; ++e)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[mi][e][v] = 0.0f;
+
+#pragma unroll
+  for (int q = 0; q < NBUF - 1; ++q) issue(q);
+  if (NBUF - 2 <= nst - 1) wait_vmcnt<K::OPS * (NBUF - 2)>();
+  else wait_vmcnt<0>();
+  block_barrier();
+  // the transition into stage st refills with st + NBUF - 1; stage 0 has no
+  // transition, so its refill (stage NBUF - 1) is issued here
+  issue(NBUF - 1);
+  Regs R0, R1;
+  lds_read(0, R0);
+
+  const int nkb = nst * KI;
+  auto step = [&](int kb, const Regs& Rc, Regs& Rn) __attribute__((always_inline)) {
+    const int nxt = kb + 1;
+    if (nxt < nkb) {
+      if (nxt % KI == 0) {
+        const int st = nxt / KI;
+        wait_lgkmcnt<0>();  // this wave's reads of the slot being refilled are done
+        if (st + NBUF - 2 <= nst - 1) wait_vmcnt<K::OPS * (NBUF - 2)>();
+        else wait_vmcnt<0>();
+        block_barrier();
+        issue(st + NBUF - 1);
+      }
+      lds_read(nxt, Rn);
+    }
+#pragma unroll
+    for (int mi = 0; mi < NM; ++mi)
+#pragma unroll
+      for (int e = 0; e < P; ++e) mma(acc[mi][e], Rc.a[mi], Rc.b[e]);
+  };
+  for (int kb = 0; kb < nkb; kb += 2) {
+    step(kb, R0, R1);
+    step(kb + 1, R1, R0);
+  }
+
+  const int i = ib * 32 + (lane & 31);
+  const bool icol = i < p.I;
+#pragma unroll
+  for (int mi = 0; mi < NM; ++mi) {
+    const int64_t r0 = ((int64_t)rb * WGM * NM + wave * NM + mi) * 32 + 4 * g;
+    float tv[16];
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int64_t r = r0 + 8 * (v >> 2) + (v & 3);
+      tv[v] = (icol && r < p.B) ? tc[r * p.I_sg + i] : 0.0f;
+    }
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int64_t r = r0 + 8 * (v >> 2) + (v & 3);
+      const float t2 = tv[v] + tv[v];
+      float up = 0.0f, u = 1.0f, sum = 0.0f;  // U_{-1}, U_0
+#pragma unroll
+      for (int e = 0; e < P; ++e) {
+        sum = fmaf(acc[mi][e][v] * (float)(e + 1), u, sum);
+        const float un = fmaf(t2, u, -up);
+        up = u;
+        u = un;
+      }
+      if (icol && r < p.B) dx[r * p.I + i] = sum * (1.0f - tv[v] * tv[v]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // dX: one block = 4 waves along rows x one input block (32 inputs x P degrees).
 // B fragments (coefficients, all P degrees of the input block) are shared
 // through LDS; A fragments (dy) are per-wave global loads, prefetched a stage
@@ -492,7 +645,7 @@ k_dx(const typename Elem<BF>::type* __restrict__ dYx, const typename Elem<BF>::t
   const int nst = p.KBx / KI;
 
   u32x4_t pre[CPT];
-  auto gload = [&](int st) {
+  auto gload = [&](int st) __attribute__((always_inline)) {
 #pragma unroll
     for (int q = 0; q < CPT; ++q) {
       const int c = tid + q * 256;
@@ -501,13 +654,13 @@ k_dx(const typename Elem<BF>::type* __restrict__ dYx, const typename Elem<BF>::t
           Cb + ((size_t)(ib * P + e) * p.KBx + (size_t)st * KI) * kFragElems + (size_t)off * CE);
     }
   };
-  auto lstore = [&](int buf) {
+  auto lstore = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
     for (int q = 0; q < CPT; ++q)
       *reinterpret_cast<u32x4_t*>(lds + buf * STAGE + (tid + q * 256) * CE) = pre[q];
   };
   Frag<BF> apre[NM][KI];
-  auto aload = [&](int st) {
+  auto aload = [&](int st) __attribute__((always_inline)) {
 #pragma unroll
     for (int mi = 0; mi < NM; ++mi)
 #pragma unroll
@@ -613,7 +766,7 @@ k_dc(const typename Elem<BF>::type* __restrict__ dYc, const float* __restrict__ 
   const int gi = ib * 32 + (ln & 31);
   const bool gvalid = gi < p.I;
   float tpre[8];
-  auto tload = [&](int st) {
+  auto tload = [&](int st) __attribute__((always_inline)) {
     const int64_t b0 = ((int64_t)st * KI + kg) * 16 + 8 * (ln >> 5);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -621,7 +774,7 @@ k_dc(const typename Elem<BF>::type* __restrict__ dYc, const float* __restrict__ 
       tpre[j] = (gvalid && b < p.B) ? tc[b * p.I_sg + gi] : 0.0f;
     }
   };
-  auto generate = [&](int buf) {
+  auto generate = [&](int buf) __attribute__((always_inline)) {
     float ta[8], tb[8], t2[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -644,7 +797,7 @@ k_dc(const typename Elem<BF>::type* __restrict__ dYc, const float* __restrict__ 
     }
   };
   Frag<BF> bpre[NM][KI];
-  auto bload = [&](int st) {
+  auto bload = [&](int st) __attribute__((always_inline)) {
 #pragma unroll
     for (int mi = 0; mi < NM; ++mi)
 #pragma unroll
@@ -809,6 +962,21 @@ static void dx_dispatch(const void* dYx, const void* packed, const float* t, flo
   typedef typename Elem<BF>::type E;
   constexpr int NM = BwdTile<P>::NM;
   const E* Cb = reinterpret_cast<const E*>(packed) + packed_cf_elems(p);
+  if constexpr (DxPipe<P, BF>::kOk) {
+    typedef DxPipe<P, BF> K;
+    const int n_rb = (int)ceil_div(p.B32 / 32, K::WGM * NM);
+    const int blocks = n_rb * p.NIB;
+    const size_t lds = (size_t)K::NBUF * K::STAGE_BYTES;
+    static bool attr_set = false;
+    if (!attr_set) {
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&k_dx_pipe<P, BF>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+      attr_set = true;
+    }
+    hipLaunchKernelGGL((k_dx_pipe<P, BF>), dim3(blocks), dim3(256), lds, s,
+                       reinterpret_cast<const E*>(dYx), Cb, t, dx, p, n_rb);
+    return;
+  }
   dim3 grid((unsigned)ceil_div(p.B32 / 32, 4 * NM), p.NIB);
   hipLaunchKernelGGL((k_dx<P, BF, NM, DxKI<BF>::v>), grid, dim3(256), 0, s,
                      reinterpret_cast<const E*>(dYx), Cb, t, dx, p);
@@ -832,7 +1000,7 @@ BwdLayout bwd_layout(const Plan& p, bool need_dx, bool need_dc) {
   BwdLayout L;
   size_t off = 0;
   L.dyx_off = off;
-  if (need_dx) off += align256((size_t)(p.B32 / 32) * p.KBx * kFragElems * p.esz);
+  if (need_dx) off += align256((size_t)dx_row_frags(p) * p.KBx * kFragElems * p.esz);
   L.dyc_off = off;
   if (need_dc) off += align256((size_t)p.NBf * p.KBc * kFragElems * p.esz);
   L.colsum_off = off;  // NBB partial rows + the reduced row

@@ -78,5 +78,8 @@ template <int P> struct BwdTile {
   static constexpr int WGM = 4;
 };
 inline int bwd_nm(int P) { return (16 / P) < 4 ? (16 / P) : 4; }
+// dX row fragments (32 rows each) padded to whole tiles of 4 waves x NM
+// fragments; the padding fragments of dYx hold zeros.
+inline int64_t dx_row_frags(const Plan& p) { return round_up(p.B32 / 32, 4 * bwd_nm(p.P)); }
 
 }  // namespace ckan
