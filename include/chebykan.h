@@ -125,6 +125,60 @@ int ckan_adam_step(float* p, const float* g, float* m, float* v, int64_t n, int6
                    double lr, double beta1, double beta2, double eps, double weight_decay,
                    void* stream);
 
+/* ---- resident multi-layer executor ---------------------------------------- */
+/* A stack of ChebyKAN layers (KANSequential, kan/layers/base.py:144-166)
+ * trained in place on one GPU: the executor owns fp32 master coefficients,
+ * their packed operands, activations, tanh caches, gradients, optimizer state
+ * and workspaces, allocated once at creation.  One ckan_exec_step runs
+ * forward, the loss and its gradient, backward and the optimizer update for
+ * every layer, the work of one iteration of the reference's training loop
+ * (README.md:61-69) over a KANSequential. */
+
+typedef struct ckan_exec ckan_exec;  /* opaque */
+
+typedef enum ckan_loss {
+  CKAN_LOSS_MSE = 0,  /* torch.nn.MSELoss(): mean over all B x out elements   */
+  CKAN_LOSS_CE = 1    /* torch.nn.CrossEntropyLoss(): mean over B; int64 labels */
+} ckan_loss;
+
+typedef enum ckan_optimizer {
+  CKAN_OPT_SGD = 0,   /* torch.optim.SGD (no momentum)  */
+  CKAN_OPT_ADAM = 1   /* torch.optim.Adam (no amsgrad)  */
+} ckan_optimizer;
+
+typedef struct ckan_exec_config {
+  int32_t n_layers;        /* >= 1                                          */
+  const int32_t* widths;   /* host array, n_layers + 1 entries              */
+  const int32_t* degrees;  /* host array, n_layers entries                  */
+  int64_t batch;           /* rows per step (fixed for the executor)        */
+  int32_t compute;         /* ckan_compute                                  */
+  int32_t loss;            /* ckan_loss                                     */
+  int32_t optimizer;       /* ckan_optimizer                                */
+  int32_t use_graph;       /* replay each step as a captured HIP graph      */
+  float lr, beta1, beta2, eps, weight_decay;
+} ckan_exec_config;
+
+/* Allocates every device buffer; coefficients start at zero (set them with
+ * ckan_exec_set_coeffs).  `stream` orders the initialisation. */
+int ckan_exec_create(const ckan_exec_config* cfg, ckan_exec** out, void* stream);
+int ckan_exec_destroy(ckan_exec* ex);
+/* Device-to-device copy of one layer's fp32 master coefficients [in, out, D]. */
+int ckan_exec_set_coeffs(ckan_exec* ex, int32_t layer, const float* src, void* stream);
+int ckan_exec_get_coeffs(ckan_exec* ex, int32_t layer, float* dst, void* stream);
+/* Adam moments of one layer (fp32, [in, out, D] each) and the step count,
+ * for checkpoint/resume; SGD has none (returns CKAN_ERR_UNSUPPORTED). */
+int ckan_exec_get_adam_state(ckan_exec* ex, int32_t layer, float* m, float* v,
+                             int64_t* step, void* stream);
+int ckan_exec_set_adam_state(ckan_exec* ex, int32_t layer, const float* m, const float* v,
+                             int64_t step, void* stream);
+/* One training step on x [batch, widths[0]] (fp32, device) and target:
+ * fp32 [batch, widths[n]] for MSE or int64 [batch] class indices for CE.
+ * Writes the step's loss (fp32 scalar, device) to loss_out when non-NULL. */
+int ckan_exec_step(ckan_exec* ex, const float* x, const void* target, float* loss_out,
+                   void* stream);
+/* Forward only: y [batch, widths[n]] (fp32, device). */
+int ckan_exec_forward(ckan_exec* ex, const float* x, float* y, void* stream);
+
 /* ---- diagnostics --------------------------------------------------------- */
 
 const char* ckan_last_error(void);

@@ -4,6 +4,7 @@ Public surface (mirrors the reference's names for this path):
     ChebyKANLayer, KANLayer, KANSequential, get_layer, LAYER_REGISTRY
     ChebyshevBasis, BasisFunction, get_basis, BASIS_REGISTRY
     optim.SGD, optim.Adam (fused HIP steps)
+    ResidentExecutor (whole training steps of a layer stack, resident on one GPU)
     functional.chebykan (autograd op)
 
 All compute runs in the in-tree HIP library ``libckan_gfx950.so`` (C-ABI in
@@ -12,11 +13,12 @@ include/chebykan.h); there is no CPU fallback.
 from .basis import BASIS_REGISTRY, BasisFunction, ChebyshevBasis, get_basis
 from .layers import LAYER_REGISTRY, ChebyKANLayer, KANLayer, KANSequential, get_layer
 from . import functional, optim
+from .executor import ResidentExecutor
 
 __version__ = "0.1.0"
 
 __all__ = [
     "ChebyKANLayer", "KANLayer", "KANSequential", "get_layer", "LAYER_REGISTRY",
     "ChebyshevBasis", "BasisFunction", "get_basis", "BASIS_REGISTRY",
-    "functional", "optim", "__version__",
+    "functional", "optim", "ResidentExecutor", "__version__",
 ]

@@ -77,6 +77,41 @@ SIGNATURES = {
     "ckan_profile_report": (_sz, [ctypes.c_char_p, _sz]),
 }
 
+class CkanExecConfig(ctypes.Structure):
+    _fields_ = [
+        ("n_layers", ctypes.c_int32),
+        ("widths", ctypes.POINTER(ctypes.c_int32)),
+        ("degrees", ctypes.POINTER(ctypes.c_int32)),
+        ("batch", ctypes.c_int64),
+        ("compute", ctypes.c_int32),
+        ("loss", ctypes.c_int32),
+        ("optimizer", ctypes.c_int32),
+        ("use_graph", ctypes.c_int32),
+        ("lr", ctypes.c_float),
+        ("beta1", ctypes.c_float),
+        ("beta2", ctypes.c_float),
+        ("eps", ctypes.c_float),
+        ("weight_decay", ctypes.c_float),
+    ]
+
+
+CKAN_LOSS_MSE = 0
+CKAN_LOSS_CE = 1
+CKAN_OPT_SGD = 0
+CKAN_OPT_ADAM = 1
+
+_pcfg = ctypes.POINTER(CkanExecConfig)
+SIGNATURES.update({
+    "ckan_exec_create": (ctypes.c_int, [_pcfg, ctypes.POINTER(_vp), _vp]),
+    "ckan_exec_destroy": (ctypes.c_int, [_vp]),
+    "ckan_exec_set_coeffs": (ctypes.c_int, [_vp, _i32, _vp, _vp]),
+    "ckan_exec_get_coeffs": (ctypes.c_int, [_vp, _i32, _vp, _vp]),
+    "ckan_exec_get_adam_state": (ctypes.c_int, [_vp, _i32, _vp, _vp, ctypes.POINTER(_i64), _vp]),
+    "ckan_exec_set_adam_state": (ctypes.c_int, [_vp, _i32, _vp, _vp, _i64, _vp]),
+    "ckan_exec_step": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp]),
+    "ckan_exec_forward": (ctypes.c_int, [_vp, _vp, _vp, _vp]),
+})
+
 _lib = None
 _lock = threading.Lock()
 

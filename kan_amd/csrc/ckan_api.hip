@@ -99,6 +99,8 @@ inline bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr
 
 }  // namespace
 
+void ckan::set_last_error(const char* msg) { g_err = msg; }
+
 extern "C" {
 
 const char* ckan_last_error(void) { return g_err.c_str(); }

@@ -1,0 +1,486 @@
+// Resident multi-layer executor: a KANSequential of ChebyKAN layers trained in
+// place on one GPU (include/chebykan.h, ckan_exec_*).  All device memory is
+// allocated once at creation; a training step is a fixed sequence of launches
+// (pack, forward per layer, fused loss + gradient, backward per layer,
+// optimizer) on one stream, optionally captured once into a HIP graph and
+// replayed.  The Adam step count lives on the device, so replays stay exact.
+#include <math.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+#include <vector>
+
+#include "chebykan.h"
+#include "ckan_kernels.hpp"
+
+using namespace ckan;
+
+namespace {
+
+constexpr int kLossBlocks = 256;  // fixed partial count: deterministic loss sums
+
+// MSE (torch.nn.MSELoss, reduction='mean'): loss = sum (y - t)^2 / N,
+// dy = 2 (y - t) / N.  Grid-stride over N elements with a fixed grid; each
+// block writes one partial sum.
+__global__ void __launch_bounds__(256)
+k_mse(const float* __restrict__ y, const float* __restrict__ tgt, float* __restrict__ dy,
+      int64_t n, float scale_grad, float* __restrict__ part) {
+  __shared__ float red[256];
+  float s = 0.0f;
+  for (int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; q < n;
+       q += (int64_t)gridDim.x * blockDim.x) {
+    const float d = y[q] - tgt[q];
+    s = fmaf(d, d, s);
+    dy[q] = scale_grad * d;
+  }
+  red[threadIdx.x] = s;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if (threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) part[blockIdx.x] = red[0];
+}
+
+// Softmax cross-entropy (torch.nn.CrossEntropyLoss, reduction='mean') on
+// logits y [B, O] and int64 labels: one wave per row; the row loss
+// logsumexp(y) - y[label] goes to row_loss[b], dy = (softmax(y) - onehot) / B.
+__global__ void __launch_bounds__(256)
+k_ce(const float* __restrict__ y, const int64_t* __restrict__ labels, float* __restrict__ dy,
+     int64_t B, int O, float* __restrict__ row_loss) {
+  const int lane = threadIdx.x & 63;
+  const int64_t b = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (b >= B) return;
+  const float* yr = y + b * O;
+  float m = -INFINITY;
+  for (int o = lane; o < O; o += 64) m = fmaxf(m, yr[o]);
+#pragma unroll
+  for (int w = 32; w > 0; w >>= 1) m = fmaxf(m, __shfl_xor(m, w));
+  float s = 0.0f;
+  for (int o = lane; o < O; o += 64) s += expf(yr[o] - m);
+#pragma unroll
+  for (int w = 32; w > 0; w >>= 1) s += __shfl_xor(s, w);
+  const int64_t lab = labels[b];
+  const float inv_b = 1.0f / (float)B;
+  for (int o = lane; o < O; o += 64) {
+    const float pr = expf(yr[o] - m) / s;
+    dy[b * O + o] = (pr - (o == lab ? 1.0f : 0.0f)) * inv_b;
+  }
+  if (lane == 0) {
+    const float yl = (lab >= 0 && lab < O) ? yr[lab] : 0.0f;
+    row_loss[b] = (logf(s) + m) - yl;
+  }
+}
+
+// loss = scale * sum_k part[k], k < n, in a fixed order (one block).
+__global__ void __launch_bounds__(256)
+k_sum_scalar(const float* __restrict__ part, int64_t n, float scale, float* __restrict__ out) {
+  __shared__ float red[256];
+  float s = 0.0f;
+  for (int64_t k = threadIdx.x; k < n; k += 256) s += part[k];
+  red[threadIdx.x] = s;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if (threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) *out = red[0] * scale;
+}
+
+// Adam scalars for the next step from the device step counter (one thread):
+// step += 1; sc[0] = -lr / (1 - b1^step); sc[1] = sqrt(1 - b2^step), in double
+// as torch computes them, then rounded to fp32.
+__global__ void k_adam_scalars(int64_t* __restrict__ step, double lr, double b1, double b2,
+                               float* __restrict__ sc) {
+  if (threadIdx.x == 0 && blockIdx.x == 0) {
+    const int64_t s = *step + 1;
+    *step = s;
+    sc[0] = (float)(-(lr / (1.0 - pow(b1, (double)s))));
+    sc[1] = (float)sqrt(1.0 - pow(b2, (double)s));
+  }
+}
+
+// Adam update reading its step-dependent scalars from the device.
+__global__ void __launch_bounds__(256)
+k_adam_dev(float* __restrict__ p, const float* __restrict__ g, float* __restrict__ m,
+           float* __restrict__ v, int64_t n, float w1, float beta2, float one_m_beta2,
+           float eps, float wd, const float* __restrict__ sc) {
+  const float neg_step = sc[0], bc2_sqrt = sc[1];
+  for (int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; q < n;
+       q += (int64_t)gridDim.x * blockDim.x) {
+    float gv = g[q];
+    const float pv = p[q];
+    if (wd != 0.0f) gv = gv + wd * pv;
+    float mv = m[q];
+    mv = (w1 < 0.5f) ? mv + w1 * (gv - mv) : gv - (gv - mv) * (1.0f - w1);
+    float vv = v[q] * beta2;
+    vv = vv + one_m_beta2 * gv * gv;
+    const float denom = sqrtf(vv) / bc2_sqrt + eps;
+    m[q] = mv;
+    v[q] = vv;
+    p[q] = pv + neg_step * (mv / denom);
+  }
+}
+
+__global__ void __launch_bounds__(256)
+k_copy_f32(const float* __restrict__ src, float* __restrict__ dst, int64_t n) {
+  for (int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; q < n;
+       q += (int64_t)gridDim.x * blockDim.x)
+    dst[q] = src[q];
+}
+
+int grid_of(int64_t n) {
+  int64_t g = (n + 255) / 256;
+  return (int)(g < 1 ? 1 : (g > 65536 ? 65536 : g));
+}
+
+}  // namespace
+
+struct ckan_exec {
+  struct Layer {
+    ckan_desc desc;
+    int64_t ncoef;
+    float* C = nullptr;     // fp32 master [I, O, D]
+    float* dC = nullptr;
+    float* m = nullptr;     // Adam moments
+    float* v = nullptr;
+    void* packed = nullptr;
+    float* t = nullptr;     // tanh cache
+    float* y = nullptr;     // activation out [B, O]
+    float* dy = nullptr;    // gradient wrt y  [B, O]
+    size_t packed_bytes = 0;
+  };
+  ckan_exec_config cfg;
+  std::vector<int32_t> widths, degrees;
+  std::vector<Layer> layers;
+  void* fws = nullptr;
+  size_t fws_bytes = 0;
+  void* bws = nullptr;
+  size_t bws_bytes = 0;
+  float* loss_part = nullptr;  // max(kLossBlocks, B) partials
+  float* loss = nullptr;
+  int64_t* step = nullptr;     // Adam step count (device)
+  float* adam_sc = nullptr;    // Adam scalars (device)
+  // graph mode
+  hipStream_t es = nullptr;
+  hipEvent_t ev_in = nullptr, ev_out = nullptr;
+  hipGraphExec_t graph = nullptr;
+  float* x_own = nullptr;
+  void* tgt_own = nullptr;
+  size_t tgt_bytes = 0;
+  std::vector<void*> allocs;
+};
+
+namespace {
+
+int efail(int code, const char* msg) {
+  set_last_error(msg);
+  return code;
+}
+
+int dev_alloc(ckan_exec* ex, void** p, size_t bytes) {
+  if (bytes == 0) bytes = 256;
+  if (hipMalloc(p, bytes) != hipSuccess) return efail(CKAN_ERR_HIP, "executor: hipMalloc failed");
+  ex->allocs.push_back(*p);
+  return CKAN_OK;
+}
+
+void free_all(ckan_exec* ex) {
+  if (ex->graph) hipGraphExecDestroy(ex->graph);
+  if (ex->ev_in) hipEventDestroy(ex->ev_in);
+  if (ex->ev_out) hipEventDestroy(ex->ev_out);
+  if (ex->es) hipStreamDestroy(ex->es);
+  for (void* p : ex->allocs) hipFree(p);
+  ex->allocs.clear();
+}
+
+// The step body on stream s with inputs x / target.
+int run_step(ckan_exec* ex, const float* x, const void* target, hipStream_t s) {
+  const int L = (int)ex->layers.size();
+  int rc;
+  for (int l = 0; l < L; ++l) {
+    auto& ly = ex->layers[l];
+    if ((rc = ckan_pack_coeffs(&ly.desc, ly.C, ly.packed, s))) return rc;
+    const float* in = l == 0 ? x : ex->layers[l - 1].y;
+    if ((rc = ckan_forward(&ly.desc, in, ly.packed, ly.y, ly.t, ex->fws, ex->fws_bytes, s)))
+      return rc;
+  }
+  auto& last = ex->layers[L - 1];
+  const int64_t B = ex->cfg.batch;
+  const int O = last.desc.out_dim;
+  if (ex->cfg.loss == CKAN_LOSS_MSE) {
+    const int64_t n = B * O;
+    hipLaunchKernelGGL(k_mse, dim3(kLossBlocks), dim3(256), 0, s, last.y,
+                       reinterpret_cast<const float*>(target), last.dy, n,
+                       (float)(2.0 / (double)n), ex->loss_part);
+    hipLaunchKernelGGL(k_sum_scalar, dim3(1), dim3(256), 0, s, ex->loss_part,
+                       (int64_t)kLossBlocks, (float)(1.0 / (double)n), ex->loss);
+  } else {
+    hipLaunchKernelGGL(k_ce, dim3((unsigned)((B + 3) / 4)), dim3(256), 0, s, last.y,
+                       reinterpret_cast<const int64_t*>(target), last.dy, B, O, ex->loss_part);
+    hipLaunchKernelGGL(k_sum_scalar, dim3(1), dim3(256), 0, s, ex->loss_part, B,
+                       (float)(1.0 / (double)B), ex->loss);
+  }
+  if (hipGetLastError() != hipSuccess) return efail(CKAN_ERR_HIP, "executor: loss launch failed");
+  for (int l = L - 1; l >= 0; --l) {
+    auto& ly = ex->layers[l];
+    float* dx = l > 0 ? ex->layers[l - 1].dy : nullptr;
+    if ((rc = ckan_backward(&ly.desc, ly.t, ly.packed, ly.dy, dx, ly.dC, 0, ex->bws,
+                            ex->bws_bytes, s)))
+      return rc;
+  }
+  const auto& c = ex->cfg;
+  if (c.optimizer == CKAN_OPT_SGD) {
+    for (auto& ly : ex->layers)
+      if ((rc = ckan_sgd_step(ly.C, ly.dC, ly.ncoef, c.lr, c.weight_decay, s))) return rc;
+  } else {
+    hipLaunchKernelGGL(k_adam_scalars, dim3(1), dim3(64), 0, s, ex->step, (double)c.lr,
+                       (double)c.beta1, (double)c.beta2, ex->adam_sc);
+    for (auto& ly : ex->layers)
+      hipLaunchKernelGGL(k_adam_dev, dim3(grid_of(ly.ncoef)), dim3(256), 0, s, ly.C, ly.dC,
+                         ly.m, ly.v, ly.ncoef, (float)(1.0 - (double)c.beta1), c.beta2,
+                         (float)(1.0 - (double)c.beta2), c.eps, c.weight_decay, ex->adam_sc);
+    if (hipGetLastError() != hipSuccess) return efail(CKAN_ERR_HIP, "executor: adam launch failed");
+  }
+  return CKAN_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ckan_exec_create(const ckan_exec_config* cfg, ckan_exec** out, void* stream) {
+  if (!cfg || !out) return efail(CKAN_ERR_INVALID_ARG, "executor: cfg/out is NULL");
+  *out = nullptr;
+  if (cfg->n_layers < 1 || !cfg->widths || !cfg->degrees)
+    return efail(CKAN_ERR_INVALID_ARG, "executor: need n_layers >= 1 and widths/degrees");
+  if (cfg->batch < 1) return efail(CKAN_ERR_INVALID_ARG, "executor: batch must be >= 1");
+  if (cfg->loss != CKAN_LOSS_MSE && cfg->loss != CKAN_LOSS_CE)
+    return efail(CKAN_ERR_INVALID_ARG, "executor: unknown loss");
+  if (cfg->optimizer != CKAN_OPT_SGD && cfg->optimizer != CKAN_OPT_ADAM)
+    return efail(CKAN_ERR_INVALID_ARG, "executor: unknown optimizer");
+  if (cfg->optimizer == CKAN_OPT_ADAM &&
+      !(cfg->beta1 >= 0.f && cfg->beta1 < 1.f && cfg->beta2 >= 0.f && cfg->beta2 < 1.f))
+    return efail(CKAN_ERR_INVALID_ARG, "executor: betas must lie in [0, 1)");
+  ckan_exec* ex = new ckan_exec();
+  ex->cfg = *cfg;
+  ex->widths.assign(cfg->widths, cfg->widths + cfg->n_layers + 1);
+  ex->degrees.assign(cfg->degrees, cfg->degrees + cfg->n_layers);
+  ex->cfg.widths = ex->widths.data();
+  ex->cfg.degrees = ex->degrees.data();
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  int rc = CKAN_OK;
+  ex->layers.resize(cfg->n_layers);
+  for (int l = 0; l < cfg->n_layers && rc == CKAN_OK; ++l) {
+    auto& ly = ex->layers[l];
+    ly.desc = ckan_desc{cfg->batch, ex->widths[l], ex->widths[l + 1], ex->degrees[l],
+                        cfg->compute, CKAN_DTYPE_F32, 0};
+    ly.packed_bytes = ckan_packed_bytes(&ly.desc);
+    if (ly.packed_bytes == 0) {
+      rc = efail(CKAN_ERR_INVALID_ARG, "executor: invalid layer shape or degree");
+      break;
+    }
+    ly.ncoef = (int64_t)ly.desc.in_dim * ly.desc.out_dim * (ly.desc.degree + 1);
+    const int64_t ny = cfg->batch * ly.desc.out_dim;
+    if ((rc = dev_alloc(ex, (void**)&ly.C, ly.ncoef * 4)) ||
+        (rc = dev_alloc(ex, (void**)&ly.dC, ly.ncoef * 4)) ||
+        (rc = dev_alloc(ex, &ly.packed, ly.packed_bytes)) ||
+        (rc = dev_alloc(ex, (void**)&ly.t, ckan_tcache_elems(&ly.desc) * 4)) ||
+        (rc = dev_alloc(ex, (void**)&ly.y, ny * 4)) ||
+        (rc = dev_alloc(ex, (void**)&ly.dy, ny * 4)))
+      break;
+    launch_zero_f32(ly.C, ly.ncoef, s);
+    if (cfg->optimizer == CKAN_OPT_ADAM) {
+      if ((rc = dev_alloc(ex, (void**)&ly.m, ly.ncoef * 4)) ||
+          (rc = dev_alloc(ex, (void**)&ly.v, ly.ncoef * 4)))
+        break;
+      launch_zero_f32(ly.m, ly.ncoef, s);
+      launch_zero_f32(ly.v, ly.ncoef, s);
+    }
+    const size_t f = ckan_fwd_workspace_bytes(&ly.desc);
+    const size_t b = ckan_bwd_workspace_bytes(&ly.desc, l > 0, 1);
+    if (f > ex->fws_bytes) ex->fws_bytes = f;
+    if (b > ex->bws_bytes) ex->bws_bytes = b;
+  }
+  if (rc == CKAN_OK) {
+    ex->fws_bytes = align256(ex->fws_bytes);
+    ex->bws_bytes = align256(ex->bws_bytes);
+    const int64_t nloss = cfg->batch > kLossBlocks ? cfg->batch : kLossBlocks;
+    if (!(rc = dev_alloc(ex, &ex->fws, ex->fws_bytes)) &&
+        !(rc = dev_alloc(ex, &ex->bws, ex->bws_bytes)) &&
+        !(rc = dev_alloc(ex, (void**)&ex->loss_part, nloss * 4)) &&
+        !(rc = dev_alloc(ex, (void**)&ex->loss, 256)) &&
+        !(rc = dev_alloc(ex, (void**)&ex->step, 256)) &&
+        !(rc = dev_alloc(ex, (void**)&ex->adam_sc, 256))) {
+      if (ex->fws_bytes) launch_zero(ex->fws, ex->fws_bytes, s);
+      launch_zero(ex->step, 256, s);
+    }
+  }
+  if (rc == CKAN_OK && cfg->use_graph) {
+    const int O = ex->widths[cfg->n_layers];
+    ex->tgt_bytes = cfg->loss == CKAN_LOSS_MSE ? (size_t)cfg->batch * O * 4 : (size_t)cfg->batch * 8;
+    if (!(rc = dev_alloc(ex, (void**)&ex->x_own, (size_t)cfg->batch * ex->widths[0] * 4)) &&
+        !(rc = dev_alloc(ex, &ex->tgt_own, ex->tgt_bytes))) {
+      if (hipStreamCreateWithFlags(&ex->es, hipStreamNonBlocking) != hipSuccess ||
+          hipEventCreateWithFlags(&ex->ev_in, hipEventDisableTiming) != hipSuccess ||
+          hipEventCreateWithFlags(&ex->ev_out, hipEventDisableTiming) != hipSuccess)
+        rc = efail(CKAN_ERR_HIP, "executor: stream/event creation failed");
+    }
+  }
+  if (rc == CKAN_OK && hipGetLastError() != hipSuccess)
+    rc = efail(CKAN_ERR_HIP, "executor: initialisation launch failed");
+  if (rc != CKAN_OK) {
+    free_all(ex);
+    delete ex;
+    return rc;
+  }
+  *out = ex;
+  return CKAN_OK;
+}
+
+int ckan_exec_destroy(ckan_exec* ex) {
+  if (!ex) return CKAN_OK;
+  if (ex->es) hipStreamSynchronize(ex->es);
+  hipDeviceSynchronize();
+  free_all(ex);
+  delete ex;
+  return CKAN_OK;
+}
+
+static int check_layer(ckan_exec* ex, int32_t layer) {
+  if (!ex) return efail(CKAN_ERR_INVALID_ARG, "executor is NULL");
+  if (layer < 0 || layer >= (int32_t)ex->layers.size())
+    return efail(CKAN_ERR_INVALID_ARG, "executor: layer index out of range");
+  return CKAN_OK;
+}
+
+int ckan_exec_set_coeffs(ckan_exec* ex, int32_t layer, const float* src, void* stream) {
+  int rc = check_layer(ex, layer);
+  if (rc) return rc;
+  if (!src) return efail(CKAN_ERR_INVALID_ARG, "executor: src is NULL");
+  auto& ly = ex->layers[layer];
+  hipLaunchKernelGGL(k_copy_f32, dim3(grid_of(ly.ncoef)), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), src, ly.C, ly.ncoef);
+  return hipGetLastError() == hipSuccess ? CKAN_OK : efail(CKAN_ERR_HIP, "executor: copy failed");
+}
+
+int ckan_exec_get_coeffs(ckan_exec* ex, int32_t layer, float* dst, void* stream) {
+  int rc = check_layer(ex, layer);
+  if (rc) return rc;
+  if (!dst) return efail(CKAN_ERR_INVALID_ARG, "executor: dst is NULL");
+  auto& ly = ex->layers[layer];
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (ex->es) {  // order after any graph replay on the executor stream
+    hipEventRecord(ex->ev_out, ex->es);
+    hipStreamWaitEvent(s, ex->ev_out, 0);
+  }
+  hipLaunchKernelGGL(k_copy_f32, dim3(grid_of(ly.ncoef)), dim3(256), 0, s, ly.C, dst, ly.ncoef);
+  return hipGetLastError() == hipSuccess ? CKAN_OK : efail(CKAN_ERR_HIP, "executor: copy failed");
+}
+
+int ckan_exec_get_adam_state(ckan_exec* ex, int32_t layer, float* m, float* v, int64_t* step,
+                             void* stream) {
+  int rc = check_layer(ex, layer);
+  if (rc) return rc;
+  if (ex->cfg.optimizer != CKAN_OPT_ADAM)
+    return efail(CKAN_ERR_UNSUPPORTED, "executor: optimizer has no Adam state");
+  if (!m || !v || !step) return efail(CKAN_ERR_INVALID_ARG, "executor: m/v/step is NULL");
+  auto& ly = ex->layers[layer];
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (ex->es) {
+    hipEventRecord(ex->ev_out, ex->es);
+    hipStreamWaitEvent(s, ex->ev_out, 0);
+  }
+  hipLaunchKernelGGL(k_copy_f32, dim3(grid_of(ly.ncoef)), dim3(256), 0, s, ly.m, m, ly.ncoef);
+  hipLaunchKernelGGL(k_copy_f32, dim3(grid_of(ly.ncoef)), dim3(256), 0, s, ly.v, v, ly.ncoef);
+  if (hipMemcpyAsync(step, ex->step, sizeof(int64_t), hipMemcpyDeviceToHost, s) != hipSuccess ||
+      hipStreamSynchronize(s) != hipSuccess)
+    return efail(CKAN_ERR_HIP, "executor: state copy failed");
+  return CKAN_OK;
+}
+
+int ckan_exec_set_adam_state(ckan_exec* ex, int32_t layer, const float* m, const float* v,
+                             int64_t step, void* stream) {
+  int rc = check_layer(ex, layer);
+  if (rc) return rc;
+  if (ex->cfg.optimizer != CKAN_OPT_ADAM)
+    return efail(CKAN_ERR_UNSUPPORTED, "executor: optimizer has no Adam state");
+  if (!m || !v || step < 0) return efail(CKAN_ERR_INVALID_ARG, "executor: bad m/v/step");
+  auto& ly = ex->layers[layer];
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(k_copy_f32, dim3(grid_of(ly.ncoef)), dim3(256), 0, s, m, ly.m, ly.ncoef);
+  hipLaunchKernelGGL(k_copy_f32, dim3(grid_of(ly.ncoef)), dim3(256), 0, s, v, ly.v, ly.ncoef);
+  int64_t st = step;
+  if (hipMemcpyAsync(ex->step, &st, sizeof(int64_t), hipMemcpyHostToDevice, s) != hipSuccess ||
+      hipStreamSynchronize(s) != hipSuccess)
+    return efail(CKAN_ERR_HIP, "executor: state copy failed");
+  return CKAN_OK;
+}
+
+int ckan_exec_step(ckan_exec* ex, const float* x, const void* target, float* loss_out,
+                   void* stream) {
+  if (!ex) return efail(CKAN_ERR_INVALID_ARG, "executor is NULL");
+  if (!x || !target) return efail(CKAN_ERR_INVALID_ARG, "executor: x/target is NULL");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  int rc;
+  if (!ex->cfg.use_graph) {
+    if ((rc = run_step(ex, x, target, s))) return rc;
+    if (loss_out && hipMemcpyAsync(loss_out, ex->loss, 4, hipMemcpyDeviceToDevice, s) != hipSuccess)
+      return efail(CKAN_ERR_HIP, "executor: loss copy failed");
+    return CKAN_OK;
+  }
+  // graph mode: inputs staged into executor-owned buffers outside the graph
+  if (hipEventRecord(ex->ev_in, s) != hipSuccess || hipStreamWaitEvent(ex->es, ex->ev_in, 0) != hipSuccess)
+    return efail(CKAN_ERR_HIP, "executor: stream ordering failed");
+  const size_t xb = (size_t)ex->cfg.batch * ex->widths[0] * 4;
+  if (hipMemcpyAsync(ex->x_own, x, xb, hipMemcpyDeviceToDevice, ex->es) != hipSuccess ||
+      hipMemcpyAsync(ex->tgt_own, target, ex->tgt_bytes, hipMemcpyDeviceToDevice, ex->es) != hipSuccess)
+    return efail(CKAN_ERR_HIP, "executor: input staging failed");
+  if (!ex->graph) {
+    hipGraph_t g = nullptr;
+    if (hipStreamBeginCapture(ex->es, hipStreamCaptureModeThreadLocal) != hipSuccess)
+      return efail(CKAN_ERR_HIP, "executor: graph capture failed to start");
+    rc = run_step(ex, ex->x_own, ex->tgt_own, ex->es);
+    const hipError_t ec = hipStreamEndCapture(ex->es, &g);
+    if (rc) {
+      if (g) hipGraphDestroy(g);
+      return rc;
+    }
+    if (ec != hipSuccess || hipGraphInstantiate(&ex->graph, g, nullptr, nullptr, 0) != hipSuccess) {
+      if (g) hipGraphDestroy(g);
+      return efail(CKAN_ERR_HIP, "executor: graph capture failed");
+    }
+    hipGraphDestroy(g);
+  }
+  if (hipGraphLaunch(ex->graph, ex->es) != hipSuccess)
+    return efail(CKAN_ERR_HIP, "executor: graph launch failed");
+  if (loss_out && hipMemcpyAsync(loss_out, ex->loss, 4, hipMemcpyDeviceToDevice, ex->es) != hipSuccess)
+    return efail(CKAN_ERR_HIP, "executor: loss copy failed");
+  if (hipEventRecord(ex->ev_out, ex->es) != hipSuccess || hipStreamWaitEvent(s, ex->ev_out, 0) != hipSuccess)
+    return efail(CKAN_ERR_HIP, "executor: stream ordering failed");
+  return CKAN_OK;
+}
+
+int ckan_exec_forward(ckan_exec* ex, const float* x, float* y, void* stream) {
+  if (!ex) return efail(CKAN_ERR_INVALID_ARG, "executor is NULL");
+  if (!x || !y) return efail(CKAN_ERR_INVALID_ARG, "executor: x/y is NULL");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (ex->es) {
+    hipEventRecord(ex->ev_out, ex->es);
+    hipStreamWaitEvent(s, ex->ev_out, 0);
+  }
+  const int L = (int)ex->layers.size();
+  int rc;
+  for (int l = 0; l < L; ++l) {
+    auto& ly = ex->layers[l];
+    if ((rc = ckan_pack_coeffs(&ly.desc, ly.C, ly.packed, s))) return rc;
+    const float* in = l == 0 ? x : ex->layers[l - 1].y;
+    float* out = l == L - 1 ? y : ly.y;
+    if ((rc = ckan_forward(&ly.desc, in, ly.packed, out, ly.t, ex->fws, ex->fws_bytes, s)))
+      return rc;
+  }
+  return CKAN_OK;
+}
+
+}  // extern "C"

@@ -8,6 +8,9 @@ namespace ckan {
 
 inline size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
+// Sets the thread-local message returned by ckan_last_error().
+void set_last_error(const char* msg);
+
 // ---- packed coefficients: [Cf][Cb][bias partials] -------------------------
 inline size_t packed_cf_elems(const Plan& p) { return (size_t)p.NBf * p.KB * kFragElems; }
 inline size_t packed_cb_elems(const Plan& p) { return (size_t)p.NIB * p.P * p.KBx * kFragElems; }

@@ -1,0 +1,141 @@
+"""Resident multi-layer executor over the C-ABI (ckan_exec_*).
+
+Trains a KANSequential of ChebyKAN layers (kan/layers/base.py:144-166) in place
+on one GPU: the library owns fp32 master coefficients, packed operands,
+activations, tanh caches, gradients and optimizer state, and one ``step`` runs
+forward, the loss and its gradient, backward and the optimizer for every
+layer -- one iteration of the reference training loop (README.md:61-69).
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import List, Optional, Sequence
+
+import torch
+
+from . import _lib
+from .functional import compute_code
+from .layers import ChebyKANLayer, KANSequential
+
+_LOSS = {"mse": _lib.CKAN_LOSS_MSE, "ce": _lib.CKAN_LOSS_CE, "cross_entropy": _lib.CKAN_LOSS_CE}
+_OPT = {"sgd": _lib.CKAN_OPT_SGD, "adam": _lib.CKAN_OPT_ADAM}
+
+
+class ResidentExecutor:
+    """A resident ChebyKAN stack: ``widths`` has n_layers + 1 entries."""
+
+    def __init__(self, widths: Sequence[int], degrees: Sequence[int], batch: int,
+                 compute: str = "bf16", loss: str = "mse", optimizer: str = "sgd",
+                 lr: float = 0.01, betas=(0.9, 0.999), eps: float = 1e-8,
+                 weight_decay: float = 0.0, use_graph: bool = False, device="cuda"):
+        self.device = torch.device(device)
+        if self.device.type != "cuda":
+            raise RuntimeError("ResidentExecutor runs only on a ROCm device")
+        if len(widths) != len(degrees) + 1:
+            raise ValueError("widths must have one more entry than degrees")
+        if loss not in _LOSS:
+            raise ValueError(f"loss must be one of {sorted(_LOSS)}")
+        if optimizer not in _OPT:
+            raise ValueError(f"optimizer must be one of {sorted(_OPT)}")
+        self.widths = [int(w) for w in widths]
+        self.degrees = [int(d) for d in degrees]
+        self.batch = int(batch)
+        self.loss_name = loss
+        self.optimizer = optimizer
+        self._lib = _lib.load()
+        self._w = (ctypes.c_int32 * len(self.widths))(*self.widths)
+        self._d = (ctypes.c_int32 * len(self.degrees))(*self.degrees)
+        cfg = _lib.CkanExecConfig(
+            len(self.degrees), self._w, self._d, self.batch, compute_code(compute),
+            _LOSS[loss], _OPT[optimizer], 1 if use_graph else 0, float(lr), float(betas[0]),
+            float(betas[1]), float(eps), float(weight_decay))
+        handle = ctypes.c_void_p()
+        with torch.cuda.device(self.device):
+            _lib.check(self._lib.ckan_exec_create(ctypes.byref(cfg), ctypes.byref(handle),
+                                                  self._stream()))
+        self._h = handle
+        self._loss = torch.empty((), dtype=torch.float32, device=self.device)
+
+    def _stream(self) -> int:
+        return _lib.stream_ptr(self.device)
+
+    def _shape(self, layer: int):
+        return (self.widths[layer], self.widths[layer + 1], self.degrees[layer] + 1)
+
+    @classmethod
+    def from_sequential(cls, model: KANSequential, batch: int, **kw) -> "ResidentExecutor":
+        layers: List[ChebyKANLayer] = [m for m in model if isinstance(m, ChebyKANLayer)]
+        widths = [layers[0].input_dim] + [m.output_dim for m in layers]
+        ex = cls(widths, [m.degree for m in layers], batch, **kw)
+        for l, m in enumerate(layers):
+            ex.set_coeffs(l, m.cheby_coeffs.detach())
+        return ex
+
+    def set_coeffs(self, layer: int, coeffs: torch.Tensor) -> None:
+        c = coeffs.detach().to(self.device, torch.float32).contiguous()
+        if tuple(c.shape) != self._shape(layer):
+            raise RuntimeError(f"layer {layer} coefficients must be {self._shape(layer)}")
+        _lib.check(self._lib.ckan_exec_set_coeffs(self._h, layer, c.data_ptr(), self._stream()))
+        torch.cuda.current_stream(self.device).synchronize()
+
+    def get_coeffs(self, layer: int) -> torch.Tensor:
+        out = torch.empty(self._shape(layer), dtype=torch.float32, device=self.device)
+        _lib.check(self._lib.ckan_exec_get_coeffs(self._h, layer, out.data_ptr(), self._stream()))
+        return out
+
+    def step(self, x: torch.Tensor, target: torch.Tensor) -> torch.Tensor:
+        """One training step; returns the loss as a device scalar."""
+        x = x.to(self.device, torch.float32).contiguous()
+        if tuple(x.shape) != (self.batch, self.widths[0]):
+            raise RuntimeError(f"x must be [{self.batch}, {self.widths[0]}]")
+        if self.loss_name == "mse":
+            target = target.to(self.device, torch.float32).contiguous()
+            if tuple(target.shape) != (self.batch, self.widths[-1]):
+                raise RuntimeError(f"target must be [{self.batch}, {self.widths[-1]}]")
+        else:
+            target = target.to(self.device, torch.int64).contiguous()
+            if tuple(target.shape) != (self.batch,):
+                raise RuntimeError(f"labels must be [{self.batch}]")
+        _lib.check(self._lib.ckan_exec_step(self._h, x.data_ptr(), target.data_ptr(),
+                                            self._loss.data_ptr(), self._stream()))
+        return self._loss
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        x = x.to(self.device, torch.float32).contiguous()
+        y = torch.empty(self.batch, self.widths[-1], dtype=torch.float32, device=self.device)
+        _lib.check(self._lib.ckan_exec_forward(self._h, x.data_ptr(), y.data_ptr(), self._stream()))
+        return y
+
+    def state_dict(self) -> dict:
+        """Master coefficients (and Adam moments + step) for checkpointing."""
+        sd = {"widths": list(self.widths), "degrees": list(self.degrees)}
+        for l in range(len(self.degrees)):
+            sd[f"{l}.cheby_coeffs"] = self.get_coeffs(l).cpu()
+            if self.optimizer == "adam":
+                m = torch.empty(self._shape(l), device=self.device)
+                v = torch.empty(self._shape(l), device=self.device)
+                st = ctypes.c_int64()
+                _lib.check(self._lib.ckan_exec_get_adam_state(self._h, l, m.data_ptr(), v.data_ptr(),
+                                                              ctypes.byref(st), self._stream()))
+                sd[f"{l}.exp_avg"], sd[f"{l}.exp_avg_sq"], sd["step"] = m.cpu(), v.cpu(), st.value
+        return sd
+
+    def load_state_dict(self, sd: dict) -> None:
+        for l in range(len(self.degrees)):
+            self.set_coeffs(l, sd[f"{l}.cheby_coeffs"])
+            if self.optimizer == "adam" and f"{l}.exp_avg" in sd:
+                m = sd[f"{l}.exp_avg"].to(self.device, torch.float32).contiguous()
+                v = sd[f"{l}.exp_avg_sq"].to(self.device, torch.float32).contiguous()
+                _lib.check(self._lib.ckan_exec_set_adam_state(self._h, l, m.data_ptr(), v.data_ptr(),
+                                                              int(sd["step"]), self._stream()))
+
+    def close(self) -> None:
+        if getattr(self, "_h", None) is not None and self._h.value:
+            self._lib.ckan_exec_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -1,0 +1,112 @@
+"""GPU tests of the resident executor against the CPU oracle's training loop.
+
+Configs 2 (784->64->10, deg 4, CE, SGD) and 4-like stacks (MSE, SGD) at
+sizes the oracle finishes quickly, plus the config-1 Adam loop; fp32 MFMA so
+the 1e-5-class tolerances of the layer apply per step (trajectories are
+compared with a looser bound because rounding differences compound).
+"""
+import math
+
+import pytest
+import torch
+
+from oracle import chebykan_oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def _rel(a, b):
+    a = a.detach().double().cpu()
+    b = b.detach().double().cpu()
+    return ((a - b).norm() / b.norm().clamp_min(1e-30)).item()
+
+
+def _make(widths, degrees, seed):
+    torch.manual_seed(seed)
+    return [orc.init_coeffs(widths[l], widths[l + 1], degrees[l]) for l in range(len(degrees))]
+
+
+@pytest.mark.parametrize("use_graph", [False, True])
+def test_config2_ce_sgd_matches_oracle(use_graph):
+    from kan_amd import ResidentExecutor
+    print(f"executor cfg2 graph={use_graph}", flush=True)
+    widths, degrees, B = [784, 64, 10], [4, 4], 256
+    g = torch.Generator().manual_seed(2)
+    x = torch.rand(B, 784, generator=g) * (torch.rand(B, 784, generator=g) >= 0.8).float()
+    labels = torch.randint(0, 10, (B,), generator=g)
+    coeffs = _make(widths, degrees, 20)
+    ex = ResidentExecutor(widths, degrees, B, compute="fp32", loss="ce", optimizer="sgd",
+                          lr=0.01, use_graph=use_graph)
+    for l, c in enumerate(coeffs):
+        ex.set_coeffs(l, c)
+    xd, ld = x.cuda(), labels.cuda()
+    losses = [ex.step(xd, ld).item() for _ in range(5)]
+    c_ref, losses_ref = orc.train_steps(x, labels, coeffs, steps=5, loss="ce", optimizer="sgd", lr=0.01)
+    for a, b in zip(losses, losses_ref):
+        assert abs(a - b) <= 1e-5 * abs(b) + 1e-6
+    for l in range(2):
+        assert _rel(ex.get_coeffs(l), c_ref[l]) <= 1e-5
+    ex.close()
+
+
+def test_mse_stack_deg16_sgd_matches_oracle():
+    from kan_amd import ResidentExecutor
+    print("executor mse deg16 stack", flush=True)
+    widths, degrees, B = [64, 64, 64, 16], [16, 16, 16], 512
+    g = torch.Generator().manual_seed(4)
+    x = torch.rand(B, 64, generator=g) * 6 - 3
+    W = torch.randn(64, 16, generator=g) / 8
+    y = x @ W + 0.1 * torch.randn(B, 16, generator=g)
+    coeffs = _make(widths, degrees, 40)
+    ex = ResidentExecutor(widths, degrees, B, compute="fp32", loss="mse", optimizer="sgd", lr=0.01)
+    for l, c in enumerate(coeffs):
+        ex.set_coeffs(l, c)
+    losses = [ex.step(x.cuda(), y.cuda()).item() for _ in range(4)]
+    c_ref, losses_ref = orc.train_steps(x, y, coeffs, steps=4, loss="mse", optimizer="sgd", lr=0.01)
+    for a, b in zip(losses, losses_ref):
+        assert abs(a - b) <= 1e-5 * abs(b) + 1e-7
+    for l in range(3):
+        assert _rel(ex.get_coeffs(l), c_ref[l]) <= 1e-5
+    ex.close()
+
+
+def test_config1_adam_executor_and_checkpoint():
+    from kan_amd import ResidentExecutor
+    print("executor cfg1 adam", flush=True)
+    x = torch.linspace(-1, 1, 100).reshape(-1, 1)
+    y = torch.sin(2 * math.pi * x)
+    coeffs = _make([1, 1], [8], 0)
+    ex = ResidentExecutor([1, 1], [8], 100, compute="fp32", loss="mse", optimizer="adam", lr=0.01,
+                          use_graph=True)
+    ex.set_coeffs(0, coeffs[0])
+    xd, yd = x.cuda(), y.cuda()
+    for _ in range(300):
+        ex.step(xd, yd)
+    sd = ex.state_dict()
+    assert sd["step"] == 300
+    for _ in range(700):
+        loss = ex.step(xd, yd)
+    c_ref, losses_ref = orc.train_steps(x, y, coeffs, steps=1000, loss="mse", optimizer="adam", lr=0.01)
+    assert abs(loss.item() - losses_ref[-1]) <= 1e-3 * losses_ref[0]
+    assert _rel(ex.get_coeffs(0), c_ref[0]) <= 1e-3
+    # resume from the checkpoint in a fresh executor: same trajectory
+    ex2 = ResidentExecutor([1, 1], [8], 100, compute="fp32", loss="mse", optimizer="adam", lr=0.01)
+    ex2.load_state_dict(sd)
+    for _ in range(700):
+        loss2 = ex2.step(xd, yd)
+    assert _rel(ex2.get_coeffs(0), ex.get_coeffs(0)) <= 1e-6
+    ex.close()
+    ex2.close()
+
+
+def test_executor_forward_matches_layers():
+    import kan_amd
+    from kan_amd import ResidentExecutor
+    torch.manual_seed(5)
+    seq = kan_amd.KANSequential(kan_amd.ChebyKANLayer(32, 48, 5), kan_amd.ChebyKANLayer(48, 8, 3))
+    x = torch.randn(96, 32)
+    ex = ResidentExecutor.from_sequential(seq, 96, compute="fp32")
+    y = ex.forward(x.cuda()).cpu()
+    y_ref = orc.mlp_forward(x, [m.cheby_coeffs.detach() for m in seq])
+    assert _rel(y, y_ref) <= 1e-5
+    ex.close()
