@@ -266,7 +266,13 @@ k_dc_finalize(const float* __restrict__ part, int S, const float* __restrict__ c
       float v = 0.0f;
       if (ok && e < p.deg) {
         const float* src = part + ((size_t)e * p.I32 + i) * p.O32 + o;
-        for (int s = 0; s < S; ++s) v += src[s * sstride];
+        for (int s0 = 0; s0 < S; s0 += 4) {  // 4 loads in flight, added in split order
+          float w[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) w[j] = (s0 + j < S) ? src[(size_t)(s0 + j) * sstride] : 0.0f;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) v += w[j];
+        }
       }
       if (e < p.deg) tile[(il * 64 + ol) * D + e + 1] = v;
     }

@@ -16,6 +16,21 @@
 
 namespace ckan {
 
+// s0 + sum_{z < n} src[z * stride], added in z order; loads are issued 8 at a
+// time so a long split count does not serialise on memory latency.
+__device__ __forceinline__ float split_sum(const float* __restrict__ src, size_t stride,
+                                           unsigned n, float s0) {
+  float s = s0;
+  for (unsigned z0 = 0; z0 < n; z0 += 8) {
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = (z0 + j < n) ? src[(size_t)(z0 + j) * stride] : 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s += v[j];
+  }
+  return s;
+}
+
 // ---------------------------------------------------------------------------
 // Forward
 // ---------------------------------------------------------------------------
@@ -28,7 +43,7 @@ template <int P, bool BF, int NM, int NN, int WGM, int WGN>
 __global__ void __launch_bounds__(256)
 k_fwd(const float* __restrict__ tc, const typename Elem<BF>::type* __restrict__ Cf,
       const float* __restrict__ bias_f, float* __restrict__ y, float* __restrict__ part,
-      unsigned* __restrict__ counters, Plan p, int sg_per_split) {
+      Plan p, int sg_per_split) {
   typedef typename Elem<BF>::type E;
   typedef FwdGroup<P> G;
   static_assert(WGM * WGN == 4, "4 waves per block");
@@ -173,7 +188,7 @@ k_fwd(const float* __restrict__ tc, const typename Elem<BF>::type* __restrict__ 
     return;
   }
 
-  // split-K: partial tile, then the last block of this tile reduces.
+  // split-K: write the partial tile; k_fwd_reduce adds the splits in order
 #pragma unroll
   for (int ni = 0; ni < NN; ++ni) {
     const int nb = nb0 + wn * NN + ni;
@@ -190,28 +205,6 @@ k_fwd(const float* __restrict__ tc, const typename Elem<BF>::type* __restrict__ 
       }
     }
   }
-  __threadfence();
-  __syncthreads();
-  __shared__ unsigned s_last;
-  const unsigned tile_id = blockIdx.y * gridDim.x + blockIdx.x;
-  if (tid == 0) {
-    const unsigned prev = atomicAdd(&counters[tile_id], 1u);
-    s_last = (prev == gridDim.z - 1) ? 1u : 0u;
-  }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  constexpr int BN = BNF * 32;
-  for (int idx = tid; idx < BM * BN; idx += 256) {
-    const int rl = idx / BN, cl = idx - rl * BN;
-    const int64_t r = m_blk + rl;
-    const int o = nb0 * 32 + cl;
-    if (r >= p.B || o >= p.O) continue;
-    float s = bias_f[o];
-    for (unsigned z = 0; z < gridDim.z; ++z) s += part[((size_t)z * p.B32 + r) * p.O32 + o];
-    y[r * p.O + o] = s;
-  }
-  if (tid == 0) counters[tile_id] = 0u;
 }
 
 // ---------------------------------------------------------------------------
@@ -255,7 +248,7 @@ template <int P, bool BF>
 __global__ void __launch_bounds__(512)
 k_fwd_pipe(const float* __restrict__ tc, const typename Elem<BF>::type* __restrict__ Cf,
            const float* __restrict__ bias_f, float* __restrict__ y, float* __restrict__ part,
-           unsigned* __restrict__ counters, Plan p, int sg_per_split) {
+           Plan p, int sg_per_split) {
   typedef FwdPipe<P, BF> K;
   typedef typename K::E E;
   typedef typename K::G G;
@@ -421,46 +414,151 @@ k_fwd_pipe(const float* __restrict__ tc, const typename Elem<BF>::type* __restri
     return;
   }
 
-  if (half == 0) {
+  if (half != 0) return;
+  // split-K: write the partial tile; k_fwd_reduce adds the splits in order
 #pragma unroll
-    for (int ni = 0; ni < NN; ++ni) {
-      const int nb = nb0 + ni;
-      if (nb >= p.NBf) continue;
-      const int o = nb * 32 + (lane & 31);
+  for (int ni = 0; ni < NN; ++ni) {
+    const int nb = nb0 + ni;
+    if (nb >= p.NBf) continue;
+    const int o = nb * 32 + (lane & 31);
 #pragma unroll
-      for (int mi = 0; mi < NM; ++mi) {
-        const int64_t r0 = m_blk + (wq * NM + mi) * 32;
+    for (int mi = 0; mi < NM; ++mi) {
+      const int64_t r0 = m_blk + (wq * NM + mi) * 32;
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int64_t r = r0 + acc_row(v, g);
-          if (r < p.B32) part[((size_t)blockIdx.z * p.B32 + r) * p.O32 + o] = acc[mi][ni][v];
+      for (int v = 0; v < 16; ++v) {
+        const int64_t r = r0 + acc_row(v, g);
+        if (r < p.B32) part[((size_t)blockIdx.z * p.B32 + r) * p.O32 + o] = acc[mi][ni][v];
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Forward, small batch (B <= 64): coefficient streaming.  The work is the
+// HBM stream of Cf; the MFMAs run at a few percent of their peak.  Each wave
+// takes one 32-output column block and SPW super-groups (16 k-blocks) of the
+// reduction and issues all of its loads at once: the coefficient fragments
+// straight into registers (one coalesced 1 KiB wave load per fragment, no
+// LDS) and its rows of x.  It computes tanh itself (writing the tanh cache
+// from the blocks of column block 0), builds its basis fragments, and
+// accumulates NMS x 32 rows.  The 4 waves of a block reduce through LDS and
+// write one partial tile; k_fwd_reduce adds the partials in order.
+// ---------------------------------------------------------------------------
+template <int P, bool BF> struct FwdStream {
+  typedef FwdGroup<P> G;
+  static constexpr int SPW = 16 / G::SGK;         // super-groups per wave
+  static constexpr int KPW = SPW * G::SGK;        // k-blocks per wave (16)
+  static constexpr int WAVES = 4;
+};
+
+template <int P, bool BF, int NMS>
+__global__ void __launch_bounds__(256)
+k_fwd_stream(const float* __restrict__ x, float* __restrict__ tc,
+             const typename Elem<BF>::type* __restrict__ Cf, float* __restrict__ part, Plan p,
+             int bpn) {
+  typedef FwdGroup<P> G;
+  typedef FwdStream<P, BF> K;
+  constexpr int SPW = K::SPW, KPW = K::KPW, LT = G::LANE_T;
+  __shared__ float red[K::WAVES][NMS * 32][33];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 5;
+  const int nb = blockIdx.x / bpn, blk = blockIdx.x - nb * bpn;
+  const int nsg = p.I_sg / G::SGI;
+  const int sg0 = (blk * K::WAVES + wave) * SPW;
+
+  // every load of this wave, in flight together
+  Frag<BF> bfr[KPW];
+#pragma unroll
+  for (int q = 0; q < KPW; ++q) {
+    const int sg = sg0 + q / G::SGK;
+    bfr[q] = (sg < nsg)
+        ? load_frag<BF>(Cf + ((size_t)nb * p.KB + (size_t)sg0 * G::SGK + q) * kFragElems, lane)
+        : zero_frag<BF>();
+  }
+  float xv[NMS][SPW][LT];
+  const bool xvec = (p.I & 3) == 0;  // LT is a multiple of 4, so are the lane offsets
+#pragma unroll
+  for (int mi = 0; mi < NMS; ++mi) {
+    const int r = mi * 32 + (lane & 31);
+#pragma unroll
+    for (int j = 0; j < SPW; ++j) {
+      const int i0 = (sg0 + j) * G::SGI + g * LT;
+      const float* xr = x + (size_t)r * p.I + i0;
+#pragma unroll
+      for (int q = 0; q < LT; q += 4) {
+        if (r < p.B && xvec && i0 + q + 4 <= p.I) {
+          const f32x4_t w = *reinterpret_cast<const f32x4_t*>(xr + q);
+          xv[mi][j][q] = w[0]; xv[mi][j][q + 1] = w[1]; xv[mi][j][q + 2] = w[2]; xv[mi][j][q + 3] = w[3];
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            xv[mi][j][q + e] = (r < p.B && i0 + q + e < p.I) ? xr[q + e] : 0.0f;
         }
       }
     }
   }
-  __threadfence();
-  __syncthreads();
-  // the ticket flag lives past the reduction tile in the (now idle) ring
-  unsigned* s_last = reinterpret_cast<unsigned*>(smem + K::RED_BYTES);
-  const unsigned tile_id = blockIdx.y * gridDim.x + blockIdx.x;
-  if (tid == 0) {
-    const unsigned prev = atomicAdd(&counters[tile_id], 1u);
-    *s_last = (prev == gridDim.z - 1) ? 1u : 0u;
+  f32x16_t acc[NMS];
+#pragma unroll
+  for (int mi = 0; mi < NMS; ++mi)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) acc[mi][v] = 0.0f;
+
+#pragma unroll
+  for (int mi = 0; mi < NMS; ++mi) {
+    const int r = mi * 32 + (lane & 31);
+#pragma unroll
+    for (int j = 0; j < SPW; ++j) {
+      const int sg = sg0 + j;
+      float tv[LT];
+#pragma unroll
+      for (int q = 0; q < LT; ++q) tv[q] = tanhf(xv[mi][j][q]);
+      if (nb == 0 && r < p.B && sg < nsg) {  // the tanh cache, written once
+        f32x4_t* dst = reinterpret_cast<f32x4_t*>(tc + (size_t)r * p.I_sg + (size_t)sg * G::SGI + g * LT);
+#pragma unroll
+        for (int q = 0; q < LT / 4; ++q)
+          dst[q] = f32x4_t{tv[4 * q], tv[4 * q + 1], tv[4 * q + 2], tv[4 * q + 3]};
+      }
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) {
+        float vals[8 * G::KBG];
+#pragma unroll
+        for (int u = 0; u < G::IPG / 2; ++u) cheb_T<P>(tv[s4 * (G::IPG / 2) + u], vals + u * P);
+#pragma unroll
+        for (int h = 0; h < G::KBG; ++h)
+          mma(acc[mi], make_frag<BF>(vals + 8 * h), bfr[j * G::SGK + s4 * G::KBG + h]);
+      }
+    }
   }
+
+  // reduce the 4 waves' tiles (valid rows only) and write this block's partial
+#pragma unroll
+  for (int mi = 0; mi < NMS; ++mi)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int r = mi * 32 + acc_row(v, g);
+      if (r < p.B) red[wave][r][lane & 31] = acc[mi][v];
+    }
   __syncthreads();
-  if (!*s_last) return;
-  __threadfence();
-  constexpr int BN = BNF * 32;
-  for (int idx = tid; idx < BM * BN; idx += TH) {
-    const int rl = idx / BN, cl = idx - rl * BN;
-    const int64_t r = m_blk + rl;
-    const int o = nb0 * 32 + cl;
-    if (r >= p.B || o >= p.O) continue;
-    float s = bias_f[o];
-    for (unsigned z = 0; z < gridDim.z; ++z) s += part[((size_t)z * p.B32 + r) * p.O32 + o];
-    y[r * p.O + o] = s;
+  const int nrow = p.B < NMS * 32 ? (int)p.B : NMS * 32;
+  for (int idx = tid; idx < nrow * 32; idx += 256) {
+    const int r = idx >> 5, c = idx & 31;
+    part[((size_t)blk * p.B32 + r) * p.O32 + nb * 32 + c] =
+        ((red[0][r][c] + red[1][r][c]) + red[2][r][c]) + red[3][r][c];
   }
-  if (tid == 0) counters[tile_id] = 0u;
+}
+
+// y[r, o] = bias[o] + sum_z part[z][r][o], z in split order.
+__global__ void __launch_bounds__(256)
+k_fwd_reduce(const float* __restrict__ part, int S, const float* __restrict__ bias_f,
+             float* __restrict__ y, Plan p) {
+  const int64_t n = p.B * (int64_t)p.O;
+  for (int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; q < n;
+       q += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = q / p.O;
+    const int o = (int)(q - r * p.O);
+    y[q] = split_sum(part + (size_t)r * p.O32 + o, (size_t)p.B32 * p.O32, (unsigned)S, bias_f[o]);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -876,9 +974,22 @@ static constexpr int kChipBlocks = 256;
 
 FwdChoice choose_fwd(const Plan& p) {
   FwdChoice c;
+  if (p.B <= 64) {
+    // coefficient streaming: one 4-wave block per 4 x SPW super-groups of a column block
+    const int spw = 16 / p.SGK;
+    const int nsg = p.I_sg / p.SGI;
+    c.tile = p.B <= 32 ? kFwdStream32 : kFwdStream64;
+    c.bm = p.B <= 32 ? 32 : 64;
+    c.bnf = 1;
+    c.tiles_m = 1;
+    c.tiles_n = p.NBf;
+    c.splits = (int)ceil_div(nsg, 4 * spw);  // blocks per column block
+    c.sg_per_split = 4 * spw;
+    return c;
+  }
   if (p.B <= 32) {
     c.tile = kFwdSmall32; c.bm = 32; c.bnf = 4;
-  } else if (p.B <= 64) {
+  } else if (p.B <= 64 || (p.B <= 512 && ceil_div(p.B, 256) * ceil_div(p.NBf, 4) < 64)) {
     c.tile = kFwdSmall64; c.bm = 64; c.bnf = 4;
   } else {
     c.tile = kFwdBig; c.bm = 256; c.bnf = 4;
@@ -890,7 +1001,8 @@ FwdChoice choose_fwd(const Plan& p) {
   const int target = (c.tile == kFwdBig) ? kChipBlocks : 2 * kChipBlocks;
   int splits = 1;
   if (tiles < target) splits = (int)ceil_div(target, tiles);
-  if (splits > nsg) splits = nsg;
+  const int max_splits = (int)ceil_div(nsg, 4);  // at least 4 super-groups per split
+  if (splits > max_splits) splits = max_splits;
   if (splits > 64) splits = 64;
   if (splits < 1) splits = 1;
   c.sg_per_split = (int)ceil_div(nsg, splits);
@@ -900,56 +1012,66 @@ FwdChoice choose_fwd(const Plan& p) {
 }
 
 template <int P, bool BF>
-static void fwd_dispatch(const float* t, const void* packed, float* y, void* ws, const Plan& p,
-                         const FwdChoice& c, hipStream_t s) {
+static void fwd_dispatch(const float* x, float* t, const void* packed, float* y, void* ws,
+                         const Plan& p, const FwdChoice& c, hipStream_t s) {
   typedef typename Elem<BF>::type E;
   const E* Cf = reinterpret_cast<const E*>(packed);
   const float* bias =
       reinterpret_cast<const float*>(reinterpret_cast<const char*>(packed) + packed_biasf_offset(p));
-  unsigned* counters = nullptr;
-  float* part = nullptr;
-  if (c.splits > 1) {
-    counters = reinterpret_cast<unsigned*>(ws);
-    part = reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + fwd_counters_bytes(c));
+  float* part = reinterpret_cast<float*>(ws);
+  const bool split = c.splits > 1 || fwd_streaming(c);
+  if (fwd_streaming(c)) {
+    dim3 g1(c.tiles_n * c.splits);
+    if (c.tile == kFwdStream32)
+      hipLaunchKernelGGL((k_fwd_stream<P, BF, 1>), g1, dim3(256), 0, s, x, t, Cf, part, p, c.splits);
+    else
+      hipLaunchKernelGGL((k_fwd_stream<P, BF, 2>), g1, dim3(256), 0, s, x, t, Cf, part, p, c.splits);
+  } else {
+    dim3 grid(c.tiles_m, c.tiles_n, c.splits);
+    switch (c.tile) {
+      case kFwdSmall32:
+        hipLaunchKernelGGL((k_fwd<P, BF, 1, 1, 1, 4>), grid, dim3(256), 0, s, t, Cf, bias, y, part,
+                           p, c.sg_per_split);
+        break;
+      case kFwdSmall64:
+        hipLaunchKernelGGL((k_fwd<P, BF, 2, 1, 1, 4>), grid, dim3(256), 0, s, t, Cf, bias, y, part,
+                           p, c.sg_per_split);
+        break;
+      default:
+        if constexpr (FwdPipe<P, BF>::kOk) {
+          typedef FwdPipe<P, BF> K;
+          const size_t lds = (size_t)K::LDS_BYTES;
+          static bool attr_set = false;  // one-time raise of the dynamic LDS limit
+          if (!attr_set) {
+            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fwd_pipe<P, BF>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+            attr_set = true;
+          }
+          hipLaunchKernelGGL((k_fwd_pipe<P, BF>), grid, dim3(K::THREADS), lds, s, t, Cf, bias, y,
+                             part, p, c.sg_per_split);
+        } else {
+          hipLaunchKernelGGL((k_fwd<P, BF, 2, 4, 4, 1>), grid, dim3(256), 0, s, t, Cf, bias, y,
+                             part, p, c.sg_per_split);
+        }
+        break;
+    }
   }
-  dim3 grid(c.tiles_m, c.tiles_n, c.splits);
-  switch (c.tile) {
-    case kFwdSmall32:
-      hipLaunchKernelGGL((k_fwd<P, BF, 1, 1, 1, 4>), grid, dim3(256), 0, s, t, Cf, bias, y, part,
-                         counters, p, c.sg_per_split);
-      break;
-    case kFwdSmall64:
-      hipLaunchKernelGGL((k_fwd<P, BF, 2, 1, 1, 4>), grid, dim3(256), 0, s, t, Cf, bias, y, part,
-                         counters, p, c.sg_per_split);
-      break;
-    default:
-      if constexpr (FwdPipe<P, BF>::kOk) {
-      typedef FwdPipe<P, BF> K;
-      const size_t lds = (size_t)K::LDS_BYTES;
-      static bool attr_set = false;  // one-time raise of the dynamic LDS limit
-      if (!attr_set) {
-        hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fwd_pipe<P, BF>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        attr_set = true;
-      }
-      hipLaunchKernelGGL((k_fwd_pipe<P, BF>), grid, dim3(K::THREADS), lds, s, t, Cf, bias, y, part,
-                         counters, p, c.sg_per_split);
-      } else {
-        hipLaunchKernelGGL((k_fwd<P, BF, 2, 4, 4, 1>), grid, dim3(256), 0, s, t, Cf, bias, y,
-                           part, counters, p, c.sg_per_split);
-      }
-      break;
+  if (split) {
+    const int64_t n = p.B * (int64_t)p.O;
+    int64_t gsz = (n + 255) / 256;
+    if (gsz > 65536) gsz = 65536;
+    hipLaunchKernelGGL(k_fwd_reduce, dim3((unsigned)gsz), dim3(256), 0, s, part, c.splits, bias, y, p);
   }
 }
 
-void launch_fwd_gemm(const float* t, const void* packed, float* y, void* ws, const Plan& p,
-                     const FwdChoice& c, hipStream_t s) {
+void launch_fwd_gemm(const float* x, float* t, const void* packed, float* y, void* ws,
+                     const Plan& p, const FwdChoice& c, hipStream_t s) {
   const bool bf = p.esz == 2;
   switch (p.P) {
-    case 2: bf ? fwd_dispatch<2, true>(t, packed, y, ws, p, c, s) : fwd_dispatch<2, false>(t, packed, y, ws, p, c, s); break;
-    case 4: bf ? fwd_dispatch<4, true>(t, packed, y, ws, p, c, s) : fwd_dispatch<4, false>(t, packed, y, ws, p, c, s); break;
-    case 8: bf ? fwd_dispatch<8, true>(t, packed, y, ws, p, c, s) : fwd_dispatch<8, false>(t, packed, y, ws, p, c, s); break;
-    default: bf ? fwd_dispatch<16, true>(t, packed, y, ws, p, c, s) : fwd_dispatch<16, false>(t, packed, y, ws, p, c, s); break;
+    case 2: bf ? fwd_dispatch<2, true>(x, t, packed, y, ws, p, c, s) : fwd_dispatch<2, false>(x, t, packed, y, ws, p, c, s); break;
+    case 4: bf ? fwd_dispatch<4, true>(x, t, packed, y, ws, p, c, s) : fwd_dispatch<4, false>(x, t, packed, y, ws, p, c, s); break;
+    case 8: bf ? fwd_dispatch<8, true>(x, t, packed, y, ws, p, c, s) : fwd_dispatch<8, false>(x, t, packed, y, ws, p, c, s); break;
+    default: bf ? fwd_dispatch<16, true>(x, t, packed, y, ws, p, c, s) : fwd_dispatch<16, false>(x, t, packed, y, ws, p, c, s); break;
   }
 }
 
@@ -969,7 +1091,7 @@ static void dx_dispatch(const void* dYx, const void* packed, const float* t, flo
     const size_t lds = (size_t)K::NBUF * K::STAGE_BYTES;
     static bool attr_set = false;
     if (!attr_set) {
-      hipFuncSetAttribute(reinterpret_cast<const void*>(&k_dx_pipe<P, BF>),
+      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_dx_pipe<P, BF>),
                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
       attr_set = true;
     }

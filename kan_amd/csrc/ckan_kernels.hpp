@@ -27,7 +27,7 @@ inline size_t packed_bytes(const Plan& p) {
 
 // ---- forward: tile configuration and split-K -------------------------------
 // Tile shapes (waves along M x waves along N, fragments per wave M x N):
-enum FwdTile { kFwdBig = 0, kFwdSmall32 = 1, kFwdSmall64 = 2 };
+enum FwdTile { kFwdBig = 0, kFwdSmall32 = 1, kFwdSmall64 = 2, kFwdStream32 = 3, kFwdStream64 = 4 };
 struct FwdChoice {
   int tile;           // FwdTile
   int bm, bnf;        // block rows, block N fragments
@@ -35,12 +35,11 @@ struct FwdChoice {
   int splits, sg_per_split;
 };
 FwdChoice choose_fwd(const Plan& p);
-inline size_t fwd_counters_bytes(const FwdChoice& c) {
-  return c.splits > 1 ? align256((size_t)c.tiles_m * c.tiles_n * sizeof(unsigned)) : 0;
-}
+inline bool fwd_streaming(const FwdChoice& c) { return c.tile == kFwdStream32 || c.tile == kFwdStream64; }
+// split-K partials [splits][B32][O32] fp32, summed in order by k_fwd_reduce
 inline size_t fwd_ws_bytes(const Plan& p, const FwdChoice& c) {
-  if (c.splits <= 1) return 0;
-  return fwd_counters_bytes(c) + align256((size_t)c.splits * p.B32 * p.O32 * sizeof(float));
+  if (c.splits <= 1 && !fwd_streaming(c)) return 0;
+  return align256((size_t)c.splits * p.B32 * p.O32 * sizeof(float));
 }
 
 // ---- backward workspace: [dYx][dYc][colsum partials][dC split partials] ----
@@ -57,8 +56,10 @@ void launch_prep_dy(const float* dy, void* dYx, void* dYc, float* colsum_part, c
                     bool need_dx, bool need_dc, hipStream_t s);
 void launch_dc_finalize(const float* part, int S, float* colsum_part, float* dC,
                         bool accumulate, const Plan& p, hipStream_t s);
-void launch_fwd_gemm(const float* t, const void* packed, float* y, void* ws, const Plan& p,
-                     const FwdChoice& c, hipStream_t s);
+// x is read only by the small-batch streaming kernel, which also writes t;
+// the other paths read t written by launch_tanh.
+void launch_fwd_gemm(const float* x, float* t, const void* packed, float* y, void* ws,
+                     const Plan& p, const FwdChoice& c, hipStream_t s);
 void launch_dx_gemm(const void* dYx, const void* packed, const float* t, float* dx,
                     const Plan& p, hipStream_t s);
 void launch_dc_gemm(const void* dYc, const float* t, float* part, const Plan& p,
