@@ -12,6 +12,8 @@
 // recurrence; in dC the block builds the basis operand once per stage into
 // LDS.  The coefficient operands are pre-packed fragment-major and staged
 // through LDS with a register double buffer (one barrier per stage).
+#include <type_traits>
+
 #include "ckan_kernels.hpp"
 
 namespace ckan {
@@ -315,10 +317,16 @@ k_fwd_pipe(const float* __restrict__ tc, const typename Elem<BF>::type* __restri
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[mi][ni][v] = 0.0f;
 
+  // One super-group of this wave's rows.  Software-pipelined one k-block
+  // ahead: the B fragments of k-block k+1 are read from LDS and the basis
+  // fragments of the next sub-step generated (VALU) while the MFMAs of
+  // k-block k run; scheduling barriers keep that order and interleave the
+  // generation with the MFMAs.
   auto compute = [&](int slot) __attribute__((always_inline)) {
     const char* base = smem + slot * K::STAGE_BYTES;
     const float* tl = reinterpret_cast<const float*>(base + K::B_BYTES);
     const E* bl = reinterpret_cast<const E*>(base);
+    constexpr int SGK = G::SGK, KBG = G::KBG;
     float tv[NM][G::LANE_T];
 #pragma unroll
     for (int mi = 0; mi < NM; ++mi) {
@@ -331,26 +339,44 @@ k_fwd_pipe(const float* __restrict__ tc, const typename Elem<BF>::type* __restri
         tv[mi][4 * q + 2] = w[2]; tv[mi][4 * q + 3] = w[3];
       }
     }
+    Frag<BF> bq[2][NN];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      Frag<BF> af[NM][G::KBG];
+    for (int ni = 0; ni < NN; ++ni) bq[0][ni] = load_frag<BF>(bl + (ni * SGK) * kFragElems, lane);
+    Frag<BF> af[2][NM][KBG];
+    auto gen = [&](int s, Frag<BF> (&dst)[NM][KBG]) __attribute__((always_inline)) {
 #pragma unroll
       for (int mi = 0; mi < NM; ++mi) {
-        float vals[8 * G::KBG];
+        float vals[8 * KBG];
 #pragma unroll
         for (int u = 0; u < G::IPG / 2; ++u) cheb_T<P>(tv[mi][s * (G::IPG / 2) + u], vals + u * P);
 #pragma unroll
-        for (int h = 0; h < G::KBG; ++h) af[mi][h] = make_frag<BF>(vals + 8 * h);
+        for (int h = 0; h < KBG; ++h) dst[mi][h] = make_frag<BF>(vals + 8 * h);
       }
+    };
+    gen(0, af[0]);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int h = 0; h < G::KBG; ++h) {
-        const int kbl = s * G::KBG + h;
+    for (int s = 0; s < 4; ++s) {
 #pragma unroll
-        for (int ni = 0; ni < NN; ++ni) {
-          const Frag<BF> bfr = load_frag<BF>(bl + (ni * G::SGK + kbl) * kFragElems, lane);
+      for (int h = 0; h < KBG; ++h) {
+        const int kbl = s * KBG + h;
+        if (kbl + 1 < SGK) {
 #pragma unroll
-          for (int mi = 0; mi < NM; ++mi) mma(acc[mi][ni], af[mi][h], bfr);
+          for (int ni = 0; ni < NN; ++ni)
+            bq[(kbl + 1) & 1][ni] = load_frag<BF>(bl + (ni * SGK + kbl + 1) * kFragElems, lane);
         }
+        __builtin_amdgcn_sched_barrier(0);
+        if (h == KBG - 1 && s < 3) gen(s + 1, af[(s + 1) & 1]);
+#pragma unroll
+        for (int ni = 0; ni < NN; ++ni)
+#pragma unroll
+          for (int mi = 0; mi < NM; ++mi) mma(acc[mi][ni], af[s & 1][mi][h], bq[kbl & 1][ni]);
+#pragma unroll
+        for (int q = 0; q < NN * NM; ++q) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+          __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // then up to four VALU
+        }
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
   };
@@ -368,68 +394,71 @@ k_fwd_pipe(const float* __restrict__ tc, const typename Elem<BF>::type* __restri
     if (sg0 + 2 * j + half < sg1) compute((j % NPB) * 2 + half);
   }
 
-  // sum the two halves' tiles through LDS (the ring is free once all waves
-  // pass the barrier); every barrier below is reached by all 8 waves
+  // Sum the two halves' tiles through LDS (the ring is free once all waves
+  // pass the barrier).  Each half keeps NN/2 column blocks: it hands the
+  // other half's column blocks over, adds the ones it receives, and stores
+  // its own, so all 8 waves share the stores.  Every barrier is reached by
+  // all 8 waves.
+  constexpr int NH = NN / 2;
   wait_lgkmcnt<0>();
   block_barrier();
   float* red = reinterpret_cast<float*>(smem);
-  if (half == 1) {
+  auto red_at = [&](int giver, int mi, int j, int v) __attribute__((always_inline)) {
+    return red + ((((giver * 4 + wq) * NM + mi) * NH + j) * 16 + v) * 64 + lane;
+  };
+  auto exchange = [&](auto KEEP) __attribute__((always_inline)) {
+    constexpr int keep0 = decltype(KEEP)::value, give0 = NH - keep0;
 #pragma unroll
     for (int mi = 0; mi < NM; ++mi)
 #pragma unroll
-      for (int ni = 0; ni < NN; ++ni)
+      for (int j = 0; j < NH; ++j)
 #pragma unroll
-        for (int v = 0; v < 16; ++v)
-          red[(((wq * NM + mi) * NN + ni) * 16 + v) * 64 + lane] = acc[mi][ni][v];
-  }
-  __syncthreads();
-  if (half == 0) {
+        for (int v = 0; v < 16; ++v) *red_at(half, mi, j, v) = acc[mi][give0 + j][v];
+    wait_lgkmcnt<0>();
+    block_barrier();
 #pragma unroll
     for (int mi = 0; mi < NM; ++mi)
 #pragma unroll
-      for (int ni = 0; ni < NN; ++ni)
+      for (int j = 0; j < NH; ++j)
 #pragma unroll
-        for (int v = 0; v < 16; ++v)
-          acc[mi][ni][v] += red[(((wq * NM + mi) * NN + ni) * 16 + v) * 64 + lane];
-  }
-
+        for (int v = 0; v < 16; ++v) acc[mi][keep0 + j][v] += *red_at(half ^ 1, mi, j, v);
+  };
   const bool split = gridDim.z > 1;
-  if (!split) {
-    if (half != 0) return;
+  const bool full_rows = m_blk + BM <= (split ? p.B32 : p.B);
+  auto store = [&](auto KEEP) __attribute__((always_inline)) {
+    constexpr int keep0 = decltype(KEEP)::value;
 #pragma unroll
-    for (int ni = 0; ni < NN; ++ni) {
-      const int o = (nb0 + ni) * 32 + (lane & 31);
-      if (o >= p.O) continue;
-      const float bias = bias_f[o];
+    for (int j = 0; j < NH; ++j) {
+      const int nb = nb0 + keep0 + j;
+      const int o = nb * 32 + (lane & 31);
+      if (split ? nb >= p.NBf : o >= p.O) continue;
+      const float add = split ? 0.0f : bias_f[o];
+      const int64_t pitch = split ? p.O32 : p.O;
+      const int64_t nrow = split ? p.B32 : p.B;
+      float* out = split ? part + (size_t)blockIdx.z * p.B32 * p.O32 : y;
 #pragma unroll
       for (int mi = 0; mi < NM; ++mi) {
-        const int64_t r0 = m_blk + (wq * NM + mi) * 32;
+        const int64_t r0 = m_blk + (wq * NM + mi) * 32 + 4 * g;
+        float* op = out + r0 * pitch + o;
+        if (full_rows) {
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int64_t r = r0 + acc_row(v, g);
-          if (r < p.B) y[r * p.O + o] = acc[mi][ni][v] + bias;
+          for (int v = 0; v < 16; ++v) op[(8 * (v >> 2) + (v & 3)) * pitch] = acc[mi][keep0 + j][v] + add;
+        } else {
+#pragma unroll
+          for (int v = 0; v < 16; ++v)
+            if (r0 + 8 * (v >> 2) + (v & 3) < nrow)
+              op[(8 * (v >> 2) + (v & 3)) * pitch] = acc[mi][keep0 + j][v] + add;
         }
       }
     }
-    return;
-  }
-
-  if (half != 0) return;
-  // split-K: write the partial tile; k_fwd_reduce adds the splits in order
-#pragma unroll
-  for (int ni = 0; ni < NN; ++ni) {
-    const int nb = nb0 + ni;
-    if (nb >= p.NBf) continue;
-    const int o = nb * 32 + (lane & 31);
-#pragma unroll
-    for (int mi = 0; mi < NM; ++mi) {
-      const int64_t r0 = m_blk + (wq * NM + mi) * 32;
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int64_t r = r0 + acc_row(v, g);
-        if (r < p.B32) part[((size_t)blockIdx.z * p.B32 + r) * p.O32 + o] = acc[mi][ni][v];
-      }
-    }
+  };
+  // split-K blocks write partial tiles; k_fwd_reduce adds the splits in order
+  if (half == 0) {
+    exchange(std::integral_constant<int, 0>{});
+    store(std::integral_constant<int, 0>{});
+  } else {
+    exchange(std::integral_constant<int, NH>{});
+    store(std::integral_constant<int, NH>{});
   }
 }
 
