@@ -222,14 +222,22 @@ int ckan_backward(const ckan_desc* desc, const float* t_cache, const void* packe
   }
   if ((rc = check_launch("dx_gemm"))) return rc;
   if (need_dc) {
+    const float* colsum_r = nullptr;
+    {
+      ProfScope ps("colsum", s);
+      colsum_r = launch_colsum_reduce(colsum, p, s);
+    }
     {
       ProfScope ps("dc_gemm", s);
-      launch_dc_gemm(dYc, t_cache, part, p, L, s);
+      launch_dc_gemm(dYc, t_cache, colsum_r, part, dcoeffs, accumulate != 0, p, L, s);
     }
     if ((rc = check_launch("dc_gemm"))) return rc;
-    {
+    if (!L.dc_pipe) {
       ProfScope ps("dc_finalize", s);
-      launch_dc_finalize(part, L.dc_splits, colsum, dcoeffs, accumulate != 0, p, s);
+      launch_dc_finalize(part, L.dc_splits, colsum_r, dcoeffs, accumulate != 0, p, s);
+    } else if (L.dc_splits > 1) {
+      ProfScope ps("dc_finalize", s);
+      launch_dc_sum(part, L.dc_splits, dcoeffs, accumulate != 0, p, s);
     }
     if ((rc = check_launch("dc_finalize"))) return rc;
   }

@@ -447,20 +447,45 @@ void launch_prep_dy(const float* dy, void* dYx, void* dYc, float* colsum_part, c
                        colsum_part, p, (int)need_dx, (int)need_dc, nob, nbb, dx_rows);
 }
 
-void launch_dc_finalize(const float* part, int S, float* colsum_part, float* dC,
-                        bool accumulate, const Plan& p, hipStream_t s) {
-  // column sums of dy: reduce the per-row-block partials in place into row 0
+float* launch_colsum_reduce(float* colsum_part, const Plan& p, hipStream_t s) {
   float* colsum = colsum_part + (size_t)p.NBB * p.O32;
   hipLaunchKernelGGL(k_col_reduce, dim3((unsigned)ceil_div(p.O32, 64)), dim3(256), 0, s,
                      colsum_part, p.NBB, p.O32, p.O32, colsum);
-  const float* colsum_part_r = colsum;
+  return colsum;
+}
+
+void launch_dc_finalize(const float* part, int S, const float* colsum, float* dC,
+                        bool accumulate, const Plan& p, hipStream_t s) {
   dim3 grid((unsigned)ceil_div(p.I, 16), (unsigned)ceil_div(p.O, 64));
   switch (p.P) {
-    case 2: hipLaunchKernelGGL((k_dc_finalize<2>), grid, dim3(256), 0, s, part, S, colsum_part_r, dC, (int)accumulate, p); break;
-    case 4: hipLaunchKernelGGL((k_dc_finalize<4>), grid, dim3(256), 0, s, part, S, colsum_part_r, dC, (int)accumulate, p); break;
-    case 8: hipLaunchKernelGGL((k_dc_finalize<8>), grid, dim3(256), 0, s, part, S, colsum_part_r, dC, (int)accumulate, p); break;
-    default: hipLaunchKernelGGL((k_dc_finalize<16>), grid, dim3(256), 0, s, part, S, colsum_part_r, dC, (int)accumulate, p); break;
+    case 2: hipLaunchKernelGGL((k_dc_finalize<2>), grid, dim3(256), 0, s, part, S, colsum, dC, (int)accumulate, p); break;
+    case 4: hipLaunchKernelGGL((k_dc_finalize<4>), grid, dim3(256), 0, s, part, S, colsum, dC, (int)accumulate, p); break;
+    case 8: hipLaunchKernelGGL((k_dc_finalize<8>), grid, dim3(256), 0, s, part, S, colsum, dC, (int)accumulate, p); break;
+    default: hipLaunchKernelGGL((k_dc_finalize<16>), grid, dim3(256), 0, s, part, S, colsum, dC, (int)accumulate, p); break;
   }
+}
+
+// dC[q] (=|+=) sum_z part[z][q], z in split order (slices of I*O*D floats).
+__global__ void __launch_bounds__(256)
+k_dc_sum(const float* __restrict__ part, int S, float* __restrict__ dC, int64_t n, int accumulate) {
+  for (int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; q < n;
+       q += (int64_t)gridDim.x * blockDim.x) {
+    float acc = accumulate ? dC[q] : 0.0f;
+    int z = 0;
+    for (; z + 4 <= S; z += 4) {
+      const float a = part[(size_t)z * n + q], b = part[(size_t)(z + 1) * n + q];
+      const float c = part[(size_t)(z + 2) * n + q], d = part[(size_t)(z + 3) * n + q];
+      acc = (((acc + a) + b) + c) + d;
+    }
+    for (; z < S; ++z) acc += part[(size_t)z * n + q];
+    dC[q] = acc;
+  }
+}
+
+void launch_dc_sum(const float* part, int S, float* dC, bool accumulate, const Plan& p,
+                   hipStream_t s) {
+  const int64_t n = (int64_t)p.I * p.O * p.D;
+  hipLaunchKernelGGL(k_dc_sum, dim3(grid_for(n)), dim3(256), 0, s, part, S, dC, n, (int)accumulate);
 }
 
 void launch_sgd(float* p, const float* g, int64_t n, float lr, float wd, hipStream_t s) {

@@ -995,6 +995,288 @@ k_dc(const typename Elem<BF>::type* __restrict__ dYc, const float* __restrict__ 
 }
 
 // ---------------------------------------------------------------------------
+// dC, pipelined: dC[i, o, d] = sum_b T_d(t[b, i]) dy[b, o] for d >= 1.
+// One block = 8 waves: two halves that take alternate stages of KI k-blocks
+// (16 batch rows each) of the reduction; in a half, wave (dh, og) accumulates
+// PH = P/2 degrees (dh) x NN output fragments (og) for the block's 32 inputs.
+// Both streamed operands arrive by LDS DMA, with no vector-register loads in
+// the loop: tanh tiles three pairs of stages ahead, dy fragments two pairs
+// ahead.  The basis operand (P fragments per k-block) is generated from the
+// tanh tile into LDS one pair ahead, interleaved with the MFMAs.  The halves'
+// tiles are summed through LDS, then each output group is staged as
+// [input][output][degree] (d = 0 from the reduced dy column sums) so that the
+// block writes contiguous runs of dC, or of its split-K slice.
+// ---------------------------------------------------------------------------
+template <int P, bool BF>
+struct DcPipe {
+  typedef typename Elem<BF>::type E;
+  static constexpr int PH = P / 2;
+  static constexpr int NN = PH >= 8 ? 1 : (8 / PH > 4 ? 4 : 8 / PH);
+  static constexpr int NO = 2 * NN;  // output fragments per block
+  static constexpr int NF = PH * NN;  // accumulator fragments per wave
+  static constexpr int KI = (BF && P != 2 && P != 16) ? 2 : 1;
+  static constexpr int FB = kFragElems * (int)sizeof(E);
+  static constexpr int BAS_STAGE = P * KI * FB;
+  static constexpr int DY_STAGE = NO * KI * FB;
+  static constexpr int DY_CHUNKS = 2 * DY_STAGE / 16;             // real chunks per pair
+  static constexpr int DY_OPS = (DY_CHUNKS + 511) / 512;          // dma16 per thread per pair
+  static constexpr int DY_SLOT = DY_OPS * 8192;                   // bytes per pair slot
+  static constexpr int T_STAGE = KI * 16 * 32 * 4;                // tanh rows x 32 inputs
+  static constexpr int T_CHUNKS = 2 * T_STAGE / 16;
+  static constexpr int T_SLOT = 8192;                             // one dma16 per thread
+  static constexpr int BAS_BYTES = 2 * 2 * BAS_STAGE;             // two pairs of stages
+  static constexpr int MAIN_BYTES = BAS_BYTES + 3 * DY_SLOT + 3 * T_SLOT;
+  static constexpr int XCH_BYTES = 8 * (NF / 2) * 16 * 64 * 4;
+  static constexpr int STG_BYTES = 32 * NN * 32 * (P + 1) * 4;
+  static constexpr int LDS_BYTES = MAIN_BYTES > XCH_BYTES
+      ? (MAIN_BYTES > STG_BYTES ? MAIN_BYTES : STG_BYTES)
+      : (XCH_BYTES > STG_BYTES ? XCH_BYTES : STG_BYTES);
+  static constexpr int RPT = 2 * KI;  // batch rows per generating thread
+  static constexpr bool kOk = LDS_BYTES <= 160 * 1024 && T_CHUNKS <= 512 && NF % 2 == 0;
+};
+
+template <int P, bool BF>
+__global__ void __launch_bounds__(512)
+k_dc_pipe(const typename Elem<BF>::type* __restrict__ dYc, const float* __restrict__ tc,
+          const float* __restrict__ colsum, float* __restrict__ out, Plan p, int st_per_split,
+          int accumulate) {
+  typedef DcPipe<P, BF> K;
+  typedef typename K::E E;
+  constexpr int PH = K::PH, NN = K::NN, NO = K::NO, NF = K::NF, KI = K::KI, FB = K::FB;
+  constexpr int RPT = K::RPT, DY_OPS = K::DY_OPS;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int half = wave >> 2, wq = wave & 3, dh = wq & 1, og = wq >> 1;
+  const int g = lane >> 5;
+  const int ib = blockIdx.x, obk = blockIdx.y;
+  const int nst_all = (int)(p.KBc / KI);
+  const int st0 = blockIdx.z * st_per_split;
+  const int st1 = min(nst_all, st0 + st_per_split);
+  const int npair = (st1 - st0) / 2;  // split stage counts are even
+  char* bas = smem;
+  char* dyr = smem + K::BAS_BYTES;
+  char* tlr = dyr + 3 * K::DY_SLOT;
+
+  // dy DMA: chunk c < DY_CHUNKS of a pair is [stage hs][fragment f][k-block kk][16 B];
+  // chunks past that repeat real ones into the unused end of the slot
+  constexpr int CPF = FB / 16;
+  const char* dyb = reinterpret_cast<const char*>(dYc);
+  size_t doff[DY_OPS];
+  int dhs[DY_OPS];
+#pragma unroll
+  for (int q = 0; q < DY_OPS; ++q) {
+    const int c = (q * 512 + tid) % K::DY_CHUNKS;
+    const int hs = c / (NO * KI * CPF), r1 = c - hs * (NO * KI * CPF);
+    const int f = r1 / (KI * CPF), r2 = r1 - f * (KI * CPF);
+    const int kk = r2 / CPF, piece = r2 - kk * CPF;
+    const int mf = min(obk * NO + f, p.NBf - 1);
+    dhs[q] = hs;
+    doff[q] = ((size_t)mf * p.KBc + kk) * FB + (size_t)piece * 16;
+  }
+  // tanh DMA: chunk c = tid % T_CHUNKS is [stage hs][row rr][16 B of the 32 inputs]
+  const int tcn = tid % K::T_CHUNKS;
+  const int ths = tcn / (K::T_STAGE / 16), trr = (tcn % (K::T_STAGE / 16)) / 8;
+  const int tcol = min(ib * 32 + (tcn % 8) * 4, p.I_sg - 4);  // inputs past I_sg: never stored
+  const char* tcb = reinterpret_cast<const char*>(tc);
+  auto dma_dy = [&](int j) __attribute__((always_inline)) {
+    char* dst = dyr + (j % 3) * K::DY_SLOT + wave * 1024;
+#pragma unroll
+    for (int q = 0; q < DY_OPS; ++q) {
+      int st = st0 + 2 * j + dhs[q];
+      if (st >= st1) st = st0;  // past the end: any in-range source, never read
+      dma16(dyb + doff[q] + (size_t)st * KI * FB, dst + q * 8192);
+    }
+  };
+  auto dma_t = [&](int j) __attribute__((always_inline)) {
+    int st = st0 + 2 * j + ths;
+    if (st >= st1) st = st0;
+    int64_t b = (int64_t)st * KI * 16 + trr;
+    if (b >= p.B) b = p.B - 1;  // dy is zero on rows past B
+    dma16(tcb + ((size_t)b * p.I_sg + tcol) * 4, tlr + (j % 3) * K::T_SLOT + wave * 1024);
+  };
+
+  // basis generation slot of this thread within its half: k-block gkk,
+  // fragment lane gl, rows grh*RPT .. +RPT of the lane's 8
+  const int th = tid & 255;
+  const int gslot = th % (KI * 64), gkk = gslot / 64, gl = gslot % 64;
+  const int grh = th / (KI * 64);
+  const int trow0 = gkk * 16 + 8 * (gl >> 5) + grh * RPT;
+  auto gen = [&](int j) __attribute__((always_inline)) {
+    const float* tl = reinterpret_cast<const float*>(tlr + (j % 3) * K::T_SLOT + half * K::T_STAGE);
+    float tv[RPT];
+#pragma unroll
+    for (int r = 0; r < RPT; ++r) tv[r] = tl[(trow0 + r) * 32 + (gl & 31)];
+    char* dst = bas + ((j & 1) * 2 + half) * K::BAS_STAGE + gkk * FB + (gl * 8 + grh * RPT) * (int)sizeof(E);
+    float a[RPT], b[RPT], t2[RPT];
+#pragma unroll
+    for (int r = 0; r < RPT; ++r) { a[r] = 1.0f; b[r] = tv[r]; t2[r] = tv[r] + tv[r]; }
+#pragma unroll
+    for (int e = 0; e < P; ++e) {
+      if (e > 0) {
+#pragma unroll
+        for (int r = 0; r < RPT; ++r) {
+          const float n = fmaf(t2[r], b[r], -a[r]);
+          a[r] = b[r];
+          b[r] = n;
+        }
+      }
+      char* d = dst + e * KI * FB;
+      if constexpr (BF) {
+        if constexpr (RPT == 4) {
+          bf16x4_t w;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) w[r] = (__bf16)b[r];
+          *reinterpret_cast<bf16x4_t*>(d) = w;
+        } else {
+          bf16x2_t w;
+#pragma unroll
+          for (int r = 0; r < 2; ++r) w[r] = (__bf16)b[r];
+          *reinterpret_cast<bf16x2_t*>(d) = w;
+        }
+      } else {
+        *reinterpret_cast<f32x2_t*>(d) = f32x2_t{b[0], b[1]};
+      }
+    }
+  };
+
+  f32x16_t acc[PH][NN];
+#pragma unroll
+  for (int e = 0; e < PH; ++e)
+#pragma unroll
+    for (int ni = 0; ni < NN; ++ni)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[e][ni][v] = 0.0f;
+
+  // One pair step of this wave: the fragments of all KI k-blocks of its stage
+  // are read from LDS up front, and the basis generation for the next pair
+  // (VALU + LDS traffic) is interleaved with the MFMAs.
+  auto step = [&](int j) __attribute__((always_inline)) {
+    const E* ab = reinterpret_cast<const E*>(bas + ((j & 1) * 2 + half) * K::BAS_STAGE) +
+                  (size_t)(dh * PH) * KI * kFragElems;
+    const E* bb = reinterpret_cast<const E*>(dyr + (j % 3) * K::DY_SLOT + half * K::DY_STAGE) +
+                  (size_t)(og * NN) * KI * kFragElems;
+    Frag<BF> fa[KI][PH], fb[KI][NN];
+#pragma unroll
+    for (int kk = 0; kk < KI; ++kk) {
+#pragma unroll
+      for (int e = 0; e < PH; ++e) fa[kk][e] = load_frag<BF>(ab + (e * KI + kk) * kFragElems, lane);
+#pragma unroll
+      for (int ni = 0; ni < NN; ++ni) fb[kk][ni] = load_frag<BF>(bb + (ni * KI + kk) * kFragElems, lane);
+      __builtin_amdgcn_sched_barrier(0);  // k-block order of the reads (LDS returns in order)
+    }
+    gen(j + 1);
+#pragma unroll
+    for (int kk = 0; kk < KI; ++kk)
+#pragma unroll
+      for (int e = 0; e < PH; ++e)
+#pragma unroll
+        for (int ni = 0; ni < NN; ++ni) mma(acc[e][ni], fa[kk][e], fb[kk][ni]);
+#pragma unroll
+    for (int q = 0; q < KI * PH * NN; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // up to four VALU
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // up to one LDS read
+      __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // up to one LDS write
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // prologue: tanh tiles of pairs 0..2, dy of pairs 0..1, basis of pair 0.
+  // Every pair issues 1 + DY_OPS DMA ops per thread in the order t(j+3),
+  // dy(j+2); past the end they fetch in-range data that is never read.
+  constexpr int OPS = 1 + DY_OPS;
+  dma_t(0);
+  dma_t(1);
+  dma_dy(0);
+  dma_t(2);
+  dma_dy(1);
+  wait_vmcnt<2 * OPS>();  // t(0) landed
+  block_barrier();
+  gen(0);
+  for (int j = 0; j < npair; ++j) {
+    // dy(j) and t(j+1) have landed once only the ops of pair j+1's
+    // issue step (t(j+2), dy(j+1)) may be in flight
+    wait_vmcnt<OPS>();
+    wait_lgkmcnt<0>();  // this thread's basis writes for pair j are done
+    block_barrier();
+    dma_t(j + 3);
+    dma_dy(j + 2);
+    step(j);  // also generates pair j+1 (unused after the last pair)
+  }
+  wait_vmcnt<0>();  // the prefetches past the end land before the LDS is reused
+
+  // halves' exchange: half 0 keeps fragments [0, NF/2), half 1 the rest
+  wait_lgkmcnt<0>();
+  block_barrier();
+  float* xch = reinterpret_cast<float*>(smem);
+  auto xat = [&](int giver, int fj, int v) __attribute__((always_inline)) {
+    return xch + (((giver * 4 + wq) * (NF / 2) + fj) * 16 + v) * 64 + lane;
+  };
+  auto exchange = [&](auto KEEP) __attribute__((always_inline)) {
+    constexpr int keep0 = decltype(KEEP)::value, give0 = NF / 2 - keep0;
+#pragma unroll
+    for (int fj = 0; fj < NF / 2; ++fj)
+#pragma unroll
+      for (int v = 0; v < 16; ++v)
+        *xat(half, fj, v) = acc[(give0 + fj) / NN][(give0 + fj) % NN][v];
+    wait_lgkmcnt<0>();
+    block_barrier();
+#pragma unroll
+    for (int fj = 0; fj < NF / 2; ++fj)
+#pragma unroll
+      for (int v = 0; v < 16; ++v)
+        acc[(keep0 + fj) / NN][(keep0 + fj) % NN][v] += *xat(half ^ 1, fj, v);
+  };
+  // staging of output group c: [32 inputs][NN*32 outputs][D degrees]
+  float* stg = reinterpret_cast<float*>(smem);
+  constexpr int OW = NN * 32;
+  auto stage_own = [&](auto KEEP) __attribute__((always_inline)) {
+    constexpr int keep0 = decltype(KEEP)::value;
+#pragma unroll
+    for (int fj = 0; fj < NF / 2; ++fj) {
+      const int e = (keep0 + fj) / NN, ni = (keep0 + fj) % NN;
+      const int d = dh * PH + e + 1;
+      if (d > p.deg) continue;
+      const int ol = ni * 32 + (lane & 31);
+#pragma unroll
+      for (int v = 0; v < 16; ++v) stg[(acc_row(v, g) * OW + ol) * p.D + d] = acc[e][ni][v];
+    }
+  };
+  float* outz = out + (size_t)blockIdx.z * p.I * p.O * p.D;
+  const int ivalid = min(32, p.I - ib * 32);
+  if (half == 0) exchange(std::integral_constant<int, 0>{});
+  else exchange(std::integral_constant<int, NF / 2>{});
+#pragma unroll 1
+  for (int c = 0; c < 2; ++c) {
+    const int o0 = (obk * NO + c * NN) * 32;
+    const int ovalid = min(OW, p.O - o0);
+    block_barrier();  // previous readers of the LDS are done
+    if (og == c) {
+      if (half == 0) stage_own(std::integral_constant<int, 0>{});
+      else stage_own(std::integral_constant<int, NF / 2>{});
+    }
+    for (int q = tid; q < 32 * OW; q += 512) {
+      const int il = q / OW, ol = q - il * OW;
+      stg[q * p.D] = (blockIdx.z == 0 && ol < ovalid) ? colsum[o0 + ol] : 0.0f;
+    }
+    wait_lgkmcnt<0>();
+    block_barrier();
+    if (ovalid > 0) {
+      const int run = ovalid * p.D;  // contiguous floats per input row
+      for (int il = 0; il < ivalid; ++il) {
+        float* dst = outz + ((size_t)(ib * 32 + il) * p.O + o0) * p.D;
+        const float* src = stg + il * OW * p.D;
+        for (int k = tid; k < run; k += 512) {
+          const float v = src[k];
+          dst[k] = accumulate ? dst[k] + v : v;
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Host-side configuration and launchers
 // ---------------------------------------------------------------------------
 
@@ -1147,6 +1429,31 @@ void launch_dx_gemm(const void* dYx, const void* packed, const float* t, float* 
 // dC stage depth in k-blocks: 4 for bf16, 2 for fp32 (LDS bound).
 template <bool BF> struct DcKI { static constexpr int v = BF ? 4 : 2; };
 
+static bool dc_pipe_ok(const Plan& p) {
+  const bool bf = p.esz == 2;
+  switch (p.P) {
+    case 2: return bf ? DcPipe<2, true>::kOk : DcPipe<2, false>::kOk;
+    case 4: return bf ? DcPipe<4, true>::kOk : DcPipe<4, false>::kOk;
+    case 8: return bf ? DcPipe<8, true>::kOk : DcPipe<8, false>::kOk;
+    default: return bf ? DcPipe<16, true>::kOk : DcPipe<16, false>::kOk;
+  }
+}
+
+// output fragments per dC block and k-blocks per stage of the pipelined kernel
+template <int P, bool BF> static void dc_shape_t(int& no, int& ki) {
+  no = DcPipe<P, BF>::NO;
+  ki = DcPipe<P, BF>::KI;
+}
+static void dc_pipe_shape(const Plan& p, int& no, int& ki) {
+  const bool bf = p.esz == 2;
+  switch (p.P) {
+    case 2: bf ? dc_shape_t<2, true>(no, ki) : dc_shape_t<2, false>(no, ki); break;
+    case 4: bf ? dc_shape_t<4, true>(no, ki) : dc_shape_t<4, false>(no, ki); break;
+    case 8: bf ? dc_shape_t<8, true>(no, ki) : dc_shape_t<8, false>(no, ki); break;
+    default: bf ? dc_shape_t<16, true>(no, ki) : dc_shape_t<16, false>(no, ki); break;
+  }
+}
+
 BwdLayout bwd_layout(const Plan& p, bool need_dx, bool need_dc) {
   BwdLayout L;
   size_t off = 0;
@@ -1159,7 +1466,23 @@ BwdLayout bwd_layout(const Plan& p, bool need_dx, bool need_dc) {
   L.part_off = off;
   L.dc_splits = 1;
   L.dc_st_per_split = 0;
-  if (need_dc) {
+  L.dc_pipe = need_dc && dc_pipe_ok(p);
+  if (need_dc && L.dc_pipe) {
+    int no, ki;
+    dc_pipe_shape(p, no, ki);
+    const int64_t tiles = (int64_t)p.NIB * ceil_div(p.NBf, no);
+    const int nst = (int)(p.KBc / ki);
+    int splits = 1;
+    if (tiles < kChipBlocks) splits = (int)ceil_div(kChipBlocks, tiles);
+    const int max_splits = nst / 4 > 1 ? nst / 4 : 1;  // at least two pairs of stages each
+    if (splits > max_splits) splits = max_splits;
+    if (splits > 64) splits = 64;
+    if (splits < 1) splits = 1;
+    // even stage counts per split (nst is even: Bc is a multiple of 64 rows)
+    L.dc_st_per_split = (int)round_up(ceil_div(nst, splits), 2);
+    L.dc_splits = (int)ceil_div(nst, L.dc_st_per_split);
+    if (L.dc_splits > 1) off += align256((size_t)L.dc_splits * p.I * p.O * p.D * sizeof(float));
+  } else if (need_dc) {
     const int nm = bwd_nm(p.P);
     const int64_t tiles = ceil_div(p.NBf, 4 * nm) * (int64_t)p.NIB;
     const int nst = (int)(p.KBc / (p.esz == 2 ? DcKI<true>::v : DcKI<false>::v));
@@ -1178,24 +1501,44 @@ BwdLayout bwd_layout(const Plan& p, bool need_dx, bool need_dc) {
 }
 
 template <int P, bool BF>
-static void dc_dispatch(const void* dYc, const float* t, float* part, const Plan& p,
-                        const BwdLayout& L, hipStream_t s) {
+static void dc_dispatch(const void* dYc, const float* t, const float* colsum, float* part,
+                        float* dC, bool accumulate, const Plan& p, const BwdLayout& L,
+                        hipStream_t s) {
   typedef typename Elem<BF>::type E;
+  if constexpr (DcPipe<P, BF>::kOk) {
+    if (L.dc_pipe) {
+      typedef DcPipe<P, BF> K;
+      static bool attr_set = false;  // one-time raise of the dynamic LDS limit
+      if (!attr_set) {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_dc_pipe<P, BF>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, K::LDS_BYTES);
+        attr_set = true;
+      }
+      const bool split = L.dc_splits > 1;
+      dim3 grid(p.NIB, (unsigned)ceil_div(p.NBf, K::NO), L.dc_splits);
+      hipLaunchKernelGGL((k_dc_pipe<P, BF>), grid, dim3(512), K::LDS_BYTES, s,
+                         reinterpret_cast<const E*>(dYc), t, colsum, split ? part : dC, p,
+                         L.dc_st_per_split, (!split && accumulate) ? 1 : 0);
+      return;
+    }
+  }
   constexpr int NM = BwdTile<P>::NM;
   dim3 grid((unsigned)ceil_div(p.NBf, 4 * NM), p.NIB, L.dc_splits);
   hipLaunchKernelGGL((k_dc<P, BF, NM, DcKI<BF>::v>), grid, dim3(256), 0, s,
                      reinterpret_cast<const E*>(dYc), t, part, p, L.dc_st_per_split);
 }
 
-void launch_dc_gemm(const void* dYc, const float* t, float* part, const Plan& p,
-                    const BwdLayout& L, hipStream_t s) {
+void launch_dc_gemm(const void* dYc, const float* t, const float* colsum, float* part, float* dC,
+                    bool accumulate, const Plan& p, const BwdLayout& L, hipStream_t s) {
   const bool bf = p.esz == 2;
+#define CKAN_DC(PP, BB) dc_dispatch<PP, BB>(dYc, t, colsum, part, dC, accumulate, p, L, s)
   switch (p.P) {
-    case 2: bf ? dc_dispatch<2, true>(dYc, t, part, p, L, s) : dc_dispatch<2, false>(dYc, t, part, p, L, s); break;
-    case 4: bf ? dc_dispatch<4, true>(dYc, t, part, p, L, s) : dc_dispatch<4, false>(dYc, t, part, p, L, s); break;
-    case 8: bf ? dc_dispatch<8, true>(dYc, t, part, p, L, s) : dc_dispatch<8, false>(dYc, t, part, p, L, s); break;
-    default: bf ? dc_dispatch<16, true>(dYc, t, part, p, L, s) : dc_dispatch<16, false>(dYc, t, part, p, L, s); break;
+    case 2: bf ? CKAN_DC(2, true) : CKAN_DC(2, false); break;
+    case 4: bf ? CKAN_DC(4, true) : CKAN_DC(4, false); break;
+    case 8: bf ? CKAN_DC(8, true) : CKAN_DC(8, false); break;
+    default: bf ? CKAN_DC(16, true) : CKAN_DC(16, false); break;
   }
+#undef CKAN_DC
 }
 
 }  // namespace ckan

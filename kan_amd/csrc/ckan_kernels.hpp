@@ -43,9 +43,13 @@ inline size_t fwd_ws_bytes(const Plan& p, const FwdChoice& c) {
 }
 
 // ---- backward workspace: [dYx][dYc][colsum partials][dC split partials] ----
+// dc_pipe: the pipelined dC kernel writes dC (dc_splits == 1) or split slices
+// [split][I][O][D] summed by launch_dc_sum; otherwise partials
+// [split][P][I32][O32] go through launch_dc_finalize.
 struct BwdLayout {
   size_t dyx_off, dyc_off, colsum_off, part_off, total;
   int dc_splits, dc_st_per_split;
+  bool dc_pipe;
 };
 BwdLayout bwd_layout(const Plan& p, bool need_dx, bool need_dc);
 
@@ -54,16 +58,20 @@ void launch_tanh(const float* x, float* t, const Plan& p, hipStream_t s);
 void launch_pack(const void* C, bool c_bf16, void* packed, const Plan& p, hipStream_t s);
 void launch_prep_dy(const float* dy, void* dYx, void* dYc, float* colsum_part, const Plan& p,
                     bool need_dx, bool need_dc, hipStream_t s);
-void launch_dc_finalize(const float* part, int S, float* colsum_part, float* dC,
+// reduces the dy column-sum partials into row NBB and returns that row
+float* launch_colsum_reduce(float* colsum_part, const Plan& p, hipStream_t s);
+void launch_dc_finalize(const float* part, int S, const float* colsum, float* dC,
                         bool accumulate, const Plan& p, hipStream_t s);
+void launch_dc_sum(const float* part, int S, float* dC, bool accumulate, const Plan& p,
+                   hipStream_t s);
 // x is read only by the small-batch streaming kernel, which also writes t;
 // the other paths read t written by launch_tanh.
 void launch_fwd_gemm(const float* x, float* t, const void* packed, float* y, void* ws,
                      const Plan& p, const FwdChoice& c, hipStream_t s);
 void launch_dx_gemm(const void* dYx, const void* packed, const float* t, float* dx,
                     const Plan& p, hipStream_t s);
-void launch_dc_gemm(const void* dYc, const float* t, float* part, const Plan& p,
-                    const BwdLayout& L, hipStream_t s);
+void launch_dc_gemm(const void* dYc, const float* t, const float* colsum, float* part, float* dC,
+                    bool accumulate, const Plan& p, const BwdLayout& L, hipStream_t s);
 void launch_sgd(float* p, const float* g, int64_t n, float lr, float wd, hipStream_t s);
 void launch_adam(float* p, const float* g, float* m, float* v, int64_t n, float w1, float beta2,
                  float one_m_beta2, float bc2_sqrt, float eps, float neg_step, float wd,
