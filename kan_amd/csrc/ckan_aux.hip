@@ -140,7 +140,8 @@ k_pack(const CT* __restrict__ C, typename Elem<BF>::type* __restrict__ Cf,
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int ol = 16 * kbl + 8 * g + j;
-      v[j] = (e + 1 <= p.deg) ? tile[il * RP + ol * D + e + 1] : 0.0f;
+      // scaled by the degree d = e + 1, the factor of dT_d/dt = d U_{d-1}(t)
+      v[j] = (e + 1 <= p.deg) ? tile[il * RP + ol * D + e + 1] * (float)(e + 1) : 0.0f;
     }
     store_frag<BF>(Cb + ((size_t)(ib * P + e) * p.KBx + kbx) * kFragElems, lane, v);
   }

@@ -733,7 +733,7 @@ k_dx_pipe(const typename Elem<BF>::type* __restrict__ dYx,
       float up = 0.0f, u = 1.0f, sum = 0.0f;  // U_{-1}, U_0
 #pragma unroll
       for (int e = 0; e < P; ++e) {
-        sum = fmaf(acc[mi][e][v] * (float)(e + 1), u, sum);
+        sum = fmaf(acc[mi][e][v], u, sum);
         const float un = fmaf(t2, u, -up);
         up = u;
         u = un;
@@ -741,6 +741,185 @@ k_dx_pipe(const typename Elem<BF>::type* __restrict__ dYx,
       if (icol && r < p.B) dx[r * p.I + i] = sum * (1.0f - tv[v] * tv[v]);
     }
   }
+}
+
+// ---------------------------------------------------------------------------
+// dX, two resident blocks per CU.  One block = 4 waves (dh, rg): wave rg takes
+// NM = 2 fragments of 32 rows, wave dh half of the P degrees, for one input
+// block (32 inputs); acc = NM x P/2 fragments, so two blocks share a CU and
+// one block's epilogue overlaps the other's MFMAs.  Both operands (dy rows and
+// the degree-scaled coefficients) arrive by LDS DMA in a ring of NBUF stages
+// of KI k-blocks.  Epilogue: each wave sums its degrees with U_{d-1}(t), the
+// dh pair exchanges halves through LDS, and each wave stores one fragment row
+// of dx = (1 - t^2) sum_d d C U_{d-1}(t) dy.
+// ---------------------------------------------------------------------------
+template <int P, bool BF>
+struct DxTwo {
+  typedef typename Elem<BF>::type E;
+  static constexpr int NM = 2, PH = P / 2;
+  static constexpr int FB = kFragElems * (int)sizeof(E);
+  static constexpr int KI_BF = (P == 16) ? 1 : 2;
+  static constexpr int KI = BF ? KI_BF : 1;
+  static constexpr int A_BYTES = 2 * NM * KI * FB;  // 4 row fragments
+  static constexpr int B_BYTES = P * KI * FB;
+  static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
+  static constexpr int NBUF = 3;
+  static constexpr int LDS_BYTES = NBUF * STAGE_BYTES;
+  static constexpr int OPS = STAGE_BYTES / 4096;  // dma16 per thread per stage
+  static constexpr int A_OPS = A_BYTES / 4096;
+  static constexpr bool kOk = P >= 2 && P <= 8 && LDS_BYTES <= 80 * 1024 && A_BYTES % 4096 == 0 &&
+                              B_BYTES % 4096 == 0 && 2 * 16 * 64 * 4 * 4 <= LDS_BYTES;
+};
+
+template <int P, bool BF>
+__global__ void __launch_bounds__(256, 2)
+k_dx_two(const typename Elem<BF>::type* __restrict__ dYx,
+         const typename Elem<BF>::type* __restrict__ Cb, const float* __restrict__ tc,
+         float* __restrict__ dx, Plan p, int n_rb) {
+  typedef DxTwo<P, BF> K;
+  typedef typename K::E E;
+  constexpr int NM = K::NM, PH = K::PH, KI = K::KI, FB = K::FB, NBUF = K::NBUF, OPS = K::OPS;
+  constexpr int RUN = KI * FB / 16;  // 16-byte chunks per fragment run of a stage
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int dh = wave & 1, rg = wave >> 1;
+  const int g = lane >> 5;
+  const int nst = p.KBx / KI;
+  const int rb = blockIdx.x % n_rb, ib = blockIdx.x / n_rb;
+
+  // per-op source offsets; dYx rows are padded to whole row blocks
+  const char* abase = reinterpret_cast<const char*>(dYx) + (size_t)rb * 2 * NM * p.KBx * FB;
+  const char* bbase = reinterpret_cast<const char*>(Cb) + (size_t)ib * P * p.KBx * FB;
+  size_t off[OPS];
+#pragma unroll
+  for (int q = 0; q < OPS; ++q) {
+    const int c = q * 256 + tid;
+    if (q < K::A_OPS) {
+      const int run = c / RUN, w = c - run * RUN;
+      off[q] = (size_t)run * p.KBx * FB + w * 16;
+    } else {
+      const int cc = c - K::A_OPS * 256;
+      const int e = cc / RUN, w = cc - e * RUN;
+      off[q] = (size_t)e * p.KBx * FB + w * 16;
+    }
+  }
+  auto issue = [&](int st) __attribute__((always_inline)) {
+    if (st >= nst) st = nst - 1;  // past the end: in-range data, never read
+    const size_t sb = (size_t)st * KI * FB;
+    char* dst = smem + (st % NBUF) * K::STAGE_BYTES + wave * 1024;
+#pragma unroll
+    for (int q = 0; q < OPS; ++q) dma16((q < K::A_OPS ? abase : bbase) + sb + off[q], dst + q * 4096);
+  };
+
+  // epilogue tanh values, loaded up front (they complete long before use)
+  const int i = ib * 32 + (lane & 31);
+  const bool icol = i < p.I;
+  float tt[NM][16];
+#pragma unroll
+  for (int mi = 0; mi < NM; ++mi) {
+    const int64_t r0 = ((int64_t)rb * 2 * NM + rg * NM + mi) * 32 + 4 * g;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int64_t r = r0 + 8 * (v >> 2) + (v & 3);
+      tt[mi][v] = (icol && r < p.B) ? tc[r * p.I_sg + i] : 0.0f;
+    }
+  }
+
+  f32x16_t acc[NM][PH];
+#pragma unroll
+  for (int mi = 0; mi < NM; ++mi)
+#pragma unroll
+    for (int e = 0; e < PH; ++e)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[mi][e][v] = 0.0f;
+
+  // the stage that empties slot (st % NBUF) is consumed before the barrier of
+  // stage st + 1; the refill of that slot is issued after it
+#pragma unroll
+  for (int q = 0; q < NBUF - 1; ++q) issue(q);
+  for (int st = 0; st < nst; ++st) {
+    wait_vmcnt<OPS * (NBUF - 2)>();  // stage st landed (st+1 may be in flight)
+    block_barrier();
+    issue(st + NBUF - 1);
+    const char* base = smem + (st % NBUF) * K::STAGE_BYTES;
+    Frag<BF> fa[KI][NM], fb[KI][PH];
+#pragma unroll
+    for (int kk = 0; kk < KI; ++kk) {
+#pragma unroll
+      for (int mi = 0; mi < NM; ++mi)
+        fa[kk][mi] = load_frag<BF>(reinterpret_cast<const E*>(base + ((rg * NM + mi) * KI + kk) * FB), lane);
+#pragma unroll
+      for (int e = 0; e < PH; ++e)
+        fb[kk][e] = load_frag<BF>(reinterpret_cast<const E*>(base + K::A_BYTES + ((dh * PH + e) * KI + kk) * FB), lane);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int kk = 0; kk < KI; ++kk)
+#pragma unroll
+      for (int mi = 0; mi < NM; ++mi)
+#pragma unroll
+        for (int e = 0; e < PH; ++e) mma(acc[mi][e], fa[kk][mi], fb[kk][e]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  wait_vmcnt<0>();
+  wait_lgkmcnt<0>();
+  block_barrier();  // the ring is free
+
+  // partial sums over this wave's degrees d = dh*PH + e + 1 (weights U_{d-1})
+  float part[NM][16];
+#pragma unroll
+  for (int mi = 0; mi < NM; ++mi)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const float t2 = tt[mi][v] + tt[mi][v];
+      float up = 0.0f, u = 1.0f;  // U_{-1}, U_0; advanced to U_{dh*PH}
+#pragma unroll
+      for (int k = 0; k < PH; ++k) {
+        const float un = fmaf(t2, u, -up);
+        up = dh ? u : up;
+        u = dh ? un : u;
+      }
+      float sum = 0.0f;
+#pragma unroll
+      for (int e = 0; e < PH; ++e) {
+        sum = fmaf(acc[mi][e][v], u, sum);
+        const float un = fmaf(t2, u, -up);
+        up = u;
+        u = un;
+      }
+      part[mi][v] = sum;
+    }
+  // wave (dh, rg) keeps fragment row mi = dh and hands mi = 1 - dh to its pair
+  float* xch = reinterpret_cast<float*>(smem);
+  auto finish = [&](auto DH) __attribute__((always_inline)) {
+    constexpr int d = decltype(DH)::value, keep = d, give = 1 - d;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) xch[((rg * 2 + d) * 16 + v) * 64 + lane] = part[give][v];
+    wait_lgkmcnt<0>();
+    block_barrier();
+    const int64_t r0 = ((int64_t)rb * 2 * NM + rg * NM + keep) * 32 + 4 * g;
+    float res[16];
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const float other = xch[((rg * 2 + (d ^ 1)) * 16 + v) * 64 + lane];
+      const float t = tt[keep][v];
+      // fixed order: the lower degrees' half first
+      const float sum = d ? other + part[keep][v] : part[keep][v] + other;
+      res[v] = sum * (1.0f - t * t);
+    }
+    float* dp = dx + r0 * p.I + i;
+    if (icol && r0 - 4 * g + 32 <= p.B) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) dp[(int64_t)(8 * (v >> 2) + (v & 3)) * p.I] = res[v];
+    } else if (icol) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v)
+        if (r0 + 8 * (v >> 2) + (v & 3) < p.B) dp[(int64_t)(8 * (v >> 2) + (v & 3)) * p.I] = res[v];
+    }
+  };
+  if (dh) finish(std::integral_constant<int, 1>{});
+  else finish(std::integral_constant<int, 0>{});
 }
 
 // ---------------------------------------------------------------------------
@@ -851,7 +1030,7 @@ k_dx(const typename Elem<BF>::type* __restrict__ dYx, const typename Elem<BF>::t
       float up = 0.0f, u = 1.0f, s = 0.0f;  // U_{-1}, U_0
 #pragma unroll
       for (int e = 0; e < P; ++e) {
-        s = fmaf(acc[mi][e][v] * (float)(e + 1), u, s);
+        s = fmaf(acc[mi][e][v], u, s);
         const float un = fmaf(t2, u, -up);
         up = u;
         u = un;
@@ -1395,6 +1574,19 @@ static void dx_dispatch(const void* dYx, const void* packed, const float* t, flo
   typedef typename Elem<BF>::type E;
   constexpr int NM = BwdTile<P>::NM;
   const E* Cb = reinterpret_cast<const E*>(packed) + packed_cf_elems(p);
+  if constexpr (DxTwo<P, BF>::kOk) {
+    typedef DxTwo<P, BF> K;
+    const int n_rb = (int)ceil_div(p.B32 / 32, 2 * K::NM);
+    static bool attr_set = false;
+    if (!attr_set) {
+      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_dx_two<P, BF>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, K::LDS_BYTES);
+      attr_set = true;
+    }
+    hipLaunchKernelGGL((k_dx_two<P, BF>), dim3(n_rb * p.NIB), dim3(256), K::LDS_BYTES, s,
+                       reinterpret_cast<const E*>(dYx), Cb, t, dx, p, n_rb);
+    return;
+  }
   if constexpr (DxPipe<P, BF>::kOk) {
     typedef DxPipe<P, BF> K;
     const int n_rb = (int)ceil_div(p.B32 / 32, K::WGM * NM);

@@ -11,7 +11,10 @@ inline size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 // Sets the thread-local message returned by ckan_last_error().
 void set_last_error(const char* msg);
 
-// ---- packed coefficients: [Cf][Cb][bias partials] -------------------------
+// ---- packed coefficients: [Cf][Cb][bias partials][bias] -------------------
+// Cf: forward B operand, C[i, o, d] for d >= 1 by (input, degree) k-blocks.
+// Cb: dX B operand, d * C[i, o, d] (the factor of dT_d/dt = d U_{d-1}) by
+// (input block, degree) and output k-blocks.
 inline size_t packed_cf_elems(const Plan& p) { return (size_t)p.NBf * p.KB * kFragElems; }
 inline size_t packed_cb_elems(const Plan& p) { return (size_t)p.NIB * p.P * p.KBx * kFragElems; }
 inline size_t packed_bias_offset(const Plan& p) {
