@@ -208,17 +208,33 @@ def _cpu_baseline(sample_rows: int, reps: int):
     }
 
 
+def _traffic(kernel: str, compute: str):
+    """HBM bytes per launch of `kernel` from the committed counter summary
+    (rocprofv3 FETCH_SIZE and WRITE_SIZE passes over this benchmark, each
+    scaled by the same counter's reading on a plain copy of known size), or
+    None when no summary for this kernel and precision is present."""
+    path = os.path.join(ROOT, "profiles", f"traffic_cfg3_{compute}.json")
+    try:
+        with open(path) as f:
+            data = json.load(f)
+        return data["kernels"][kernel]["hbm_bytes"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--compute", default="bf16", choices=["bf16", "fp32"])
     ap.add_argument("--cpu-rows", type=int, default=1024)
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-fp32", action="store_true")
     ap.add_argument("--no-suite", action="store_true", help="skip configs 1, 2, 4, 5")
+    ap.add_argument("--copy-calib-mib", type=int, default=0,
+                    help="run a plain device copy of this many MiB first (counter calibration)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -238,6 +254,15 @@ def main():
     layer = layer.to(dev)
     x = torch.randn(B, I, generator=g).to(dev).requires_grad_(True)
     dy = torch.randn(B, O, generator=g).to(dev)
+
+    if args.copy_calib_mib > 0:
+        # a plain elementwise copy of known size: reads and writes N MiB once
+        n = args.copy_calib_mib * (1 << 20) // 4
+        src = torch.rand(n, device=dev)
+        dst = torch.empty_like(src)
+        torch.mul(src, 1.0, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
 
     ms = _time_gpu(layer, x, dy, args.steps, args.warmup)
     kernels = _kernel_breakdown(layer, x, dy, args.steps)
@@ -284,7 +309,7 @@ def main():
             "peak": peak,
             "unit": "TFLOP/s",
             "frac": achieved / peak,
-            "traffic": None,
+            "traffic": _traffic(dom, args.compute),
         },
         "kernels_avg_ms": {k: round(v["avg_ms"], 5) for k, v in kernels.items()},
         **extra,
