@@ -1176,8 +1176,9 @@ k_dc(const typename Elem<BF>::type* __restrict__ dYc, const float* __restrict__ 
 // ---------------------------------------------------------------------------
 // dC, pipelined: dC[i, o, d] = sum_b T_d(t[b, i]) dy[b, o] for d >= 1.
 // One block = 8 waves: two halves that take alternate stages of KI k-blocks
-// (16 batch rows each) of the reduction; in a half, wave (dh, og) accumulates
-// PH = P/2 degrees (dh) x NN output fragments (og) for the block's 32 inputs.
+// (16 batch rows each) of the reduction; in a half, wave (dq, og) accumulates
+// PH = min(P, 4) degrees (group dq) x NN output fragments (group og) for the
+// block's 32 inputs, always 8 accumulator fragments.
 // Both streamed operands arrive by LDS DMA, with no vector-register loads in
 // the loop: tanh tiles three pairs of stages ahead, dy fragments two pairs
 // ahead.  The basis operand (P fragments per k-block) is generated from the
@@ -1189,10 +1190,12 @@ k_dc(const typename Elem<BF>::type* __restrict__ dYc, const float* __restrict__ 
 template <int P, bool BF>
 struct DcPipe {
   typedef typename Elem<BF>::type E;
-  static constexpr int PH = P / 2;
-  static constexpr int NN = PH >= 8 ? 1 : (8 / PH > 4 ? 4 : 8 / PH);
-  static constexpr int NO = 2 * NN;  // output fragments per block
-  static constexpr int NF = PH * NN;  // accumulator fragments per wave
+  static constexpr int PH = P < 4 ? P : 4;  // degrees per wave
+  static constexpr int DQ = P / PH;         // degree groups in a half
+  static constexpr int OG = 4 / DQ;         // output groups in a half
+  static constexpr int NN = 8 / PH;         // output fragments per wave
+  static constexpr int NO = OG * NN;        // output fragments per block
+  static constexpr int NF = PH * NN;        // accumulator fragments per wave (8)
   static constexpr int KI = (BF && P != 2 && P != 16) ? 2 : 1;
   static constexpr int FB = kFragElems * (int)sizeof(E);
   static constexpr int BAS_STAGE = P * KI * FB;
@@ -1206,7 +1209,7 @@ struct DcPipe {
   static constexpr int BAS_BYTES = 2 * 2 * BAS_STAGE;             // two pairs of stages
   static constexpr int MAIN_BYTES = BAS_BYTES + 3 * DY_SLOT + 3 * T_SLOT;
   static constexpr int XCH_BYTES = 8 * (NF / 2) * 16 * 64 * 4;
-  static constexpr int STG_BYTES = 32 * NN * 32 * (P + 1) * 4;
+  static constexpr int STG_BYTES = 32 * NN * 32 * (P + 1) * 4;  // one output group
   static constexpr int LDS_BYTES = MAIN_BYTES > XCH_BYTES
       ? (MAIN_BYTES > STG_BYTES ? MAIN_BYTES : STG_BYTES)
       : (XCH_BYTES > STG_BYTES ? XCH_BYTES : STG_BYTES);
@@ -1221,12 +1224,13 @@ k_dc_pipe(const typename Elem<BF>::type* __restrict__ dYc, const float* __restri
           int accumulate) {
   typedef DcPipe<P, BF> K;
   typedef typename K::E E;
-  constexpr int PH = K::PH, NN = K::NN, NO = K::NO, NF = K::NF, KI = K::KI, FB = K::FB;
+  constexpr int PH = K::PH, DQ = K::DQ, OG = K::OG, NN = K::NN, NO = K::NO, NF = K::NF;
+  constexpr int KI = K::KI, FB = K::FB;
   constexpr int RPT = K::RPT, DY_OPS = K::DY_OPS;
   extern __shared__ __attribute__((aligned(16))) char smem[];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int half = wave >> 2, wq = wave & 3, dh = wq & 1, og = wq >> 1;
+  const int half = wave >> 2, wq = wave & 3, dh = wq % DQ, og = wq / DQ;
   const int g = lane >> 5;
   const int ib = blockIdx.x, obk = blockIdx.y;
   const int nst_all = (int)(p.KBc / KI);
@@ -1427,7 +1431,7 @@ k_dc_pipe(const typename Elem<BF>::type* __restrict__ dYc, const float* __restri
   if (half == 0) exchange(std::integral_constant<int, 0>{});
   else exchange(std::integral_constant<int, NF / 2>{});
 #pragma unroll 1
-  for (int c = 0; c < 2; ++c) {
+  for (int c = 0; c < OG; ++c) {
     const int o0 = (obk * NO + c * NN) * 32;
     const int ovalid = min(OW, p.O - o0);
     block_barrier();  // previous readers of the LDS are done
