@@ -222,14 +222,16 @@ int ckan_backward(const ckan_desc* desc, const float* t_cache, const void* packe
   }
   if ((rc = check_launch("dx_gemm"))) return rc;
   if (need_dc) {
+    // the pipelined dC kernel reduces the column-sum partials itself
     const float* colsum_r = nullptr;
-    {
+    if (!L.dc_pipe) {
       ProfScope ps("colsum", s);
       colsum_r = launch_colsum_reduce(colsum, p, s);
     }
     {
       ProfScope ps("dc_gemm", s);
-      launch_dc_gemm(dYc, t_cache, colsum_r, part, dcoeffs, accumulate != 0, p, L, s);
+      launch_dc_gemm(dYc, t_cache, L.dc_pipe ? colsum : colsum_r, part, dcoeffs,
+                     accumulate != 0, p, L, s);
     }
     if ((rc = check_launch("dc_gemm"))) return rc;
     if (!L.dc_pipe) {

@@ -183,29 +183,31 @@ __device__ __forceinline__ void load_row8(const float* __restrict__ dy, int64_t 
 // Re-lays dy [B, O] (fp32) into
 //   dYx: dX A operand  [B32/32][KBx][64][8]  (rows b, reduction o)
 //   dYc: dC B operand  [NBf][KBc][64][8]     (columns o, reduction b)
-// and writes colsum_part[bb][o] = sum of dy over rows [256 bb, 256 bb + 256).
-// One wave per (32 columns, 256 rows); each fragment lane reads its 8 values
-// straight from dy (a 32-byte row run for dYx, one coalesced 128-byte row
-// segment per value for dYc) and writes one 16- or 32-byte vector.
+// and writes colsum_part[bb][o] = sum of dy over rows [64 bb, 64 bb + 64).
+// One wave per (32 columns, 64 rows).  The wave reads its tile of dy once
+// (each lane 8 consecutive columns of a row: the dYx fragment layout) and,
+// when dYc is needed, transposes it through LDS for the dYc fragments (each
+// lane 8 consecutive rows of a column).
 template <bool BF>
 __global__ void __launch_bounds__(256)
 k_prep_dy(const float* __restrict__ dy, typename Elem<BF>::type* __restrict__ dYx,
           typename Elem<BF>::type* __restrict__ dYc, float* __restrict__ colsum_part,
           Plan p, int need_dx, int need_dc, int nob, int nbb, int64_t dx_rows) {
-  const int lane = threadIdx.x & 63;
-  const int w = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (w >= nob * nbb) return;
+  constexpr int TP = 33;  // padded row pitch of the transpose tile
+  __shared__ float tile[4][kPrepRows * TP];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int w = blockIdx.x * 4 + wv;
+  if (w >= nob * nbb) return;  // whole waves only: no block barrier below
   const int ob = w % nob, bb = w / nob;
   const int g = lane >> 5, c = lane & 31;
   const int64_t r0 = (int64_t)bb * kPrepRows;
+  float v[kPrepRows / 32][2][8];
+#pragma unroll
+  for (int mbl = 0; mbl < kPrepRows / 32; ++mbl)
+#pragma unroll
+    for (int kbl = 0; kbl < 2; ++kbl)
+      load_row8(dy, r0 + mbl * 32 + c, ob * 32 + 16 * kbl + 8 * g, p, v[mbl][kbl]);
   if (need_dx) {
-    // all loads of the wave's rows first, then the conversions and stores
-    float v[kPrepRows / 32][2][8];
-#pragma unroll
-    for (int mbl = 0; mbl < kPrepRows / 32; ++mbl)
-#pragma unroll
-      for (int kbl = 0; kbl < 2; ++kbl)
-        load_row8(dy, r0 + mbl * 32 + c, ob * 32 + 16 * kbl + 8 * g, p, v[mbl][kbl]);
 #pragma unroll
     for (int mbl = 0; mbl < kPrepRows / 32; ++mbl) {
       const int64_t b0 = r0 + mbl * 32;
@@ -217,27 +219,32 @@ k_prep_dy(const float* __restrict__ dy, typename Elem<BF>::type* __restrict__ dY
     }
   }
   if (need_dc && ob < p.NBf) {
-    const int o = ob * 32 + c;
-    const bool ocol = o < p.O;
-    float v[kPrepRows / 16][8];
+    float* t = tile[wv];
+#pragma unroll
+    for (int mbl = 0; mbl < kPrepRows / 32; ++mbl)
+#pragma unroll
+      for (int kbl = 0; kbl < 2; ++kbl)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) t[(mbl * 32 + c) * TP + 16 * kbl + 8 * g + j] = v[mbl][kbl][j];
+    // the tile is private to this wave, whose LDS accesses are performed in
+    // issue order; the compiler barrier keeps the reads after the writes
+    asm volatile("" ::: "memory");
+    float u[kPrepRows / 16][8];
 #pragma unroll
     for (int kbl = 0; kbl < kPrepRows / 16; ++kbl)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int64_t b = r0 + kbl * 16 + 8 * g + j;
-        v[kbl][j] = (ocol && b < p.B) ? dy[b * p.O + o] : 0.0f;
-      }
+      for (int j = 0; j < 8; ++j) u[kbl][j] = t[(kbl * 16 + 8 * g + j) * TP + c];
     float cs = 0.0f;
 #pragma unroll
     for (int kbl = 0; kbl < kPrepRows / 16; ++kbl) {
       const int64_t b0 = r0 + kbl * 16;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) cs += v[kbl][j];
-      if (b0 < p.Bc) store_frag<BF>(dYc + ((size_t)ob * p.KBc + b0 / 16) * kFragElems, lane, v[kbl]);
+      for (int j = 0; j < 8; ++j) cs += u[kbl][j];
+      if (b0 < p.Bc) store_frag<BF>(dYc + ((size_t)ob * p.KBc + b0 / 16) * kFragElems, lane, u[kbl]);
     }
     // rows of lane halves interleave in blocks of 8; add the halves in a fixed order
     const float other = __shfl_xor(cs, 32);
-    if (g == 0 && bb < p.NBB) colsum_part[(size_t)bb * p.O32 + o] = cs + other;
+    if (g == 0 && bb < p.NBB) colsum_part[(size_t)bb * p.O32 + ob * 32 + c] = cs + other;
   }
 }
 

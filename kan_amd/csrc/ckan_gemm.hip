@@ -1210,9 +1210,11 @@ struct DcPipe {
   static constexpr int MAIN_BYTES = BAS_BYTES + 3 * DY_SLOT + 3 * T_SLOT;
   static constexpr int XCH_BYTES = 8 * (NF / 2) * 16 * 64 * 4;
   static constexpr int STG_BYTES = 32 * NN * 32 * (P + 1) * 4;  // one output group
-  static constexpr int LDS_BYTES = MAIN_BYTES > XCH_BYTES
+  static constexpr int BIG_BYTES = MAIN_BYTES > XCH_BYTES
       ? (MAIN_BYTES > STG_BYTES ? MAIN_BYTES : STG_BYTES)
       : (XCH_BYTES > STG_BYTES ? XCH_BYTES : STG_BYTES);
+  static constexpr int CS_BYTES = 512 * 4;  // column-sum partials of the block's outputs
+  static constexpr int LDS_BYTES = BIG_BYTES + CS_BYTES;
   static constexpr int RPT = 2 * KI;  // batch rows per generating thread
   static constexpr bool kOk = LDS_BYTES <= 160 * 1024 && T_CHUNKS <= 512 && NF % 2 == 0;
 };
@@ -1220,7 +1222,7 @@ struct DcPipe {
 template <int P, bool BF>
 __global__ void __launch_bounds__(512)
 k_dc_pipe(const typename Elem<BF>::type* __restrict__ dYc, const float* __restrict__ tc,
-          const float* __restrict__ colsum, float* __restrict__ out, Plan p, int st_per_split,
+          const float* __restrict__ colsum_part, float* __restrict__ out, Plan p, int st_per_split,
           int accumulate) {
   typedef DcPipe<P, BF> K;
   typedef typename K::E E;
@@ -1389,6 +1391,29 @@ k_dc_pipe(const typename Elem<BF>::type* __restrict__ dYc, const float* __restri
   }
   wait_vmcnt<0>();  // the prefetches past the end land before the LDS is reused
 
+  // d = 0 column, sum_b dy[b, o]: thread (rgp, oi) adds every RS-th of the
+  // NBB per-64-row partials of output oi (fixed order); the RS results are
+  // combined in order when staged
+  constexpr int NOW = NO * 32, RS = 512 / NOW;
+  float* cpart = reinterpret_cast<float*>(smem + K::BIG_BYTES);
+  if (blockIdx.z == 0) {
+    const int oi = tid % NOW, rgp = tid / NOW;
+    if (rgp < RS) {
+      const int o = min(obk * NOW + oi, p.O32 - 1);
+      const float* cp = colsum_part + o;
+      float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+      int k = rgp;
+      for (; k + 3 * RS < p.NBB; k += 4 * RS) {
+        a0 += cp[(size_t)k * p.O32];
+        a1 += cp[(size_t)(k + RS) * p.O32];
+        a2 += cp[(size_t)(k + 2 * RS) * p.O32];
+        a3 += cp[(size_t)(k + 3 * RS) * p.O32];
+      }
+      for (; k < p.NBB; k += RS) a0 += cp[(size_t)k * p.O32];
+      cpart[rgp * NOW + oi] = ((a0 + a1) + a2) + a3;
+    }
+  }
+
   // halves' exchange: half 0 keeps fragments [0, NF/2), half 1 the rest
   wait_lgkmcnt<0>();
   block_barrier();
@@ -1441,7 +1466,12 @@ k_dc_pipe(const typename Elem<BF>::type* __restrict__ dYc, const float* __restri
     }
     for (int q = tid; q < 32 * OW; q += 512) {
       const int il = q / OW, ol = q - il * OW;
-      stg[q * p.D] = (blockIdx.z == 0 && ol < ovalid) ? colsum[o0 + ol] : 0.0f;
+      float cs = 0.0f;
+      if (blockIdx.z == 0 && ol < ovalid) {
+#pragma unroll
+        for (int r = 0; r < RS; ++r) cs += cpart[r * NOW + c * OW + ol];
+      }
+      stg[q * p.D] = cs;
     }
     wait_lgkmcnt<0>();
     block_barrier();

@@ -73,6 +73,8 @@ void launch_fwd_gemm(const float* x, float* t, const void* packed, float* y, voi
                      const Plan& p, const FwdChoice& c, hipStream_t s);
 void launch_dx_gemm(const void* dYx, const void* packed, const float* t, float* dx,
                     const Plan& p, hipStream_t s);
+// colsum: the per-64-row column-sum partials for the pipelined kernel (which
+// reduces them itself), the reduced row otherwise.
 void launch_dc_gemm(const void* dYc, const float* t, const float* colsum, float* part, float* dC,
                     bool accumulate, const Plan& p, const BwdLayout& L, hipStream_t s);
 void launch_sgd(float* p, const float* g, int64_t n, float lr, float wd, hipStream_t s);
