@@ -15,10 +15,9 @@
  *   - Every call returns a ckan_status; on failure ckan_last_error() returns a
  *     thread-local message.  Argument checks happen on the host before any
  *     launch, so an invalid call launches nothing.
- *   - Workspaces are caller-allocated.  A forward workspace must be zero-filled
- *     once before its first use (ckan_workspace_init); every call leaves its
- *     split-K counters back at zero.  Calls that share one workspace must not
- *     overlap in time.
+ *   - Workspaces are caller-allocated scratch (split-K partials, re-laid
+ *     operands); no call needs them zeroed.  Calls that share one workspace
+ *     must not overlap in time.
  */
 #ifndef CHEBYKAN_H
 #define CHEBYKAN_H
@@ -71,7 +70,8 @@ size_t ckan_tcache_elems(const ckan_desc* desc);
 size_t ckan_fwd_workspace_bytes(const ckan_desc* desc);
 size_t ckan_bwd_workspace_bytes(const ckan_desc* desc, int need_dx, int need_dcoeffs);
 
-/* Zero-fill a workspace on `stream` with a fill kernel (no hipMemset). */
+/* Zero-fill a workspace on `stream` with a fill kernel (no hipMemset).  No
+ * entry point requires it; kept for callers that want defined contents. */
 int ckan_workspace_init(void* ws, size_t ws_bytes, void* stream);
 
 /* ---- layer operators ---------------------------------------------------- */
