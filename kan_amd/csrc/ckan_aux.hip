@@ -7,26 +7,30 @@
 namespace ckan {
 
 // t[b, i] = tanh(x[b, i]) for i < I, 0 for I <= i < I_sg.  Row pitch I_sg.
-// Replaces torch.tanh (kan/basis/chebyshev.py:78).
+// Replaces torch.tanh (kan/basis/chebyshev.py:78).  tpr threads per row
+// (a power of two dividing 256) take float4 columns; 256/tpr rows per block.
 __global__ void __launch_bounds__(256)
-k_tanh(const float* __restrict__ x, float* __restrict__ t, int64_t B, int I, int I_sg) {
-  const int64_t n4 = B * (int64_t)(I_sg / 4);
+k_tanh(const float* __restrict__ x, float* __restrict__ t, int64_t B, int I, int I_sg, int tpr) {
+  const int rpb = 256 / tpr;
+  const int64_t b = (int64_t)blockIdx.x * rpb + threadIdx.x / tpr;
+  if (b >= B) return;
+  const int n4 = I_sg / 4;
   const bool vec = (I % 4) == 0;
-  for (int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; q < n4;
-       q += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t b = q / (I_sg / 4);
-    const int i = (int)(q - b * (I_sg / 4)) * 4;
+  const float* xr = x + b * I;
+  float* tr = t + b * I_sg;
+  for (int c4 = threadIdx.x % tpr; c4 < n4; c4 += tpr) {
+    const int i = c4 * 4;
     f32x4_t v;
     if (vec && i < I) {
-      v = *reinterpret_cast<const f32x4_t*>(x + b * I + i);
+      v = *reinterpret_cast<const f32x4_t*>(xr + i);
     } else {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) v[j] = (i + j < I) ? x[b * I + i + j] : 0.0f;
+      for (int j = 0; j < 4; ++j) v[j] = (i + j < I) ? xr[i + j] : 0.0f;
     }
     f32x4_t r;
 #pragma unroll
     for (int j = 0; j < 4; ++j) r[j] = (i + j < I) ? tanhf(v[j]) : 0.0f;
-    *reinterpret_cast<f32x4_t*>(t + b * I_sg + i) = r;
+    *reinterpret_cast<f32x4_t*>(tr + i) = r;
   }
 }
 
@@ -399,8 +403,10 @@ static int grid_for(int64_t work, int per_block = 256) {
 }
 
 void launch_tanh(const float* x, float* t, const Plan& p, hipStream_t s) {
-  const int64_t n4 = p.B * (p.I_sg / 4);
-  hipLaunchKernelGGL(k_tanh, dim3(grid_for(n4)), dim3(256), 0, s, x, t, p.B, p.I, p.I_sg);
+  int tpr = 1;
+  while (tpr < 256 && tpr < p.I_sg / 4) tpr *= 2;
+  const int64_t blocks = ceil_div(p.B, 256 / tpr);
+  hipLaunchKernelGGL(k_tanh, dim3((unsigned)blocks), dim3(256), 0, s, x, t, p.B, p.I, p.I_sg, tpr);
 }
 
 template <int P, bool BF>
