@@ -104,13 +104,18 @@ def _suite():
     m = kan_amd.ChebyKANLayer(1, 1, 8)
     x1 = torch.linspace(-1, 1, 100).reshape(-1, 1).to(dev)
     y1 = torch.sin(2 * math.pi * x1)
-    ex = kan_amd.ResidentExecutor([1, 1], [8], 100, compute="fp32", loss="mse",
-                                  optimizer="adam", lr=0.01, use_graph=True)
-    ex.set_coeffs(0, m.cheby_coeffs.detach())
-    ms = _time_loop(lambda: ex.step(x1, y1), 1000, 0)
-    out["cfg1"] = {"workload": "ChebyKANLayer(1,1,8) sin(2 pi x), 100 pts, MSE+Adam, resident, HIP graph",
-                   "us_per_step": ms * 1e3, "steps": 1000, "final_loss": float(ex.step(x1, y1).item())}
-    ex.close()
+    res1 = {}
+    for graph in (False, True):
+        ex = kan_amd.ResidentExecutor([1, 1], [8], 100, compute="fp32", loss="mse",
+                                      optimizer="adam", lr=0.01, use_graph=graph)
+        ex.set_coeffs(0, m.cheby_coeffs.detach())
+        ms = _time_loop(lambda: ex.step(x1, y1), 1000, 0)
+        res1["graph" if graph else "eager"] = (ms, float(ex.step(x1, y1).item()))
+        ex.close()
+    out["cfg1"] = {"workload": "ChebyKANLayer(1,1,8) sin(2 pi x), 100 pts, MSE+Adam, resident, eager launches",
+                   "us_per_step": res1["eager"][0] * 1e3, "steps": 1000,
+                   "final_loss": res1["eager"][1],
+                   "us_per_step_hip_graph": res1["graph"][0] * 1e3}
 
     # config 2: 784->64->10, deg 4, fp32, B=256, CE + SGD lr 0.01
     g = torch.Generator().manual_seed(2)
@@ -118,13 +123,17 @@ def _suite():
     l2 = torch.randint(0, 10, (256,), generator=g).to(dev)
     torch.manual_seed(2)
     seq = kan_amd.KANSequential(kan_amd.ChebyKANLayer(784, 64, 4), kan_amd.ChebyKANLayer(64, 10, 4))
-    ex = kan_amd.ResidentExecutor.from_sequential(seq, 256, compute="fp32", loss="ce",
-                                                  optimizer="sgd", lr=0.01, use_graph=True)
-    ms = _time_loop(lambda: ex.step(x2, l2), 200, 20)
-    out["cfg2"] = {"workload": "784->64->10 deg 4 fp32 B=256, CE+SGD, resident, HIP graph",
+    res2 = {}
+    for graph in (False, True):
+        ex = kan_amd.ResidentExecutor.from_sequential(seq, 256, compute="fp32", loss="ce",
+                                                      optimizer="sgd", lr=0.01, use_graph=graph)
+        res2["graph" if graph else "eager"] = _time_loop(lambda: ex.step(x2, l2), 200, 20)
+        ex.close()
+    ms = res2["eager"]
+    out["cfg2"] = {"workload": "784->64->10 deg 4 fp32 B=256, CE+SGD, resident, eager launches",
                    "us_per_step": ms * 1e3, "samples_per_s": 256 / (ms * 1e-3),
-                   "tflops": 2.618e8 / (ms * 1e-3) / 1e12}
-    ex.close()
+                   "tflops": 2.618e8 / (ms * 1e-3) / 1e12,
+                   "us_per_step_hip_graph": res2["graph"] * 1e3}
 
     # config 4: 512->512->512->512->64, deg 16, B=65536, fp32 masters + bf16 compute, MSE + SGD, 100 steps
     g = torch.Generator().manual_seed(4)
@@ -191,20 +200,35 @@ def _cpu_baseline(sample_rows: int, reps: int):
     dy = torch.randn(sample_rows, O, generator=g)
     orc.layer_forward_backward(x, c, dy)  # warm-up
     times = []
-    for _ in range(reps):
+    t_start = time.perf_counter()
+    # at least `reps` steps, and about 10 s of CPU work in all
+    while len(times) < reps or time.perf_counter() - t_start < 10.0:
         t0 = time.perf_counter()
         orc.layer_forward_backward(x, c, dy)
         times.append(time.perf_counter() - t0)
+        if len(times) >= 1000:
+            break
     t = statistics.median(times)
+    model = "unknown CPU"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
     return {
         "value": sample_rows / t,
         "unit": "samples/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
+        "cpu_model": model,
         "sample": (f"config-3 layer (1024->1024, deg 8) fwd+bwd(dx,dC) on {sample_rows} of the "
                    f"8192 rows, fp32 torch CPU op-for-op restatement of "
-                   f"kan/basis/chebyshev.py:78,92-101,130-145 + autograd; median of {reps} "
-                   f"after 1 warm-up ({t * 1e3:.1f} ms/step)"),
+                   f"kan/basis/chebyshev.py:78,92-101,130-145 + autograd; median of {len(times)} "
+                   f"steps after 1 warm-up ({t * 1e3:.1f} ms/step, "
+                   f"{time.perf_counter() - t_start:.1f} s of CPU work)"),
     }
 
 

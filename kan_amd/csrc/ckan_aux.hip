@@ -414,7 +414,9 @@ static void launch_pack_t(const void* C, bool c_bf16, void* packed, const Plan& 
   typedef typename Elem<BF>::type E;
   E* Cf = reinterpret_cast<E*>(packed);
   E* Cb = Cf + packed_cf_elems(p);
-  float* bias = reinterpret_cast<float*>(reinterpret_cast<char*>(packed) + packed_bias_offset(p));
+  // with one input block its bias partial is the bias itself
+  float* bias = reinterpret_cast<float*>(reinterpret_cast<char*>(packed) +
+                                         (p.NIB == 1 ? packed_biasf_offset(p) : packed_bias_offset(p)));
   dim3 grid(p.NIB, p.O64 / 32);
   if (c_bf16)
     hipLaunchKernelGGL((k_pack<P, BF, uint16_t>), grid, dim3(256), 0, s,
@@ -427,20 +429,16 @@ static void launch_pack_t(const void* C, bool c_bf16, void* packed, const Plan& 
 void launch_pack(const void* C, bool c_bf16, void* packed, const Plan& p, hipStream_t s) {
   const bool bf = p.esz == 2;
   char* base = reinterpret_cast<char*>(packed);
-  struct Reduce {
-    char* base; const Plan& p; hipStream_t s;
-    ~Reduce() {
-      hipLaunchKernelGGL(k_col_reduce, dim3((unsigned)ceil_div(p.O32, 64)), dim3(256), 0, s,
-                         reinterpret_cast<const float*>(base + packed_bias_offset(p)), p.NIB,
-                         p.O32, p.O32, reinterpret_cast<float*>(base + packed_biasf_offset(p)));
-    }
-  } reduce{base, p, s};
   switch (p.P) {
     case 2: bf ? launch_pack_t<2, true>(C, c_bf16, packed, p, s) : launch_pack_t<2, false>(C, c_bf16, packed, p, s); break;
     case 4: bf ? launch_pack_t<4, true>(C, c_bf16, packed, p, s) : launch_pack_t<4, false>(C, c_bf16, packed, p, s); break;
     case 8: bf ? launch_pack_t<8, true>(C, c_bf16, packed, p, s) : launch_pack_t<8, false>(C, c_bf16, packed, p, s); break;
     default: bf ? launch_pack_t<16, true>(C, c_bf16, packed, p, s) : launch_pack_t<16, false>(C, c_bf16, packed, p, s); break;
   }
+  if (p.NIB > 1)  // bias = sum of the per-input-block partials, in block order
+    hipLaunchKernelGGL(k_col_reduce, dim3((unsigned)ceil_div(p.O32, 64)), dim3(256), 0, s,
+                       reinterpret_cast<const float*>(base + packed_bias_offset(p)), p.NIB,
+                       p.O32, p.O32, reinterpret_cast<float*>(base + packed_biasf_offset(p)));
 }
 
 void launch_prep_dy(const float* dy, void* dYx, void* dYc, float* colsum_part, const Plan& p,
