@@ -424,20 +424,28 @@ int ckan_exec_step(ckan_exec* ex, const float* x, const void* target, float* los
   if (!x || !target) return efail(CKAN_ERR_INVALID_ARG, "executor: x/target is NULL");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   int rc;
+  // small device copies use a kernel: a DMA-engine copy adds tens of us of latency
+  auto copy = [&](void* dst, const void* src, size_t bytes, hipStream_t st) {
+    const int64_t n = (int64_t)(bytes / 4);
+    hipLaunchKernelGGL(k_copy_f32, dim3(grid_of(n)), dim3(256), 0, st,
+                       reinterpret_cast<const float*>(src), reinterpret_cast<float*>(dst), n);
+    return hipGetLastError() == hipSuccess;
+  };
   if (!ex->cfg.use_graph) {
     if ((rc = run_step(ex, x, target, s))) return rc;
-    if (loss_out && hipMemcpyAsync(loss_out, ex->loss, 4, hipMemcpyDeviceToDevice, s) != hipSuccess)
+    if (loss_out && !copy(loss_out, ex->loss, 4, s))
       return efail(CKAN_ERR_HIP, "executor: loss copy failed");
     return CKAN_OK;
   }
-  // graph mode: inputs staged into executor-owned buffers outside the graph
-  if (hipEventRecord(ex->ev_in, s) != hipSuccess || hipStreamWaitEvent(ex->es, ex->ev_in, 0) != hipSuccess)
-    return efail(CKAN_ERR_HIP, "executor: stream ordering failed");
+  // graph mode: inputs staged into executor-owned buffers outside the graph;
+  // the graph (captured once on the executor's stream) is replayed on `stream`
   const size_t xb = (size_t)ex->cfg.batch * ex->widths[0] * 4;
-  if (hipMemcpyAsync(ex->x_own, x, xb, hipMemcpyDeviceToDevice, ex->es) != hipSuccess ||
-      hipMemcpyAsync(ex->tgt_own, target, ex->tgt_bytes, hipMemcpyDeviceToDevice, ex->es) != hipSuccess)
+  if (!copy(ex->x_own, x, xb, s) || !copy(ex->tgt_own, target, ex->tgt_bytes, s))
     return efail(CKAN_ERR_HIP, "executor: input staging failed");
   if (!ex->graph) {
+    // capture on the executor's own stream, ordered after the staging copies
+    if (hipEventRecord(ex->ev_in, s) != hipSuccess || hipStreamWaitEvent(ex->es, ex->ev_in, 0) != hipSuccess)
+      return efail(CKAN_ERR_HIP, "executor: stream ordering failed");
     hipGraph_t g = nullptr;
     if (hipStreamBeginCapture(ex->es, hipStreamCaptureModeThreadLocal) != hipSuccess)
       return efail(CKAN_ERR_HIP, "executor: graph capture failed to start");
@@ -453,12 +461,10 @@ int ckan_exec_step(ckan_exec* ex, const float* x, const void* target, float* los
     }
     hipGraphDestroy(g);
   }
-  if (hipGraphLaunch(ex->graph, ex->es) != hipSuccess)
+  if (hipGraphLaunch(ex->graph, s) != hipSuccess)
     return efail(CKAN_ERR_HIP, "executor: graph launch failed");
-  if (loss_out && hipMemcpyAsync(loss_out, ex->loss, 4, hipMemcpyDeviceToDevice, ex->es) != hipSuccess)
+  if (loss_out && !copy(loss_out, ex->loss, 4, s))
     return efail(CKAN_ERR_HIP, "executor: loss copy failed");
-  if (hipEventRecord(ex->ev_out, ex->es) != hipSuccess || hipStreamWaitEvent(s, ex->ev_out, 0) != hipSuccess)
-    return efail(CKAN_ERR_HIP, "executor: stream ordering failed");
   return CKAN_OK;
 }
 
