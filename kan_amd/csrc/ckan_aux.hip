@@ -478,11 +478,13 @@ void launch_dc_finalize(const float* part, int S, const float* colsum, float* dC
 }
 
 // dC[q] (=|+=) sum_z part[z][q], z in split order (slices of I*O*D floats).
+// The split sum is formed first, so accumulating adds exactly the gradient a
+// non-accumulating call writes.
 __global__ void __launch_bounds__(256)
 k_dc_sum(const float* __restrict__ part, int S, float* __restrict__ dC, int64_t n, int accumulate) {
   for (int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; q < n;
        q += (int64_t)gridDim.x * blockDim.x) {
-    float acc = accumulate ? dC[q] : 0.0f;
+    float acc = 0.0f;
     int z = 0;
     for (; z + 4 <= S; z += 4) {
       const float a = part[(size_t)z * n + q], b = part[(size_t)(z + 1) * n + q];
@@ -490,7 +492,7 @@ k_dc_sum(const float* __restrict__ part, int S, float* __restrict__ dC, int64_t 
       acc = (((acc + a) + b) + c) + d;
     }
     for (; z < S; ++z) acc += part[(size_t)z * n + q];
-    dC[q] = acc;
+    dC[q] = accumulate ? dC[q] + acc : acc;
   }
 }
 

@@ -161,6 +161,45 @@ def test_split_k_paths_fp32():
         assert _rel(dc, dc_ref) <= FP32_TOL
 
 
+@pytest.mark.parametrize("B,I,O,deg,compute", [
+    (128, 1024, 1024, 8, "bf16"),   # pipelined dC, one split: accumulates in its epilogue
+    (1024, 100, 70, 5, "bf16"),     # pipelined dC, split batch: accumulates in the split sum
+    (64, 48, 40, 15, "fp32"),       # fp32 degree 16: older dC kernel + finalize
+])
+def test_backward_accumulate_into_existing_grad(B, I, O, deg, compute):
+    """ckan_backward(accumulate=1) adds to dcoeffs: R + G elementwise, bit for bit."""
+    from kan_amd import _lib
+    print(f"accumulate B={B} I={I} O={O} deg={deg} {compute}", flush=True)
+    L = _lib.load()
+    x, c, dy = _inputs(B, I, O, deg, seed=B + deg)
+    code = _lib.CKAN_COMPUTE_BF16 if compute == "bf16" else _lib.CKAN_COMPUTE_FP32
+    d = _lib.make_desc(B, I, O, deg, code, _lib.CKAN_DTYPE_F32)
+    st = torch.cuda.current_stream().cuda_stream
+    xd, cd, dyd = x.cuda(), c.cuda(), dy.cuda()
+    packed = torch.empty(L.ckan_packed_bytes(d), dtype=torch.uint8, device="cuda")
+    t = torch.empty(L.ckan_tcache_elems(d), device="cuda")
+    y = torch.empty(B, O, device="cuda")
+    fwb = max(L.ckan_fwd_workspace_bytes(d), 256)
+    fws = torch.empty(fwb, dtype=torch.uint8, device="cuda")
+    bwb = L.ckan_bwd_workspace_bytes(d, 0, 1)
+    bws = torch.empty(bwb, dtype=torch.uint8, device="cuda")
+    _lib.check(L.ckan_pack_coeffs(d, cd.data_ptr(), packed.data_ptr(), st))
+    _lib.check(L.ckan_forward(d, xd.data_ptr(), packed.data_ptr(), y.data_ptr(), t.data_ptr(),
+                              fws.data_ptr(), fwb, st))
+    g = torch.empty(I, O, deg + 1, device="cuda")
+    _lib.check(L.ckan_backward(d, t.data_ptr(), packed.data_ptr(), dyd.data_ptr(), None,
+                               g.data_ptr(), 0, bws.data_ptr(), bwb, st))
+    r = torch.randn(I, O, deg + 1, generator=torch.Generator().manual_seed(7)).cuda()
+    acc = r.clone()
+    _lib.check(L.ckan_backward(d, t.data_ptr(), packed.data_ptr(), dyd.data_ptr(), None,
+                               acc.data_ptr(), 1, bws.data_ptr(), bwb, st))
+    torch.cuda.synchronize()
+    assert torch.equal(acc, r + g)
+    _, _, dc_ref = orc.layer_forward_backward(x, c, dy, need_dx=False)
+    tol = BF16_TOL if compute == "bf16" else FP32_TOL
+    assert _rel(g, dc_ref) <= tol
+
+
 def test_deterministic_results():
     x, c, dy = _inputs(512, 128, 128, 8, seed=9)
     a = _gpu_fwd_bwd(x, c, dy, "bf16")
