@@ -216,6 +216,15 @@ def test_only_coeff_grad_skips_dx():
     assert _rel(dc, dc_ref) <= FP32_TOL
 
 
+@pytest.mark.parametrize("compute,tol", [("fp32", FP32_TOL), ("bf16", BF16_TOL)])
+def test_only_input_grad_skips_dc(compute, tol):
+    x, c, dy = _inputs(512, 256, 128, 8, seed=5)
+    y_ref, dx_ref, _ = orc.layer_forward_backward(x, c, dy)
+    y, dx, dc = _gpu_fwd_bwd(x, c, dy, compute, need_dc=False)
+    assert dc is None
+    assert _rel(dx, dx_ref) <= tol
+
+
 def test_saturation_is_finite_and_analytic():
     """Divergence from the reference by design: for |x| >= 9.0108 the
     reference's dx is NaN; this path returns the analytic limit."""
