@@ -12,6 +12,7 @@
 // recurrence; in dC the block builds the basis operand once per stage into
 // LDS.  The coefficient operands are pre-packed fragment-major and staged
 // through LDS with a register double buffer (one barrier per stage).
+#include <atomic>
 #include <type_traits>
 
 #include "ckan_kernels.hpp"
@@ -1493,6 +1494,17 @@ k_dc_pipe(const typename Elem<BF>::type* __restrict__ dYc, const float* __restri
 // Host-side configuration and launchers
 // ---------------------------------------------------------------------------
 
+// Raises a kernel's dynamic-LDS limit before its first launch on each device
+// (the attribute is per device).  `done` holds one bit per device.
+static void ensure_lds_limit(const void* fn, int bytes, std::atomic<uint32_t>& done) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 32) dev = 0;
+  const uint32_t bit = 1u << dev;
+  if (done.load(std::memory_order_acquire) & bit) return;
+  (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  done.fetch_or(bit, std::memory_order_acq_rel);
+}
+
 // Number of workgroups that fills the chip once: 256 CUs, one 4-wave block each.
 static constexpr int kChipBlocks = 256;
 
@@ -1565,12 +1577,8 @@ static void fwd_dispatch(const float* x, float* t, const void* packed, float* y,
         if constexpr (FwdPipe<P, BF>::kOk) {
           typedef FwdPipe<P, BF> K;
           const size_t lds = (size_t)K::LDS_BYTES;
-          static bool attr_set = false;  // one-time raise of the dynamic LDS limit
-          if (!attr_set) {
-            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_fwd_pipe<P, BF>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-            attr_set = true;
-          }
+          static std::atomic<uint32_t> lds_set{0};
+          ensure_lds_limit(reinterpret_cast<const void*>(&k_fwd_pipe<P, BF>), (int)lds, lds_set);
           hipLaunchKernelGGL((k_fwd_pipe<P, BF>), grid, dim3(K::THREADS), lds, s, t, Cf, bias, y,
                              part, p, c.sg_per_split);
         } else {
@@ -1611,12 +1619,8 @@ static void dx_dispatch(const void* dYx, const void* packed, const float* t, flo
   if constexpr (DxTwo<P, BF>::kOk) {
     typedef DxTwo<P, BF> K;
     const int n_rb = (int)ceil_div(p.B32 / 32, 2 * K::NM);
-    static bool attr_set = false;
-    if (!attr_set) {
-      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_dx_two<P, BF>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, K::LDS_BYTES);
-      attr_set = true;
-    }
+    static std::atomic<uint32_t> lds_set{0};
+    ensure_lds_limit(reinterpret_cast<const void*>(&k_dx_two<P, BF>), K::LDS_BYTES, lds_set);
     hipLaunchKernelGGL((k_dx_two<P, BF>), dim3(n_rb * p.NIB), dim3(256), K::LDS_BYTES, s,
                        reinterpret_cast<const E*>(dYx), Cb, t, dx, p, n_rb);
     return;
@@ -1626,12 +1630,8 @@ static void dx_dispatch(const void* dYx, const void* packed, const float* t, flo
     const int n_rb = (int)ceil_div(p.B32 / 32, K::WGM * NM);
     const int blocks = n_rb * p.NIB;
     const size_t lds = (size_t)K::NBUF * K::STAGE_BYTES;
-    static bool attr_set = false;
-    if (!attr_set) {
-      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_dx_pipe<P, BF>),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-      attr_set = true;
-    }
+    static std::atomic<uint32_t> lds_set{0};
+    ensure_lds_limit(reinterpret_cast<const void*>(&k_dx_pipe<P, BF>), (int)lds, lds_set);
     hipLaunchKernelGGL((k_dx_pipe<P, BF>), dim3(blocks), dim3(256), lds, s,
                        reinterpret_cast<const E*>(dYx), Cb, t, dx, p, n_rb);
     return;
@@ -1734,12 +1734,8 @@ static void dc_dispatch(const void* dYc, const float* t, const float* colsum, fl
   if constexpr (DcPipe<P, BF>::kOk) {
     if (L.dc_pipe) {
       typedef DcPipe<P, BF> K;
-      static bool attr_set = false;  // one-time raise of the dynamic LDS limit
-      if (!attr_set) {
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&k_dc_pipe<P, BF>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, K::LDS_BYTES);
-        attr_set = true;
-      }
+      static std::atomic<uint32_t> lds_set{0};
+      ensure_lds_limit(reinterpret_cast<const void*>(&k_dc_pipe<P, BF>), K::LDS_BYTES, lds_set);
       const bool split = L.dc_splits > 1;
       dim3 grid(p.NIB, (unsigned)ceil_div(p.NBf, K::NO), L.dc_splits);
       hipLaunchKernelGGL((k_dc_pipe<P, BF>), grid, dim3(512), K::LDS_BYTES, s,
