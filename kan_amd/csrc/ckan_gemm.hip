@@ -1176,10 +1176,13 @@ k_dc(const typename Elem<BF>::type* __restrict__ dYc, const float* __restrict__ 
 
 // ---------------------------------------------------------------------------
 // dC, pipelined: dC[i, o, d] = sum_b T_d(t[b, i]) dy[b, o] for d >= 1.
-// One block = 8 waves: two halves that take alternate stages of KI k-blocks
-// (16 batch rows each) of the reduction; in a half, wave (dq, og) accumulates
-// PH = min(P, 4) degrees (group dq) x NN output fragments (group og) for the
-// block's 32 inputs, always 8 accumulator fragments.
+// One block = 8 waves in H groups ("halves") that take alternate stages of KI
+// k-blocks (16 batch rows each) of the reduction; in a group, wave (dq, og)
+// accumulates PH = min(P, 4) degrees (group dq) x NN output fragments (group
+// og) for the block's 32 inputs, always 8 accumulator fragments.  H = 2 (a
+// K split inside the block), or H = 1 for degree 16 with at least 4 output
+// fragments: 4 output fragments per block keep basis generation at 3 VALU
+// per MFMA.
 // Both streamed operands arrive by LDS DMA, with no vector-register loads in
 // the loop: tanh tiles three pairs of stages ahead, dy fragments two pairs
 // ahead.  The basis operand (P fragments per k-block) is generated from the
@@ -1188,63 +1191,65 @@ k_dc(const typename Elem<BF>::type* __restrict__ dYc, const float* __restrict__ 
 // [input][output][degree] (d = 0 from the reduced dy column sums) so that the
 // block writes contiguous runs of dC, or of its split-K slice.
 // ---------------------------------------------------------------------------
-template <int P, bool BF>
+template <int P, bool BF, int H_>
 struct DcPipe {
   typedef typename Elem<BF>::type E;
+  static constexpr int H = H_;              // stage groups (K split inside the block)
+  static constexpr int WG = 8 / H;          // waves per group
   static constexpr int PH = P < 4 ? P : 4;  // degrees per wave
-  static constexpr int DQ = P / PH;         // degree groups in a half
-  static constexpr int OG = 4 / DQ;         // output groups in a half
+  static constexpr int DQ = P / PH;         // degree groups in a group
+  static constexpr int OG = WG / DQ;        // output groups in a group
   static constexpr int NN = 8 / PH;         // output fragments per wave
   static constexpr int NO = OG * NN;        // output fragments per block
   static constexpr int NF = PH * NN;        // accumulator fragments per wave (8)
-  static constexpr int KI = (BF && P != 2 && P != 16) ? 2 : 1;
+  static constexpr int KI = (BF && P != 2 && (P != 16 || H == 1)) ? 2 : 1;
   static constexpr int FB = kFragElems * (int)sizeof(E);
   static constexpr int BAS_STAGE = P * KI * FB;
   static constexpr int DY_STAGE = NO * KI * FB;
-  static constexpr int DY_CHUNKS = 2 * DY_STAGE / 16;             // real chunks per pair
-  static constexpr int DY_OPS = (DY_CHUNKS + 511) / 512;          // dma16 per thread per pair
-  static constexpr int DY_SLOT = DY_OPS * 8192;                   // bytes per pair slot
+  static constexpr int DY_CHUNKS = H * DY_STAGE / 16;             // real chunks per step
+  static constexpr int DY_OPS = (DY_CHUNKS + 511) / 512;          // dma16 per thread per step
+  static constexpr int DY_SLOT = DY_OPS * 8192;                   // bytes per step slot
   static constexpr int T_STAGE = KI * 16 * 32 * 4;                // tanh rows x 32 inputs
-  static constexpr int T_CHUNKS = 2 * T_STAGE / 16;
+  static constexpr int T_CHUNKS = H * T_STAGE / 16;
   static constexpr int T_SLOT = 8192;                             // one dma16 per thread
-  static constexpr int BAS_BYTES = 2 * 2 * BAS_STAGE;             // two pairs of stages
+  static constexpr int BAS_BYTES = 2 * H * BAS_STAGE;             // two steps of H stages
   static constexpr int MAIN_BYTES = BAS_BYTES + 3 * DY_SLOT + 3 * T_SLOT;
-  static constexpr int XCH_BYTES = 8 * (NF / 2) * 16 * 64 * 4;
+  static constexpr int XCH_BYTES = H == 2 ? 8 * (NF / 2) * 16 * 64 * 4 : 0;
   static constexpr int STG_BYTES = 32 * NN * 32 * (P + 1) * 4;  // one output group
   static constexpr int BIG_BYTES = MAIN_BYTES > XCH_BYTES
       ? (MAIN_BYTES > STG_BYTES ? MAIN_BYTES : STG_BYTES)
       : (XCH_BYTES > STG_BYTES ? XCH_BYTES : STG_BYTES);
   static constexpr int CS_BYTES = 512 * 4;  // column-sum partials of the block's outputs
   static constexpr int LDS_BYTES = BIG_BYTES + CS_BYTES;
-  static constexpr int RPT = 2 * KI;  // batch rows per generating thread
+  static constexpr int RPT = KI * H;  // batch rows per generating thread (of a lane's 8)
   static constexpr bool kOk = LDS_BYTES <= 160 * 1024 && T_CHUNKS <= 512 && NF % 2 == 0;
 };
 
-template <int P, bool BF>
+template <int P, bool BF, int H_>
 __global__ void __launch_bounds__(512)
 k_dc_pipe(const typename Elem<BF>::type* __restrict__ dYc, const float* __restrict__ tc,
           const float* __restrict__ colsum_part, float* __restrict__ out, Plan p, int st_per_split,
           int accumulate) {
-  typedef DcPipe<P, BF> K;
+  typedef DcPipe<P, BF, H_> K;
   typedef typename K::E E;
   constexpr int PH = K::PH, DQ = K::DQ, OG = K::OG, NN = K::NN, NO = K::NO, NF = K::NF;
-  constexpr int KI = K::KI, FB = K::FB;
+  constexpr int KI = K::KI, FB = K::FB, H = K::H, WG = K::WG;
   constexpr int RPT = K::RPT, DY_OPS = K::DY_OPS;
   extern __shared__ __attribute__((aligned(16))) char smem[];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int half = wave >> 2, wq = wave & 3, dh = wq % DQ, og = wq / DQ;
+  const int half = wave / WG, wq = wave % WG, dh = wq % DQ, og = wq / DQ;
   const int g = lane >> 5;
   const int ib = blockIdx.x, obk = blockIdx.y;
   const int nst_all = (int)(p.KBc / KI);
   const int st0 = blockIdx.z * st_per_split;
   const int st1 = min(nst_all, st0 + st_per_split);
-  const int npair = (st1 - st0) / 2;  // split stage counts are even
+  const int npair = (st1 - st0) / H;  // steps of H stages (split stage counts are even)
   char* bas = smem;
   char* dyr = smem + K::BAS_BYTES;
   char* tlr = dyr + 3 * K::DY_SLOT;
 
-  // dy DMA: chunk c < DY_CHUNKS of a pair is [stage hs][fragment f][k-block kk][16 B];
+  // dy DMA: chunk c < DY_CHUNKS of a step is [stage hs][fragment f][k-block kk][16 B];
   // chunks past that repeat real ones into the unused end of the slot
   constexpr int CPF = FB / 16;
   const char* dyb = reinterpret_cast<const char*>(dYc);
@@ -1269,13 +1274,13 @@ k_dc_pipe(const typename Elem<BF>::type* __restrict__ dYc, const float* __restri
     char* dst = dyr + (j % 3) * K::DY_SLOT + wave * 1024;
 #pragma unroll
     for (int q = 0; q < DY_OPS; ++q) {
-      int st = st0 + 2 * j + dhs[q];
+      int st = st0 + H * j + dhs[q];
       if (st >= st1) st = st0;  // past the end: any in-range source, never read
       dma16(dyb + doff[q] + (size_t)st * KI * FB, dst + q * 8192);
     }
   };
   auto dma_t = [&](int j) __attribute__((always_inline)) {
-    int st = st0 + 2 * j + ths;
+    int st = st0 + H * j + ths;
     if (st >= st1) st = st0;
     int64_t b = (int64_t)st * KI * 16 + trr;
     if (b >= p.B) b = p.B - 1;  // dy is zero on rows past B
@@ -1284,7 +1289,7 @@ k_dc_pipe(const typename Elem<BF>::type* __restrict__ dYc, const float* __restri
 
   // basis generation slot of this thread within its half: k-block gkk,
   // fragment lane gl, rows grh*RPT .. +RPT of the lane's 8
-  const int th = tid & 255;
+  const int th = tid % (512 / H);
   const int gslot = th % (KI * 64), gkk = gslot / 64, gl = gslot % 64;
   const int grh = th / (KI * 64);
   const int trow0 = gkk * 16 + 8 * (gl >> 5) + grh * RPT;
@@ -1293,7 +1298,7 @@ k_dc_pipe(const typename Elem<BF>::type* __restrict__ dYc, const float* __restri
     float tv[RPT];
 #pragma unroll
     for (int r = 0; r < RPT; ++r) tv[r] = tl[(trow0 + r) * 32 + (gl & 31)];
-    char* dst = bas + ((j & 1) * 2 + half) * K::BAS_STAGE + gkk * FB + (gl * 8 + grh * RPT) * (int)sizeof(E);
+    char* dst = bas + ((j & 1) * H + half) * K::BAS_STAGE + gkk * FB + (gl * 8 + grh * RPT) * (int)sizeof(E);
     float a[RPT], b[RPT], t2[RPT];
 #pragma unroll
     for (int r = 0; r < RPT; ++r) { a[r] = 1.0f; b[r] = tv[r]; t2[r] = tv[r] + tv[r]; }
@@ -1314,14 +1319,17 @@ k_dc_pipe(const typename Elem<BF>::type* __restrict__ dYc, const float* __restri
 #pragma unroll
           for (int r = 0; r < 4; ++r) w[r] = (__bf16)b[r];
           *reinterpret_cast<bf16x4_t*>(d) = w;
-        } else {
+        } else if constexpr (RPT == 2) {
           bf16x2_t w;
 #pragma unroll
           for (int r = 0; r < 2; ++r) w[r] = (__bf16)b[r];
           *reinterpret_cast<bf16x2_t*>(d) = w;
+        } else {
+          *reinterpret_cast<__bf16*>(d) = (__bf16)b[0];
         }
       } else {
-        *reinterpret_cast<f32x2_t*>(d) = f32x2_t{b[0], b[1]};
+        if constexpr (RPT == 2) *reinterpret_cast<f32x2_t*>(d) = f32x2_t{b[0], b[1]};
+        else *reinterpret_cast<float*>(d) = b[0];
       }
     }
   };
@@ -1338,7 +1346,7 @@ k_dc_pipe(const typename Elem<BF>::type* __restrict__ dYc, const float* __restri
   // are read from LDS up front, and the basis generation for the next pair
   // (VALU + LDS traffic) is interleaved with the MFMAs.
   auto step = [&](int j) __attribute__((always_inline)) {
-    const E* ab = reinterpret_cast<const E*>(bas + ((j & 1) * 2 + half) * K::BAS_STAGE) +
+    const E* ab = reinterpret_cast<const E*>(bas + ((j & 1) * H + half) * K::BAS_STAGE) +
                   (size_t)(dh * PH) * KI * kFragElems;
     const E* bb = reinterpret_cast<const E*>(dyr + (j % 3) * K::DY_SLOT + half * K::DY_STAGE) +
                   (size_t)(og * NN) * KI * kFragElems;
@@ -1415,7 +1423,8 @@ k_dc_pipe(const typename Elem<BF>::type* __restrict__ dYc, const float* __restri
     }
   }
 
-  // halves' exchange: half 0 keeps fragments [0, NF/2), half 1 the rest
+  // with H = 2 the groups exchange: group 0 keeps fragments [0, NF/2),
+  // group 1 the rest; with H = 1 every wave keeps all NF
   wait_lgkmcnt<0>();
   block_barrier();
   float* xch = reinterpret_cast<float*>(smem);
@@ -1440,10 +1449,11 @@ k_dc_pipe(const typename Elem<BF>::type* __restrict__ dYc, const float* __restri
   // staging of output group c: [32 inputs][NN*32 outputs][D degrees]
   float* stg = reinterpret_cast<float*>(smem);
   constexpr int OW = NN * 32;
+  constexpr int NK = H == 2 ? NF / 2 : NF;  // fragments a wave stages
   auto stage_own = [&](auto KEEP) __attribute__((always_inline)) {
     constexpr int keep0 = decltype(KEEP)::value;
 #pragma unroll
-    for (int fj = 0; fj < NF / 2; ++fj) {
+    for (int fj = 0; fj < NK; ++fj) {
       const int e = (keep0 + fj) / NN, ni = (keep0 + fj) % NN;
       const int d = dh * PH + e + 1;
       if (d > p.deg) continue;
@@ -1454,8 +1464,10 @@ k_dc_pipe(const typename Elem<BF>::type* __restrict__ dYc, const float* __restri
   };
   float* outz = out + (size_t)blockIdx.z * p.I * p.O * p.D;
   const int ivalid = min(32, p.I - ib * 32);
-  if (half == 0) exchange(std::integral_constant<int, 0>{});
-  else exchange(std::integral_constant<int, NF / 2>{});
+  if constexpr (H == 2) {
+    if (half == 0) exchange(std::integral_constant<int, 0>{});
+    else exchange(std::integral_constant<int, NF / 2>{});
+  }
 #pragma unroll 1
   for (int c = 0; c < OG; ++c) {
     const int o0 = (obk * NO + c * NN) * 32;
@@ -1463,7 +1475,7 @@ k_dc_pipe(const typename Elem<BF>::type* __restrict__ dYc, const float* __restri
     block_barrier();  // previous readers of the LDS are done
     if (og == c) {
       if (half == 0) stage_own(std::integral_constant<int, 0>{});
-      else stage_own(std::integral_constant<int, NF / 2>{});
+      else stage_own(std::integral_constant<int, NK>{});
     }
     for (int q = tid; q < 32 * OW; q += 512) {
       const int il = q / OW, ol = q - il * OW;
@@ -1655,28 +1667,36 @@ void launch_dx_gemm(const void* dYx, const void* packed, const float* t, float* 
 // dC stage depth in k-blocks: 4 for bf16, 2 for fp32 (LDS bound).
 template <bool BF> struct DcKI { static constexpr int v = BF ? 4 : 2; };
 
+// Stage groups of the pipelined dC kernel for this shape (see DcPipe).
+static int dc_h(const Plan& p) { return (p.P == 16 && p.NBf >= 4) ? 1 : 2; }
+
+template <int P, bool BF> static bool dc_ok_t(int h) {
+  return h == 1 ? DcPipe<P, BF, 1>::kOk : DcPipe<P, BF, 2>::kOk;
+}
 static bool dc_pipe_ok(const Plan& p) {
   const bool bf = p.esz == 2;
+  const int h = dc_h(p);
   switch (p.P) {
-    case 2: return bf ? DcPipe<2, true>::kOk : DcPipe<2, false>::kOk;
-    case 4: return bf ? DcPipe<4, true>::kOk : DcPipe<4, false>::kOk;
-    case 8: return bf ? DcPipe<8, true>::kOk : DcPipe<8, false>::kOk;
-    default: return bf ? DcPipe<16, true>::kOk : DcPipe<16, false>::kOk;
+    case 2: return bf ? dc_ok_t<2, true>(h) : dc_ok_t<2, false>(h);
+    case 4: return bf ? dc_ok_t<4, true>(h) : dc_ok_t<4, false>(h);
+    case 8: return bf ? dc_ok_t<8, true>(h) : dc_ok_t<8, false>(h);
+    default: return bf ? dc_ok_t<16, true>(h) : dc_ok_t<16, false>(h);
   }
 }
 
 // output fragments per dC block and k-blocks per stage of the pipelined kernel
-template <int P, bool BF> static void dc_shape_t(int& no, int& ki) {
-  no = DcPipe<P, BF>::NO;
-  ki = DcPipe<P, BF>::KI;
+template <int P, bool BF> static void dc_shape_t(int h, int& no, int& ki) {
+  no = h == 1 ? DcPipe<P, BF, 1>::NO : DcPipe<P, BF, 2>::NO;
+  ki = h == 1 ? DcPipe<P, BF, 1>::KI : DcPipe<P, BF, 2>::KI;
 }
 static void dc_pipe_shape(const Plan& p, int& no, int& ki) {
   const bool bf = p.esz == 2;
+  const int h = dc_h(p);
   switch (p.P) {
-    case 2: bf ? dc_shape_t<2, true>(no, ki) : dc_shape_t<2, false>(no, ki); break;
-    case 4: bf ? dc_shape_t<4, true>(no, ki) : dc_shape_t<4, false>(no, ki); break;
-    case 8: bf ? dc_shape_t<8, true>(no, ki) : dc_shape_t<8, false>(no, ki); break;
-    default: bf ? dc_shape_t<16, true>(no, ki) : dc_shape_t<16, false>(no, ki); break;
+    case 2: bf ? dc_shape_t<2, true>(h, no, ki) : dc_shape_t<2, false>(h, no, ki); break;
+    case 4: bf ? dc_shape_t<4, true>(h, no, ki) : dc_shape_t<4, false>(h, no, ki); break;
+    case 8: bf ? dc_shape_t<8, true>(h, no, ki) : dc_shape_t<8, false>(h, no, ki); break;
+    default: bf ? dc_shape_t<16, true>(h, no, ki) : dc_shape_t<16, false>(h, no, ki); break;
   }
 }
 
@@ -1726,23 +1746,37 @@ BwdLayout bwd_layout(const Plan& p, bool need_dx, bool need_dc) {
   return L;
 }
 
+template <int P, bool BF, int H>
+static bool dc_pipe_launch(const void* dYc, const float* t, const float* colsum, float* part,
+                           float* dC, bool accumulate, const Plan& p, const BwdLayout& L,
+                           hipStream_t s) {
+  typedef typename Elem<BF>::type E;
+  if constexpr (DcPipe<P, BF, H>::kOk) {
+    typedef DcPipe<P, BF, H> K;
+    static std::atomic<uint32_t> lds_set{0};
+    ensure_lds_limit(reinterpret_cast<const void*>(&k_dc_pipe<P, BF, H>), K::LDS_BYTES, lds_set);
+    const bool split = L.dc_splits > 1;
+    dim3 grid(p.NIB, (unsigned)ceil_div(p.NBf, K::NO), L.dc_splits);
+    hipLaunchKernelGGL((k_dc_pipe<P, BF, H>), grid, dim3(512), K::LDS_BYTES, s,
+                       reinterpret_cast<const E*>(dYc), t, colsum, split ? part : dC, p,
+                       L.dc_st_per_split, (!split && accumulate) ? 1 : 0);
+    return true;
+  }
+  return false;
+}
+
 template <int P, bool BF>
 static void dc_dispatch(const void* dYc, const float* t, const float* colsum, float* part,
                         float* dC, bool accumulate, const Plan& p, const BwdLayout& L,
                         hipStream_t s) {
   typedef typename Elem<BF>::type E;
-  if constexpr (DcPipe<P, BF>::kOk) {
-    if (L.dc_pipe) {
-      typedef DcPipe<P, BF> K;
-      static std::atomic<uint32_t> lds_set{0};
-      ensure_lds_limit(reinterpret_cast<const void*>(&k_dc_pipe<P, BF>), K::LDS_BYTES, lds_set);
-      const bool split = L.dc_splits > 1;
-      dim3 grid(p.NIB, (unsigned)ceil_div(p.NBf, K::NO), L.dc_splits);
-      hipLaunchKernelGGL((k_dc_pipe<P, BF>), grid, dim3(512), K::LDS_BYTES, s,
-                         reinterpret_cast<const E*>(dYc), t, colsum, split ? part : dC, p,
-                         L.dc_st_per_split, (!split && accumulate) ? 1 : 0);
-      return;
+  if (L.dc_pipe) {
+    bool done = false;
+    if constexpr (P == 16) {  // dc_h(p) is 1 only for degree 16
+      if (dc_h(p) == 1) done = dc_pipe_launch<P, BF, 1>(dYc, t, colsum, part, dC, accumulate, p, L, s);
     }
+    if (!done) done = dc_pipe_launch<P, BF, 2>(dYc, t, colsum, part, dC, accumulate, p, L, s);
+    if (done) return;
   }
   constexpr int NM = BwdTile<P>::NM;
   dim3 grid((unsigned)ceil_div(p.NBf, 4 * NM), p.NIB, L.dc_splits);
