@@ -200,6 +200,42 @@ def test_backward_accumulate_into_existing_grad(B, I, O, deg, compute):
     assert _rel(g, dc_ref) <= tol
 
 
+def test_integration_ctypes_stub():
+    """The minimal ctypes binding a maintainer of the reference would add
+    (the stub printed in the integration notes), run as written."""
+    import ctypes
+    from kan_amd import _lib
+    _L = ctypes.CDLL(_lib.LIB_PATH)
+    for _f in ("ckan_packed_bytes", "ckan_tcache_elems", "ckan_fwd_workspace_bytes"):
+        getattr(_L, _f).restype = ctypes.c_size_t
+    _vp = ctypes.c_void_p
+
+    class _Desc(ctypes.Structure):
+        _fields_ = [("batch", ctypes.c_int64), ("in_dim", ctypes.c_int32), ("out_dim", ctypes.c_int32),
+                    ("degree", ctypes.c_int32), ("compute", ctypes.c_int32),
+                    ("coeff_dtype", ctypes.c_int32), ("reserved", ctypes.c_int32)]
+
+    def chebykan_forward(x, C):
+        d = _Desc(x.shape[0], C.shape[0], C.shape[1], C.shape[2] - 1, 0, 0, 0)
+        s = torch.cuda.current_stream().cuda_stream
+        packed = torch.empty(_L.ckan_packed_bytes(ctypes.byref(d)), dtype=torch.uint8, device=x.device)
+        t = torch.empty(_L.ckan_tcache_elems(ctypes.byref(d)), device=x.device)
+        y = torch.empty(x.shape[0], C.shape[1], device=x.device)
+        wsb = _L.ckan_fwd_workspace_bytes(ctypes.byref(d))
+        ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=x.device)
+        assert _L.ckan_pack_coeffs(ctypes.byref(d), _vp(C.data_ptr()), _vp(packed.data_ptr()), _vp(s)) == 0
+        assert _L.ckan_forward(ctypes.byref(d), _vp(x.data_ptr()), _vp(packed.data_ptr()),
+                               _vp(y.data_ptr()), _vp(t.data_ptr()), _vp(ws.data_ptr()),
+                               ctypes.c_size_t(wsb), _vp(s)) == 0
+        return y, t, packed
+
+    for B, I, O, deg in [(300, 64, 48, 8), (8, 512, 40, 5)]:  # a tile path and a split-K path
+        x, c, _ = _inputs(B, I, O, deg, seed=11)
+        y, _, _ = chebykan_forward(x.cuda(), c.cuda())
+        torch.cuda.synchronize()
+        assert _rel(y.cpu(), orc.layer_forward(x, c)) <= FP32_TOL
+
+
 def test_deterministic_results():
     x, c, dy = _inputs(512, 128, 128, 8, seed=9)
     a = _gpu_fwd_bwd(x, c, dy, "bf16")
