@@ -225,6 +225,22 @@ k_fwd(const float* __restrict__ tc, const typename Elem<BF>::type* __restrict__ 
 // costs one barrier.  Out-of-range rows and output fragments read a clamped
 // in-bounds address; their results are never stored.
 // ---------------------------------------------------------------------------
+// Workgroups go to the 8 XCDs round-robin by linear id, and each XCD has its
+// own L2.  When the grid is exactly 256 tiles of (8a) x (4b), give each XCD an
+// 8 x 4 patch (8 values of the x tile index, 4 of y) so that the operands the
+// patch shares stay in one L2; otherwise keep the launch order.
+__device__ __forceinline__ void xcd_patch(int& bx, int& by) {
+  bx = blockIdx.x;
+  by = blockIdx.y;
+  if (gridDim.x * gridDim.y == 256 && gridDim.x % 8 == 0 && gridDim.y % 4 == 0 && gridDim.z == 1) {
+    const int lin = blockIdx.x + gridDim.x * blockIdx.y;
+    const int xcd = lin & 7, loc = lin >> 3;
+    const int px = gridDim.x / 8;  // patches along x
+    bx = (xcd % px) * 8 + (loc & 7);
+    by = (xcd / px) * 4 + (loc >> 3);
+  }
+}
+
 template <int P, bool BF>
 struct FwdPipe {
   typedef typename Elem<BF>::type E;
@@ -262,8 +278,10 @@ k_fwd_pipe(const float* __restrict__ tc, const typename Elem<BF>::type* __restri
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int half = wave >> 2, wq = wave & 3;
   const int g = lane >> 5;
-  const int64_t m_blk = (int64_t)blockIdx.x * BM;
-  const int nb0 = blockIdx.y * BNF;
+  int bx, by;
+  xcd_patch(bx, by);
+  const int64_t m_blk = (int64_t)bx * BM;
+  const int nb0 = by * BNF;
   const int nsg = p.I_sg / G::SGI;
   const int sg0 = blockIdx.z * sg_per_split;
   const int sg1 = min(nsg, sg0 + sg_per_split);
@@ -1240,7 +1258,8 @@ k_dc_pipe(const typename Elem<BF>::type* __restrict__ dYc, const float* __restri
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int half = wave / WG, wq = wave % WG, dh = wq % DQ, og = wq / DQ;
   const int g = lane >> 5;
-  const int ib = blockIdx.x, obk = blockIdx.y;
+  int ib, obk;
+  xcd_patch(ib, obk);
   const int nst_all = (int)(p.KBc / KI);
   const int st0 = blockIdx.z * st_per_split;
   const int st1 = min(nst_all, st0 + st_per_split);
