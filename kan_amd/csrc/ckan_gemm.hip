@@ -763,39 +763,43 @@ k_dx_pipe(const typename Elem<BF>::type* __restrict__ dYx,
 }
 
 // ---------------------------------------------------------------------------
-// dX, two resident blocks per CU.  One block = 4 waves (dh, rg): wave rg takes
+// dX for degrees up to 8.  One block = 2*RG waves (dh, rg): wave rg takes
 // NM = 2 fragments of 32 rows, wave dh half of the P degrees, for one input
-// block (32 inputs); acc = NM x P/2 fragments, so two blocks share a CU and
-// one block's epilogue overlaps the other's MFMAs.  Both operands (dy rows and
-// the degree-scaled coefficients) arrive by LDS DMA in a ring of NBUF stages
-// of KI k-blocks.  Epilogue: each wave sums its degrees with U_{d-1}(t), the
-// dh pair exchanges halves through LDS, and each wave stores one fragment row
-// of dx = (1 - t^2) sum_d d C U_{d-1}(t) dy.
+// block (32 inputs); acc = NM x P/2 fragments, two waves per SIMD.  RG = 4
+// (256 rows per block, one block per CU) streams a third less operand data
+// per MFMA than RG = 2 (two 128-row blocks per CU, whose epilogues overlap
+// each other's MFMAs) and measures faster.  Both operands (dy rows and the
+// degree-scaled coefficients) arrive by LDS DMA in a ring of NBUF stages of
+// KI k-blocks.  Epilogue: each wave sums its degrees with U_{d-1}(t), the dh
+// pair exchanges halves through LDS, and each wave stores one fragment row of
+// dx = (1 - t^2) sum_d d C U_{d-1}(t) dy.
 // ---------------------------------------------------------------------------
 template <int P, bool BF>
-struct DxTwo {
+struct DxDh {
   typedef typename Elem<BF>::type E;
-  static constexpr int NM = 2, PH = P / 2;
+  static constexpr int RG = 4;  // row groups: 2 * RG waves
+  static constexpr int NM = 2, PH = P / 2, THR = 2 * RG * 64;
   static constexpr int FB = kFragElems * (int)sizeof(E);
   static constexpr int KI_BF = (P == 16) ? 1 : 2;
   static constexpr int KI = BF ? KI_BF : 1;
-  static constexpr int A_BYTES = 2 * NM * KI * FB;  // 4 row fragments
+  static constexpr int A_BYTES = RG * NM * KI * FB;
   static constexpr int B_BYTES = P * KI * FB;
   static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
   static constexpr int NBUF = 3;
   static constexpr int LDS_BYTES = NBUF * STAGE_BYTES;
-  static constexpr int OPS = STAGE_BYTES / 4096;  // dma16 per thread per stage
-  static constexpr int A_OPS = A_BYTES / 4096;
-  static constexpr bool kOk = P >= 2 && P <= 8 && LDS_BYTES <= 80 * 1024 && A_BYTES % 4096 == 0 &&
-                              B_BYTES % 4096 == 0 && 2 * 16 * 64 * 4 * 4 <= LDS_BYTES;
+  static constexpr int OPS = STAGE_BYTES / (THR * 16);  // dma16 per thread per stage
+  static constexpr int A_OPS = A_BYTES / (THR * 16);
+  static constexpr bool kOk = P >= 2 && P <= 8 && LDS_BYTES <= 160 * 1024 &&
+                              A_BYTES % (THR * 16) == 0 && B_BYTES % (THR * 16) == 0 &&
+                              2 * RG * 16 * 64 * 4 <= LDS_BYTES;
 };
 
 template <int P, bool BF>
-__global__ void __launch_bounds__(256, 2)
-k_dx_two(const typename Elem<BF>::type* __restrict__ dYx,
+__global__ void __launch_bounds__(512)
+k_dx_dh(const typename Elem<BF>::type* __restrict__ dYx,
          const typename Elem<BF>::type* __restrict__ Cb, const float* __restrict__ tc,
          float* __restrict__ dx, Plan p, int n_rb) {
-  typedef DxTwo<P, BF> K;
+  typedef DxDh<P, BF> K;
   typedef typename K::E E;
   constexpr int NM = K::NM, PH = K::PH, KI = K::KI, FB = K::FB, NBUF = K::NBUF, OPS = K::OPS;
   constexpr int RUN = KI * FB / 16;  // 16-byte chunks per fragment run of a stage
@@ -808,17 +812,19 @@ k_dx_two(const typename Elem<BF>::type* __restrict__ dYx,
   const int rb = blockIdx.x % n_rb, ib = blockIdx.x / n_rb;
 
   // per-op source offsets; dYx rows are padded to whole row blocks
-  const char* abase = reinterpret_cast<const char*>(dYx) + (size_t)rb * 2 * NM * p.KBx * FB;
+  constexpr int RG = K::RG, THR = K::THR;
+  static_assert(THR == 512, "launch bounds");
+  const char* abase = reinterpret_cast<const char*>(dYx) + (size_t)rb * RG * NM * p.KBx * FB;
   const char* bbase = reinterpret_cast<const char*>(Cb) + (size_t)ib * P * p.KBx * FB;
   size_t off[OPS];
 #pragma unroll
   for (int q = 0; q < OPS; ++q) {
-    const int c = q * 256 + tid;
+    const int c = q * THR + tid;
     if (q < K::A_OPS) {
       const int run = c / RUN, w = c - run * RUN;
       off[q] = (size_t)run * p.KBx * FB + w * 16;
     } else {
-      const int cc = c - K::A_OPS * 256;
+      const int cc = c - K::A_OPS * THR;
       const int e = cc / RUN, w = cc - e * RUN;
       off[q] = (size_t)e * p.KBx * FB + w * 16;
     }
@@ -828,7 +834,7 @@ k_dx_two(const typename Elem<BF>::type* __restrict__ dYx,
     const size_t sb = (size_t)st * KI * FB;
     char* dst = smem + (st % NBUF) * K::STAGE_BYTES + wave * 1024;
 #pragma unroll
-    for (int q = 0; q < OPS; ++q) dma16((q < K::A_OPS ? abase : bbase) + sb + off[q], dst + q * 4096);
+    for (int q = 0; q < OPS; ++q) dma16((q < K::A_OPS ? abase : bbase) + sb + off[q], dst + q * (THR * 16));
   };
 
   // epilogue tanh values, loaded up front (they complete long before use)
@@ -837,7 +843,7 @@ k_dx_two(const typename Elem<BF>::type* __restrict__ dYx,
   float tt[NM][16];
 #pragma unroll
   for (int mi = 0; mi < NM; ++mi) {
-    const int64_t r0 = ((int64_t)rb * 2 * NM + rg * NM + mi) * 32 + 4 * g;
+    const int64_t r0 = ((int64_t)rb * RG * NM + rg * NM + mi) * 32 + 4 * g;
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
       const int64_t r = r0 + 8 * (v >> 2) + (v & 3);
@@ -917,7 +923,7 @@ k_dx_two(const typename Elem<BF>::type* __restrict__ dYx,
     for (int v = 0; v < 16; ++v) xch[((rg * 2 + d) * 16 + v) * 64 + lane] = part[give][v];
     wait_lgkmcnt<0>();
     block_barrier();
-    const int64_t r0 = ((int64_t)rb * 2 * NM + rg * NM + keep) * 32 + 4 * g;
+    const int64_t r0 = ((int64_t)rb * RG * NM + rg * NM + keep) * 32 + 4 * g;
     float res[16];
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
@@ -1647,12 +1653,12 @@ static void dx_dispatch(const void* dYx, const void* packed, const float* t, flo
   typedef typename Elem<BF>::type E;
   constexpr int NM = BwdTile<P>::NM;
   const E* Cb = reinterpret_cast<const E*>(packed) + packed_cf_elems(p);
-  if constexpr (DxTwo<P, BF>::kOk) {
-    typedef DxTwo<P, BF> K;
-    const int n_rb = (int)ceil_div(p.B32 / 32, 2 * K::NM);
+  if constexpr (DxDh<P, BF>::kOk) {
+    typedef DxDh<P, BF> K;
+    const int n_rb = (int)ceil_div(p.B32 / 32, K::RG * K::NM);
     static std::atomic<uint32_t> lds_set{0};
-    ensure_lds_limit(reinterpret_cast<const void*>(&k_dx_two<P, BF>), K::LDS_BYTES, lds_set);
-    hipLaunchKernelGGL((k_dx_two<P, BF>), dim3(n_rb * p.NIB), dim3(256), K::LDS_BYTES, s,
+    ensure_lds_limit(reinterpret_cast<const void*>(&k_dx_dh<P, BF>), K::LDS_BYTES, lds_set);
+    hipLaunchKernelGGL((k_dx_dh<P, BF>), dim3(n_rb * p.NIB), dim3(K::THR), K::LDS_BYTES, s,
                        reinterpret_cast<const E*>(dYx), Cb, t, dx, p, n_rb);
     return;
   }
