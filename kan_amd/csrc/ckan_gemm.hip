@@ -778,10 +778,9 @@ template <int P, bool BF>
 struct DxDh {
   typedef typename Elem<BF>::type E;
   static constexpr int RG = 4;  // row groups: 2 * RG waves
-  static constexpr int NM = 2, PH = P / 2, THR = 2 * RG * 64;
+  static constexpr int NM = P == 16 ? 1 : 2, PH = P / 2, THR = 2 * RG * 64;
   static constexpr int FB = kFragElems * (int)sizeof(E);
-  static constexpr int KI_BF = (P == 16) ? 1 : 2;
-  static constexpr int KI = BF ? KI_BF : 1;
+  static constexpr int KI = BF ? 2 : 1;
   static constexpr int A_BYTES = RG * NM * KI * FB;
   static constexpr int B_BYTES = P * KI * FB;
   static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
@@ -789,7 +788,7 @@ struct DxDh {
   static constexpr int LDS_BYTES = NBUF * STAGE_BYTES;
   static constexpr int OPS = STAGE_BYTES / (THR * 16);  // dma16 per thread per stage
   static constexpr int A_OPS = A_BYTES / (THR * 16);
-  static constexpr bool kOk = P >= 2 && P <= 8 && LDS_BYTES <= 160 * 1024 &&
+  static constexpr bool kOk = P >= 2 && LDS_BYTES <= 160 * 1024 &&
                               A_BYTES % (THR * 16) == 0 && B_BYTES % (THR * 16) == 0 &&
                               2 * RG * 16 * 64 * 4 <= LDS_BYTES;
 };
@@ -915,14 +914,19 @@ k_dx_dh(const typename Elem<BF>::type* __restrict__ dYx,
       }
       part[mi][v] = sum;
     }
-  // wave (dh, rg) keeps fragment row mi = dh and hands mi = 1 - dh to its pair
+  // with NM = 2 wave (dh, rg) keeps fragment row mi = dh and hands mi = 1 - dh
+  // to its pair; with NM = 1 the dh = 1 wave hands its sums to the dh = 0 wave
   float* xch = reinterpret_cast<float*>(smem);
   auto finish = [&](auto DH) __attribute__((always_inline)) {
-    constexpr int d = decltype(DH)::value, keep = d, give = 1 - d;
+    constexpr int d = decltype(DH)::value;
+    constexpr int keep = NM == 2 ? d : 0, give = NM == 2 ? 1 - d : 0;
+    if (NM == 2 || d == 1) {
 #pragma unroll
-    for (int v = 0; v < 16; ++v) xch[((rg * 2 + d) * 16 + v) * 64 + lane] = part[give][v];
+      for (int v = 0; v < 16; ++v) xch[((rg * 2 + d) * 16 + v) * 64 + lane] = part[give][v];
+    }
     wait_lgkmcnt<0>();
     block_barrier();
+    if (NM == 1 && d == 1) return;  // no barrier follows
     const int64_t r0 = ((int64_t)rb * RG * NM + rg * NM + keep) * 32 + 4 * g;
     float res[16];
 #pragma unroll
