@@ -10,12 +10,13 @@ namespace ckan {
 // Replaces torch.tanh (kan/basis/chebyshev.py:78).  tpr threads per row
 // (a power of two dividing 256) take float4 columns; 256/tpr rows per block.
 __global__ void __launch_bounds__(256)
-k_tanh(const float* __restrict__ x, float* __restrict__ t, int64_t B, int I, int I_sg, int tpr) {
+k_tanh(const float* __restrict__ x, float* __restrict__ t, int64_t B, int I, int I_sg, int tpr,
+       int xal) {
   const int rpb = 256 / tpr;
   const int64_t b = (int64_t)blockIdx.x * rpb + threadIdx.x / tpr;
   if (b >= B) return;
   const int n4 = I_sg / 4;
-  const bool vec = (I % 4) == 0;
+  const bool vec = xal && (I % 4) == 0;
   const float* xr = x + b * I;
   float* tr = t + b * I_sg;
   for (int c4 = threadIdx.x % tpr; c4 < n4; c4 += tpr) {
@@ -31,6 +32,30 @@ k_tanh(const float* __restrict__ x, float* __restrict__ t, int64_t B, int I, int
 #pragma unroll
     for (int j = 0; j < 4; ++j) r[j] = (i + j < I) ? tanhf(v[j]) : 0.0f;
     *reinterpret_cast<f32x4_t*>(tr + i) = r;
+  }
+}
+
+// Same, when rows need no padding (I == I_sg, I % 4 == 0): x and t are flat
+// arrays of n4 float4.  Each thread issues its kTanhU loads (block-strided, so
+// each instruction is one contiguous 4 KiB run per block) before any tanh.
+// Two per thread measured fastest (one to eight tried).
+constexpr int kTanhU = 2;
+__global__ void __launch_bounds__(256)
+k_tanh_flat(const f32x4_t* __restrict__ x, f32x4_t* __restrict__ t, int64_t n4) {
+  const int64_t base = (int64_t)blockIdx.x * (256 * kTanhU) + threadIdx.x;
+  f32x4_t v[kTanhU];
+#pragma unroll
+  for (int u = 0; u < kTanhU; ++u) {
+    const int64_t k = base + u * 256;
+    v[u] = k < n4 ? x[k] : f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+#pragma unroll
+  for (int u = 0; u < kTanhU; ++u) {
+    const int64_t k = base + u * 256;
+    f32x4_t r;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) r[j] = tanhf(v[u][j]);
+    if (k < n4) t[k] = r;
   }
 }
 
@@ -51,7 +76,7 @@ template <> __device__ __forceinline__ float to_f32<uint16_t>(uint16_t v) {
 template <int P, bool BF, typename CT>
 __global__ void __launch_bounds__(256)
 k_pack(const CT* __restrict__ C, typename Elem<BF>::type* __restrict__ Cf,
-       typename Elem<BF>::type* __restrict__ Cb, float* __restrict__ bias_part, Plan p) {
+       typename Elem<BF>::type* __restrict__ Cb, float* __restrict__ bias_part, Plan p, int cal) {
   using G = FwdGroup<P>;
   constexpr int RPMAX = 32 * (P + 1) + 1;
   __shared__ float tile[32 * RPMAX];
@@ -65,7 +90,7 @@ k_pack(const CT* __restrict__ C, typename Elem<BF>::type* __restrict__ Cf,
   const int nrow = ocount > 0 ? ocount * D : 0;
   // Each input's run of 32*D values is contiguous in C.  When the run is
   // 16-byte aligned, every thread issues its float4 loads before any use.
-  const bool vec = sizeof(CT) == 4 && ((size_t)p.O * D) % 4 == 0 && ocount == 32;
+  const bool vec = sizeof(CT) == 4 && cal && ((size_t)p.O * D) % 4 == 0 && ocount == 32;
   if (vec) {
     constexpr int MAXV = (32 * 32 * (P + 1) / 4 + 255) / 256;  // float4 per thread
     const int nv = 32 * 8 * D;                                   // float4 in the tile
@@ -170,69 +195,64 @@ k_col_reduce(const float* __restrict__ part, int nparts, int pitch, int n, float
   if (q == 0 && o < n) out[o] = ((q4[0][ol] + q4[1][ol]) + q4[2][ol]) + q4[3][ol];
 }
 
-// 8 consecutive values of row b of dy starting at column o (zero outside B x O).
-__device__ __forceinline__ void load_row8(const float* __restrict__ dy, int64_t b, int o,
-                                          const Plan& p, float* v) {
-  if (b < p.B && o + 8 <= p.O && (p.O & 3) == 0) {
-    const f32x4_t* src = reinterpret_cast<const f32x4_t*>(dy + b * p.O + o);
-    const f32x4_t a = src[0], c = src[1];
-    v[0] = a[0]; v[1] = a[1]; v[2] = a[2]; v[3] = a[3];
-    v[4] = c[0]; v[5] = c[1]; v[6] = c[2]; v[7] = c[3];
-  } else {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = (b < p.B && o + j < p.O) ? dy[b * p.O + o + j] : 0.0f;
-  }
-}
-
 // Re-lays dy [B, O] (fp32) into
 //   dYx: dX A operand  [B32/32][KBx][64][8]  (rows b, reduction o)
 //   dYc: dC B operand  [NBf][KBc][64][8]     (columns o, reduction b)
 // and writes colsum_part[bb][o] = sum of dy over rows [64 bb, 64 bb + 64).
-// One wave per (32 columns, 64 rows).  The wave reads its tile of dy once
-// (each lane 8 consecutive columns of a row: the dYx fragment layout) and,
-// when dYc is needed, transposes it through LDS for the dYc fragments (each
-// lane 8 consecutive rows of a column).
+// One wave per (32 columns, 64 rows).  The wave reads its tile of dy once,
+// each load instruction covering 8 whole 128-byte row segments, writes it to a
+// private LDS tile and reads it back in both fragment orders: 8 consecutive
+// columns of a row per lane (dYx) and 8 consecutive rows of a column (dYc).
 template <bool BF>
 __global__ void __launch_bounds__(256)
 k_prep_dy(const float* __restrict__ dy, typename Elem<BF>::type* __restrict__ dYx,
-          typename Elem<BF>::type* __restrict__ dYc, float* __restrict__ colsum_part,
-          Plan p, int need_dx, int need_dc, int nob, int nbb, int64_t dx_rows) {
-  constexpr int TP = 33;  // padded row pitch of the transpose tile
-  __shared__ float tile[4][kPrepRows * TP];
+           typename Elem<BF>::type* __restrict__ dYc, float* __restrict__ colsum_part,
+           Plan p, int need_dx, int need_dc, int nob, int nbb, int64_t dx_rows, int dyal) {
+  constexpr int TP = 36;  // row pitch (floats): 16-byte aligned rows
+  __shared__ __attribute__((aligned(16))) float tile[4][kPrepRows * TP];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int w = blockIdx.x * 4 + wv;
-  if (w >= nob * nbb) return;  // whole waves only: no block barrier below
+  if (w >= nob * nbb) return;
   const int ob = w % nob, bb = w / nob;
   const int g = lane >> 5, c = lane & 31;
+  const int rs = lane >> 3, q = lane & 7;
   const int64_t r0 = (int64_t)bb * kPrepRows;
-  float v[kPrepRows / 32][2][8];
+  const int o = ob * 32 + 4 * q;
+  const bool vec = dyal && (p.O & 3) == 0 && o + 4 <= p.O;
+  f32x4_t v[kPrepRows / 8];
 #pragma unroll
-  for (int mbl = 0; mbl < kPrepRows / 32; ++mbl)
+  for (int m = 0; m < kPrepRows / 8; ++m) {
+    const int64_t b = r0 + m * 8 + rs;
+    if (b < p.B && vec) {
+      v[m] = *reinterpret_cast<const f32x4_t*>(dy + b * p.O + o);
+    } else {
 #pragma unroll
-    for (int kbl = 0; kbl < 2; ++kbl)
-      load_row8(dy, r0 + mbl * 32 + c, ob * 32 + 16 * kbl + 8 * g, p, v[mbl][kbl]);
+      for (int j = 0; j < 4; ++j) v[m][j] = (b < p.B && o + j < p.O) ? dy[b * p.O + o + j] : 0.0f;
+    }
+  }
+  float* t = tile[wv];
+#pragma unroll
+  for (int m = 0; m < kPrepRows / 8; ++m) *reinterpret_cast<f32x4_t*>(t + (m * 8 + rs) * TP + 4 * q) = v[m];
+  // the tile is private to this wave, whose LDS accesses are performed in
+  // issue order; the compiler barrier keeps the reads after the writes
+  asm volatile("" ::: "memory");
   if (need_dx) {
 #pragma unroll
     for (int mbl = 0; mbl < kPrepRows / 32; ++mbl) {
       const int64_t b0 = r0 + mbl * 32;
       if (b0 < dx_rows) {
 #pragma unroll
-        for (int kbl = 0; kbl < 2; ++kbl)
-          store_frag<BF>(dYx + ((size_t)(b0 / 32) * p.KBx + ob * 2 + kbl) * kFragElems, lane, v[mbl][kbl]);
+        for (int kbl = 0; kbl < 2; ++kbl) {
+          const float* src = t + (mbl * 32 + c) * TP + 16 * kbl + 8 * g;
+          const f32x4_t a = *reinterpret_cast<const f32x4_t*>(src);
+          const f32x4_t e = *reinterpret_cast<const f32x4_t*>(src + 4);
+          const float vv[8] = {a[0], a[1], a[2], a[3], e[0], e[1], e[2], e[3]};
+          store_frag<BF>(dYx + ((size_t)(b0 / 32) * p.KBx + ob * 2 + kbl) * kFragElems, lane, vv);
+        }
       }
     }
   }
   if (need_dc && ob < p.NBf) {
-    float* t = tile[wv];
-#pragma unroll
-    for (int mbl = 0; mbl < kPrepRows / 32; ++mbl)
-#pragma unroll
-      for (int kbl = 0; kbl < 2; ++kbl)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) t[(mbl * 32 + c) * TP + 16 * kbl + 8 * g + j] = v[mbl][kbl][j];
-    // the tile is private to this wave, whose LDS accesses are performed in
-    // issue order; the compiler barrier keeps the reads after the writes
-    asm volatile("" ::: "memory");
     float u[kPrepRows / 16][8];
 #pragma unroll
     for (int kbl = 0; kbl < kPrepRows / 16; ++kbl)
@@ -403,10 +423,17 @@ static int grid_for(int64_t work, int per_block = 256) {
 }
 
 void launch_tanh(const float* x, float* t, const Plan& p, hipStream_t s) {
+  if (p.I == p.I_sg && p.I % 4 == 0 && is_al16(x)) {
+    const int64_t n4 = p.B * p.I / 4;
+    hipLaunchKernelGGL(k_tanh_flat, dim3((unsigned)ceil_div(n4, 256 * kTanhU)), dim3(256), 0, s,
+                       reinterpret_cast<const f32x4_t*>(x), reinterpret_cast<f32x4_t*>(t), n4);
+    return;
+  }
   int tpr = 1;
   while (tpr < 256 && tpr < p.I_sg / 4) tpr *= 2;
   const int64_t blocks = ceil_div(p.B, 256 / tpr);
-  hipLaunchKernelGGL(k_tanh, dim3((unsigned)blocks), dim3(256), 0, s, x, t, p.B, p.I, p.I_sg, tpr);
+  hipLaunchKernelGGL(k_tanh, dim3((unsigned)blocks), dim3(256), 0, s, x, t, p.B, p.I, p.I_sg, tpr,
+                     (int)is_al16(x));
 }
 
 template <int P, bool BF>
@@ -420,10 +447,10 @@ static void launch_pack_t(const void* C, bool c_bf16, void* packed, const Plan& 
   dim3 grid(p.NIB, p.O64 / 32);
   if (c_bf16)
     hipLaunchKernelGGL((k_pack<P, BF, uint16_t>), grid, dim3(256), 0, s,
-                       reinterpret_cast<const uint16_t*>(C), Cf, Cb, bias, p);
+                       reinterpret_cast<const uint16_t*>(C), Cf, Cb, bias, p, 0);
   else
     hipLaunchKernelGGL((k_pack<P, BF, float>), grid, dim3(256), 0, s,
-                       reinterpret_cast<const float*>(C), Cf, Cb, bias, p);
+                       reinterpret_cast<const float*>(C), Cf, Cb, bias, p, (int)is_al16(C));
 }
 
 void launch_pack(const void* C, bool c_bf16, void* packed, const Plan& p, hipStream_t s) {
@@ -452,11 +479,11 @@ void launch_prep_dy(const float* dy, void* dYx, void* dYc, float* colsum_part, c
   if (p.esz == 2)
     hipLaunchKernelGGL((k_prep_dy<true>), grid, dim3(256), 0, s, dy,
                        reinterpret_cast<uint16_t*>(dYx), reinterpret_cast<uint16_t*>(dYc),
-                       colsum_part, p, (int)need_dx, (int)need_dc, nob, nbb, dx_rows);
+                       colsum_part, p, (int)need_dx, (int)need_dc, nob, nbb, dx_rows, (int)is_al16(dy));
   else
     hipLaunchKernelGGL((k_prep_dy<false>), grid, dim3(256), 0, s, dy,
                        reinterpret_cast<float*>(dYx), reinterpret_cast<float*>(dYc),
-                       colsum_part, p, (int)need_dx, (int)need_dc, nob, nbb, dx_rows);
+                       colsum_part, p, (int)need_dx, (int)need_dc, nob, nbb, dx_rows, (int)is_al16(dy));
 }
 
 float* launch_colsum_reduce(float* colsum_part, const Plan& p, hipStream_t s) {

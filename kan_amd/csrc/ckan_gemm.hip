@@ -503,7 +503,7 @@ template <int P, bool BF, int NMS>
 __global__ void __launch_bounds__(256)
 k_fwd_stream(const float* __restrict__ x, float* __restrict__ tc,
              const typename Elem<BF>::type* __restrict__ Cf, float* __restrict__ part, Plan p,
-             int bpn) {
+             int bpn, int xal) {
   typedef FwdGroup<P> G;
   typedef FwdStream<P, BF> K;
   constexpr int SPW = K::SPW, KPW = K::KPW, LT = G::LANE_T;
@@ -525,7 +525,7 @@ k_fwd_stream(const float* __restrict__ x, float* __restrict__ tc,
         : zero_frag<BF>();
   }
   float xv[NMS][SPW][LT];
-  const bool xvec = (p.I & 3) == 0;  // LT is a multiple of 4, so are the lane offsets
+  const bool xvec = xal && (p.I & 3) == 0;  // LT is a multiple of 4, so are the lane offsets
 #pragma unroll
   for (int mi = 0; mi < NMS; ++mi) {
     const int r = mi * 32 + (lane & 31);
@@ -1600,9 +1600,9 @@ static void fwd_dispatch(const float* x, float* t, const void* packed, float* y,
   if (fwd_streaming(c)) {
     dim3 g1(c.tiles_n * c.splits);
     if (c.tile == kFwdStream32)
-      hipLaunchKernelGGL((k_fwd_stream<P, BF, 1>), g1, dim3(256), 0, s, x, t, Cf, part, p, c.splits);
+      hipLaunchKernelGGL((k_fwd_stream<P, BF, 1>), g1, dim3(256), 0, s, x, t, Cf, part, p, c.splits, (int)is_al16(x));
     else
-      hipLaunchKernelGGL((k_fwd_stream<P, BF, 2>), g1, dim3(256), 0, s, x, t, Cf, part, p, c.splits);
+      hipLaunchKernelGGL((k_fwd_stream<P, BF, 2>), g1, dim3(256), 0, s, x, t, Cf, part, p, c.splits, (int)is_al16(x));
   } else {
     dim3 grid(c.tiles_m, c.tiles_n, c.splits);
     switch (c.tile) {

@@ -7,6 +7,8 @@
 namespace ckan {
 
 inline size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+// 16-byte aligned: the float4 load paths of x, dy and C require it.
+inline bool is_al16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
 
 // Sets the thread-local message returned by ckan_last_error().
 void set_last_error(const char* msg);

@@ -236,6 +236,33 @@ def test_integration_ctypes_stub():
         assert _rel(y.cpu(), orc.layer_forward(x, c)) <= FP32_TOL
 
 
+def _offset_view(t):
+    """A contiguous copy of t whose data pointer is 4 bytes past a 16-byte boundary."""
+    full = torch.empty(t.numel() + 4, dtype=t.dtype, device=t.device)
+    v = full[1:1 + t.numel()].view(t.shape)
+    v.copy_(t)
+    return v
+
+
+@pytest.mark.parametrize("B,I,O,deg", [(512, 256, 128, 8), (16, 512, 96, 4), (300, 64, 48, 16)])
+def test_misaligned_inputs_take_scalar_loads(B, I, O, deg):
+    """x, dy and C at 4-byte (not 16-byte) alignment: the float4 load paths must not be taken."""
+    from kan_amd import functional as F
+    print(f"misaligned inputs B={B} I={I} O={O} deg={deg}", flush=True)
+    x, c, dy = _inputs(B, I, O, deg, seed=B + deg)
+    y_ref, dx_ref, dc_ref = orc.layer_forward_backward(x, c, dy)
+    xd = _offset_view(x.cuda()).requires_grad_(True)
+    cd = _offset_view(c.cuda()).requires_grad_(True)
+    dyd = _offset_view(dy.cuda())
+    assert xd.data_ptr() % 16 == 4 and cd.data_ptr() % 16 == 4 and dyd.data_ptr() % 16 == 4
+    y = F.chebykan(xd, cd, "fp32")
+    y.backward(dyd)
+    torch.cuda.synchronize()
+    assert _rel(y, y_ref) <= FP32_TOL
+    assert _rel(xd.grad, dx_ref) <= FP32_TOL
+    assert _rel(cd.grad, dc_ref) <= FP32_TOL
+
+
 def test_deterministic_results():
     x, c, dy = _inputs(512, 128, 128, 8, seed=9)
     a = _gpu_fwd_bwd(x, c, dy, "bf16")
