@@ -263,6 +263,16 @@ struct FwdPipe {
                               B_BYTES % (16 * THREADS) == 0 && T_BYTES % (16 * THREADS) == 0;
 };
 
+// XOR applied to the 16-byte chunk index of row r of the forward kernel's tanh
+// tile (CR chunks per row).  A wave reads one chunk of 32 consecutive rows per
+// instruction; with it, every 16-lane (64 banks) and 8-lane (32 banks) group of
+// a 16-byte read covers distinct banks.  XOR-linear in the row bits.
+template <int CR> __device__ __forceinline__ int fwd_t_xor(int r) {
+  if constexpr (CR == 2) return ((r >> 2) ^ (r >> 3)) & 1;
+  else if constexpr (CR == 4) return ((r >> 2) & 1) | ((((r >> 1) ^ (r >> 3)) & 1) << 1);
+  else return ((r >> 1) & 1) | (((r >> 2) & 1) << 1) | (((r ^ (r >> 3)) & 1) << 2);
+}
+
 template <int P, bool BF>
 __global__ void __launch_bounds__(512)
 k_fwd_pipe(const float* __restrict__ tc, const typename Elem<BF>::type* __restrict__ Cf,
@@ -303,10 +313,10 @@ k_fwd_pipe(const float* __restrict__ tc, const typename Elem<BF>::type* __restri
 #pragma unroll
   for (int q = 0; q < K::T_OPS; ++q) {
     const int c = (q * 8 + wave) * 64 + lane;
-    const int rl = c / (G::SGI / 4), part4 = c - rl * (G::SGI / 4);
+    const int rl = c / (G::SGI / 4), part4 = c - rl * (G::SGI / 4);  // stored chunk
     int64_t r = m_blk + rl;
     if (r >= p.B) r = p.B - 1;
-    toff[q] = ((size_t)r * p.I_sg + part4 * 4) * 4;
+    toff[q] = ((size_t)r * p.I_sg + (part4 ^ fwd_t_xor<G::SGI / 4>(rl)) * 4) * 4;
   }
   const size_t b_stride = (size_t)G::SGK * kFragElems * sizeof(E);
   const size_t t_stride = (size_t)G::SGI * 4;
@@ -350,10 +360,11 @@ k_fwd_pipe(const float* __restrict__ tc, const typename Elem<BF>::type* __restri
 #pragma unroll
     for (int mi = 0; mi < NM; ++mi) {
       const int rl = (wq * NM + mi) * 32 + (lane & 31);
-      const f32x4_t* src = reinterpret_cast<const f32x4_t*>(tl + rl * G::SGI + g * G::LANE_T);
+      const f32x4_t* src = reinterpret_cast<const f32x4_t*>(tl + rl * G::SGI);
+      const int sx = fwd_t_xor<G::SGI / 4>(rl);
 #pragma unroll
       for (int q = 0; q < G::LANE_T / 4; ++q) {
-        const f32x4_t w = src[q];
+        const f32x4_t w = src[(g * (G::LANE_T / 4) + q) ^ sx];
         tv[mi][4 * q + 0] = w[0]; tv[mi][4 * q + 1] = w[1];
         tv[mi][4 * q + 2] = w[2]; tv[mi][4 * q + 3] = w[3];
       }
@@ -1294,10 +1305,23 @@ k_dc_pipe(const typename Elem<BF>::type* __restrict__ dYc, const float* __restri
     dhs[q] = hs;
     doff[q] = ((size_t)mf * p.KBc + kk) * FB + (size_t)piece * 16;
   }
-  // tanh DMA: chunk c = tid % T_CHUNKS is [stage hs][row rr][16 B of the 32 inputs]
+  // tanh tile of a stage: rows of 32 fp32 inputs.  Row rho is stored at row
+  // t_row(rho) with its 16-byte chunks XOR-ed by t_xor(rho) / 4, so that the
+  // generation reads (G row groups x 64/G columns per wave, see gen) hit 64
+  // distinct banks, and each 32-lane half 32 distinct banks.  t_row only flips
+  // bit 0 and t_xor reads bits 1..2, so both are unchanged by t_row.
+  constexpr int G = 8 / RPT;  // generation row groups
+  auto t_row = [](int r) __attribute__((always_inline)) {
+    return RPT == 4 ? r ^ ((r >> 2) & 1) : RPT == 2 ? r ^ ((r >> 1) & 1) : r;
+  };
+  auto t_xor = [](int r) __attribute__((always_inline)) {
+    return RPT == 4 ? 16 * ((r >> 2) & 1) : RPT == 2 ? 8 * ((r >> 1) & 3) : 4 * (r & 7);
+  };
+  // tanh DMA: chunk c = tid % T_CHUNKS fills [stage hs][stored row rr][chunk c % 8]
   const int tcn = tid % K::T_CHUNKS;
   const int ths = tcn / (K::T_STAGE / 16), trr = (tcn % (K::T_STAGE / 16)) / 8;
-  const int tcol = min(ib * 32 + (tcn % 8) * 4, p.I_sg - 4);  // inputs past I_sg: never stored
+  const int tsrc_row = t_row(trr);  // t_row is an involution
+  const int tcol = min(ib * 32 + (((tcn % 8) * 4) ^ t_xor(trr)), p.I_sg - 4);  // inputs past I_sg: never stored
   const char* tcb = reinterpret_cast<const char*>(tc);
   auto dma_dy = [&](int j) __attribute__((always_inline)) {
     char* dst = dyr + (j % 3) * K::DY_SLOT + wave * 1024;
@@ -1311,22 +1335,22 @@ k_dc_pipe(const typename Elem<BF>::type* __restrict__ dYc, const float* __restri
   auto dma_t = [&](int j) __attribute__((always_inline)) {
     int st = st0 + H * j + ths;
     if (st >= st1) st = st0;
-    int64_t b = (int64_t)st * KI * 16 + trr;
+    int64_t b = (int64_t)st * KI * 16 + tsrc_row;
     if (b >= p.B) b = p.B - 1;  // dy is zero on rows past B
     dma16(tcb + ((size_t)b * p.I_sg + tcol) * 4, tlr + (j % 3) * K::T_SLOT + wave * 1024);
   };
 
   // basis generation slot of this thread within its half: k-block gkk,
-  // fragment lane gl, rows grh*RPT .. +RPT of the lane's 8
+  // fragment lane gl, rows grh*RPT .. +RPT of the lane's 8.  The G threads of
+  // one fragment lane are adjacent, so each wave writes one contiguous run.
   const int th = tid % (512 / H);
-  const int gslot = th % (KI * 64), gkk = gslot / 64, gl = gslot % 64;
-  const int grh = th / (KI * 64);
+  const int grh = th % G, gl = (th / G) % 64, gkk = th / (G * 64);
   const int trow0 = gkk * 16 + 8 * (gl >> 5) + grh * RPT;
   auto gen = [&](int j) __attribute__((always_inline)) {
     const float* tl = reinterpret_cast<const float*>(tlr + (j % 3) * K::T_SLOT + half * K::T_STAGE);
     float tv[RPT];
 #pragma unroll
-    for (int r = 0; r < RPT; ++r) tv[r] = tl[(trow0 + r) * 32 + (gl & 31)];
+    for (int r = 0; r < RPT; ++r) tv[r] = tl[t_row(trow0 + r) * 32 + ((gl & 31) ^ t_xor(trow0 + r))];
     char* dst = bas + ((j & 1) * H + half) * K::BAS_STAGE + gkk * FB + (gl * 8 + grh * RPT) * (int)sizeof(E);
     float a[RPT], b[RPT], t2[RPT];
 #pragma unroll
