@@ -103,6 +103,55 @@ int ckan_backward(const ckan_desc* desc, const float* t_cache, const void* packe
                   const float* dy, float* dx, float* dcoeffs, int accumulate,
                   void* ws, size_t ws_bytes, void* stream);
 
+/* ---- other polynomial bases through the same kernels ---------------------
+ * A layer whose basis is a three-term-recurrence family P_0..P_deg evaluated
+ * at s * tanh(x) is the ChebyKAN layer with coefficients C' = C M, where
+ *   P_n(s u) = sum_k M[n, k] T_k(u)      (M lower triangular, exact),
+ * and its coefficient gradient is dC = dC' M^T; the input gradient is the
+ * ChebyKAN layer's with C'.  So ckan_pack_coeffs_basis + ckan_forward +
+ * ckan_backward (into dC') + ckan_coeff_grad_from_chebyshev run such a layer.
+ * Families and the reference code each replaces:
+ *   JACOBI     P_n^(alpha,beta), alpha, beta > -1, s = 1: JacobiBasis
+ *              (kan/basis/jacobi.py:84-117,147-188), JacobiKANLayer
+ *              (kan/layers/jacobikan.py:26-77)
+ *   HERMITE    physicists' H_n; HermiteKANLayer's default input map is
+ *              s = 3 (kan/basis/hermite.py:85-116,158-193)
+ *   HERMITE_E  probabilists' He_n, s = 3 (kan/basis/hermite.py:195-233)
+ *   CHEBYSHEV  T_n (M = identity)
+ */
+typedef enum ckan_basis_family {
+  CKAN_BASIS_CHEBYSHEV = 0,
+  CKAN_BASIS_JACOBI = 1,
+  CKAN_BASIS_HERMITE = 2,
+  CKAN_BASIS_HERMITE_E = 3
+} ckan_basis_family;
+
+typedef struct ckan_basis_spec {
+  int32_t family;   /* ckan_basis_family                                      */
+  int32_t degree;   /* 0..16; equal to desc->degree where a desc is passed too */
+  double alpha;     /* Jacobi parameters (> -1); ignored by the other families */
+  double beta;
+  double scale;     /* s: the basis is evaluated at s * tanh(x) (finite)       */
+} ckan_basis_spec;
+
+/* Host only: M as (degree+1)^2 doubles, M[n * (degree+1) + k]. */
+int ckan_basis_to_chebyshev(const ckan_basis_spec* spec, double* M);
+/* ckan_pack_coeffs of C' = C M, for C in the family's basis (fp32 or bf16 per
+ * desc->coeff_dtype).  M is built on the host and passed by value. */
+int ckan_pack_coeffs_basis(const ckan_desc* desc, const ckan_basis_spec* spec, const void* coeffs,
+                           void* packed, void* stream);
+/* dcoeffs[i, o, n] (+)= sum_k dcheb[i, o, k] M[n, k] (fp32 [in, out, D]);
+ * dcheb may equal dcoeffs when accumulate == 0 (in place). */
+int ckan_coeff_grad_from_chebyshev(const ckan_desc* desc, const ckan_basis_spec* spec,
+                                   const float* dcheb, float* dcoeffs, int accumulate, void* stream);
+/* out[q, n] = P_n(t[q]), n = 0..degree, by the family's recurrence (the
+ * reference's basis_functions of an already-normalised input; s unused). */
+int ckan_family_basis(const ckan_basis_spec* spec, const float* t, int64_t n, float* out,
+                      void* stream);
+/* dt[q] = sum_n g[q, n] P_n'(t[q]): backward of ckan_family_basis. */
+int ckan_family_basis_backward(const ckan_basis_spec* spec, const float* t, const float* g,
+                               int64_t n, float* dt, void* stream);
+
 /* out[n, d] = T_d(t[n]) for d = 0..degree (fp32).  Replaces
  * ChebyshevBasis.basis_functions (kan/basis/chebyshev.py:103-172). */
 int ckan_basis(const float* t, int64_t n, int32_t degree, float* out, void* stream);

@@ -41,6 +41,27 @@ class CkanDesc(ctypes.Structure):
     ]
 
 
+CKAN_BASIS_CHEBYSHEV = 0
+CKAN_BASIS_JACOBI = 1
+CKAN_BASIS_HERMITE = 2
+CKAN_BASIS_HERMITE_E = 3
+
+
+class CkanBasisSpec(ctypes.Structure):
+    _fields_ = [
+        ("family", ctypes.c_int32),
+        ("degree", ctypes.c_int32),
+        ("alpha", ctypes.c_double),
+        ("beta", ctypes.c_double),
+        ("scale", ctypes.c_double),
+    ]
+
+
+def make_spec(family: int, degree: int, alpha: float = 0.0, beta: float = 0.0,
+              scale: float = 1.0) -> CkanBasisSpec:
+    return CkanBasisSpec(int(family), int(degree), float(alpha), float(beta), float(scale))
+
+
 class CkanError(RuntimeError):
     """Raised when a C-ABI call returns a non-zero ckan_status."""
 
@@ -56,6 +77,7 @@ _i32 = ctypes.c_int32
 _f32 = ctypes.c_float
 _f64 = ctypes.c_double
 _pdesc = ctypes.POINTER(CkanDesc)
+_pspec = ctypes.POINTER(CkanBasisSpec)
 
 # name -> (restype, argtypes); every function declared in include/chebykan.h
 SIGNATURES = {
@@ -67,6 +89,11 @@ SIGNATURES = {
     "ckan_pack_coeffs": (ctypes.c_int, [_pdesc, _vp, _vp, _vp]),
     "ckan_forward": (ctypes.c_int, [_pdesc, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "ckan_backward": (ctypes.c_int, [_pdesc, _vp, _vp, _vp, _vp, _vp, ctypes.c_int, _vp, _sz, _vp]),
+    "ckan_basis_to_chebyshev": (ctypes.c_int, [_pspec, ctypes.POINTER(_f64)]),
+    "ckan_pack_coeffs_basis": (ctypes.c_int, [_pdesc, _pspec, _vp, _vp, _vp]),
+    "ckan_coeff_grad_from_chebyshev": (ctypes.c_int, [_pdesc, _pspec, _vp, _vp, ctypes.c_int, _vp]),
+    "ckan_family_basis": (ctypes.c_int, [_pspec, _vp, _i64, _vp, _vp]),
+    "ckan_family_basis_backward": (ctypes.c_int, [_pspec, _vp, _vp, _i64, _vp, _vp]),
     "ckan_basis": (ctypes.c_int, [_vp, _i64, _i32, _vp, _vp]),
     "ckan_basis_backward": (ctypes.c_int, [_vp, _vp, _i64, _i32, _vp, _vp]),
     "ckan_sgd_step": (ctypes.c_int, [_vp, _vp, _i64, _f32, _f32, _vp]),

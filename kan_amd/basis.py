@@ -1,4 +1,4 @@
-"""Basis plug-in interface and the Chebyshev basis.
+"""Basis plug-in interface, the Chebyshev basis and the Jacobi / Hermite bases.
 
 Mirrors the reference's ``BasisFunction`` ABC (kan/basis/base.py:7-94) and
 ``ChebyshevBasis`` (kan/basis/chebyshev.py:8-172): same constructor, names,
@@ -7,14 +7,23 @@ registry name ``'chebyshev'`` (kan/basis/__init__.py:19-46).  The math runs
 in the HIP library; both the closed form (default) and the recurrence
 variant of the reference compute T_n(t), which this build evaluates with the
 three-term recurrence in fp32 registers.
+
+``JacobiBasis`` (kan/basis/jacobi.py:14-188) and ``HermiteBasis``
+(kan/basis/hermite.py:14-233) keep their reference constructors, names and
+registry names ``'jacobi'`` / ``'hermite'``.  Their ``forward`` runs the same
+HIP kernels: the library re-expresses the family's coefficients in the
+Chebyshev basis of the same tanh input (an exact change of basis) and maps
+the coefficient gradient back.
 """
 from __future__ import annotations
 
 from abc import ABC, abstractmethod
-from typing import Tuple
+import math
+from typing import Optional, Tuple
 
 import torch
 
+from . import _lib
 from . import functional as F
 
 
@@ -84,7 +93,100 @@ class ChebyshevBasis(BasisFunction):
         return F.chebyshev_basis(x, self.degree)
 
 
-BASIS_REGISTRY = {"chebyshev": ChebyshevBasis}
+class JacobiBasis(BasisFunction):
+    """Jacobi polynomials P_n^(alpha, beta)(tanh x), alpha, beta > -1."""
+
+    def __init__(self, degree: int, alpha: float = 0.0, beta: float = 0.0,
+                 domain: Tuple[float, float] = (-1, 1), compute: str = "fp32"):
+        super().__init__(degree)
+        if alpha <= -1 or beta <= -1:
+            raise ValueError(f"Parameters must satisfy α, β > -1, got α={alpha}, β={beta}")
+        self.alpha = alpha
+        self.beta = beta
+        self._domain = domain
+        F.compute_code(compute)
+        self.compute = compute
+        self.arange = torch.arange(0, degree + 1, dtype=torch.float32)
+
+    @property
+    def name(self) -> str:
+        return f"Jacobi-{self.degree}-{self.alpha}-{self.beta}"
+
+    @property
+    def domain(self) -> Tuple[float, float]:
+        return self._domain
+
+    def normalize_input(self, x: torch.Tensor) -> torch.Tensor:
+        return torch.tanh(x)
+
+    def spec(self) -> _lib.CkanBasisSpec:
+        return _lib.make_spec(_lib.CKAN_BASIS_JACOBI, self.degree, self.alpha, self.beta, 1.0)
+
+    def forward(self, x: torch.Tensor, coefficients: torch.Tensor) -> torch.Tensor:
+        x = x.view(-1, coefficients.shape[0])
+        return F.family_kan(x, coefficients, self.spec(), self.compute)
+
+    def basis_functions(self, x: torch.Tensor) -> torch.Tensor:
+        """P_0..P_degree of an already-normalised x (kan/basis/jacobi.py:119-188)."""
+        return F.family_basis(x, self.spec())
+
+
+class HermiteBasis(BasisFunction):
+    """Hermite polynomials, physicists' H_n or probabilists' He_n, of 3 tanh(x)."""
+
+    def __init__(self, degree: int, scaling: str = "physicist",
+                 domain: Optional[Tuple[float, float]] = None, normalize_domain: bool = True,
+                 compute: str = "fp32"):
+        super().__init__(degree)
+        if scaling not in ["physicist", "probabilist"]:
+            raise ValueError(f"Invalid scaling: {scaling}. "
+                             f"Must be one of ['physicist', 'probabilist']")
+        self.scaling = scaling
+        self._normalize_domain = normalize_domain
+        self._domain = domain or (-float("inf"), float("inf"))
+        F.compute_code(compute)
+        self.compute = compute
+        self.arange = torch.arange(0, degree + 1, dtype=torch.float32)
+
+    @property
+    def name(self) -> str:
+        return f"Hermite-{self.degree}-{self.scaling}"
+
+    @property
+    def domain(self) -> Tuple[float, float]:
+        return self._domain
+
+    def _affine_map(self) -> bool:
+        """True when the reference maps a finite domain linearly onto [-3, 3]
+        (kan/basis/hermite.py:102-112) instead of using 3 tanh(x)."""
+        lo, hi = self._domain
+        return bool(self._normalize_domain and math.isfinite(lo) and math.isfinite(hi))
+
+    def normalize_input(self, x: torch.Tensor) -> torch.Tensor:
+        if self._affine_map():
+            lo, hi = self._domain
+            return 6.0 / (hi - lo) * (x - lo) - 3.0
+        return torch.tanh(x) * 3.0
+
+    def spec(self) -> _lib.CkanBasisSpec:
+        fam = _lib.CKAN_BASIS_HERMITE if self.scaling == "physicist" else _lib.CKAN_BASIS_HERMITE_E
+        return _lib.make_spec(fam, self.degree, 0.0, 0.0, 3.0)
+
+    def forward(self, x: torch.Tensor, coefficients: torch.Tensor) -> torch.Tensor:
+        if self._affine_map():
+            raise RuntimeError(
+                "kan_amd HermiteBasis: a finite domain with normalize_domain=True maps inputs "
+                "linearly (no tanh); this build's HIP path implements the 3*tanh(x) input map "
+                "only. Pass domain=None or normalize_domain=False.")
+        x = x.view(-1, coefficients.shape[0])
+        return F.family_kan(x, coefficients, self.spec(), self.compute)
+
+    def basis_functions(self, x: torch.Tensor) -> torch.Tensor:
+        """H_0..H_degree (or He_n) of an already-normalised x (kan/basis/hermite.py:141-233)."""
+        return F.family_basis(x, self.spec())
+
+
+BASIS_REGISTRY = {"chebyshev": ChebyshevBasis, "jacobi": JacobiBasis, "hermite": HermiteBasis}
 
 
 def get_basis(name: str, **kwargs) -> BasisFunction:

@@ -267,6 +267,117 @@ int ckan_basis_backward(const float* t, const float* g, int64_t n, int32_t degre
   return check_launch("basis_backward");
 }
 
+namespace {
+// Validates a basis spec (and its degree against `degree` when >= 0) and
+// fills the family's recurrence.
+int family_of(const ckan_basis_spec* spec, int degree, double* a, double* b, double* c) {
+  if (!spec) return fail(CKAN_ERR_INVALID_ARG, "basis spec is NULL");
+  if (spec->degree < 0 || spec->degree >= kMaxD)
+    return fail(spec->degree < 0 ? CKAN_ERR_INVALID_ARG : CKAN_ERR_UNSUPPORTED,
+                "basis degree %d outside 0..%d", spec->degree, kMaxD - 1);
+  if (degree >= 0 && spec->degree != degree)
+    return fail(CKAN_ERR_INVALID_ARG, "basis degree %d != layer degree %d", spec->degree, degree);
+  if (!isfinite(spec->scale)) return fail(CKAN_ERR_INVALID_ARG, "basis scale must be finite");
+  if (!family_recurrence(spec->family, spec->degree, spec->alpha, spec->beta, a, b, c))
+    return fail(CKAN_ERR_INVALID_ARG, "invalid basis family %d or parameters (alpha=%g, beta=%g; "
+                "Jacobi needs alpha, beta > -1)", spec->family, spec->alpha, spec->beta);
+  return CKAN_OK;
+}
+
+int family_xform(const ckan_basis_spec* spec, int degree, BasisXform* xf) {
+  double a[kMaxD], b[kMaxD], c[kMaxD];
+  int rc = family_of(spec, degree, a, b, c);
+  if (rc) return rc;
+  const int D = spec->degree + 1;
+  double M[kMaxD * kMaxD];
+  family_to_chebyshev(a, b, c, spec->degree, spec->scale, M);
+  for (int i = 0; i < kMaxD * kMaxD; ++i) xf->m[i] = 0.0f;
+  for (int n = 0; n < D; ++n)
+    for (int k = 0; k < D; ++k) xf->m[n * kMaxD + k] = (float)M[n * D + k];
+  return CKAN_OK;
+}
+
+int family_recur(const ckan_basis_spec* spec, Recur3* r) {
+  double a[kMaxD], b[kMaxD], c[kMaxD];
+  int rc = family_of(spec, -1, a, b, c);
+  if (rc) return rc;
+  for (int n = 0; n < kMaxD; ++n) {
+    r->a[n] = (float)a[n];
+    r->b[n] = (float)b[n];
+    r->c[n] = (float)c[n];
+  }
+  return CKAN_OK;
+}
+}  // namespace
+
+int ckan_basis_to_chebyshev(const ckan_basis_spec* spec, double* M) {
+  double a[kMaxD], b[kMaxD], c[kMaxD];
+  int rc = family_of(spec, -1, a, b, c);
+  if (rc) return rc;
+  if (!M) return fail(CKAN_ERR_INVALID_ARG, "M is NULL");
+  family_to_chebyshev(a, b, c, spec->degree, spec->scale, M);
+  return CKAN_OK;
+}
+
+int ckan_pack_coeffs_basis(const ckan_desc* desc, const ckan_basis_spec* spec, const void* coeffs,
+                           void* packed, void* stream) {
+  int rc = validate_desc(desc);
+  if (rc) return rc;
+  BasisXform xf;
+  if ((rc = family_xform(spec, desc->degree, &xf))) return rc;
+  if (!coeffs || !packed) return fail(CKAN_ERR_INVALID_ARG, "coeffs/packed is NULL");
+  if (!aligned16(packed)) return fail(CKAN_ERR_INVALID_ARG, "packed buffer must be 16-byte aligned");
+  const Plan p = plan_of(desc);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  ProfScope ps("pack", s);
+  launch_pack(coeffs, desc->coeff_dtype == CKAN_DTYPE_BF16, packed, p, s, &xf);
+  return check_launch("pack_coeffs_basis");
+}
+
+int ckan_coeff_grad_from_chebyshev(const ckan_desc* desc, const ckan_basis_spec* spec,
+                                   const float* dcheb, float* dcoeffs, int accumulate, void* stream) {
+  int rc = validate_desc(desc);
+  if (rc) return rc;
+  BasisXform xf;
+  if ((rc = family_xform(spec, desc->degree, &xf))) return rc;
+  if (!dcheb || !dcoeffs) return fail(CKAN_ERR_INVALID_ARG, "dcheb/dcoeffs is NULL");
+  if (dcheb == dcoeffs && accumulate)
+    return fail(CKAN_ERR_INVALID_ARG, "in-place transform (dcheb == dcoeffs) cannot accumulate");
+  const Plan p = plan_of(desc);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  ProfScope ps("coeff_from_cheb", s);
+  launch_coeff_from_cheb(dcheb, dcoeffs, p, accumulate != 0, xf, s);
+  return check_launch("coeff_grad_from_chebyshev");
+}
+
+int ckan_family_basis(const ckan_basis_spec* spec, const float* t, int64_t n, float* out,
+                      void* stream) {
+  Recur3 r;
+  int rc = family_recur(spec, &r);
+  if (rc) return rc;
+  if (n < 0) return fail(CKAN_ERR_INVALID_ARG, "n must be >= 0");
+  if (n == 0) return CKAN_OK;
+  if (!t || !out) return fail(CKAN_ERR_INVALID_ARG, "t/out is NULL");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  ProfScope ps("basis", s);
+  launch_basis_family(t, n, spec->degree, r, out, s);
+  return check_launch("family_basis");
+}
+
+int ckan_family_basis_backward(const ckan_basis_spec* spec, const float* t, const float* g,
+                               int64_t n, float* dt, void* stream) {
+  Recur3 r;
+  int rc = family_recur(spec, &r);
+  if (rc) return rc;
+  if (n < 0) return fail(CKAN_ERR_INVALID_ARG, "n must be >= 0");
+  if (n == 0) return CKAN_OK;
+  if (!t || !g || !dt) return fail(CKAN_ERR_INVALID_ARG, "t/g/dt is NULL");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  ProfScope ps("basis_bwd", s);
+  launch_basis_family_bwd(t, g, n, spec->degree, r, dt, s);
+  return check_launch("family_basis_backward");
+}
+
 int ckan_sgd_step(float* p, const float* g, int64_t n, float lr, float weight_decay,
                   void* stream) {
   if (n < 0) return fail(CKAN_ERR_INVALID_ARG, "n must be >= 0");

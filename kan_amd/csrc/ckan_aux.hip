@@ -73,10 +73,17 @@ template <> __device__ __forceinline__ float to_f32<uint16_t>(uint16_t v) {
 // global read of C is one contiguous run of 32*D values per input.  The LDS
 // row pitch 32*D+1 is odd, so the column-wise reads of the Cb re-layout hit
 // 32 distinct banks.
-template <int P, bool BF, typename CT>
+// With XF, each (input, output) row of D coefficients is first replaced by
+// its Chebyshev-basis equivalent c'[k] = sum_n c[n] m[n][k] (another
+// polynomial family's coefficients re-expressed for these kernels).
+template <bool XF> struct XfArg { BasisXform x; };
+template <> struct XfArg<false> {};
+
+template <int P, bool BF, typename CT, bool XF>
 __global__ void __launch_bounds__(256)
 k_pack(const CT* __restrict__ C, typename Elem<BF>::type* __restrict__ Cf,
-       typename Elem<BF>::type* __restrict__ Cb, float* __restrict__ bias_part, Plan p, int cal) {
+       typename Elem<BF>::type* __restrict__ Cb, float* __restrict__ bias_part, Plan p, int cal,
+       XfArg<XF> xf) {
   using G = FwdGroup<P>;
   constexpr int RPMAX = 32 * (P + 1) + 1;
   __shared__ float tile[32 * RPMAX];
@@ -123,6 +130,23 @@ k_pack(const CT* __restrict__ C, typename Elem<BF>::type* __restrict__ Cf,
     }
   }
   __syncthreads();
+
+  if constexpr (XF) {
+    for (int row = tid; row < 32 * 32; row += 256) {
+      float* r = tile + (row >> 5) * RP + (row & 31) * D;
+      float v[P + 1];
+#pragma unroll
+      for (int n = 0; n <= P; ++n) v[n] = n < D ? r[n] : 0.0f;
+#pragma unroll
+      for (int k = 0; k <= P; ++k) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int n = k; n <= P; ++n) acc = fmaf(v[n], xf.x.m[n * kMaxD + k], acc);  // m[n][k] = 0 for k > n
+        if (k < D) r[k] = acc;
+      }
+    }
+    __syncthreads();
+  }
 
   {  // bias partial: 8 groups of 4 inputs, then a fixed-order sum
     const int ol = tid & 31, grp = tid >> 5;
@@ -436,8 +460,9 @@ void launch_tanh(const float* x, float* t, const Plan& p, hipStream_t s) {
                      (int)is_al16(x));
 }
 
-template <int P, bool BF>
-static void launch_pack_t(const void* C, bool c_bf16, void* packed, const Plan& p, hipStream_t s) {
+template <int P, bool BF, bool XF>
+static void launch_pack_t(const void* C, bool c_bf16, void* packed, const Plan& p, hipStream_t s,
+                          const XfArg<XF>& xf) {
   typedef typename Elem<BF>::type E;
   E* Cf = reinterpret_cast<E*>(packed);
   E* Cb = Cf + packed_cf_elems(p);
@@ -446,21 +471,34 @@ static void launch_pack_t(const void* C, bool c_bf16, void* packed, const Plan& 
                                          (p.NIB == 1 ? packed_biasf_offset(p) : packed_bias_offset(p)));
   dim3 grid(p.NIB, p.O64 / 32);
   if (c_bf16)
-    hipLaunchKernelGGL((k_pack<P, BF, uint16_t>), grid, dim3(256), 0, s,
-                       reinterpret_cast<const uint16_t*>(C), Cf, Cb, bias, p, 0);
+    hipLaunchKernelGGL((k_pack<P, BF, uint16_t, XF>), grid, dim3(256), 0, s,
+                       reinterpret_cast<const uint16_t*>(C), Cf, Cb, bias, p, 0, xf);
   else
-    hipLaunchKernelGGL((k_pack<P, BF, float>), grid, dim3(256), 0, s,
-                       reinterpret_cast<const float*>(C), Cf, Cb, bias, p, (int)is_al16(C));
+    hipLaunchKernelGGL((k_pack<P, BF, float, XF>), grid, dim3(256), 0, s,
+                       reinterpret_cast<const float*>(C), Cf, Cb, bias, p, (int)is_al16(C), xf);
 }
 
-void launch_pack(const void* C, bool c_bf16, void* packed, const Plan& p, hipStream_t s) {
+template <bool XF>
+static void launch_pack_x(const void* C, bool c_bf16, void* packed, const Plan& p, hipStream_t s,
+                          const XfArg<XF>& xf) {
   const bool bf = p.esz == 2;
-  char* base = reinterpret_cast<char*>(packed);
   switch (p.P) {
-    case 2: bf ? launch_pack_t<2, true>(C, c_bf16, packed, p, s) : launch_pack_t<2, false>(C, c_bf16, packed, p, s); break;
-    case 4: bf ? launch_pack_t<4, true>(C, c_bf16, packed, p, s) : launch_pack_t<4, false>(C, c_bf16, packed, p, s); break;
-    case 8: bf ? launch_pack_t<8, true>(C, c_bf16, packed, p, s) : launch_pack_t<8, false>(C, c_bf16, packed, p, s); break;
-    default: bf ? launch_pack_t<16, true>(C, c_bf16, packed, p, s) : launch_pack_t<16, false>(C, c_bf16, packed, p, s); break;
+    case 2: bf ? launch_pack_t<2, true>(C, c_bf16, packed, p, s, xf) : launch_pack_t<2, false>(C, c_bf16, packed, p, s, xf); break;
+    case 4: bf ? launch_pack_t<4, true>(C, c_bf16, packed, p, s, xf) : launch_pack_t<4, false>(C, c_bf16, packed, p, s, xf); break;
+    case 8: bf ? launch_pack_t<8, true>(C, c_bf16, packed, p, s, xf) : launch_pack_t<8, false>(C, c_bf16, packed, p, s, xf); break;
+    default: bf ? launch_pack_t<16, true>(C, c_bf16, packed, p, s, xf) : launch_pack_t<16, false>(C, c_bf16, packed, p, s, xf); break;
+  }
+}
+
+void launch_pack(const void* C, bool c_bf16, void* packed, const Plan& p, hipStream_t s,
+                 const BasisXform* xf) {
+  char* base = reinterpret_cast<char*>(packed);
+  if (xf) {
+    XfArg<true> a;
+    a.x = *xf;
+    launch_pack_x<true>(C, c_bf16, packed, p, s, a);
+  } else {
+    launch_pack_x<false>(C, c_bf16, packed, p, s, XfArg<false>{});
   }
   if (p.NIB > 1)  // bias = sum of the per-input-block partials, in block order
     hipLaunchKernelGGL(k_col_reduce, dim3((unsigned)ceil_div(p.O32, 64)), dim3(256), 0, s,

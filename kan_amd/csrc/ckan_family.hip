@@ -1,0 +1,194 @@
+// Other orthogonal-polynomial bases of the reference (Jacobi, Hermite) served
+// by the Chebyshev kernels.  A family P_0..P_deg evaluated at s * tanh(x) is a
+// polynomial of degree <= deg in u = tanh(x), so
+//   sum_n C[i, o, n] P_n(s u) = sum_k C'[i, o, k] T_k(u),   C' = C M,
+// with the lower-triangular change of basis P_n(s u) = sum_k M[n, k] T_k(u).
+// The forward and the input gradient are the ChebyKAN layer's with C'; the
+// coefficient gradient is dC = dC' M^T.  M is built here exactly (fp64) from
+// the family's three-term recurrence; this file also holds the kernels of
+// that transform and of the materialised family basis.
+#include "chebykan.h"
+#include "ckan_kernels.hpp"
+
+#include <math.h>
+
+#include <vector>
+
+namespace ckan {
+
+// Recurrences of kan/basis/jacobi.py:147-188 (P^(alpha,beta)_n, written as
+// (a_n t + b_n) P_{n-1} - c_n P_{n-2}), kan/basis/hermite.py:158-193
+// (physicists' H_n) and :195-233 (probabilists' He_n), and T_n itself.
+bool family_recurrence(int family, int degree, double alpha, double beta, double* a, double* b,
+                       double* c) {
+  if (degree < 0 || degree >= kMaxD) return false;
+  for (int n = 0; n < kMaxD; ++n) a[n] = b[n] = c[n] = 0.0;
+  switch (family) {
+    case CKAN_BASIS_CHEBYSHEV:
+      a[1] = 1.0;
+      for (int n = 2; n <= degree; ++n) { a[n] = 2.0; c[n] = 1.0; }
+      return true;
+    case CKAN_BASIS_JACOBI: {
+      if (!(alpha > -1.0) || !(beta > -1.0) || !isfinite(alpha) || !isfinite(beta)) return false;
+      const double ab = alpha + beta;
+      a[1] = (ab + 2.0) / 2.0;
+      b[1] = (alpha - beta) / 2.0;
+      for (int n = 2; n <= degree; ++n) {
+        const double ct = 2.0 * n + ab - 1.0;
+        const double den = 2.0 * n * (n + ab) * (2.0 * n + ab - 2.0);
+        a[n] = ct * (2.0 * n + ab) * (2.0 * n + ab - 2.0) / den;
+        b[n] = ct * (alpha * alpha - beta * beta) / den;
+        c[n] = 2.0 * (n + alpha - 1.0) * (n + beta - 1.0) * (2.0 * n + ab) / den;
+      }
+      return true;
+    }
+    case CKAN_BASIS_HERMITE:
+      a[1] = 2.0;
+      for (int n = 2; n <= degree; ++n) { a[n] = 2.0; c[n] = 2.0 * (n - 1); }
+      return true;
+    case CKAN_BASIS_HERMITE_E:
+      a[1] = 1.0;
+      for (int n = 2; n <= degree; ++n) { a[n] = 1.0; c[n] = (double)(n - 1); }
+      return true;
+    default:
+      return false;
+  }
+}
+
+// The recurrence run on Chebyshev coefficient vectors: multiplication by u is
+// u T_0 = T_1 and u T_k = (T_{k+1} + T_{k-1}) / 2 for k >= 1.
+void family_to_chebyshev(const double* a, const double* b, const double* c, int degree,
+                         double scale, double* M) {
+  const int D = degree + 1;
+  std::vector<double> v((size_t)D * D, 0.0);  // v[n * D + k]
+  auto mul_u = [&](const double* src, double* dst, int deg_src) {
+    for (int k = 0; k <= deg_src + 1 && k < D; ++k) dst[k] = 0.0;
+    for (int k = 0; k <= deg_src; ++k) {
+      if (src[k] == 0.0) continue;
+      if (k == 0) {
+        dst[1] += src[0];
+      } else {
+        dst[k + 1] += 0.5 * src[k];
+        dst[k - 1] += 0.5 * src[k];
+      }
+    }
+  };
+  v[0] = 1.0;
+  std::vector<double> uv(D + 1, 0.0);
+  for (int n = 1; n < D; ++n) {
+    const double* p1 = &v[(size_t)(n - 1) * D];
+    double* out = &v[(size_t)n * D];
+    mul_u(p1, uv.data(), n - 1);
+    for (int k = 0; k <= n; ++k) {
+      double x = a[n] * scale * uv[k] + b[n] * (k <= n - 1 ? p1[k] : 0.0);
+      if (n >= 2 && k <= n - 2) x -= c[n] * v[(size_t)(n - 2) * D + k];
+      out[k] = x;
+    }
+  }
+  for (int i = 0; i < D * D; ++i) M[i] = v[i];
+}
+
+// dc[q, n] (+)= sum_{k <= n} dcheb[q, k] m[n][k].  One thread per (i, o) row;
+// every load of a row precedes its stores, so dcheb may alias dc.
+template <int DM>
+__global__ void __launch_bounds__(256)
+k_coeff_from_cheb(const float* dcheb, float* dc, int64_t rows, int D, int accumulate,
+                  BasisXform xf) {
+  for (int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; q < rows;
+       q += (int64_t)gridDim.x * blockDim.x) {
+    const float* src = dcheb + q * D;
+    float g[DM];
+#pragma unroll
+    for (int k = 0; k < DM; ++k) g[k] = k < D ? src[k] : 0.0f;
+    float r[DM];
+#pragma unroll
+    for (int n = 0; n < DM; ++n) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int k = 0; k <= n; ++k) acc = fmaf(g[k], xf.m[n * kMaxD + k], acc);
+      r[n] = acc;
+    }
+    float* dst = dc + q * D;
+#pragma unroll
+    for (int n = 0; n < DM; ++n)
+      if (n < D) dst[n] = accumulate ? dst[n] + r[n] : r[n];
+  }
+}
+
+// out[q, n] = P_n(t[q]) by the family's recurrence, n = 0..deg.
+__global__ void __launch_bounds__(256)
+k_basis_family(const float* __restrict__ t, int64_t n, int deg, Recur3 r, float* __restrict__ out) {
+  for (int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; q < n;
+       q += (int64_t)gridDim.x * blockDim.x) {
+    const float tv = t[q];
+    float* o = out + q * (deg + 1);
+    o[0] = 1.0f;
+    if (deg < 1) continue;
+    float p0 = 1.0f, p1 = fmaf(r.a[1], tv, r.b[1]);
+    o[1] = p1;
+    for (int d = 2; d <= deg; ++d) {
+      const float pn = fmaf(fmaf(r.a[d], tv, r.b[d]), p1, -r.c[d] * p0);
+      o[d] = pn;
+      p0 = p1;
+      p1 = pn;
+    }
+  }
+}
+
+// dt[q] = sum_n g[q, n] P_n'(t[q]), with the differentiated recurrence
+// P_n' = a_n P_{n-1} + (a_n t + b_n) P_{n-1}' - c_n P_{n-2}'.
+__global__ void __launch_bounds__(256)
+k_basis_family_bwd(const float* __restrict__ t, const float* __restrict__ g, int64_t n, int deg,
+                   Recur3 r, float* __restrict__ dt) {
+  for (int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; q < n;
+       q += (int64_t)gridDim.x * blockDim.x) {
+    const float tv = t[q];
+    const float* gq = g + q * (deg + 1);
+    float s = 0.0f;
+    if (deg >= 1) {
+      float p0 = 1.0f, p1 = fmaf(r.a[1], tv, r.b[1]);  // P_{n-2}, P_{n-1}
+      float d0 = 0.0f, d1 = r.a[1];                     // their derivatives
+      s = gq[1] * d1;
+      for (int d = 2; d <= deg; ++d) {
+        const float lin = fmaf(r.a[d], tv, r.b[d]);
+        const float pn = fmaf(lin, p1, -r.c[d] * p0);
+        const float dn = fmaf(r.a[d], p1, fmaf(lin, d1, -r.c[d] * d0));
+        s = fmaf(gq[d], dn, s);
+        p0 = p1; p1 = pn;
+        d0 = d1; d1 = dn;
+      }
+    }
+    dt[q] = s;
+  }
+}
+
+static unsigned grid_of(int64_t work) {
+  int64_t g = (work + 255) / 256;
+  if (g > 65536) g = 65536;
+  if (g < 1) g = 1;
+  return (unsigned)g;
+}
+
+void launch_coeff_from_cheb(const float* dcheb, float* dc, const Plan& p, bool accumulate,
+                            const BasisXform& xf, hipStream_t s) {
+  const int64_t rows = (int64_t)p.I * p.O;
+  const dim3 g(grid_of(rows));
+  switch (p.P) {
+    case 2: hipLaunchKernelGGL((k_coeff_from_cheb<3>), g, dim3(256), 0, s, dcheb, dc, rows, p.D, (int)accumulate, xf); break;
+    case 4: hipLaunchKernelGGL((k_coeff_from_cheb<5>), g, dim3(256), 0, s, dcheb, dc, rows, p.D, (int)accumulate, xf); break;
+    case 8: hipLaunchKernelGGL((k_coeff_from_cheb<9>), g, dim3(256), 0, s, dcheb, dc, rows, p.D, (int)accumulate, xf); break;
+    default: hipLaunchKernelGGL((k_coeff_from_cheb<17>), g, dim3(256), 0, s, dcheb, dc, rows, p.D, (int)accumulate, xf); break;
+  }
+}
+
+void launch_basis_family(const float* t, int64_t n, int deg, const Recur3& r, float* out,
+                         hipStream_t s) {
+  hipLaunchKernelGGL(k_basis_family, dim3(grid_of(n)), dim3(256), 0, s, t, n, deg, r, out);
+}
+
+void launch_basis_family_bwd(const float* t, const float* g, int64_t n, int deg, const Recur3& r,
+                             float* dt, hipStream_t s) {
+  hipLaunchKernelGGL(k_basis_family_bwd, dim3(grid_of(n)), dim3(256), 0, s, t, g, n, deg, r, dt);
+}
+
+}  // namespace ckan

@@ -58,9 +58,33 @@ struct BwdLayout {
 };
 BwdLayout bwd_layout(const Plan& p, bool need_dx, bool need_dc);
 
+// ---- other polynomial bases expressed in the Chebyshev basis --------------
+constexpr int kMaxD = 17;  // degree <= 16
+// Three-term recurrence: P_0 = 1, P_1 = a[1] t + b[1],
+// P_n = (a[n] t + b[n]) P_{n-1} - c[n] P_{n-2}  (n >= 2).
+struct Recur3 { float a[kMaxD], b[kMaxD], c[kMaxD]; };
+// Change of basis P_n(s u) = sum_k m[n * kMaxD + k] T_k(u), zero-padded.
+struct BasisXform { float m[kMaxD * kMaxD]; };
+// Recurrence coefficients (double) of a ckan_basis_family; false if the
+// family or its parameters are invalid.
+bool family_recurrence(int family, int degree, double alpha, double beta, double* a, double* b,
+                       double* c);
+// M[n * (degree + 1) + k] with P_n(scale u) = sum_k M[n, k] T_k(u) (exact, fp64).
+void family_to_chebyshev(const double* a, const double* b, const double* c, int degree,
+                         double scale, double* M);
+// dc[q, n] (+)= sum_k dcheb[q, k] m[n][k] over the I*O rows q; dcheb may be dc.
+void launch_coeff_from_cheb(const float* dcheb, float* dc, const Plan& p, bool accumulate,
+                            const BasisXform& xf, hipStream_t s);
+void launch_basis_family(const float* t, int64_t n, int deg, const Recur3& r, float* out,
+                         hipStream_t s);
+void launch_basis_family_bwd(const float* t, const float* g, int64_t n, int deg, const Recur3& r,
+                             float* dt, hipStream_t s);
+
 // ---- launchers -------------------------------------------------------------
 void launch_tanh(const float* x, float* t, const Plan& p, hipStream_t s);
-void launch_pack(const void* C, bool c_bf16, void* packed, const Plan& p, hipStream_t s);
+// xf (optional, host struct passed by value to the kernel): pack C xf instead of C
+void launch_pack(const void* C, bool c_bf16, void* packed, const Plan& p, hipStream_t s,
+                 const BasisXform* xf = nullptr);
 void launch_prep_dy(const float* dy, void* dYx, void* dYc, float* colsum_part, const Plan& p,
                     bool need_dx, bool need_dc, hipStream_t s);
 // reduces the dy column-sum partials into row NBB and returns that row

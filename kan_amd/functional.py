@@ -54,10 +54,16 @@ def coeff_code(dtype: torch.dtype) -> int:
 
 
 class ChebyKANFunction(torch.autograd.Function):
-    """y = einsum('bid,iod->bo', T(tanh x), C) with hand-written HIP backward."""
+    """y = einsum('bid,iod->bo', T(tanh x), C) with hand-written HIP backward.
+
+    With a basis ``spec`` (``_lib.CkanBasisSpec``), C holds the coefficients
+    of that family P_n(s tanh x) instead: the library packs C M (the same
+    function in the Chebyshev basis) and maps the coefficient gradient back
+    through M^T.
+    """
 
     @staticmethod
-    def forward(ctx, x: torch.Tensor, coeffs: torch.Tensor, compute: str = "fp32"):
+    def forward(ctx, x: torch.Tensor, coeffs: torch.Tensor, compute: str = "fp32", spec=None):
         _require_device(x, coeffs)
         if coeffs.dim() != 3:
             raise RuntimeError(f"coefficients must be [in, out, degree+1], got {tuple(coeffs.shape)}")
@@ -72,7 +78,10 @@ class ChebyKANFunction(torch.autograd.Function):
                               coeff_code(c.dtype))
         stream = _lib.stream_ptr(dev)
         packed = torch.empty(lib.ckan_packed_bytes(desc), dtype=torch.uint8, device=dev)
-        _lib.check(lib.ckan_pack_coeffs(desc, c.data_ptr(), packed.data_ptr(), stream))
+        if spec is None:
+            _lib.check(lib.ckan_pack_coeffs(desc, c.data_ptr(), packed.data_ptr(), stream))
+        else:
+            _lib.check(lib.ckan_pack_coeffs_basis(desc, spec, c.data_ptr(), packed.data_ptr(), stream))
         t = torch.empty(lib.ckan_tcache_elems(desc), dtype=torch.float32, device=dev)
         y = torch.empty(x32.shape[0], out_dim, dtype=torch.float32, device=dev)
         ws_bytes = lib.ckan_fwd_workspace_bytes(desc)
@@ -81,6 +90,7 @@ class ChebyKANFunction(torch.autograd.Function):
                                     t.data_ptr(), _lib.ptr(ws), ws_bytes, stream))
         ctx.save_for_backward(t, packed)
         ctx.desc = desc
+        ctx.spec = spec
         ctx.x_dtype = x.dtype
         ctx.c_dtype = coeffs.dtype
         return y
@@ -91,7 +101,7 @@ class ChebyKANFunction(torch.autograd.Function):
         desc = ctx.desc
         need_dx, need_dc = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
         if not (need_dx or need_dc):
-            return None, None, None
+            return None, None, None, None
         lib = _lib.load()
         dev = dy.device
         dy32 = dy.contiguous() if dy.dtype == torch.float32 else dy.float().contiguous()
@@ -100,14 +110,18 @@ class ChebyKANFunction(torch.autograd.Function):
               if need_dc else None)
         ws_bytes = lib.ckan_bwd_workspace_bytes(desc, int(need_dx), int(need_dc))
         ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
+        stream = _lib.stream_ptr(dev)
         _lib.check(lib.ckan_backward(desc, t.data_ptr(), packed.data_ptr(), dy32.data_ptr(),
                                      _lib.ptr(dx), _lib.ptr(dc), 0, ws.data_ptr(), ws_bytes,
-                                     _lib.stream_ptr(dev)))
+                                     stream))
+        if dc is not None and ctx.spec is not None:  # dC = dC' M^T, in place
+            _lib.check(lib.ckan_coeff_grad_from_chebyshev(desc, ctx.spec, dc.data_ptr(),
+                                                          dc.data_ptr(), 0, stream))
         if dx is not None and ctx.x_dtype != torch.float32:
             dx = dx.to(ctx.x_dtype)
         if dc is not None and ctx.c_dtype != torch.float32:
             dc = dc.to(ctx.c_dtype)
-        return dx, dc, None
+        return dx, dc, None, None
 
 
 class ChebyshevBasisFunction(torch.autograd.Function):
@@ -140,9 +154,48 @@ class ChebyshevBasisFunction(torch.autograd.Function):
         return dt.to(ctx.t_dtype), None
 
 
+class FamilyBasisFunction(torch.autograd.Function):
+    """P_n(t) for n = 0..degree of a recurrence family, materialised (fp32)."""
+
+    @staticmethod
+    def forward(ctx, t: torch.Tensor, spec):
+        _require_device(t)
+        lib = _lib.load()
+        t32 = t.contiguous() if t.dtype == torch.float32 else t.float().contiguous()
+        out = torch.empty(*t32.shape, spec.degree + 1, dtype=torch.float32, device=t.device)
+        _lib.check(lib.ckan_family_basis(spec, t32.data_ptr(), t32.numel(), out.data_ptr(),
+                                         _lib.stream_ptr(t.device)))
+        ctx.save_for_backward(t32)
+        ctx.spec = spec
+        ctx.t_dtype = t.dtype
+        return out
+
+    @staticmethod
+    def backward(ctx, g: torch.Tensor):
+        (t32,) = ctx.saved_tensors
+        if not ctx.needs_input_grad[0]:
+            return None, None
+        lib = _lib.load()
+        g32 = g.contiguous() if g.dtype == torch.float32 else g.float().contiguous()
+        dt = torch.empty_like(t32)
+        _lib.check(lib.ckan_family_basis_backward(ctx.spec, t32.data_ptr(), g32.data_ptr(),
+                                                  t32.numel(), dt.data_ptr(),
+                                                  _lib.stream_ptr(t32.device)))
+        return dt.to(ctx.t_dtype), None
+
+
 def chebykan(x: torch.Tensor, coeffs: torch.Tensor, compute: str = "fp32") -> torch.Tensor:
     """Functional ChebyKAN layer: x [B, in], coeffs [in, out, D] -> y [B, out]."""
-    return ChebyKANFunction.apply(x, coeffs, compute)
+    return ChebyKANFunction.apply(x, coeffs, compute, None)
+
+
+def family_kan(x: torch.Tensor, coeffs: torch.Tensor, spec, compute: str = "fp32") -> torch.Tensor:
+    """y = einsum('bid,iod->bo', P(s tanh x), C) for the family of ``spec``."""
+    return ChebyKANFunction.apply(x, coeffs, compute, spec)
+
+
+def family_basis(t: torch.Tensor, spec) -> torch.Tensor:
+    return FamilyBasisFunction.apply(t, spec)
 
 
 def chebyshev_basis(t: torch.Tensor, degree: int) -> torch.Tensor:

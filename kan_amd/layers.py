@@ -9,16 +9,21 @@ construction yields bit-identical coefficients and ``state_dict`` keys.
 ``forward`` does ``x.view(-1, in)`` (chebykan.py:64) and runs the HIP path.
 The extra keyword ``compute`` ('fp32' default, or 'bf16') selects the MFMA
 precision.
+
+``JacobiKANLayer`` (kan/layers/jacobikan.py:10-120) and ``HermiteKANLayer``
+(kan/layers/hermitekan.py:10-125) mirror their reference constructors and
+parameters (``jacobi_coeffs`` / ``hermite_coeffs``, same init order) and run
+on the same kernels through the change of basis in ``kan_amd.basis``.
 """
 from __future__ import annotations
 
 from abc import ABC, abstractmethod
-from typing import Any, Dict, List, Optional
+from typing import Any, Dict, List, Optional, Tuple
 
 import torch
 import torch.nn as nn
 
-from .basis import BasisFunction, ChebyshevBasis
+from .basis import BasisFunction, ChebyshevBasis, HermiteBasis, JacobiBasis
 
 
 class KANLayer(nn.Module, ABC):
@@ -91,6 +96,104 @@ class ChebyKANLayer(KANLayer):
         return f"input_dim={self.input_dim}, output_dim={self.output_dim}, degree={self.degree}"
 
 
+class _ComputeMixin:
+    @property
+    def compute(self) -> str:
+        return self.basis_function.compute
+
+    @compute.setter
+    def compute(self, value: str) -> None:
+        from .functional import compute_code
+        compute_code(value)
+        self.basis_function.compute = value
+
+
+class JacobiKANLayer(_ComputeMixin, KANLayer):
+    """KAN layer with a tanh-squashed Jacobi basis (kan/layers/jacobikan.py:10-120)."""
+
+    def __init__(self, input_dim: int, output_dim: int, degree: int, alpha: float = 0.0,
+                 beta: float = 0.0, init_scale: Optional[float] = None, compute: str = "fp32"):
+        if alpha <= -1 or beta <= -1:
+            raise ValueError(f"Parameters must satisfy α, β > -1, got α={alpha}, β={beta}")
+        basis_function = JacobiBasis(degree=degree, alpha=alpha, beta=beta, compute=compute)
+        super().__init__(input_dim=input_dim, output_dim=output_dim,
+                         basis_function=basis_function)
+        self.degree = degree
+        self.alpha = alpha
+        self.beta = beta
+        init_scale = init_scale or 1.0 / (input_dim * (degree + 1))
+        self.jacobi_coeffs = nn.Parameter(torch.empty(input_dim, output_dim, degree + 1))
+        nn.init.normal_(self.jacobi_coeffs, mean=0.0, std=init_scale)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        x = x.view(-1, self.input_dim)
+        return self.basis_function.forward(x, self.jacobi_coeffs)
+
+    def get_analytical_form(self) -> Dict[str, Any]:
+        return {
+            "type": "JacobiKANLayer",
+            "input_dim": self.input_dim,
+            "output_dim": self.output_dim,
+            "degree": self.degree,
+            "alpha": self.alpha,
+            "beta": self.beta,
+            "basis": self.basis_function.name,
+            "coefficients": self.jacobi_coeffs.detach().cpu().numpy(),
+        }
+
+    def get_coefficients(self) -> torch.Tensor:
+        return self.jacobi_coeffs
+
+    def extra_repr(self) -> str:
+        return (f"input_dim={self.input_dim}, output_dim={self.output_dim}, degree={self.degree}, "
+                f"alpha={self.alpha}, beta={self.beta}")
+
+
+class HermiteKANLayer(_ComputeMixin, KANLayer):
+    """KAN layer with a Hermite basis of 3 tanh(x) (kan/layers/hermitekan.py:10-125)."""
+
+    def __init__(self, input_dim: int, output_dim: int, degree: int, scaling: str = "physicist",
+                 domain: Optional[Tuple[float, float]] = None, normalize_domain: bool = True,
+                 init_scale: Optional[float] = None, compute: str = "fp32"):
+        basis_function = HermiteBasis(degree=degree, scaling=scaling, domain=domain,
+                                      normalize_domain=normalize_domain, compute=compute)
+        super().__init__(input_dim=input_dim, output_dim=output_dim,
+                         basis_function=basis_function)
+        self.degree = degree
+        self.scaling = scaling
+        self.domain = domain
+        self.normalize_domain = normalize_domain
+        init_scale = init_scale or 1.0 / (input_dim * (degree + 1))
+        self.hermite_coeffs = nn.Parameter(torch.empty(input_dim, output_dim, degree + 1))
+        nn.init.normal_(self.hermite_coeffs, mean=0.0, std=init_scale)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        x = x.view(-1, self.input_dim)
+        return self.basis_function.forward(x, self.hermite_coeffs)
+
+    def get_analytical_form(self) -> Dict[str, Any]:
+        return {
+            "type": "HermiteKANLayer",
+            "input_dim": self.input_dim,
+            "output_dim": self.output_dim,
+            "degree": self.degree,
+            "scaling": self.scaling,
+            "domain": self.domain,
+            "normalize_domain": self.normalize_domain,
+            "basis": self.basis_function.name,
+            "coefficients": self.hermite_coeffs.detach().cpu().numpy(),
+        }
+
+    def get_coefficients(self) -> torch.Tensor:
+        return self.hermite_coeffs
+
+    def extra_repr(self) -> str:
+        domain_str = f", domain={self.domain}" if self.domain else ""
+        normalize_str = f", normalize_domain={self.normalize_domain}"
+        return (f"input_dim={self.input_dim}, output_dim={self.output_dim}, "
+                f"degree={self.degree}, scaling={self.scaling}{domain_str}{normalize_str}")
+
+
 class KANSequential(nn.Sequential):
     """Sequential container of KAN layers (kan/layers/base.py:144-166)."""
 
@@ -98,7 +201,8 @@ class KANSequential(nn.Sequential):
         return [m.get_analytical_form() for m in self if isinstance(m, KANLayer)]
 
 
-LAYER_REGISTRY = {"chebykan": ChebyKANLayer}
+LAYER_REGISTRY = {"chebykan": ChebyKANLayer, "jacobikan": JacobiKANLayer,
+                  "hermitekan": HermiteKANLayer}
 
 
 def get_layer(name: str, **kwargs) -> KANLayer:

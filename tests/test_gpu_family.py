@@ -1,0 +1,134 @@
+"""GPU parity of the Jacobi / Hermite layers (HIP path through the C-ABI)
+against the CPU oracle oracle/family_oracle.py.
+
+Tolerances (norm-wise, ||a - b|| / ||b||), as for the Chebyshev layer:
+  fp32 MFMA path:  1e-5 for y, dx and dC
+  bf16 MFMA path:  2e-2
+"""
+import ctypes
+
+import pytest
+import torch
+
+from kan_amd import _lib
+from oracle import family_oracle as fo
+
+pytestmark = pytest.mark.gpu
+
+FP32_TOL = 1e-5
+BF16_TOL = 2e-2
+
+
+def _rel(a, b):
+    a = a.detach().double().cpu()
+    b = b.detach().double().cpu()
+    n = b.norm().item()
+    return (a - b).norm().item() / (n if n > 0 else 1.0)
+
+
+def _spec(family, deg, alpha=0.0, beta=0.0):
+    if family == "jacobi":
+        return _lib.make_spec(_lib.CKAN_BASIS_JACOBI, deg, alpha, beta, 1.0)
+    fam = _lib.CKAN_BASIS_HERMITE if family == "hermite" else _lib.CKAN_BASIS_HERMITE_E
+    return _lib.make_spec(fam, deg, 0.0, 0.0, 3.0)
+
+
+CASES = [
+    # family, alpha, beta, B, I, O, deg
+    ("jacobi", 0.0, 0.0, 256, 64, 48, 8),
+    ("jacobi", 1.5, 0.5, 300, 40, 70, 3),
+    ("jacobi", -0.5, 0.25, 2048, 256, 128, 8),   # pipelined forward (B > 512)
+    ("jacobi", 2.0, 3.0, 16, 512, 96, 5),        # coefficient-streaming forward (B <= 64)
+    ("hermite", 0, 0, 129, 64, 96, 16),
+    ("hermite", 0, 0, 7, 5, 3, 1),
+    ("hermite_e", 0, 0, 200, 72, 50, 12),
+    ("hermite_e", 0, 0, 1024, 128, 256, 4),
+]
+
+
+@pytest.mark.parametrize("compute,tol", [("fp32", FP32_TOL), ("bf16", BF16_TOL)])
+@pytest.mark.parametrize("family,alpha,beta,B,I,O,deg", CASES)
+def test_family_layer_forward_backward_parity(family, alpha, beta, B, I, O, deg, compute, tol):
+    from kan_amd import functional as F
+    print(f"{family}({alpha},{beta}) {compute} B={B} I={I} O={O} deg={deg}", flush=True)
+    g = torch.Generator().manual_seed(B + I + deg)
+    x = torch.randn(B, I, generator=g) * 1.5
+    c = torch.randn(I, O, deg + 1, generator=g) / (I * (deg + 1))
+    dy = torch.randn(B, O, generator=g)
+    y_ref, dx_ref, dc_ref = fo.family_forward_backward(x, c, dy, family, alpha, beta)
+    xd = x.cuda().requires_grad_(True)
+    cd = c.cuda().requires_grad_(True)
+    y = F.family_kan(xd, cd, _spec(family, deg, alpha, beta), compute)
+    y.backward(dy.cuda())
+    torch.cuda.synchronize()
+    assert _rel(y, y_ref) <= tol
+    assert _rel(xd.grad, dx_ref) <= tol
+    assert _rel(cd.grad, dc_ref) <= tol
+
+
+def test_family_layers_through_module_api():
+    import kan_amd
+    torch.manual_seed(0)
+    jl = kan_amd.JacobiKANLayer(64, 32, 6, alpha=0.5, beta=-0.25).cuda()
+    hl = kan_amd.HermiteKANLayer(32, 10, 5, scaling="physicist").cuda()
+    model = kan_amd.KANSequential(jl, hl)
+    x = torch.randn(96, 64)
+    y = model(x.cuda())
+    y.sum().backward()
+    torch.cuda.synchronize()
+    cj = jl.jacobi_coeffs.detach().cpu().requires_grad_(True)
+    ch = hl.hermite_coeffs.detach().cpu().requires_grad_(True)
+    h1 = fo.family_forward(x, cj, "jacobi", 0.5, -0.25)
+    y_ref = fo.family_forward(h1, ch, "hermite")
+    y_ref.sum().backward()
+    assert _rel(y, y_ref) <= FP32_TOL
+    assert _rel(jl.jacobi_coeffs.grad, cj.grad) <= FP32_TOL
+    assert _rel(hl.hermite_coeffs.grad, ch.grad) <= FP32_TOL
+    # a second backward accumulates into .grad
+    g1 = jl.jacobi_coeffs.grad.clone()
+    model(x.cuda()).sum().backward()
+    torch.cuda.synchronize()
+    assert _rel(jl.jacobi_coeffs.grad, 2 * g1) <= FP32_TOL
+
+
+@pytest.mark.parametrize("family,alpha,beta", [("jacobi", 1.0, 0.5), ("hermite", 0, 0),
+                                               ("hermite_e", 0, 0)])
+def test_family_basis_functions_and_backward(family, alpha, beta):
+    from kan_amd import functional as F
+    deg = 9
+    s = 1.0 if family == "jacobi" else 3.0
+    t = (torch.rand(300, 7, generator=torch.Generator().manual_seed(1)) * 2 - 1) * s
+    g = torch.randn(300, 7, deg + 1, generator=torch.Generator().manual_seed(2))
+    tr = t.clone().double().requires_grad_(True)
+    ref = fo.family_basis(tr, family, deg, alpha, beta)
+    (ref * g.double()).sum().backward()
+    td = t.cuda().requires_grad_(True)
+    out = F.family_basis(td, _spec(family, deg, alpha, beta))
+    (out * g.cuda()).sum().backward()
+    torch.cuda.synchronize()
+    assert _rel(out, ref) <= FP32_TOL
+    assert _rel(td.grad, tr.grad) <= FP32_TOL
+
+
+def test_coeff_grad_transform_accumulates():
+    """dC (+)= dC' M^T through the C-ABI, against the same product on the CPU."""
+    import numpy as np
+    lib = _lib.load()
+    I, O, deg = 37, 19, 7
+    spec = _spec("hermite", deg)
+    M = (ctypes.c_double * ((deg + 1) ** 2))()
+    assert lib.ckan_basis_to_chebyshev(spec, M) == 0
+    Mn = torch.tensor(np.array(M[:]).reshape(deg + 1, deg + 1))
+    g = torch.Generator().manual_seed(4)
+    dcheb = torch.randn(I, O, deg + 1, generator=g)
+    base = torch.randn(I, O, deg + 1, generator=g)
+    d = _lib.make_desc(1, I, O, deg, 0, 0)
+    out = base.cuda()
+    st = _lib.stream_ptr(out.device)
+    _lib.check(lib.ckan_coeff_grad_from_chebyshev(d, spec, dcheb.cuda().data_ptr(), out.data_ptr(), 1, st))
+    expect = base.double() + torch.einsum("iok,nk->ion", dcheb.double(), Mn)
+    assert _rel(out, expect) <= FP32_TOL
+    inplace = dcheb.cuda()
+    _lib.check(lib.ckan_coeff_grad_from_chebyshev(d, spec, inplace.data_ptr(), inplace.data_ptr(), 0, st))
+    torch.cuda.synchronize()
+    assert _rel(inplace, torch.einsum("iok,nk->ion", dcheb.double(), Mn)) <= FP32_TOL
