@@ -38,7 +38,7 @@ STEP_FLOP = 3.0 * GEMM_FLOP          # x requires grad: fwd + dX + dC
 
 
 def _step(layer, x, dy):
-    layer.cheby_coeffs.grad = None
+    layer.get_coefficients().grad = None
     x.grad = None
     y = layer(x)
     y.backward(dy)
@@ -89,8 +89,11 @@ def _time_loop(fn, iters, warmup):
     return e0.elapsed_time(e1) / iters
 
 
-def _suite():
-    """Secondary BASELINE configs (1, 2, 4, 5); each takes well under a minute."""
+SUITE = ("cfg1", "cfg2", "cfg4", "cfg5", "families")
+
+
+def _suite(only=SUITE):
+    """Secondary BASELINE configs (1, 2, 4, 5) and the other bases; each takes well under a minute."""
     import ctypes
     import math
     import torch
@@ -99,94 +102,121 @@ def _suite():
     dev = torch.device("cuda:0")
     out = {}
 
-    # config 1: ChebyKANLayer(1,1,8), 100 points, MSE + Adam lr 0.01, 1000 steps (README.md:42-73)
-    torch.manual_seed(0)
-    m = kan_amd.ChebyKANLayer(1, 1, 8)
-    x1 = torch.linspace(-1, 1, 100).reshape(-1, 1).to(dev)
-    y1 = torch.sin(2 * math.pi * x1)
-    res1 = {}
-    for graph in (False, True):
-        ex = kan_amd.ResidentExecutor([1, 1], [8], 100, compute="fp32", loss="mse",
-                                      optimizer="adam", lr=0.01, use_graph=graph)
-        ex.set_coeffs(0, m.cheby_coeffs.detach())
-        ms = _time_loop(lambda: ex.step(x1, y1), 1000, 0)
-        res1["graph" if graph else "eager"] = (ms, float(ex.step(x1, y1).item()))
+    if "cfg1" in only:
+        # config 1: ChebyKANLayer(1,1,8), 100 points, MSE + Adam lr 0.01, 1000 steps (README.md:42-73)
+        torch.manual_seed(0)
+        m = kan_amd.ChebyKANLayer(1, 1, 8)
+        x1 = torch.linspace(-1, 1, 100).reshape(-1, 1).to(dev)
+        y1 = torch.sin(2 * math.pi * x1)
+        res1 = {}
+        for graph in (False, True):
+            ex = kan_amd.ResidentExecutor([1, 1], [8], 100, compute="fp32", loss="mse",
+                                          optimizer="adam", lr=0.01, use_graph=graph)
+            ex.set_coeffs(0, m.cheby_coeffs.detach())
+            ms = _time_loop(lambda: ex.step(x1, y1), 1000, 0)
+            res1["graph" if graph else "eager"] = (ms, float(ex.step(x1, y1).item()))
+            ex.close()
+        out["cfg1"] = {"workload": "ChebyKANLayer(1,1,8) sin(2 pi x), 100 pts, MSE+Adam, resident, eager launches",
+                       "us_per_step": res1["eager"][0] * 1e3, "steps": 1000,
+                       "final_loss": res1["eager"][1],
+                       "us_per_step_hip_graph": res1["graph"][0] * 1e3}
+
+    if "cfg2" in only:
+        # config 2: 784->64->10, deg 4, fp32, B=256, CE + SGD lr 0.01
+        g = torch.Generator().manual_seed(2)
+        x2 = (torch.rand(256, 784, generator=g) * (torch.rand(256, 784, generator=g) >= 0.8).float()).to(dev)
+        l2 = torch.randint(0, 10, (256,), generator=g).to(dev)
+        torch.manual_seed(2)
+        seq = kan_amd.KANSequential(kan_amd.ChebyKANLayer(784, 64, 4), kan_amd.ChebyKANLayer(64, 10, 4))
+        res2 = {}
+        for graph in (False, True):
+            ex = kan_amd.ResidentExecutor.from_sequential(seq, 256, compute="fp32", loss="ce",
+                                                          optimizer="sgd", lr=0.01, use_graph=graph)
+            res2["graph" if graph else "eager"] = _time_loop(lambda: ex.step(x2, l2), 200, 20)
+            ex.close()
+        ms = res2["eager"]
+        out["cfg2"] = {"workload": "784->64->10 deg 4 fp32 B=256, CE+SGD, resident, eager launches",
+                       "us_per_step": ms * 1e3, "samples_per_s": 256 / (ms * 1e-3),
+                       "tflops": 2.618e8 / (ms * 1e-3) / 1e12,
+                       "us_per_step_hip_graph": res2["graph"] * 1e3}
+
+    if "cfg4" in only:
+        # config 4: 512->512->512->512->64, deg 16, B=65536, fp32 masters + bf16 compute, MSE + SGD, 100 steps
+        g = torch.Generator().manual_seed(4)
+        x4 = (torch.rand(65536, 512, generator=g) * 6 - 3).to(dev)
+        W = (torch.randn(512, 64, generator=g) / math.sqrt(512)).to(dev)
+        t4 = x4 @ W + 0.1 * torch.randn(65536, 64, generator=g).to(dev)
+        torch.manual_seed(4)
+        seq = kan_amd.KANSequential(*[kan_amd.ChebyKANLayer(a, b, 16)
+                                      for a, b in [(512, 512), (512, 512), (512, 512), (512, 64)]])
+        ex = kan_amd.ResidentExecutor.from_sequential(seq, 65536, compute="bf16", loss="mse",
+                                                      optimizer="sgd", lr=0.01)
+        ms = _time_loop(lambda: ex.step(x4, t4), 100, 3)
+        out["cfg4"] = {"workload": "512->512->512->512->64 deg 16 B=65536 bf16 MFMA, fp32 masters, MSE+SGD, resident",
+                       "ms_per_step": ms, "samples_per_s": 65536 / (ms * 1e-3),
+                       "tflops": 4.8920e12 / (ms * 1e-3) / 1e12,
+                       "frac_bf16_peak": 4.8920e12 / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
+                       "final_loss": float(ex.step(x4, t4).item())}
         ex.close()
-    out["cfg1"] = {"workload": "ChebyKANLayer(1,1,8) sin(2 pi x), 100 pts, MSE+Adam, resident, eager launches",
-                   "us_per_step": res1["eager"][0] * 1e3, "steps": 1000,
-                   "final_loss": res1["eager"][1],
-                   "us_per_step_hip_graph": res1["graph"][0] * 1e3}
 
-    # config 2: 784->64->10, deg 4, fp32, B=256, CE + SGD lr 0.01
-    g = torch.Generator().manual_seed(2)
-    x2 = (torch.rand(256, 784, generator=g) * (torch.rand(256, 784, generator=g) >= 0.8).float()).to(dev)
-    l2 = torch.randint(0, 10, (256,), generator=g).to(dev)
-    torch.manual_seed(2)
-    seq = kan_amd.KANSequential(kan_amd.ChebyKANLayer(784, 64, 4), kan_amd.ChebyKANLayer(64, 10, 4))
-    res2 = {}
-    for graph in (False, True):
-        ex = kan_amd.ResidentExecutor.from_sequential(seq, 256, compute="fp32", loss="ce",
-                                                      optimizer="sgd", lr=0.01, use_graph=graph)
-        res2["graph" if graph else "eager"] = _time_loop(lambda: ex.step(x2, l2), 200, 20)
-        ex.close()
-    ms = res2["eager"]
-    out["cfg2"] = {"workload": "784->64->10 deg 4 fp32 B=256, CE+SGD, resident, eager launches",
-                   "us_per_step": ms * 1e3, "samples_per_s": 256 / (ms * 1e-3),
-                   "tflops": 2.618e8 / (ms * 1e-3) / 1e12,
-                   "us_per_step_hip_graph": res2["graph"] * 1e3}
+    if "cfg5" in only:
+        # config 5: 2048->2048 deg 8, bf16 coefficients packed once, forward at B = 1, 16, 64
+        L = _lib.load()
+        I5 = O5 = 2048
+        g = torch.Generator().manual_seed(5)
+        c5 = (torch.randn(I5, O5, 9, generator=g) / (I5 * 9)).bfloat16().to(dev)
+        res5 = {}
+        for B5 in (1, 16, 64):
+            d = _lib.make_desc(B5, I5, O5, 8, _lib.CKAN_COMPUTE_BF16, _lib.CKAN_DTYPE_BF16)
+            st = _lib.stream_ptr(dev)
+            packed = torch.empty(L.ckan_packed_bytes(d), dtype=torch.uint8, device=dev)
+            _lib.check(L.ckan_pack_coeffs(d, c5.data_ptr(), packed.data_ptr(), st))
+            x5 = torch.randn(B5, I5, generator=g).to(dev)
+            y5 = torch.empty(B5, O5, device=dev)
+            t5 = torch.empty(L.ckan_tcache_elems(d), device=dev)
+            wsb = L.ckan_fwd_workspace_bytes(d)
+            ws = torch.zeros(max(wsb, 256), dtype=torch.uint8, device=dev)
+            fwd = lambda: _lib.check(L.ckan_forward(d, x5.data_ptr(), packed.data_ptr(), y5.data_ptr(),
+                                                    t5.data_ptr(), ws.data_ptr(), wsb, st))
+            ms = _time_loop(fwd, 200, 20)
+            _lib.profile_report()
+            _lib.profile_enable(True)
+            for _ in range(50):
+                fwd()
+            torch.cuda.synchronize()
+            _lib.profile_enable(False)
+            rep = _lib.profile_report()
+            gemm_ms = rep["fwd_gemm"][1] / rep["fwd_gemm"][0]
+            alg_bytes = I5 * O5 * 9 * 2 + B5 * I5 * 4 + B5 * O5 * 4
+            res5[f"B{B5}"] = {"us_forward": ms * 1e3, "us_gemm": gemm_ms * 1e3,
+                              "gemm_GBps": alg_bytes / (gemm_ms * 1e-3) / 1e9,
+                              "frac_hbm_peak": alg_bytes / (gemm_ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
+                              "alg_bytes": alg_bytes}
+        out["cfg5"] = {"workload": "ChebyKANLayer(2048,2048,8) inference, bf16 coefficients (packed once)",
+                       **res5}
 
-    # config 4: 512->512->512->512->64, deg 16, B=65536, fp32 masters + bf16 compute, MSE + SGD, 100 steps
-    g = torch.Generator().manual_seed(4)
-    x4 = (torch.rand(65536, 512, generator=g) * 6 - 3).to(dev)
-    W = (torch.randn(512, 64, generator=g) / math.sqrt(512)).to(dev)
-    t4 = x4 @ W + 0.1 * torch.randn(65536, 64, generator=g).to(dev)
-    torch.manual_seed(4)
-    seq = kan_amd.KANSequential(*[kan_amd.ChebyKANLayer(a, b, 16)
-                                  for a, b in [(512, 512), (512, 512), (512, 512), (512, 64)]])
-    ex = kan_amd.ResidentExecutor.from_sequential(seq, 65536, compute="bf16", loss="mse",
-                                                  optimizer="sgd", lr=0.01)
-    ms = _time_loop(lambda: ex.step(x4, t4), 100, 3)
-    out["cfg4"] = {"workload": "512->512->512->512->64 deg 16 B=65536 bf16 MFMA, fp32 masters, MSE+SGD, resident",
-                   "ms_per_step": ms, "samples_per_s": 65536 / (ms * 1e-3),
-                   "tflops": 4.8920e12 / (ms * 1e-3) / 1e12,
-                   "frac_bf16_peak": 4.8920e12 / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
-                   "final_loss": float(ex.step(x4, t4).item())}
-    ex.close()
+    if "families" in only:
+        # the Jacobi / Hermite layers at the config-3 shape: same kernels plus the
+        # change of basis in the pack and the dC back-transform
+        fam = {}
+        g = torch.Generator().manual_seed(6)
+        xf = torch.randn(B, I, generator=g).to(dev).requires_grad_(True)
+        dyf = torch.randn(B, O, generator=g).to(dev)
+        for name, make in (("JacobiKANLayer(alpha=0.5,beta=0.5)",
+                            lambda: kan_amd.JacobiKANLayer(I, O, DEG, alpha=0.5, beta=0.5, compute="bf16")),
+                           ("HermiteKANLayer(physicist)",
+                            lambda: kan_amd.HermiteKANLayer(I, O, DEG, compute="bf16"))):
+            torch.manual_seed(6)
+            layer = make().to(dev)
+            ms = _time_gpu(layer, xf, dyf, 30, 10)
+            kern = _kernel_breakdown(layer, xf, dyf, 10)
+            fam[name] = {"ms_per_step": ms, "samples_per_s": B / (ms * 1e-3),
+                         "tflops": STEP_FLOP / (ms * 1e-3) / 1e12,
+                         "pack_ms": kern["pack"]["avg_ms"],
+                         "coeff_from_cheb_ms": kern["coeff_from_cheb"]["avg_ms"]}
+        out["families_cfg3_shape"] = {"workload": "1024->1024 deg 8, B=8192, bf16 MFMA, pack+fwd+bwd",
+                                      **fam}
 
-    # config 5: 2048->2048 deg 8, bf16 coefficients packed once, forward at B = 1, 16, 64
-    L = _lib.load()
-    I5 = O5 = 2048
-    g = torch.Generator().manual_seed(5)
-    c5 = (torch.randn(I5, O5, 9, generator=g) / (I5 * 9)).bfloat16().to(dev)
-    res5 = {}
-    for B5 in (1, 16, 64):
-        d = _lib.make_desc(B5, I5, O5, 8, _lib.CKAN_COMPUTE_BF16, _lib.CKAN_DTYPE_BF16)
-        st = _lib.stream_ptr(dev)
-        packed = torch.empty(L.ckan_packed_bytes(d), dtype=torch.uint8, device=dev)
-        _lib.check(L.ckan_pack_coeffs(d, c5.data_ptr(), packed.data_ptr(), st))
-        x5 = torch.randn(B5, I5, generator=g).to(dev)
-        y5 = torch.empty(B5, O5, device=dev)
-        t5 = torch.empty(L.ckan_tcache_elems(d), device=dev)
-        wsb = L.ckan_fwd_workspace_bytes(d)
-        ws = torch.zeros(max(wsb, 256), dtype=torch.uint8, device=dev)
-        fwd = lambda: _lib.check(L.ckan_forward(d, x5.data_ptr(), packed.data_ptr(), y5.data_ptr(),
-                                                t5.data_ptr(), ws.data_ptr(), wsb, st))
-        ms = _time_loop(fwd, 200, 20)
-        _lib.profile_report()
-        _lib.profile_enable(True)
-        for _ in range(50):
-            fwd()
-        torch.cuda.synchronize()
-        _lib.profile_enable(False)
-        rep = _lib.profile_report()
-        gemm_ms = rep["fwd_gemm"][1] / rep["fwd_gemm"][0]
-        alg_bytes = I5 * O5 * 9 * 2 + B5 * I5 * 4 + B5 * O5 * 4
-        res5[f"B{B5}"] = {"us_forward": ms * 1e3, "us_gemm": gemm_ms * 1e3,
-                          "gemm_GBps": alg_bytes / (gemm_ms * 1e-3) / 1e9,
-                          "frac_hbm_peak": alg_bytes / (gemm_ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
-                          "alg_bytes": alg_bytes}
-    out["cfg5"] = {"workload": "ChebyKANLayer(2048,2048,8) inference, bf16 coefficients (packed once)",
-                   **res5}
     return out
 
 
@@ -257,6 +287,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-fp32", action="store_true")
     ap.add_argument("--no-suite", action="store_true", help="skip configs 1, 2, 4, 5")
+    ap.add_argument("--suite-only", default=",".join(SUITE),
+                    help="comma list of suite entries to run (default: all of %s)" % (SUITE,))
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="run a plain device copy of this many MiB first (counter calibration)")
     args = ap.parse_args()
@@ -339,7 +371,11 @@ def main():
         **extra,
     }
     if not args.no_suite:
-        out["configs"] = _suite()
+        only = tuple(n for n in args.suite_only.split(",") if n)
+        unknown = set(only) - set(SUITE)
+        if unknown:
+            ap.error(f"unknown suite entries {sorted(unknown)}")
+        out["configs"] = _suite(only)
     if not args.no_cpu:
         out["cpu_baseline"] = _cpu_baseline(args.cpu_rows, args.cpu_reps)
     print(json.dumps(out))
