@@ -88,30 +88,54 @@ void family_to_chebyshev(const double* a, const double* b, const double* c, int 
   for (int i = 0; i < D * D; ++i) M[i] = v[i];
 }
 
-// dc[q, n] (+)= sum_{k <= n} dcheb[q, k] m[n][k].  One thread per (i, o) row;
-// every load of a row precedes its stores, so dcheb may alias dc.
+// dc[q, n] (+)= sum_{k <= n} dcheb[q, k] m[n][k] over rows q of D values.
+// A block takes 256 consecutive rows: one contiguous run of 256 * D floats,
+// moved with float4 accesses when aligned and staged in LDS (odd D: the
+// per-row reads hit distinct banks).  Every load of a block precedes its
+// stores and blocks own disjoint rows, so dcheb may alias dc.
 template <int DM>
 __global__ void __launch_bounds__(256)
-k_coeff_from_cheb(const float* dcheb, float* dc, int64_t rows, int D, int accumulate,
+k_coeff_from_cheb(const float* dcheb, float* dc, int64_t rows, int D, int accumulate, int vec,
                   BasisXform xf) {
-  for (int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; q < rows;
-       q += (int64_t)gridDim.x * blockDim.x) {
-    const float* src = dcheb + q * D;
+  __shared__ __attribute__((aligned(16))) float tile[256 * DM];
+  const int tid = threadIdx.x;
+  const int64_t r0 = (int64_t)blockIdx.x * 256;
+  const int nr = (int)min<int64_t>(256, rows - r0);
+  const int n = nr * D;
+  const bool v4 = vec && (n % 4) == 0;
+  const float* src = dcheb + r0 * D;
+  float* dst = dc + r0 * D;
+  if (v4) {
+    for (int k = tid; k < n / 4; k += 256)
+      reinterpret_cast<f32x4_t*>(tile)[k] = reinterpret_cast<const f32x4_t*>(src)[k];
+  } else {
+    for (int k = tid; k < n; k += 256) tile[k] = src[k];
+  }
+  __syncthreads();
+  if (tid < nr) {
     float g[DM];
 #pragma unroll
-    for (int k = 0; k < DM; ++k) g[k] = k < D ? src[k] : 0.0f;
-    float r[DM];
+    for (int k = 0; k < DM; ++k) g[k] = k < D ? tile[tid * D + k] : 0.0f;
 #pragma unroll
-    for (int n = 0; n < DM; ++n) {
+    for (int m = 0; m < DM; ++m) {
       float acc = 0.0f;
 #pragma unroll
-      for (int k = 0; k <= n; ++k) acc = fmaf(g[k], xf.m[n * kMaxD + k], acc);
-      r[n] = acc;
+      for (int k = 0; k <= m; ++k) acc = fmaf(g[k], xf.m[m * kMaxD + k], acc);
+      if (m < D) tile[tid * D + m] = acc;
     }
-    float* dst = dc + q * D;
-#pragma unroll
-    for (int n = 0; n < DM; ++n)
-      if (n < D) dst[n] = accumulate ? dst[n] + r[n] : r[n];
+  }
+  __syncthreads();
+  if (v4) {
+    for (int k = tid; k < n / 4; k += 256) {
+      f32x4_t r = reinterpret_cast<const f32x4_t*>(tile)[k];
+      if (accumulate) {
+        const f32x4_t o = reinterpret_cast<const f32x4_t*>(dst)[k];
+        r = f32x4_t{o[0] + r[0], o[1] + r[1], o[2] + r[2], o[3] + r[3]};
+      }
+      reinterpret_cast<f32x4_t*>(dst)[k] = r;
+    }
+  } else {
+    for (int k = tid; k < n; k += 256) dst[k] = accumulate ? dst[k] + tile[k] : tile[k];
   }
 }
 
@@ -172,12 +196,14 @@ static unsigned grid_of(int64_t work) {
 void launch_coeff_from_cheb(const float* dcheb, float* dc, const Plan& p, bool accumulate,
                             const BasisXform& xf, hipStream_t s) {
   const int64_t rows = (int64_t)p.I * p.O;
-  const dim3 g(grid_of(rows));
+  const dim3 g((unsigned)((rows + 255) / 256));
+  const int vec = is_al16(dcheb) && is_al16(dc);
+  const int acc = accumulate ? 1 : 0;
   switch (p.P) {
-    case 2: hipLaunchKernelGGL((k_coeff_from_cheb<3>), g, dim3(256), 0, s, dcheb, dc, rows, p.D, (int)accumulate, xf); break;
-    case 4: hipLaunchKernelGGL((k_coeff_from_cheb<5>), g, dim3(256), 0, s, dcheb, dc, rows, p.D, (int)accumulate, xf); break;
-    case 8: hipLaunchKernelGGL((k_coeff_from_cheb<9>), g, dim3(256), 0, s, dcheb, dc, rows, p.D, (int)accumulate, xf); break;
-    default: hipLaunchKernelGGL((k_coeff_from_cheb<17>), g, dim3(256), 0, s, dcheb, dc, rows, p.D, (int)accumulate, xf); break;
+    case 2: hipLaunchKernelGGL((k_coeff_from_cheb<3>), g, dim3(256), 0, s, dcheb, dc, rows, p.D, acc, vec, xf); break;
+    case 4: hipLaunchKernelGGL((k_coeff_from_cheb<5>), g, dim3(256), 0, s, dcheb, dc, rows, p.D, acc, vec, xf); break;
+    case 8: hipLaunchKernelGGL((k_coeff_from_cheb<9>), g, dim3(256), 0, s, dcheb, dc, rows, p.D, acc, vec, xf); break;
+    default: hipLaunchKernelGGL((k_coeff_from_cheb<17>), g, dim3(256), 0, s, dcheb, dc, rows, p.D, acc, vec, xf); break;
   }
 }
 

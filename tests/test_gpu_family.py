@@ -110,11 +110,12 @@ def test_family_basis_functions_and_backward(family, alpha, beta):
     assert _rel(td.grad, tr.grad) <= FP32_TOL
 
 
-def test_coeff_grad_transform_accumulates():
-    """dC (+)= dC' M^T through the C-ABI, against the same product on the CPU."""
+@pytest.mark.parametrize("I,O,deg", [(37, 19, 7), (5, 7, 8), (300, 260, 16)])
+def test_coeff_grad_transform_accumulates(I, O, deg):
+    """dC (+)= dC' M^T through the C-ABI, against the same product on the CPU
+    (float4 blocks, a scalar tail of odd length, and a partial last block)."""
     import numpy as np
     lib = _lib.load()
-    I, O, deg = 37, 19, 7
     spec = _spec("hermite", deg)
     M = (ctypes.c_double * ((deg + 1) ** 2))()
     assert lib.ckan_basis_to_chebyshev(spec, M) == 0
@@ -125,7 +126,8 @@ def test_coeff_grad_transform_accumulates():
     d = _lib.make_desc(1, I, O, deg, 0, 0)
     out = base.cuda()
     st = _lib.stream_ptr(out.device)
-    _lib.check(lib.ckan_coeff_grad_from_chebyshev(d, spec, dcheb.cuda().data_ptr(), out.data_ptr(), 1, st))
+    dch = dcheb.cuda()
+    _lib.check(lib.ckan_coeff_grad_from_chebyshev(d, spec, dch.data_ptr(), out.data_ptr(), 1, st))
     expect = base.double() + torch.einsum("iok,nk->ion", dcheb.double(), Mn)
     assert _rel(out, expect) <= FP32_TOL
     inplace = dcheb.cuda()
