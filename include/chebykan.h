@@ -103,6 +103,21 @@ int ckan_backward(const ckan_desc* desc, const float* t_cache, const void* packe
                   const float* dy, float* dx, float* dcoeffs, int accumulate,
                   void* ws, size_t ws_bytes, void* stream);
 
+/* ---- fp64 path ------------------------------------------------------------
+ * The reference layer computes in fp64 when its parameter is fp64
+ * (kan/layers/chebykan.py:48-51 after .double(); kan/basis/chebyshev.py:78-101
+ * then runs in fp64).  These entry points run that case in fp64 end to end
+ * (fp64 FMA on the vector ALU).  x, coeffs [in, out, D], y, t_cache [B, in],
+ * dy, dx and dcoeffs are fp64; desc->compute and desc->coeff_dtype must be 0.
+ * No packing and no workspace: coeffs are read in their own layout.
+ * Same formulas, NULL rules and accumulate semantics as ckan_forward /
+ * ckan_backward, and the same finite value at tanh saturation (|x| >= 19.06
+ * in fp64). */
+int ckan_forward_f64(const ckan_desc* desc, const double* x, const double* coeffs, double* y,
+                     double* t_cache, void* stream);
+int ckan_backward_f64(const ckan_desc* desc, const double* t_cache, const double* coeffs,
+                      const double* dy, double* dx, double* dcoeffs, int accumulate, void* stream);
+
 /* ---- other polynomial bases through the same kernels ---------------------
  * A layer whose basis is a three-term-recurrence family P_0..P_deg evaluated
  * at s * tanh(x) is the ChebyKAN layer with coefficients C' = C M, where

@@ -267,6 +267,44 @@ int ckan_basis_backward(const float* t, const float* g, int64_t n, int32_t degre
   return check_launch("basis_backward");
 }
 
+int ckan_forward_f64(const ckan_desc* desc, const double* x, const double* coeffs, double* y,
+                     double* t_cache, void* stream) {
+  int rc = validate_desc(desc);
+  if (rc) return rc;
+  if (desc->compute != CKAN_COMPUTE_FP32 || desc->coeff_dtype != CKAN_DTYPE_F32)
+    return fail(CKAN_ERR_INVALID_ARG, "fp64 path: desc->compute and desc->coeff_dtype must be 0");
+  if (desc->batch == 0) return CKAN_OK;
+  if (!x || !coeffs || !y || !t_cache) return fail(CKAN_ERR_INVALID_ARG, "x/coeffs/y/t_cache is NULL");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  ProfScope ps("fwd_f64", s);
+  launch_forward_f64(x, coeffs, y, t_cache, desc->batch, desc->in_dim, desc->out_dim, desc->degree, s);
+  return check_launch("forward_f64");
+}
+
+int ckan_backward_f64(const ckan_desc* desc, const double* t_cache, const double* coeffs,
+                      const double* dy, double* dx, double* dcoeffs, int accumulate, void* stream) {
+  int rc = validate_desc(desc);
+  if (rc) return rc;
+  if (desc->compute != CKAN_COMPUTE_FP32 || desc->coeff_dtype != CKAN_DTYPE_F32)
+    return fail(CKAN_ERR_INVALID_ARG, "fp64 path: desc->compute and desc->coeff_dtype must be 0");
+  if (!dx && !dcoeffs) return CKAN_OK;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (desc->batch == 0) {
+    if (dcoeffs && !accumulate) {  // fp64 zero is all-zero bits: fill as 2 floats per value
+      launch_zero_f32(reinterpret_cast<float*>(dcoeffs),
+                      2 * (int64_t)desc->in_dim * desc->out_dim * (desc->degree + 1), s);
+      return check_launch("zero dcoeffs");
+    }
+    return CKAN_OK;
+  }
+  if (!t_cache || !dy || (dx && !coeffs))
+    return fail(CKAN_ERR_INVALID_ARG, "t_cache/dy/coeffs is NULL");
+  ProfScope ps("bwd_f64", s);
+  launch_backward_f64(t_cache, coeffs, dy, dx, dcoeffs, accumulate != 0, desc->batch, desc->in_dim,
+                      desc->out_dim, desc->degree, s);
+  return check_launch("backward_f64");
+}
+
 namespace {
 // Validates a basis spec (and its degree against `degree` when >= 0) and
 // fills the family's recurrence.

@@ -80,6 +80,13 @@ void launch_basis_family(const float* t, int64_t n, int deg, const Recur3& r, fl
 void launch_basis_family_bwd(const float* t, const float* g, int64_t n, int deg, const Recur3& r,
                              float* dt, hipStream_t s);
 
+// ---- fp64 path (ckan_f64.hip): x, C, y, t, dy, dx, dC all fp64 -------------
+void launch_forward_f64(const double* x, const double* C, double* y, double* t, int64_t B, int I,
+                        int O, int deg, hipStream_t s);
+void launch_backward_f64(const double* t, const double* C, const double* dy, double* dx,
+                         double* dC, bool accumulate, int64_t B, int I, int O, int deg,
+                         hipStream_t s);
+
 // ---- launchers -------------------------------------------------------------
 void launch_tanh(const float* x, float* t, const Plan& p, hipStream_t s);
 // xf (optional, host struct passed by value to the kernel): pack C xf instead of C

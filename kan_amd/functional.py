@@ -184,13 +184,66 @@ class FamilyBasisFunction(torch.autograd.Function):
         return dt.to(ctx.t_dtype), None
 
 
+class ChebyKANFunction64(torch.autograd.Function):
+    """The layer in fp64 end to end (the reference's behaviour for fp64
+    parameters): x is taken as fp64, y, dx and dC are fp64."""
+
+    @staticmethod
+    def forward(ctx, x: torch.Tensor, coeffs: torch.Tensor):
+        _require_device(x, coeffs)
+        if coeffs.dim() != 3:
+            raise RuntimeError(f"coefficients must be [in, out, degree+1], got {tuple(coeffs.shape)}")
+        in_dim, out_dim, dd = coeffs.shape
+        if x.dim() != 2 or x.shape[1] != in_dim:
+            raise RuntimeError(f"x must be [batch, {in_dim}], got {tuple(x.shape)}")
+        lib = _lib.load()
+        dev = x.device
+        x64 = x.contiguous() if x.dtype == torch.float64 else x.double().contiguous()
+        c = coeffs.detach().contiguous()
+        desc = _lib.make_desc(x64.shape[0], in_dim, out_dim, dd - 1, 0, 0)
+        t = torch.empty(x64.shape[0], in_dim, dtype=torch.float64, device=dev)
+        y = torch.empty(x64.shape[0], out_dim, dtype=torch.float64, device=dev)
+        _lib.check(lib.ckan_forward_f64(desc, x64.data_ptr(), c.data_ptr(), y.data_ptr(),
+                                        t.data_ptr(), _lib.stream_ptr(dev)))
+        ctx.save_for_backward(t, c)
+        ctx.desc = desc
+        ctx.x_dtype = x.dtype
+        return y
+
+    @staticmethod
+    def backward(ctx, dy: torch.Tensor):
+        t, c = ctx.saved_tensors
+        desc = ctx.desc
+        need_dx, need_dc = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        if not (need_dx or need_dc):
+            return None, None
+        lib = _lib.load()
+        dev = dy.device
+        dy64 = dy.contiguous() if dy.dtype == torch.float64 else dy.double().contiguous()
+        dx = torch.empty(desc.batch, desc.in_dim, dtype=torch.float64, device=dev) if need_dx else None
+        dc = (torch.empty(desc.in_dim, desc.out_dim, desc.degree + 1, dtype=torch.float64, device=dev)
+              if need_dc else None)
+        _lib.check(lib.ckan_backward_f64(desc, t.data_ptr(), c.data_ptr(), dy64.data_ptr(),
+                                         _lib.ptr(dx), _lib.ptr(dc), 0, _lib.stream_ptr(dev)))
+        if dx is not None and ctx.x_dtype != torch.float64:
+            dx = dx.to(ctx.x_dtype)
+        return dx, dc
+
+
 def chebykan(x: torch.Tensor, coeffs: torch.Tensor, compute: str = "fp32") -> torch.Tensor:
-    """Functional ChebyKAN layer: x [B, in], coeffs [in, out, D] -> y [B, out]."""
+    """Functional ChebyKAN layer: x [B, in], coeffs [in, out, D] -> y [B, out].
+
+    fp64 coefficients select the fp64 path (``compute`` does not apply there)."""
+    if coeffs.dtype == torch.float64:
+        return ChebyKANFunction64.apply(x, coeffs)
     return ChebyKANFunction.apply(x, coeffs, compute, None)
 
 
 def family_kan(x: torch.Tensor, coeffs: torch.Tensor, spec, compute: str = "fp32") -> torch.Tensor:
     """y = einsum('bid,iod->bo', P(s tanh x), C) for the family of ``spec``."""
+    if coeffs.dtype == torch.float64:
+        raise RuntimeError("kan_amd: the fp64 path serves the Chebyshev layer; Jacobi / Hermite "
+                           "layers take float32 or bfloat16 coefficients")
     return ChebyKANFunction.apply(x, coeffs, compute, spec)
 
 
