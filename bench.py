@@ -89,7 +89,8 @@ def _time_loop(fn, iters, warmup):
     return e0.elapsed_time(e1) / iters
 
 
-SUITE = ("cfg1", "cfg2", "cfg4", "cfg5", "families")
+SUITE = ("cfg1", "cfg2", "cfg4", "cfg5", "families", "fp64")
+PEAK_FP64_TFLOPS = 78.6     # MI355X dense fp64
 
 
 def _suite(only=SUITE):
@@ -217,6 +218,21 @@ def _suite(only=SUITE):
         out["families_cfg3_shape"] = {"workload": "1024->1024 deg 8, B=8192, bf16 MFMA, pack+fwd+bwd",
                                       **fam}
 
+
+    if "fp64" in only:
+        # the layer with fp64 parameters (the reference computes in fp64 then), config-3 shape
+        torch.manual_seed(7)
+        layer = kan_amd.ChebyKANLayer(I, O, DEG).double().to(dev)
+        g = torch.Generator().manual_seed(7)
+        x64 = torch.randn(B, I, generator=g, dtype=torch.float64).to(dev).requires_grad_(True)
+        dy64 = torch.randn(B, O, generator=g, dtype=torch.float64).to(dev)
+        ms = _time_gpu(layer, x64, dy64, 5, 2)
+        kern = _kernel_breakdown(layer, x64, dy64, 3)
+        t = STEP_FLOP / (ms * 1e-3) / 1e12
+        out["fp64_cfg3_shape"] = {"workload": "ChebyKANLayer(1024,1024,8).double(), B=8192, fwd+bwd in fp64",
+                                  "ms_per_step": ms, "samples_per_s": B / (ms * 1e-3), "tflops": t,
+                                  "frac_fp64_peak": t / PEAK_FP64_TFLOPS,
+                                  "fwd_ms": kern["fwd_f64"]["avg_ms"], "bwd_ms": kern["bwd_f64"]["avg_ms"]}
     return out
 
 

@@ -91,45 +91,50 @@ k_fwd_f64(const double* __restrict__ t, const double* __restrict__ C, double* __
   }
 }
 
-// dx: block tile 64 rows x 8 inputs; thread (r, ii) = (tid / 8 + 32 h, tid % 8)
-// for h < 2 owns G[b, i, 0..D) in registers.  Outputs are taken 32 at a time:
-// dy [64][32] and C as [8 inputs][32 outputs][D] in LDS.
+// dx: block tile 128 rows x 8 inputs; thread (rr, ii) = (tid / 8, tid % 8)
+// owns G[b, i, 0..D) of rows rr + 32 h (h < 4) in registers.  Outputs are
+// taken 16 at a time: dy [128][16] and C as [8 inputs][16 outputs][D] in LDS,
+// the per-input stride padded to an odd number of doubles so the 8 inputs of
+// a wave read distinct banks.
 template <int DM>
 __global__ void __launch_bounds__(256)
 k_dx_f64(const double* __restrict__ t, const double* __restrict__ C, const double* __restrict__ dy,
          double* __restrict__ dx, int64_t B, int I, int O, int D) {
-  __shared__ double ys[64][33];
-  __shared__ double cs[8][32][DM + 1];
+  constexpr int OC = 16, CST = OC * (DM + 1) + 1;
+  __shared__ double ys[128][OC + 1];
+  __shared__ double cs[8 * CST];
   const int tid = threadIdx.x, rr = tid >> 3, ii = tid & 7;
-  const int64_t b0 = (int64_t)blockIdx.x * 64;
+  const int64_t b0 = (int64_t)blockIdx.x * 128;
   const int i0 = blockIdx.y * 8;
-  double g[2][DM];
+  double g[4][DM];
 #pragma unroll
-  for (int h = 0; h < 2; ++h)
+  for (int h = 0; h < 4; ++h)
 #pragma unroll
     for (int d = 0; d < DM; ++d) g[h][d] = 0.0;
-  for (int oc = 0; oc < O; oc += 32) {
+  for (int oc = 0; oc < O; oc += OC) {
     __syncthreads();
-    for (int k = tid; k < 64 * 32; k += 256) {
-      const int r = k >> 5, ol = k & 31;
+    for (int k = tid; k < 128 * OC; k += 256) {
+      const int r = k / OC, ol = k % OC;
       const int64_t b = b0 + r;
       ys[r][ol] = (b < B && oc + ol < O) ? dy[b * O + oc + ol] : 0.0;
     }
-    for (int k = tid; k < 8 * 32 * D; k += 256) {
-      const int il = k / (32 * D), rem = k % (32 * D), ol = rem / D, d = rem % D;
+    for (int k = tid; k < 8 * OC * D; k += 256) {
+      const int il = k / (OC * D), rem = k % (OC * D), ol = rem / D, d = rem % D;
       const int i = i0 + il, o = oc + ol;
-      cs[il][ol][d] = (i < I && o < O) ? C[((size_t)i * O + o) * D + d] : 0.0;
+      cs[il * CST + ol * (DM + 1) + d] = (i < I && o < O) ? C[((size_t)i * O + o) * D + d] : 0.0;
     }
     __syncthreads();
-#pragma unroll 2
-    for (int ol = 0; ol < 32; ++ol) {
-      const double a0 = ys[rr][ol], a1 = ys[rr + 32][ol];
+    for (int ol = 0; ol < OC; ++ol) {
+      double a[4];
+#pragma unroll
+      for (int h = 0; h < 4; ++h) a[h] = ys[rr + 32 * h][ol];
+      const double* cr = cs + ii * CST + ol * (DM + 1);
 #pragma unroll
       for (int d = 0; d < DM; ++d) {
         if (d < D) {
-          const double cv = cs[ii][ol][d];
-          g[0][d] = fma(a0, cv, g[0][d]);
-          g[1][d] = fma(a1, cv, g[1][d]);
+          const double cv = cr[d];
+#pragma unroll
+          for (int h = 0; h < 4; ++h) g[h][d] = fma(a[h], cv, g[h][d]);
         }
       }
     }
@@ -137,7 +142,7 @@ k_dx_f64(const double* __restrict__ t, const double* __restrict__ C, const doubl
   const int i = i0 + ii;
   if (i >= I) return;
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
+  for (int h = 0; h < 4; ++h) {
     const int64_t b = b0 + rr + 32 * h;
     if (b >= B) continue;
     const double tv = t[b * I + i];
@@ -156,22 +161,23 @@ k_dx_f64(const double* __restrict__ t, const double* __restrict__ C, const doubl
   }
 }
 
-// dC: block tile 8 inputs x 64 outputs; thread (il, ol) = (tid / 32, tid % 32)
-// owns outputs ol and ol + 32 of input il, all D degrees.  Rows are taken
-// 32 at a time: t [32][8] and dy [32][64] in LDS.
+// dC: block tile 8 inputs x 128 outputs; thread (il, ol) = (tid / 32, tid % 32)
+// owns outputs ol + 32 c (c < 4) of input il, all D degrees, so each basis
+// recurrence serves four outputs.  Rows are taken 32 at a time: t [32][8] and
+// dy [32][128] in LDS.
 template <int DM>
 __global__ void __launch_bounds__(256)
 k_dc_f64(const double* __restrict__ t, const double* __restrict__ dy, double* __restrict__ dC,
          int64_t B, int I, int O, int D, int accumulate) {
   __shared__ double ts[32][9];
-  __shared__ double ys[32][65];
+  __shared__ double ys[32][129];
   const int tid = threadIdx.x, il = tid >> 5, ol = tid & 31;
-  const int i0 = blockIdx.x * 8, o0 = blockIdx.y * 64;
-  double acc[2][DM];
+  const int i0 = blockIdx.x * 8, o0 = blockIdx.y * 128;
+  double acc[4][DM];
 #pragma unroll
-  for (int h = 0; h < 2; ++h)
+  for (int c = 0; c < 4; ++c)
 #pragma unroll
-    for (int d = 0; d < DM; ++d) acc[h][d] = 0.0;
+    for (int d = 0; d < DM; ++d) acc[c][d] = 0.0;
   for (int64_t bc = 0; bc < B; bc += 32) {
     __syncthreads();
     {
@@ -179,22 +185,23 @@ k_dc_f64(const double* __restrict__ t, const double* __restrict__ dy, double* __
       const int64_t b = bc + r;
       ts[r][k] = (b < B && i0 + k < I) ? t[b * I + i0 + k] : 0.0;
     }
-    for (int k = tid; k < 32 * 64; k += 256) {
-      const int r = k >> 6, o = k & 63;
+    for (int k = tid; k < 32 * 128; k += 256) {
+      const int r = k >> 7, o = k & 127;
       const int64_t b = bc + r;
       ys[r][o] = (b < B && o0 + o < O) ? dy[b * O + o0 + o] : 0.0;
     }
     __syncthreads();
-#pragma unroll 2
     for (int r = 0; r < 32; ++r) {
       const double tv = ts[r][il], t2 = 2.0 * tv;
-      const double y0 = ys[r][ol], y1 = ys[r][ol + 32];
+      double yv[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) yv[c] = ys[r][ol + 32 * c];
       double tp = 0.0, tc = 1.0;
 #pragma unroll
       for (int d = 0; d < DM; ++d) {
         if (d < D) {
-          acc[0][d] = fma(tc, y0, acc[0][d]);
-          acc[1][d] = fma(tc, y1, acc[1][d]);
+#pragma unroll
+          for (int c = 0; c < 4; ++c) acc[c][d] = fma(tc, yv[c], acc[c][d]);
           const double nx = d == 0 ? tv : fma(t2, tc, -tp);
           tp = tc;
           tc = nx;
@@ -205,13 +212,13 @@ k_dc_f64(const double* __restrict__ t, const double* __restrict__ dy, double* __
   const int i = i0 + il;
   if (i >= I) return;
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int o = o0 + ol + 32 * h;
+  for (int c = 0; c < 4; ++c) {
+    const int o = o0 + ol + 32 * c;
     if (o >= O) continue;
     double* dst = dC + ((size_t)i * O + o) * D;
 #pragma unroll
     for (int d = 0; d < DM; ++d)
-      if (d < D) dst[d] = accumulate ? dst[d] + acc[h][d] : acc[h][d];
+      if (d < D) dst[d] = accumulate ? dst[d] + acc[c][d] : acc[c][d];
   }
 }
 
@@ -237,14 +244,14 @@ void launch_backward_f64(const double* t, const double* C, const double* dy, dou
                          hipStream_t s) {
   const int D = deg + 1;
   if (dx) {
-    const dim3 g((unsigned)((B + 63) / 64), (unsigned)((I + 7) / 8));
+    const dim3 g((unsigned)((B + 127) / 128), (unsigned)((I + 7) / 8));
     if (D <= 3) hipLaunchKernelGGL((k_dx_f64<3>), g, dim3(256), 0, s, t, C, dy, dx, B, I, O, D);
     else if (D <= 5) hipLaunchKernelGGL((k_dx_f64<5>), g, dim3(256), 0, s, t, C, dy, dx, B, I, O, D);
     else if (D <= 9) hipLaunchKernelGGL((k_dx_f64<9>), g, dim3(256), 0, s, t, C, dy, dx, B, I, O, D);
     else hipLaunchKernelGGL((k_dx_f64<17>), g, dim3(256), 0, s, t, C, dy, dx, B, I, O, D);
   }
   if (dC) {
-    const dim3 g((unsigned)((I + 7) / 8), (unsigned)((O + 63) / 64));
+    const dim3 g((unsigned)((I + 7) / 8), (unsigned)((O + 127) / 128));
     const int acc = accumulate ? 1 : 0;
     if (D <= 3) hipLaunchKernelGGL((k_dc_f64<3>), g, dim3(256), 0, s, t, dy, dC, B, I, O, D, acc);
     else if (D <= 5) hipLaunchKernelGGL((k_dc_f64<5>), g, dim3(256), 0, s, t, dy, dC, B, I, O, D, acc);
