@@ -216,6 +216,24 @@ __device__ __forceinline__ void block_barrier() {
 __device__ __forceinline__ void dma16(const void* src, void* lds_base) {
   __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds_base, 16, 0, 0);
 }
+// The same copy in saddr form, for pipelined loops: lane l's 16 bytes at
+// sbase + voff land at LDS byte lds + 16 * l, with sbase and lds wave-uniform
+// (SGPRs) and voff a per-lane 32-bit offset.  Two measured reasons for the
+// inline assembly:
+//  * the compiler counts an LDS-DMA instruction as an LGKM event of another
+//    kind than ds_read and then waits with lgkmcnt(0) at every LDS read of a
+//    loop that contains one, which serialises each prefetched fragment read;
+//    the hardware counts these copies only in vmcnt (an lgkmcnt(0) right
+//    after one returns at once), so the copies are hidden from the compiler
+//    and the loops wait for them with explicit vmcnt waits;
+//  * vector-ALU address work for a copy (64-bit adds, readfirstlane of the
+//    LDS address) issues slowly while another wave of the SIMD streams MFMAs
+//    (copy rate fell from ~58 to ~7 B/clk per CU); here issuing is SALU only.
+// Callers keep voff + sbase inside the source allocation.
+__device__ __forceinline__ void dma16s(const void* sbase, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :: "v"(voff), "s"(sbase), "s"(lds) : "memory", "m0");
+}
 
 // Row of accumulator value v (0..15) for lane half g in a 32x32 MFMA result;
 // the column is lane % 32.

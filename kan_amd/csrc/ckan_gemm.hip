@@ -297,40 +297,47 @@ k_fwd_pipe(const float* __restrict__ tc, const typename Elem<BF>::type* __restri
   const int sg1 = min(nsg, sg0 + sg_per_split);
   const int npair = (sg1 - sg0 + 1) / 2;
 
-  // stage-invariant DMA source offsets (bytes); chunk c = (q*8 + wave)*64 + lane
+  // DMA: the 4 waves of half 0 issue every copy of a stage (HB_OPS coefficient
+  // and HT_OPS tanh copies per thread); chunk c = (q*4 + wq)*64 + lane lands at
+  // byte 16*c of the stage's coefficient or tanh area.  Sources are a
+  // wave-uniform base (the block's first output fragment / row, plus the
+  // stage) and a per-lane 32-bit offset fixed for the kernel.
+  constexpr int HB_OPS = 2 * K::B_OPS, HT_OPS = 2 * K::T_OPS, HOPS = 2 * (HB_OPS + HT_OPS);
   constexpr int CPF = kFragElems * (int)sizeof(E) / 16;  // 16-byte chunks per fragment
-  const char* cf = reinterpret_cast<const char*>(Cf);
-  size_t boff[K::B_OPS];
+  const int wqs = __builtin_amdgcn_readfirstlane(wq);
+  const char* bbase = reinterpret_cast<const char*>(Cf) + (size_t)nb0 * p.KB * kFragElems * sizeof(E);
+  uint32_t boff[HB_OPS];
 #pragma unroll
-  for (int q = 0; q < K::B_OPS; ++q) {
-    const int c = (q * 8 + wave) * 64 + lane;
+  for (int q = 0; q < HB_OPS; ++q) {
+    const int c = (q * 4 + wq) * 64 + lane;
     const int nbl = c / (G::SGK * CPF), off = c - nbl * (G::SGK * CPF);
     const int nb = min(nb0 + nbl, p.NBf - 1);
-    boff[q] = (size_t)nb * p.KB * kFragElems * sizeof(E) + (size_t)off * 16;
+    boff[q] = (uint32_t)((size_t)(nb - nb0) * p.KB * kFragElems * sizeof(E) + (size_t)off * 16);
   }
-  const char* tcb = reinterpret_cast<const char*>(tc);
-  size_t toff[K::T_OPS];
+  const char* tbase = reinterpret_cast<const char*>(tc) + (size_t)m_blk * p.I_sg * 4;
+  uint32_t toff[HT_OPS];
 #pragma unroll
-  for (int q = 0; q < K::T_OPS; ++q) {
-    const int c = (q * 8 + wave) * 64 + lane;
+  for (int q = 0; q < HT_OPS; ++q) {
+    const int c = (q * 4 + wq) * 64 + lane;
     const int rl = c / (G::SGI / 4), part4 = c - rl * (G::SGI / 4);  // stored chunk
     int64_t r = m_blk + rl;
     if (r >= p.B) r = p.B - 1;
-    toff[q] = ((size_t)r * p.I_sg + (part4 ^ fwd_t_xor<G::SGI / 4>(rl)) * 4) * 4;
+    toff[q] = (uint32_t)(((size_t)(r - m_blk) * p.I_sg + (part4 ^ fwd_t_xor<G::SGI / 4>(rl)) * 4) * 4);
   }
   const size_t b_stride = (size_t)G::SGK * kFragElems * sizeof(E);
   const size_t t_stride = (size_t)G::SGI * 4;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
 
-  // stage `sg` (if it exists) into ring slot `slot` (0 .. 2*NPB-1)
+  // stage `sg` (if it exists) into ring slot `slot` (0 .. 2*NPB-1); half 0 only
   auto issue = [&](int sg, int slot) __attribute__((always_inline)) {
     if (sg >= sg1) return;
-    char* base = smem + slot * K::STAGE_BYTES;
+    const uint32_t l = lds0 + slot * K::STAGE_BYTES + wqs * 1024;
 #pragma unroll
-    for (int q = 0; q < K::B_OPS; ++q)
-      dma16(cf + boff[q] + (size_t)sg * b_stride, base + (q * 8 + wave) * 1024);
+    for (int q = 0; q < HB_OPS; ++q)
+      dma16s(bbase + (size_t)sg * b_stride, boff[q], l + q * 4096);
 #pragma unroll
-    for (int q = 0; q < K::T_OPS; ++q)
-      dma16(tcb + toff[q] + (size_t)sg * t_stride, base + K::B_BYTES + (q * 8 + wave) * 1024);
+    for (int q = 0; q < HT_OPS; ++q)
+      dma16s(tbase + (size_t)sg * t_stride, toff[q], l + K::B_BYTES + q * 4096);
   };
   auto issue_pair = [&](int j) __attribute__((always_inline)) {
     const int slot = (j % NPB) * 2;
@@ -411,17 +418,28 @@ k_fwd_pipe(const float* __restrict__ tc, const typename Elem<BF>::type* __restri
     }
   };
 
+  // Pair j is copied by half 0: pairs 0 .. NPB-2 before the loop, pair
+  // j + NPB - 1 right after half 0's MFMAs of iteration j, while half 1's
+  // MFMAs of that iteration still run (the older waves of a SIMD are issued
+  // first, so half 0 reaches the end of its super-group first).  Copies
+  // interleaved with the MFMAs of every wave measured slower: each copy
+  // occupies the CU's address unit ~20 clk and stalls its wave meanwhile.
+  if (half == 0) {
 #pragma unroll
-  for (int j = 0; j < NPB - 1; ++j)
-    if (j < npair) issue_pair(j);
+    for (int j = 0; j < NPB - 1; ++j)
+      if (j < npair) issue_pair(j);
+  }
   for (int j = 0; j < npair; ++j) {
-    // pair j has landed once at most (pairs issued after it) * OPS remain;
-    // only the last pair can be a single stage, so near the end wait for all
-    if (j + NPB - 2 < npair - 1) wait_vmcnt<K::OPS * (NPB - 2)>();
-    else wait_vmcnt<0>();
+    // half 0: pair j has landed once only the copies of pairs j+1 .. j+NPB-2
+    // (HOPS each) remain; only the last pair can be a single stage, so near
+    // the end wait for all.  The barrier publishes the copies to half 1.
+    if (half == 0) {
+      if (j + NPB - 2 < npair - 1) wait_vmcnt<HOPS * (NPB - 2)>();
+      else wait_vmcnt<0>();
+    }
     block_barrier();
-    if (j + NPB - 1 < npair) issue_pair(j + NPB - 1);
     if (sg0 + 2 * j + half < sg1) compute((j % NPB) * 2 + half);
+    if (half == 0 && j + NPB - 1 < npair) issue_pair(j + NPB - 1);
   }
 
   // Sum the two halves' tiles through LDS (the ring is free once all waves
@@ -821,30 +839,35 @@ k_dx_dh(const typename Elem<BF>::type* __restrict__ dYx,
   const int nst = p.KBx / KI;
   const int rb = blockIdx.x % n_rb, ib = blockIdx.x / n_rb;
 
-  // per-op source offsets; dYx rows are padded to whole row blocks
+  // DMA: waves 0-3 issue every copy of a stage, HOPS per thread; chunk
+  // c = q*256 + tid lands at byte 16*c of the stage (dy rows first, then the
+  // coefficient fragments).  Sources: a wave-uniform base (block operand +
+  // stage) and a per-lane 32-bit offset; dYx rows are padded to whole row blocks.
   constexpr int RG = K::RG, THR = K::THR;
   static_assert(THR == 512, "launch bounds");
+  constexpr int HOPS = 2 * OPS, HA_OPS = 2 * K::A_OPS;
   const char* abase = reinterpret_cast<const char*>(dYx) + (size_t)rb * RG * NM * p.KBx * FB;
   const char* bbase = reinterpret_cast<const char*>(Cb) + (size_t)ib * P * p.KBx * FB;
-  size_t off[OPS];
+  uint32_t off[HOPS];
 #pragma unroll
-  for (int q = 0; q < OPS; ++q) {
-    const int c = q * THR + tid;
-    if (q < K::A_OPS) {
+  for (int q = 0; q < HOPS; ++q) {
+    const int c = q * 256 + (tid & 255);
+    if (q < HA_OPS) {
       const int run = c / RUN, w = c - run * RUN;
-      off[q] = (size_t)run * p.KBx * FB + w * 16;
+      off[q] = (uint32_t)((size_t)run * p.KBx * FB + w * 16);
     } else {
-      const int cc = c - K::A_OPS * THR;
+      const int cc = c - HA_OPS * 256;
       const int e = cc / RUN, w = cc - e * RUN;
-      off[q] = (size_t)e * p.KBx * FB + w * 16;
+      off[q] = (uint32_t)((size_t)e * p.KBx * FB + w * 16);
     }
   }
+  const uint32_t lds0 = (uint32_t)(uintptr_t)smem + (uint32_t)__builtin_amdgcn_readfirstlane(wave & 3) * 1024;
   auto issue = [&](int st) __attribute__((always_inline)) {
     if (st >= nst) st = nst - 1;  // past the end: in-range data, never read
     const size_t sb = (size_t)st * KI * FB;
-    char* dst = smem + (st % NBUF) * K::STAGE_BYTES + wave * 1024;
+    const uint32_t l = lds0 + (st % NBUF) * K::STAGE_BYTES;
 #pragma unroll
-    for (int q = 0; q < OPS; ++q) dma16((q < K::A_OPS ? abase : bbase) + sb + off[q], dst + q * (THR * 16));
+    for (int q = 0; q < HOPS; ++q) dma16s((q < HA_OPS ? abase : bbase) + sb, off[q], l + q * 4096);
   };
 
   // epilogue tanh values, loaded up front (they complete long before use)
@@ -869,14 +892,17 @@ k_dx_dh(const typename Elem<BF>::type* __restrict__ dYx,
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[mi][e][v] = 0.0f;
 
-  // the stage that empties slot (st % NBUF) is consumed before the barrier of
-  // stage st + 1; the refill of that slot is issued after it
+  // Waves 0-3 copy stage st + NBUF - 1 after their MFMAs of stage st, while
+  // waves 4-7 (the younger wave of each SIMD, issued second) still run theirs.
+  // Its slot was last read in stage st - 1, before this stage's barrier.
+  const bool copier = wave < 4;
+  if (copier) {
 #pragma unroll
-  for (int q = 0; q < NBUF - 1; ++q) issue(q);
+    for (int q = 0; q < NBUF - 1; ++q) issue(q);
+  }
   for (int st = 0; st < nst; ++st) {
-    wait_vmcnt<OPS * (NBUF - 2)>();  // stage st landed (st+1 may be in flight)
+    if (copier) wait_vmcnt<HOPS * (NBUF - 2)>();  // stage st landed (st+1 may be in flight)
     block_barrier();
-    issue(st + NBUF - 1);
     const char* base = smem + (st % NBUF) * K::STAGE_BYTES;
     Frag<BF> fa[KI][NM], fb[KI][PH];
 #pragma unroll
@@ -896,6 +922,7 @@ k_dx_dh(const typename Elem<BF>::type* __restrict__ dYx,
 #pragma unroll
         for (int e = 0; e < PH; ++e) mma(acc[mi][e], fa[kk][mi], fb[kk][e]);
     __builtin_amdgcn_sched_barrier(0);
+    if (copier) issue(st + NBUF - 1);
   }
   wait_vmcnt<0>();
   wait_lgkmcnt<0>();
@@ -1573,6 +1600,13 @@ static void ensure_lds_limit(const void* fn, int bytes, std::atomic<uint32_t>& d
 // Number of workgroups that fills the chip once: 256 CUs, one 4-wave block each.
 static constexpr int kChipBlocks = 256;
 
+// The pipelined forward addresses its copies as a block base plus a per-lane
+// 32-bit offset: up to 4 output fragments of coefficients, 256 tanh rows.
+static bool fwd_pipe_offsets_fit(const Plan& p) {
+  return (uint64_t)4 * p.KB * kFragElems * p.esz < (1ull << 32) &&
+         (uint64_t)256 * p.I_sg * sizeof(float) < (1ull << 32);
+}
+
 FwdChoice choose_fwd(const Plan& p) {
   FwdChoice c;
   if (p.B <= 64) {
@@ -1641,6 +1675,11 @@ static void fwd_dispatch(const float* x, float* t, const void* packed, float* y,
       default:
         if constexpr (FwdPipe<P, BF>::kOk) {
           typedef FwdPipe<P, BF> K;
+          if (!fwd_pipe_offsets_fit(p)) {  // per-lane copy offsets are 32-bit
+            hipLaunchKernelGGL((k_fwd<P, BF, 2, 4, 4, 1>), grid, dim3(256), 0, s, t, Cf, bias, y,
+                               part, p, c.sg_per_split);
+            break;
+          }
           const size_t lds = (size_t)K::LDS_BYTES;
           static std::atomic<uint32_t> lds_set{0};
           ensure_lds_limit(reinterpret_cast<const void*>(&k_fwd_pipe<P, BF>), (int)lds, lds_set);
