@@ -229,10 +229,16 @@ __device__ __forceinline__ void dma16(const void* src, void* lds_base) {
 //  * vector-ALU address work for a copy (64-bit adds, readfirstlane of the
 //    LDS address) issues slowly while another wave of the SIMD streams MFMAs
 //    (copy rate fell from ~58 to ~7 B/clk per CU); here issuing is SALU only.
-// Callers keep voff + sbase inside the source allocation.
+// Callers keep voff + sbase inside the source allocation and pass sbase and
+// lds wave-uniform; readfirstlane only moves them to SGPRs where the compiler
+// cannot prove that (it folds away for values it knows are uniform).
 __device__ __forceinline__ void dma16s(const void* sbase, uint32_t voff, uint32_t lds) {
+  const uint64_t a = (uint64_t)(uintptr_t)sbase;
+  const uint64_t s = ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32)) << 32) |
+                     (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)a);
+  const uint32_t l = __builtin_amdgcn_readfirstlane(lds);
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
-               :: "v"(voff), "s"(sbase), "s"(lds) : "memory", "m0");
+               :: "v"(voff), "s"(s), "s"(l) : "memory", "m0");
 }
 
 // Row of accumulator value v (0..15) for lane half g in a 32x32 MFMA result;

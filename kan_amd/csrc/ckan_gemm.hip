@@ -1316,21 +1316,29 @@ k_dc_pipe(const typename Elem<BF>::type* __restrict__ dYc, const float* __restri
   char* dyr = smem + K::BAS_BYTES;
   char* tlr = dyr + 3 * K::DY_SLOT;
 
-  // dy DMA: chunk c < DY_CHUNKS of a step is [stage hs][fragment f][k-block kk][16 B];
-  // chunks past that repeat real ones into the unused end of the slot
+  // DMA: waves 0-3 issue every copy of a step (the H stages of one pair step),
+  // DH_OPS dy and TH_OPS tanh copies per thread, after their MFMAs of the
+  // step before (see the loop).  Sources are a wave-uniform base plus a
+  // per-lane 32-bit offset fixed for the kernel.
   constexpr int CPF = FB / 16;
-  const char* dyb = reinterpret_cast<const char*>(dYc);
-  size_t doff[DY_OPS];
-  int dhs[DY_OPS];
+  constexpr int DH_OPS = (K::DY_CHUNKS + 255) / 256, TH_OPS = (K::T_CHUNKS + 255) / 256;
+  constexpr int HOPS = DH_OPS + TH_OPS;  // copies per thread per step
+  static_assert(DH_OPS * 4096 <= K::DY_SLOT && TH_OPS * 4096 <= K::T_SLOT, "copy slots");
+  const int t256 = tid & 255;
+  const uint32_t w1k = (uint32_t)__builtin_amdgcn_readfirstlane(wave & 3) * 1024;
+  // dy: chunk c < DY_CHUNKS of a step is [stage hs][fragment f][k-block kk][16 B];
+  // chunks past that repeat real ones into the unused end of the slot
+  const char* dyb = reinterpret_cast<const char*>(dYc) + (size_t)obk * NO * p.KBc * FB;
+  uint32_t doff[DH_OPS];
 #pragma unroll
-  for (int q = 0; q < DY_OPS; ++q) {
-    const int c = (q * 512 + tid) % K::DY_CHUNKS;
+  for (int q = 0; q < DH_OPS; ++q) {
+    const int c = (q * 256 + t256) % K::DY_CHUNKS;
     const int hs = c / (NO * KI * CPF), r1 = c - hs * (NO * KI * CPF);
     const int f = r1 / (KI * CPF), r2 = r1 - f * (KI * CPF);
     const int kk = r2 / CPF, piece = r2 - kk * CPF;
     const int mf = min(obk * NO + f, p.NBf - 1);
-    dhs[q] = hs;
-    doff[q] = ((size_t)mf * p.KBc + kk) * FB + (size_t)piece * 16;
+    doff[q] = (uint32_t)(((size_t)(mf - obk * NO) * p.KBc + kk) * FB + (size_t)piece * 16 +
+                         (size_t)hs * KI * FB);
   }
   // tanh tile of a stage: rows of 32 fp32 inputs.  Row rho is stored at row
   // t_row(rho) with its 16-byte chunks XOR-ed by t_xor(rho) / 4, so that the
@@ -1344,27 +1352,47 @@ k_dc_pipe(const typename Elem<BF>::type* __restrict__ dYc, const float* __restri
   auto t_xor = [](int r) __attribute__((always_inline)) {
     return RPT == 4 ? 16 * ((r >> 2) & 1) : RPT == 2 ? 8 * ((r >> 1) & 3) : 4 * (r & 7);
   };
-  // tanh DMA: chunk c = tid % T_CHUNKS fills [stage hs][stored row rr][chunk c % 8]
-  const int tcn = tid % K::T_CHUNKS;
-  const int ths = tcn / (K::T_STAGE / 16), trr = (tcn % (K::T_STAGE / 16)) / 8;
-  const int tsrc_row = t_row(trr);  // t_row is an involution
-  const int tcol = min(ib * 32 + (((tcn % 8) * 4) ^ t_xor(trr)), p.I_sg - 4);  // inputs past I_sg: never stored
-  const char* tcb = reinterpret_cast<const char*>(tc);
-  auto dma_dy = [&](int j) __attribute__((always_inline)) {
-    char* dst = dyr + (j % 3) * K::DY_SLOT + wave * 1024;
+  // tanh copy q: chunk c = (q*256 + t256) % T_CHUNKS fills [stage ths][stored row trr][chunk c % 8]
+  constexpr int SROWS = KI * 16;  // batch rows per stage
+  int tsr[TH_OPS], tcl[TH_OPS], tst[TH_OPS];
+  uint32_t toff[TH_OPS];
 #pragma unroll
-    for (int q = 0; q < DY_OPS; ++q) {
-      int st = st0 + H * j + dhs[q];
-      if (st >= st1) st = st0;  // past the end: any in-range source, never read
-      dma16(dyb + doff[q] + (size_t)st * KI * FB, dst + q * 8192);
-    }
+  for (int q = 0; q < TH_OPS; ++q) {
+    const int c = (q * 256 + t256) % K::T_CHUNKS;
+    tst[q] = c / (K::T_STAGE / 16);
+    const int trr = (c % (K::T_STAGE / 16)) / 8;
+    tsr[q] = t_row(trr);  // t_row is an involution
+    tcl[q] = min(ib * 32 + (((c % 8) * 4) ^ t_xor(trr)), p.I_sg - 4);  // inputs past I_sg: never stored
+    toff[q] = (uint32_t)(((size_t)tsr[q] * p.I_sg + tcl[q]) * 4);
+  }
+  const char* tcb = reinterpret_cast<const char*>(tc);
+  const uint32_t dyl0 = (uint32_t)(uintptr_t)dyr + w1k, tll0 = (uint32_t)(uintptr_t)tlr + w1k;
+  auto dma_dy = [&](int j) __attribute__((always_inline)) {
+    int st = st0 + H * j;
+    if (st + H > st1) st = st0;  // past the end: any in-range source, never read
+    const char* sb = dyb + (size_t)st * KI * FB;
+    const uint32_t l = dyl0 + (j % 3) * K::DY_SLOT;
+#pragma unroll
+    for (int q = 0; q < DH_OPS; ++q) dma16s(sb, doff[q], l + q * 4096);
   };
   auto dma_t = [&](int j) __attribute__((always_inline)) {
-    int st = st0 + H * j + ths;
-    if (st >= st1) st = st0;
-    int64_t b = (int64_t)st * KI * 16 + tsrc_row;
-    if (b >= p.B) b = p.B - 1;  // dy is zero on rows past B
-    dma16(tcb + ((size_t)b * p.I_sg + tcol) * 4, tlr + (j % 3) * K::T_SLOT + wave * 1024);
+    int st = st0 + H * j;
+    if (st + H > st1) st = st0;
+    const uint32_t l = tll0 + (j % 3) * K::T_SLOT;
+#pragma unroll
+    for (int q = 0; q < TH_OPS; ++q) {
+      const int64_t row0 = (int64_t)(st + tst[q]) * SROWS;
+      if (row0 + SROWS <= p.B) {
+        dma16s(tcb + (size_t)row0 * p.I_sg * 4, toff[q], l + q * 4096);
+      } else {
+        // a stage past the last row: rows clamped to B - 1 (dy is zero there)
+        const int64_t rb0 = row0 < p.B ? row0 : p.B - 1;
+        int64_t b = row0 + tsr[q];
+        if (b >= p.B) b = p.B - 1;
+        dma16s(tcb + (size_t)rb0 * p.I_sg * 4, (uint32_t)(((size_t)(b - rb0) * p.I_sg + tcl[q]) * 4),
+               l + q * 4096);
+      }
+    }
   };
 
   // basis generation slot of this thread within its half: k-block gkk,
@@ -1457,26 +1485,32 @@ k_dc_pipe(const typename Elem<BF>::type* __restrict__ dYc, const float* __restri
   };
 
   // prologue: tanh tiles of pairs 0..2, dy of pairs 0..1, basis of pair 0.
-  // Every pair issues 1 + DY_OPS DMA ops per thread in the order t(j+3),
-  // dy(j+2); past the end they fetch in-range data that is never read.
-  constexpr int OPS = 1 + DY_OPS;
-  dma_t(0);
-  dma_t(1);
-  dma_dy(0);
-  dma_t(2);
-  dma_dy(1);
-  wait_vmcnt<2 * OPS>();  // t(0) landed
+  // Waves 0-3 (the older wave of each SIMD, issued first) copy t(j+3) and
+  // dy(j+2) after their MFMAs of step j, while waves 4-7 still run theirs;
+  // both slots were last read in step j-1, before step j's barrier.  Past
+  // the end the copies fetch in-range data that is never read.
+  const bool copier = wave < 4;
+  if (copier) {
+    dma_t(0);
+    dma_t(1);
+    dma_dy(0);
+    dma_t(2);
+    dma_dy(1);
+    wait_vmcnt<2 * HOPS>();  // t(0) landed
+  }
   block_barrier();
   gen(0);
   for (int j = 0; j < npair; ++j) {
-    // dy(j) and t(j+1) have landed once only the ops of pair j+1's
-    // issue step (t(j+2), dy(j+1)) may be in flight
-    wait_vmcnt<OPS>();
+    // dy(j) and t(j+1) have landed once only the copies of the last issue
+    // (t(j+2), dy(j+1)) may be in flight
+    if (copier) wait_vmcnt<HOPS>();
     wait_lgkmcnt<0>();  // this thread's basis writes for pair j are done
     block_barrier();
-    dma_t(j + 3);
-    dma_dy(j + 2);
     step(j);  // also generates pair j+1 (unused after the last pair)
+    if (copier) {
+      dma_t(j + 3);
+      dma_dy(j + 2);
+    }
   }
   wait_vmcnt<0>();  // the prefetches past the end land before the LDS is reused
 
