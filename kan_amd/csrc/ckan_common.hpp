@@ -241,6 +241,16 @@ __device__ __forceinline__ void dma16s(const void* sbase, uint32_t voff, uint32_
                :: "v"(voff), "s"(s), "s"(l) : "memory", "m0");
 }
 
+// Makes a wave-uniform value (a kernel argument) live in SGPRs from here on.
+// Without it the compiler may issue the scalar load of an argument that is
+// only used after a pipelined loop right before that loop; a scalar load in
+// flight turns every LDS wait inside the loop into lgkmcnt(0), since scalar
+// loads may complete out of order.
+template <typename T>
+__device__ __forceinline__ void pin_sgpr(T v) {
+  asm volatile("" ::"s"(v));
+}
+
 // Row of accumulator value v (0..15) for lane half g in a 32x32 MFMA result;
 // the column is lane % 32.
 __device__ __forceinline__ int acc_row(int v, int g) { return 8 * (v >> 2) + 4 * g + (v & 3); }

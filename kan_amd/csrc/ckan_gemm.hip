@@ -424,6 +424,9 @@ k_fwd_pipe(const float* __restrict__ tc, const typename Elem<BF>::type* __restri
   // first, so half 0 reaches the end of its super-group first).  Copies
   // interleaved with the MFMAs of every wave measured slower: each copy
   // occupies the CU's address unit ~20 clk and stalls its wave meanwhile.
+  pin_sgpr(y);  // used after the loop
+  pin_sgpr(part);
+  pin_sgpr(bias_f);
   if (half == 0) {
 #pragma unroll
     for (int j = 0; j < NPB - 1; ++j)
@@ -896,6 +899,7 @@ k_dx_dh(const typename Elem<BF>::type* __restrict__ dYx,
   // waves 4-7 (the younger wave of each SIMD, issued second) still run theirs.
   // Its slot was last read in stage st - 1, before this stage's barrier.
   const bool copier = wave < 4;
+  pin_sgpr(dx);  // used after the loop
   if (copier) {
 #pragma unroll
     for (int q = 0; q < NBUF - 1; ++q) issue(q);
@@ -904,6 +908,8 @@ k_dx_dh(const typename Elem<BF>::type* __restrict__ dYx,
     if (copier) wait_vmcnt<HOPS * (NBUF - 2)>();  // stage st landed (st+1 may be in flight)
     block_barrier();
     const char* base = smem + (st % NBUF) * K::STAGE_BYTES;
+    // all reads first, in k-block order; the MFMAs of k-block kk wait only for
+    // its own reads (LDS returns in order)
     Frag<BF> fa[KI][NM], fb[KI][PH];
 #pragma unroll
     for (int kk = 0; kk < KI; ++kk) {
@@ -916,12 +922,13 @@ k_dx_dh(const typename Elem<BF>::type* __restrict__ dYx,
       __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
-    for (int kk = 0; kk < KI; ++kk)
+    for (int kk = 0; kk < KI; ++kk) {
 #pragma unroll
       for (int mi = 0; mi < NM; ++mi)
 #pragma unroll
         for (int e = 0; e < PH; ++e) mma(acc[mi][e], fa[kk][mi], fb[kk][e]);
-    __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
     if (copier) issue(st + NBUF - 1);
   }
   wait_vmcnt<0>();
@@ -1401,11 +1408,14 @@ k_dc_pipe(const typename Elem<BF>::type* __restrict__ dYc, const float* __restri
   const int th = tid % (512 / H);
   const int grh = th % G, gl = (th / G) % 64, gkk = th / (G * 64);
   const int trow0 = gkk * 16 + 8 * (gl >> 5) + grh * RPT;
-  auto gen = [&](int j) __attribute__((always_inline)) {
+  // the generation's tanh reads, issued apart so that they can go ahead of
+  // the step's fragment reads (LDS returns in order)
+  auto gen_read = [&](int j, float (&tv)[RPT]) __attribute__((always_inline)) {
     const float* tl = reinterpret_cast<const float*>(tlr + (j % 3) * K::T_SLOT + half * K::T_STAGE);
-    float tv[RPT];
 #pragma unroll
     for (int r = 0; r < RPT; ++r) tv[r] = tl[t_row(trow0 + r) * 32 + ((gl & 31) ^ t_xor(trow0 + r))];
+  };
+  auto gen_write = [&](int j, const float (&tv)[RPT]) __attribute__((always_inline)) {
     char* dst = bas + ((j & 1) * H + half) * K::BAS_STAGE + gkk * FB + (gl * 8 + grh * RPT) * (int)sizeof(E);
     float a[RPT], b[RPT], t2[RPT];
 #pragma unroll
@@ -1458,6 +1468,9 @@ k_dc_pipe(const typename Elem<BF>::type* __restrict__ dYc, const float* __restri
                   (size_t)(dh * PH) * KI * kFragElems;
     const E* bb = reinterpret_cast<const E*>(dyr + (j % 3) * K::DY_SLOT + half * K::DY_STAGE) +
                   (size_t)(og * NN) * KI * kFragElems;
+    float tv[RPT];
+    gen_read(j + 1, tv);
+    __builtin_amdgcn_sched_barrier(0);
     Frag<BF> fa[KI][PH], fb[KI][NN];
 #pragma unroll
     for (int kk = 0; kk < KI; ++kk) {
@@ -1467,7 +1480,7 @@ k_dc_pipe(const typename Elem<BF>::type* __restrict__ dYc, const float* __restri
       for (int ni = 0; ni < NN; ++ni) fb[kk][ni] = load_frag<BF>(bb + (ni * KI + kk) * kFragElems, lane);
       __builtin_amdgcn_sched_barrier(0);  // k-block order of the reads (LDS returns in order)
     }
-    gen(j + 1);
+    gen_write(j + 1, tv);
 #pragma unroll
     for (int kk = 0; kk < KI; ++kk)
 #pragma unroll
@@ -1490,6 +1503,8 @@ k_dc_pipe(const typename Elem<BF>::type* __restrict__ dYc, const float* __restri
   // both slots were last read in step j-1, before step j's barrier.  Past
   // the end the copies fetch in-range data that is never read.
   const bool copier = wave < 4;
+  pin_sgpr(colsum_part);  // used after the loop
+  pin_sgpr(out);
   if (copier) {
     dma_t(0);
     dma_t(1);
@@ -1499,7 +1514,11 @@ k_dc_pipe(const typename Elem<BF>::type* __restrict__ dYc, const float* __restri
     wait_vmcnt<2 * HOPS>();  // t(0) landed
   }
   block_barrier();
-  gen(0);
+  {
+    float tv0[RPT];
+    gen_read(0, tv0);
+    gen_write(0, tv0);
+  }
   for (int j = 0; j < npair; ++j) {
     // dy(j) and t(j+1) have landed once only the copies of the last issue
     // (t(j+2), dy(j+1)) may be in flight
