@@ -1543,16 +1543,21 @@ k_dc_pipe(const typename Elem<BF>::type* __restrict__ dYc, const float* __restri
     if (rgp < RS) {
       const int o = min(obk * NOW + oi, p.O32 - 1);
       const float* cp = colsum_part + o;
-      float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+      // batches of 16 independent loads, each batch summed as a fixed tree
+      float a = 0.0f;
       int k = rgp;
-      for (; k + 3 * RS < p.NBB; k += 4 * RS) {
-        a0 += cp[(size_t)k * p.O32];
-        a1 += cp[(size_t)(k + RS) * p.O32];
-        a2 += cp[(size_t)(k + 2 * RS) * p.O32];
-        a3 += cp[(size_t)(k + 3 * RS) * p.O32];
+      for (; k + 15 * RS < p.NBB; k += 16 * RS) {
+        float v[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) v[u] = cp[(size_t)(k + u * RS) * p.O32];
+#pragma unroll
+        for (int w = 8; w >= 1; w >>= 1)
+#pragma unroll
+          for (int u = 0; u < w; ++u) v[u] += v[u + w];
+        a += v[0];
       }
-      for (; k < p.NBB; k += RS) a0 += cp[(size_t)k * p.O32];
-      cpart[rgp * NOW + oi] = ((a0 + a1) + a2) + a3;
+      for (; k < p.NBB; k += RS) a += cp[(size_t)k * p.O32];
+      cpart[rgp * NOW + oi] = a;
     }
   }
 
@@ -1622,13 +1627,25 @@ k_dc_pipe(const typename Elem<BF>::type* __restrict__ dYc, const float* __restri
     wait_lgkmcnt<0>();
     block_barrier();
     if (ovalid > 0) {
-      const int run = ovalid * p.D;  // contiguous floats per input row
-      for (int il = 0; il < ivalid; ++il) {
-        float* dst = outz + ((size_t)(ib * 32 + il) * p.O + o0) * p.D;
-        const float* src = stg + il * OW * p.D;
-        for (int k = tid; k < run; k += 512) {
-          const float v = src[k];
-          dst[k] = accumulate ? dst[k] + v : v;
+      // ivalid runs of ovalid * D contiguous floats (one per input row), as
+      // float4 when every run starts 16-byte aligned
+      const int run = ovalid * p.D;
+      float* dst0 = outz + ((size_t)ib * 32 * p.O + o0) * p.D;
+      const size_t pitch = (size_t)p.O * p.D;  // floats between input rows
+      if (run % 4 == 0 && pitch % 4 == 0 && (reinterpret_cast<uintptr_t>(dst0) & 15) == 0) {
+        const int run4 = run / 4;
+        for (int q = tid; q < ivalid * run4; q += 512) {
+          const int il = q / run4, k4 = q - il * run4;
+          const f32x4_t v = *reinterpret_cast<const f32x4_t*>(stg + il * OW * p.D + 4 * k4);
+          f32x4_t* d = reinterpret_cast<f32x4_t*>(dst0 + il * pitch) + k4;
+          *d = accumulate ? *d + v : v;
+        }
+      } else {
+        for (int q = tid; q < ivalid * run; q += 512) {
+          const int il = q / run, k = q - il * run;
+          const float v = stg[il * OW * p.D + k];
+          float* d = dst0 + il * pitch + k;
+          *d = accumulate ? *d + v : v;
         }
       }
     }
