@@ -167,6 +167,36 @@ int ckan_family_basis(const ckan_basis_spec* spec, const float* t, int64_t n, fl
 int ckan_family_basis_backward(const ckan_basis_spec* spec, const float* t, const float* g,
                                int64_t n, float* dt, void* stream);
 
+/* ---- derivatives with respect to the input --------------------------------
+ * Each univariate function of a layer, f(x) = sum_n C[i, o, n] P_n(s tanh x)
+ * (spec NULL: the ChebyKAN layer's T_n(tanh x)), has an order-k derivative in
+ * x that is again a Chebyshev series in t = tanh x, of degree degree + k:
+ *   d^k f / dx^k = sum_j Ck[i, o, j] T_j(t),   Ck = C R,   R = M L^k,
+ * with M the family's change of basis and L : p -> (1 - t^2) p'(t) (exact in
+ * the T basis).  Requires degree + k <= 16 and fp32 coefficients.
+ * Replaces KANLayer.compute_derivatives / jacobian (kan/layers/base.py:102-141)
+ * and ChebyshevBasis.derivative (kan/basis/chebyshev.py:174-267).  Divergence:
+ * the reference's derivative coefficients are wrong for n >= 3, omit the
+ * tanh chain factor and its jacobian adds the other inputs' derivatives at 0;
+ * these return the exact derivatives with respect to x. */
+/* R (fp64, row-major [degree + 1][degree + 1 + order]); host only. */
+int ckan_derivative_matrix(const ckan_basis_spec* spec, int32_t degree, int32_t order, double* R);
+/* out [in, out, degree + 1 + order] = coeffs [in, out, degree + 1] R; a
+ * ChebyKAN forward of degree desc->degree + order with `out` then gives
+ * sum_i d^k f_{i,o} / dx^k (x_i), the layer's compute_derivatives(x, k). */
+int ckan_derivative_coeffs(const ckan_desc* desc, const ckan_basis_spec* spec, int32_t order,
+                           const float* coeffs, float* out, void* stream);
+/* dcoeffs [in, out, degree + 1] = dout_grad [in, out, degree + 1 + order] R^T
+ * (the gradient of ckan_derivative_coeffs). */
+int ckan_derivative_coeffs_backward(const ckan_desc* desc, const ckan_basis_spec* spec,
+                                    int32_t order, const float* dout_grad, float* dcoeffs,
+                                    void* stream);
+/* jac [batch, out, in]: jac[b, o, i] = d y[b, o] / d x[b, i] for x [batch, in]
+ * and fp32 coeffs; the workspace holds the order-1 coefficients re-laid out. */
+size_t ckan_jacobian_workspace_bytes(const ckan_desc* desc);
+int ckan_jacobian(const ckan_desc* desc, const ckan_basis_spec* spec, const float* x,
+                  const float* coeffs, float* jac, void* ws, size_t ws_bytes, void* stream);
+
 /* out[n, d] = T_d(t[n]) for d = 0..degree (fp32).  Replaces
  * ChebyshevBasis.basis_functions (kan/basis/chebyshev.py:103-172). */
 int ckan_basis(const float* t, int64_t n, int32_t degree, float* out, void* stream);

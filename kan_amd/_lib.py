@@ -96,6 +96,11 @@ SIGNATURES = {
     "ckan_coeff_grad_from_chebyshev": (ctypes.c_int, [_pdesc, _pspec, _vp, _vp, ctypes.c_int, _vp]),
     "ckan_family_basis": (ctypes.c_int, [_pspec, _vp, _i64, _vp, _vp]),
     "ckan_family_basis_backward": (ctypes.c_int, [_pspec, _vp, _vp, _i64, _vp, _vp]),
+    "ckan_derivative_matrix": (ctypes.c_int, [_pspec, _i32, _i32, ctypes.POINTER(_f64)]),
+    "ckan_derivative_coeffs": (ctypes.c_int, [_pdesc, _pspec, _i32, _vp, _vp, _vp]),
+    "ckan_derivative_coeffs_backward": (ctypes.c_int, [_pdesc, _pspec, _i32, _vp, _vp, _vp]),
+    "ckan_jacobian_workspace_bytes": (_sz, [_pdesc]),
+    "ckan_jacobian": (ctypes.c_int, [_pdesc, _pspec, _vp, _vp, _vp, _vp, _sz, _vp]),
     "ckan_basis": (ctypes.c_int, [_vp, _i64, _i32, _vp, _vp]),
     "ckan_basis_backward": (ctypes.c_int, [_vp, _vp, _i64, _i32, _vp, _vp]),
     "ckan_sgd_step": (ctypes.c_int, [_vp, _vp, _i64, _f32, _f32, _vp]),
@@ -188,6 +193,17 @@ def ptr(t) -> int:
 
 def profile_enable(on: bool) -> None:
     check(load().ckan_profile_enable(1 if on else 0))
+
+
+def derivative_matrix(spec, degree: int, order: int):
+    """R [degree+1, degree+1+order] (fp64, host): the Chebyshev coefficients in
+    t = tanh x of d^order/dx^order P_n(s tanh x) (spec None: T_n(tanh x))."""
+    import numpy as np
+    out = np.zeros((degree + 1) * (degree + 1 + order), dtype=np.float64)
+    sp = None if spec is None else ctypes.byref(spec)
+    check(load().ckan_derivative_matrix(sp, int(degree), int(order),
+                                        out.ctypes.data_as(ctypes.POINTER(_f64))))
+    return out.reshape(degree + 1, degree + 1 + order)
 
 
 def profile_report() -> dict:

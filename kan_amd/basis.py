@@ -172,12 +172,15 @@ class HermiteBasis(BasisFunction):
         fam = _lib.CKAN_BASIS_HERMITE if self.scaling == "physicist" else _lib.CKAN_BASIS_HERMITE_E
         return _lib.make_spec(fam, self.degree, 0.0, 0.0, 3.0)
 
-    def forward(self, x: torch.Tensor, coefficients: torch.Tensor) -> torch.Tensor:
+    def _check_input_map(self) -> None:
         if self._affine_map():
             raise RuntimeError(
                 "kan_amd HermiteBasis: a finite domain with normalize_domain=True maps inputs "
                 "linearly (no tanh); this build's HIP path implements the 3*tanh(x) input map "
                 "only. Pass domain=None or normalize_domain=False.")
+
+    def forward(self, x: torch.Tensor, coefficients: torch.Tensor) -> torch.Tensor:
+        self._check_input_map()
         x = x.view(-1, coefficients.shape[0])
         return F.family_kan(x, coefficients, self.spec(), self.compute)
 

@@ -388,6 +388,113 @@ int ckan_coeff_grad_from_chebyshev(const ckan_desc* desc, const ckan_basis_spec*
   return check_launch("coeff_grad_from_chebyshev");
 }
 
+namespace {
+// R = M L^order for a layer of degree `degree` (spec NULL: Chebyshev, M = I),
+// as floats in r->m[n * kMaxD + k] (transposed: r->m[k * kMaxD + n]); *dout = D + order.
+int derivative_xform(const ckan_basis_spec* spec, int degree, int order, bool transposed,
+                     BasisXform* r, int* dout, double* Rout = nullptr) {
+  if (degree < 0) return fail(CKAN_ERR_INVALID_ARG, "degree must be >= 0");
+  if (order < 0) return fail(CKAN_ERR_INVALID_ARG, "derivative order must be >= 0");
+  if (degree + order >= kMaxD)
+    return fail(CKAN_ERR_UNSUPPORTED, "degree %d + derivative order %d exceeds %d", degree, order,
+                kMaxD - 1);
+  const int D = degree + 1, DO = D + order;
+  double M[kMaxD * kMaxD];
+  if (spec) {
+    double a[kMaxD], b[kMaxD], c[kMaxD];
+    int rc = family_of(spec, degree, a, b, c);
+    if (rc) return rc;
+    family_to_chebyshev(a, b, c, degree, spec->scale, M);
+  } else {
+    for (int n = 0; n < D; ++n)
+      for (int k = 0; k < D; ++k) M[n * D + k] = n == k ? 1.0 : 0.0;
+  }
+  double R[kMaxD * kMaxD];
+  if (!derivative_to_chebyshev(M, degree, order, R))
+    return fail(CKAN_ERR_UNSUPPORTED, "derivative of order %d at degree %d", order, degree);
+  if (Rout)
+    for (int q = 0; q < D * DO; ++q) Rout[q] = R[q];
+  if (r) {
+    for (int q = 0; q < kMaxD * kMaxD; ++q) r->m[q] = 0.0f;
+    for (int n = 0; n < D; ++n)
+      for (int k = 0; k < DO; ++k)
+        r->m[transposed ? k * kMaxD + n : n * kMaxD + k] = (float)R[n * DO + k];
+  }
+  if (dout) *dout = DO;
+  return CKAN_OK;
+}
+
+int check_f32_layer(const ckan_desc* desc) {
+  int rc = validate_desc(desc);
+  if (rc) return rc;
+  if (desc->coeff_dtype != CKAN_DTYPE_F32)
+    return fail(CKAN_ERR_UNSUPPORTED, "derivatives take fp32 coefficients");
+  return CKAN_OK;
+}
+}  // namespace
+
+int ckan_derivative_matrix(const ckan_basis_spec* spec, int32_t degree, int32_t order, double* R) {
+  if (!R) return fail(CKAN_ERR_INVALID_ARG, "R is NULL");
+  return derivative_xform(spec, degree, order, false, nullptr, nullptr, R);
+}
+
+int ckan_derivative_coeffs(const ckan_desc* desc, const ckan_basis_spec* spec, int32_t order,
+                           const float* coeffs, float* out, void* stream) {
+  int rc = check_f32_layer(desc);
+  if (rc) return rc;
+  BasisXform r;
+  int dout = 0;
+  if ((rc = derivative_xform(spec, desc->degree, order, false, &r, &dout))) return rc;
+  if (!coeffs || !out) return fail(CKAN_ERR_INVALID_ARG, "coeffs/out is NULL");
+  const int64_t rows = (int64_t)desc->in_dim * desc->out_dim;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  ProfScope ps("deriv_coeffs", s);
+  launch_coeff_xform(coeffs, out, rows, desc->degree + 1, dout, 0, r, s);
+  return check_launch("derivative_coeffs");
+}
+
+int ckan_derivative_coeffs_backward(const ckan_desc* desc, const ckan_basis_spec* spec,
+                                    int32_t order, const float* dout_grad, float* dcoeffs,
+                                    void* stream) {
+  int rc = check_f32_layer(desc);
+  if (rc) return rc;
+  BasisXform rt;
+  int dout = 0;
+  if ((rc = derivative_xform(spec, desc->degree, order, true, &rt, &dout))) return rc;
+  if (!dout_grad || !dcoeffs) return fail(CKAN_ERR_INVALID_ARG, "dout_grad/dcoeffs is NULL");
+  const int64_t rows = (int64_t)desc->in_dim * desc->out_dim;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  ProfScope ps("deriv_coeffs_bwd", s);
+  launch_coeff_xform(dout_grad, dcoeffs, rows, dout, desc->degree + 1, 0, rt, s);
+  return check_launch("derivative_coeffs_backward");
+}
+
+size_t ckan_jacobian_workspace_bytes(const ckan_desc* desc) {
+  if (validate_desc(desc) != CKAN_OK) return 0;
+  return (size_t)desc->in_dim * desc->out_dim * (desc->degree + 2) * sizeof(float);
+}
+
+int ckan_jacobian(const ckan_desc* desc, const ckan_basis_spec* spec, const float* x,
+                  const float* coeffs, float* jac, void* ws, size_t ws_bytes, void* stream) {
+  int rc = check_f32_layer(desc);
+  if (rc) return rc;
+  BasisXform r;
+  int dout = 0;
+  if ((rc = derivative_xform(spec, desc->degree, 1, false, &r, &dout))) return rc;
+  if (desc->batch == 0) return CKAN_OK;
+  if (!x || !coeffs || !jac) return fail(CKAN_ERR_INVALID_ARG, "x/coeffs/jac is NULL");
+  const size_t need = ckan_jacobian_workspace_bytes(desc);
+  if (!ws || ws_bytes < need)
+    return fail(CKAN_ERR_WORKSPACE, "jacobian workspace needs %zu bytes, got %zu", need, ws_bytes);
+  const int64_t rows = (int64_t)desc->in_dim * desc->out_dim;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  ProfScope ps("jacobian", s);
+  float* c1t = reinterpret_cast<float*>(ws);
+  launch_coeff_xform(coeffs, c1t, rows, desc->degree + 1, dout, desc->out_dim, r, s);
+  launch_jacobian(x, c1t, jac, desc->batch, desc->in_dim, desc->out_dim, dout, s);
+  return check_launch("jacobian");
+}
+
 int ckan_family_basis(const ckan_basis_spec* spec, const float* t, int64_t n, float* out,
                       void* stream) {
   Recur3 r;

@@ -88,6 +88,100 @@ void family_to_chebyshev(const double* a, const double* b, const double* c, int 
   for (int i = 0; i < D * D; ++i) M[i] = v[i];
 }
 
+// d/dx of a Chebyshev series in t = tanh x: p -> (1 - t^2) p'(t).  p' by the
+// Chebyshev derivative recurrence b_{k-1} = b_{k+1} + 2 k a_k (b_0 halved);
+// (1 - t^2) q = q - u (u q) with the multiplication by u of family_to_chebyshev.
+static void chebyshev_dx(const double* a, int deg, double* out /* deg + 2 */) {
+  std::vector<double> b(deg + 2, 0.0), u1(deg + 2, 0.0), u2(deg + 3, 0.0);
+  for (int k = deg; k >= 1; --k) b[k - 1] = b[k + 1] + 2.0 * k * a[k];
+  b[0] *= 0.5;  // p' has degree deg - 1
+  auto mul_u = [](const double* src, int dsrc, double* dst) {
+    for (int k = 0; k <= dsrc + 1; ++k) dst[k] = 0.0;
+    for (int k = 0; k <= dsrc; ++k) {
+      if (k == 0) dst[1] += src[0];
+      else { dst[k + 1] += 0.5 * src[k]; dst[k - 1] += 0.5 * src[k]; }
+    }
+  };
+  const int dq = deg - 1;  // degree of p'
+  if (dq < 0) {
+    for (int k = 0; k <= deg + 1; ++k) out[k] = 0.0;
+    return;
+  }
+  mul_u(b.data(), dq, u1.data());      // degree dq + 1
+  mul_u(u1.data(), dq + 1, u2.data()); // degree dq + 2 = deg + 1
+  for (int k = 0; k <= deg + 1; ++k) out[k] = (k <= dq ? b[k] : 0.0) - u2[k];
+}
+
+bool derivative_to_chebyshev(const double* M, int degree, int order, double* R) {
+  if (degree < 0 || order < 0 || degree + order >= kMaxD) return false;
+  const int D = degree + 1, DO = D + order;
+  std::vector<double> cur(DO, 0.0), nxt(DO + 1, 0.0);
+  for (int n = 0; n < D; ++n) {
+    for (int k = 0; k < DO; ++k) cur[k] = k < D ? M[n * D + k] : 0.0;
+    int deg = degree;
+    for (int s = 0; s < order; ++s) {
+      chebyshev_dx(cur.data(), deg, nxt.data());
+      ++deg;
+      for (int k = 0; k < DO; ++k) cur[k] = k <= deg ? nxt[k] : 0.0;
+    }
+    for (int k = 0; k < DO; ++k) R[(size_t)n * DO + k] = cur[k];
+  }
+  return true;
+}
+
+// out[q, k] = sum_n in[q, n] r[n][k].  One thread per row; with transposed_o
+// the thread of row q = i * O + o writes [o][k][i] (consecutive threads take
+// consecutive i, so those stores coalesce).
+__global__ void __launch_bounds__(256)
+k_coeff_xform(const float* __restrict__ in, float* __restrict__ out, int64_t rows, int din,
+              int dout, int tO, BasisXform r) {
+  const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (t >= rows) return;
+  int64_t q = t;
+  int64_t o = 0, i = 0, I = 0;
+  if (tO > 0) {
+    I = rows / tO;
+    o = t / I;
+    i = t - o * I;
+    q = i * tO + o;
+  }
+  float v[kMaxD];
+#pragma unroll
+  for (int n = 0; n < kMaxD; ++n) v[n] = n < din ? in[q * din + n] : 0.0f;
+  for (int k = 0; k < dout; ++k) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int n = 0; n < kMaxD; ++n) acc = fmaf(v[n], r.m[n * kMaxD + k], acc);
+    if (tO > 0) out[(o * dout + k) * I + i] = acc;
+    else out[q * dout + k] = acc;
+  }
+}
+
+// jac[b, o, i] = sum_k c1t[o][k][i] T_k(tanh x[b, i]): block (i-block, b),
+// one input per thread, the T_k in registers, a loop over outputs.
+template <int DM>
+__global__ void __launch_bounds__(256)
+k_jacobian(const float* __restrict__ x, const float* __restrict__ c1t, float* __restrict__ jac,
+           int64_t B, int I, int O, int dout) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  const int64_t b = blockIdx.y;
+  if (i >= I) return;
+  const float t = tanhf(x[b * I + i]);
+  float T[DM];
+  T[0] = 1.0f;
+  if (DM > 1) T[1] = t;
+#pragma unroll
+  for (int k = 2; k < DM; ++k) T[k] = fmaf(2.0f * t, T[k - 1], -T[k - 2]);
+  for (int o = 0; o < O; ++o) {
+    const float* c = c1t + (size_t)o * dout * I + i;
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < DM; ++k)
+      if (k < dout) acc = fmaf(c[(size_t)k * I], T[k], acc);
+    jac[((size_t)b * O + o) * I + i] = acc;
+  }
+}
+
 // dc[q, n] (+)= sum_{k <= n} dcheb[q, k] m[n][k] over rows q of D values.
 // A block takes 256 consecutive rows: one contiguous run of 256 * D floats,
 // moved with float4 accesses when aligned and staged in LDS (odd D: the
@@ -204,6 +298,29 @@ void launch_coeff_from_cheb(const float* dcheb, float* dc, const Plan& p, bool a
     case 4: hipLaunchKernelGGL((k_coeff_from_cheb<5>), g, dim3(256), 0, s, dcheb, dc, rows, p.D, acc, vec, xf); break;
     case 8: hipLaunchKernelGGL((k_coeff_from_cheb<9>), g, dim3(256), 0, s, dcheb, dc, rows, p.D, acc, vec, xf); break;
     default: hipLaunchKernelGGL((k_coeff_from_cheb<17>), g, dim3(256), 0, s, dcheb, dc, rows, p.D, acc, vec, xf); break;
+  }
+}
+
+void launch_coeff_xform(const float* in, float* out, int64_t rows, int din, int dout,
+                        int transposed_o, const BasisXform& r, hipStream_t s) {
+  const dim3 g((unsigned)((rows + 255) / 256));
+  hipLaunchKernelGGL(k_coeff_xform, g, dim3(256), 0, s, in, out, rows, din, dout, transposed_o, r);
+}
+
+void launch_jacobian(const float* x, const float* c1t, float* jac, int64_t B, int I, int O,
+                     int dout, hipStream_t s) {
+  constexpr int64_t kMaxGridY = 65535;
+  for (int64_t b0 = 0; b0 < B; b0 += kMaxGridY) {  // rows in chunks of the grid's y limit
+    const int64_t nb = B - b0 < kMaxGridY ? B - b0 : kMaxGridY;
+    const dim3 g((unsigned)((I + 255) / 256), (unsigned)nb);
+    const float* xb = x + b0 * I;
+    float* jb = jac + b0 * O * I;
+    if (dout <= 5)
+      hipLaunchKernelGGL((k_jacobian<5>), g, dim3(256), 0, s, xb, c1t, jb, nb, I, O, dout);
+    else if (dout <= 9)
+      hipLaunchKernelGGL((k_jacobian<9>), g, dim3(256), 0, s, xb, c1t, jb, nb, I, O, dout);
+    else
+      hipLaunchKernelGGL((k_jacobian<17>), g, dim3(256), 0, s, xb, c1t, jb, nb, I, O, dout);
   }
 }
 

@@ -4,6 +4,7 @@ is the HIP library's.  Tensors on the CPU are rejected: there is no CPU path.
 """
 from __future__ import annotations
 
+import ctypes
 import threading
 
 import torch
@@ -253,3 +254,88 @@ def family_basis(t: torch.Tensor, spec) -> torch.Tensor:
 
 def chebyshev_basis(t: torch.Tensor, degree: int) -> torch.Tensor:
     return ChebyshevBasisFunction.apply(t, degree)
+
+
+# ---- derivatives with respect to the input (kan/layers/base.py:102-141) ------
+
+def _spec_ref(spec):
+    return None if spec is None else ctypes.byref(spec)
+
+
+def _derivative_desc(coeffs: torch.Tensor, batch: int = 0) -> "_lib.CkanDesc":
+    in_dim, out_dim, dd = coeffs.shape
+    return _lib.make_desc(batch, in_dim, out_dim, dd - 1, _lib.CKAN_COMPUTE_FP32, _lib.CKAN_DTYPE_F32)
+
+
+def _f32_coeffs(coeffs: torch.Tensor) -> torch.Tensor:
+    _require_device(coeffs)
+    if coeffs.dim() != 3:
+        raise RuntimeError(f"coefficients must be [in, out, degree+1], got {tuple(coeffs.shape)}")
+    if coeffs.dtype == torch.float64:
+        raise RuntimeError("kan_amd derivatives take float32 (or bfloat16) coefficients; the fp64 "
+                           "path serves the forward and backward only")
+    return coeffs.float().contiguous()
+
+
+class DerivativeCoeffsFunction(torch.autograd.Function):
+    """Ck = C R [in, out, D + order]: the Chebyshev coefficients in tanh x of
+    the order-k x-derivative of each univariate function (R from the library,
+    exact in fp64, applied in fp32); backward dC = dCk R^T."""
+
+    @staticmethod
+    def forward(ctx, coeffs: torch.Tensor, spec, order: int):
+        c = _f32_coeffs(coeffs.detach())
+        in_dim, out_dim, dd = c.shape
+        out = torch.empty(in_dim, out_dim, dd + order, dtype=torch.float32, device=c.device)
+        desc = _derivative_desc(c)
+        lib = _lib.load()
+        _lib.check(lib.ckan_derivative_coeffs(desc, _spec_ref(spec), int(order), c.data_ptr(),
+                                              out.data_ptr(), _lib.stream_ptr(c.device)))
+        ctx.desc, ctx.spec, ctx.order, ctx.c_dtype = desc, spec, order, coeffs.dtype
+        return out
+
+    @staticmethod
+    def backward(ctx, g: torch.Tensor):
+        g = g.float().contiguous()
+        d = ctx.desc
+        dc = torch.empty(d.in_dim, d.out_dim, d.degree + 1, dtype=torch.float32, device=g.device)
+        lib = _lib.load()
+        _lib.check(lib.ckan_derivative_coeffs_backward(d, _spec_ref(ctx.spec), int(ctx.order),
+                                                       g.data_ptr(), dc.data_ptr(),
+                                                       _lib.stream_ptr(g.device)))
+        if ctx.c_dtype != torch.float32:
+            dc = dc.to(ctx.c_dtype)
+        return dc, None, None
+
+
+def derivative_coeffs(coeffs: torch.Tensor, spec, order: int) -> torch.Tensor:
+    return DerivativeCoeffsFunction.apply(coeffs, spec, int(order))
+
+
+def derivatives(x: torch.Tensor, coeffs: torch.Tensor, spec, order: int = 1,
+                compute: str = "fp32") -> torch.Tensor:
+    """[B, out]: sum_i d^order f_{i,o} / dx^order (x[b, i]), the sum over inputs of
+    each univariate function's order-th x-derivative (differentiable in x and C)."""
+    if order < 0:
+        raise ValueError(f"order must be >= 0, got {order}")
+    if order == 0:
+        return chebykan(x, coeffs, compute) if spec is None else family_kan(x, coeffs, spec, compute)
+    return ChebyKANFunction.apply(x, derivative_coeffs(coeffs, spec, order), compute, None)
+
+
+def jacobian(x: torch.Tensor, coeffs: torch.Tensor, spec) -> torch.Tensor:
+    """[B, out, in]: d y[b, o] / d x[b, i] (fp32; not differentiable)."""
+    c = _f32_coeffs(coeffs.detach())
+    _require_device(x)
+    in_dim, out_dim, _ = c.shape
+    if x.dim() != 2 or x.shape[1] != in_dim:
+        raise RuntimeError(f"x must be [batch, {in_dim}], got {tuple(x.shape)}")
+    x32 = x.detach().float().contiguous()
+    desc = _derivative_desc(c, x32.shape[0])
+    lib = _lib.load()
+    jac = torch.empty(x32.shape[0], out_dim, in_dim, dtype=torch.float32, device=x.device)
+    ws_bytes = lib.ckan_jacobian_workspace_bytes(desc)
+    ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=x.device)
+    _lib.check(lib.ckan_jacobian(desc, _spec_ref(spec), x32.data_ptr(), c.data_ptr(),
+                                 jac.data_ptr(), ws.data_ptr(), ws_bytes, _lib.stream_ptr(x.device)))
+    return jac

@@ -23,6 +23,7 @@ from typing import Any, Dict, List, Optional, Tuple
 import torch
 import torch.nn as nn
 
+from . import functional as F
 from .basis import BasisFunction, ChebyshevBasis, HermiteBasis, JacobiBasis
 
 
@@ -48,6 +49,41 @@ class KANLayer(nn.Module, ABC):
 
     @abstractmethod
     def get_coefficients(self) -> torch.Tensor: ...
+
+    def _basis_spec(self):
+        spec = getattr(self.basis_function, "spec", None)
+        return spec() if callable(spec) else None
+
+    def _compute_mode(self) -> str:
+        return getattr(self.basis_function, "compute", "fp32")
+
+    def compute_derivatives(self, x: torch.Tensor, order: int = 1) -> torch.Tensor:
+        """[batch, output_dim]: sum over inputs i of the order-th derivative in
+        x_i of each univariate function f_{i,o} (kan/layers/base.py:102-114).
+
+        Divergence: the reference evaluates ChebyshevBasis.derivative, whose
+        coefficients are wrong from degree 3 on and which differentiates in
+        tanh(x) without the chain factor; this returns the exact x-derivative
+        (a Chebyshev series of degree degree + order, so degree + order <= 16)."""
+        check = getattr(self.basis_function, "_check_input_map", None)
+        if callable(check):
+            check()
+        x = x.reshape(-1, self.input_dim)
+        return F.derivatives(x, self.get_coefficients(), self._basis_spec(), order,
+                             self._compute_mode())
+
+    def jacobian(self, x: torch.Tensor) -> torch.Tensor:
+        """[batch, output_dim, input_dim]: d y[b, o] / d x[b, i] (kan/layers/base.py:116-141).
+
+        Divergence: the reference fills column i with compute_derivatives of x
+        with the other inputs zeroed, which adds their derivatives at 0 (and
+        the reference's derivative is itself inexact); this is the exact
+        Jacobian.  Computed in fp32; not differentiable."""
+        check = getattr(self.basis_function, "_check_input_map", None)
+        if callable(check):
+            check()
+        x = x.reshape(-1, self.input_dim)
+        return F.jacobian(x, self.get_coefficients(), self._basis_spec())
 
 
 class ChebyKANLayer(KANLayer):

@@ -1,0 +1,150 @@
+"""GPU parity of KANLayer.compute_derivatives / jacobian (HIP path through the
+C-ABI: ckan_derivative_coeffs + the ChebyKAN forward, ckan_jacobian) against
+the CPU oracle oracle/derivative_oracle.py (fp64 autograd through the
+reference's forward).
+
+Tolerances (norm-wise, ||a - b|| / ||b||):
+  fp32 path:  1e-5 for the derivatives, the Jacobian and their gradients
+  bf16 MFMA path:  2e-2 (the derivative layer's forward in bf16)
+
+Divergence from the reference (documented in kan_amd/layers.py): these are
+the exact x-derivatives; the reference's are not (see the oracle's header).
+"""
+import pytest
+import torch
+
+import kan_amd
+from kan_amd import _lib
+from oracle import derivative_oracle as do
+from oracle import family_oracle as fo
+
+pytestmark = pytest.mark.gpu
+
+FP32_TOL = 1e-5
+BF16_TOL = 2e-2
+
+
+def _rel(a, b):
+    a = a.detach().double().cpu()
+    b = b.detach().double().cpu()
+    n = b.norm().item()
+    return (a - b).norm().item() / (n if n > 0 else 1.0)
+
+
+def _inputs(seed, B, I, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(B, I, generator=g) * scale
+
+
+CHEB_CASES = [
+    # B, I, O, deg, order
+    (64, 16, 12, 4, 1),
+    (300, 40, 24, 8, 1),
+    (300, 40, 24, 8, 2),
+    (128, 32, 20, 5, 3),
+    (1024, 64, 48, 8, 1),    # pipelined forward of the derivative layer (degree 9 -> P = 16)
+    (700, 48, 40, 12, 4),    # degree 16 derivative layer
+]
+
+
+@pytest.mark.parametrize("B,I,O,deg,order", CHEB_CASES)
+def test_chebykan_derivatives_fp32(B, I, O, deg, order):
+    torch.manual_seed(B + deg + order)
+    layer = kan_amd.ChebyKANLayer(I, O, deg).cuda()
+    x = _inputs(order, B, I)
+    got = layer.compute_derivatives(x.cuda(), order=order)
+    ref = do.derivatives(x, layer.cheby_coeffs.detach().cpu(), order)
+    assert got.shape == (B, O)
+    assert _rel(got, ref) <= FP32_TOL
+
+
+@pytest.mark.parametrize("order", [1, 2])
+def test_chebykan_derivatives_bf16(order):
+    B, I, O, deg = 2048, 128, 96, 8
+    torch.manual_seed(7)
+    layer = kan_amd.ChebyKANLayer(I, O, deg, compute="bf16").cuda()
+    x = _inputs(3, B, I)
+    got = layer.compute_derivatives(x.cuda(), order=order)
+    ref = do.derivatives(x, layer.cheby_coeffs.detach().cpu(), order)
+    assert _rel(got, ref) <= BF16_TOL
+
+
+def test_order_zero_is_the_forward():
+    torch.manual_seed(3)
+    layer = kan_amd.ChebyKANLayer(20, 10, 6).cuda()
+    x = _inputs(1, 50, 20).cuda()
+    torch.testing.assert_close(layer.compute_derivatives(x, order=0), layer(x))
+
+
+@pytest.mark.parametrize("B,I,O,deg", [(37, 9, 7, 5), (256, 64, 32, 8), (5, 3, 130, 15)])
+def test_chebykan_jacobian(B, I, O, deg):
+    torch.manual_seed(B)
+    layer = kan_amd.ChebyKANLayer(I, O, deg).cuda()
+    x = _inputs(2, B, I)
+    J = layer.jacobian(x.cuda())
+    ref = do.jacobian(x, layer.cheby_coeffs.detach().cpu())
+    assert J.shape == (B, O, I)
+    assert _rel(J, ref) <= FP32_TOL
+    # its sum over inputs is compute_derivatives(order=1)
+    assert _rel(J.sum(dim=2), layer.compute_derivatives(x.cuda(), 1)) <= FP32_TOL
+
+
+FAMILY_CASES = [
+    ("jacobi", dict(alpha=0.5, beta=-0.25), 1),
+    ("jacobi", dict(alpha=0.0, beta=0.0), 2),
+    ("hermite", dict(scaling="physicist"), 1),
+    ("hermite_e", dict(scaling="probabilist"), 2),
+]
+
+
+@pytest.mark.parametrize("family,kw,order", FAMILY_CASES)
+def test_family_derivatives_and_jacobian(family, kw, order):
+    B, I, O, deg = 300, 24, 20, 6
+    torch.manual_seed(11 + order)
+    if family == "jacobi":
+        layer = kan_amd.JacobiKANLayer(I, O, deg, **kw).cuda()
+        fwd = lambda xx, cc: fo.family_forward(xx, cc, "jacobi", kw["alpha"], kw["beta"])
+    else:
+        layer = kan_amd.HermiteKANLayer(I, O, deg, **kw).cuda()
+        fwd = lambda xx, cc: fo.family_forward(xx, cc, family)
+    c = layer.get_coefficients().detach().cpu()
+    x = _inputs(4, B, I, scale=0.8)
+    got = layer.compute_derivatives(x.cuda(), order=order)
+    assert _rel(got, do.derivatives(x, c, order, fwd)) <= FP32_TOL
+    assert _rel(layer.jacobian(x.cuda()), do.jacobian(x, c, fwd)) <= FP32_TOL
+
+
+def test_derivatives_are_differentiable():
+    """d/dC and d/dx of a loss of compute_derivatives (the physics-informed use)."""
+    B, I, O, deg = 200, 16, 12, 6
+    torch.manual_seed(5)
+    layer = kan_amd.ChebyKANLayer(I, O, deg).cuda()
+    x = _inputs(6, B, I)
+    w = torch.randn(B, O)
+    xd = x.cuda().requires_grad_(True)
+    (layer.compute_derivatives(xd, order=2) * w.cuda()).sum().backward()
+    xr = x.double().requires_grad_(True)
+    cr = layer.cheby_coeffs.detach().cpu().double().requires_grad_(True)
+    yr = do.chebykan_forward64(xr, cr)
+    d2 = torch.stack([torch.autograd.grad(
+        torch.autograd.grad(yr[:, o].sum(), xr, create_graph=True)[0].sum(), xr,
+        create_graph=True)[0].sum(1) for o in range(O)], 1)
+    (d2 * w.double()).sum().backward()
+    assert _rel(layer.cheby_coeffs.grad, cr.grad) <= FP32_TOL
+    assert _rel(xd.grad, xr.grad) <= FP32_TOL
+
+
+def test_derivative_errors():
+    layer = kan_amd.ChebyKANLayer(8, 4, 14).cuda()
+    x = torch.randn(10, 8, device="cuda")
+    with pytest.raises(_lib.CkanError) as e:
+        layer.compute_derivatives(x, order=3)  # degree 17 derivative layer
+    assert e.value.code == _lib.CKAN_ERR_UNSUPPORTED
+    with pytest.raises(ValueError):
+        layer.compute_derivatives(x, order=-1)
+    with pytest.raises(_lib.CkanError) as e:  # the order-1 series of degree 17
+        kan_amd.ChebyKANLayer(8, 4, 16).cuda().jacobian(x)
+    assert e.value.code == _lib.CKAN_ERR_UNSUPPORTED
+    layer64 = kan_amd.ChebyKANLayer(8, 4, 3).cuda().double()
+    with pytest.raises(RuntimeError):
+        layer64.compute_derivatives(x.double(), order=1)
