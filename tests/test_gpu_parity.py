@@ -63,6 +63,8 @@ SHAPES = [
     (96, 48, 40, 9),
     (200, 72, 50, 15),
     (256, 128, 64, 16),
+    (1000, 100, 150, 6),  # pipelined forward: ragged rows, padded inputs, partial tiles
+    (777, 40, 300, 12),   # the same at degree 16 (P = 16)
 ]
 
 
