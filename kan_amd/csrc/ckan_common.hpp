@@ -236,8 +236,8 @@ __device__ __forceinline__ void dma16(const void* src, void* lds_base) {
 // A vector memory instruction that reads an SGPR written by a VALU
 // instruction (v_readfirstlane here) needs 5 wait states in between on this
 // GPU generation, or it reads the SGPR's previous contents.  The compiler's
-// hazard pass does not look inside inline assembly, so each asm block below
-// supplies the 5 itself (s_mov counts as one, s_nop N as N + 1).
+// hazard pass does not look inside inline assembly, so dma16s supplies the 5
+// itself (s_mov counts as one, s_nop N as N + 1).
 __device__ __forceinline__ void dma16s(const void* sbase, uint32_t voff, uint32_t lds) {
   const uint64_t a = (uint64_t)(uintptr_t)sbase;
   const uint64_t s = ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32)) << 32) |
@@ -259,28 +259,6 @@ __device__ __forceinline__ void dma16s_salu(const void* sbase, uint32_t voff, ui
   const uint32_t l = __builtin_amdgcn_readfirstlane(lds);
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
                :: "v"(voff), "s"(s), "s"(l) : "memory", "m0");
-}
-
-// 16-byte register load in saddr form (wave-uniform SGPR base + per-lane
-// 32-bit offset, 5 wait states after the base's readfirstlane as for dma16s),
-// hidden from the compiler's wait-count pass like dma16s: the
-// caller waits for it with wait_vmcnt_regs, which names the destination
-// registers, before any use of the value.  Loads and LDS copies retire from
-// vmcnt in issue order.
-__device__ __forceinline__ f32x4_t gload16s(const void* sbase, uint32_t voff) {
-  const uint64_t a = (uint64_t)(uintptr_t)sbase;
-  const uint64_t s = ((uint64_t)__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32)) << 32) |
-                     (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)a);
-  f32x4_t v;
-  asm volatile("s_nop 4\n\tglobal_load_dwordx4 %0, %1, %2" : "=v"(v) : "v"(voff), "s"(s) : "memory");
-  return v;
-}
-// s_waitcnt vmcnt(N) that also marks a and b as written there, so the
-// compiler reads the registers of an earlier gload16s only after the wait.
-template <int N>
-__device__ __forceinline__ void wait_vmcnt_regs(f32x4_t& a, f32x4_t& b) {
-  static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit field");
-  asm volatile("s_waitcnt vmcnt(%2)" : "+v"(a), "+v"(b) : "n"(N) : "memory");
 }
 
 // Makes a wave-uniform value (a kernel argument) live in SGPRs from here on.

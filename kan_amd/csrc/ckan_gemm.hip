@@ -246,16 +246,13 @@ struct FwdPipe {
   typedef typename Elem<BF>::type E;
   typedef FwdGroup<P> G;
   static constexpr int NM = 2, NN = 4, BM = 256, BNF = 4, THREADS = 512;
-  // TR: each lane's tanh values of a super-group are one 16-byte run of its
-  // row, loaded straight into registers one super-group ahead (no LDS tile).
-  static constexpr bool TR = G::LANE_T == 4;
   static constexpr int B_BYTES = BNF * G::SGK * kFragElems * (int)sizeof(E);
-  static constexpr int T_BYTES = TR ? 0 : BM * G::SGI * 4;
+  static constexpr int T_BYTES = BM * G::SGI * 4;
   static constexpr int STAGE_BYTES = B_BYTES + T_BYTES;
   static constexpr int PAIR_BYTES = 2 * STAGE_BYTES;
   static constexpr int RED_BYTES = BM * BNF * 32 * 4;  // one partial tile, fp32
   static constexpr int NPB_FIT = (160 * 1024) / PAIR_BYTES;
-  static constexpr int NPB = NPB_FIT > 3 ? 3 : NPB_FIT;  // the TR waits assume NPB <= 3
+  static constexpr int NPB = NPB_FIT > 3 ? 3 : NPB_FIT;
   static constexpr int RING_BYTES = NPB * PAIR_BYTES;
   static constexpr int LDS_BYTES = RING_BYTES > RED_BYTES + 16 ? RING_BYTES : RED_BYTES + 16;
   // dma16 ops per thread per stage (each op moves 512 x 16 bytes per block)
@@ -318,7 +315,7 @@ k_fwd_pipe(const float* __restrict__ tc, const typename Elem<BF>::type* __restri
     boff[q] = (uint32_t)((size_t)(nb - nb0) * p.KB * kFragElems * sizeof(E) + (size_t)off * 16);
   }
   const char* tbase = reinterpret_cast<const char*>(tc) + (size_t)m_blk * p.I_sg * 4;
-  uint32_t toff[HT_OPS > 0 ? HT_OPS : 1];
+  uint32_t toff[HT_OPS];
 #pragma unroll
   for (int q = 0; q < HT_OPS; ++q) {
     const int c = (q * 4 + wq) * 64 + lane;
@@ -330,22 +327,6 @@ k_fwd_pipe(const float* __restrict__ tc, const typename Elem<BF>::type* __restri
   const size_t b_stride = (size_t)G::SGK * kFragElems * sizeof(E);
   const size_t t_stride = (size_t)G::SGI * 4;
   const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
-  // TR: lane (row, g) of fragment row block mi reads the 4 tanh values
-  // 4g .. 4g + 3 of its row's super-group (rows past B read row B - 1).
-  uint32_t troff[NM];
-#pragma unroll
-  for (int mi = 0; mi < NM; ++mi) {
-    int64_t r = m_blk + (wq * NM + mi) * 32 + (lane & 31);
-    if (r >= p.B) r = p.B - 1;
-    troff[mi] = (uint32_t)(((size_t)(r - m_blk) * p.I_sg + g * 4) * 4);
-  }
-  // every wave loads its next super-group's tanh values whether or not it
-  // computes one, so that its vmcnt waits count the same operations
-  auto tload = [&](int sg, f32x4_t (&dst)[NM]) __attribute__((always_inline)) {
-    const char* b = tbase + (size_t)min(sg, nsg - 1) * t_stride;
-#pragma unroll
-    for (int mi = 0; mi < NM; ++mi) dst[mi] = gload16s(b, troff[mi]);
-  };
 
   // stage `sg` (if it exists) into ring slot `slot` (0 .. 2*NPB-1); half 0 only
   auto issue = [&](int sg, int slot) __attribute__((always_inline)) {
@@ -377,29 +358,22 @@ k_fwd_pipe(const float* __restrict__ tc, const typename Elem<BF>::type* __restri
   // fragments of the next sub-step generated (VALU) while the MFMAs of
   // k-block k run; scheduling barriers keep that order and interleave the
   // generation with the MFMAs.
-  auto compute = [&](int slot, const f32x4_t (&treg)[NM]) __attribute__((always_inline)) {
+  auto compute = [&](int slot) __attribute__((always_inline)) {
     const char* base = smem + slot * K::STAGE_BYTES;
+    const float* tl = reinterpret_cast<const float*>(base + K::B_BYTES);
     const E* bl = reinterpret_cast<const E*>(base);
     constexpr int SGK = G::SGK, KBG = G::KBG;
     float tv[NM][G::LANE_T];
-    if constexpr (K::TR) {
 #pragma unroll
-      for (int mi = 0; mi < NM; ++mi)
+    for (int mi = 0; mi < NM; ++mi) {
+      const int rl = (wq * NM + mi) * 32 + (lane & 31);
+      const f32x4_t* src = reinterpret_cast<const f32x4_t*>(tl + rl * G::SGI);
+      const int sx = fwd_t_xor<G::SGI / 4>(rl);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) tv[mi][q] = treg[mi][q];
-    } else {
-      const float* tl = reinterpret_cast<const float*>(base + K::B_BYTES);
-#pragma unroll
-      for (int mi = 0; mi < NM; ++mi) {
-        const int rl = (wq * NM + mi) * 32 + (lane & 31);
-        const f32x4_t* src = reinterpret_cast<const f32x4_t*>(tl + rl * G::SGI);
-        const int sx = fwd_t_xor<G::SGI / 4>(rl);
-#pragma unroll
-        for (int q = 0; q < G::LANE_T / 4; ++q) {
-          const f32x4_t w = src[(g * (G::LANE_T / 4) + q) ^ sx];
-          tv[mi][4 * q + 0] = w[0]; tv[mi][4 * q + 1] = w[1];
-          tv[mi][4 * q + 2] = w[2]; tv[mi][4 * q + 3] = w[3];
-        }
+      for (int q = 0; q < G::LANE_T / 4; ++q) {
+        const f32x4_t w = src[(g * (G::LANE_T / 4) + q) ^ sx];
+        tv[mi][4 * q + 0] = w[0]; tv[mi][4 * q + 1] = w[1];
+        tv[mi][4 * q + 2] = w[2]; tv[mi][4 * q + 3] = w[3];
       }
     }
     Frag<BF> bq[2][NN];
@@ -453,52 +427,22 @@ k_fwd_pipe(const float* __restrict__ tc, const typename Elem<BF>::type* __restri
   pin_sgpr(y);  // used after the loop
   pin_sgpr(part);
   pin_sgpr(bias_f);
-  f32x4_t tcur[NM], tnext[NM];
-  if constexpr (!K::TR) {
+  if (half == 0) {
+#pragma unroll
+    for (int j = 0; j < NPB - 1; ++j)
+      if (j < npair) issue_pair(j);
+  }
+  for (int j = 0; j < npair; ++j) {
+    // half 0: pair j has landed once only the copies of pairs j+1 .. j+NPB-2
+    // (HOPS each) remain; only the last pair can be a single stage, so near
+    // the end wait for all.  The barrier publishes the copies to half 1.
     if (half == 0) {
-#pragma unroll
-      for (int j = 0; j < NPB - 1; ++j)
-        if (j < npair) issue_pair(j);
+      if (j + NPB - 2 < npair - 1) wait_vmcnt<HOPS * (NPB - 2)>();
+      else wait_vmcnt<0>();
     }
-    for (int j = 0; j < npair; ++j) {
-      // half 0: pair j has landed once only the copies of pairs j+1 .. j+NPB-2
-      // (HOPS each) remain; only the last pair can be a single stage, so near
-      // the end wait for all.  The barrier publishes the copies to half 1.
-      if (half == 0) {
-        if (j + NPB - 2 < npair - 1) wait_vmcnt<HOPS * (NPB - 2)>();
-        else wait_vmcnt<0>();
-      }
-      block_barrier();
-      if (sg0 + 2 * j + half < sg1) compute((j % NPB) * 2 + half, tcur);
-      if (half == 0 && j + NPB - 1 < npair) issue_pair(j + NPB - 1);
-    }
-  } else {
-    static_assert(NPB == 2 || NPB == 3, "the waits below count NPB <= 3");
-    // Each wave's tanh values for iteration j are loaded into tnext right
-    // after the barrier of iteration j - 1, and waited for (naming tnext) at
-    // the top of iteration j, before they are copied to tcur.  Half 0's vm
-    // queue, in issue order: ... pair j, t(j), pair j + NPB - 2, t(j + 1) ...;
-    // so pair j and t(j) have landed once only pair j + NPB - 2 (HOPS copies)
-    // remains, which is pair j + 1 for NPB = 3 and nothing for NPB = 2.
-    // Half 1 issues only its tanh loads.
-    if (half == 0) {
-#pragma unroll
-      for (int j = 0; j < NPB - 2; ++j)
-        if (j < npair) issue_pair(j);
-    }
-    tload(sg0 + half, tnext);
-    if (half == 0 && NPB - 2 < npair) issue_pair(NPB - 2);
-    for (int j = 0; j < npair; ++j) {
-      if (half == 0 && j + NPB - 2 < npair - 1) wait_vmcnt_regs<HOPS * (NPB - 2)>(tnext[0], tnext[1]);
-      else wait_vmcnt_regs<0>(tnext[0], tnext[1]);
-      block_barrier();
-#pragma unroll
-      for (int mi = 0; mi < NM; ++mi) tcur[mi] = tnext[mi];
-      tload(sg0 + 2 * (j + 1) + half, tnext);
-      if (sg0 + 2 * j + half < sg1) compute((j % NPB) * 2 + half, tcur);
-      if (half == 0 && j + NPB - 1 < npair) issue_pair(j + NPB - 1);
-    }
-    wait_vmcnt_regs<0>(tnext[0], tnext[1]);  // the last (unused) loads land before exit
+    block_barrier();
+    if (sg0 + 2 * j + half < sg1) compute((j % NPB) * 2 + half);
+    if (half == 0 && j + NPB - 1 < npair) issue_pair(j + NPB - 1);
   }
 
   // Sum the two halves' tiles through LDS (the ring is free once all waves
@@ -898,26 +842,32 @@ k_dx_dh(const typename Elem<BF>::type* __restrict__ dYx,
   const int nst = p.KBx / KI;
   const int rb = blockIdx.x % n_rb, ib = blockIdx.x / n_rb;
 
-  // DMA: waves 0-3 issue every copy of a stage, HOPS per thread; chunk
-  // c = q*256 + tid lands at byte 16*c of the stage (dy rows first, then the
-  // coefficient fragments).  Sources: a wave-uniform base (block operand +
-  // stage) and a per-lane 32-bit offset; dYx rows are padded to whole row blocks.
+  // DMA: the copies of a stage are HOPS per thread of one 256-thread half,
+  // chunk c = q*256 + (tid & 255) landing at byte 16*c of the stage (dy rows
+  // first, then the coefficient fragments).  Waves 0-3 issue q < H0, waves
+  // 4-7 the rest (see the loop for when).  Sources: a wave-uniform base (block
+  // operand + stage) and a per-lane 32-bit offset; dYx rows are padded to
+  // whole row blocks.
   constexpr int RG = K::RG, THR = K::THR;
   static_assert(THR == 512, "launch bounds");
   constexpr int HOPS = 2 * OPS, HA_OPS = 2 * K::A_OPS;
+  constexpr int H0 = HOPS / 2, H1 = HOPS - H0;  // copies per thread of waves 0-3 / 4-7
   const char* abase = reinterpret_cast<const char*>(dYx) + (size_t)rb * RG * NM * p.KBx * FB;
   const char* bbase = reinterpret_cast<const char*>(Cb) + (size_t)ib * P * p.KBx * FB;
-  uint32_t off[HOPS];
+  const int hw = __builtin_amdgcn_readfirstlane(wave) >> 2;  // 0: waves 0-3, 1: waves 4-7
+  const int q0 = hw ? H0 : 0, nq = hw ? H1 : H0;
+  uint32_t off[H1];
 #pragma unroll
-  for (int q = 0; q < HOPS; ++q) {
+  for (int qi = 0; qi < H1; ++qi) {
+    const int q = q0 + qi;
     const int c = q * 256 + (tid & 255);
     if (q < HA_OPS) {
       const int run = c / RUN, w = c - run * RUN;
-      off[q] = (uint32_t)((size_t)run * p.KBx * FB + w * 16);
+      off[qi] = (uint32_t)((size_t)run * p.KBx * FB + w * 16);
     } else {
       const int cc = c - HA_OPS * 256;
       const int e = cc / RUN, w = cc - e * RUN;
-      off[q] = (uint32_t)((size_t)e * p.KBx * FB + w * 16);
+      off[qi] = (uint32_t)((size_t)e * p.KBx * FB + w * 16);
     }
   }
   const uint32_t lds0 = (uint32_t)(uintptr_t)smem + (uint32_t)__builtin_amdgcn_readfirstlane(wave & 3) * 1024;
@@ -926,7 +876,9 @@ k_dx_dh(const typename Elem<BF>::type* __restrict__ dYx,
     const size_t sb = (size_t)st * KI * FB;
     const uint32_t l = lds0 + (st % NBUF) * K::STAGE_BYTES;
 #pragma unroll
-    for (int q = 0; q < HOPS; ++q) dma16s_salu((q < HA_OPS ? abase : bbase) + sb, off[q], l + q * 4096);
+    for (int qi = 0; qi < H1; ++qi)
+      if (qi < nq)
+        dma16s_salu((q0 + qi < HA_OPS ? abase : bbase) + sb, off[qi], l + (q0 + qi) * 4096);
   };
 
   // epilogue tanh values, loaded up front (they complete long before use)
@@ -951,17 +903,21 @@ k_dx_dh(const typename Elem<BF>::type* __restrict__ dYx,
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[mi][e][v] = 0.0f;
 
-  // Waves 0-3 copy stage st + NBUF - 1 after their MFMAs of stage st, while
-  // waves 4-7 (the younger wave of each SIMD, issued second) still run theirs.
-  // Its slot was last read in stage st - 1, before this stage's barrier.
-  const bool copier = wave < 4;
+  // The copies of stage st + NBUF - 1 are split between the two waves of each
+  // SIMD and issued apart in time: waves 4-7 (the younger wave of a SIMD,
+  // issued second) right after their fragment reads of stage st, while waves
+  // 0-3 run their MFMAs; waves 0-3 after their MFMAs, while waves 4-7 still run
+  // theirs.  A copy stalls its wave while the CU's address unit takes it, so
+  // neither wave carries all of a stage's copies.  The slot was last read in
+  // stage st - 1, whose reads every wave completed before this stage's
+  // barrier.  Each wave waits only for its own copies (vmcnt).
   pin_sgpr(dx);  // used after the loop
-  if (copier) {
 #pragma unroll
-    for (int q = 0; q < NBUF - 1; ++q) issue(q);
-  }
+  for (int q = 0; q < NBUF - 1; ++q) issue(q);
   for (int st = 0; st < nst; ++st) {
-    if (copier) wait_vmcnt<HOPS * (NBUF - 2)>();  // stage st landed (st+1 may be in flight)
+    // stage st landed (this wave's copies of st+1 may be in flight)
+    if (hw) wait_vmcnt<H1 * (NBUF - 2)>();
+    else wait_vmcnt<H0 * (NBUF - 2)>();
     block_barrier();
     const char* base = smem + (st % NBUF) * K::STAGE_BYTES;
     // all reads first, in k-block order; the MFMAs of k-block kk wait only for
@@ -977,6 +933,8 @@ k_dx_dh(const typename Elem<BF>::type* __restrict__ dYx,
         fb[kk][e] = load_frag<BF>(reinterpret_cast<const E*>(base + K::A_BYTES + ((dh * PH + e) * KI + kk) * FB), lane);
       __builtin_amdgcn_sched_barrier(0);
     }
+    if (hw) issue(st + NBUF - 1);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int kk = 0; kk < KI; ++kk) {
 #pragma unroll
@@ -985,7 +943,7 @@ k_dx_dh(const typename Elem<BF>::type* __restrict__ dYx,
         for (int e = 0; e < PH; ++e) mma(acc[mi][e], fa[kk][mi], fb[kk][e]);
       __builtin_amdgcn_sched_barrier(0);
     }
-    if (copier) issue(st + NBUF - 1);
+    if (!hw) issue(st + NBUF - 1);
   }
   wait_vmcnt<0>();
   wait_lgkmcnt<0>();
