@@ -547,35 +547,52 @@ k_fwd_stream(const float* __restrict__ x, float* __restrict__ tc,
   const int nsg = p.I_sg / G::SGI;
   const int sg0 = (blk * K::WAVES + wave) * SPW;
 
-  // every load of this wave, in flight together
+  // every load of this wave, in flight together: its rows of x first, so
+  // that tanh and the basis (which need only x) can run while the
+  // coefficient fragments are still streaming in (vector loads retire in
+  // issue order, so each MFMA then waits only for its own fragment).  The
+  // loads are unconditional, from clamped in-range addresses; values past B,
+  // I or the last super-group are zeroed only after every load is issued (a
+  // use of a loaded value between the loads made the compiler wait for it).
+  float xv[NMS][SPW][LT];
+  const bool xvec = xal && (p.I & 3) == 0;  // LT is a multiple of 4, so are the lane offsets
+  f32x4_t xraw[NMS][SPW][LT / 4];
+#pragma unroll
+  for (int mi = 0; mi < NMS; ++mi) {
+    const int r = mi * 32 + (lane & 31);
+    const float* xr = x + (size_t)(r < p.B ? r : (int)p.B - 1) * p.I;
+#pragma unroll
+    for (int j = 0; j < SPW; ++j) {
+      const int i0 = (sg0 + j) * G::SGI + g * LT;
+#pragma unroll
+      for (int q = 0; q < LT; q += 4) {
+        if (xvec) {  // I % 4 == 0: a float4 is all in or all out
+          xraw[mi][j][q / 4] = *reinterpret_cast<const f32x4_t*>(xr + (i0 + q + 4 <= p.I ? i0 + q : p.I - 4));
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) xraw[mi][j][q / 4][e] = xr[min(i0 + q + e, p.I - 1)];
+        }
+      }
+    }
+  }
   Frag<BF> bfr[KPW];
 #pragma unroll
   for (int q = 0; q < KPW; ++q) {
-    const int sg = sg0 + q / G::SGK;
-    bfr[q] = (sg < nsg)
-        ? load_frag<BF>(Cf + ((size_t)nb * p.KB + (size_t)sg0 * G::SGK + q) * kFragElems, lane)
-        : zero_frag<BF>();
+    const int sg = min(sg0 + q / G::SGK, nsg - 1);
+    bfr[q] = load_frag<BF>(Cf + ((size_t)nb * p.KB + (size_t)sg * G::SGK + q % G::SGK) * kFragElems, lane);
   }
-  float xv[NMS][SPW][LT];
-  const bool xvec = xal && (p.I & 3) == 0;  // LT is a multiple of 4, so are the lane offsets
+#pragma unroll
+  for (int q = 0; q < KPW; ++q)
+    if (sg0 + q / G::SGK >= nsg) bfr[q] = zero_frag<BF>();
 #pragma unroll
   for (int mi = 0; mi < NMS; ++mi) {
     const int r = mi * 32 + (lane & 31);
 #pragma unroll
     for (int j = 0; j < SPW; ++j) {
       const int i0 = (sg0 + j) * G::SGI + g * LT;
-      const float* xr = x + (size_t)r * p.I + i0;
 #pragma unroll
-      for (int q = 0; q < LT; q += 4) {
-        if (r < p.B && xvec && i0 + q + 4 <= p.I) {
-          const f32x4_t w = *reinterpret_cast<const f32x4_t*>(xr + q);
-          xv[mi][j][q] = w[0]; xv[mi][j][q + 1] = w[1]; xv[mi][j][q + 2] = w[2]; xv[mi][j][q + 3] = w[3];
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            xv[mi][j][q + e] = (r < p.B && i0 + q + e < p.I) ? xr[q + e] : 0.0f;
-        }
-      }
+      for (int q = 0; q < LT; ++q)
+        xv[mi][j][q] = (r < p.B && i0 + q < p.I) ? xraw[mi][j][q / 4][q % 4] : 0.0f;
     }
   }
   f32x16_t acc[NMS];
