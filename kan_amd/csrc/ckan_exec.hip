@@ -165,7 +165,12 @@ struct ckan_exec {
   // graph mode
   hipStream_t es = nullptr;
   hipEvent_t ev_in = nullptr, ev_out = nullptr;
-  hipGraphExec_t graph = nullptr;
+  hipGraphExec_t graph = nullptr;         // captured on the executor-owned input buffers
+  hipGraphExec_t graph_direct = nullptr;  // captured on the caller's x / target (gd_x, gd_t)
+  const void* gd_x = nullptr;
+  const void* gd_t = nullptr;
+  const void* last_x = nullptr;           // the previous step's input pointers
+  const void* last_t = nullptr;
   float* x_own = nullptr;
   void* tgt_own = nullptr;
   size_t tgt_bytes = 0;
@@ -188,6 +193,7 @@ int dev_alloc(ckan_exec* ex, void** p, size_t bytes) {
 
 void free_all(ckan_exec* ex) {
   if (ex->graph) hipGraphExecDestroy(ex->graph);
+  if (ex->graph_direct) hipGraphExecDestroy(ex->graph_direct);
   if (ex->ev_in) hipEventDestroy(ex->ev_in);
   if (ex->ev_out) hipEventDestroy(ex->ev_out);
   if (ex->es) hipStreamDestroy(ex->es);
@@ -437,32 +443,56 @@ int ckan_exec_step(ckan_exec* ex, const float* x, const void* target, float* los
       return efail(CKAN_ERR_HIP, "executor: loss copy failed");
     return CKAN_OK;
   }
-  // graph mode: inputs staged into executor-owned buffers outside the graph;
-  // the graph (captured once on the executor's stream) is replayed on `stream`
-  const size_t xb = (size_t)ex->cfg.batch * ex->widths[0] * 4;
-  if (!copy(ex->x_own, x, xb, s) || !copy(ex->tgt_own, target, ex->tgt_bytes, s))
-    return efail(CKAN_ERR_HIP, "executor: input staging failed");
-  if (!ex->graph) {
-    // capture on the executor's own stream, ordered after the staging copies
+  // graph mode.  The graph is captured once on the executor's own stream and
+  // replayed on `stream`.  A step whose x and target pointers are those of
+  // the step before replays a graph captured on those buffers (the usual
+  // training loop reuses them; the graph reads whatever they hold when it
+  // runs); otherwise the inputs are first copied into executor-owned buffers
+  // and a graph captured on those is replayed (two small copy kernels more).
+  auto capture = [&](const float* cx, const void* ct, hipGraphExec_t* out) -> int {
     if (hipEventRecord(ex->ev_in, s) != hipSuccess || hipStreamWaitEvent(ex->es, ex->ev_in, 0) != hipSuccess)
       return efail(CKAN_ERR_HIP, "executor: stream ordering failed");
     hipGraph_t g = nullptr;
     if (hipStreamBeginCapture(ex->es, hipStreamCaptureModeThreadLocal) != hipSuccess)
       return efail(CKAN_ERR_HIP, "executor: graph capture failed to start");
-    rc = run_step(ex, ex->x_own, ex->tgt_own, ex->es);
+    const int rc2 = run_step(ex, cx, ct, ex->es);
     const hipError_t ec = hipStreamEndCapture(ex->es, &g);
-    if (rc) {
+    if (rc2) {
       if (g) hipGraphDestroy(g);
-      return rc;
+      return rc2;
     }
-    if (ec != hipSuccess || hipGraphInstantiate(&ex->graph, g, nullptr, nullptr, 0) != hipSuccess) {
+    if (ec != hipSuccess || hipGraphInstantiate(out, g, nullptr, nullptr, 0) != hipSuccess) {
       if (g) hipGraphDestroy(g);
       return efail(CKAN_ERR_HIP, "executor: graph capture failed");
     }
     hipGraphDestroy(g);
+    return CKAN_OK;
+  };
+  const bool repeat = x == ex->last_x && target == ex->last_t;
+  ex->last_x = x;
+  ex->last_t = target;
+  if (repeat) {
+    if (ex->graph_direct && (ex->gd_x != x || ex->gd_t != target)) {
+      // a graph on other buffers: let its replays finish before it goes
+      if (hipStreamSynchronize(s) != hipSuccess) return efail(CKAN_ERR_HIP, "executor: sync failed");
+      hipGraphExecDestroy(ex->graph_direct);
+      ex->graph_direct = nullptr;
+    }
+    if (!ex->graph_direct) {
+      if ((rc = capture(x, target, &ex->graph_direct))) return rc;
+      ex->gd_x = x;
+      ex->gd_t = target;
+    }
+    if (hipGraphLaunch(ex->graph_direct, s) != hipSuccess)
+      return efail(CKAN_ERR_HIP, "executor: graph launch failed");
+  } else {
+    const size_t xb = (size_t)ex->cfg.batch * ex->widths[0] * 4;
+    if (!copy(ex->x_own, x, xb, s) || !copy(ex->tgt_own, target, ex->tgt_bytes, s))
+      return efail(CKAN_ERR_HIP, "executor: input staging failed");
+    if (!ex->graph && (rc = capture(ex->x_own, ex->tgt_own, &ex->graph))) return rc;
+    if (hipGraphLaunch(ex->graph, s) != hipSuccess)
+      return efail(CKAN_ERR_HIP, "executor: graph launch failed");
   }
-  if (hipGraphLaunch(ex->graph, s) != hipSuccess)
-    return efail(CKAN_ERR_HIP, "executor: graph launch failed");
   if (loss_out && !copy(loss_out, ex->loss, 4, s))
     return efail(CKAN_ERR_HIP, "executor: loss copy failed");
   return CKAN_OK;

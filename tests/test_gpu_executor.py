@@ -110,3 +110,33 @@ def test_executor_forward_matches_layers():
     y_ref = orc.mlp_forward(x, [m.cheby_coeffs.detach() for m in seq])
     assert _rel(y, y_ref) <= 1e-5
     ex.close()
+
+
+def test_graph_steps_follow_the_callers_buffers():
+    """Graph mode replays a graph captured on the caller's x / target when they
+    are the previous step's buffers, and stages inputs otherwise: switching
+    buffers and rewriting one in place must give the eager executor's losses."""
+    from kan_amd import ResidentExecutor
+    print("executor graph buffer switching", flush=True)
+    widths, degrees, B = [48, 32, 10], [4, 3], 128
+    g = torch.Generator().manual_seed(8)
+    xa, xb = torch.randn(B, 48, generator=g).cuda(), torch.randn(B, 48, generator=g).cuda()
+    la, lb = torch.randint(0, 10, (B,), generator=g).cuda(), torch.randint(0, 10, (B,), generator=g).cuda()
+    coeffs = _make(widths, degrees, 12)
+    exs = [ResidentExecutor(widths, degrees, B, compute="fp32", loss="ce", optimizer="sgd", lr=0.05,
+                            use_graph=ug) for ug in (False, True)]
+    for ex in exs:
+        for l, c in enumerate(coeffs):
+            ex.set_coeffs(l, c)
+    plan = [(xa, la), (xa, la), (xa, la), (xb, lb), (xb, lb), (xa, la), (xa, la)]
+    for k, (x, lab) in enumerate(plan):
+        if k == 2:
+            xa.mul_(0.5)  # same buffer, new contents
+        if k == 6:
+            xa.add_(0.25)
+        eager, graph = (ex.step(x, lab).item() for ex in exs)
+        assert eager == graph, (k, eager, graph)
+    for l in range(2):
+        assert torch.equal(exs[0].get_coeffs(l), exs[1].get_coeffs(l))
+    for ex in exs:
+        ex.close()
