@@ -170,7 +170,7 @@ int ckan_forward(const ckan_desc* desc, const float* x, const void* packed, floa
     return fail(CKAN_ERR_WORKSPACE, "forward workspace too small: %zu < %zu bytes", ws_bytes, need);
   if (need && !ws) return fail(CKAN_ERR_INVALID_ARG, "workspace is NULL");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  if (!fwd_streaming(c)) {  // the streaming kernel computes tanh itself
+  if (fwd_reads_tcache(c)) {
     ProfScope ps("tanh", s);
     launch_tanh(x, t_cache, p, s);
   }

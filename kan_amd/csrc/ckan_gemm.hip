@@ -519,8 +519,10 @@ k_fwd_pipe(const float* __restrict__ tc, const typename Elem<BF>::type* __restri
 // takes one 32-output column block and SPW super-groups (16 k-blocks) of the
 // reduction and issues all of its loads at once: the coefficient fragments
 // straight into registers (one coalesced 1 KiB wave load per fragment, no
-// LDS) and its rows of x.  It computes tanh itself (writing the tanh cache
-// from the blocks of column block 0), builds its basis fragments, and
+// LDS) and its rows of x.  With up to 32 rows it computes tanh itself
+// (writing the tanh cache from the blocks of column block 0); with 33..64
+// (TPRE) it reads the cache written by launch_tanh instead, since every
+// column block needs the same values.  It builds its basis fragments, and
 // accumulates NMS x 32 rows.  The 4 waves of a block reduce through LDS and
 // write one partial tile; k_fwd_reduce adds the partials in order.
 // ---------------------------------------------------------------------------
@@ -531,7 +533,7 @@ template <int P, bool BF> struct FwdStream {
   static constexpr int WAVES = 4;
 };
 
-template <int P, bool BF, int NMS>
+template <int P, bool BF, int NMS, bool TPRE>
 __global__ void __launch_bounds__(256)
 k_fwd_stream(const float* __restrict__ x, float* __restrict__ tc,
              const typename Elem<BF>::type* __restrict__ Cf, float* __restrict__ part, Plan p,
@@ -557,6 +559,21 @@ k_fwd_stream(const float* __restrict__ x, float* __restrict__ tc,
   float xv[NMS][SPW][LT];
   const bool xvec = xal && (p.I & 3) == 0;  // LT is a multiple of 4, so are the lane offsets
   f32x4_t xraw[NMS][SPW][LT / 4];
+  if constexpr (TPRE) {
+    // the tanh values come from the cache (pitch I_sg, zero past I): one
+    // 16-byte load each, rows past B clamped and zeroed below
+#pragma unroll
+    for (int mi = 0; mi < NMS; ++mi) {
+      const int r = mi * 32 + (lane & 31);
+      const float* tr = tc + (size_t)(r < p.B ? r : (int)p.B - 1) * p.I_sg;
+#pragma unroll
+      for (int j = 0; j < SPW; ++j) {
+        const int i0 = min(sg0 + j, nsg - 1) * G::SGI + g * LT;
+#pragma unroll
+        for (int q = 0; q < LT; q += 4) xraw[mi][j][q / 4] = *reinterpret_cast<const f32x4_t*>(tr + i0 + q);
+      }
+    }
+  } else
 #pragma unroll
   for (int mi = 0; mi < NMS; ++mi) {
     const int r = mi * 32 + (lane & 31);
@@ -609,8 +626,8 @@ k_fwd_stream(const float* __restrict__ x, float* __restrict__ tc,
       const int sg = sg0 + j;
       float tv[LT];
 #pragma unroll
-      for (int q = 0; q < LT; ++q) tv[q] = tanhf(xv[mi][j][q]);
-      if (nb == 0 && r < p.B && sg < nsg) {  // the tanh cache, written once
+      for (int q = 0; q < LT; ++q) tv[q] = TPRE ? xv[mi][j][q] : tanhf(xv[mi][j][q]);
+      if (!TPRE && nb == 0 && r < p.B && sg < nsg) {  // the tanh cache, written once
         f32x4_t* dst = reinterpret_cast<f32x4_t*>(tc + (size_t)r * p.I_sg + (size_t)sg * G::SGI + g * LT);
 #pragma unroll
         for (int q = 0; q < LT / 4; ++q)
@@ -1759,9 +1776,9 @@ static void fwd_dispatch(const float* x, float* t, const void* packed, float* y,
   if (fwd_streaming(c)) {
     dim3 g1(c.tiles_n * c.splits);
     if (c.tile == kFwdStream32)
-      hipLaunchKernelGGL((k_fwd_stream<P, BF, 1>), g1, dim3(256), 0, s, x, t, Cf, part, p, c.splits, (int)is_al16(x));
-    else
-      hipLaunchKernelGGL((k_fwd_stream<P, BF, 2>), g1, dim3(256), 0, s, x, t, Cf, part, p, c.splits, (int)is_al16(x));
+      hipLaunchKernelGGL((k_fwd_stream<P, BF, 1, false>), g1, dim3(256), 0, s, x, t, Cf, part, p, c.splits, (int)is_al16(x));
+    else  // 33..64 rows: tanh once by launch_tanh, not once per column block
+      hipLaunchKernelGGL((k_fwd_stream<P, BF, 2, true>), g1, dim3(256), 0, s, x, t, Cf, part, p, c.splits, (int)is_al16(x));
   } else {
     dim3 grid(c.tiles_m, c.tiles_n, c.splits);
     switch (c.tile) {

@@ -41,6 +41,10 @@ struct FwdChoice {
 };
 FwdChoice choose_fwd(const Plan& p);
 inline bool fwd_streaming(const FwdChoice& c) { return c.tile == kFwdStream32 || c.tile == kFwdStream64; }
+// The 32-row streaming forward computes tanh itself (each value is needed by
+// every column block, cheap at <= 32 rows); every other path reads the tanh
+// cache written by launch_tanh first.
+inline bool fwd_reads_tcache(const FwdChoice& c) { return c.tile != kFwdStream32; }
 // split-K partials [splits][B32][O32] fp32, summed in order by k_fwd_reduce
 inline size_t fwd_ws_bytes(const Plan& p, const FwdChoice& c) {
   if (c.splits <= 1 && !fwd_streaming(c)) return 0;
