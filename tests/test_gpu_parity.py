@@ -65,6 +65,7 @@ SHAPES = [
     (256, 128, 64, 16),
     (1000, 100, 150, 6),  # pipelined forward: ragged rows, padded inputs, partial tiles
     (777, 40, 300, 12),   # the same at degree 16 (P = 16)
+    (50, 100, 70, 6),     # streaming forward, 33..64 rows (tanh from the cache), padded inputs
 ]
 
 
