@@ -101,6 +101,71 @@ inline bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr
 
 void ckan::set_last_error(const char* msg) { g_err = msg; }
 
+int ckan::backward_impl(const ckan_desc* desc, const float* t_cache, const void* packed,
+                        const float* dy, float* dx, float* dcoeffs, DcOut om, void* ws,
+                        size_t ws_bytes, void* stream) {
+  int rc = validate_desc(desc);
+  if (rc) return rc;
+  const Plan p = plan_of(desc);
+  const bool need_dx = dx != nullptr, need_dc = dcoeffs != nullptr;
+  if (!need_dx && !need_dc) return CKAN_OK;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (p.B == 0) {
+    // empty batch: dC = 0 (or unchanged when accumulating), dx is empty
+    if (need_dc && om.mode == kDcSgd)
+      return fail(CKAN_ERR_UNSUPPORTED, "backward: an SGD-applying call needs batch >= 1");
+    if (need_dc && om.mode == kDcStore) {
+      launch_zero_f32(dcoeffs, (int64_t)p.I * p.O * p.D, s);
+      return check_launch("zero dcoeffs");
+    }
+    return CKAN_OK;
+  }
+  if (!t_cache || !dy || (need_dx && !packed))
+    return fail(CKAN_ERR_INVALID_ARG, "t_cache/dy/packed is NULL");
+  if (need_dx && !aligned16(packed)) return fail(CKAN_ERR_INVALID_ARG, "packed must be 16-byte aligned");
+  const BwdLayout L = bwd_layout(p, need_dx, need_dc);
+  if (ws_bytes < L.total)
+    return fail(CKAN_ERR_WORKSPACE, "backward workspace too small: %zu < %zu bytes", ws_bytes, L.total);
+  if (!ws || !aligned16(ws)) return fail(CKAN_ERR_INVALID_ARG, "workspace is NULL or misaligned");
+  char* w = reinterpret_cast<char*>(ws);
+  void* dYx = w + L.dyx_off;
+  void* dYc = w + L.dyc_off;
+  float* colsum = reinterpret_cast<float*>(w + L.colsum_off);
+  float* part = reinterpret_cast<float*>(w + L.part_off);
+  {
+    ProfScope ps("prep_dy", s);
+    launch_prep_dy(dy, dYx, dYc, colsum, p, need_dx, need_dc, s);
+  }
+  if ((rc = check_launch("prep_dy"))) return rc;
+  if (need_dx) {
+    ProfScope ps("dx_gemm", s);
+    launch_dx_gemm(dYx, packed, t_cache, dx, p, s);
+  }
+  if ((rc = check_launch("dx_gemm"))) return rc;
+  if (need_dc) {
+    // the pipelined dC kernel reduces the column-sum partials itself
+    const float* colsum_r = nullptr;
+    if (!L.dc_pipe) {
+      ProfScope ps("colsum", s);
+      colsum_r = launch_colsum_reduce(colsum, p, s);
+    }
+    {
+      ProfScope ps("dc_gemm", s);
+      launch_dc_gemm(dYc, t_cache, L.dc_pipe ? colsum : colsum_r, part, dcoeffs, om, p, L, s);
+    }
+    if ((rc = check_launch("dc_gemm"))) return rc;
+    if (!L.dc_pipe) {
+      ProfScope ps("dc_finalize", s);
+      launch_dc_finalize(part, L.dc_splits, colsum_r, dcoeffs, om, p, s);
+    } else if (L.dc_splits > 1) {
+      ProfScope ps("dc_finalize", s);
+      launch_dc_sum(part, L.dc_splits, dcoeffs, om, p, s);
+    }
+    if ((rc = check_launch("dc_finalize"))) return rc;
+  }
+  return CKAN_OK;
+}
+
 extern "C" {
 
 const char* ckan_last_error(void) { return g_err.c_str(); }
@@ -185,65 +250,8 @@ int ckan_forward(const ckan_desc* desc, const float* x, const void* packed, floa
 int ckan_backward(const ckan_desc* desc, const float* t_cache, const void* packed,
                   const float* dy, float* dx, float* dcoeffs, int accumulate, void* ws,
                   size_t ws_bytes, void* stream) {
-  int rc = validate_desc(desc);
-  if (rc) return rc;
-  const Plan p = plan_of(desc);
-  const bool need_dx = dx != nullptr, need_dc = dcoeffs != nullptr;
-  if (!need_dx && !need_dc) return CKAN_OK;
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  if (p.B == 0) {
-    // empty batch: dC = 0 (or unchanged when accumulating), dx is empty
-    if (need_dc && !accumulate) {
-      launch_zero_f32(dcoeffs, (int64_t)p.I * p.O * p.D, s);
-      return check_launch("zero dcoeffs");
-    }
-    return CKAN_OK;
-  }
-  if (!t_cache || !dy || (need_dx && !packed))
-    return fail(CKAN_ERR_INVALID_ARG, "t_cache/dy/packed is NULL");
-  if (need_dx && !aligned16(packed)) return fail(CKAN_ERR_INVALID_ARG, "packed must be 16-byte aligned");
-  const BwdLayout L = bwd_layout(p, need_dx, need_dc);
-  if (ws_bytes < L.total)
-    return fail(CKAN_ERR_WORKSPACE, "backward workspace too small: %zu < %zu bytes", ws_bytes, L.total);
-  if (!ws || !aligned16(ws)) return fail(CKAN_ERR_INVALID_ARG, "workspace is NULL or misaligned");
-  char* w = reinterpret_cast<char*>(ws);
-  void* dYx = w + L.dyx_off;
-  void* dYc = w + L.dyc_off;
-  float* colsum = reinterpret_cast<float*>(w + L.colsum_off);
-  float* part = reinterpret_cast<float*>(w + L.part_off);
-  {
-    ProfScope ps("prep_dy", s);
-    launch_prep_dy(dy, dYx, dYc, colsum, p, need_dx, need_dc, s);
-  }
-  if ((rc = check_launch("prep_dy"))) return rc;
-  if (need_dx) {
-    ProfScope ps("dx_gemm", s);
-    launch_dx_gemm(dYx, packed, t_cache, dx, p, s);
-  }
-  if ((rc = check_launch("dx_gemm"))) return rc;
-  if (need_dc) {
-    // the pipelined dC kernel reduces the column-sum partials itself
-    const float* colsum_r = nullptr;
-    if (!L.dc_pipe) {
-      ProfScope ps("colsum", s);
-      colsum_r = launch_colsum_reduce(colsum, p, s);
-    }
-    {
-      ProfScope ps("dc_gemm", s);
-      launch_dc_gemm(dYc, t_cache, L.dc_pipe ? colsum : colsum_r, part, dcoeffs,
-                     accumulate != 0, p, L, s);
-    }
-    if ((rc = check_launch("dc_gemm"))) return rc;
-    if (!L.dc_pipe) {
-      ProfScope ps("dc_finalize", s);
-      launch_dc_finalize(part, L.dc_splits, colsum_r, dcoeffs, accumulate != 0, p, s);
-    } else if (L.dc_splits > 1) {
-      ProfScope ps("dc_finalize", s);
-      launch_dc_sum(part, L.dc_splits, dcoeffs, accumulate != 0, p, s);
-    }
-    if ((rc = check_launch("dc_finalize"))) return rc;
-  }
-  return CKAN_OK;
+  const DcOut om{accumulate ? kDcAccumulate : kDcStore, 0.0f, 0.0f};
+  return backward_impl(desc, t_cache, packed, dy, dx, dcoeffs, om, ws, ws_bytes, stream);
 }
 
 int ckan_basis(const float* t, int64_t n, int32_t degree, float* out, void* stream) {

@@ -296,14 +296,14 @@ k_prep_dy(const float* __restrict__ dy, typename Elem<BF>::type* __restrict__ dY
   }
 }
 
-// dC[i, o, d] (=|+=) for d = 0: sum_b dy[b, o] (from the colsum partials);
+// dC[i, o, d] (stored, added or applied as an SGD step, by om) for d = 0: sum_b dy[b, o] (from the colsum partials);
 // for d >= 1: sum over the S split partials part[s][d-1][i][o].
 // One block per (16 inputs, 64 outputs); the tile is transposed through LDS
 // so the write of dC is one contiguous run of 64*D values per input.
 template <int P>
 __global__ void __launch_bounds__(256)
 k_dc_finalize(const float* __restrict__ part, int S, const float* __restrict__ colsum,
-              float* __restrict__ dC, int accumulate, Plan p) {
+              float* __restrict__ dC, DcOut om, Plan p) {
   __shared__ float tile[16 * 64 * (P + 1)];
   __shared__ float csq[1][64];
   const int tid = threadIdx.x;
@@ -345,7 +345,7 @@ k_dc_finalize(const float* __restrict__ part, int S, const float* __restrict__ c
     const float* src = tile + il * 64 * D;
     for (int idx = tid; idx < nrow; idx += 256) {
       const float v = src[idx];
-      dst[idx] = accumulate ? dst[idx] + v : v;
+      dc_write(dst + idx, v, om);
     }
   }
 }
@@ -354,9 +354,7 @@ __global__ void __launch_bounds__(256)
 k_sgd(float* __restrict__ p, const float* __restrict__ g, int64_t n, float lr, float wd) {
   for (int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; q < n;
        q += (int64_t)gridDim.x * blockDim.x) {
-    float gv = g[q];
-    if (wd != 0.0f) gv = gv + wd * p[q];
-    p[q] = p[q] - lr * gv;
+    p[q] = sgd_update(p[q], g[q], lr, wd);
   }
 }
 
@@ -532,21 +530,21 @@ float* launch_colsum_reduce(float* colsum_part, const Plan& p, hipStream_t s) {
 }
 
 void launch_dc_finalize(const float* part, int S, const float* colsum, float* dC,
-                        bool accumulate, const Plan& p, hipStream_t s) {
+                        DcOut om, const Plan& p, hipStream_t s) {
   dim3 grid((unsigned)ceil_div(p.I, 16), (unsigned)ceil_div(p.O, 64));
   switch (p.P) {
-    case 2: hipLaunchKernelGGL((k_dc_finalize<2>), grid, dim3(256), 0, s, part, S, colsum, dC, (int)accumulate, p); break;
-    case 4: hipLaunchKernelGGL((k_dc_finalize<4>), grid, dim3(256), 0, s, part, S, colsum, dC, (int)accumulate, p); break;
-    case 8: hipLaunchKernelGGL((k_dc_finalize<8>), grid, dim3(256), 0, s, part, S, colsum, dC, (int)accumulate, p); break;
-    default: hipLaunchKernelGGL((k_dc_finalize<16>), grid, dim3(256), 0, s, part, S, colsum, dC, (int)accumulate, p); break;
+    case 2: hipLaunchKernelGGL((k_dc_finalize<2>), grid, dim3(256), 0, s, part, S, colsum, dC, om, p); break;
+    case 4: hipLaunchKernelGGL((k_dc_finalize<4>), grid, dim3(256), 0, s, part, S, colsum, dC, om, p); break;
+    case 8: hipLaunchKernelGGL((k_dc_finalize<8>), grid, dim3(256), 0, s, part, S, colsum, dC, om, p); break;
+    default: hipLaunchKernelGGL((k_dc_finalize<16>), grid, dim3(256), 0, s, part, S, colsum, dC, om, p); break;
   }
 }
 
-// dC[q] (=|+=) sum_z part[z][q], z in split order (slices of I*O*D floats).
-// The split sum is formed first, so accumulating adds exactly the gradient a
-// non-accumulating call writes.
+// dC[q] (stored, added or applied as an SGD step, by om) = sum_z part[z][q],
+// z in split order (slices of I*O*D floats).  The split sum is formed first,
+// so accumulating adds exactly the gradient a storing call writes.
 __global__ void __launch_bounds__(256)
-k_dc_sum(const float* __restrict__ part, int S, float* __restrict__ dC, int64_t n, int accumulate) {
+k_dc_sum(const float* __restrict__ part, int S, float* __restrict__ dC, int64_t n, DcOut om) {
   for (int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; q < n;
        q += (int64_t)gridDim.x * blockDim.x) {
     float acc = 0.0f;
@@ -557,14 +555,13 @@ k_dc_sum(const float* __restrict__ part, int S, float* __restrict__ dC, int64_t 
       acc = (((acc + a) + b) + c) + d;
     }
     for (; z < S; ++z) acc += part[(size_t)z * n + q];
-    dC[q] = accumulate ? dC[q] + acc : acc;
+    dc_write(dC + q, acc, om);
   }
 }
 
-void launch_dc_sum(const float* part, int S, float* dC, bool accumulate, const Plan& p,
-                   hipStream_t s) {
+void launch_dc_sum(const float* part, int S, float* dC, DcOut om, const Plan& p, hipStream_t s) {
   const int64_t n = (int64_t)p.I * p.O * p.D;
-  hipLaunchKernelGGL(k_dc_sum, dim3(grid_for(n)), dim3(256), 0, s, part, S, dC, n, (int)accumulate);
+  hipLaunchKernelGGL(k_dc_sum, dim3(grid_for(n)), dim3(256), 0, s, part, S, dC, n, om);
 }
 
 void launch_sgd(float* p, const float* g, int64_t n, float lr, float wd, hipStream_t s) {

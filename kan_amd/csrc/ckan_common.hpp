@@ -78,6 +78,45 @@ struct Plan {
   int esz;         // bytes per packed operand element (2 bf16, 4 fp32)
 };
 
+// How the dC kernels write the finished gradient g into the destination d:
+// store it, add it, or (for a caller that wants only the updated parameter,
+// with d the parameter itself) apply the SGD step d -= lr * (g + wd * d).
+enum DcMode : int { kDcStore = 0, kDcAccumulate = 1, kDcSgd = 2 };
+struct DcOut {
+  int mode;
+  float lr, wd;
+};
+
+// The SGD update of one parameter: the arithmetic of every SGD path here.
+__device__ __forceinline__ float sgd_update(float p, float g, float lr, float wd) {
+  float gv = g;
+  if (wd != 0.0f) gv = gv + wd * p;
+  return p - lr * gv;
+}
+
+__device__ __forceinline__ void dc_write(float* d, float g, const DcOut& o) {
+  if (o.mode == kDcStore) *d = g;
+  else if (o.mode == kDcAccumulate) *d = *d + g;
+  else *d = sgd_update(*d, g, o.lr, o.wd);
+}
+
+__device__ __forceinline__ void dc_write4(f32x4_t* d, f32x4_t g, const DcOut& o) {
+  if (o.mode == kDcStore) {
+    *d = g;
+  } else {
+    f32x4_t v = *d;
+    if (o.mode == kDcAccumulate) {
+      v = v + g;
+    } else {
+      v.x = sgd_update(v.x, g.x, o.lr, o.wd);
+      v.y = sgd_update(v.y, g.y, o.lr, o.wd);
+      v.z = sgd_update(v.z, g.z, o.lr, o.wd);
+      v.w = sgd_update(v.w, g.w, o.lr, o.wd);
+    }
+    *d = v;
+  }
+}
+
 inline Plan make_plan(int64_t B, int I, int O, int deg, bool bf16) {
   Plan p;
   p.B = B; p.I = I; p.O = O; p.deg = deg; p.D = deg + 1;

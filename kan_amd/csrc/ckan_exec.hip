@@ -229,18 +229,19 @@ int run_step(ckan_exec* ex, const float* x, const void* target, hipStream_t s) {
                        (float)(1.0 / (double)B), ex->loss);
   }
   if (hipGetLastError() != hipSuccess) return efail(CKAN_ERR_HIP, "executor: loss launch failed");
+  const auto& c = ex->cfg;
+  // SGD is applied by the dC kernels themselves, into C: nothing reads a
+  // layer's C after its dC (the dX pass reads the packed copy).
+  const bool sgd = c.optimizer == CKAN_OPT_SGD;
+  const DcOut om = sgd ? DcOut{kDcSgd, c.lr, c.weight_decay} : DcOut{kDcStore, 0.0f, 0.0f};
   for (int l = L - 1; l >= 0; --l) {
     auto& ly = ex->layers[l];
     float* dx = l > 0 ? ex->layers[l - 1].dy : nullptr;
-    if ((rc = ckan_backward(&ly.desc, ly.t, ly.packed, ly.dy, dx, ly.dC, 0, ex->bws,
+    if ((rc = backward_impl(&ly.desc, ly.t, ly.packed, ly.dy, dx, sgd ? ly.C : ly.dC, om, ex->bws,
                             ex->bws_bytes, s)))
       return rc;
   }
-  const auto& c = ex->cfg;
-  if (c.optimizer == CKAN_OPT_SGD) {
-    for (auto& ly : ex->layers)
-      if ((rc = ckan_sgd_step(ly.C, ly.dC, ly.ncoef, c.lr, c.weight_decay, s))) return rc;
-  } else {
+  if (!sgd) {
     hipLaunchKernelGGL(k_adam_scalars, dim3(1), dim3(64), 0, s, ex->step, (double)c.lr,
                        (double)c.beta1, (double)c.beta2, ex->adam_sc);
     for (auto& ly : ex->layers)
@@ -290,7 +291,8 @@ int ckan_exec_create(const ckan_exec_config* cfg, ckan_exec** out, void* stream)
     ly.ncoef = (int64_t)ly.desc.in_dim * ly.desc.out_dim * (ly.desc.degree + 1);
     const int64_t ny = cfg->batch * ly.desc.out_dim;
     if ((rc = dev_alloc(ex, (void**)&ly.C, ly.ncoef * 4)) ||
-        (rc = dev_alloc(ex, (void**)&ly.dC, ly.ncoef * 4)) ||
+        // with SGD the dC kernels update C in place and no gradient is kept
+        (cfg->optimizer != CKAN_OPT_SGD && (rc = dev_alloc(ex, (void**)&ly.dC, ly.ncoef * 4))) ||
         (rc = dev_alloc(ex, &ly.packed, ly.packed_bytes)) ||
         (rc = dev_alloc(ex, (void**)&ly.t, ckan_tcache_elems(&ly.desc) * 4)) ||
         (rc = dev_alloc(ex, (void**)&ly.y, ny * 4)) ||

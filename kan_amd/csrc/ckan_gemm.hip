@@ -1350,7 +1350,7 @@ template <int P, bool BF, int H_>
 __global__ void __launch_bounds__(512)
 k_dc_pipe(const typename Elem<BF>::type* __restrict__ dYc, const float* __restrict__ tc,
           const float* __restrict__ colsum_part, float* __restrict__ out, Plan p, int st_per_split,
-          int accumulate) {
+          DcOut om) {
   typedef DcPipe<P, BF, H_> K;
   typedef typename K::E E;
   constexpr int PH = K::PH, DQ = K::DQ, OG = K::OG, NN = K::NN, NO = K::NO, NF = K::NF;
@@ -1686,14 +1686,14 @@ k_dc_pipe(const typename Elem<BF>::type* __restrict__ dYc, const float* __restri
           const int il = q / run4, k4 = q - il * run4;
           const f32x4_t v = *reinterpret_cast<const f32x4_t*>(stg + il * OW * p.D + 4 * k4);
           f32x4_t* d = reinterpret_cast<f32x4_t*>(dst0 + il * pitch) + k4;
-          *d = accumulate ? *d + v : v;
+          dc_write4(d, v, om);
         }
       } else {
         for (int q = tid; q < ivalid * run; q += 512) {
           const int il = q / run, k = q - il * run;
           const float v = stg[il * OW * p.D + k];
           float* d = dst0 + il * pitch + k;
-          *d = accumulate ? *d + v : v;
+          dc_write(d, v, om);
         }
       }
     }
@@ -1964,7 +1964,7 @@ BwdLayout bwd_layout(const Plan& p, bool need_dx, bool need_dc) {
 
 template <int P, bool BF, int H>
 static bool dc_pipe_launch(const void* dYc, const float* t, const float* colsum, float* part,
-                           float* dC, bool accumulate, const Plan& p, const BwdLayout& L,
+                           float* dC, DcOut om, const Plan& p, const BwdLayout& L,
                            hipStream_t s) {
   typedef typename Elem<BF>::type E;
   if constexpr (DcPipe<P, BF, H>::kOk) {
@@ -1975,7 +1975,7 @@ static bool dc_pipe_launch(const void* dYc, const float* t, const float* colsum,
     dim3 grid(p.NIB, (unsigned)ceil_div(p.NBf, K::NO), L.dc_splits);
     hipLaunchKernelGGL((k_dc_pipe<P, BF, H>), grid, dim3(512), K::LDS_BYTES, s,
                        reinterpret_cast<const E*>(dYc), t, colsum, split ? part : dC, p,
-                       L.dc_st_per_split, (!split && accumulate) ? 1 : 0);
+                       L.dc_st_per_split, split ? DcOut{kDcStore, 0.0f, 0.0f} : om);
     return true;
   }
   return false;
@@ -1983,15 +1983,15 @@ static bool dc_pipe_launch(const void* dYc, const float* t, const float* colsum,
 
 template <int P, bool BF>
 static void dc_dispatch(const void* dYc, const float* t, const float* colsum, float* part,
-                        float* dC, bool accumulate, const Plan& p, const BwdLayout& L,
+                        float* dC, DcOut om, const Plan& p, const BwdLayout& L,
                         hipStream_t s) {
   typedef typename Elem<BF>::type E;
   if (L.dc_pipe) {
     bool done = false;
     if constexpr (P == 16) {  // dc_h(p) is 1 only for degree 16
-      if (dc_h(p) == 1) done = dc_pipe_launch<P, BF, 1>(dYc, t, colsum, part, dC, accumulate, p, L, s);
+      if (dc_h(p) == 1) done = dc_pipe_launch<P, BF, 1>(dYc, t, colsum, part, dC, om, p, L, s);
     }
-    if (!done) done = dc_pipe_launch<P, BF, 2>(dYc, t, colsum, part, dC, accumulate, p, L, s);
+    if (!done) done = dc_pipe_launch<P, BF, 2>(dYc, t, colsum, part, dC, om, p, L, s);
     if (done) return;
   }
   constexpr int NM = BwdTile<P>::NM;
@@ -2001,9 +2001,9 @@ static void dc_dispatch(const void* dYc, const float* t, const float* colsum, fl
 }
 
 void launch_dc_gemm(const void* dYc, const float* t, const float* colsum, float* part, float* dC,
-                    bool accumulate, const Plan& p, const BwdLayout& L, hipStream_t s) {
+                    DcOut om, const Plan& p, const BwdLayout& L, hipStream_t s) {
   const bool bf = p.esz == 2;
-#define CKAN_DC(PP, BB) dc_dispatch<PP, BB>(dYc, t, colsum, part, dC, accumulate, p, L, s)
+#define CKAN_DC(PP, BB) dc_dispatch<PP, BB>(dYc, t, colsum, part, dC, om, p, L, s)
   switch (p.P) {
     case 2: bf ? CKAN_DC(2, true) : CKAN_DC(2, false); break;
     case 4: bf ? CKAN_DC(4, true) : CKAN_DC(4, false); break;

@@ -116,9 +116,8 @@ void launch_prep_dy(const float* dy, void* dYx, void* dYc, float* colsum_part, c
 // reduces the dy column-sum partials into row NBB and returns that row
 float* launch_colsum_reduce(float* colsum_part, const Plan& p, hipStream_t s);
 void launch_dc_finalize(const float* part, int S, const float* colsum, float* dC,
-                        bool accumulate, const Plan& p, hipStream_t s);
-void launch_dc_sum(const float* part, int S, float* dC, bool accumulate, const Plan& p,
-                   hipStream_t s);
+                        DcOut om, const Plan& p, hipStream_t s);
+void launch_dc_sum(const float* part, int S, float* dC, DcOut om, const Plan& p, hipStream_t s);
 // x is read only by the small-batch streaming kernel, which also writes t;
 // the other paths read t written by launch_tanh.
 void launch_fwd_gemm(const float* x, float* t, const void* packed, float* y, void* ws,
@@ -128,8 +127,13 @@ void launch_dx_gemm(const void* dYx, const void* packed, const float* t, float* 
 // colsum: the per-64-row column-sum partials for the pipelined kernel (which
 // reduces them itself), the reduced row otherwise.
 void launch_dc_gemm(const void* dYc, const float* t, const float* colsum, float* part, float* dC,
-                    bool accumulate, const Plan& p, const BwdLayout& L, hipStream_t s);
+                    DcOut om, const Plan& p, const BwdLayout& L, hipStream_t s);
 void launch_sgd(float* p, const float* g, int64_t n, float lr, float wd, hipStream_t s);
+// ckan_backward with the dC write mode given by om; with om.mode == kDcSgd,
+// dcoeffs is the parameter and receives its SGD step (batch >= 1 only).
+int backward_impl(const struct ckan_desc* desc, const float* t_cache, const void* packed,
+                  const float* dy, float* dx, float* dcoeffs, DcOut om, void* ws,
+                  size_t ws_bytes, void* stream);
 void launch_adam(float* p, const float* g, float* m, float* v, int64_t n, float w1, float beta2,
                  float one_m_beta2, float bc2_sqrt, float eps, float neg_step, float wd,
                  hipStream_t s);

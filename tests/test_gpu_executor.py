@@ -70,6 +70,39 @@ def test_mse_stack_deg16_sgd_matches_oracle():
     ex.close()
 
 
+@pytest.mark.parametrize("widths,degrees,B,compute", [
+    ([96, 64, 10], [4, 4], 128, "fp32"),    # dC written in place by the pipelined kernel
+    ([96, 64, 10], [4, 4], 512, "fp32"),    # split dC: the split-sum kernel applies the step
+    ([64, 48, 16], [15, 15], 256, "fp32"),  # fp32 degree 16: the finalize kernel applies it
+    ([256, 128, 10], [8, 8], 512, "bf16"),
+])
+def test_sgd_weight_decay_applied_by_dc_kernels(widths, degrees, B, compute):
+    """One SGD step with weight decay: C1 = C0 - lr * (g + wd * C0), where
+    C0 - lr * g is the oracle's step without decay."""
+    from kan_amd import ResidentExecutor
+    print(f"executor sgd wd {widths} {degrees} B={B} {compute}", flush=True)
+    lr, wd = 0.02, 0.5
+    g = torch.Generator().manual_seed(7)
+    x = torch.rand(B, widths[0], generator=g) * 4 - 2
+    y = torch.randn(B, widths[-1], generator=g)
+    coeffs = _make(widths, degrees, 70)
+    c_ref, _ = orc.train_steps(x, y, coeffs, steps=1, loss="mse", optimizer="sgd", lr=lr)
+    ex = ResidentExecutor(widths, degrees, B, compute=compute, loss="mse", optimizer="sgd",
+                          lr=lr, weight_decay=wd)
+    for l, c in enumerate(coeffs):
+        ex.set_coeffs(l, c)
+    ex.step(x.cuda(), y.cuda())
+    tol = 1e-5 if compute == "fp32" else 1e-3
+    for l in range(len(degrees)):
+        want = c_ref[l].double() - lr * wd * coeffs[l].double()
+        got = ex.get_coeffs(l)
+        assert _rel(got, want) <= tol, (l, _rel(got, want))
+        # the decay term (relative size lr * wd = 1e-2) is far above the
+        # tolerance: dropping it would fail
+        assert _rel(got, c_ref[l]) > 5 * tol
+    ex.close()
+
+
 def test_config1_adam_executor_and_checkpoint():
     from kan_amd import ResidentExecutor
     print("executor cfg1 adam", flush=True)
