@@ -112,8 +112,8 @@ int ckan::backward_impl(const ckan_desc* desc, const float* t_cache, const void*
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (p.B == 0) {
     // empty batch: dC = 0 (or unchanged when accumulating), dx is empty
-    if (need_dc && om.mode == kDcSgd)
-      return fail(CKAN_ERR_UNSUPPORTED, "backward: an SGD-applying call needs batch >= 1");
+    if (need_dc && om.mode >= kDcSgd)
+      return fail(CKAN_ERR_UNSUPPORTED, "backward: an optimizer-applying call needs batch >= 1");
     if (need_dc && om.mode == kDcStore) {
       launch_zero_f32(dcoeffs, (int64_t)p.I * p.O * p.D, s);
       return check_launch("zero dcoeffs");
@@ -250,7 +250,7 @@ int ckan_forward(const ckan_desc* desc, const float* x, const void* packed, floa
 int ckan_backward(const ckan_desc* desc, const float* t_cache, const void* packed,
                   const float* dy, float* dx, float* dcoeffs, int accumulate, void* ws,
                   size_t ws_bytes, void* stream) {
-  const DcOut om{accumulate ? kDcAccumulate : kDcStore, 0.0f, 0.0f};
+  const DcOut om{accumulate ? kDcAccumulate : kDcStore};
   return backward_impl(desc, t_cache, packed, dy, dx, dcoeffs, om, ws, ws_bytes, stream);
 }
 

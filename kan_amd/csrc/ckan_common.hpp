@@ -80,11 +80,18 @@ struct Plan {
 
 // How the dC kernels write the finished gradient g into the destination d:
 // store it, add it, or (for a caller that wants only the updated parameter,
-// with d the parameter itself) apply the SGD step d -= lr * (g + wd * d).
-enum DcMode : int { kDcStore = 0, kDcAccumulate = 1, kDcSgd = 2 };
+// with d the parameter itself) apply the SGD step d -= lr * (g + wd * d) or
+// an Adam step (moments m, v at the offset of d from base; the step's
+// -lr / (1 - b1^t) and sqrt(1 - b2^t) read from sc[0], sc[1] on the device).
+enum DcMode : int { kDcStore = 0, kDcAccumulate = 1, kDcSgd = 2, kDcAdam = 3 };
 struct DcOut {
   int mode;
   float lr, wd;
+  float w1, beta2, one_m_beta2, eps;  // Adam: w1 = 1 - beta1
+  const float* base;
+  float* m;
+  float* v;
+  const float* sc;
 };
 
 // The SGD update of one parameter: the arithmetic of every SGD path here.
@@ -94,15 +101,47 @@ __device__ __forceinline__ float sgd_update(float p, float g, float lr, float wd
   return p - lr * gv;
 }
 
+// The Adam update of one parameter pv with gradient g and moments *m, *v
+// (torch's single-tensor order of operations): the arithmetic of the
+// executor's Adam paths.
+__device__ __forceinline__ float adam_update(float pv, float g, float* m, float* v, float w1,
+                                             float beta2, float one_m_beta2, float eps, float wd,
+                                             float neg_step, float bc2_sqrt) {
+  float gv = g;
+  if (wd != 0.0f) gv = gv + wd * pv;
+  float mv = *m;
+  mv = (w1 < 0.5f) ? mv + w1 * (gv - mv) : gv - (gv - mv) * (1.0f - w1);
+  float vv = *v * beta2;
+  vv = vv + one_m_beta2 * gv * gv;
+  const float denom = sqrtf(vv) / bc2_sqrt + eps;
+  *m = mv;
+  *v = vv;
+  return pv + neg_step * (mv / denom);
+}
+
 __device__ __forceinline__ void dc_write(float* d, float g, const DcOut& o) {
-  if (o.mode == kDcStore) *d = g;
-  else if (o.mode == kDcAccumulate) *d = *d + g;
-  else *d = sgd_update(*d, g, o.lr, o.wd);
+  if (o.mode == kDcStore) {
+    *d = g;
+  } else if (o.mode == kDcAccumulate) {
+    *d = *d + g;
+  } else if (o.mode == kDcSgd) {
+    *d = sgd_update(*d, g, o.lr, o.wd);
+  } else {
+    const size_t q = (size_t)(d - o.base);
+    *d = adam_update(*d, g, o.m + q, o.v + q, o.w1, o.beta2, o.one_m_beta2, o.eps, o.wd, o.sc[0],
+                     o.sc[1]);
+  }
 }
 
 __device__ __forceinline__ void dc_write4(f32x4_t* d, f32x4_t g, const DcOut& o) {
   if (o.mode == kDcStore) {
     *d = g;
+  } else if (o.mode == kDcAdam) {
+    float* e = reinterpret_cast<float*>(d);
+    dc_write(e, g.x, o);
+    dc_write(e + 1, g.y, o);
+    dc_write(e + 2, g.z, o);
+    dc_write(e + 3, g.w, o);
   } else {
     f32x4_t v = *d;
     if (o.mode == kDcAccumulate) {

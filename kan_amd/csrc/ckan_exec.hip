@@ -101,28 +101,6 @@ __global__ void k_adam_scalars(int64_t* __restrict__ step, double lr, double b1,
   }
 }
 
-// Adam update reading its step-dependent scalars from the device.
-__global__ void __launch_bounds__(256)
-k_adam_dev(float* __restrict__ p, const float* __restrict__ g, float* __restrict__ m,
-           float* __restrict__ v, int64_t n, float w1, float beta2, float one_m_beta2,
-           float eps, float wd, const float* __restrict__ sc) {
-  const float neg_step = sc[0], bc2_sqrt = sc[1];
-  for (int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; q < n;
-       q += (int64_t)gridDim.x * blockDim.x) {
-    float gv = g[q];
-    const float pv = p[q];
-    if (wd != 0.0f) gv = gv + wd * pv;
-    float mv = m[q];
-    mv = (w1 < 0.5f) ? mv + w1 * (gv - mv) : gv - (gv - mv) * (1.0f - w1);
-    float vv = v[q] * beta2;
-    vv = vv + one_m_beta2 * gv * gv;
-    const float denom = sqrtf(vv) / bc2_sqrt + eps;
-    m[q] = mv;
-    v[q] = vv;
-    p[q] = pv + neg_step * (mv / denom);
-  }
-}
-
 __global__ void __launch_bounds__(256)
 k_copy_f32(const float* __restrict__ src, float* __restrict__ dst, int64_t n) {
   for (int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; q < n;
@@ -142,7 +120,6 @@ struct ckan_exec {
     ckan_desc desc;
     int64_t ncoef;
     float* C = nullptr;     // fp32 master [I, O, D]
-    float* dC = nullptr;
     float* m = nullptr;     // Adam moments
     float* v = nullptr;
     void* packed = nullptr;
@@ -230,25 +207,25 @@ int run_step(ckan_exec* ex, const float* x, const void* target, hipStream_t s) {
   }
   if (hipGetLastError() != hipSuccess) return efail(CKAN_ERR_HIP, "executor: loss launch failed");
   const auto& c = ex->cfg;
-  // SGD is applied by the dC kernels themselves, into C: nothing reads a
-  // layer's C after its dC (the dX pass reads the packed copy).
+  // The optimizer step is applied by the dC kernels themselves, into C:
+  // nothing reads a layer's C after its dC (the dX pass reads the packed copy).
   const bool sgd = c.optimizer == CKAN_OPT_SGD;
-  const DcOut om = sgd ? DcOut{kDcSgd, c.lr, c.weight_decay} : DcOut{kDcStore, 0.0f, 0.0f};
-  for (int l = L - 1; l >= 0; --l) {
-    auto& ly = ex->layers[l];
-    float* dx = l > 0 ? ex->layers[l - 1].dy : nullptr;
-    if ((rc = backward_impl(&ly.desc, ly.t, ly.packed, ly.dy, dx, sgd ? ly.C : ly.dC, om, ex->bws,
-                            ex->bws_bytes, s)))
-      return rc;
-  }
   if (!sgd) {
     hipLaunchKernelGGL(k_adam_scalars, dim3(1), dim3(64), 0, s, ex->step, (double)c.lr,
                        (double)c.beta1, (double)c.beta2, ex->adam_sc);
-    for (auto& ly : ex->layers)
-      hipLaunchKernelGGL(k_adam_dev, dim3(grid_of(ly.ncoef)), dim3(256), 0, s, ly.C, ly.dC,
-                         ly.m, ly.v, ly.ncoef, (float)(1.0 - (double)c.beta1), c.beta2,
-                         (float)(1.0 - (double)c.beta2), c.eps, c.weight_decay, ex->adam_sc);
     if (hipGetLastError() != hipSuccess) return efail(CKAN_ERR_HIP, "executor: adam launch failed");
+  }
+  for (int l = L - 1; l >= 0; --l) {
+    auto& ly = ex->layers[l];
+    float* dx = l > 0 ? ex->layers[l - 1].dy : nullptr;
+    DcOut om{kDcSgd, c.lr, c.weight_decay};
+    if (!sgd) {
+      om = DcOut{kDcAdam, 0.0f, c.weight_decay, (float)(1.0 - (double)c.beta1), c.beta2,
+                 (float)(1.0 - (double)c.beta2), c.eps, ly.C, ly.m, ly.v, ex->adam_sc};
+    }
+    if ((rc = backward_impl(&ly.desc, ly.t, ly.packed, ly.dy, dx, ly.C, om, ex->bws,
+                            ex->bws_bytes, s)))
+      return rc;
   }
   return CKAN_OK;
 }
@@ -291,8 +268,6 @@ int ckan_exec_create(const ckan_exec_config* cfg, ckan_exec** out, void* stream)
     ly.ncoef = (int64_t)ly.desc.in_dim * ly.desc.out_dim * (ly.desc.degree + 1);
     const int64_t ny = cfg->batch * ly.desc.out_dim;
     if ((rc = dev_alloc(ex, (void**)&ly.C, ly.ncoef * 4)) ||
-        // with SGD the dC kernels update C in place and no gradient is kept
-        (cfg->optimizer != CKAN_OPT_SGD && (rc = dev_alloc(ex, (void**)&ly.dC, ly.ncoef * 4))) ||
         (rc = dev_alloc(ex, &ly.packed, ly.packed_bytes)) ||
         (rc = dev_alloc(ex, (void**)&ly.t, ckan_tcache_elems(&ly.desc) * 4)) ||
         (rc = dev_alloc(ex, (void**)&ly.y, ny * 4)) ||

@@ -1975,7 +1975,7 @@ static bool dc_pipe_launch(const void* dYc, const float* t, const float* colsum,
     dim3 grid(p.NIB, (unsigned)ceil_div(p.NBf, K::NO), L.dc_splits);
     hipLaunchKernelGGL((k_dc_pipe<P, BF, H>), grid, dim3(512), K::LDS_BYTES, s,
                        reinterpret_cast<const E*>(dYc), t, colsum, split ? part : dC, p,
-                       L.dc_st_per_split, split ? DcOut{kDcStore, 0.0f, 0.0f} : om);
+                       L.dc_st_per_split, split ? DcOut{kDcStore} : om);
     return true;
   }
   return false;

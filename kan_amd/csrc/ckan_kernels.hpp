@@ -129,8 +129,9 @@ void launch_dx_gemm(const void* dYx, const void* packed, const float* t, float* 
 void launch_dc_gemm(const void* dYc, const float* t, const float* colsum, float* part, float* dC,
                     DcOut om, const Plan& p, const BwdLayout& L, hipStream_t s);
 void launch_sgd(float* p, const float* g, int64_t n, float lr, float wd, hipStream_t s);
-// ckan_backward with the dC write mode given by om; with om.mode == kDcSgd,
-// dcoeffs is the parameter and receives its SGD step (batch >= 1 only).
+// ckan_backward with the dC write mode given by om; with om.mode kDcSgd or
+// kDcAdam, dcoeffs is the parameter and receives its optimizer step (batch
+// >= 1 only).
 int backward_impl(const struct ckan_desc* desc, const float* t_cache, const void* packed,
                   const float* dy, float* dx, float* dcoeffs, DcOut om, void* ws,
                   size_t ws_bytes, void* stream);
