@@ -84,7 +84,7 @@ class ResidentExecutor:
         return out
 
     def step(self, x: torch.Tensor, target: torch.Tensor) -> torch.Tensor:
-        """One training step; returns the loss as a device scalar."""
+        """One training step; returns the step's loss as a new device scalar."""
         x = x.to(self.device, torch.float32).contiguous()
         if tuple(x.shape) != (self.batch, self.widths[0]):
             raise RuntimeError(f"x must be [{self.batch}, {self.widths[0]}]")
@@ -98,7 +98,9 @@ class ResidentExecutor:
                 raise RuntimeError(f"labels must be [{self.batch}]")
         _lib.check(self._lib.ckan_exec_step(self._h, x.data_ptr(), target.data_ptr(),
                                             self._loss.data_ptr(), self._stream()))
-        return self._loss
+        # the library writes every step's loss into the same 4 bytes: hand the
+        # caller its own copy, as a torch loss tensor would be
+        return self._loss.clone()
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         x = x.to(self.device, torch.float32).contiguous()

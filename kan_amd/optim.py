@@ -72,14 +72,22 @@ class Adam(torch.optim.Optimizer):
                 _check_param(p)
                 st = self.state[p]
                 if not st:
-                    st["step"] = 0
-                    st["exp_avg"] = torch.zeros_like(p)
-                    st["exp_avg_sq"] = torch.zeros_like(p)
+                    # torch.optim.Adam keeps the count as a float32 CPU tensor, so
+                    # state_dicts load both ways
+                    st["step"] = torch.tensor(0.0, dtype=torch.float32)
+                    st["exp_avg"] = torch.zeros_like(p, memory_format=torch.preserve_format)
+                    st["exp_avg_sq"] = torch.zeros_like(p, memory_format=torch.preserve_format)
+                if not torch.is_tensor(st["step"]):
+                    st["step"] = torch.tensor(float(st["step"]), dtype=torch.float32)
+                for k in ("exp_avg", "exp_avg_sq"):
+                    if st[k].device != p.device or not st[k].is_contiguous():
+                        st[k] = st[k].to(p.device, torch.float32).contiguous()
                 st["step"] += 1
+                step = int(st["step"].item())
                 g = p.grad.contiguous()
                 _lib.check(lib.ckan_adam_step(
                     p.data_ptr(), g.data_ptr(), st["exp_avg"].data_ptr(),
-                    st["exp_avg_sq"].data_ptr(), p.numel(), st["step"], float(group["lr"]),
+                    st["exp_avg_sq"].data_ptr(), p.numel(), step, float(group["lr"]),
                     float(b1), float(b2), float(group["eps"]), float(group["weight_decay"]),
                     _lib.stream_ptr(p.device)))
         return loss

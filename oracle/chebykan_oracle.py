@@ -41,7 +41,7 @@ __all__ = [
     "normalize_input", "basis_closed_form", "basis_recurrence", "layer_forward",
     "layer_forward_backward", "init_coeffs", "adam_step", "sgd_step",
     "cheb_T_fp64", "cheb_T_powersum_fp64", "cheb_U_fp64", "forward_fp64",
-    "backward_fp64", "forward_bruteforce", "mlp_forward", "train_steps",
+    "backward_fp64", "forward_bruteforce", "mlp_forward", "train_steps", "round_bf16_ste",
     "SATURATION_X",
 ]
 
@@ -152,29 +152,47 @@ def sgd_step(p: torch.Tensor, g: torch.Tensor, lr: float, weight_decay: float = 
     p.add_(g, alpha=-lr)
 
 
-def mlp_forward(x: torch.Tensor, coeff_list, use_recurrence: bool = False) -> torch.Tensor:
-    """A stack of ChebyKAN layers as in KANSequential (kan/layers/base.py:144-153)."""
+def round_bf16_ste(c: torch.Tensor) -> torch.Tensor:
+    """c rounded to bf16 (round to nearest even) in the forward, identity in
+    the backward: the operand a bf16-MFMA layer multiplies with while its
+    fp32 master parameter receives the gradient unchanged."""
+    return c + (c.to(torch.bfloat16).to(c.dtype) - c).detach()
+
+
+def mlp_forward(x: torch.Tensor, coeff_list, use_recurrence: bool = False,
+                bf16_coeffs: bool = False) -> torch.Tensor:
+    """A stack of ChebyKAN layers as in KANSequential (kan/layers/base.py:144-153).
+
+    ``bf16_coeffs`` evaluates each layer with its coefficients rounded to
+    bf16 (the bf16-compute case; the reference itself cannot run bf16
+    coefficients, so its fp32 math on the rounded operands is the check)."""
     h = x
     for c in coeff_list:
-        h = layer_forward(h, c, use_recurrence)
+        h = layer_forward(h, round_bf16_ste(c) if bf16_coeffs else c, use_recurrence)
     return h
 
 
 def train_steps(x: torch.Tensor, target: torch.Tensor, coeff_list, steps: int,
-                loss: str = "mse", optimizer: str = "adam", lr: float = 0.01):
+                loss: str = "mse", optimizer: str = "adam", lr: float = 0.01,
+                weight_decay: float = 0.0, eps: float = 1e-8, bf16_coeffs: bool = False,
+                return_state: bool = False):
     """The reference training loop (README.md:55-69) on the restatement.
 
-    Returns (final coefficient list, list of per-step losses).
+    zero_grad -> forward -> loss (MSELoss / CrossEntropyLoss, mean reduction)
+    -> backward -> torch.optim.Adam / SGD step, ``steps`` times.
+    Returns (final coefficient list, list of per-step losses), plus the
+    optimizer's per-parameter state list (exp_avg, exp_avg_sq, step for
+    Adam) when ``return_state``.
     """
     params = [c.detach().clone().requires_grad_(True) for c in coeff_list]
     if optimizer == "adam":
-        opt = torch.optim.Adam(params, lr=lr)
+        opt = torch.optim.Adam(params, lr=lr, eps=eps, weight_decay=weight_decay)
     else:
-        opt = torch.optim.SGD(params, lr=lr)
+        opt = torch.optim.SGD(params, lr=lr, weight_decay=weight_decay)
     losses = []
     for _ in range(steps):
         opt.zero_grad()
-        out = mlp_forward(x, params)
+        out = mlp_forward(x, params, bf16_coeffs=bf16_coeffs)
         if loss == "mse":
             l = F.mse_loss(out, target)
         else:
@@ -182,7 +200,10 @@ def train_steps(x: torch.Tensor, target: torch.Tensor, coeff_list, steps: int,
         l.backward()
         opt.step()
         losses.append(float(l.detach()))
-    return [p.detach() for p in params], losses
+    coeffs = [p.detach() for p in params]
+    if return_state:
+        return coeffs, losses, [dict(opt.state[p]) for p in params]
+    return coeffs, losses
 
 
 # ---------------------------------------------------------------------------

@@ -134,3 +134,23 @@ def test_layer_api_matches_reference_surface():
     assert len(seq.get_analytical_form()) == 2
     with pytest.raises(ValueError):
         kan_amd.ChebyKANLayer(3, 3, 3, compute="fp8")
+
+
+def test_adam_state_dict_interoperates_with_torch_optim():
+    """A torch.optim.Adam checkpoint loads into kan_amd.optim.Adam (step kept as
+    torch keeps it, a float tensor) and the other way round."""
+    from kan_amd import optim
+    p = torch.nn.Parameter(torch.randn(7))
+    ref = torch.optim.Adam([p], lr=0.01)
+    p.grad = torch.randn(7)
+    ref.step()
+    ref.step()
+    q = torch.nn.Parameter(p.detach().clone())
+    ours = optim.Adam([q], lr=0.01)
+    ours.load_state_dict(ref.state_dict())
+    st = ours.state[q]
+    assert torch.is_tensor(st["step"]) and float(st["step"]) == 2.0
+    assert torch.equal(st["exp_avg"], ref.state[p]["exp_avg"])
+    back = torch.optim.Adam([torch.nn.Parameter(p.detach().clone())], lr=0.01)
+    back.load_state_dict(ours.state_dict())
+    assert float(next(iter(back.state.values()))["step"]) == 2.0

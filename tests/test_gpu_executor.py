@@ -103,6 +103,57 @@ def test_sgd_weight_decay_applied_by_dc_kernels(widths, degrees, B, compute):
     ex.close()
 
 
+@pytest.mark.parametrize("widths,degrees,B,compute,loss", [
+    ([96, 64, 10], [4, 4], 128, "fp32", "mse"),    # pipelined dC writes C in place
+    ([96, 64, 10], [4, 4], 512, "fp32", "mse"),    # split dC: the split-sum kernel applies Adam
+    ([64, 48, 16], [15, 15], 256, "fp32", "mse"),  # fp32 degree 16: the finalize kernel applies it
+    ([64, 48, 16], [2, 1], 256, "fp32", "mse"),    # fp32 degree 1-2: the finalize kernel as well
+    ([256, 128, 10], [8, 8], 512, "bf16", "mse"),
+    ([784, 64, 10], [4, 4], 256, "fp32", "ce"),    # the config-2 shape with Adam
+])
+def test_adam_with_weight_decay_applied_by_dc_kernels(widths, degrees, B, compute, loss):
+    """Three executor Adam steps with weight decay against torch.optim.Adam on
+    the oracle's gradients: coefficients, exp_avg, exp_avg_sq and the step
+    count, through every dC write path."""
+    from kan_amd import ResidentExecutor
+    print(f"executor adam wd {widths} {degrees} B={B} {compute} {loss}", flush=True)
+    lr, wd, steps = 0.01, 0.3, 3
+    g = torch.Generator().manual_seed(9)
+    x = torch.rand(B, widths[0], generator=g) * 4 - 2
+    if loss == "mse":
+        y = torch.randn(B, widths[-1], generator=g)
+    else:
+        y = torch.randint(0, widths[-1], (B,), generator=g)
+    coeffs = _make(widths, degrees, 90)
+    bf = compute == "bf16"
+    # eps near the gradients' scale keeps Adam's update Lipschitz in the
+    # gradient, so the gradient's rounding (bf16 above all) stays visible at
+    # its own size rather than as sign flips of near-zero entries
+    c_sgd, _ = orc.train_steps(x, y, coeffs, steps=1, loss=loss, optimizer="sgd", lr=1.0,
+                               bf16_coeffs=bf)
+    g0 = [c0 - c1 for c0, c1 in zip(coeffs, c_sgd)]  # first-step gradients (lr = 1)
+    eps = 0.1 * min(float(d.abs().median()) for d in g0)
+    c_ref, _, st_ref = orc.train_steps(x, y, coeffs, steps=steps, loss=loss, optimizer="adam", lr=lr,
+                                       weight_decay=wd, eps=eps, bf16_coeffs=bf, return_state=True)
+    ex = ResidentExecutor(widths, degrees, B, compute=compute, loss=loss, optimizer="adam", lr=lr,
+                          eps=eps, weight_decay=wd)
+    for l, c in enumerate(coeffs):
+        ex.set_coeffs(l, c)
+    xd, yd = x.cuda(), y.cuda()
+    for _ in range(steps):
+        ex.step(xd, yd)
+    sd = ex.state_dict()
+    assert sd["step"] == steps
+    tol = 1e-4 if compute == "fp32" else 2e-2
+    for l in range(len(degrees)):
+        d_got = sd[f"{l}.cheby_coeffs"].double() - coeffs[l].double()
+        d_want = c_ref[l].double() - coeffs[l].double()
+        assert _rel(d_got, d_want) <= tol, (l, "C", _rel(d_got, d_want))
+        assert _rel(sd[f"{l}.exp_avg"], st_ref[l]["exp_avg"]) <= tol, (l, "exp_avg")
+        assert _rel(sd[f"{l}.exp_avg_sq"], st_ref[l]["exp_avg_sq"]) <= 2 * tol, (l, "exp_avg_sq")
+    ex.close()
+
+
 def test_config1_adam_executor_and_checkpoint():
     from kan_amd import ResidentExecutor
     print("executor cfg1 adam", flush=True)

@@ -386,3 +386,76 @@ def test_config1_training_loop_matches_oracle():
     c_ref, losses_ref = orc.train_steps(x, y, [c0], steps=1000, loss="mse", optimizer="adam", lr=0.01)
     assert abs(losses[-1].item() - losses_ref[-1]) <= 1e-3 * max(losses_ref[0], 1e-6) + 1e-5
     assert _rel(m.cheby_coeffs.detach().cpu(), c_ref[0]) <= 1e-3
+
+
+@pytest.mark.parametrize("compute,tol", [("fp32", FP32_TOL), ("bf16", BF16_TOL)])
+def test_use_recurrence_layer_matches_recurrence_oracle(compute, tol):
+    """ChebyKANLayer(..., use_recurrence=True) (kan/basis/chebyshev.py:147-172,
+    dispatch at :114-117) against the oracle's recurrence path: y and dC.  The
+    reference's recurrence writes slices in place, so autograd cannot give its
+    dx; dx is checked against the closed-form oracle instead."""
+    import kan_amd
+    B, I, O, deg = 384, 96, 80, 8
+    print(f"use_recurrence layer {compute}", flush=True)
+    torch.manual_seed(31)
+    m = kan_amd.ChebyKANLayer(I, O, deg, use_recurrence=True, compute=compute)
+    assert m.basis.use_recurrence
+    c = m.cheby_coeffs.detach().clone()
+    g = torch.Generator().manual_seed(32)
+    x = torch.randn(B, I, generator=g) * 1.5
+    dy = torch.randn(B, O, generator=g)
+    c_ref = c.to(torch.bfloat16).float() if compute == "bf16" else c
+    y_ref, _, dc_ref = orc.layer_forward_backward(x, c_ref, dy, need_dx=False, use_recurrence=True)
+    _, dx_ref, _ = orc.layer_forward_backward(x, c_ref, dy)
+    m = m.cuda()
+    xd = x.cuda().requires_grad_(True)
+    y = m(xd)
+    y.backward(dy.cuda())
+    assert _rel(y.detach().cpu(), y_ref) <= tol
+    assert _rel(m.cheby_coeffs.grad.cpu(), dc_ref) <= tol
+    assert _rel(xd.grad.cpu(), dx_ref) <= tol
+
+
+def test_use_recurrence_at_saturation_is_exact_and_finite():
+    """At |x| >= 9.0108 fp32 tanh(x) is exactly +-1, where the recurrence
+    gives T_n(+-1) = (+-1)^n exactly; y and dC match the recurrence oracle and
+    dx is the finite analytic limit (the reference gives no dx there)."""
+    import kan_amd
+    torch.manual_seed(33)
+    m = kan_amd.ChebyKANLayer(3, 4, 7, use_recurrence=True)
+    c = m.cheby_coeffs.detach().clone()
+    x = torch.tensor([[9.5, -12.0, 0.3], [20.0, 1.0, -9.2], [0.0, -30.0, 10.0]])
+    dy = torch.randn(3, 4, generator=torch.Generator().manual_seed(34))
+    y_ref, _, dc_ref = orc.layer_forward_backward(x, c, dy, need_dx=False, use_recurrence=True)
+    m = m.cuda()
+    xd = x.cuda().requires_grad_(True)
+    y = m(xd)
+    y.backward(dy.cuda())
+    assert _rel(y.detach().cpu(), y_ref) <= FP32_TOL
+    assert _rel(m.cheby_coeffs.grad.cpu(), dc_ref) <= FP32_TOL
+    dx64, _ = orc.backward_fp64(x.numpy(), c.numpy(), dy.numpy())
+    assert torch.isfinite(xd.grad).all()
+    assert np.allclose(xd.grad.cpu().numpy(), dx64, rtol=1e-4, atol=1e-6)
+
+
+def test_adam_resumes_from_a_torch_optim_checkpoint():
+    """kan_amd.optim.Adam continues a torch.optim.Adam run from its
+    state_dict (step stored as a float tensor) on the device."""
+    from kan_amd import optim
+    g = torch.Generator().manual_seed(35)
+    p0 = torch.randn(500, generator=g)
+    grads = [torch.randn(500, generator=g) for _ in range(4)]
+    pr = p0.clone().requires_grad_(True)
+    ref = torch.optim.Adam([pr], lr=0.01)
+    for gr in grads[:2]:
+        pr.grad = gr.clone()
+        ref.step()
+    pd = pr.detach().clone().cuda().requires_grad_(True)
+    ours = optim.Adam([pd], lr=0.01)
+    ours.load_state_dict(ref.state_dict())
+    for gr in grads[2:]:
+        pr.grad = gr.clone()
+        ref.step()
+        pd.grad = gr.cuda()
+        ours.step()
+    assert torch.allclose(pd.detach().cpu(), pr.detach(), rtol=0, atol=1e-6)

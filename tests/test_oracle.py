@@ -197,3 +197,100 @@ def test_train_steps_cfg1_decreases_loss():
     c = orc.init_coeffs(1, 1, 8, seed=0)
     _, losses = orc.train_steps(x, y, [c], steps=200, loss="mse", optimizer="adam", lr=0.01)
     assert losses[-1] < 0.25 * losses[0]
+
+
+def _mlp_grads_fp64(x, coeffs, target, loss):
+    """fp64 loss and coefficient gradients of a ChebyKAN stack, chained by hand
+    through backward_fp64 (independent of torch autograd)."""
+    hs = [np.asarray(x, dtype=np.float64)]
+    for c in coeffs:
+        hs.append(orc.forward_fp64(hs[-1], c.numpy()))
+    y = hs[-1]
+    B, O = y.shape
+    if loss == "mse":
+        t = target.double().numpy()
+        lval = ((y - t) ** 2).mean()
+        dy = 2.0 * (y - t) / (B * O)
+    else:
+        lab = target.numpy()
+        z = y - y.max(1, keepdims=True)
+        p = np.exp(z) / np.exp(z).sum(1, keepdims=True)
+        lval = -np.log(p[np.arange(B), lab]).mean()
+        dy = p.copy()
+        dy[np.arange(B), lab] -= 1.0
+        dy /= B
+    grads = [None] * len(coeffs)
+    for l in range(len(coeffs) - 1, -1, -1):
+        dh, grads[l] = orc.backward_fp64(hs[l], coeffs[l].numpy(), dy)
+        dy = dh
+    return lval, grads
+
+
+@pytest.mark.parametrize("loss", ["mse", "ce"])
+@pytest.mark.parametrize("wd", [0.0, 0.3])
+def test_train_steps_one_sgd_step_closed_form(loss, wd):
+    """One step of the loop is C1 = C0 - lr (dC + wd C0), with dC the fp64
+    analytic gradient of the mean-reduced loss.  A missing zero_grad, a sum
+    instead of a mean, or a dropped layer gradient fails this."""
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(24, 6, generator=g)
+    coeffs = [torch.randn(6, 5, 4, generator=g) * 0.2, torch.randn(5, 3, 6, generator=g) * 0.2]
+    target = torch.randn(24, 3, generator=g) if loss == "mse" else torch.randint(0, 3, (24,), generator=g)
+    lr = 0.05
+    lval, grads = _mlp_grads_fp64(x, coeffs, target, loss)
+    c1, losses = orc.train_steps(x, target, coeffs, steps=1, loss=loss, optimizer="sgd", lr=lr,
+                                 weight_decay=wd)
+    assert abs(losses[0] - lval) <= 1e-5 * abs(lval)
+    for l in range(2):
+        want = coeffs[l].double().numpy() - lr * (grads[l] + wd * coeffs[l].double().numpy())
+        delta = c1[l].double().numpy() - coeffs[l].double().numpy()
+        dwant = want - coeffs[l].double().numpy()
+        assert np.linalg.norm(delta - dwant) <= 1e-5 * np.linalg.norm(dwant)
+    # two steps: the second gradient is taken at C1 (not accumulated onto the first)
+    c2, _ = orc.train_steps(x, target, coeffs, steps=2, loss=loss, optimizer="sgd", lr=lr,
+                            weight_decay=wd)
+    _, grads1 = _mlp_grads_fp64(x, c1, target, loss)
+    for l in range(2):
+        dwant = -lr * (grads1[l] + wd * c1[l].double().numpy())
+        delta = c2[l].double().numpy() - c1[l].double().numpy()
+        assert np.linalg.norm(delta - dwant) <= 1e-4 * np.linalg.norm(dwant)
+
+
+def test_train_steps_one_adam_step_closed_form():
+    """Adam's first step: m = (1-b1) g, v = (1-b2) g^2, so
+    C1 = C0 - lr g / (|g| + eps) elementwise; the returned state holds m, v."""
+    g = torch.Generator().manual_seed(12)
+    x = torch.randn(32, 5, generator=g)
+    coeffs = [torch.randn(5, 4, 9, generator=g) * 0.1]
+    target = torch.randn(32, 4, generator=g)
+    lr, eps = 0.01, 1e-3
+    _, grads = _mlp_grads_fp64(x, coeffs, target, "mse")
+    c1, _, state = orc.train_steps(x, target, coeffs, steps=1, loss="mse", optimizer="adam", lr=lr,
+                                   eps=eps, return_state=True)
+    gr = grads[0]
+    want = coeffs[0].double().numpy() - lr * gr / (np.abs(gr) + eps)
+    assert np.abs(c1[0].double().numpy() - want).max() <= 1e-6
+    assert np.allclose(state[0]["exp_avg"].double().numpy(), 0.1 * gr, rtol=1e-4, atol=1e-9)
+    assert np.allclose(state[0]["exp_avg_sq"].double().numpy(), 0.001 * gr * gr, rtol=1e-3,
+                       atol=1e-14)
+    assert float(state[0]["step"]) == 1.0
+
+
+def test_train_steps_bf16_coeffs_rounds_the_operand_only():
+    """bf16_coeffs: the forward uses bf16(C) (round to nearest even), and the
+    fp32 master receives the gradient taken at bf16(C) unchanged."""
+    g = torch.Generator().manual_seed(13)
+    x = torch.randn(16, 4, generator=g)
+    c = [torch.randn(4, 3, 6, generator=g) * 0.3 + 1e-3]
+    target = torch.randn(16, 3, generator=g)
+    cr = [c[0].to(torch.bfloat16).float()]
+    assert not torch.equal(cr[0], c[0])
+    y = orc.mlp_forward(x, c, bf16_coeffs=True)
+    assert np.allclose(y.double().numpy(), orc.forward_fp64(x.numpy(), cr[0].numpy()), rtol=1e-5,
+                       atol=1e-6)
+    lr = 0.1
+    _, grads = _mlp_grads_fp64(x, cr, target, "mse")
+    c1, _ = orc.train_steps(x, target, c, steps=1, loss="mse", optimizer="sgd", lr=lr,
+                            bf16_coeffs=True)
+    delta = c1[0].double().numpy() - c[0].double().numpy()
+    assert np.linalg.norm(delta + lr * grads[0]) <= 1e-5 * np.linalg.norm(lr * grads[0])
