@@ -82,7 +82,9 @@ class Adam(torch.optim.Optimizer):
                 for k in ("exp_avg", "exp_avg_sq"):
                     if st[k].device != p.device or not st[k].is_contiguous():
                         st[k] = st[k].to(p.device, torch.float32).contiguous()
-                st["step"] += 1
+                # rebind rather than add in place: a loaded state_dict may share
+                # this tensor with the optimizer it came from
+                st["step"] = st["step"] + 1
                 step = int(st["step"].item())
                 g = p.grad.contiguous()
                 _lib.check(lib.ckan_adam_step(

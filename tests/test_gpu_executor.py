@@ -117,7 +117,14 @@ def test_adam_with_weight_decay_applied_by_dc_kernels(widths, degrees, B, comput
     count, through every dC write path."""
     from kan_amd import ResidentExecutor
     print(f"executor adam wd {widths} {degrees} B={B} {compute} {loss}", flush=True)
-    lr, wd, steps = 0.01, 0.3, 3
+    bf = compute == "bf16"
+    # lr 1e-3: Adam moves every coefficient by ~lr per step, tens of times the
+    # init scale 1/(in * D).  At lr 0.01 the config-2 shape drives layer-2
+    # inputs past |x| = 9.01 within two steps, where the reference's backward
+    # is NaN by design, and at the bf16 shape merely rounding the coefficients
+    # to bf16 moves the oracle's own 3-step trajectory by 17 % (eps 0.1 x the
+    # median gradient); with eps = the median gradient it moves 0.3 %.
+    lr, wd, steps = 1e-3, 0.3, 3
     g = torch.Generator().manual_seed(9)
     x = torch.rand(B, widths[0], generator=g) * 4 - 2
     if loss == "mse":
@@ -125,32 +132,39 @@ def test_adam_with_weight_decay_applied_by_dc_kernels(widths, degrees, B, comput
     else:
         y = torch.randint(0, widths[-1], (B,), generator=g)
     coeffs = _make(widths, degrees, 90)
-    bf = compute == "bf16"
     # eps near the gradients' scale keeps Adam's update Lipschitz in the
     # gradient, so the gradient's rounding (bf16 above all) stays visible at
     # its own size rather than as sign flips of near-zero entries
     c_sgd, _ = orc.train_steps(x, y, coeffs, steps=1, loss=loss, optimizer="sgd", lr=1.0,
                                bf16_coeffs=bf)
     g0 = [c0 - c1 for c0, c1 in zip(coeffs, c_sgd)]  # first-step gradients (lr = 1)
-    eps = 0.1 * min(float(d.abs().median()) for d in g0)
-    c_ref, _, st_ref = orc.train_steps(x, y, coeffs, steps=steps, loss=loss, optimizer="adam", lr=lr,
-                                       weight_decay=wd, eps=eps, bf16_coeffs=bf, return_state=True)
+    eps = (1.0 if bf else 0.1) * min(float(d.abs().median()) for d in g0)
     ex = ResidentExecutor(widths, degrees, B, compute=compute, loss=loss, optimizer="adam", lr=lr,
                           eps=eps, weight_decay=wd)
     for l, c in enumerate(coeffs):
         ex.set_coeffs(l, c)
     xd, yd = x.cuda(), y.cuda()
-    for _ in range(steps):
-        ex.step(xd, yd)
-    sd = ex.state_dict()
-    assert sd["step"] == steps
-    tol = 1e-4 if compute == "fp32" else 2e-2
-    for l in range(len(degrees)):
-        d_got = sd[f"{l}.cheby_coeffs"].double() - coeffs[l].double()
-        d_want = c_ref[l].double() - coeffs[l].double()
-        assert _rel(d_got, d_want) <= tol, (l, "C", _rel(d_got, d_want))
-        assert _rel(sd[f"{l}.exp_avg"], st_ref[l]["exp_avg"]) <= tol, (l, "exp_avg")
-        assert _rel(sd[f"{l}.exp_avg_sq"], st_ref[l]["exp_avg_sq"]) <= 2 * tol, (l, "exp_avg_sq")
+    # step 1 at the layer's own bar (exp_avg is then exactly 0.1 * (g + wd C0)),
+    # the 3-step trajectory with room for rounding differences compounding
+    done = 0
+    for k, tol in ((1, 2e-5 if not bf else 2e-2), (steps, 5e-4 if not bf else 3e-2)):
+        while done < k:
+            ex.step(xd, yd)
+            done += 1
+        c_ref, _, st_ref = orc.train_steps(x, y, coeffs, steps=k, loss=loss, optimizer="adam", lr=lr,
+                                           weight_decay=wd, eps=eps, bf16_coeffs=bf,
+                                           return_state=True)
+        assert all(torch.isfinite(c).all() for c in c_ref)  # no saturation NaN in the oracle
+        sd = ex.state_dict()
+        assert sd["step"] == k
+        for l in range(len(degrees)):
+            d_got = sd[f"{l}.cheby_coeffs"].double() - coeffs[l].double()
+            d_want = c_ref[l].double() - coeffs[l].double()
+            assert _rel(d_got, d_want) <= tol, (k, l, "C", _rel(d_got, d_want))
+            r_m = _rel(sd[f"{l}.exp_avg"], st_ref[l]["exp_avg"])
+            r_v = _rel(sd[f"{l}.exp_avg_sq"], st_ref[l]["exp_avg_sq"])
+            assert r_m <= tol, (k, l, "exp_avg", r_m)
+            assert r_v <= 2 * tol, (k, l, "exp_avg_sq", r_v)
     ex.close()
 
 

@@ -8,6 +8,7 @@ Tolerances (norm-wise, ||a - b|| / ||b||):
 Inputs keep |x| < 9 so the reference's saturation NaN (|x| >= 9.0108) does
 not arise; that divergence is tested separately.
 """
+import io
 import math
 
 import numpy as np
@@ -452,7 +453,10 @@ def test_adam_resumes_from_a_torch_optim_checkpoint():
         ref.step()
     pd = pr.detach().clone().cuda().requires_grad_(True)
     ours = optim.Adam([pd], lr=0.01)
-    ours.load_state_dict(ref.state_dict())
+    buf = io.BytesIO()  # through a checkpoint file, as a resume would
+    torch.save(ref.state_dict(), buf)
+    buf.seek(0)
+    ours.load_state_dict(torch.load(buf, weights_only=True))
     for gr in grads[2:]:
         pr.grad = gr.clone()
         ref.step()
