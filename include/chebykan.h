@@ -90,6 +90,20 @@ int ckan_pack_coeffs(const ckan_desc* desc, const void* coeffs, void* packed, vo
 int ckan_forward(const ckan_desc* desc, const float* x, const void* packed, float* y,
                  float* t_cache, void* ws, size_t ws_bytes, void* stream);
 
+/* ckan_forward without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops and
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  The
+ * split-K partials of the small-batch paths go to a fixed device array of
+ * CKAN_NOALLOC_SCRATCH_BYTES, one per GPU, held until the process ends; the
+ * call allocates nothing (no hipMalloc / hipFree).  Shapes whose
+ * ckan_fwd_workspace_bytes exceeds that size return CKAN_ERR_WORKSPACE and
+ * launch nothing.  Every call on one GPU shares that GPU's array, so calls that
+ * overlap in time on one GPU (e.g. on two streams) race; calls in one stream
+ * order are safe.  Results are identical to ckan_forward's. */
+#define CKAN_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
+int ckan_forward_noalloc(const ckan_desc* desc, const float* x, const void* packed, float* y,
+                         float* t_cache, void* stream);
+
 /* Gradients of the forward for upstream gradient dy [B, out]:
  *   dx[b, i]    = (1 - t^2) sum_{o, d} dy[b, o] C[i, o, d] d U_{d-1}(t)   (dx may be NULL)
  *   dC[i, o, d] = sum_b T_d(t[b, i]) dy[b, o]                            (dcoeffs may be NULL)

@@ -22,6 +22,8 @@ CKAN_ERR_INVALID_ARG = 1
 CKAN_ERR_UNSUPPORTED = 2
 CKAN_ERR_WORKSPACE = 3
 CKAN_ERR_HIP = 4
+# size of the fixed device scratch of ckan_forward_noalloc (include/chebykan.h)
+CKAN_NOALLOC_SCRATCH_BYTES = 16 << 20
 
 CKAN_COMPUTE_FP32 = 0
 CKAN_COMPUTE_BF16 = 1
@@ -88,6 +90,7 @@ SIGNATURES = {
     "ckan_workspace_init": (ctypes.c_int, [_vp, _sz, _vp]),
     "ckan_pack_coeffs": (ctypes.c_int, [_pdesc, _vp, _vp, _vp]),
     "ckan_forward": (ctypes.c_int, [_pdesc, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "ckan_forward_noalloc": (ctypes.c_int, [_pdesc, _vp, _vp, _vp, _vp, _vp]),
     "ckan_backward": (ctypes.c_int, [_pdesc, _vp, _vp, _vp, _vp, _vp, ctypes.c_int, _vp, _sz, _vp]),
     "ckan_forward_f64": (ctypes.c_int, [_pdesc, _vp, _vp, _vp, _vp, _vp]),
     "ckan_backward_f64": (ctypes.c_int, [_pdesc, _vp, _vp, _vp, _vp, _vp, ctypes.c_int, _vp]),

@@ -99,6 +99,40 @@ inline bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr
 
 }  // namespace
 
+// ---- fixed scratch of the allocation-free forward ---------------------------
+// Each GPU the library runs on holds one copy of this array until the process
+// ends.  Host code never passes `scratch` itself to a kernel (on the host the
+// name is only a stand-in for the device symbol): the device address is looked
+// up once per device by hipGetSymbolAddress, with that device current, and
+// kept in g_scratch_ptr.
+static __device__ __align__(256) char scratch[CKAN_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's address of `scratch`.
+int scratch_ptr(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(CKAN_ERR_HIP, "hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(CKAN_ERR_UNSUPPORTED, "device %d: at most %d devices are supported", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return fail(CKAN_ERR_HIP, "hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                  hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return CKAN_OK;
+}
+}  // namespace
+
 void ckan::set_last_error(const char* msg) { g_err = msg; }
 
 int ckan::backward_impl(const ckan_desc* desc, const float* t_cache, const void* packed,
@@ -245,6 +279,25 @@ int ckan_forward(const ckan_desc* desc, const float* x, const void* packed, floa
     launch_fwd_gemm(x, t_cache, packed, y, ws, p, c, s);
   }
   return check_launch("fwd_gemm");
+}
+
+int ckan_forward_noalloc(const ckan_desc* desc, const float* x, const void* packed, float* y,
+                         float* t_cache, void* stream) {
+  int rc = validate_desc(desc);
+  if (rc) return rc;
+  const Plan p = plan_of(desc);
+  if (p.B == 0) return CKAN_OK;
+  const size_t need = fwd_ws_bytes(p, choose_fwd(p));
+  if (need > CKAN_NOALLOC_SCRATCH_BYTES)
+    return fail(CKAN_ERR_WORKSPACE,
+                "forward_noalloc: this shape needs %zu bytes of scratch, above the fixed %zu",
+                need, (size_t)CKAN_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  if (need > 0 && (rc = scratch_ptr(&ws))) return rc;
+  // the split-K partials are written before they are read: nothing in the
+  // scratch needs clearing between calls
+  return ckan_forward(desc, x, packed, y, t_cache, ws, need > 0 ? (size_t)CKAN_NOALLOC_SCRATCH_BYTES : 0,
+                      stream);
 }
 
 int ckan_backward(const ckan_desc* desc, const float* t_cache, const void* packed,
