@@ -44,6 +44,22 @@ def _step(layer, x, dy):
     y.backward(dy)
 
 
+def _settle(layer, x, dy, seconds):
+    """Untimed steps until `seconds` of wall time have passed: the GPU leaves
+    its idle clock state and the caches reach the loop's steady state before
+    the warm-up and timed steps.  Returns (steps, seconds) for the JSON line."""
+    import torch
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        for _ in range(10):
+            _step(layer, x, dy)
+        n += 10
+        torch.cuda.synchronize()
+        if time.perf_counter() - t0 >= seconds:
+            return n, time.perf_counter() - t0
+
+
 def _time_gpu(layer, x, dy, steps, warmup):
     import torch
     for _ in range(warmup):
@@ -93,8 +109,9 @@ SUITE = ("cfg1", "cfg2", "cfg4", "cfg5", "families", "fp64")
 PEAK_FP64_TFLOPS = 78.6     # MI355X dense fp64
 
 
-def _suite(only=SUITE):
-    """Secondary BASELINE configs (1, 2, 4, 5) and the other bases; each takes well under a minute."""
+def _suite(only=SUITE, cpu=True):
+    """Secondary BASELINE configs (1, 2, 4, 5) and the other bases; each takes well under a minute.
+    With `cpu`, configs 1, 2, 4 and 5 carry the oracle's CPU timing on this host beside the GPU's."""
     import ctypes
     import math
     import torch
@@ -121,6 +138,16 @@ def _suite(only=SUITE):
                        "us_per_step": res1["eager"][0] * 1e3, "steps": 1000,
                        "final_loss": res1["eager"][1],
                        "us_per_step_hip_graph": res1["graph"][0] * 1e3}
+        if cpu:
+            cores = _cpu_threads()
+            xc, yc = x1.cpu(), y1.cpu()
+            torch.manual_seed(0)
+            t, n, spent = _cpu_train([1, 1], [8], xc, yc, "mse", "adam", 0.01, 10, 2.0)
+            out["cfg1"]["cpu_baseline"] = {
+                "value": 1e6 * t, "unit": "us/step", "cores": cores, "kind": "port",
+                "sample": f"the full config (100 points, Adam step), median of {n} steps after 1 warm-up "
+                          f"({spent:.1f} s of CPU work)",
+                "gpu_speedup": t * 1e6 / out["cfg1"]["us_per_step"]}
 
     if "cfg2" in only:
         # config 2: 784->64->10, deg 4, fp32, B=256, CE + SGD lr 0.01
@@ -140,6 +167,16 @@ def _suite(only=SUITE):
                        "us_per_step": ms * 1e3, "samples_per_s": 256 / (ms * 1e-3),
                        "tflops": 2.618e8 / (ms * 1e-3) / 1e12,
                        "us_per_step_hip_graph": res2["graph"] * 1e3}
+        if cpu:
+            cores = _cpu_threads()
+            torch.manual_seed(2)
+            t, n, spent = _cpu_train([784, 64, 10], [4, 4], x2.cpu(), l2.cpu(), "ce", "sgd", 0.01, 10, 2.0)
+            out["cfg2"]["cpu_baseline"] = {
+                "value": 256 / t, "unit": "samples/s", "us_per_step": 1e6 * t, "cores": cores,
+                "kind": "port",
+                "sample": f"the full config (B=256, CE + SGD step), median of {n} steps after 1 warm-up "
+                          f"({spent:.1f} s of CPU work)",
+                "gpu_speedup": t * 1e3 / ms}
 
     if "cfg4" in only:
         # config 4: 512->512->512->512->64, deg 16, B=65536, fp32 masters + bf16 compute, MSE + SGD, 100 steps
@@ -159,41 +196,102 @@ def _suite(only=SUITE):
                        "frac_bf16_peak": 4.8920e12 / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS,
                        "final_loss": float(ex.step(x4, t4).item())}
         ex.close()
+        if cpu:
+            # one warm-up step on 4096 rows, then one timed step at the full 65536
+            # rows (the per-step cost of 100 steps is 100 x this one)
+            import torch.nn.functional as F
+            from oracle import chebykan_oracle as orc
+            cores = _cpu_threads()
+            xc, tc4 = x4.cpu(), t4.cpu()
+            torch.manual_seed(4)
+            ps = [orc.init_coeffs(a, b, 16).requires_grad_(True)
+                  for a, b in [(512, 512), (512, 512), (512, 512), (512, 64)]]
+            opt = torch.optim.SGD(ps, lr=0.01)
+
+            def step4(xs, ts):
+                opt.zero_grad()
+                F.mse_loss(orc.mlp_forward(xs, ps), ts).backward()
+                opt.step()
+            step4(xc[:4096], tc4[:4096])
+            t0 = time.perf_counter()
+            step4(xc, tc4)
+            t = time.perf_counter() - t0
+            del xc, tc4, ps, opt
+            out["cfg4"]["cpu_baseline"] = {
+                "value": 65536 / t, "unit": "samples/s", "s_per_step": t,
+                "s_per_100_steps_extrapolated": 100 * t, "cores": cores, "kind": "port",
+                "sample": "one full step (B=65536, MSE + SGD) after one 4096-row warm-up step; the "
+                          "100-step figure is 100 x that step (extrapolated, not run)",
+                "gpu_speedup": t * 1e3 / ms}
 
     if "cfg5" in only:
-        # config 5: 2048->2048 deg 8, bf16 coefficients packed once, forward at B = 1, 16, 64
+        # config 5: 2048->2048 deg 8, bf16 coefficients packed once, forward at B = 1, 16, 64.
+        # "warm": the same packed coefficients every call (75.5 MB, inside the 256 MB
+        # Infinity Cache after the first); "cold": calls rotate over NROT packed copies
+        # whose forward operands total more than that cache, so each call streams its
+        # coefficients from HBM.
         L = _lib.load()
         I5 = O5 = 2048
+        NROT = 6
         g = torch.Generator().manual_seed(5)
-        c5 = (torch.randn(I5, O5, 9, generator=g) / (I5 * 9)).bfloat16().to(dev)
+        c5 = (torch.randn(I5, O5, 9, generator=g) / (I5 * 9)).bfloat16()
         res5 = {}
+        packs = None
         for B5 in (1, 16, 64):
             d = _lib.make_desc(B5, I5, O5, 8, _lib.CKAN_COMPUTE_BF16, _lib.CKAN_DTYPE_BF16)
             st = _lib.stream_ptr(dev)
-            packed = torch.empty(L.ckan_packed_bytes(d), dtype=torch.uint8, device=dev)
-            _lib.check(L.ckan_pack_coeffs(d, c5.data_ptr(), packed.data_ptr(), st))
+            if packs is None:  # the packed layout does not depend on the batch
+                cdev = c5.to(dev)
+                packs = []
+                for _ in range(NROT):
+                    pk = torch.empty(L.ckan_packed_bytes(d), dtype=torch.uint8, device=dev)
+                    _lib.check(L.ckan_pack_coeffs(d, cdev.data_ptr(), pk.data_ptr(), st))
+                    packs.append(pk)
+                del cdev
             x5 = torch.randn(B5, I5, generator=g).to(dev)
             y5 = torch.empty(B5, O5, device=dev)
             t5 = torch.empty(L.ckan_tcache_elems(d), device=dev)
             wsb = L.ckan_fwd_workspace_bytes(d)
             ws = torch.zeros(max(wsb, 256), dtype=torch.uint8, device=dev)
-            fwd = lambda: _lib.check(L.ckan_forward(d, x5.data_ptr(), packed.data_ptr(), y5.data_ptr(),
-                                                    t5.data_ptr(), ws.data_ptr(), wsb, st))
-            ms = _time_loop(fwd, 200, 20)
-            _lib.profile_report()
-            _lib.profile_enable(True)
-            for _ in range(50):
-                fwd()
-            torch.cuda.synchronize()
-            _lib.profile_enable(False)
-            rep = _lib.profile_report()
-            gemm_ms = rep["fwd_gemm"][1] / rep["fwd_gemm"][0]
+            k = [0]
+
+            def fwd(rotate):
+                pk = packs[k[0] % NROT] if rotate else packs[0]
+                k[0] += 1
+                _lib.check(L.ckan_forward(d, x5.data_ptr(), pk.data_ptr(), y5.data_ptr(),
+                                          t5.data_ptr(), ws.data_ptr(), wsb, st))
             alg_bytes = I5 * O5 * 9 * 2 + B5 * I5 * 4 + B5 * O5 * 4
-            res5[f"B{B5}"] = {"us_forward": ms * 1e3, "us_gemm": gemm_ms * 1e3,
-                              "gemm_GBps": alg_bytes / (gemm_ms * 1e-3) / 1e9,
-                              "frac_hbm_peak": alg_bytes / (gemm_ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
-                              "alg_bytes": alg_bytes}
-        out["cfg5"] = {"workload": "ChebyKANLayer(2048,2048,8) inference, bf16 coefficients (packed once)",
+            ent = {"alg_bytes": alg_bytes}
+            for mode, rot in (("warm", False), ("cold", True)):
+                ms = _time_loop(lambda: fwd(rot), 300, 30)
+                _lib.profile_report()
+                _lib.profile_enable(True)
+                for _ in range(60):
+                    fwd(rot)
+                torch.cuda.synchronize()
+                _lib.profile_enable(False)
+                rep = _lib.profile_report()
+                gemm_ms = rep["fwd_gemm"][1] / rep["fwd_gemm"][0]
+                ent[mode] = {"us_forward": ms * 1e3, "us_gemm": gemm_ms * 1e3,
+                             "gemm_GBps": alg_bytes / (gemm_ms * 1e-3) / 1e9,
+                             "frac_hbm_peak": alg_bytes / (gemm_ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
+                             "forward_GBps": alg_bytes / (ms * 1e-3) / 1e9}
+            if cpu:
+                from oracle import chebykan_oracle as orc
+                cores = _cpu_threads()
+                xc, cc = x5.cpu(), c5.float()
+                t, n, spent = _cpu_median(lambda: orc.layer_forward(xc, cc), 3, 1.5, 50)
+                ent["cpu_baseline"] = {
+                    "value": B5 / t, "unit": "samples/s", "ms_per_forward": 1e3 * t, "cores": cores,
+                    "kind": "port",
+                    "sample": f"the full forward at B={B5} (fp32 math on the bf16-rounded coefficients), "
+                              f"median of {n} calls after 1 warm-up ({spent:.1f} s of CPU work)",
+                    "gpu_speedup_cold": t * 1e3 / ent["cold"]["us_forward"] * 1e3}
+            res5[f"B{B5}"] = ent
+        del packs
+        out["cfg5"] = {"workload": "ChebyKANLayer(2048,2048,8) inference, bf16 coefficients (packed once); "
+                                   f"warm = one packed copy, cold = {NROT} copies rotated (forward "
+                                   "operands above the 256 MB Infinity Cache)",
                        **res5}
 
     if "families" in only:
@@ -236,46 +334,86 @@ def _suite(only=SUITE):
     return out
 
 
+def _cpu_info():
+    """The host the CPU baselines ran on: nproc, the CPUs this process may use,
+    the threads torch runs with, and lscpu's identification of the part."""
+    import subprocess
+    import torch
+    info = {"nproc": os.cpu_count(), "affinity_cpus": len(os.sched_getaffinity(0)),
+            "threads": torch.get_num_threads()}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20).stdout
+        for line in out.splitlines():
+            key, _, val = line.partition(":")
+            key = key.strip()
+            if key in ("Model name", "CPU family", "Model", "Stepping", "Socket(s)",
+                       "Core(s) per socket", "Thread(s) per core", "Vendor ID"):
+                info["lscpu " + key] = val.strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return info
+
+
+def _cpu_threads():
+    import torch
+    torch.set_num_threads(len(os.sched_getaffinity(0)) or 1)
+    return torch.get_num_threads()
+
+
+def _cpu_median(fn, min_reps, min_seconds, max_reps=1000):
+    """One warm-up call, then at least `min_reps` timed calls and about
+    `min_seconds` of work; returns (median seconds, calls timed, seconds spent)."""
+    fn()
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < min_reps or (time.perf_counter() - t_start < min_seconds and len(times) < max_reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times), time.perf_counter() - t_start
+
+
 def _cpu_baseline(sample_rows: int, reps: int):
+    """Config 3 on the CPU: the oracle's op-for-op restatement of the reference
+    layer (forward + autograd backward, dx and dC) on a sample of the rows."""
     import torch
     from oracle import chebykan_oracle as orc
-    torch.set_num_threads(os.cpu_count() or 1)
+    cores = _cpu_threads()
     g = torch.Generator().manual_seed(1234)
     x = torch.randn(sample_rows, I, generator=g)
     c = torch.randn(I, O, DEG + 1, generator=g) / (I * (DEG + 1))
     dy = torch.randn(sample_rows, O, generator=g)
-    orc.layer_forward_backward(x, c, dy)  # warm-up
-    times = []
-    t_start = time.perf_counter()
-    # at least `reps` steps, and about 10 s of CPU work in all
-    while len(times) < reps or time.perf_counter() - t_start < 10.0:
-        t0 = time.perf_counter()
-        orc.layer_forward_backward(x, c, dy)
-        times.append(time.perf_counter() - t0)
-        if len(times) >= 1000:
-            break
-    t = statistics.median(times)
-    model = "unknown CPU"
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    model = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
+    t, n, spent = _cpu_median(lambda: orc.layer_forward_backward(x, c, dy), reps, 10.0)
     return {
         "value": sample_rows / t,
         "unit": "samples/s",
-        "cores": torch.get_num_threads(),
+        "cores": cores,
         "kind": "port",
-        "cpu_model": model,
+        "host": _cpu_info(),
         "sample": (f"config-3 layer (1024->1024, deg 8) fwd+bwd(dx,dC) on {sample_rows} of the "
                    f"8192 rows, fp32 torch CPU op-for-op restatement of "
-                   f"kan/basis/chebyshev.py:78,92-101,130-145 + autograd; median of {len(times)} "
-                   f"steps after 1 warm-up ({t * 1e3:.1f} ms/step, "
-                   f"{time.perf_counter() - t_start:.1f} s of CPU work)"),
+                   f"kan/basis/chebyshev.py:78,92-101,130-145 + autograd; median of {n} "
+                   f"steps after 1 warm-up ({t * 1e3:.1f} ms/step, {spent:.1f} s of CPU work)"),
     }
+
+
+def _cpu_train(widths, degrees, x, target, loss, optimizer, lr, min_reps, min_seconds):
+    """Median CPU time of one reference training step (README.md:61-69 over a
+    KANSequential): zero_grad, the oracle's forward, torch's loss, backward and
+    torch.optim's step."""
+    import torch
+    import torch.nn.functional as F
+    from oracle import chebykan_oracle as orc
+    ps = [orc.init_coeffs(widths[l], widths[l + 1], degrees[l]).requires_grad_(True)
+          for l in range(len(degrees))]
+    opt = (torch.optim.Adam if optimizer == "adam" else torch.optim.SGD)(ps, lr=lr)
+    lossf = F.mse_loss if loss == "mse" else F.cross_entropy
+
+    def step():
+        opt.zero_grad()
+        lossf(orc.mlp_forward(x, ps), target).backward()
+        opt.step()
+    return _cpu_median(step, min_reps, min_seconds)
 
 
 def _traffic(kernel: str, compute: str):
@@ -296,7 +434,10 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--settle-s", type=float, default=1.0,
+                    help="untimed steps for this many seconds before the warm-up (0: none); "
+                         "reported in the JSON line")
     ap.add_argument("--compute", default="bf16", choices=["bf16", "fp32"])
     ap.add_argument("--cpu-rows", type=int, default=1024)
     ap.add_argument("--cpu-reps", type=int, default=3)
@@ -336,6 +477,7 @@ def main():
         torch.cuda.synchronize()
         del src, dst
 
+    settle_steps, settle_s = _settle(layer, x, dy, args.settle_s) if args.settle_s > 0 else (0, 0.0)
     ms = _time_gpu(layer, x, dy, args.steps, args.warmup)
     kernels = _kernel_breakdown(layer, x, dy, args.steps)
 
@@ -383,6 +525,9 @@ def main():
             "frac": achieved / peak,
             "traffic": _traffic(dom, args.compute),
         },
+        "settle": {"steps": settle_steps, "seconds": round(settle_s, 3),
+                   "note": "untimed steps run before the warm-up steps, so the timed steps "
+                           "see the GPU's steady-state clocks rather than its idle state"},
         "kernels_avg_ms": {k: round(v["avg_ms"], 5) for k, v in kernels.items()},
         **extra,
     }
@@ -391,7 +536,7 @@ def main():
         unknown = set(only) - set(SUITE)
         if unknown:
             ap.error(f"unknown suite entries {sorted(unknown)}")
-        out["configs"] = _suite(only)
+        out["configs"] = _suite(only, cpu=not args.no_cpu)
     if not args.no_cpu:
         out["cpu_baseline"] = _cpu_baseline(args.cpu_rows, args.cpu_reps)
     print(json.dumps(out))

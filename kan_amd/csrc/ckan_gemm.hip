@@ -40,8 +40,8 @@ __device__ __forceinline__ float split_sum(const float* __restrict__ src, size_t
 // Block = 4 waves arranged WGM x WGN; wave tile NM x NN fragments of 32x32.
 // The reduction runs over super-groups (SG): SGI inputs = SGK k-blocks.
 // With gridDim.z > 1 the SGs are split over blocks; each block writes its
-// partial tile and the last block of a tile (atomic ticket) reduces them in
-// fixed split order and re-arms the ticket.
+// partial tile to the workspace and k_fwd_reduce, a separate launch, adds the
+// partials in fixed split order.
 template <int P, bool BF, int NM, int NN, int WGM, int WGN>
 __global__ void __launch_bounds__(256)
 k_fwd(const float* __restrict__ tc, const typename Elem<BF>::type* __restrict__ Cf,

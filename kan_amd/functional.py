@@ -13,9 +13,9 @@ from . import _lib
 
 _COMPUTE = {"fp32": _lib.CKAN_COMPUTE_FP32, "bf16": _lib.CKAN_COMPUTE_BF16}
 
-# Forward workspaces hold split-K tickets that must start at zero; the
-# library re-arms them at the end of every call.  One per (device, stream):
-# calls sharing a workspace must not overlap in time.
+# Forward workspaces hold the split-K partial tiles of the small-batch paths
+# (written before they are read, so never cleared).  One per (device,
+# stream): calls sharing a workspace must not overlap in time.
 _fwd_ws = {}
 _fwd_ws_lock = threading.Lock()
 

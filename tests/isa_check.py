@@ -12,7 +12,7 @@ checks that every path into every vector memory instruction has them: it walks
 backwards through the fall-through predecessor and every branch to a label,
 counting one state per instruction and N + 1 per ``s_nop N``.
 
-Usage:  python -m kan_amd.isa_check file.s [...]   (exit status 1 on a finding)
+Usage:  python tests/isa_check.py file.s [...]   (exit status 1 on a finding)
 """
 from __future__ import annotations
 

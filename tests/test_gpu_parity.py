@@ -147,7 +147,7 @@ def test_config5_small_batch_bf16_coeffs(B):
     torch.cuda.synchronize()
     y_ref = orc.layer_forward(x, c.float())
     assert _rel(y.cpu(), y_ref) <= BF16_TOL
-    # repeated calls reuse the split-K tickets; results must not drift
+    # repeated calls reuse the workspace's split-K partials; results must not drift
     y2 = F.chebykan(x.cuda(), c.cuda(), "bf16")
     torch.cuda.synchronize()
     assert torch.equal(y.cpu(), y2.cpu())

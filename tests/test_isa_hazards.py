@@ -1,7 +1,7 @@
 """CPU check of the compiled gfx950 device code: no vector memory instruction
 reads an SGPR fewer than 5 wait states after a VALU instruction wrote it
 (the hazard the library's inline-asm copies and loads must guard themselves;
-kan_amd/isa_check.py).  Compiles every library source to device assembly
+tests/isa_check.py).  Compiles every library source to device assembly
 with the build's flags (hipcc cross-compiles here, no GPU needed)."""
 import os
 import shutil
@@ -12,7 +12,7 @@ from concurrent.futures import ThreadPoolExecutor
 import pytest
 
 from kan_amd import build as kbuild
-from kan_amd import isa_check
+import isa_check
 
 
 def test_checker_finds_short_paths():
