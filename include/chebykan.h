@@ -264,7 +264,16 @@ typedef struct ckan_exec_config {
   int32_t optimizer;       /* ckan_optimizer                                */
   int32_t use_graph;       /* replay each step as a captured HIP graph      */
   float lr, beta1, beta2, eps, weight_decay;
+  int32_t flags;           /* ckan_exec_flags, 0 for the defaults           */
 } ckan_exec_config;
+
+typedef enum ckan_exec_flags {
+  /* A stack whose step is at most 2^18 multiply-adds (e.g. the README's
+   * ChebyKANLayer(1, 1, 8) on 100 points) runs each step as one launch of a
+   * single-workgroup kernel instead of the per-layer kernel sequence; this
+   * flag keeps the kernel sequence for such stacks too. */
+  CKAN_EXEC_NO_FUSED_SMALL = 1
+} ckan_exec_flags;
 
 /* Allocates every device buffer; coefficients start at zero (set them with
  * ckan_exec_set_coeffs).  `stream` orders the initialisation. */
@@ -284,6 +293,12 @@ int ckan_exec_set_adam_state(ckan_exec* ex, int32_t layer, const float* m, const
  * Writes the step's loss (fp32 scalar, device) to loss_out when non-NULL. */
 int ckan_exec_step(ckan_exec* ex, const float* x, const void* target, float* loss_out,
                    void* stream);
+/* `nsteps` training steps on the same x and target (the reference loop's
+ * full-batch epochs, README.md:61-69), issued from the library without a
+ * return to the caller between steps; step k's loss goes to losses[k] (fp32,
+ * device, nsteps entries) when losses is non-NULL.  Runs eagerly (no graph). */
+int ckan_exec_steps(ckan_exec* ex, const float* x, const void* target, int64_t nsteps,
+                    float* losses, void* stream);
 /* Forward only: y [batch, widths[n]] (fp32, device). */
 int ckan_exec_forward(ckan_exec* ex, const float* x, float* y, void* stream);
 

@@ -129,7 +129,11 @@ class CkanExecConfig(ctypes.Structure):
         ("beta2", ctypes.c_float),
         ("eps", ctypes.c_float),
         ("weight_decay", ctypes.c_float),
+        ("flags", ctypes.c_int32),
     ]
+
+
+CKAN_EXEC_NO_FUSED_SMALL = 1
 
 
 CKAN_LOSS_MSE = 0
@@ -147,6 +151,7 @@ SIGNATURES.update({
     "ckan_exec_set_adam_state": (ctypes.c_int, [_vp, _i32, _vp, _vp, _i64, _vp]),
     "ckan_exec_step": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp]),
     "ckan_exec_forward": (ctypes.c_int, [_vp, _vp, _vp, _vp]),
+    "ckan_exec_steps": (ctypes.c_int, [_vp, _vp, _vp, _i64, _vp, _vp]),
 })
 
 _lib = None

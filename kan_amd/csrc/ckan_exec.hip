@@ -108,6 +108,219 @@ k_copy_f32(const float* __restrict__ src, float* __restrict__ dst, int64_t n) {
     dst[q] = src[q];
 }
 
+// ---------------------------------------------------------------------------
+// Small stacks: one training step in one workgroup.  For a network whose whole
+// step is a few hundred thousand multiply-adds (config 1, the README loop,
+// is 1.8 thousand), the multi-kernel step costs ~10 launches of a few us
+// each while the arithmetic takes well under a microsecond.  k_tiny_step runs
+// the same step in one launch: tanh and the Chebyshev recurrence in fp32, the
+// contractions as fixed-order fp32 sums (with the bf16 compute mode's operand
+// rounding: basis values, coefficients and dy of the d >= 1 terms rounded to
+// bf16, the T_0 terms kept in fp32, as the MFMA path does), the loss and its
+// gradient, then per layer from the last: dx (with the coefficients before
+// their update), dC and the SGD / Adam update.  All reductions are in a fixed
+// order, so steps are bitwise reproducible.
+// ---------------------------------------------------------------------------
+constexpr int kTinyMaxLayers = 8;
+constexpr int kTinyMaxD = 17;
+constexpr int64_t kTinyMaxMacs = (int64_t)1 << 18;  // multiply-adds per step
+
+struct TinyLayerArg {
+  float* C;
+  float* m;
+  float* v;
+  float* t;   // tanh of the layer input [B, I]
+  float* y;   // layer output [B, O]
+  float* dy;  // gradient wrt y [B, O]
+  int I, O, D;
+};
+
+struct TinyArgs {
+  TinyLayerArg L[kTinyMaxLayers];
+  int nl;
+  int loss;
+  int opt;
+  int bf16;
+  int64_t B;
+  float lr, wd, w1, beta2, one_m_beta2, eps;
+  double lr_d, b1_d, b2_d;
+};
+
+__device__ __forceinline__ float tiny_round(float v, int bf) { return bf ? (float)(__bf16)v : v; }
+
+// Sum of red[0..n) (n a power of two, every thread of the block calls it) by a
+// fixed tree; the result is returned to every thread.
+__device__ float tiny_block_sum(float* red, float v) {
+  const int tid = threadIdx.x;
+  red[tid] = v;
+  __syncthreads();
+  for (int w = blockDim.x >> 1; w > 0; w >>= 1) {
+    if (tid < w) red[tid] += red[tid + w];
+    __syncthreads();
+  }
+  const float r = red[0];
+  __syncthreads();
+  return r;
+}
+
+__global__ void __launch_bounds__(1024)
+k_tiny_step(TinyArgs a, const float* __restrict__ x, const void* __restrict__ target,
+            int64_t* __restrict__ step, float* __restrict__ loss, float* __restrict__ loss_copy) {
+  __shared__ float red[1024];
+  __shared__ float sc[2];
+  const int tid = threadIdx.x, nt = blockDim.x;
+  const int64_t B = a.B;
+  const int bf = a.bf16;
+  if (a.opt == CKAN_OPT_ADAM && tid == 0) {  // the device step count, as k_adam_scalars
+    const int64_t s1 = *step + 1;
+    *step = s1;
+    sc[0] = (float)(-(a.lr_d / (1.0 - pow(a.b1_d, (double)s1))));
+    sc[1] = (float)sqrt(1.0 - pow(a.b2_d, (double)s1));
+  }
+
+  // ---- forward: t = tanh(in); y = sum_i C[i,o,0] + sum_{i,d>=1} T_d(t) C[i,o,d]
+  const float* in = x;
+  for (int l = 0; l < a.nl; ++l) {
+    const TinyLayerArg ly = a.L[l];
+    const int I = ly.I, O = ly.O, D = ly.D;
+    for (int64_t q = tid; q < B * I; q += nt) ly.t[q] = tanhf(in[q]);
+    __syncthreads();
+    for (int64_t q = tid; q < B * O; q += nt) {
+      const int64_t b = q / O;
+      const int o = (int)(q - b * O);
+      const float* tb = ly.t + b * I;
+      float acc = 0.0f, bias = 0.0f;
+      for (int i = 0; i < I; ++i) {
+        const float* c = ly.C + ((size_t)i * O + o) * D;
+        const float tv = tb[i], t2 = tv + tv;
+        bias += c[0];
+        float tm = 1.0f, tc = tv;
+        for (int d = 1; d < D; ++d) {
+          acc = fmaf(tiny_round(tc, bf), tiny_round(c[d], bf), acc);
+          const float tn = fmaf(t2, tc, -tm);
+          tm = tc;
+          tc = tn;
+        }
+      }
+      ly.y[q] = acc + bias;
+    }
+    __syncthreads();
+    in = ly.y;
+  }
+
+  // ---- loss and its gradient (mean reduction)
+  const TinyLayerArg last = a.L[a.nl - 1];
+  const int O = last.O;
+  float part = 0.0f;
+  if (a.loss == CKAN_LOSS_MSE) {
+    const int64_t n = B * O;
+    const float gs = (float)(2.0 / (double)n);
+    const float* tgt = reinterpret_cast<const float*>(target);
+    for (int64_t q = tid; q < n; q += nt) {
+      const float d = last.y[q] - tgt[q];
+      part = fmaf(d, d, part);
+      last.dy[q] = gs * d;
+    }
+    part = tiny_block_sum(red, part) * (float)(1.0 / (double)n);
+  } else {
+    const int64_t* lab = reinterpret_cast<const int64_t*>(target);
+    const float inv_b = 1.0f / (float)B;
+    for (int64_t b = tid; b < B; b += nt) {
+      const float* yr = last.y + b * O;
+      float m = -INFINITY;
+      for (int o = 0; o < O; ++o) m = fmaxf(m, yr[o]);
+      float s = 0.0f;
+      for (int o = 0; o < O; ++o) s += expf(yr[o] - m);
+      const int64_t lb = lab[b];
+      for (int o = 0; o < O; ++o)
+        last.dy[b * O + o] = (expf(yr[o] - m) / s - (o == lb ? 1.0f : 0.0f)) * inv_b;
+      part += (logf(s) + m) - ((lb >= 0 && lb < O) ? yr[lb] : 0.0f);
+    }
+    part = tiny_block_sum(red, part) * (float)(1.0 / (double)B);
+  }
+  if (tid == 0) {
+    *loss = part;
+    if (loss_copy) *loss_copy = part;
+  }
+  __syncthreads();
+
+  // ---- backward and the optimizer, last layer first
+  for (int l = a.nl - 1; l >= 0; --l) {
+    const TinyLayerArg ly = a.L[l];
+    const int I = ly.I, Ol = ly.O, D = ly.D;
+    if (l > 0) {
+      // dx[b,i] = (1 - t^2) sum_d U_{d-1}(t) sum_o dy[b,o] d C[i,o,d]
+      float* dx = a.L[l - 1].dy;
+      for (int64_t q = tid; q < B * I; q += nt) {
+        const int64_t b = q / I;
+        const int i = (int)(q - b * I);
+        const float tv = ly.t[q], t2 = tv + tv;
+        float dt[kTinyMaxD];
+#pragma unroll
+        for (int d = 0; d < kTinyMaxD; ++d) dt[d] = 0.0f;
+        for (int o = 0; o < Ol; ++o) {
+          const float g = tiny_round(ly.dy[b * Ol + o], bf);
+          const float* c = ly.C + ((size_t)i * Ol + o) * D;
+#pragma unroll
+          for (int d = 1; d < kTinyMaxD; ++d)
+            if (d < D) dt[d] = fmaf(g, tiny_round(c[d] * (float)d, bf), dt[d]);
+        }
+        float sum = 0.0f, up = 0.0f, u = 1.0f;  // U_{-1}, U_0
+#pragma unroll
+        for (int d = 1; d < kTinyMaxD; ++d) {
+          if (d < D) sum = fmaf(dt[d], u, sum);
+          const float un = fmaf(t2, u, -up);
+          up = u;
+          u = un;
+        }
+        dx[q] = sum * (1.0f - tv * tv);
+      }
+      __syncthreads();  // dx used the coefficients before their update
+    }
+    // dC[i,o,0] = sum_b dy[b,o]; dC[i,o,d] = sum_b T_d(t[b,i]) dy[b,o], one wave per
+    // (i, o): lane k sums rows k, k + 64, ..., then a fixed butterfly over the
+    // lanes; lane d < D then applies the update of coefficient d
+    const int lane = tid & 63, wv = tid >> 6, nwv = nt >> 6;
+    for (int64_t q = wv; q < (int64_t)I * Ol; q += nwv) {
+      const int i = (int)(q / Ol), o = (int)(q - (int64_t)i * Ol);
+      float g[kTinyMaxD];
+#pragma unroll
+      for (int d = 0; d < kTinyMaxD; ++d) g[d] = 0.0f;
+      for (int64_t b = lane; b < B; b += 64) {
+        const float dyv = ly.dy[b * Ol + o], dyr = tiny_round(dyv, bf);
+        const float tv = ly.t[b * I + i], t2 = tv + tv;
+        g[0] += dyv;
+        float tm = 1.0f, tc = tv;
+#pragma unroll
+        for (int d = 1; d < kTinyMaxD; ++d) {
+          if (d < D) g[d] = fmaf(tiny_round(tc, bf), dyr, g[d]);
+          const float tn = fmaf(t2, tc, -tm);
+          tm = tc;
+          tc = tn;
+        }
+      }
+#pragma unroll
+      for (int w = 32; w > 0; w >>= 1)
+#pragma unroll
+        for (int d = 0; d < kTinyMaxD; ++d) g[d] += __shfl_xor(g[d], w);
+      float gd = 0.0f;  // this lane's coefficient gradient (lane < D)
+#pragma unroll
+      for (int d = 0; d < kTinyMaxD; ++d) gd = lane == d ? g[d] : gd;
+      if (lane < D) {
+        const size_t k = (size_t)q * D + lane;
+        float* c = ly.C + k;
+        if (a.opt == CKAN_OPT_SGD) {
+          *c = sgd_update(*c, gd, a.lr, a.wd);
+        } else {
+          *c = adam_update(*c, gd, ly.m + k, ly.v + k, a.w1, a.beta2, a.one_m_beta2, a.eps,
+                           a.wd, sc[0], sc[1]);
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
 int grid_of(int64_t n) {
   int64_t g = (n + 255) / 256;
   return (int)(g < 1 ? 1 : (g > 65536 ? 65536 : g));
@@ -139,6 +352,7 @@ struct ckan_exec {
   float* loss = nullptr;
   int64_t* step = nullptr;     // Adam step count (device)
   float* adam_sc = nullptr;    // Adam scalars (device)
+  bool tiny = false;           // the whole step runs as one k_tiny_step launch
   // graph mode
   hipStream_t es = nullptr;
   hipEvent_t ev_in = nullptr, ev_out = nullptr;
@@ -178,8 +392,50 @@ void free_all(ckan_exec* ex) {
   ex->allocs.clear();
 }
 
+// Whether the stack is small enough for the one-launch step.
+bool tiny_eligible(const ckan_exec* ex) {
+  const auto& c = ex->cfg;
+  if (c.flags & CKAN_EXEC_NO_FUSED_SMALL) return false;
+  if (c.n_layers > kTinyMaxLayers) return false;
+  int64_t macs = 0;
+  for (int l = 0; l < c.n_layers; ++l) {
+    const int64_t io = (int64_t)ex->widths[l] * ex->widths[l + 1];
+    if (ex->degrees[l] + 1 > kTinyMaxD) return false;
+    macs += c.batch * io * (ex->degrees[l] + 1) * (l > 0 ? 3 : 2);
+  }
+  return macs <= kTinyMaxMacs;
+}
+
+int run_tiny(ckan_exec* ex, const float* x, const void* target, float* loss_copy, hipStream_t s) {
+  const auto& c = ex->cfg;
+  TinyArgs a{};
+  a.nl = c.n_layers;
+  for (int l = 0; l < a.nl; ++l) {
+    const auto& ly = ex->layers[l];
+    a.L[l] = TinyLayerArg{ly.C, ly.m, ly.v, ly.t, ly.y, ly.dy, ly.desc.in_dim, ly.desc.out_dim,
+                          ly.desc.degree + 1};
+  }
+  a.loss = c.loss;
+  a.opt = c.optimizer;
+  a.bf16 = c.compute == CKAN_COMPUTE_BF16;
+  a.B = c.batch;
+  a.lr = c.lr;
+  a.wd = c.weight_decay;
+  a.w1 = (float)(1.0 - (double)c.beta1);
+  a.beta2 = c.beta2;
+  a.one_m_beta2 = (float)(1.0 - (double)c.beta2);
+  a.eps = c.eps;
+  a.lr_d = (double)c.lr;
+  a.b1_d = (double)c.beta1;
+  a.b2_d = (double)c.beta2;
+  hipLaunchKernelGGL(k_tiny_step, dim3(1), dim3(1024), 0, s, a, x, target, ex->step, ex->loss,
+                     loss_copy);
+  return hipGetLastError() == hipSuccess ? CKAN_OK : efail(CKAN_ERR_HIP, "executor: step launch failed");
+}
+
 // The step body on stream s with inputs x / target.
 int run_step(ckan_exec* ex, const float* x, const void* target, hipStream_t s) {
+  if (ex->tiny) return run_tiny(ex, x, target, nullptr, s);
   const int L = (int)ex->layers.size();
   int rc;
   for (int l = 0; l < L; ++l) {
@@ -300,6 +556,7 @@ int ckan_exec_create(const ckan_exec_config* cfg, ckan_exec** out, void* stream)
       launch_zero(ex->step, 256, s);
     }
   }
+  if (rc == CKAN_OK) ex->tiny = tiny_eligible(ex);
   if (rc == CKAN_OK && cfg->use_graph) {
     const int O = ex->widths[cfg->n_layers];
     ex->tgt_bytes = cfg->loss == CKAN_LOSS_MSE ? (size_t)cfg->batch * O * 4 : (size_t)cfg->batch * 8;
@@ -415,6 +672,7 @@ int ckan_exec_step(ckan_exec* ex, const float* x, const void* target, float* los
     return hipGetLastError() == hipSuccess;
   };
   if (!ex->cfg.use_graph) {
+    if (ex->tiny) return run_tiny(ex, x, target, loss_out, s);  // writes loss_out itself
     if ((rc = run_step(ex, x, target, s))) return rc;
     if (loss_out && !copy(loss_out, ex->loss, 4, s))
       return efail(CKAN_ERR_HIP, "executor: loss copy failed");
@@ -472,6 +730,32 @@ int ckan_exec_step(ckan_exec* ex, const float* x, const void* target, float* los
   }
   if (loss_out && !copy(loss_out, ex->loss, 4, s))
     return efail(CKAN_ERR_HIP, "executor: loss copy failed");
+  return CKAN_OK;
+}
+
+int ckan_exec_steps(ckan_exec* ex, const float* x, const void* target, int64_t nsteps,
+                    float* losses, void* stream) {
+  if (!ex) return efail(CKAN_ERR_INVALID_ARG, "executor is NULL");
+  if (!x || !target) return efail(CKAN_ERR_INVALID_ARG, "executor: x/target is NULL");
+  if (nsteps < 0) return efail(CKAN_ERR_INVALID_ARG, "executor: nsteps must be >= 0");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (ex->es) {  // order after any graph replay on the executor stream
+    hipEventRecord(ex->ev_out, ex->es);
+    hipStreamWaitEvent(s, ex->ev_out, 0);
+  }
+  int rc;
+  for (int64_t k = 0; k < nsteps; ++k) {
+    float* lk = losses ? losses + k : nullptr;
+    if (ex->tiny) {
+      if ((rc = run_tiny(ex, x, target, lk, s))) return rc;
+      continue;
+    }
+    if ((rc = run_step(ex, x, target, s))) return rc;
+    if (lk) {
+      hipLaunchKernelGGL(k_copy_f32, dim3(1), dim3(256), 0, s, ex->loss, lk, (int64_t)1);
+      if (hipGetLastError() != hipSuccess) return efail(CKAN_ERR_HIP, "executor: loss copy failed");
+    }
+  }
   return CKAN_OK;
 }
 

@@ -27,7 +27,8 @@ class ResidentExecutor:
     def __init__(self, widths: Sequence[int], degrees: Sequence[int], batch: int,
                  compute: str = "bf16", loss: str = "mse", optimizer: str = "sgd",
                  lr: float = 0.01, betas=(0.9, 0.999), eps: float = 1e-8,
-                 weight_decay: float = 0.0, use_graph: bool = False, device="cuda"):
+                 weight_decay: float = 0.0, use_graph: bool = False, fused_small: bool = True,
+                 device="cuda"):
         self.device = torch.device(device)
         if self.device.type != "cuda":
             raise RuntimeError("ResidentExecutor runs only on a ROCm device")
@@ -48,7 +49,8 @@ class ResidentExecutor:
         cfg = _lib.CkanExecConfig(
             len(self.degrees), self._w, self._d, self.batch, compute_code(compute),
             _LOSS[loss], _OPT[optimizer], 1 if use_graph else 0, float(lr), float(betas[0]),
-            float(betas[1]), float(eps), float(weight_decay))
+            float(betas[1]), float(eps), float(weight_decay),
+            0 if fused_small else _lib.CKAN_EXEC_NO_FUSED_SMALL)
         handle = ctypes.c_void_p()
         with torch.cuda.device(self.device):
             _lib.check(self._lib.ckan_exec_create(ctypes.byref(cfg), ctypes.byref(handle),
@@ -101,6 +103,30 @@ class ResidentExecutor:
         # the library writes every step's loss into the same 4 bytes: hand the
         # caller its own copy, as a torch loss tensor would be
         return self._loss.clone()
+
+    def _inputs(self, x: torch.Tensor, target: torch.Tensor):
+        x = x.to(self.device, torch.float32).contiguous()
+        if tuple(x.shape) != (self.batch, self.widths[0]):
+            raise RuntimeError(f"x must be [{self.batch}, {self.widths[0]}]")
+        if self.loss_name == "mse":
+            target = target.to(self.device, torch.float32).contiguous()
+            if tuple(target.shape) != (self.batch, self.widths[-1]):
+                raise RuntimeError(f"target must be [{self.batch}, {self.widths[-1]}]")
+        else:
+            target = target.to(self.device, torch.int64).contiguous()
+            if tuple(target.shape) != (self.batch,):
+                raise RuntimeError(f"labels must be [{self.batch}]")
+        return x, target
+
+    def fit(self, x: torch.Tensor, target: torch.Tensor, steps: int) -> torch.Tensor:
+        """``steps`` training steps on the same batch (the reference loop's
+        full-batch epochs, README.md:61-69) issued in one library call;
+        returns the per-step losses as a device tensor [steps]."""
+        x, target = self._inputs(x, target)
+        losses = torch.empty(int(steps), dtype=torch.float32, device=self.device)
+        _lib.check(self._lib.ckan_exec_steps(self._h, x.data_ptr(), target.data_ptr(), int(steps),
+                                             losses.data_ptr(), self._stream()))
+        return losses
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         x = x.to(self.device, torch.float32).contiguous()

@@ -238,3 +238,75 @@ def test_graph_steps_follow_the_callers_buffers():
         assert torch.equal(exs[0].get_coeffs(l), exs[1].get_coeffs(l))
     for ex in exs:
         ex.close()
+
+
+@pytest.mark.parametrize("widths,degrees,B,compute,loss,opt", [
+    ([1, 1], [8], 100, "fp32", "mse", "adam"),        # config 1, the README loop
+    ([8, 6, 3], [3, 5], 40, "fp32", "ce", "sgd"),      # two layers: the dx path
+    ([8, 6, 3], [3, 5], 40, "bf16", "ce", "sgd"),
+    ([5, 7, 4], [16, 2], 33, "fp32", "mse", "adam"),   # degree 16, Adam with weight decay
+])
+def test_fused_small_step_matches_oracle_and_kernel_sequence(widths, degrees, B, compute, loss, opt):
+    """Stacks of at most 2^18 multiply-adds per step run each step as one
+    single-workgroup launch; it must follow the oracle's training loop, and
+    the per-layer kernel sequence (fused_small=False) on the same inputs."""
+    from kan_amd import ResidentExecutor
+    print(f"fused small step {widths} {degrees} B={B} {compute} {loss} {opt}", flush=True)
+    g = torch.Generator().manual_seed(21)
+    x = torch.rand(B, widths[0], generator=g) * 4 - 2
+    y = (torch.randn(B, widths[-1], generator=g) if loss == "mse"
+         else torch.randint(0, widths[-1], (B,), generator=g))
+    coeffs = _make(widths, degrees, 22)
+    wd = 0.1 if opt == "adam" and degrees[0] == 16 else 0.0
+    lr = 0.01 if opt == "adam" else 0.05
+    steps = 5
+    bf = compute == "bf16"
+    c_ref, l_ref = orc.train_steps(x, y, coeffs, steps=steps, loss=loss, optimizer=opt, lr=lr,
+                                   weight_decay=wd, bf16_coeffs=bf)
+    tol = 2e-2 if bf else 1e-4
+    res = {}
+    for fused in (True, False):
+        ex = ResidentExecutor(widths, degrees, B, compute=compute, loss=loss, optimizer=opt, lr=lr,
+                              weight_decay=wd, fused_small=fused)
+        for l, c in enumerate(coeffs):
+            ex.set_coeffs(l, c)
+        xd, yd = x.cuda(), y.cuda()
+        losses = [ex.step(xd, yd).item() for _ in range(steps)]
+        cs = [ex.get_coeffs(l).cpu() for l in range(len(degrees))]
+        for k, (a, b) in enumerate(zip(losses, l_ref)):
+            assert abs(a - b) <= tol * abs(b) + 1e-7, (fused, k, a, b)
+        for l in range(len(degrees)):
+            d_got, d_want = cs[l].double() - coeffs[l].double(), c_ref[l].double() - coeffs[l].double()
+            assert _rel(d_got, d_want) <= tol, (fused, l, _rel(d_got, d_want))
+        res[fused] = cs
+        ex.close()
+    for l in range(len(degrees)):
+        assert _rel(res[True][l] - coeffs[l], res[False][l] - coeffs[l]) <= tol
+
+
+@pytest.mark.parametrize("widths,degrees,B,loss,opt", [
+    ([1, 1], [8], 100, "mse", "adam"),      # one-launch steps
+    ([48, 32, 10], [4, 3], 128, "ce", "sgd"),  # the per-layer kernel sequence
+])
+def test_fit_equals_the_step_loop(widths, degrees, B, loss, opt):
+    """fit(x, y, n) issues n steps from the library: the same losses and
+    coefficients, bit for bit, as n calls of step()."""
+    from kan_amd import ResidentExecutor
+    print(f"fit vs step loop {widths} {loss} {opt}", flush=True)
+    g = torch.Generator().manual_seed(23)
+    x = (torch.rand(B, widths[0], generator=g) * 4 - 2).cuda()
+    y = (torch.randn(B, widths[-1], generator=g) if loss == "mse"
+         else torch.randint(0, widths[-1], (B,), generator=g)).cuda()
+    coeffs = _make(widths, degrees, 24)
+    exs = [ResidentExecutor(widths, degrees, B, compute="fp32", loss=loss, optimizer=opt, lr=0.02)
+           for _ in range(2)]
+    for ex in exs:
+        for l, c in enumerate(coeffs):
+            ex.set_coeffs(l, c)
+    looped = torch.stack([exs[0].step(x, y) for _ in range(7)])
+    fitted = exs[1].fit(x, y, 7)
+    assert torch.equal(looped, fitted)
+    for l in range(len(degrees)):
+        assert torch.equal(exs[0].get_coeffs(l), exs[1].get_coeffs(l))
+    for ex in exs:
+        ex.close()
