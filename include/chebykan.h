@@ -90,6 +90,19 @@ int ckan_pack_coeffs(const ckan_desc* desc, const void* coeffs, void* packed, vo
 int ckan_forward(const ckan_desc* desc, const float* x, const void* packed, float* y,
                  float* t_cache, void* ws, size_t ws_bytes, void* stream);
 
+/* ckan_pack_coeffs (or, with a non-NULL basis spec, ckan_pack_coeffs_basis,
+ * below) followed by ckan_forward, in fewer launches: the tanh of x is
+ * computed by the pack launch itself where the layout allows, and the
+ * per-output bias sum is reduced by the forward GEMM where it can.  Same
+ * arguments, results and packed-buffer contents as the two calls.
+ * Replaces: the layer forward as the reference runs it on every call, the
+ * einsum's coefficient re-layout included (kan/layers/chebykan.py:64-67,
+ * kan/basis/chebyshev.py:78,92-101). */
+struct ckan_basis_spec;
+int ckan_pack_forward(const ckan_desc* desc, const struct ckan_basis_spec* spec,
+                      const void* coeffs, void* packed, const float* x, float* y, float* t_cache,
+                      void* ws, size_t ws_bytes, void* stream);
+
 /* ckan_forward without a workspace argument, for callers that cannot
  * allocate device memory (code under HIP graph capture, serving loops and
  * harnesses that forbid hipMalloc).  No counterpart in the reference.  The

@@ -91,6 +91,7 @@ SIGNATURES = {
     "ckan_pack_coeffs": (ctypes.c_int, [_pdesc, _vp, _vp, _vp]),
     "ckan_forward": (ctypes.c_int, [_pdesc, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "ckan_forward_noalloc": (ctypes.c_int, [_pdesc, _vp, _vp, _vp, _vp, _vp]),
+    "ckan_pack_forward": (ctypes.c_int, [_pdesc, _pspec, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "ckan_backward": (ctypes.c_int, [_pdesc, _vp, _vp, _vp, _vp, _vp, ctypes.c_int, _vp, _sz, _vp]),
     "ckan_forward_f64": (ctypes.c_int, [_pdesc, _vp, _vp, _vp, _vp, _vp]),
     "ckan_backward_f64": (ctypes.c_int, [_pdesc, _vp, _vp, _vp, _vp, _vp, ctypes.c_int, _vp]),

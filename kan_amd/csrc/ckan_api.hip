@@ -300,6 +300,56 @@ int ckan_forward_noalloc(const ckan_desc* desc, const float* x, const void* pack
                       stream);
 }
 
+namespace {
+int family_xform(const ckan_basis_spec* spec, int degree, BasisXform* xf);
+}
+
+int ckan_pack_forward(const ckan_desc* desc, const ckan_basis_spec* spec, const void* coeffs,
+                      void* packed, const float* x, float* y, float* t_cache, void* ws,
+                      size_t ws_bytes, void* stream) {
+  int rc = validate_desc(desc);
+  if (rc) return rc;
+  BasisXform xf;
+  if (spec && (rc = family_xform(spec, desc->degree, &xf))) return rc;
+  if (!coeffs || !packed) return fail(CKAN_ERR_INVALID_ARG, "coeffs/packed is NULL");
+  if (!aligned16(packed)) return fail(CKAN_ERR_INVALID_ARG, "packed buffer must be 16-byte aligned");
+  const Plan p = plan_of(desc);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const bool cbf = desc->coeff_dtype == CKAN_DTYPE_BF16;
+  if (p.B == 0) {
+    ProfScope ps("pack", s);
+    launch_pack(coeffs, cbf, packed, p, s, spec ? &xf : nullptr);
+    return check_launch("pack_forward");
+  }
+  if (!x || !y || !t_cache) return fail(CKAN_ERR_INVALID_ARG, "x/y/t_cache is NULL");
+  if (!aligned16(t_cache)) return fail(CKAN_ERR_INVALID_ARG, "t_cache must be 16-byte aligned");
+  const FwdChoice c = choose_fwd(p);
+  const size_t need = fwd_ws_bytes(p, c);
+  if (ws_bytes < need)
+    return fail(CKAN_ERR_WORKSPACE, "forward workspace too small: %zu < %zu bytes", ws_bytes, need);
+  if (need && !ws) return fail(CKAN_ERR_INVALID_ARG, "workspace is NULL");
+  // the bias partials are summed by the forward GEMM where it can, and the
+  // tanh of x rides in the pack launch where the layout allows: fewer launches
+  const bool sum_in_gemm = fwd_sums_bias(p, c);
+  const bool fuse_tanh = fwd_reads_tcache(c) && pack_tanh_fusable(p, x);
+  {
+    ProfScope ps(fuse_tanh ? "pack_tanh" : "pack", s);
+    launch_pack(coeffs, cbf, packed, p, s, spec ? &xf : nullptr, !sum_in_gemm,
+                fuse_tanh ? x : nullptr, fuse_tanh ? t_cache : nullptr);
+  }
+  if ((rc = check_launch("pack_forward: pack"))) return rc;
+  if (fwd_reads_tcache(c) && !fuse_tanh) {
+    ProfScope ps("tanh", s);
+    launch_tanh(x, t_cache, p, s);
+  }
+  if ((rc = check_launch("pack_forward: tanh"))) return rc;
+  {
+    ProfScope ps("fwd_gemm", s);
+    launch_fwd_gemm(x, t_cache, packed, y, ws, p, c, s, sum_in_gemm);
+  }
+  return check_launch("pack_forward: fwd_gemm");
+}
+
 int ckan_backward(const ckan_desc* desc, const float* t_cache, const void* packed,
                   const float* dy, float* dx, float* dcoeffs, int accumulate, void* ws,
                   size_t ws_bytes, void* stream) {

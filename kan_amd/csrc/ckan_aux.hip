@@ -79,17 +79,36 @@ template <> __device__ __forceinline__ float to_f32<uint16_t>(uint16_t v) {
 template <bool XF> struct XfArg { BasisXform x; };
 template <> struct XfArg<false> {};
 
+// The optional tanh share of a pack launch (t = tanh(x) as flat float4
+// arrays, rows unpadded): block k takes float4 [k * per, (k + 1) * per).
+struct TanhJob {
+  const f32x4_t* x;
+  f32x4_t* t;
+  int64_t n4, per;
+};
+constexpr int kPackTanhU = 8;  // tanh float4 per thread in flight at once
+
 template <int P, bool BF, typename CT, bool XF>
 __global__ void __launch_bounds__(256)
 k_pack(const CT* __restrict__ C, typename Elem<BF>::type* __restrict__ Cf,
        typename Elem<BF>::type* __restrict__ Cb, float* __restrict__ bias_part, Plan p, int cal,
-       XfArg<XF> xf) {
+       XfArg<XF> xf, TanhJob tj) {
   using G = FwdGroup<P>;
   constexpr int RPMAX = 32 * (P + 1) + 1;
   __shared__ float tile[32 * RPMAX];
   __shared__ float bsum[8][32];
   const int tid = threadIdx.x;
   const int ib = blockIdx.x, ob = blockIdx.y;
+  // tanh share: the first chunk's loads go out with the tile's, so both streams
+  // are in flight together; the tanh itself runs after the re-layout
+  const int64_t tj0 = tj.per * (blockIdx.x + (int64_t)gridDim.x * blockIdx.y);
+  const int64_t tj1 = tj.x ? (tj0 + tj.per < tj.n4 ? tj0 + tj.per : tj.n4) : 0;
+  f32x4_t tx[kPackTanhU];
+#pragma unroll
+  for (int u = 0; u < kPackTanhU; ++u) {
+    const int64_t k = tj0 + tid + u * 256;
+    tx[u] = k < tj1 ? tj.x[k] : f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
   const int i0 = ib * 32, o0 = ob * 32;
   const int D = p.D;
   const int RP = 32 * D + 1;
@@ -197,6 +216,24 @@ k_pack(const CT* __restrict__ C, typename Elem<BF>::type* __restrict__ Cf,
       v[j] = (e + 1 <= p.deg) ? tile[il * RP + ol * D + e + 1] * (float)(e + 1) : 0.0f;
     }
     store_frag<BF>(Cb + ((size_t)(ib * P + e) * p.KBx + kbx) * kFragElems, lane, v);
+  }
+
+  for (int64_t c0 = tj0; c0 < tj1; c0 += 256 * kPackTanhU) {
+    if (c0 > tj0) {
+#pragma unroll
+      for (int u = 0; u < kPackTanhU; ++u) {
+        const int64_t k = c0 + tid + u * 256;
+        tx[u] = k < tj1 ? tj.x[k] : f32x4_t{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kPackTanhU; ++u) {
+      const int64_t k = c0 + tid + u * 256;
+      f32x4_t r;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) r[j] = tanhf(tx[u][j]);
+      if (k < tj1) tj.t[k] = r;
+    }
   }
 }
 
@@ -460,7 +497,7 @@ void launch_tanh(const float* x, float* t, const Plan& p, hipStream_t s) {
 
 template <int P, bool BF, bool XF>
 static void launch_pack_t(const void* C, bool c_bf16, void* packed, const Plan& p, hipStream_t s,
-                          const XfArg<XF>& xf) {
+                          const XfArg<XF>& xf, const TanhJob& tj) {
   typedef typename Elem<BF>::type E;
   E* Cf = reinterpret_cast<E*>(packed);
   E* Cb = Cf + packed_cf_elems(p);
@@ -470,35 +507,57 @@ static void launch_pack_t(const void* C, bool c_bf16, void* packed, const Plan& 
   dim3 grid(p.NIB, p.O64 / 32);
   if (c_bf16)
     hipLaunchKernelGGL((k_pack<P, BF, uint16_t, XF>), grid, dim3(256), 0, s,
-                       reinterpret_cast<const uint16_t*>(C), Cf, Cb, bias, p, 0, xf);
+                       reinterpret_cast<const uint16_t*>(C), Cf, Cb, bias, p, 0, xf, tj);
   else
     hipLaunchKernelGGL((k_pack<P, BF, float, XF>), grid, dim3(256), 0, s,
-                       reinterpret_cast<const float*>(C), Cf, Cb, bias, p, (int)is_al16(C), xf);
+                       reinterpret_cast<const float*>(C), Cf, Cb, bias, p, (int)is_al16(C), xf, tj);
 }
 
 template <bool XF>
 static void launch_pack_x(const void* C, bool c_bf16, void* packed, const Plan& p, hipStream_t s,
-                          const XfArg<XF>& xf) {
+                          const XfArg<XF>& xf, const TanhJob& tj) {
   const bool bf = p.esz == 2;
+#define CKAN_PK(PP, BB) launch_pack_t<PP, BB>(C, c_bf16, packed, p, s, xf, tj)
   switch (p.P) {
-    case 2: bf ? launch_pack_t<2, true>(C, c_bf16, packed, p, s, xf) : launch_pack_t<2, false>(C, c_bf16, packed, p, s, xf); break;
-    case 4: bf ? launch_pack_t<4, true>(C, c_bf16, packed, p, s, xf) : launch_pack_t<4, false>(C, c_bf16, packed, p, s, xf); break;
-    case 8: bf ? launch_pack_t<8, true>(C, c_bf16, packed, p, s, xf) : launch_pack_t<8, false>(C, c_bf16, packed, p, s, xf); break;
-    default: bf ? launch_pack_t<16, true>(C, c_bf16, packed, p, s, xf) : launch_pack_t<16, false>(C, c_bf16, packed, p, s, xf); break;
+    case 2: bf ? CKAN_PK(2, true) : CKAN_PK(2, false); break;
+    case 4: bf ? CKAN_PK(4, true) : CKAN_PK(4, false); break;
+    case 8: bf ? CKAN_PK(8, true) : CKAN_PK(8, false); break;
+    default: bf ? CKAN_PK(16, true) : CKAN_PK(16, false); break;
   }
+#undef CKAN_PK
+}
+
+bool pack_tanh_fusable(const Plan& p, const float* x) {
+  return x && p.I == p.I_sg && p.I % 4 == 0 && is_al16(x);
 }
 
 void launch_pack(const void* C, bool c_bf16, void* packed, const Plan& p, hipStream_t s,
-                 const BasisXform* xf) {
+                 const BasisXform* xf, bool reduce_bias, const float* x, float* t) {
   char* base = reinterpret_cast<char*>(packed);
+  TanhJob tj{nullptr, nullptr, 0, 0};
+  if (x && t) {  // pack_tanh_fusable(p, x) holds: the caller checked
+    tj.x = reinterpret_cast<const f32x4_t*>(x);
+    tj.t = reinterpret_cast<f32x4_t*>(t);
+    tj.n4 = p.B * p.I / 4;
+    const int64_t blocks = (int64_t)p.NIB * (p.O64 / 32);
+    tj.per = round_up(ceil_div(tj.n4, blocks), 256);
+  }
   if (xf) {
     XfArg<true> a;
     a.x = *xf;
-    launch_pack_x<true>(C, c_bf16, packed, p, s, a);
+    launch_pack_x<true>(C, c_bf16, packed, p, s, a, tj);
   } else {
-    launch_pack_x<false>(C, c_bf16, packed, p, s, XfArg<false>{});
+    launch_pack_x<false>(C, c_bf16, packed, p, s, XfArg<false>{}, tj);
   }
-  if (p.NIB > 1)  // bias = sum of the per-input-block partials, in block order
+  if (p.NIB > 1 && reduce_bias)  // bias = sum of the per-input-block partials, in block order
+    hipLaunchKernelGGL(k_col_reduce, dim3((unsigned)ceil_div(p.O32, 64)), dim3(256), 0, s,
+                       reinterpret_cast<const float*>(base + packed_bias_offset(p)), p.NIB,
+                       p.O32, p.O32, reinterpret_cast<float*>(base + packed_biasf_offset(p)));
+}
+
+void launch_bias_reduce(void* packed, const Plan& p, hipStream_t s) {
+  char* base = reinterpret_cast<char*>(packed);
+  if (p.NIB > 1)
     hipLaunchKernelGGL(k_col_reduce, dim3((unsigned)ceil_div(p.O32, 64)), dim3(256), 0, s,
                        reinterpret_cast<const float*>(base + packed_bias_offset(p)), p.NIB,
                        p.O32, p.O32, reinterpret_cast<float*>(base + packed_biasf_offset(p)));

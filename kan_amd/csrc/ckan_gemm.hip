@@ -254,7 +254,10 @@ struct FwdPipe {
   static constexpr int NPB_FIT = (160 * 1024) / PAIR_BYTES;
   static constexpr int NPB = NPB_FIT > 3 ? 3 : NPB_FIT;
   static constexpr int RING_BYTES = NPB * PAIR_BYTES;
-  static constexpr int LDS_BYTES = RING_BYTES > RED_BYTES + 16 ? RING_BYTES : RED_BYTES + 16;
+  // bias sums of the block's outputs (epilogue only, after the halves' tiles)
+  static constexpr int BIAS_OFF = RED_BYTES + 16;
+  static constexpr int BIAS_END = BIAS_OFF + BNF * 32 * 4;
+  static constexpr int LDS_BYTES = RING_BYTES > BIAS_END ? RING_BYTES : BIAS_END;
   // dma16 ops per thread per stage (each op moves 512 x 16 bytes per block)
   static constexpr int B_OPS = B_BYTES / (16 * THREADS);
   static constexpr int T_OPS = T_BYTES / (16 * THREADS);
@@ -273,11 +276,16 @@ template <int CR> __device__ __forceinline__ int fwd_t_xor(int r) {
   else return ((r >> 1) & 1) | (((r >> 2) & 1) << 1) | (((r ^ (r >> 3)) & 1) << 2);
 }
 
+// The bias: bias_f[o] when nib == 0; otherwise the block sums the nib
+// per-input-block partials bias_part[ib][o] itself (in the order k_col_reduce
+// adds them, so the two give the same bits), and the first row tile also
+// writes the sums to bias_out.
 template <int P, bool BF>
 __global__ void __launch_bounds__(512)
 k_fwd_pipe(const float* __restrict__ tc, const typename Elem<BF>::type* __restrict__ Cf,
            const float* __restrict__ bias_f, float* __restrict__ y, float* __restrict__ part,
-           Plan p, int sg_per_split) {
+           Plan p, int sg_per_split, const float* __restrict__ bias_part, int nib,
+           float* __restrict__ bias_out) {
   typedef FwdPipe<P, BF> K;
   typedef typename K::E E;
   typedef typename K::G G;
@@ -427,6 +435,9 @@ k_fwd_pipe(const float* __restrict__ tc, const typename Elem<BF>::type* __restri
   pin_sgpr(y);  // used after the loop
   pin_sgpr(part);
   pin_sgpr(bias_f);
+  pin_sgpr(bias_part);
+  pin_sgpr(bias_out);
+  pin_sgpr(nib);
   if (half == 0) {
 #pragma unroll
     for (int j = 0; j < NPB - 1; ++j)
@@ -451,8 +462,25 @@ k_fwd_pipe(const float* __restrict__ tc, const typename Elem<BF>::type* __restri
   // its own, so all 8 waves share the stores.  Every barrier is reached by
   // all 8 waves.
   constexpr int NH = NN / 2;
+  // bias from the partials: thread t sums partials k = t % 4, t % 4 + 4, ... of
+  // output nb0 * 32 + t / 4 (loads issued here, ahead of the LDS hand-over)
+  float bsum = 0.0f;
+  const int bo = nb0 * 32 + (tid >> 2);
+  if (nib > 0 && bo < p.O32)
+    for (int k = tid & 3; k < nib; k += 4) bsum += bias_part[(size_t)k * p.O32 + bo];
   wait_lgkmcnt<0>();
   block_barrier();
+  float* bias_l = reinterpret_cast<float*>(smem + K::BIAS_OFF);
+  if (nib > 0) {
+    const int q0 = lane & ~3;
+    const float s0 = __shfl(bsum, q0), s1 = __shfl(bsum, q0 + 1);
+    const float s2 = __shfl(bsum, q0 + 2), s3 = __shfl(bsum, q0 + 3);
+    const float tot = ((s0 + s1) + s2) + s3;
+    if ((tid & 3) == 0) {
+      bias_l[tid >> 2] = tot;
+      if (bias_out && bx == 0 && blockIdx.z == 0 && bo < p.O32) bias_out[bo] = tot;
+    }
+  }
   float* red = reinterpret_cast<float*>(smem);
   auto red_at = [&](int giver, int mi, int j, int v) __attribute__((always_inline)) {
     return red + ((((giver * 4 + wq) * NM + mi) * NH + j) * 16 + v) * 64 + lane;
@@ -483,7 +511,7 @@ k_fwd_pipe(const float* __restrict__ tc, const typename Elem<BF>::type* __restri
       const int nb = nb0 + keep0 + j;
       const int o = nb * 32 + (lane & 31);
       if (split ? nb >= p.NBf : o >= p.O) continue;
-      const float add = split ? 0.0f : bias_f[o];
+      const float add = split ? 0.0f : (nib > 0 ? bias_l[(keep0 + j) * 32 + (lane & 31)] : bias_f[o]);
       const int64_t pitch = split ? p.O32 : p.O;
       const int64_t nrow = split ? p.B32 : p.B;
       float* out = split ? part + (size_t)blockIdx.z * p.B32 * p.O32 : y;
@@ -533,8 +561,15 @@ template <int P, bool BF> struct FwdStream {
   static constexpr int WAVES = 4;
 };
 
+// Waves per SIMD the streaming kernel asks the compiler to fit.  The grid
+// runs 16 waves per CU; at more than 128 registers a lane only 3 fit per
+// SIMD and the last quarter of the waves runs as a second round.  The bf16
+// kernels of degree 8 and 16 fit 4 per SIMD without spilling; the others
+// keep the default (they would spill).
+template <int P, bool BF> struct StreamWaves { static constexpr int v = (BF && P >= 8) ? 4 : 1; };
+
 template <int P, bool BF, int NMS, bool TPRE>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(StreamWaves<P, BF>::v)))
 k_fwd_stream(const float* __restrict__ x, float* __restrict__ tc,
              const typename Elem<BF>::type* __restrict__ Cf, float* __restrict__ part, Plan p,
              int bpn, int xal) {
@@ -1770,7 +1805,7 @@ FwdChoice choose_fwd(const Plan& p) {
 
 template <int P, bool BF>
 static void fwd_dispatch(const float* x, float* t, const void* packed, float* y, void* ws,
-                         const Plan& p, const FwdChoice& c, hipStream_t s) {
+                         const Plan& p, const FwdChoice& c, hipStream_t s, int nib) {
   typedef typename Elem<BF>::type E;
   const E* Cf = reinterpret_cast<const E*>(packed);
   const float* bias =
@@ -1805,8 +1840,12 @@ static void fwd_dispatch(const float* x, float* t, const void* packed, float* y,
           const size_t lds = (size_t)K::LDS_BYTES;
           static std::atomic<uint32_t> lds_set{0};
           ensure_lds_limit(reinterpret_cast<const void*>(&k_fwd_pipe<P, BF>), (int)lds, lds_set);
+          // nib > 0: the bias partials, summed in the kernel, which also fills the bias slot
+          char* pk = const_cast<char*>(reinterpret_cast<const char*>(packed));
           hipLaunchKernelGGL((k_fwd_pipe<P, BF>), grid, dim3(K::THREADS), lds, s, t, Cf, bias, y,
-                             part, p, c.sg_per_split);
+                             part, p, c.sg_per_split,
+                             reinterpret_cast<const float*>(pk + packed_bias_offset(p)), nib,
+                             nib > 0 ? reinterpret_cast<float*>(pk + packed_biasf_offset(p)) : nullptr);
         } else {
           hipLaunchKernelGGL((k_fwd<P, BF, 2, 4, 4, 1>), grid, dim3(256), 0, s, t, Cf, bias, y,
                              part, p, c.sg_per_split);
@@ -1822,15 +1861,29 @@ static void fwd_dispatch(const float* x, float* t, const void* packed, float* y,
   }
 }
 
-void launch_fwd_gemm(const float* x, float* t, const void* packed, float* y, void* ws,
-                     const Plan& p, const FwdChoice& c, hipStream_t s) {
+bool fwd_sums_bias(const Plan& p, const FwdChoice& c) {
+  if (c.tile != kFwdBig || c.splits > 1 || p.NIB <= 1 || !fwd_pipe_offsets_fit(p)) return false;
   const bool bf = p.esz == 2;
   switch (p.P) {
-    case 2: bf ? fwd_dispatch<2, true>(x, t, packed, y, ws, p, c, s) : fwd_dispatch<2, false>(x, t, packed, y, ws, p, c, s); break;
-    case 4: bf ? fwd_dispatch<4, true>(x, t, packed, y, ws, p, c, s) : fwd_dispatch<4, false>(x, t, packed, y, ws, p, c, s); break;
-    case 8: bf ? fwd_dispatch<8, true>(x, t, packed, y, ws, p, c, s) : fwd_dispatch<8, false>(x, t, packed, y, ws, p, c, s); break;
-    default: bf ? fwd_dispatch<16, true>(x, t, packed, y, ws, p, c, s) : fwd_dispatch<16, false>(x, t, packed, y, ws, p, c, s); break;
+    case 2: return bf ? FwdPipe<2, true>::kOk : FwdPipe<2, false>::kOk;
+    case 4: return bf ? FwdPipe<4, true>::kOk : FwdPipe<4, false>::kOk;
+    case 8: return bf ? FwdPipe<8, true>::kOk : FwdPipe<8, false>::kOk;
+    default: return bf ? FwdPipe<16, true>::kOk : FwdPipe<16, false>::kOk;
   }
+}
+
+void launch_fwd_gemm(const float* x, float* t, const void* packed, float* y, void* ws,
+                     const Plan& p, const FwdChoice& c, hipStream_t s, bool sum_bias) {
+  const bool bf = p.esz == 2;
+  const int nib = sum_bias && fwd_sums_bias(p, c) ? p.NIB : 0;
+#define CKAN_FW(PP, BB) fwd_dispatch<PP, BB>(x, t, packed, y, ws, p, c, s, nib)
+  switch (p.P) {
+    case 2: bf ? CKAN_FW(2, true) : CKAN_FW(2, false); break;
+    case 4: bf ? CKAN_FW(4, true) : CKAN_FW(4, false); break;
+    case 8: bf ? CKAN_FW(8, true) : CKAN_FW(8, false); break;
+    default: bf ? CKAN_FW(16, true) : CKAN_FW(16, false); break;
+  }
+#undef CKAN_FW
 }
 
 // dX stage depth: 4 k-blocks for bf16; fp32 halves it to bound LDS.

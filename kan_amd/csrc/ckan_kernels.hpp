@@ -108,9 +108,16 @@ void launch_backward_f64(const double* t, const double* C, const double* dy, dou
 
 // ---- launchers -------------------------------------------------------------
 void launch_tanh(const float* x, float* t, const Plan& p, hipStream_t s);
-// xf (optional, host struct passed by value to the kernel): pack C xf instead of C
+// xf (optional, host struct passed by value to the kernel): pack C xf instead of C.
+// reduce_bias = false leaves only the per-input-block bias partials (for a
+// forward that sums them itself).  With x and t (pack_tanh_fusable(p, x)), the
+// same launch also writes t = tanh(x) (the forward's tanh cache).
 void launch_pack(const void* C, bool c_bf16, void* packed, const Plan& p, hipStream_t s,
-                 const BasisXform* xf = nullptr);
+                 const BasisXform* xf = nullptr, bool reduce_bias = true,
+                 const float* x = nullptr, float* t = nullptr);
+// x's tanh can ride in the pack launch: rows need no padding (I == I_sg),
+// I % 4 == 0 and x is 16-byte aligned (the flat float4 layout).
+bool pack_tanh_fusable(const Plan& p, const float* x);
 void launch_prep_dy(const float* dy, void* dYx, void* dYc, float* colsum_part, const Plan& p,
                     bool need_dx, bool need_dc, hipStream_t s);
 // reduces the dy column-sum partials into row NBB and returns that row
@@ -120,8 +127,15 @@ void launch_dc_finalize(const float* part, int S, const float* colsum, float* dC
 void launch_dc_sum(const float* part, int S, float* dC, DcOut om, const Plan& p, hipStream_t s);
 // x is read only by the small-batch streaming kernel, which also writes t;
 // the other paths read t written by launch_tanh.
+// sum_bias: the packed buffer holds only the bias partials (launch_pack with
+// reduce_bias = false) and the forward must reduce them; the pipelined kernel
+// does so in its epilogue (and fills the bias slot) when fwd_sums_bias holds,
+// the caller launches the reduction first otherwise.
 void launch_fwd_gemm(const float* x, float* t, const void* packed, float* y, void* ws,
-                     const Plan& p, const FwdChoice& c, hipStream_t s);
+                     const Plan& p, const FwdChoice& c, hipStream_t s, bool sum_bias = false);
+bool fwd_sums_bias(const Plan& p, const FwdChoice& c);
+// bias = sum of the per-input-block partials, into the packed buffer's bias slot
+void launch_bias_reduce(void* packed, const Plan& p, hipStream_t s);
 void launch_dx_gemm(const void* dYx, const void* packed, const float* t, float* dx,
                     const Plan& p, hipStream_t s);
 // colsum: the per-64-row column-sum partials for the pipelined kernel (which

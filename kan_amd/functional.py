@@ -79,16 +79,14 @@ class ChebyKANFunction(torch.autograd.Function):
                               coeff_code(c.dtype))
         stream = _lib.stream_ptr(dev)
         packed = torch.empty(lib.ckan_packed_bytes(desc), dtype=torch.uint8, device=dev)
-        if spec is None:
-            _lib.check(lib.ckan_pack_coeffs(desc, c.data_ptr(), packed.data_ptr(), stream))
-        else:
-            _lib.check(lib.ckan_pack_coeffs_basis(desc, spec, c.data_ptr(), packed.data_ptr(), stream))
         t = torch.empty(lib.ckan_tcache_elems(desc), dtype=torch.float32, device=dev)
         y = torch.empty(x32.shape[0], out_dim, dtype=torch.float32, device=dev)
         ws_bytes = lib.ckan_fwd_workspace_bytes(desc)
         ws = _forward_workspace(dev, ws_bytes) if ws_bytes else None
-        _lib.check(lib.ckan_forward(desc, x32.data_ptr(), packed.data_ptr(), y.data_ptr(),
-                                    t.data_ptr(), _lib.ptr(ws), ws_bytes, stream))
+        # pack (in the family's basis when a spec is given) and forward in one call
+        _lib.check(lib.ckan_pack_forward(desc, spec,
+                                         c.data_ptr(), packed.data_ptr(), x32.data_ptr(),
+                                         y.data_ptr(), t.data_ptr(), _lib.ptr(ws), ws_bytes, stream))
         ctx.save_for_backward(t, packed)
         ctx.desc = desc
         ctx.spec = spec

@@ -463,3 +463,56 @@ def test_adam_resumes_from_a_torch_optim_checkpoint():
         pd.grad = gr.cuda()
         ours.step()
     assert torch.allclose(pd.detach().cpu(), pr.detach(), rtol=0, atol=1e-6)
+
+
+@pytest.mark.parametrize("B,I,O,deg,compute,family", [
+    (8192, 1024, 1024, 8, 1, None),  # unsplit pipelined forward sums the bias; tanh in the pack launch
+    (16384, 512, 512, 16, 1, None),  # the same at degree 16 (config-4 layer shape)
+    (8192, 1024, 1024, 8, 0, "jacobi"),  # fp32, family basis, bias summed in the forward
+    (1000, 100, 150, 6, 0, None),    # padded inputs: tanh launched on its own
+    (300, 256, 200, 3, 1, None),     # split small-batch forward: bias reduced by a launch
+    (20, 512, 64, 8, 1, None),       # streaming forward (tanh computed in the stream kernel)
+    (2048, 256, 256, 16, 1, "jacobi"),
+])
+def test_pack_forward_equals_pack_then_forward(B, I, O, deg, compute, family):
+    """ckan_pack_forward gives the bits of ckan_pack_coeffs(_basis) followed
+    by ckan_forward: y, the tanh cache and the whole packed buffer."""
+    import ctypes
+    from kan_amd import _lib
+    lib = _lib.load()
+    print(f"pack_forward B={B} I={I} O={O} deg={deg} compute={compute} family={family}", flush=True)
+    g = torch.Generator().manual_seed(B + I + deg)
+    x = (torch.randn(B, I, generator=g) * 1.5).cuda()
+    c = (torch.randn(I, O, deg + 1, generator=g) / (I * (deg + 1))).cuda()
+    d = _lib.make_desc(B, I, O, deg, compute, 0)
+    spec = _lib.make_spec(_lib.CKAN_BASIS_JACOBI, deg, 0.5, -0.25) if family else None
+    s = _lib.stream_ptr(x.device)
+    nb = lib.ckan_packed_bytes(ctypes.byref(d))
+    nt = lib.ckan_tcache_elems(ctypes.byref(d))
+    wsb = lib.ckan_fwd_workspace_bytes(ctypes.byref(d))
+    outs = []
+    for fused in (False, True):
+        packed = torch.zeros(nb, dtype=torch.uint8, device="cuda")
+        t = torch.zeros(nt, device="cuda")
+        y = torch.zeros(B, O, device="cuda")
+        ws = torch.zeros(max(wsb, 256), dtype=torch.uint8, device="cuda")
+        if fused:
+            _lib.check(lib.ckan_pack_forward(ctypes.byref(d), spec, c.data_ptr(), packed.data_ptr(),
+                                             x.data_ptr(), y.data_ptr(), t.data_ptr(), ws.data_ptr(),
+                                             wsb, s))
+        else:
+            if spec is None:
+                _lib.check(lib.ckan_pack_coeffs(ctypes.byref(d), c.data_ptr(), packed.data_ptr(), s))
+            else:
+                _lib.check(lib.ckan_pack_coeffs_basis(ctypes.byref(d), spec, c.data_ptr(),
+                                                      packed.data_ptr(), s))
+            _lib.check(lib.ckan_forward(ctypes.byref(d), x.data_ptr(), packed.data_ptr(), y.data_ptr(),
+                                        t.data_ptr(), ws.data_ptr(), wsb, s))
+        torch.cuda.synchronize()
+        outs.append((y, t, packed))
+    (y0, t0, p0), (y1, t1, p1) = outs
+    assert torch.equal(y0, y1)
+    assert torch.equal(t0, t1)
+    assert torch.equal(p0, p1)
+    if family is None and B * I <= 4096 * 1024:
+        assert _rel(y1.cpu(), orc.layer_forward(x.cpu(), c.cpu())) <= (FP32_TOL if compute == 0 else BF16_TOL)
