@@ -54,6 +54,57 @@ class BasisFunction(ABC):
         """Default squash to (-1, 1) (kan/basis/base.py:67-78)."""
         return torch.tanh(x)
 
+    def _spec_or_none(self):
+        spec = getattr(self, "spec", None)
+        return spec() if callable(spec) else None
+
+    def derivative(self, x: torch.Tensor, coefficients: torch.Tensor, order: int = 1) -> torch.Tensor:
+        """[B, out]: sum over inputs of the order-th x-derivative of each
+        univariate function f_{i,o}(x_i) = sum_n C[i,o,n] P_n(normalize_input(x_i))
+        (kan/basis/base.py:81-94, kan/basis/chebyshev.py:174-228).
+
+        Divergence: the reference's Chebyshev derivative coefficients are wrong
+        from degree 3 on and leave out the input map's chain factor; this is the
+        exact derivative in x, the same quantity KANLayer.compute_derivatives
+        returns (degree + order <= 16)."""
+        check = getattr(self, "_check_input_map", None)
+        if callable(check):
+            check()
+        x = x.reshape(-1, coefficients.shape[0])
+        return F.derivatives(x, coefficients, self._spec_or_none(), order,
+                             getattr(self, "compute", "fp32"))
+
+    def numerical_derivative(self, x: torch.Tensor, coefficients: torch.Tensor, order: int = 1,
+                             eps: float = 1e-6) -> torch.Tensor:
+        """Central finite differences of forward in x, shifting every input by
+        the same step, so order 1 approximates derivative(x, coefficients, 1)
+        (kan/basis/base.py:96-125).  Divergence: for order > 1 the reference
+        differentiates its first derivative as if it were coefficients; this
+        applies the central difference order times to the forward."""
+        if order < 0:
+            raise ValueError(f"order must be >= 0, got {order}")
+        with torch.no_grad():
+            def diff(k: int, xs: torch.Tensor) -> torch.Tensor:
+                if k == 0:
+                    return self.forward(xs, coefficients)
+                return (diff(k - 1, xs + eps) - diff(k - 1, xs - eps)) / (2 * eps)
+            return diff(order, x)
+
+    @staticmethod
+    def to_numpy(x):
+        """torch tensor -> numpy array (kan/basis/base.py:127-139)."""
+        if isinstance(x, torch.Tensor):
+            return x.detach().cpu().numpy()
+        return x
+
+    @staticmethod
+    def normalize_domain(x: torch.Tensor, src_domain: Tuple[float, float],
+                         dst_domain: Tuple[float, float]) -> torch.Tensor:
+        """Linear map of src_domain onto dst_domain (kan/basis/base.py:178-196)."""
+        src_min, src_max = src_domain
+        dst_min, dst_max = dst_domain
+        return ((x - src_min) / (src_max - src_min)) * (dst_max - dst_min) + dst_min
+
 
 class ChebyshevBasis(BasisFunction):
     """Chebyshev polynomials of the first kind, T_n(tanh x).

@@ -231,10 +231,18 @@ class HermiteKANLayer(_ComputeMixin, KANLayer):
 
 
 class KANSequential(nn.Sequential):
-    """Sequential container of KAN layers (kan/layers/base.py:144-166)."""
+    """Sequential container of KAN layers (kan/layers/base.py:144-193)."""
 
     def get_analytical_form(self) -> List[Dict[str, Any]]:
         return [m.get_analytical_form() for m in self if isinstance(m, KANLayer)]
+
+    def visualize_network(self, **kwargs):
+        """Not provided, as in the reference (kan/layers/base.py:168-179)."""
+        raise NotImplementedError("Network visualization is not implemented yet")
+
+    def jacobian(self, x: torch.Tensor) -> torch.Tensor:
+        """Not provided, as in the reference (kan/layers/base.py:181-193)."""
+        raise NotImplementedError("Network Jacobian computation is not implemented yet")
 
 
 LAYER_REGISTRY = {"chebykan": ChebyKANLayer, "jacobikan": JacobiKANLayer,

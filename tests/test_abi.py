@@ -154,3 +154,16 @@ def test_adam_state_dict_interoperates_with_torch_optim():
     back = torch.optim.Adam([torch.nn.Parameter(p.detach().clone())], lr=0.01)
     back.load_state_dict(ours.state_dict())
     assert float(next(iter(back.state.values()))["step"]) == 2.0
+
+
+def test_basis_helpers_and_network_stubs_mirror_reference():
+    import kan_amd
+    b = kan_amd.ChebyshevBasis(degree=3)
+    x = torch.tensor([[0.0, 0.5], [1.0, 2.0]])
+    assert torch.allclose(b.normalize_domain(x, (0.0, 2.0), (-1.0, 1.0)), x - 1.0)
+    assert b.to_numpy(x).shape == (2, 2)
+    seq = kan_amd.KANSequential(kan_amd.ChebyKANLayer(2, 2, 2))
+    with pytest.raises(NotImplementedError, match="visualization"):
+        seq.visualize_network()
+    with pytest.raises(NotImplementedError, match="Jacobian"):
+        seq.jacobian(torch.zeros(1, 2))

@@ -148,3 +148,30 @@ def test_derivative_errors():
     layer64 = kan_amd.ChebyKANLayer(8, 4, 3).cuda().double()
     with pytest.raises(RuntimeError):
         layer64.compute_derivatives(x.double(), order=1)
+
+
+def test_basis_derivative_and_numerical_derivative():
+    """ChebyshevBasis.derivative is the exact x-derivative summed over inputs
+    (what compute_derivatives returns); numerical_derivative (central
+    differences of forward, every input shifted together) approximates it, at
+    order 1 and, unlike the reference's recursion, at order 2."""
+    import kan_amd
+    torch.manual_seed(3)
+    m = kan_amd.ChebyKANLayer(6, 4, 5).cuda()
+    b = m.basis
+    x = (torch.rand(32, 6) * 2 - 1).cuda()
+    c = m.cheby_coeffs.detach()
+    for order in (1, 2):
+        exact = b.derivative(x, c, order)
+        assert torch.allclose(exact, m.compute_derivatives(x, order))
+        c64 = c.double().cpu()
+        # fp64 finite differences of the oracle's forward, for the same quantity
+        from oracle import chebykan_oracle as orc
+        h = 1e-4
+        f = lambda xs: torch.from_numpy(orc.forward_fp64(xs.numpy(), c64.numpy()))
+        xc = x.double().cpu()
+        ref = ((f(xc + h) - f(xc - h)) / (2 * h) if order == 1
+               else (f(xc + h) - 2 * f(xc) + f(xc - h)) / (h * h))
+        assert ((exact.double().cpu() - ref).norm() / ref.norm()).item() <= 1e-4
+        num = b.numerical_derivative(x, c, order, eps=1e-2)
+        assert ((num.double().cpu() - ref).norm() / ref.norm()).item() <= 5e-2
