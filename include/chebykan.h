@@ -47,6 +47,16 @@ typedef enum ckan_dtype {
   CKAN_DTYPE_BF16 = 1
 } ckan_dtype;
 
+/* How the layer maps an input x to the argument t of its basis. */
+typedef enum ckan_input_map {
+  CKAN_INPUT_TANH = 0,    /* t = tanh(x), the reference's default
+                             (kan/basis/chebyshev.py:68-78)                */
+  CKAN_INPUT_AFFINE = 1   /* t = in_scale * x + in_shift: the Hermite
+                             layer's map of a finite domain onto [-3, 3]
+                             (kan/basis/hermite.py:102-112), expressed on
+                             [-1, 1] with the basis scale 3               */
+} ckan_input_map;
+
 /* Problem descriptor: one ChebyKANLayer(in_dim, out_dim, degree) applied to a
  * batch of `batch` rows (kan/layers/chebykan.py:21-22,64). */
 typedef struct ckan_desc {
@@ -56,7 +66,9 @@ typedef struct ckan_desc {
   int32_t degree;       /* deg; D = deg + 1 coefficients per (i, o)        */
   int32_t compute;      /* ckan_compute                                    */
   int32_t coeff_dtype;  /* ckan_dtype of C passed to ckan_pack_coeffs      */
-  int32_t reserved;     /* must be 0                                       */
+  int32_t input_map;    /* ckan_input_map (0: tanh)                        */
+  float in_scale;       /* CKAN_INPUT_AFFINE: t = in_scale * x + in_shift  */
+  float in_shift;       /* (both 0 with CKAN_INPUT_TANH)                   */
 } ckan_desc;
 
 /* ---- sizes (host only, no device work) ---------------------------------- */

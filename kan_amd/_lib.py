@@ -39,8 +39,14 @@ class CkanDesc(ctypes.Structure):
         ("degree", ctypes.c_int32),
         ("compute", ctypes.c_int32),
         ("coeff_dtype", ctypes.c_int32),
-        ("reserved", ctypes.c_int32),
+        ("input_map", ctypes.c_int32),
+        ("in_scale", ctypes.c_float),
+        ("in_shift", ctypes.c_float),
     ]
+
+
+CKAN_INPUT_TANH = 0
+CKAN_INPUT_AFFINE = 1
 
 
 CKAN_BASIS_CHEBYSHEV = 0
@@ -186,9 +192,14 @@ def check(rc: int) -> None:
 
 
 def make_desc(batch: int, in_dim: int, out_dim: int, degree: int, compute: int,
-              coeff_dtype: int) -> CkanDesc:
+              coeff_dtype: int, affine=None) -> CkanDesc:
+    """``affine`` = (scale, shift) selects the input map t = scale * x + shift
+    instead of tanh(x)."""
+    if affine is None:
+        return CkanDesc(int(batch), int(in_dim), int(out_dim), int(degree), int(compute),
+                        int(coeff_dtype), CKAN_INPUT_TANH, 0.0, 0.0)
     return CkanDesc(int(batch), int(in_dim), int(out_dim), int(degree), int(compute),
-                    int(coeff_dtype), 0)
+                    int(coeff_dtype), CKAN_INPUT_AFFINE, float(affine[0]), float(affine[1]))
 
 
 def stream_ptr(device: torch.device) -> int:

@@ -223,17 +223,26 @@ class HermiteBasis(BasisFunction):
         fam = _lib.CKAN_BASIS_HERMITE if self.scaling == "physicist" else _lib.CKAN_BASIS_HERMITE_E
         return _lib.make_spec(fam, self.degree, 0.0, 0.0, 3.0)
 
+    def _affine(self):
+        """(a, b) with u = a x + b: the finite-domain map onto [-3, 3] of
+        kan/basis/hermite.py:102-112, z = 6 (x - lo) / (hi - lo) - 3, written
+        as z = 3 u with u on [-1, 1] (the basis then runs at scale 3, as for
+        the 3 tanh(x) map); None for the tanh map."""
+        if not self._affine_map():
+            return None
+        lo, hi = self._domain
+        return 2.0 / (hi - lo), -(hi + lo) / (hi - lo)
+
     def _check_input_map(self) -> None:
+        """compute_derivatives / jacobian serve the tanh input map only."""
         if self._affine_map():
             raise RuntimeError(
-                "kan_amd HermiteBasis: a finite domain with normalize_domain=True maps inputs "
-                "linearly (no tanh); this build's HIP path implements the 3*tanh(x) input map "
-                "only. Pass domain=None or normalize_domain=False.")
+                "kan_amd HermiteBasis: derivatives and the Jacobian are computed for the "
+                "3*tanh(x) input map only; this layer maps a finite domain linearly.")
 
     def forward(self, x: torch.Tensor, coefficients: torch.Tensor) -> torch.Tensor:
-        self._check_input_map()
         x = x.view(-1, coefficients.shape[0])
-        return F.family_kan(x, coefficients, self.spec(), self.compute)
+        return F.family_kan(x, coefficients, self.spec(), self.compute, self._affine())
 
     def basis_functions(self, x: torch.Tensor) -> torch.Tensor:
         """H_0..H_degree (or He_n) of an already-normalised x (kan/basis/hermite.py:141-233)."""

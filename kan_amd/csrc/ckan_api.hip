@@ -81,7 +81,15 @@ int validate_desc(const ckan_desc* d) {
     return fail(CKAN_ERR_INVALID_ARG, "unknown compute mode %d", d->compute);
   if (d->coeff_dtype != CKAN_DTYPE_F32 && d->coeff_dtype != CKAN_DTYPE_BF16)
     return fail(CKAN_ERR_INVALID_ARG, "unknown coefficient dtype %d", d->coeff_dtype);
-  if (d->reserved != 0) return fail(CKAN_ERR_INVALID_ARG, "reserved field must be 0");
+  if (d->input_map == CKAN_INPUT_TANH) {
+    if (d->in_scale != 0.0f || d->in_shift != 0.0f)
+      return fail(CKAN_ERR_INVALID_ARG, "in_scale/in_shift must be 0 with the tanh input map");
+  } else if (d->input_map == CKAN_INPUT_AFFINE) {
+    if (!isfinite(d->in_scale) || !isfinite(d->in_shift) || d->in_scale == 0.0f)
+      return fail(CKAN_ERR_INVALID_ARG, "affine input map needs a finite non-zero in_scale and finite in_shift");
+  } else {
+    return fail(CKAN_ERR_INVALID_ARG, "unknown input map %d", d->input_map);
+  }
   // Index arithmetic inside the kernels uses 64-bit offsets; bound the
   // 32-bit grid dimensions.
   if (d->in_dim > (1 << 20) || d->out_dim > (1 << 20))
@@ -92,7 +100,18 @@ int validate_desc(const ckan_desc* d) {
 }
 
 Plan plan_of(const ckan_desc* d) {
-  return make_plan(d->batch, d->in_dim, d->out_dim, d->degree, d->compute == CKAN_COMPUTE_BF16);
+  Plan p = make_plan(d->batch, d->in_dim, d->out_dim, d->degree, d->compute == CKAN_COMPUTE_BF16);
+  p.imap = d->input_map;
+  p.ima = d->in_scale;
+  p.imb = d->in_shift;
+  return p;
+}
+
+// Paths that implement only the tanh input map.
+int require_tanh_map(const ckan_desc* d, const char* what) {
+  if (d->input_map != CKAN_INPUT_TANH)
+    return fail(CKAN_ERR_UNSUPPORTED, "%s: only the tanh input map is served", what);
+  return CKAN_OK;
 }
 
 inline bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
@@ -384,6 +403,7 @@ int ckan_forward_f64(const ckan_desc* desc, const double* x, const double* coeff
   if (rc) return rc;
   if (desc->compute != CKAN_COMPUTE_FP32 || desc->coeff_dtype != CKAN_DTYPE_F32)
     return fail(CKAN_ERR_INVALID_ARG, "fp64 path: desc->compute and desc->coeff_dtype must be 0");
+  if ((rc = require_tanh_map(desc, "fp64 path"))) return rc;
   if (desc->batch == 0) return CKAN_OK;
   if (!x || !coeffs || !y || !t_cache) return fail(CKAN_ERR_INVALID_ARG, "x/coeffs/y/t_cache is NULL");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
@@ -398,6 +418,7 @@ int ckan_backward_f64(const ckan_desc* desc, const double* t_cache, const double
   if (rc) return rc;
   if (desc->compute != CKAN_COMPUTE_FP32 || desc->coeff_dtype != CKAN_DTYPE_F32)
     return fail(CKAN_ERR_INVALID_ARG, "fp64 path: desc->compute and desc->coeff_dtype must be 0");
+  if ((rc = require_tanh_map(desc, "fp64 path"))) return rc;
   if (!dx && !dcoeffs) return CKAN_OK;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (desc->batch == 0) {
@@ -538,6 +559,7 @@ int derivative_xform(const ckan_basis_spec* spec, int degree, int order, bool tr
 int check_f32_layer(const ckan_desc* desc) {
   int rc = validate_desc(desc);
   if (rc) return rc;
+  if ((rc = require_tanh_map(desc, "derivatives"))) return rc;
   if (desc->coeff_dtype != CKAN_DTYPE_F32)
     return fail(CKAN_ERR_UNSUPPORTED, "derivatives take fp32 coefficients");
   return CKAN_OK;

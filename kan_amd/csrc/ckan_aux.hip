@@ -11,7 +11,7 @@ namespace ckan {
 // (a power of two dividing 256) take float4 columns; 256/tpr rows per block.
 __global__ void __launch_bounds__(256)
 k_tanh(const float* __restrict__ x, float* __restrict__ t, int64_t B, int I, int I_sg, int tpr,
-       int xal) {
+       int xal, int imap, float ima, float imb) {
   const int rpb = 256 / tpr;
   const int64_t b = (int64_t)blockIdx.x * rpb + threadIdx.x / tpr;
   if (b >= B) return;
@@ -30,7 +30,7 @@ k_tanh(const float* __restrict__ x, float* __restrict__ t, int64_t B, int I, int
     }
     f32x4_t r;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) r[j] = (i + j < I) ? tanhf(v[j]) : 0.0f;
+    for (int j = 0; j < 4; ++j) r[j] = (i + j < I) ? input_map(v[j], imap, ima, imb) : 0.0f;
     *reinterpret_cast<f32x4_t*>(tr + i) = r;
   }
 }
@@ -41,7 +41,8 @@ k_tanh(const float* __restrict__ x, float* __restrict__ t, int64_t B, int I, int
 // Two per thread measured fastest (one to eight tried).
 constexpr int kTanhU = 2;
 __global__ void __launch_bounds__(256)
-k_tanh_flat(const f32x4_t* __restrict__ x, f32x4_t* __restrict__ t, int64_t n4) {
+k_tanh_flat(const f32x4_t* __restrict__ x, f32x4_t* __restrict__ t, int64_t n4, int imap, float ima,
+            float imb) {
   const int64_t base = (int64_t)blockIdx.x * (256 * kTanhU) + threadIdx.x;
   f32x4_t v[kTanhU];
 #pragma unroll
@@ -54,7 +55,7 @@ k_tanh_flat(const f32x4_t* __restrict__ x, f32x4_t* __restrict__ t, int64_t n4) 
     const int64_t k = base + u * 256;
     f32x4_t r;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) r[j] = tanhf(v[u][j]);
+    for (int j = 0; j < 4; ++j) r[j] = input_map(v[u][j], imap, ima, imb);
     if (k < n4) t[k] = r;
   }
 }
@@ -85,6 +86,8 @@ struct TanhJob {
   const f32x4_t* x;
   f32x4_t* t;
   int64_t n4, per;
+  int imap;
+  float ima, imb;
 };
 constexpr int kPackTanhU = 8;  // tanh float4 per thread in flight at once
 
@@ -231,7 +234,7 @@ k_pack(const CT* __restrict__ C, typename Elem<BF>::type* __restrict__ Cf,
       const int64_t k = c0 + tid + u * 256;
       f32x4_t r;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) r[j] = tanhf(tx[u][j]);
+      for (int j = 0; j < 4; ++j) r[j] = input_map(tx[u][j], tj.imap, tj.ima, tj.imb);
       if (k < tj1) tj.t[k] = r;
     }
   }
@@ -485,14 +488,15 @@ void launch_tanh(const float* x, float* t, const Plan& p, hipStream_t s) {
   if (p.I == p.I_sg && p.I % 4 == 0 && is_al16(x)) {
     const int64_t n4 = p.B * p.I / 4;
     hipLaunchKernelGGL(k_tanh_flat, dim3((unsigned)ceil_div(n4, 256 * kTanhU)), dim3(256), 0, s,
-                       reinterpret_cast<const f32x4_t*>(x), reinterpret_cast<f32x4_t*>(t), n4);
+                       reinterpret_cast<const f32x4_t*>(x), reinterpret_cast<f32x4_t*>(t), n4, p.imap,
+                       p.ima, p.imb);
     return;
   }
   int tpr = 1;
   while (tpr < 256 && tpr < p.I_sg / 4) tpr *= 2;
   const int64_t blocks = ceil_div(p.B, 256 / tpr);
   hipLaunchKernelGGL(k_tanh, dim3((unsigned)blocks), dim3(256), 0, s, x, t, p.B, p.I, p.I_sg, tpr,
-                     (int)is_al16(x));
+                     (int)is_al16(x), p.imap, p.ima, p.imb);
 }
 
 template <int P, bool BF, bool XF>
@@ -534,7 +538,7 @@ bool pack_tanh_fusable(const Plan& p, const float* x) {
 void launch_pack(const void* C, bool c_bf16, void* packed, const Plan& p, hipStream_t s,
                  const BasisXform* xf, bool reduce_bias, const float* x, float* t) {
   char* base = reinterpret_cast<char*>(packed);
-  TanhJob tj{nullptr, nullptr, 0, 0};
+  TanhJob tj{nullptr, nullptr, 0, 0, p.imap, p.ima, p.imb};
   if (x && t) {  // pack_tanh_fusable(p, x) holds: the caller checked
     tj.x = reinterpret_cast<const f32x4_t*>(x);
     tj.t = reinterpret_cast<f32x4_t*>(t);

@@ -76,7 +76,17 @@ struct Plan {
   int64_t Bc, KBc; // rows padded to kDcStageRows; dC reduction k-blocks
   int NBB;         // prep_dy row blocks (colsum partials)
   int esz;         // bytes per packed operand element (2 bf16, 4 fp32)
+  int imap;        // input map: 0 t = tanh(x), 1 t = ima * x + imb
+  float ima, imb;
 };
+
+// The basis argument t of an input x, and dt/dx as a function of t.
+__device__ __forceinline__ float input_map(float x, int imap, float a, float b) {
+  return imap ? fmaf(a, x, b) : tanhf(x);
+}
+__device__ __forceinline__ float input_slope(float t, const Plan& p) {
+  return p.imap ? p.ima : 1.0f - t * t;
+}
 
 // How the dC kernels write the finished gradient g into the destination d:
 // store it, add it, or (for a caller that wants only the updated parameter,
@@ -175,6 +185,8 @@ inline Plan make_plan(int64_t B, int I, int O, int deg, bool bf16) {
   p.KBc = p.Bc / 16;
   p.NBB = (int)ceil_div(B, kPrepRows);
   p.esz = bf16 ? 2 : 4;
+  p.imap = 0;
+  p.ima = p.imb = 0.0f;
   return p;
 }
 

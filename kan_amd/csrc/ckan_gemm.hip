@@ -661,7 +661,7 @@ k_fwd_stream(const float* __restrict__ x, float* __restrict__ tc,
       const int sg = sg0 + j;
       float tv[LT];
 #pragma unroll
-      for (int q = 0; q < LT; ++q) tv[q] = TPRE ? xv[mi][j][q] : tanhf(xv[mi][j][q]);
+      for (int q = 0; q < LT; ++q) tv[q] = TPRE ? xv[mi][j][q] : input_map(xv[mi][j][q], p.imap, p.ima, p.imb);
       if (!TPRE && nb == 0 && r < p.B && sg < nsg) {  // the tanh cache, written once
         f32x4_t* dst = reinterpret_cast<f32x4_t*>(tc + (size_t)r * p.I_sg + (size_t)sg * G::SGI + g * LT);
 #pragma unroll
@@ -858,7 +858,7 @@ k_dx_pipe(const typename Elem<BF>::type* __restrict__ dYx,
         up = u;
         u = un;
       }
-      if (icol && r < p.B) dx[r * p.I + i] = sum * (1.0f - tv[v] * tv[v]);
+      if (icol && r < p.B) dx[r * p.I + i] = sum * input_slope(tv[v], p);
     }
   }
 }
@@ -1063,7 +1063,7 @@ k_dx_dh(const typename Elem<BF>::type* __restrict__ dYx,
       const float t = tt[keep][v];
       // fixed order: the lower degrees' half first
       const float sum = d ? other + part[keep][v] : part[keep][v] + other;
-      res[v] = sum * (1.0f - t * t);
+      res[v] = sum * input_slope(t, p);
     }
     float* dp = dx + r0 * p.I + i;
     if (icol && r0 - 4 * g + 32 <= p.B) {
@@ -1192,7 +1192,7 @@ k_dx(const typename Elem<BF>::type* __restrict__ dYx, const typename Elem<BF>::t
         up = u;
         u = un;
       }
-      if (ok) dx[r * p.I + i] = s * (1.0f - tv * tv);
+      if (ok) dx[r * p.I + i] = s * input_slope(tv, p);
     }
   }
 }

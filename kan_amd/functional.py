@@ -64,7 +64,8 @@ class ChebyKANFunction(torch.autograd.Function):
     """
 
     @staticmethod
-    def forward(ctx, x: torch.Tensor, coeffs: torch.Tensor, compute: str = "fp32", spec=None):
+    def forward(ctx, x: torch.Tensor, coeffs: torch.Tensor, compute: str = "fp32", spec=None,
+                affine=None):
         _require_device(x, coeffs)
         if coeffs.dim() != 3:
             raise RuntimeError(f"coefficients must be [in, out, degree+1], got {tuple(coeffs.shape)}")
@@ -76,7 +77,7 @@ class ChebyKANFunction(torch.autograd.Function):
         x32 = x.contiguous() if x.dtype == torch.float32 else x.float().contiguous()
         c = coeffs.detach().contiguous()
         desc = _lib.make_desc(x32.shape[0], in_dim, out_dim, dd - 1, compute_code(compute),
-                              coeff_code(c.dtype))
+                              coeff_code(c.dtype), affine)
         stream = _lib.stream_ptr(dev)
         packed = torch.empty(lib.ckan_packed_bytes(desc), dtype=torch.uint8, device=dev)
         t = torch.empty(lib.ckan_tcache_elems(desc), dtype=torch.float32, device=dev)
@@ -100,7 +101,7 @@ class ChebyKANFunction(torch.autograd.Function):
         desc = ctx.desc
         need_dx, need_dc = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
         if not (need_dx or need_dc):
-            return None, None, None, None
+            return None, None, None, None, None
         lib = _lib.load()
         dev = dy.device
         dy32 = dy.contiguous() if dy.dtype == torch.float32 else dy.float().contiguous()
@@ -120,7 +121,7 @@ class ChebyKANFunction(torch.autograd.Function):
             dx = dx.to(ctx.x_dtype)
         if dc is not None and ctx.c_dtype != torch.float32:
             dc = dc.to(ctx.c_dtype)
-        return dx, dc, None, None
+        return dx, dc, None, None, None
 
 
 class ChebyshevBasisFunction(torch.autograd.Function):
@@ -238,12 +239,14 @@ def chebykan(x: torch.Tensor, coeffs: torch.Tensor, compute: str = "fp32") -> to
     return ChebyKANFunction.apply(x, coeffs, compute, None)
 
 
-def family_kan(x: torch.Tensor, coeffs: torch.Tensor, spec, compute: str = "fp32") -> torch.Tensor:
-    """y = einsum('bid,iod->bo', P(s tanh x), C) for the family of ``spec``."""
+def family_kan(x: torch.Tensor, coeffs: torch.Tensor, spec, compute: str = "fp32",
+               affine=None) -> torch.Tensor:
+    """y = einsum('bid,iod->bo', P(s u), C) for the family of ``spec``, with
+    u = tanh x, or u = affine[0] x + affine[1] when ``affine`` is given."""
     if coeffs.dtype == torch.float64:
         raise RuntimeError("kan_amd: the fp64 path serves the Chebyshev layer; Jacobi / Hermite "
                            "layers take float32 or bfloat16 coefficients")
-    return ChebyKANFunction.apply(x, coeffs, compute, spec)
+    return ChebyKANFunction.apply(x, coeffs, compute, spec, affine)
 
 
 def family_basis(t: torch.Tensor, spec) -> torch.Tensor:

@@ -93,19 +93,24 @@ def family_basis(t: torch.Tensor, family: str, degree: int, alpha: float = 0.0,
 
 
 def family_forward(x: torch.Tensor, coeffs: torch.Tensor, family: str, alpha: float = 0.0,
-                   beta: float = 0.0) -> torch.Tensor:
-    """y = einsum('bid,iod->bo', P(map(x)), C); map = tanh (Jacobi) or 3 tanh (Hermite)."""
+                   beta: float = 0.0, domain: Optional[Tuple[float, float]] = None,
+                   normalize_domain: bool = True) -> torch.Tensor:
+    """y = einsum('bid,iod->bo', P(map(x)), C); map = tanh (Jacobi) or the
+    Hermite input map of hermite_normalize (3 tanh, or the affine map of a
+    finite domain) (jacobi.py:96-117, hermite.py:118-139)."""
     x = x.view(-1, coeffs.shape[0])
-    t = torch.tanh(x) if family == "jacobi" else hermite_normalize(x)
+    t = torch.tanh(x) if family == "jacobi" else hermite_normalize(x, domain, normalize_domain)
     basis = family_basis(t, family, coeffs.shape[2] - 1, alpha, beta)
     return torch.einsum("bid,iod->bo", basis, coeffs)
 
 
 def family_forward_backward(x: torch.Tensor, coeffs: torch.Tensor, dy: torch.Tensor, family: str,
-                            alpha: float = 0.0, beta: float = 0.0):
+                            alpha: float = 0.0, beta: float = 0.0,
+                            domain: Optional[Tuple[float, float]] = None,
+                            normalize_domain: bool = True):
     xr = x.detach().clone().requires_grad_(True)
     cr = coeffs.detach().clone().requires_grad_(True)
-    y = family_forward(xr, cr, family, alpha, beta)
+    y = family_forward(xr, cr, family, alpha, beta, domain, normalize_domain)
     y.backward(dy)
     return y.detach(), xr.grad.detach(), cr.grad.detach()
 
@@ -176,24 +181,34 @@ def _family_deriv_fp64(t, family, degree, alpha, beta):
     return out
 
 
-def family_forward_fp64(x: np.ndarray, c: np.ndarray, family: str, alpha: float = 0.0,
-                        beta: float = 0.0) -> np.ndarray:
+def _input_map_fp64(x: np.ndarray, family: str, domain):
+    """(t, dt/dx) of the layer's input map in float64: tanh (Jacobi), 3 tanh
+    (Hermite), or for Hermite with a finite domain (lo, hi) the affine map
+    t = 6 (x - lo) / (hi - lo) - 3."""
+    x = np.asarray(x, dtype=np.float64)
+    if family != "jacobi" and domain is not None:
+        lo, hi = domain
+        a = 6.0 / (hi - lo)
+        return a * (x - lo) - 3.0, np.full_like(x, a)
     s = 1.0 if family == "jacobi" else 3.0
-    t = s * np.tanh(np.asarray(x, dtype=np.float64))
+    u = np.tanh(x)
+    return s * u, s * (1.0 - u * u)
+
+
+def family_forward_fp64(x: np.ndarray, c: np.ndarray, family: str, alpha: float = 0.0,
+                        beta: float = 0.0, domain=None) -> np.ndarray:
+    t, _ = _input_map_fp64(x, family, domain)
     return np.einsum("bid,iod->bo", _family_fp64(t, family, c.shape[2] - 1, alpha, beta), c)
 
 
 def family_backward_fp64(x: np.ndarray, c: np.ndarray, dy: np.ndarray, family: str,
-                         alpha: float = 0.0, beta: float = 0.0):
+                         alpha: float = 0.0, beta: float = 0.0, domain=None):
     """(dx, dC) of family_forward_fp64 for upstream gradient dy."""
-    x = np.asarray(x, dtype=np.float64)
-    s = 1.0 if family == "jacobi" else 3.0
-    u = np.tanh(x)
-    t = s * u
+    t, dtdx = _input_map_fp64(x, family, domain)
     deg = c.shape[2] - 1
     basis = _family_fp64(t, family, deg, alpha, beta)
     dbasis = _family_deriv_fp64(t, family, deg, alpha, beta)
     g = np.einsum("bo,iod->bid", dy, c)
-    dx = np.einsum("bid,bid->bi", g, dbasis) * s * (1.0 - u * u)
+    dx = np.einsum("bid,bid->bi", g, dbasis) * dtdx
     dc = np.einsum("bid,bo->iod", basis, dy)
     return dx, dc

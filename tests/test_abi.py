@@ -46,7 +46,9 @@ def _desc(B=8, I=4, O=3, deg=8, compute=0, cdt=0):
     ("degree", 17, _lib.CKAN_ERR_UNSUPPORTED),
     ("compute", 7, _lib.CKAN_ERR_INVALID_ARG),
     ("coeff_dtype", 5, _lib.CKAN_ERR_INVALID_ARG),
-    ("reserved", 1, _lib.CKAN_ERR_INVALID_ARG),
+    ("input_map", 1, _lib.CKAN_ERR_INVALID_ARG),   # affine with in_scale 0
+    ("input_map", 7, _lib.CKAN_ERR_INVALID_ARG),
+    ("in_scale", 0.5, _lib.CKAN_ERR_INVALID_ARG),  # set with the tanh map
 ])
 def test_descriptor_validation(field, value, code):
     lib = _lib.load()

@@ -134,3 +134,43 @@ def test_coeff_grad_transform_accumulates(I, O, deg):
     _lib.check(lib.ckan_coeff_grad_from_chebyshev(d, spec, inplace.data_ptr(), inplace.data_ptr(), 0, st))
     torch.cuda.synchronize()
     assert _rel(inplace, torch.einsum("iok,nk->ion", dcheb.double(), Mn)) <= FP32_TOL
+
+
+@pytest.mark.parametrize("compute,tol", [("fp32", FP32_TOL), ("bf16", BF16_TOL)])
+@pytest.mark.parametrize("scaling,B,I,O,deg", [
+    ("physicist", 300, 40, 70, 6),       # small-batch forward (split partials)
+    ("probabilist", 2048, 256, 128, 8),  # pipelined forward, tanh stage replaced in the pack launch
+    ("physicist", 20, 512, 64, 5),       # coefficient-streaming forward (affine map in the stream kernel)
+    ("probabilist", 1000, 100, 150, 12),  # padded inputs: the separate input-map launch
+])
+def test_hermite_finite_domain_affine_map(scaling, B, I, O, deg, compute, tol):
+    """HermiteKANLayer(domain=(lo, hi), normalize_domain=True) maps x linearly
+    onto [-3, 3] (kan/basis/hermite.py:102-112) instead of 3 tanh(x): y, dx
+    (chain factor 6 / (hi - lo)) and dC against the oracle, with some x outside
+    the domain."""
+    import kan_amd
+    print(f"hermite affine {scaling} {compute} B={B} I={I} O={O} deg={deg}", flush=True)
+    dom = (-2.0, 5.0)
+    torch.manual_seed(B + deg)
+    m = kan_amd.HermiteKANLayer(I, O, deg, scaling=scaling, domain=dom, normalize_domain=True,
+                                compute=compute)
+    c = m.hermite_coeffs.detach().clone()
+    g = torch.Generator().manual_seed(B + I)
+    # [-2.5, 5.5): partly outside [lo, hi], where |u| > 1 and T_k(u) grows
+    # like cosh(k acosh |u|) (bf16 rounding grows with it)
+    x = torch.rand(B, I, generator=g) * 8 - 2.5
+    dy = torch.randn(B, O, generator=g)
+    fam = "hermite" if scaling == "physicist" else "hermite_e"
+    c_ref = c  # the bf16 path rounds C M (the Chebyshev-basis coefficients), as for the tanh map
+    y_ref, dx_ref, dc_ref = fo.family_forward_backward(x, c_ref, dy, fam, domain=dom)
+    m = m.cuda()
+    xd = x.cuda().requires_grad_(True)
+    y = m(xd)
+    y.backward(dy.cuda())
+    torch.cuda.synchronize()
+    assert _rel(y, y_ref) <= tol
+    assert _rel(xd.grad, dx_ref) <= tol
+    assert _rel(m.hermite_coeffs.grad, dc_ref) <= tol
+    # the tanh map would give a different function
+    y_tanh = fo.family_forward(x, c_ref, fam)
+    assert _rel(y, y_tanh) > 10 * tol

@@ -217,10 +217,11 @@ def test_integration_ctypes_stub():
     class _Desc(ctypes.Structure):
         _fields_ = [("batch", ctypes.c_int64), ("in_dim", ctypes.c_int32), ("out_dim", ctypes.c_int32),
                     ("degree", ctypes.c_int32), ("compute", ctypes.c_int32),
-                    ("coeff_dtype", ctypes.c_int32), ("reserved", ctypes.c_int32)]
+                    ("coeff_dtype", ctypes.c_int32), ("input_map", ctypes.c_int32),
+                    ("in_scale", ctypes.c_float), ("in_shift", ctypes.c_float)]
 
     def chebykan_forward(x, C):
-        d = _Desc(x.shape[0], C.shape[0], C.shape[1], C.shape[2] - 1, 0, 0, 0)
+        d = _Desc(x.shape[0], C.shape[0], C.shape[1], C.shape[2] - 1, 0, 0, 0, 0.0, 0.0)
         s = torch.cuda.current_stream().cuda_stream
         packed = torch.empty(_L.ckan_packed_bytes(ctypes.byref(d)), dtype=torch.uint8, device=x.device)
         t = torch.empty(_L.ckan_tcache_elems(ctypes.byref(d)), device=x.device)

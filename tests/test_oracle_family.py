@@ -142,6 +142,40 @@ def test_family_backward_autograd_matches_closed_form_and_fd(family, alpha, beta
             assert float((fd[b] * dy.numpy()[b]).sum()) == pytest.approx(dx64[b, i], rel=1e-5, abs=1e-6)
 
 
+@pytest.mark.parametrize("family", ["hermite", "hermite_e"])
+def test_hermite_affine_domain_map_forward_backward(family):
+    """A finite domain with normalize_domain maps x linearly onto [-3, 3]
+    (kan/basis/hermite.py:102-112): the op-for-op forward equals the fp64 form
+    on that map, and the fp64 gradients (chain factor 6 / (hi - lo)) match
+    autograd and central differences, also for x outside the domain."""
+    g = torch.Generator().manual_seed(6)
+    B, I, O, deg, dom = 5, 3, 2, 6, (-2.0, 5.0)
+    x = torch.rand(B, I, generator=g, dtype=torch.float64) * 11 - 4  # some outside [lo, hi]
+    c = torch.randn(I, O, deg + 1, generator=g, dtype=torch.float64)
+    dy = torch.randn(B, O, generator=g, dtype=torch.float64)
+    y = fo.family_forward(x, c, family, domain=dom)
+    t = 6.0 / (dom[1] - dom[0]) * (x - dom[0]) - 3.0
+    assert torch.allclose(fo.hermite_normalize(x, dom), t)
+    np.testing.assert_allclose(y.numpy(), fo.family_forward_fp64(x.numpy(), c.numpy(), family, domain=dom),
+                               rtol=1e-10, atol=1e-10)
+    # the default (tanh) map gives a different function
+    assert not np.allclose(y.numpy(), fo.family_forward_fp64(x.numpy(), c.numpy(), family))
+    _, dx, dc = fo.family_forward_backward(x, c, dy, family, domain=dom)
+    dx64, dc64 = fo.family_backward_fp64(x.numpy(), c.numpy(), dy.numpy(), family, domain=dom)
+    np.testing.assert_allclose(dx.numpy(), dx64, rtol=1e-9, atol=1e-9 * np.abs(dx64).max())
+    np.testing.assert_allclose(dc.numpy(), dc64, rtol=1e-9, atol=1e-12)
+    h = 1e-6
+    xn = x.numpy()
+    for b in range(B):
+        for i in range(I):
+            xp, xm = xn.copy(), xn.copy()
+            xp[b, i] += h
+            xm[b, i] -= h
+            fd = (fo.family_forward_fp64(xp, c.numpy(), family, domain=dom)
+                  - fo.family_forward_fp64(xm, c.numpy(), family, domain=dom)) / (2 * h)
+            assert float((fd[b] * dy.numpy()[b]).sum()) == pytest.approx(dx64[b, i], rel=1e-5, abs=1e-6)
+
+
 # ---- library host function: the change of basis used by the HIP path ------
 
 def _M(family, deg, alpha=0.0, beta=0.0, scale=1.0):
