@@ -58,12 +58,17 @@ typedef enum ckan_input_map {
 } ckan_input_map;
 
 /* Problem descriptor: one ChebyKANLayer(in_dim, out_dim, degree) applied to a
- * batch of `batch` rows (kan/layers/chebykan.py:21-22,64). */
+ * batch of `batch` rows (kan/layers/chebykan.py:21-22,64).
+ * Degrees 0..16 run on the MFMA kernels in the compute precision.  Degrees
+ * 17..256 (the reference layer takes any degree, kan/layers/chebykan.py:21-51)
+ * run on vector-ALU kernels in fp32 whatever `compute` asks, with the tanh
+ * input map only; their packed buffer is C widened to fp32 in its own
+ * [in, out, D] layout and they need no workspace (the size queries return 0). */
 typedef struct ckan_desc {
   int64_t batch;        /* B: rows of x after x.view(-1, in_dim)          */
   int32_t in_dim;       /* I                                               */
   int32_t out_dim;      /* O                                               */
-  int32_t degree;       /* deg; D = deg + 1 coefficients per (i, o)        */
+  int32_t degree;       /* deg (0..256); D = deg + 1 coefficients per (i, o) */
   int32_t compute;      /* ckan_compute                                    */
   int32_t coeff_dtype;  /* ckan_dtype of C passed to ckan_pack_coeffs      */
   int32_t input_map;    /* ckan_input_map (0: tanh)                        */

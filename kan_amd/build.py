@@ -24,7 +24,7 @@ LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
 ARCH = "gfx950"
 
 SOURCES = ["ckan_api.hip", "ckan_aux.hip", "ckan_gemm.hip", "ckan_exec.hip", "ckan_family.hip",
-           "ckan_f64.hip"]
+           "ckan_valu.hip"]
 
 COMMON_FLAGS = [
     f"--offload-arch={ARCH}",

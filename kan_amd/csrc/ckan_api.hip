@@ -75,8 +75,9 @@ int validate_desc(const ckan_desc* d) {
   if (d->in_dim < 1) return fail(CKAN_ERR_INVALID_ARG, "in_dim must be >= 1 (got %d)", d->in_dim);
   if (d->out_dim < 1) return fail(CKAN_ERR_INVALID_ARG, "out_dim must be >= 1 (got %d)", d->out_dim);
   if (d->degree < 0) return fail(CKAN_ERR_INVALID_ARG, "degree must be >= 0 (got %d)", d->degree);
-  if (d->degree > 16)
-    return fail(CKAN_ERR_UNSUPPORTED, "degree %d > 16 is not supported by this build", d->degree);
+  if (d->degree > kValuMaxDegree)
+    return fail(CKAN_ERR_UNSUPPORTED, "degree %d > %d is not supported by this build", d->degree,
+                kValuMaxDegree);
   if (d->compute != CKAN_COMPUTE_FP32 && d->compute != CKAN_COMPUTE_BF16)
     return fail(CKAN_ERR_INVALID_ARG, "unknown compute mode %d", d->compute);
   if (d->coeff_dtype != CKAN_DTYPE_F32 && d->coeff_dtype != CKAN_DTYPE_BF16)
@@ -85,6 +86,9 @@ int validate_desc(const ckan_desc* d) {
     if (d->in_scale != 0.0f || d->in_shift != 0.0f)
       return fail(CKAN_ERR_INVALID_ARG, "in_scale/in_shift must be 0 with the tanh input map");
   } else if (d->input_map == CKAN_INPUT_AFFINE) {
+    if (d->degree > kMfmaMaxDegree)
+      return fail(CKAN_ERR_UNSUPPORTED, "the affine input map is served up to degree %d",
+                  kMfmaMaxDegree);
     if (!isfinite(d->in_scale) || !isfinite(d->in_shift) || d->in_scale == 0.0f)
       return fail(CKAN_ERR_INVALID_ARG, "affine input map needs a finite non-zero in_scale and finite in_shift");
   } else {
@@ -105,6 +109,14 @@ Plan plan_of(const ckan_desc* d) {
   p.ima = d->in_scale;
   p.imb = d->in_shift;
   return p;
+}
+
+// Layers above the MFMA kernels' degree limit run on the vector-ALU kernels
+// in fp32 (whatever desc->compute asks), with C copied to fp32 in its own
+// [I, O, D] layout as the "packed" buffer and a tanh cache of row pitch I.
+inline bool valu_route(const ckan_desc* d) { return d->degree > kMfmaMaxDegree; }
+inline int64_t valu_coeffs(const ckan_desc* d) {
+  return (int64_t)d->in_dim * d->out_dim * (d->degree + 1);
 }
 
 // Paths that implement only the tanh input map.
@@ -159,10 +171,28 @@ int ckan::backward_impl(const ckan_desc* desc, const float* t_cache, const void*
                         size_t ws_bytes, void* stream) {
   int rc = validate_desc(desc);
   if (rc) return rc;
-  const Plan p = plan_of(desc);
   const bool need_dx = dx != nullptr, need_dc = dcoeffs != nullptr;
   if (!need_dx && !need_dc) return CKAN_OK;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (valu_route(desc)) {
+    if (desc->batch == 0) {
+      if (need_dc && om.mode >= kDcSgd)
+        return fail(CKAN_ERR_UNSUPPORTED, "backward: an optimizer-applying call needs batch >= 1");
+      if (need_dc && om.mode == kDcStore) {
+        launch_zero_f32(dcoeffs, valu_coeffs(desc), s);
+        return check_launch("zero dcoeffs");
+      }
+      return CKAN_OK;
+    }
+    if (!t_cache || !dy || (need_dx && !packed))
+      return fail(CKAN_ERR_INVALID_ARG, "t_cache/dy/packed is NULL");
+    ProfScope ps("bwd_valu", s);
+    launch_backward_valu<float>(t_cache, static_cast<const float*>(packed), dy, dx, dcoeffs, om,
+                                desc->batch, desc->in_dim, desc->in_dim, desc->out_dim,
+                                desc->degree, s);
+    return check_launch("backward (vector ALU)");
+  }
+  const Plan p = plan_of(desc);
   if (p.B == 0) {
     // empty batch: dC = 0 (or unchanged when accumulating), dx is empty
     if (need_dc && om.mode >= kDcSgd)
@@ -227,24 +257,26 @@ const char* ckan_version(void) { return "kan_amd-chebykan 0.1.0 (gfx950)"; }
 
 size_t ckan_packed_bytes(const ckan_desc* desc) {
   if (validate_desc(desc) != CKAN_OK) return 0;
+  if (valu_route(desc)) return align256((size_t)valu_coeffs(desc) * sizeof(float));
   return packed_bytes(plan_of(desc));
 }
 
 size_t ckan_tcache_elems(const ckan_desc* desc) {
   if (validate_desc(desc) != CKAN_OK) return 0;
+  if (valu_route(desc)) return (size_t)desc->batch * desc->in_dim;
   const Plan p = plan_of(desc);
   return (size_t)p.B * p.I_sg;
 }
 
 size_t ckan_fwd_workspace_bytes(const ckan_desc* desc) {
-  if (validate_desc(desc) != CKAN_OK) return 0;
+  if (validate_desc(desc) != CKAN_OK || valu_route(desc)) return 0;
   const Plan p = plan_of(desc);
   if (p.B == 0) return 0;
   return fwd_ws_bytes(p, choose_fwd(p));
 }
 
 size_t ckan_bwd_workspace_bytes(const ckan_desc* desc, int need_dx, int need_dcoeffs) {
-  if (validate_desc(desc) != CKAN_OK) return 0;
+  if (validate_desc(desc) != CKAN_OK || valu_route(desc)) return 0;
   const Plan p = plan_of(desc);
   return bwd_layout(p, need_dx != 0, need_dcoeffs != 0).total;
 }
@@ -265,8 +297,14 @@ int ckan_pack_coeffs(const ckan_desc* desc, const void* coeffs, void* packed, vo
   if (rc) return rc;
   if (!coeffs || !packed) return fail(CKAN_ERR_INVALID_ARG, "coeffs/packed is NULL");
   if (!aligned16(packed)) return fail(CKAN_ERR_INVALID_ARG, "packed buffer must be 16-byte aligned");
-  const Plan p = plan_of(desc);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (valu_route(desc)) {
+    ProfScope ps("pack", s);
+    launch_to_f32(coeffs, desc->coeff_dtype == CKAN_DTYPE_BF16, static_cast<float*>(packed),
+                  valu_coeffs(desc), s);
+    return check_launch("pack_coeffs");
+  }
+  const Plan p = plan_of(desc);
   ProfScope ps("pack", s);
   launch_pack(coeffs, desc->coeff_dtype == CKAN_DTYPE_BF16, packed, p, s);
   return check_launch("pack_coeffs");
@@ -276,12 +314,19 @@ int ckan_forward(const ckan_desc* desc, const float* x, const void* packed, floa
                  float* t_cache, void* ws, size_t ws_bytes, void* stream) {
   int rc = validate_desc(desc);
   if (rc) return rc;
-  const Plan p = plan_of(desc);
-  if (p.B == 0) return CKAN_OK;
+  if (desc->batch == 0) return CKAN_OK;
   if (!x || !packed || !y || !t_cache)
     return fail(CKAN_ERR_INVALID_ARG, "x/packed/y/t_cache is NULL");
   if (!aligned16(packed) || !aligned16(t_cache))
     return fail(CKAN_ERR_INVALID_ARG, "packed and t_cache must be 16-byte aligned");
+  if (valu_route(desc)) {
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    ProfScope ps("fwd_valu", s);
+    launch_forward_valu<float>(x, static_cast<const float*>(packed), y, t_cache, desc->batch,
+                               desc->in_dim, desc->in_dim, desc->out_dim, desc->degree, s);
+    return check_launch("forward (vector ALU)");
+  }
+  const Plan p = plan_of(desc);
   const FwdChoice c = choose_fwd(p);
   const size_t need = fwd_ws_bytes(p, c);
   if (ws_bytes < need)
@@ -304,9 +349,8 @@ int ckan_forward_noalloc(const ckan_desc* desc, const float* x, const void* pack
                          float* t_cache, void* stream) {
   int rc = validate_desc(desc);
   if (rc) return rc;
-  const Plan p = plan_of(desc);
-  if (p.B == 0) return CKAN_OK;
-  const size_t need = fwd_ws_bytes(p, choose_fwd(p));
+  if (desc->batch == 0) return CKAN_OK;
+  const size_t need = ckan_fwd_workspace_bytes(desc);
   if (need > CKAN_NOALLOC_SCRATCH_BYTES)
     return fail(CKAN_ERR_WORKSPACE,
                 "forward_noalloc: this shape needs %zu bytes of scratch, above the fixed %zu",
@@ -332,6 +376,10 @@ int ckan_pack_forward(const ckan_desc* desc, const ckan_basis_spec* spec, const 
   if (spec && (rc = family_xform(spec, desc->degree, &xf))) return rc;
   if (!coeffs || !packed) return fail(CKAN_ERR_INVALID_ARG, "coeffs/packed is NULL");
   if (!aligned16(packed)) return fail(CKAN_ERR_INVALID_ARG, "packed buffer must be 16-byte aligned");
+  if (valu_route(desc)) {  // spec is NULL here: family_xform serves degree <= 16 only
+    if ((rc = ckan_pack_coeffs(desc, coeffs, packed, stream))) return rc;
+    return ckan_forward(desc, x, packed, y, t_cache, ws, ws_bytes, stream);
+  }
   const Plan p = plan_of(desc);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const bool cbf = desc->coeff_dtype == CKAN_DTYPE_BF16;
@@ -408,7 +456,8 @@ int ckan_forward_f64(const ckan_desc* desc, const double* x, const double* coeff
   if (!x || !coeffs || !y || !t_cache) return fail(CKAN_ERR_INVALID_ARG, "x/coeffs/y/t_cache is NULL");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   ProfScope ps("fwd_f64", s);
-  launch_forward_f64(x, coeffs, y, t_cache, desc->batch, desc->in_dim, desc->out_dim, desc->degree, s);
+  launch_forward_valu<double>(x, coeffs, y, t_cache, desc->batch, desc->in_dim, desc->in_dim,
+                              desc->out_dim, desc->degree, s);
   return check_launch("forward_f64");
 }
 
@@ -432,8 +481,9 @@ int ckan_backward_f64(const ckan_desc* desc, const double* t_cache, const double
   if (!t_cache || !dy || (dx && !coeffs))
     return fail(CKAN_ERR_INVALID_ARG, "t_cache/dy/coeffs is NULL");
   ProfScope ps("bwd_f64", s);
-  launch_backward_f64(t_cache, coeffs, dy, dx, dcoeffs, accumulate != 0, desc->batch, desc->in_dim,
-                      desc->out_dim, desc->degree, s);
+  const DcOut om{accumulate ? kDcAccumulate : kDcStore};
+  launch_backward_valu<double>(t_cache, coeffs, dy, dx, dcoeffs, om, desc->batch, desc->in_dim,
+                               desc->in_dim, desc->out_dim, desc->degree, s);
   return check_launch("backward_f64");
 }
 

@@ -99,12 +99,20 @@ void launch_coeff_xform(const float* in, float* out, int64_t rows, int din, int 
 void launch_jacobian(const float* x, const float* c1t, float* jac, int64_t B, int I, int O,
                      int dout, hipStream_t s);
 
-// ---- fp64 path (ckan_f64.hip): x, C, y, t, dy, dx, dC all fp64 -------------
-void launch_forward_f64(const double* x, const double* C, double* y, double* t, int64_t B, int I,
-                        int O, int deg, hipStream_t s);
-void launch_backward_f64(const double* t, const double* C, const double* dy, double* dx,
-                         double* dC, bool accumulate, int64_t B, int I, int O, int deg,
-                         hipStream_t s);
+// ---- vector-ALU path (ckan_valu.hip): any degree, T = float or double ------
+// Serves fp64 layers and fp32 layers above kMfmaMaxDegree, with C in its own
+// [I, O, D] layout; t has row pitch tpitch (>= I, zero-filled past I).
+constexpr int kMfmaMaxDegree = 16;   // the packed MFMA kernels' limit
+constexpr int kValuMaxDegree = 256;  // the vector-ALU path's limit
+template <typename T>
+void launch_forward_valu(const T* x, const T* C, T* y, T* t, int64_t B, int I, int tpitch, int O,
+                         int deg, hipStream_t s);
+// dC written by mode om.mode (for T = double: store or accumulate only).
+template <typename T>
+void launch_backward_valu(const T* t, const T* C, const T* dy, T* dx, T* dC, DcOut om, int64_t B,
+                          int I, int tpitch, int O, int deg, hipStream_t s);
+// dst[q] = float(src[q]) for q < n, src fp32 or bf16.
+void launch_to_f32(const void* src, bool src_bf16, float* dst, int64_t n, hipStream_t s);
 
 // ---- launchers -------------------------------------------------------------
 void launch_tanh(const float* x, float* t, const Plan& p, hipStream_t s);

@@ -43,7 +43,7 @@ def _desc(B=8, I=4, O=3, deg=8, compute=0, cdt=0):
     ("in_dim", 0, _lib.CKAN_ERR_INVALID_ARG),
     ("out_dim", 0, _lib.CKAN_ERR_INVALID_ARG),
     ("degree", -1, _lib.CKAN_ERR_INVALID_ARG),
-    ("degree", 17, _lib.CKAN_ERR_UNSUPPORTED),
+    ("degree", 257, _lib.CKAN_ERR_UNSUPPORTED),
     ("compute", 7, _lib.CKAN_ERR_INVALID_ARG),
     ("coeff_dtype", 5, _lib.CKAN_ERR_INVALID_ARG),
     ("input_map", 1, _lib.CKAN_ERR_INVALID_ARG),   # affine with in_scale 0
@@ -57,6 +57,24 @@ def test_descriptor_validation(field, value, code):
     assert lib.ckan_forward(ctypes.byref(d), 1, 1, 1, 1, None, 0, None) == code
     assert lib.ckan_last_error()
     assert lib.ckan_packed_bytes(ctypes.byref(d)) == 0
+
+
+def test_high_degree_sizes_and_limits():
+    """Degrees 17..256 run on the vector-ALU kernels: the packed buffer is C
+    as fp32 [I, O, D], the tanh cache has row pitch I, no workspace."""
+    lib = _lib.load()
+    for deg, B, I, O in [(17, 8, 4, 3), (40, 33, 70, 5), (256, 1, 2, 2)]:
+        for compute, cdt in [(0, 0), (1, 1)]:
+            d = _lib.make_desc(B, I, O, deg, compute, cdt)
+            assert lib.ckan_packed_bytes(d) == -(-I * O * (deg + 1) * 4 // 256) * 256
+            assert lib.ckan_tcache_elems(d) == B * I
+            assert lib.ckan_fwd_workspace_bytes(d) == 0
+            assert lib.ckan_bwd_workspace_bytes(d, 1, 1) == 0
+    # the affine input map (finite-domain Hermite) is served up to degree 16
+    assert lib.ckan_packed_bytes(_lib.make_desc(8, 4, 3, 16, 0, 0, (0.5, 0.1))) > 0
+    d = _lib.make_desc(8, 4, 3, 17, 0, 0, (0.5, 0.1))
+    assert lib.ckan_forward(d, 16, 16, 16, 16, None, 0, None) == _lib.CKAN_ERR_UNSUPPORTED
+    assert b"affine" in lib.ckan_last_error()
 
 
 def test_null_pointers_rejected_before_launch():
