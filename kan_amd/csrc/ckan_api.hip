@@ -188,7 +188,7 @@ int ckan::backward_impl(const ckan_desc* desc, const float* t_cache, const void*
       return fail(CKAN_ERR_INVALID_ARG, "t_cache/dy/packed is NULL");
     ProfScope ps("bwd_valu", s);
     launch_backward_valu<float>(t_cache, static_cast<const float*>(packed), dy, dx, dcoeffs, om,
-                                desc->batch, desc->in_dim, desc->in_dim, desc->out_dim,
+                                desc->batch, desc->in_dim, desc->out_dim,
                                 desc->degree, s);
     return check_launch("backward (vector ALU)");
   }
@@ -323,7 +323,7 @@ int ckan_forward(const ckan_desc* desc, const float* x, const void* packed, floa
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     ProfScope ps("fwd_valu", s);
     launch_forward_valu<float>(x, static_cast<const float*>(packed), y, t_cache, desc->batch,
-                               desc->in_dim, desc->in_dim, desc->out_dim, desc->degree, s);
+                               desc->in_dim, desc->out_dim, desc->degree, s);
     return check_launch("forward (vector ALU)");
   }
   const Plan p = plan_of(desc);
@@ -456,7 +456,7 @@ int ckan_forward_f64(const ckan_desc* desc, const double* x, const double* coeff
   if (!x || !coeffs || !y || !t_cache) return fail(CKAN_ERR_INVALID_ARG, "x/coeffs/y/t_cache is NULL");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   ProfScope ps("fwd_f64", s);
-  launch_forward_valu<double>(x, coeffs, y, t_cache, desc->batch, desc->in_dim, desc->in_dim,
+  launch_forward_valu<double>(x, coeffs, y, t_cache, desc->batch, desc->in_dim,
                               desc->out_dim, desc->degree, s);
   return check_launch("forward_f64");
 }
@@ -483,7 +483,7 @@ int ckan_backward_f64(const ckan_desc* desc, const double* t_cache, const double
   ProfScope ps("bwd_f64", s);
   const DcOut om{accumulate ? kDcAccumulate : kDcStore};
   launch_backward_valu<double>(t_cache, coeffs, dy, dx, dcoeffs, om, desc->batch, desc->in_dim,
-                               desc->in_dim, desc->out_dim, desc->degree, s);
+                               desc->out_dim, desc->degree, s);
   return check_launch("backward_f64");
 }
 

@@ -101,16 +101,16 @@ void launch_jacobian(const float* x, const float* c1t, float* jac, int64_t B, in
 
 // ---- vector-ALU path (ckan_valu.hip): any degree, T = float or double ------
 // Serves fp64 layers and fp32 layers above kMfmaMaxDegree, with C in its own
-// [I, O, D] layout; t has row pitch tpitch (>= I, zero-filled past I).
+// [I, O, D] layout; t = tanh(x) is [B, I].
 constexpr int kMfmaMaxDegree = 16;   // the packed MFMA kernels' limit
 constexpr int kValuMaxDegree = 256;  // the vector-ALU path's limit
 template <typename T>
-void launch_forward_valu(const T* x, const T* C, T* y, T* t, int64_t B, int I, int tpitch, int O,
+void launch_forward_valu(const T* x, const T* C, T* y, T* t, int64_t B, int I, int O,
                          int deg, hipStream_t s);
 // dC written by mode om.mode (for T = double: store or accumulate only).
 template <typename T>
 void launch_backward_valu(const T* t, const T* C, const T* dy, T* dx, T* dC, DcOut om, int64_t B,
-                          int I, int tpitch, int O, int deg, hipStream_t s);
+                          int I, int O, int deg, hipStream_t s);
 // dst[q] = float(src[q]) for q < n, src fp32 or bf16.
 void launch_to_f32(const void* src, bool src_bf16, float* dst, int64_t n, hipStream_t s);
 

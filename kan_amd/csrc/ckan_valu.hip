@@ -8,58 +8,60 @@
 // layers above the MFMA kernels' degree 16 (the reference layer takes any
 // degree, kan/layers/chebykan.py:21-51).  Register-tiled kernels with LDS
 // staging read C in its own [I, O, D] layout.  The degree axis is taken in
-// chunks of at most DM = 17 degrees (one launch each): a chunk starting at d0
+// chunks of at most DM degrees (one launch each; DM = 3, 5, 9 or 17, the
+// smallest that holds D, and 17 above): a chunk starting at d0
 // first advances the recurrence to T_{d0-1}, T_{d0} (or U_{d0-2}, U_{d0-1}),
-// so register arrays stay bounded for any degree.  t has row pitch `tp`.
+// so register arrays stay bounded for any degree.  t = tanh(x) is [B, I].
 #include "ckan_kernels.hpp"
 
 #include <math.h>
 
 namespace ckan {
 
-constexpr int kValuDM = 17;  // degrees per chunk
+constexpr int kValuDM = 17;  // degrees per chunk above degree 16
 
 template <typename T> __device__ __forceinline__ T vtanh(T x);
 template <> __device__ __forceinline__ float vtanh<float>(float x) { return tanhf(x); }
 template <> __device__ __forceinline__ double vtanh<double>(double x) { return tanh(x); }
 
-// t[b, i] = tanh(x[b, i]) for i < I, 0 for I <= i < tp (row pitch tp).
 template <typename T>
 __global__ void __launch_bounds__(256)
-k_tanh_v(const T* __restrict__ x, T* __restrict__ t, int64_t B, int I, int tp) {
-  const int64_t n = B * (int64_t)tp;
+k_tanh_v(const T* __restrict__ x, T* __restrict__ t, int64_t n) {
   for (int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; q < n;
-       q += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t b = q / tp;
-    const int i = (int)(q - b * tp);
-    t[q] = i < I ? vtanh<T>(x[b * I + i]) : T(0);
-  }
+       q += (int64_t)gridDim.x * blockDim.x)
+    t[q] = vtanh<T>(x[q]);
 }
 
-// T_{d0-1} and T_{d0} of t (T_{-1} taken as T_1, which the recurrence's first
-// step T_1 = t ignores; see the step below).
+// T_{d0-1} and T_{d0} of t.  T_{-1} = t extends the recurrence
+// T_{d+1} = 2t T_d - T_{d-1} down to d = 0 (its first step gives
+// 2t - t = t = T_1 exactly), so every step below is the same FMA.
 template <typename T>
 __device__ __forceinline__ void cheb_seek(T t, int d0, T& tp, T& tc) {
-  tp = T(0);
+  tp = t;     // T_{-1}
   tc = T(1);  // T_0
   const T t2 = t + t;
   for (int d = 0; d < d0; ++d) {
-    const T nx = d == 0 ? t : fma(t2, tc, -tp);
+    const T nx = fma(t2, tc, -tp);
     tp = tc;
     tc = nx;
   }
 }
+
+// SEEK = false instantiations serve the first chunk (d0 = 0, stored, not
+// accumulated) with no seek loops in the code, as register-lean as a
+// single-chunk kernel.
 
 // Forward, degrees [d0, d0 + dn): block tile 64 rows x 64 outputs, 256
 // threads, thread (tr, to) owns rows tr + 16 r and outputs to + 16 c
 // (r, c < 4).  Inputs are taken KI at a time: t [64][KI] and the chunk of C
 // as [KI][DM][64 outputs] in LDS.  accumulate: add to y (later chunks).
 constexpr int kValuKI = 4;
-template <typename T>
+template <typename T, int DM, bool SEEK>
 __global__ void __launch_bounds__(256)
 k_fwd_v(const T* __restrict__ t, const T* __restrict__ C, T* __restrict__ y, int64_t B, int I,
-        int tpitch, int O, int D, int d0, int dn, int accumulate) {
-  constexpr int KI = kValuKI, DM = kValuDM;
+        int O, int D, int d0_arg, int dn, int accumulate) {
+  constexpr int KI = kValuKI;
+  const int d0 = SEEK ? d0_arg : 0;
   __shared__ T ts[64][KI + 1];
   __shared__ T cs[KI][DM][64];
   const int tid = threadIdx.x, tr = tid >> 4, to = tid & 15;
@@ -75,7 +77,7 @@ k_fwd_v(const T* __restrict__ t, const T* __restrict__ C, T* __restrict__ y, int
     for (int k = tid; k < 64 * KI; k += 256) {
       const int r = k / KI, ii = k % KI;
       const int64_t b = b0 + r;
-      ts[r][ii] = (b < B && i0 + ii < I) ? t[b * tpitch + i0 + ii] : T(0);
+      ts[r][ii] = (b < B && i0 + ii < I) ? t[b * I + i0 + ii] : T(0);
     }
     for (int k = tid; k < KI * 64 * dn; k += 256) {
       const int ii = k / (64 * dn), rem = k % (64 * dn), ol = rem / dn, d = rem % dn;
@@ -92,19 +94,21 @@ k_fwd_v(const T* __restrict__ t, const T* __restrict__ C, T* __restrict__ y, int
         tw[r] = tv + tv;
         cheb_seek<T>(tv, d0, tp[r], tc[r]);
       }
-      for (int d = 0; d < dn; ++d) {
-        T cv[4];
+      for (int d = 0; d < dn; ++d) {  // rolled: measured faster than unrolled here
+        {
+          T cv[4];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) cv[c] = cs[ii][d][to + 16 * c];
+          for (int c = 0; c < 4; ++c) cv[c] = cs[ii][d][to + 16 * c];
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
+          for (int r = 0; r < 4; ++r)
 #pragma unroll
-          for (int c = 0; c < 4; ++c) acc[r][c] = fma(tc[r], cv[c], acc[r][c]);
+            for (int c = 0; c < 4; ++c) acc[r][c] = fma(tc[r], cv[c], acc[r][c]);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {  // T_{d+1} = 2t T_d - T_{d-1} (T_1 = t)
-          const T nx = d0 + d == 0 ? T(0.5) * tw[r] : fma(tw[r], tc[r], -tp[r]);
-          tp[r] = tc[r];
-          tc[r] = nx;
+          for (int r = 0; r < 4; ++r) {  // T_{d+1} = 2t T_d - T_{d-1}
+            const T nx = fma(tw[r], tc[r], -tp[r]);
+            tp[r] = tc[r];
+            tc[r] = nx;
+          }
         }
       }
     }
@@ -116,7 +120,7 @@ k_fwd_v(const T* __restrict__ t, const T* __restrict__ C, T* __restrict__ y, int
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const int o = o0 + to + 16 * c;
-      if (o < O) y[b * O + o] = accumulate ? y[b * O + o] + acc[r][c] : acc[r][c];
+      if (o < O) y[b * O + o] = SEEK && accumulate ? y[b * O + o] + acc[r][c] : acc[r][c];
     }
   }
 }
@@ -127,12 +131,13 @@ k_fwd_v(const T* __restrict__ t, const T* __restrict__ C, T* __restrict__ y, int
 // chunk of C as [8 inputs][16 outputs][DM] in LDS, the per-input stride padded
 // to an odd number of elements so the 8 inputs of a wave read distinct banks.
 // accumulate: add to dx (later chunks).
-template <typename T>
+template <typename T, int DM, bool SEEK>
 __global__ void __launch_bounds__(256)
 k_dx_v(const T* __restrict__ t, const T* __restrict__ C, const T* __restrict__ dy,
-       T* __restrict__ dx, int64_t B, int I, int tpitch, int O, int D, int d0, int dn,
+       T* __restrict__ dx, int64_t B, int I, int O, int D, int d0_arg, int dn,
        int accumulate) {
-  constexpr int DM = kValuDM, OC = 16, CST = OC * (DM + 1) + 1;
+  constexpr int OC = 16, CST = OC * (DM + 1) + 1;
+  const int d0 = SEEK ? d0_arg : 0;
   __shared__ T ys[128][OC + 1];
   __shared__ T cs[8 * CST];
   const int tid = threadIdx.x, rr = tid >> 3, ii = tid & 7;
@@ -177,26 +182,32 @@ k_dx_v(const T* __restrict__ t, const T* __restrict__ C, const T* __restrict__ d
   for (int h = 0; h < 4; ++h) {
     const int64_t b = b0 + rr + 32 * h;
     if (b >= B) continue;
-    const T tv = t[b * tpitch + i];
+    const T tv = t[b * I + i];
     const T t2 = tv + tv;
-    T up = T(0), u = T(1), s = T(0);  // U_{-1}, U_0, advanced to U_{d0-2}, U_{d0-1}
+    // (up, u) = (U_{deg-2}, U_{deg-1}) at degree deg.  The first chunk starts
+    // at degree 1 (T_0 has no derivative, so G[., ., 0] is never formed) from
+    // (U_{-1}, U_0) = (0, 1); a later chunk advances the recurrence
+    // U_{n+1} = 2t U_n - U_{n-1} from (U_{-1}, U_0) to degree d0.
+    constexpr int dfirst = SEEK ? 0 : 1;
+    T up = T(0), u = T(1), s = T(0);
     for (int d = 1; d < d0; ++d) {
       const T un = fma(t2, u, -up);
       up = u;
       u = un;
     }
+    T deg = (T)(d0 + dfirst);  // counted in T (exact)
 #pragma unroll
-    for (int d = 0; d < DM; ++d) {
-      const int dd = d0 + d;  // the degree; its derivative is dd U_{dd-1}
-      if (d < dn && dd >= 1) {
-        s = fma(g[h][d] * (T)dd, u, s);
+    for (int d = dfirst; d < DM; ++d) {
+      if (d < dn) {  // dT_deg/dt = deg U_{deg-1}
+        s = fma(g[h][d] * deg, u, s);
         const T un = fma(t2, u, -up);
         up = u;
         u = un;
+        deg += T(1);
       }
     }
     const T v = s * (T(1) - tv * tv);
-    dx[b * I + i] = accumulate ? dx[b * I + i] + v : v;
+    dx[b * I + i] = SEEK && accumulate ? dx[b * I + i] + v : v;
   }
 }
 
@@ -214,11 +225,11 @@ template <> struct DcWrite<double> {  // store or accumulate
   }
 };
 
-template <typename T>
+template <typename T, int DM, bool SEEK>
 __global__ void __launch_bounds__(256)
 k_dc_v(const T* __restrict__ t, const T* __restrict__ dy, T* __restrict__ dC, int64_t B, int I,
-       int tpitch, int O, int D, int d0, int dn, DcOut om) {
-  constexpr int DM = kValuDM;
+       int O, int D, int d0_arg, int dn, DcOut om) {
+  const int d0 = SEEK ? d0_arg : 0;
   __shared__ T ts[32][9];
   __shared__ T ys[32][129];
   const int tid = threadIdx.x, il = tid >> 5, ol = tid & 31;
@@ -233,7 +244,7 @@ k_dc_v(const T* __restrict__ t, const T* __restrict__ dy, T* __restrict__ dC, in
     {
       const int r = tid >> 3, k = tid & 7;
       const int64_t b = bc + r;
-      ts[r][k] = (b < B && i0 + k < I) ? t[b * tpitch + i0 + k] : T(0);
+      ts[r][k] = (b < B && i0 + k < I) ? t[b * I + i0 + k] : T(0);
     }
     for (int k = tid; k < 32 * 128; k += 256) {
       const int r = k >> 7, o = k & 127;
@@ -253,7 +264,7 @@ k_dc_v(const T* __restrict__ t, const T* __restrict__ dy, T* __restrict__ dC, in
         if (d < dn) {
 #pragma unroll
           for (int c = 0; c < 4; ++c) acc[c][d] = fma(tc, yv[c], acc[c][d]);
-          const T nx = d0 + d == 0 ? tv : fma(t2, tc, -tp);
+          const T nx = fma(t2, tc, -tp);
           tp = tc;
           tc = nx;
         }
@@ -293,45 +304,83 @@ void launch_to_f32(const void* src, bool src_bf16, float* dst, int64_t n, hipStr
     hipLaunchKernelGGL(k_to_f32, dim3(vgrid(n)), dim3(256), 0, s, src, src_bf16 ? 1 : 0, dst, n);
 }
 
+// Chunk size: the smallest instantiated DM that holds D, 17 above.
+static int valu_dm(int D) { return D <= 3 ? 3 : D <= 5 ? 5 : D <= 9 ? 9 : kValuDM; }
+
+template <typename T, int DM>
+static void fwd_chunks(const T* t, const T* C, T* y, int64_t B, int I, int O, int D,
+                       hipStream_t s) {
+  const dim3 g((unsigned)((B + 63) / 64), (unsigned)((O + 63) / 64));
+  for (int d0 = 0; d0 < D; d0 += DM) {
+    const int dn = D - d0 < DM ? D - d0 : DM;
+    if (d0 == 0)
+      hipLaunchKernelGGL((k_fwd_v<T, DM, false>), g, dim3(256), 0, s, t, C, y, B, I, O, D,
+                         d0, dn, 0);
+    else
+      hipLaunchKernelGGL((k_fwd_v<T, DM, true>), g, dim3(256), 0, s, t, C, y, B, I, O, D,
+                         d0, dn, 1);
+  }
+}
+
+template <typename T, int DM>
+static void bwd_chunks(const T* t, const T* C, const T* dy, T* dx, T* dC, DcOut om, int64_t B,
+                       int I, int O, int D, hipStream_t s) {
+  for (int d0 = 0; d0 < D; d0 += DM) {
+    const int dn = D - d0 < DM ? D - d0 : DM;
+    if (dx && B > 0) {
+      const dim3 g((unsigned)((B + 127) / 128), (unsigned)((I + 7) / 8));
+      if (d0 == 0)
+        hipLaunchKernelGGL((k_dx_v<T, DM, false>), g, dim3(256), 0, s, t, C, dy, dx, B, I,
+                           O, D, d0, dn, 0);
+      else
+        hipLaunchKernelGGL((k_dx_v<T, DM, true>), g, dim3(256), 0, s, t, C, dy, dx, B, I,
+                           O, D, d0, dn, 1);
+    }
+    if (dC) {
+      const dim3 g((unsigned)((I + 7) / 8), (unsigned)((O + 127) / 128));
+      if (d0 == 0)
+        hipLaunchKernelGGL((k_dc_v<T, DM, false>), g, dim3(256), 0, s, t, dy, dC, B, I, O,
+                           D, d0, dn, om);
+      else
+        hipLaunchKernelGGL((k_dc_v<T, DM, true>), g, dim3(256), 0, s, t, dy, dC, B, I, O,
+                           D, d0, dn, om);
+    }
+  }
+}
+
 template <typename T>
-void launch_forward_valu(const T* x, const T* C, T* y, T* t, int64_t B, int I, int tpitch, int O,
+void launch_forward_valu(const T* x, const T* C, T* y, T* t, int64_t B, int I, int O,
                          int deg, hipStream_t s) {
   if (B == 0) return;
-  hipLaunchKernelGGL(k_tanh_v<T>, dim3(vgrid(B * tpitch)), dim3(256), 0, s, x, t, B, I, tpitch);
+  hipLaunchKernelGGL(k_tanh_v<T>, dim3(vgrid(B * I)), dim3(256), 0, s, x, t, B * I);
   const int D = deg + 1;
-  const dim3 g((unsigned)((B + 63) / 64), (unsigned)((O + 63) / 64));
-  for (int d0 = 0; d0 < D; d0 += kValuDM) {
-    const int dn = D - d0 < kValuDM ? D - d0 : kValuDM;
-    hipLaunchKernelGGL(k_fwd_v<T>, g, dim3(256), 0, s, t, C, y, B, I, tpitch, O, D, d0, dn,
-                       d0 > 0 ? 1 : 0);
+  switch (valu_dm(D)) {
+    case 3: fwd_chunks<T, 3>(t, C, y, B, I, O, D, s); break;
+    case 5: fwd_chunks<T, 5>(t, C, y, B, I, O, D, s); break;
+    case 9: fwd_chunks<T, 9>(t, C, y, B, I, O, D, s); break;
+    default: fwd_chunks<T, kValuDM>(t, C, y, B, I, O, D, s); break;
   }
 }
 
 template <typename T>
 void launch_backward_valu(const T* t, const T* C, const T* dy, T* dx, T* dC, DcOut om, int64_t B,
-                          int I, int tpitch, int O, int deg, hipStream_t s) {
+                          int I, int O, int deg, hipStream_t s) {
   const int D = deg + 1;
-  for (int d0 = 0; d0 < D; d0 += kValuDM) {
-    const int dn = D - d0 < kValuDM ? D - d0 : kValuDM;
-    if (dx && B > 0) {
-      const dim3 g((unsigned)((B + 127) / 128), (unsigned)((I + 7) / 8));
-      hipLaunchKernelGGL(k_dx_v<T>, g, dim3(256), 0, s, t, C, dy, dx, B, I, tpitch, O, D, d0, dn,
-                         d0 > 0 ? 1 : 0);
-    }
-    if (dC) {
-      const dim3 g((unsigned)((I + 7) / 8), (unsigned)((O + 127) / 128));
-      hipLaunchKernelGGL(k_dc_v<T>, g, dim3(256), 0, s, t, dy, dC, B, I, tpitch, O, D, d0, dn, om);
-    }
+  switch (valu_dm(D)) {
+    case 3: bwd_chunks<T, 3>(t, C, dy, dx, dC, om, B, I, O, D, s); break;
+    case 5: bwd_chunks<T, 5>(t, C, dy, dx, dC, om, B, I, O, D, s); break;
+    case 9: bwd_chunks<T, 9>(t, C, dy, dx, dC, om, B, I, O, D, s); break;
+    default: bwd_chunks<T, kValuDM>(t, C, dy, dx, dC, om, B, I, O, D, s); break;
   }
 }
 
 template void launch_forward_valu<float>(const float*, const float*, float*, float*, int64_t, int,
-                                         int, int, int, hipStream_t);
+                                         int, int, hipStream_t);
 template void launch_forward_valu<double>(const double*, const double*, double*, double*, int64_t,
-                                          int, int, int, int, hipStream_t);
+                                          int, int, int, hipStream_t);
 template void launch_backward_valu<float>(const float*, const float*, const float*, float*, float*,
-                                          DcOut, int64_t, int, int, int, int, hipStream_t);
+                                          DcOut, int64_t, int, int, int, hipStream_t);
 template void launch_backward_valu<double>(const double*, const double*, const double*, double*,
-                                           double*, DcOut, int64_t, int, int, int, int, hipStream_t);
+                                           double*, DcOut, int64_t, int, int, int, hipStream_t);
 
 }  // namespace ckan
