@@ -202,7 +202,7 @@ k_pack(const CT* __restrict__ C, typename Elem<BF>::type* __restrict__ Cf,
         const int i = r * G::SGI + g * 2 * G::IPG + s * (G::IPG / 2) + u;
         v[j] = (d <= p.deg) ? tile[(i - i0) * RP + ol * D + d] : 0.0f;
       }
-      store_frag<BF>(Cf + ((size_t)ob * p.KB + kb) * kFragElems, lane, v);
+      store_frag<BF>(Cf + cf_elem<BF>(p.KB, ob, kb, lane) - (size_t)lane * 8, lane, v);
     }
   }
 

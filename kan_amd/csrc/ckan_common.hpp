@@ -221,6 +221,24 @@ template <> __device__ __forceinline__ Frag<false> make_frag<false>(const float*
   return f;
 }
 
+// The bf16 forward coefficients (Cf) are stored by 8-output streams: for a
+// 32-output fragment column nb, stream (nb, sub) holds columns 8 sub .. 8 sub
+// + 7 of every k-block kb in order, each k-block as its first half (k 0-7)
+// then its second (k 8-15), 16 bytes per column.  Lane L of fragment (nb, kb)
+// (column L % 32, half L / 32) finds its 8 values at this element offset.  A
+// reader of a few columns (the small-batch forward) then streams contiguous
+// bytes; the GEMMs copy each lane's 16 bytes from here instead of from
+// fragment-contiguous storage.  fp32 fragments stay fragment-contiguous.
+__host__ __device__ inline size_t cf_bf16_elem(int KB, int nb, int kb, int L) {
+  const int ol = L & 31, g = L >> 5;
+  return ((((size_t)nb * 4 + (ol >> 3)) * KB + kb) * 2 + g) * 64 + (size_t)(ol & 7) * 8;
+}
+// Element offset of lane L's 8 values of forward fragment (nb, kb).
+template <bool BF> __host__ __device__ inline size_t cf_elem(int KB, int nb, int kb, int L) {
+  if constexpr (BF) return cf_bf16_elem(KB, nb, kb, L);
+  else return ((size_t)nb * KB + kb) * kFragElems + (size_t)L * 8;
+}
+
 // Load this lane's 8 values of a fragment stored at `base` (fragment start).
 template <bool BF> __device__ __forceinline__ Frag<BF> load_frag(const typename Elem<BF>::type* base, int lane);
 template <> __device__ __forceinline__ Frag<true> load_frag<true>(const uint16_t* base, int lane) {

@@ -85,9 +85,13 @@ k_fwd(const float* __restrict__ tc, const typename Elem<BF>::type* __restrict__ 
       const int c = tid + q * 256;
       const int nbl = c / CPN, off = c - nbl * CPN;
       const int nb = nb0 + nbl;
+      // chunk off of the stage: k-block off / CPF, lane-chunk off % CPF (a lane
+      // holds 8 values: one chunk for bf16, two for fp32)
+      constexpr int CPF = kFragElems / CE;
+      const int kbl = off / CPF, lc = off - kbl * CPF;
       if (nb < p.NBf)
         pre[q] = *reinterpret_cast<const u32x4_t*>(
-            Cf + ((size_t)nb * p.KB + (size_t)sg * G::SGK) * kFragElems + (size_t)off * CE);
+            Cf + cf_elem<BF>(p.KB, nb, sg * G::SGK + kbl, lc * CE / 8) + (size_t)(lc * CE % 8));
       else
         pre[q] = u32x4_t{0u, 0u, 0u, 0u};
     }
@@ -313,14 +317,18 @@ k_fwd_pipe(const float* __restrict__ tc, const typename Elem<BF>::type* __restri
   constexpr int HB_OPS = 2 * K::B_OPS, HT_OPS = 2 * K::T_OPS, HOPS = 2 * (HB_OPS + HT_OPS);
   constexpr int CPF = kFragElems * (int)sizeof(E) / 16;  // 16-byte chunks per fragment
   const int wqs = __builtin_amdgcn_readfirstlane(wq);
-  const char* bbase = reinterpret_cast<const char*>(Cf) + (size_t)nb0 * p.KB * kFragElems * sizeof(E);
+  const E* cf0 = Cf + cf_elem<BF>(p.KB, nb0, 0, 0);
+  const char* bbase = reinterpret_cast<const char*>(cf0);
   uint32_t boff[HB_OPS];
 #pragma unroll
   for (int q = 0; q < HB_OPS; ++q) {
     const int c = (q * 4 + wq) * 64 + lane;
     const int nbl = c / (G::SGK * CPF), off = c - nbl * (G::SGK * CPF);
     const int nb = min(nb0 + nbl, p.NBf - 1);
-    boff[q] = (uint32_t)((size_t)(nb - nb0) * p.KB * kFragElems * sizeof(E) + (size_t)off * 16);
+    const int kbl = off / CPF, lc = off - kbl * CPF;  // k-block of the stage, lane-chunk
+    constexpr int CE = 16 / (int)sizeof(E);
+    const E* src = Cf + cf_elem<BF>(p.KB, nb, kbl, lc * CE / 8) + (lc * CE % 8);
+    boff[q] = (uint32_t)((size_t)(src - cf0) * sizeof(E));
   }
   const char* tbase = reinterpret_cast<const char*>(tc) + (size_t)m_blk * p.I_sg * 4;
   uint32_t toff[HT_OPS];
@@ -332,7 +340,9 @@ k_fwd_pipe(const float* __restrict__ tc, const typename Elem<BF>::type* __restri
     if (r >= p.B) r = p.B - 1;
     toff[q] = (uint32_t)(((size_t)(r - m_blk) * p.I_sg + (part4 ^ fwd_t_xor<G::SGI / 4>(rl)) * 4) * 4);
   }
-  const size_t b_stride = (size_t)G::SGK * kFragElems * sizeof(E);
+  // one super-group further: SGK k-blocks, in every stream (bf16) or fragment column
+  const size_t b_stride =
+      (cf_elem<BF>(p.KB, 0, G::SGK, 0) - cf_elem<BF>(p.KB, 0, 0, 0)) * sizeof(E);
   const size_t t_stride = (size_t)G::SGI * 4;
   const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
 
@@ -631,7 +641,7 @@ k_fwd_stream(const float* __restrict__ x, float* __restrict__ tc,
 #pragma unroll
   for (int q = 0; q < KPW; ++q) {
     const int sg = min(sg0 + q / G::SGK, nsg - 1);
-    bfr[q] = load_frag<BF>(Cf + ((size_t)nb * p.KB + (size_t)sg * G::SGK + q % G::SGK) * kFragElems, lane);
+    bfr[q] = load_frag<BF>(Cf + cf_elem<BF>(p.KB, nb, sg * G::SGK + q % G::SGK, lane) - (size_t)lane * 8, lane);
   }
 #pragma unroll
   for (int q = 0; q < KPW; ++q)
@@ -707,6 +717,216 @@ k_fwd_reduce(const float* __restrict__ part, int S, const float* __restrict__ bi
     const int64_t r = q / p.O;
     const int o = (int)(q - r * p.O);
     y[q] = split_sum(part + (size_t)r * p.O32 + o, (size_t)p.B32 * p.O32, (unsigned)S, bias_f[o]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Forward, very small batch (B <= 4), one launch: column-owning blocks.
+// Block b owns one 8-output stream of the bf16 coefficients (cf_bf16_elem)
+// and the whole reduction, so no split-K partials and no second launch; with
+// 2048 outputs that is 256 blocks, one per CU.  Its 16 waves split the
+// reduction into batches of 4 U k-blocks, read as U / 2 contiguous 1 KiB
+// loads: lane (c, G) = (lane % 16, lane / 16) of load l gets column c % 8 of
+// half c / 8 of k-block 4 l + G.  Each load feeds two
+// v_mfma_f32_16x16x32_bf16 steps whose k-group G is that k-block: the first
+// half directly (columns 0..7), the second half rotated in from lanes 8..15
+// by a DPP row rotate; columns 8..15 of every step are duplicates whose sums
+// are not stored.  The wave's lanes build each of the batch's R x 4U distinct
+// basis vectors (row, k-group run of 8 values) once, from coalesced loads of
+// x, into a per-wave LDS area, and every MFMA lane reads its vector there
+// (rows past R read row R - 1; their sums are never stored).  Loads go out
+// one batch ahead of the MFMAs.  The 16 waves' tiles are added in wave order
+// through LDS, with the bias.
+// ---------------------------------------------------------------------------
+template <int P, int R>
+struct FwdCols {
+  typedef FwdGroup<P> G;
+  static constexpr int WAVES = 16;
+  static constexpr int NU = P <= 8 ? 8 / P : 1;        // inputs per basis vector
+  static constexpr int U = 16;                         // MFMA steps per batch
+  static constexpr int NL = U / 2;                     // 1 KiB loads per batch
+  static constexpr int KBB = 4 * NL;                   // k-blocks per batch (4 per load)
+  static constexpr int SGB = KBB / G::SGK;             // super-groups per batch
+  static constexpr int VPR = 4 * U;                    // vectors per row per batch
+  static constexpr int NV = R * VPR;                   // vectors per batch
+  static constexpr int PASSES = (NV + 63) / 64;
+};
+
+__device__ __forceinline__ void mma16(f32x4_t& acc, const bf16x8_t& a, const bf16x8_t& b) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
+}
+
+// v rotated by 8 lanes within each row of 16 (lane c takes lane (c + 8) % 16).
+__device__ __forceinline__ bf16x8_t row_rotate8(const bf16x8_t& v) {
+  const u32x4_t u = __builtin_bit_cast(u32x4_t, v);
+  u32x4_t r;
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    r[e] = (unsigned)__builtin_amdgcn_update_dpp(0, (int)u[e], 0x128, 0xF, 0xF, false);  // row_ror:8
+  return __builtin_bit_cast(bf16x8_t, r);
+}
+
+template <int P, int R>
+__global__ void __launch_bounds__(1024)
+k_fwd_cols(const float* __restrict__ x, float* __restrict__ tc, const uint16_t* __restrict__ Cf,
+           const float* __restrict__ bias_f, float* __restrict__ y, Plan p) {
+  typedef FwdCols<P, R> K;
+  typedef FwdGroup<P> G;
+  constexpr int U = K::U, NL = K::NL, NU = K::NU, SGK = G::SGK, PASSES = K::PASSES;
+  static_assert(K::KBB % SGK == 0, "a batch holds whole super-groups");
+  __shared__ bf16x8_t vec[K::WAVES][U][4][R];
+  __shared__ float red[K::WAVES][16][8];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c = lane & 15, G4 = lane >> 4;
+  // Blocks go to the 8 XCDs round-robin (block b on XCD b % 8).  With the
+  // number of 32-output blocks a multiple of 8, the 4 streams of one 32-output
+  // block get the same XCD and neighbouring dispatch slots; otherwise blocks
+  // take streams in order.
+  int nb, sub;
+  if ((p.NBf & 7) == 0) {
+    const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+    sub = slot & 3;
+    nb = (slot >> 2) * 8 + xcd;
+  } else {
+    nb = blockIdx.x >> 2;
+    sub = blockIdx.x & 3;
+  }
+  const int nsg = p.I_sg / G::SGI;
+  const int nbat = (nsg + K::SGB - 1) / K::SGB;           // batches of the whole reduction
+  const int bpw = (nbat + K::WAVES - 1) / K::WAVES;        // batches per wave
+  const int b0 = wave * bpw;
+  const int nb_w = max(0, min(b0 + bpw, nbat) - b0);       // this wave's batches
+  const int rl = c < R ? c : R - 1;                        // row whose vector this lane reads
+  const bool writes_t = nb == 0 && sub == 0;
+  // this block's stream; load l of batch bb covers its k-blocks bb KBB + 4 l .. + 3
+  const uint16_t* stream = Cf + cf_bf16_elem(p.KB, nb, 0, sub * 8) + (size_t)lane * 8;
+  const int kbmax = p.KB - 4;                              // last whole load (KB % 4 == 0)
+
+  // vector-building lane, pass q: vector v = lane + 64 q -> (row, k) with k
+  // ordered by input, so the x loads of consecutive lanes are contiguous
+  struct VecJob { int r, sgl, j, gg, off; bool on; };
+  auto vjob = [&](int q) {
+    VecJob jb;
+    const int v = lane + 64 * q;
+    jb.on = v < K::NV;
+    const int vv = jb.on ? v : 0;
+    jb.r = vv / K::VPR;
+    const int k = vv - jb.r * K::VPR;
+    jb.sgl = k / (2 * SGK);                 // super-group within the batch
+    const int e = k - jb.sgl * 2 * SGK;
+    int g, sidx, h;
+    if constexpr (P <= 8) { g = e / 4; sidx = e % 4; h = 0; }
+    else { g = e / 8; sidx = (e % 8) / 2; h = e % 2; }
+    const int kbl = jb.sgl * SGK + sidx * G::KBG + h;  // k-block within the batch
+    jb.j = 2 * (kbl >> 2) + g;                         // MFMA step: load kbl / 4, half g
+    jb.gg = kbl & 3;                                   // its k-group
+    jb.off = g * 2 * G::IPG + sidx * (G::IPG / 2);     // first input within the super-group
+    return jb;
+  };
+
+  bf16x8_t fb[2][NL];
+  float xv[2][PASSES][NU];
+  auto load = [&](int buf, int bt) {
+    const int bb = min(b0 + bt, nbat - 1);
+#pragma unroll
+    for (int q = 0; q < PASSES; ++q) {
+      const VecJob jb = vjob(q);
+      const int64_t r = jb.r < p.B ? jb.r : p.B - 1;
+      const int i0 = (bb * K::SGB + jb.sgl) * G::SGI + jb.off;
+#pragma unroll
+      for (int u = 0; u < NU; ++u) xv[buf][q][u] = x[r * p.I + min(i0 + u, p.I - 1)];
+    }
+#pragma unroll
+    for (int l = 0; l < NL; ++l) {
+      const int kb = min(bb * K::KBB + 4 * l, kbmax);
+      fb[buf][l] = *reinterpret_cast<const bf16x8_t*>(stream + (size_t)kb * 128);
+    }
+  };
+
+  f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  auto compute = [&](int buf, int bt) {
+    const bool live = bt < nb_w;
+    const int bb = min(b0 + bt, nbat - 1);
+    // this batch's basis vectors into the wave's LDS area
+#pragma unroll
+    for (int q = 0; q < PASSES; ++q) {
+      const VecJob jb = vjob(q);
+      const int sg = bb * K::SGB + jb.sgl;
+      const int i0 = sg * G::SGI + jb.off;
+      float tv[NU];
+#pragma unroll
+      for (int u = 0; u < NU; ++u)
+        tv[u] = (sg < nsg && i0 + u < p.I) ? input_map(xv[buf][q][u], p.imap, p.ima, p.imb) : 0.0f;
+      if (writes_t && live && jb.on && jb.r < p.B && sg < nsg) {
+        if constexpr (P <= 8) {
+#pragma unroll
+          for (int u = 0; u < NU; ++u) tc[(int64_t)jb.r * p.I_sg + i0 + u] = tv[u];
+        } else if ((jb.gg & 1) == 0) {  // degree-16 vectors come in degree-half pairs
+          tc[(int64_t)jb.r * p.I_sg + i0] = tv[0];
+        }
+      }
+      float vals[8 * G::KBG];
+      if constexpr (P <= 8) {
+#pragma unroll
+        for (int u = 0; u < NU; ++u) cheb_T<P>(tv[u], vals + u * P);
+      } else {
+        cheb_T<P>(tv[0], vals);
+        if (jb.gg & 1) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) vals[e] = vals[8 + e];
+        }
+      }
+      // batches past the wave's range, and super-groups past the last, add nothing
+      const bf16x8_t a = (live && sg < nsg) ? make_frag_bf(vals).v : bf16x8_t{};
+      if (jb.on) vec[wave][jb.j][jb.gg][jb.r] = a;
+    }
+    // the wave reads other lanes' writes of its own area: wait for them to
+    // complete (without the wait, reads have returned stale vectors on
+    // gfx950) and keep the compiler from moving accesses across
+    wait_lgkmcnt<0>();
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int l = 0; l < NL; ++l) {
+      mma16(acc, vec[wave][2 * l][G4][rl], fb[buf][l]);
+      mma16(acc, vec[wave][2 * l + 1][G4][rl], row_rotate8(fb[buf][l]));
+    }
+  };
+
+  // two register buffers, each batch loaded one batch ahead of its MFMAs.
+  // Inside the loop every load is unconditional, so the wait before each use
+  // counts only the loads issued after it; the last one or two batches are
+  // peeled, so no wave loads past its range.
+  int bt = 0;
+  if (nb_w > 0) load(0, 0);
+  for (; bt + 2 < nb_w; bt += 2) {
+    load(1, bt + 1);
+    compute(0, bt);
+    load(0, bt + 2);
+    compute(1, bt + 1);
+  }
+  if (bt + 1 < nb_w) {
+    load(1, bt + 1);
+    compute(0, bt);
+    compute(1, bt + 1);
+  } else if (bt < nb_w) {
+    compute(0, bt);
+  }
+
+  // the 16 waves' tiles (rows 0..15, columns 0..7), added in wave order with the bias
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    if (c < 8) red[wave][G4 * 4 + e][c] = acc[e];
+  __syncthreads();
+  for (int idx = tid; idx < R * 8; idx += 1024) {
+    const int r = idx >> 3, cc = idx & 7;
+    const int o = nb * 32 + sub * 8 + cc;
+    if (r < p.B && o < p.O) {
+      float sum = bias_f[o];
+#pragma unroll
+      for (int w = 0; w < K::WAVES; ++w) sum += red[w][r][cc];
+      y[(size_t)r * p.O + o] = sum;
+    }
   }
 }
 
@@ -1760,8 +1980,24 @@ static bool fwd_pipe_offsets_fit(const Plan& p) {
          (uint64_t)256 * p.I_sg * sizeof(float) < (1ull << 32);
 }
 
+// The one-launch small-batch forward needs a block per CU or more: 8-output
+// streams, so at least 2048 outputs.
+constexpr int kFwdColsMinBlocks = 256;
+
 FwdChoice choose_fwd(const Plan& p) {
   FwdChoice c;
+  if (p.B <= (p.P == 2 ? 2 : 4) && p.esz == 2 && p.O32 / 8 >= kFwdColsMinBlocks) {
+    // enough 8-output streams to spread the coefficient stream over the chip
+    // without a split reduction: one launch
+    c.tile = kFwdCols;
+    c.bm = p.B <= 1 ? 1 : p.B <= 2 ? 2 : 4;
+    c.bnf = 8;
+    c.tiles_m = 1;
+    c.tiles_n = p.O32 / 8;
+    c.splits = 1;
+    c.sg_per_split = p.I_sg / p.SGI;
+    return c;
+  }
   if (p.B <= 64) {
     // coefficient streaming: one 4-wave block per 4 x SPW super-groups of a column block
     const int spw = 16 / p.SGK;
@@ -1812,6 +2048,20 @@ static void fwd_dispatch(const float* x, float* t, const void* packed, float* y,
       reinterpret_cast<const float*>(reinterpret_cast<const char*>(packed) + packed_biasf_offset(p));
   float* part = reinterpret_cast<float*>(ws);
   const bool split = c.splits > 1 || fwd_streaming(c);
+  if (c.tile == kFwdCols) {
+    if constexpr (BF) {
+      const dim3 g((unsigned)c.tiles_n);
+      const uint16_t* cf = reinterpret_cast<const uint16_t*>(Cf);
+#define CKAN_COLS(R) \
+  hipLaunchKernelGGL((k_fwd_cols<P, R>), g, dim3(1024), 0, s, x, t, cf, bias, y, p)
+      // degree 2 (four inputs per vector in registers) up to 2 rows
+      if (c.bm == 1) CKAN_COLS(1);
+      else if (c.bm == 2) CKAN_COLS(2);
+      else if constexpr (P > 2) CKAN_COLS(4);
+#undef CKAN_COLS
+    }
+    return;
+  }
   if (fwd_streaming(c)) {
     dim3 g1(c.tiles_n * c.splits);
     if (c.tile == kFwdStream32)

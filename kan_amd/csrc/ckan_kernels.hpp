@@ -32,7 +32,10 @@ inline size_t packed_bytes(const Plan& p) {
 
 // ---- forward: tile configuration and split-K -------------------------------
 // Tile shapes (waves along M x waves along N, fragments per wave M x N):
-enum FwdTile { kFwdBig = 0, kFwdSmall32 = 1, kFwdSmall64 = 2, kFwdStream32 = 3, kFwdStream64 = 4 };
+enum FwdTile {
+  kFwdBig = 0, kFwdSmall32 = 1, kFwdSmall64 = 2, kFwdStream32 = 3, kFwdStream64 = 4,
+  kFwdCols = 5    // B <= 4, bf16: column-owning blocks, one launch, tanh computed in the kernel
+};
 struct FwdChoice {
   int tile;           // FwdTile
   int bm, bnf;        // block rows, block N fragments
@@ -41,10 +44,13 @@ struct FwdChoice {
 };
 FwdChoice choose_fwd(const Plan& p);
 inline bool fwd_streaming(const FwdChoice& c) { return c.tile == kFwdStream32 || c.tile == kFwdStream64; }
-// The 32-row streaming forward computes tanh itself (each value is needed by
-// every column block, cheap at <= 32 rows); every other path reads the tanh
-// cache written by launch_tanh first.
-inline bool fwd_reads_tcache(const FwdChoice& c) { return c.tile != kFwdStream32; }
+// The 32-row streaming forward and the column-owning forward compute tanh
+// themselves (each value is needed by every column block, cheap
+// at <= 32 rows); every other path reads the tanh cache written by
+// launch_tanh first.
+inline bool fwd_reads_tcache(const FwdChoice& c) {
+  return c.tile != kFwdStream32 && c.tile != kFwdCols;
+}
 // split-K partials [splits][B32][O32] fp32, summed in order by k_fwd_reduce
 inline size_t fwd_ws_bytes(const Plan& p, const FwdChoice& c) {
   if (c.splits <= 1 && !fwd_streaming(c)) return 0;

@@ -95,9 +95,12 @@ def test_null_pointers_rejected_before_launch():
 
 def test_workspace_too_small_is_reported():
     lib = _lib.load()
-    d = _desc(B=1, I=2048, O=2048, deg=8, compute=1, cdt=1)
+    d = _desc(B=16, I=2048, O=2048, deg=8, compute=1, cdt=1)
     need = lib.ckan_fwd_workspace_bytes(ctypes.byref(d))
-    assert need > 0  # small batch uses split-K partials
+    assert need > 0  # 16 rows take the split-K streaming forward (partials)
+    # up to 4 rows at 2048+ outputs take the one-launch forward: no workspace
+    assert lib.ckan_fwd_workspace_bytes(ctypes.byref(_desc(B=1, I=2048, O=2048, deg=8, compute=1,
+                                                           cdt=1))) == 0
     rc = lib.ckan_forward(ctypes.byref(d), 16, 16, 16, 16, 16, need - 256, None)
     assert rc == _lib.CKAN_ERR_WORKSPACE
     assert b"workspace" in lib.ckan_last_error()

@@ -147,10 +147,36 @@ def test_config5_small_batch_bf16_coeffs(B):
     torch.cuda.synchronize()
     y_ref = orc.layer_forward(x, c.float())
     assert _rel(y.cpu(), y_ref) <= BF16_TOL
-    # repeated calls reuse the workspace's split-K partials; results must not drift
+    # repeated calls give bitwise the same result
     y2 = F.chebykan(x.cuda(), c.cuda(), "bf16")
     torch.cuda.synchronize()
     assert torch.equal(y.cpu(), y2.cpu())
+
+
+@pytest.mark.parametrize("B,I,O,deg", [
+    (1, 1000, 2048, 8),    # ragged reduction (the last wave's range is partial)
+    (3, 256, 2050, 8),     # ragged columns: the last block has 2 of its columns
+    (2, 300, 2048, 4),     # degree 4 (two inputs per basis vector)
+    (2, 200, 2080, 2),     # degree 2 (four inputs per basis vector)
+    (3, 200, 2048, 2),     # degree 2 past 2 rows: the split-K streaming forward
+    (4, 130, 2048, 16),    # degree 16 (vectors take degree halves), 4 rows
+    (3, 8, 2048, 8),       # one super-group: the rest of the batch is masked
+    (4, 2048, 4096, 8),
+    (5, 300, 2048, 4),     # past 4 rows: the split-K streaming forward
+    (64, 130, 2048, 16),
+])
+def test_small_batch_wide_forward(B, I, O, deg):
+    """Small batches at 2048 or more outputs (bf16), where up to 4 rows take
+    the one-launch column-owning forward: y against the oracle, and dx / dC
+    through the tanh cache it writes, at shapes that exercise ragged edges."""
+    print(f"small-batch wide forward B={B} I={I} O={O} deg={deg}", flush=True)
+    x, c, dy = _inputs(B, I, O, deg, seed=7 * B + I + deg)
+    c = c.bfloat16().float()
+    y_ref, dx_ref, dc_ref = orc.layer_forward_backward(x, c, dy)
+    y, dx, dc = _gpu_fwd_bwd(x, c, dy, "bf16")
+    assert _rel(y, y_ref) <= BF16_TOL
+    assert _rel(dx, dx_ref) <= BF16_TOL
+    assert _rel(dc, dc_ref) <= BF16_TOL
 
 
 def test_split_k_paths_fp32():
