@@ -725,9 +725,10 @@ k_fwd_reduce(const float* __restrict__ part, int S, const float* __restrict__ bi
 // Block b owns one 8-output stream of the bf16 coefficients (cf_bf16_elem)
 // and the whole reduction, so no split-K partials and no second launch; with
 // 2048 outputs that is 256 blocks, one per CU.  Its 16 waves split the
-// reduction into batches of 4 U k-blocks, read as U / 2 contiguous 1 KiB
-// loads: lane (c, G) = (lane % 16, lane / 16) of load l gets column c % 8 of
-// half c / 8 of k-block 4 l + G.  Each load feeds two
+// reduction into batches of 2 U k-blocks (U MFMA steps: 16, or 8 from 4
+// rows), read as U / 2 contiguous 1 KiB loads: lane (c, G) = (lane % 16,
+// lane / 16) of load l gets column c % 8 of half c / 8 of k-block 4 l + G.
+// Each load feeds two
 // v_mfma_f32_16x16x32_bf16 steps whose k-group G is that k-block: the first
 // half directly (columns 0..7), the second half rotated in from lanes 8..15
 // by a DPP row rotate; columns 8..15 of every step are duplicates whose sums
@@ -743,7 +744,8 @@ struct FwdCols {
   typedef FwdGroup<P> G;
   static constexpr int WAVES = 16;
   static constexpr int NU = P <= 8 ? 8 / P : 1;        // inputs per basis vector
-  static constexpr int U = 16;                         // MFMA steps per batch
+  // MFMA steps per batch (measured at config 5: 16 best for 1 row, 8 for 4)
+  static constexpr int U = R >= 4 ? 8 : 16;
   static constexpr int NL = U / 2;                     // 1 KiB loads per batch
   static constexpr int KBB = 4 * NL;                   // k-blocks per batch (4 per load)
   static constexpr int SGB = KBB / G::SGK;             // super-groups per batch
