@@ -143,12 +143,25 @@ k_pack(const CT* __restrict__ C, typename Elem<BF>::type* __restrict__ Cf,
       }
     }
   } else {
-#pragma unroll 4
-    for (int il = 0; il < 32; ++il) {
-      const int i = i0 + il;
-      const CT* src = C + ((size_t)i * p.O + o0) * D;
-      for (int k = tid; k < 32 * D; k += 256)
-        tile[il * RP + k] = (i < p.I && k < nrow) ? to_f32<CT>(src[k]) : 0.0f;
+    // element k of the flattened [32 inputs][32 * D] tile; 16 loads in flight
+    // per thread before any is stored (one at a time made small packs
+    // latency-bound: 13.7 us for a 64 x 10 x 5 layer)
+    const int nt = 32 * 32 * D;
+    for (int k0 = 0; k0 < nt; k0 += 256 * 16) {
+      float v[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const int k = k0 + u * 256 + tid;
+        const int il = k / (32 * D), e = k - il * (32 * D);
+        const int i = i0 + il;
+        v[u] = (k < nt && i < p.I && e < nrow) ? to_f32<CT>(C[((size_t)i * p.O + o0) * D + e]) : 0.0f;
+      }
+#pragma unroll
+      for (int u = 0; u < 16; ++u) {
+        const int k = k0 + u * 256 + tid;
+        const int il = k / (32 * D), e = k - il * (32 * D);
+        if (k < nt) tile[il * RP + e] = v[u];
+      }
     }
   }
   __syncthreads();

@@ -379,6 +379,27 @@ __device__ __forceinline__ void pin_sgpr(T v) {
   asm volatile("" ::"s"(v));
 }
 
+// The bias sum_i C[i, o, 0] from nparts per-input-block partials
+// part[k * pitch + o], in k_col_reduce's order: four running sums over
+// k = 0, 1, 2, 3 (mod 4), then ((s0 + s1) + s2) + s3.  Every kernel that sums
+// the partials itself uses this, so its bias has the bits of the reduction
+// launch it replaces.
+__device__ __forceinline__ float bias_from_parts(const float* __restrict__ part, int nparts,
+                                                 int pitch, int o) {
+  float s0 = 0.0f, s1 = 0.0f, s2 = 0.0f, s3 = 0.0f;
+  int k = 0;
+  for (; k + 4 <= nparts; k += 4) {
+    s0 += part[(size_t)k * pitch + o];
+    s1 += part[(size_t)(k + 1) * pitch + o];
+    s2 += part[(size_t)(k + 2) * pitch + o];
+    s3 += part[(size_t)(k + 3) * pitch + o];
+  }
+  if (k < nparts) s0 += part[(size_t)k * pitch + o];
+  if (k + 1 < nparts) s1 += part[(size_t)(k + 1) * pitch + o];
+  if (k + 2 < nparts) s2 += part[(size_t)(k + 2) * pitch + o];
+  return ((s0 + s1) + s2) + s3;
+}
+
 // Row of accumulator value v (0..15) for lane half g in a 32x32 MFMA result;
 // the column is lane % 32.
 __device__ __forceinline__ int acc_row(int v, int g) { return 8 * (v >> 2) + 4 * g + (v & 3); }

@@ -73,9 +73,11 @@ k_ce(const float* __restrict__ y, const int64_t* __restrict__ labels, float* __r
   }
 }
 
-// loss = scale * sum_k part[k], k < n, in a fixed order (one block).
+// loss = scale * sum_k part[k], k < n, in a fixed order (one block); also
+// into out2 when given (the caller's per-step loss slot).
 __global__ void __launch_bounds__(256)
-k_sum_scalar(const float* __restrict__ part, int64_t n, float scale, float* __restrict__ out) {
+k_sum_scalar(const float* __restrict__ part, int64_t n, float scale, float* __restrict__ out,
+             float* __restrict__ out2) {
   __shared__ float red[256];
   float s = 0.0f;
   for (int64_t k = threadIdx.x; k < n; k += 256) s += part[k];
@@ -85,7 +87,10 @@ k_sum_scalar(const float* __restrict__ part, int64_t n, float scale, float* __re
     if (threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
     __syncthreads();
   }
-  if (threadIdx.x == 0) *out = red[0] * scale;
+  if (threadIdx.x == 0) {
+    *out = red[0] * scale;
+    if (out2) *out2 = red[0] * scale;
+  }
 }
 
 // Adam scalars for the next step from the device step counter (one thread):
@@ -433,16 +438,19 @@ int run_tiny(ckan_exec* ex, const float* x, const void* target, float* loss_copy
   return hipGetLastError() == hipSuccess ? CKAN_OK : efail(CKAN_ERR_HIP, "executor: step launch failed");
 }
 
-// The step body on stream s with inputs x / target.
-int run_step(ckan_exec* ex, const float* x, const void* target, hipStream_t s) {
-  if (ex->tiny) return run_tiny(ex, x, target, nullptr, s);
+// The step body on stream s with inputs x / target; the loss also goes to
+// loss_copy when given.
+int run_step(ckan_exec* ex, const float* x, const void* target, hipStream_t s,
+             float* loss_copy = nullptr) {
+  if (ex->tiny) return run_tiny(ex, x, target, loss_copy, s);
   const int L = (int)ex->layers.size();
   int rc;
   for (int l = 0; l < L; ++l) {
     auto& ly = ex->layers[l];
-    if ((rc = ckan_pack_coeffs(&ly.desc, ly.C, ly.packed, s))) return rc;
     const float* in = l == 0 ? x : ex->layers[l - 1].y;
-    if ((rc = ckan_forward(&ly.desc, in, ly.packed, ly.y, ly.t, ex->fws, ex->fws_bytes, s)))
+    // pack and forward in one call: tanh in the pack launch, bias summed by the forward
+    if ((rc = ckan_pack_forward(&ly.desc, nullptr, ly.C, ly.packed, in, ly.y, ly.t, ex->fws,
+                                ex->fws_bytes, s)))
       return rc;
   }
   auto& last = ex->layers[L - 1];
@@ -454,12 +462,12 @@ int run_step(ckan_exec* ex, const float* x, const void* target, hipStream_t s) {
                        reinterpret_cast<const float*>(target), last.dy, n,
                        (float)(2.0 / (double)n), ex->loss_part);
     hipLaunchKernelGGL(k_sum_scalar, dim3(1), dim3(256), 0, s, ex->loss_part,
-                       (int64_t)kLossBlocks, (float)(1.0 / (double)n), ex->loss);
+                       (int64_t)kLossBlocks, (float)(1.0 / (double)n), ex->loss, loss_copy);
   } else {
     hipLaunchKernelGGL(k_ce, dim3((unsigned)((B + 3) / 4)), dim3(256), 0, s, last.y,
                        reinterpret_cast<const int64_t*>(target), last.dy, B, O, ex->loss_part);
     hipLaunchKernelGGL(k_sum_scalar, dim3(1), dim3(256), 0, s, ex->loss_part, B,
-                       (float)(1.0 / (double)B), ex->loss);
+                       (float)(1.0 / (double)B), ex->loss, loss_copy);
   }
   if (hipGetLastError() != hipSuccess) return efail(CKAN_ERR_HIP, "executor: loss launch failed");
   const auto& c = ex->cfg;
@@ -672,11 +680,7 @@ int ckan_exec_step(ckan_exec* ex, const float* x, const void* target, float* los
     return hipGetLastError() == hipSuccess;
   };
   if (!ex->cfg.use_graph) {
-    if (ex->tiny) return run_tiny(ex, x, target, loss_out, s);  // writes loss_out itself
-    if ((rc = run_step(ex, x, target, s))) return rc;
-    if (loss_out && !copy(loss_out, ex->loss, 4, s))
-      return efail(CKAN_ERR_HIP, "executor: loss copy failed");
-    return CKAN_OK;
+    return run_step(ex, x, target, s, loss_out);  // writes loss_out itself
   }
   // graph mode.  The graph is captured once on the executor's own stream and
   // replayed on `stream`.  A step whose x and target pointers are those of
@@ -746,15 +750,7 @@ int ckan_exec_steps(ckan_exec* ex, const float* x, const void* target, int64_t n
   int rc;
   for (int64_t k = 0; k < nsteps; ++k) {
     float* lk = losses ? losses + k : nullptr;
-    if (ex->tiny) {
-      if ((rc = run_tiny(ex, x, target, lk, s))) return rc;
-      continue;
-    }
-    if ((rc = run_step(ex, x, target, s))) return rc;
-    if (lk) {
-      hipLaunchKernelGGL(k_copy_f32, dim3(1), dim3(256), 0, s, ex->loss, lk, (int64_t)1);
-      if (hipGetLastError() != hipSuccess) return efail(CKAN_ERR_HIP, "executor: loss copy failed");
-    }
+    if ((rc = run_step(ex, x, target, s, lk))) return rc;
   }
   return CKAN_OK;
 }
@@ -771,10 +767,10 @@ int ckan_exec_forward(ckan_exec* ex, const float* x, float* y, void* stream) {
   int rc;
   for (int l = 0; l < L; ++l) {
     auto& ly = ex->layers[l];
-    if ((rc = ckan_pack_coeffs(&ly.desc, ly.C, ly.packed, s))) return rc;
     const float* in = l == 0 ? x : ex->layers[l - 1].y;
     float* out = l == L - 1 ? y : ly.y;
-    if ((rc = ckan_forward(&ly.desc, in, ly.packed, out, ly.t, ex->fws, ex->fws_bytes, s)))
+    if ((rc = ckan_pack_forward(&ly.desc, nullptr, ly.C, ly.packed, in, out, ly.t, ex->fws,
+                                ex->fws_bytes, s)))
       return rc;
   }
   return CKAN_OK;

@@ -46,7 +46,8 @@ template <int P, bool BF, int NM, int NN, int WGM, int WGN>
 __global__ void __launch_bounds__(256)
 k_fwd(const float* __restrict__ tc, const typename Elem<BF>::type* __restrict__ Cf,
       const float* __restrict__ bias_f, float* __restrict__ y, float* __restrict__ part,
-      Plan p, int sg_per_split) {
+      Plan p, int sg_per_split, const float* __restrict__ bias_part, int nib,
+      float* __restrict__ bias_out) {
   typedef typename Elem<BF>::type E;
   typedef FwdGroup<P> G;
   static_assert(WGM * WGN == 4, "4 waves per block");
@@ -177,11 +178,18 @@ k_fwd(const float* __restrict__ tc, const typename Elem<BF>::type* __restrict__ 
 
   const bool split = gridDim.z > 1;
   if (!split) {
+    // nib > 0: the bias from its per-input-block partials (and the first row
+    // of blocks fills the packed bias slot for later forwards)
+    if (nib > 0 && blockIdx.x == 0)
+      for (int idx = threadIdx.x; idx < BNF * 32; idx += 256) {
+        const int o = nb0 * 32 + idx;
+        if (o < p.O32) bias_out[o] = bias_from_parts(bias_part, nib, p.O32, o);
+      }
 #pragma unroll
     for (int ni = 0; ni < NN; ++ni) {
       const int o = (nb0 + wn * NN + ni) * 32 + (lane & 31);
       if (o >= p.O) continue;
-      const float bias = bias_f[o];
+      const float bias = nib > 0 ? bias_from_parts(bias_part, nib, p.O32, o) : bias_f[o];
 #pragma unroll
       for (int mi = 0; mi < NM; ++mi) {
         const int64_t r0 = m_blk + (wm * NM + mi) * 32;
@@ -707,16 +715,23 @@ k_fwd_stream(const float* __restrict__ x, float* __restrict__ tc,
   }
 }
 
-// y[r, o] = bias[o] + sum_z part[z][r][o], z in split order.
+// y[r, o] = bias[o] + sum_z part[z][r][o], z in split order.  nib > 0: the
+// bias comes from its per-input-block partials (summed per element: the host
+// chooses this only for small outputs) and the packed bias slot is filled.
 __global__ void __launch_bounds__(256)
 k_fwd_reduce(const float* __restrict__ part, int S, const float* __restrict__ bias_f,
-             float* __restrict__ y, Plan p) {
+             float* __restrict__ y, Plan p, const float* __restrict__ bias_part, int nib,
+             float* __restrict__ bias_out) {
   const int64_t n = p.B * (int64_t)p.O;
-  for (int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; q < n;
+  const int64_t nn = n > p.O32 ? n : p.O32;
+  for (int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; q < nn;
        q += (int64_t)gridDim.x * blockDim.x) {
+    if (nib > 0 && q < p.O32) bias_out[q] = bias_from_parts(bias_part, nib, p.O32, (int)q);
+    if (q >= n) continue;
     const int64_t r = q / p.O;
     const int o = (int)(q - r * p.O);
-    y[q] = split_sum(part + (size_t)r * p.O32 + o, (size_t)p.B32 * p.O32, (unsigned)S, bias_f[o]);
+    const float bias = nib > 0 ? bias_from_parts(bias_part, nib, p.O32, o) : bias_f[o];
+    y[q] = split_sum(part + (size_t)r * p.O32 + o, (size_t)p.B32 * p.O32, (unsigned)S, bias);
   }
 }
 
@@ -771,7 +786,8 @@ __device__ __forceinline__ bf16x8_t row_rotate8(const bf16x8_t& v) {
 template <int P, int R>
 __global__ void __launch_bounds__(1024)
 k_fwd_cols(const float* __restrict__ x, float* __restrict__ tc, const uint16_t* __restrict__ Cf,
-           const float* __restrict__ bias_f, float* __restrict__ y, Plan p) {
+           const float* __restrict__ bias_f, float* __restrict__ y, Plan p,
+           const float* __restrict__ bias_part, int nib, float* __restrict__ bias_out) {
   typedef FwdCols<P, R> K;
   typedef FwdGroup<P> G;
   constexpr int U = K::U, NL = K::NL, NU = K::NU, SGK = G::SGK, PASSES = K::PASSES;
@@ -920,11 +936,15 @@ k_fwd_cols(const float* __restrict__ x, float* __restrict__ tc, const uint16_t* 
   for (int e = 0; e < 4; ++e)
     if (c < 8) red[wave][G4 * 4 + e][c] = acc[e];
   __syncthreads();
+  // nib > 0: the bias from its per-input-block partials; the block fills its
+  // 8 entries of the packed bias slot
+  if (nib > 0 && tid < 8)
+    bias_out[nb * 32 + sub * 8 + tid] = bias_from_parts(bias_part, nib, p.O32, nb * 32 + sub * 8 + tid);
   for (int idx = tid; idx < R * 8; idx += 1024) {
     const int r = idx >> 3, cc = idx & 7;
     const int o = nb * 32 + sub * 8 + cc;
     if (r < p.B && o < p.O) {
-      float sum = bias_f[o];
+      float sum = nib > 0 ? bias_from_parts(bias_part, nib, p.O32, o) : bias_f[o];
 #pragma unroll
       for (int w = 0; w < K::WAVES; ++w) sum += red[w][r][cc];
       y[(size_t)r * p.O + o] = sum;
@@ -2046,16 +2066,22 @@ static void fwd_dispatch(const float* x, float* t, const void* packed, float* y,
                          const Plan& p, const FwdChoice& c, hipStream_t s, int nib) {
   typedef typename Elem<BF>::type E;
   const E* Cf = reinterpret_cast<const E*>(packed);
-  const float* bias =
-      reinterpret_cast<const float*>(reinterpret_cast<const char*>(packed) + packed_biasf_offset(p));
+  char* pk = const_cast<char*>(reinterpret_cast<const char*>(packed));
+  const float* bias = reinterpret_cast<const float*>(pk + packed_biasf_offset(p));
+  // nib > 0: the forward sums the per-input-block bias partials itself and
+  // fills the bias slot (bias_out) for later forwards on this packed buffer
+  const float* bpart = reinterpret_cast<const float*>(pk + packed_bias_offset(p));
+  float* bias_out = nib > 0 ? reinterpret_cast<float*>(pk + packed_biasf_offset(p)) : nullptr;
   float* part = reinterpret_cast<float*>(ws);
   const bool split = c.splits > 1 || fwd_streaming(c);
+  const int nib_k = split ? 0 : nib;  // unsplit kernels add the bias, split ones leave it to the reduce
   if (c.tile == kFwdCols) {
     if constexpr (BF) {
       const dim3 g((unsigned)c.tiles_n);
       const uint16_t* cf = reinterpret_cast<const uint16_t*>(Cf);
-#define CKAN_COLS(R) \
-  hipLaunchKernelGGL((k_fwd_cols<P, R>), g, dim3(1024), 0, s, x, t, cf, bias, y, p)
+#define CKAN_COLS(R)                                                                       \
+  hipLaunchKernelGGL((k_fwd_cols<P, R>), g, dim3(1024), 0, s, x, t, cf, bias, y, p, bpart, \
+                     nib_k, bias_out)
       // degree 2 (four inputs per vector in registers) up to 2 rows
       if (c.bm == 1) CKAN_COLS(1);
       else if (c.bm == 2) CKAN_COLS(2);
@@ -2075,53 +2101,49 @@ static void fwd_dispatch(const float* x, float* t, const void* packed, float* y,
     switch (c.tile) {
       case kFwdSmall32:
         hipLaunchKernelGGL((k_fwd<P, BF, 1, 1, 1, 4>), grid, dim3(256), 0, s, t, Cf, bias, y, part,
-                           p, c.sg_per_split);
+                           p, c.sg_per_split, bpart, nib_k, bias_out);
         break;
       case kFwdSmall64:
         hipLaunchKernelGGL((k_fwd<P, BF, 2, 1, 1, 4>), grid, dim3(256), 0, s, t, Cf, bias, y, part,
-                           p, c.sg_per_split);
+                           p, c.sg_per_split, bpart, nib_k, bias_out);
         break;
       default:
         if constexpr (FwdPipe<P, BF>::kOk) {
           typedef FwdPipe<P, BF> K;
           if (!fwd_pipe_offsets_fit(p)) {  // per-lane copy offsets are 32-bit
             hipLaunchKernelGGL((k_fwd<P, BF, 2, 4, 4, 1>), grid, dim3(256), 0, s, t, Cf, bias, y,
-                               part, p, c.sg_per_split);
+                               part, p, c.sg_per_split, bpart, nib_k, bias_out);
             break;
           }
           const size_t lds = (size_t)K::LDS_BYTES;
           static std::atomic<uint32_t> lds_set{0};
           ensure_lds_limit(reinterpret_cast<const void*>(&k_fwd_pipe<P, BF>), (int)lds, lds_set);
-          // nib > 0: the bias partials, summed in the kernel, which also fills the bias slot
-          char* pk = const_cast<char*>(reinterpret_cast<const char*>(packed));
           hipLaunchKernelGGL((k_fwd_pipe<P, BF>), grid, dim3(K::THREADS), lds, s, t, Cf, bias, y,
-                             part, p, c.sg_per_split,
-                             reinterpret_cast<const float*>(pk + packed_bias_offset(p)), nib,
-                             nib > 0 ? reinterpret_cast<float*>(pk + packed_biasf_offset(p)) : nullptr);
+                             part, p, c.sg_per_split, bpart, nib_k, nib_k > 0 ? bias_out : nullptr);
         } else {
           hipLaunchKernelGGL((k_fwd<P, BF, 2, 4, 4, 1>), grid, dim3(256), 0, s, t, Cf, bias, y,
-                             part, p, c.sg_per_split);
+                             part, p, c.sg_per_split, bpart, nib_k, bias_out);
         }
         break;
     }
   }
   if (split) {
     const int64_t n = p.B * (int64_t)p.O;
-    int64_t gsz = (n + 255) / 256;
+    int64_t gsz = ((n > p.O32 ? n : p.O32) + 255) / 256;
     if (gsz > 65536) gsz = 65536;
-    hipLaunchKernelGGL(k_fwd_reduce, dim3((unsigned)gsz), dim3(256), 0, s, part, c.splits, bias, y, p);
+    hipLaunchKernelGGL(k_fwd_reduce, dim3((unsigned)gsz), dim3(256), 0, s, part, c.splits, bias, y,
+                       p, bpart, nib, bias_out);
   }
 }
 
+// The forward can sum the bias partials itself: every unsplit kernel does it
+// once per column; a split forward's reduce does it per output element, so
+// only for small outputs.
 bool fwd_sums_bias(const Plan& p, const FwdChoice& c) {
-  if (c.tile != kFwdBig || c.splits > 1 || p.NIB <= 1 || !fwd_pipe_offsets_fit(p)) return false;
-  const bool bf = p.esz == 2;
-  switch (p.P) {
-    case 2: return bf ? FwdPipe<2, true>::kOk : FwdPipe<2, false>::kOk;
-    case 4: return bf ? FwdPipe<4, true>::kOk : FwdPipe<4, false>::kOk;
-    case 8: return bf ? FwdPipe<8, true>::kOk : FwdPipe<8, false>::kOk;
-    default: return bf ? FwdPipe<16, true>::kOk : FwdPipe<16, false>::kOk;
-  }
+  if (p.NIB <= 1) return false;
+  const bool split = c.splits > 1 || fwd_streaming(c);
+  if (split) return (uint64_t)p.B * p.O * p.NIB <= ((uint64_t)1 << 22);
+  return true;
 }
 
 void launch_fwd_gemm(const float* x, float* t, const void* packed, float* y, void* ws,

@@ -497,8 +497,12 @@ def test_adam_resumes_from_a_torch_optim_checkpoint():
     (16384, 512, 512, 16, 1, None),  # the same at degree 16 (config-4 layer shape)
     (8192, 1024, 1024, 8, 0, "jacobi"),  # fp32, family basis, bias summed in the forward
     (1000, 100, 150, 6, 0, None),    # padded inputs: tanh launched on its own
-    (300, 256, 200, 3, 1, None),     # split small-batch forward: bias reduced by a launch
+    (300, 256, 200, 3, 1, None),     # split small-batch forward: bias summed by the split reduce
+    (100, 16, 96, 4, 0, None),       # unsplit small-batch forward: bias summed in its epilogue
+    (1024, 1024, 64, 8, 1, None),    # split pipelined forward: bias summed by the split reduce
     (20, 512, 64, 8, 1, None),       # streaming forward (tanh computed in the stream kernel)
+    (2, 512, 2048, 8, 1, None),      # one-launch column-owning forward
+    (64, 2048, 2048, 8, 1, None),    # streaming forward with a large output: bias by a launch
     (2048, 256, 256, 16, 1, "jacobi"),
 ])
 def test_pack_forward_equals_pack_then_forward(B, I, O, deg, compute, family):
