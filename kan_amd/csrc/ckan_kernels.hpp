@@ -130,7 +130,8 @@ void launch_pack(const void* C, bool c_bf16, void* packed, const Plan& p, hipStr
                  const BasisXform* xf = nullptr, bool reduce_bias = true,
                  const float* x = nullptr, float* t = nullptr);
 // x's tanh can ride in the pack launch: rows need no padding (I == I_sg),
-// I % 4 == 0 and x is 16-byte aligned (the flat float4 layout).
+// I % 4 == 0, x is 16-byte aligned (the flat float4 layout) and the pack's
+// blocks cover the tanh stream in one pass each.
 bool pack_tanh_fusable(const Plan& p, const float* x);
 void launch_prep_dy(const float* dy, void* dYx, void* dYc, float* colsum_part, const Plan& p,
                     bool need_dx, bool need_dc, hipStream_t s);
