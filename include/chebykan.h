@@ -217,7 +217,9 @@ int ckan_family_basis_backward(const ckan_basis_spec* spec, const float* t, cons
  * x that is again a Chebyshev series in t = tanh x, of degree degree + k:
  *   d^k f / dx^k = sum_j Ck[i, o, j] T_j(t),   Ck = C R,   R = M L^k,
  * with M the family's change of basis and L : p -> (1 - t^2) p'(t) (exact in
- * the T basis).  Requires degree + k <= 16 and fp32 coefficients.
+ * the T basis).  Requires fp32 coefficients and degree + k <= 16 for a
+ * family basis, degree + k <= 256 for the Chebyshev one (above 16 the device
+ * applies L row by row in place of the matrix R).
  * Replaces KANLayer.compute_derivatives / jacobian (kan/layers/base.py:102-141)
  * and ChebyshevBasis.derivative (kan/basis/chebyshev.py:174-267).  Divergence:
  * the reference's derivative coefficients are wrong for n >= 3, omit the

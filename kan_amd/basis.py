@@ -66,7 +66,7 @@ class BasisFunction(ABC):
         Divergence: the reference's Chebyshev derivative coefficients are wrong
         from degree 3 on and leave out the input map's chain factor; this is the
         exact derivative in x, the same quantity KANLayer.compute_derivatives
-        returns (degree + order <= 16)."""
+        returns (degree + order <= 256; 16 for the Jacobi / Hermite bases)."""
         check = getattr(self, "_check_input_map", None)
         if callable(check):
             check()

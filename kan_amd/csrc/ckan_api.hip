@@ -577,33 +577,43 @@ int derivative_xform(const ckan_basis_spec* spec, int degree, int order, bool tr
                      BasisXform* r, int* dout, double* Rout = nullptr) {
   if (degree < 0) return fail(CKAN_ERR_INVALID_ARG, "degree must be >= 0");
   if (order < 0) return fail(CKAN_ERR_INVALID_ARG, "derivative order must be >= 0");
-  if (degree + order >= kMaxD)
+  if (degree + order > kValuMaxDegree)
     return fail(CKAN_ERR_UNSUPPORTED, "degree %d + derivative order %d exceeds %d", degree, order,
-                kMaxD - 1);
+                kValuMaxDegree);
+  // the operator in kernel arguments (and every family basis) stops at
+  // degree + order = kMaxD - 1; longer Chebyshev series go row by row
+  if (degree + order >= kMaxD && (spec || r))
+    return fail(CKAN_ERR_UNSUPPORTED, "%s: degree %d + derivative order %d exceeds %d",
+                spec ? "family basis" : "operator", degree, order, kMaxD - 1);
   const int D = degree + 1, DO = D + order;
-  double M[kMaxD * kMaxD];
+  std::vector<double> M((size_t)D * D, 0.0);
   if (spec) {
     double a[kMaxD], b[kMaxD], c[kMaxD];
     int rc = family_of(spec, degree, a, b, c);
     if (rc) return rc;
-    family_to_chebyshev(a, b, c, degree, spec->scale, M);
+    family_to_chebyshev(a, b, c, degree, spec->scale, M.data());
   } else {
-    for (int n = 0; n < D; ++n)
-      for (int k = 0; k < D; ++k) M[n * D + k] = n == k ? 1.0 : 0.0;
+    for (int n = 0; n < D; ++n) M[(size_t)n * D + n] = 1.0;
   }
-  double R[kMaxD * kMaxD];
-  if (!derivative_to_chebyshev(M, degree, order, R))
+  std::vector<double> R((size_t)D * DO);
+  if (!derivative_to_chebyshev(M.data(), degree, order, R.data()))
     return fail(CKAN_ERR_UNSUPPORTED, "derivative of order %d at degree %d", order, degree);
   if (Rout)
-    for (int q = 0; q < D * DO; ++q) Rout[q] = R[q];
+    for (size_t q = 0; q < (size_t)D * DO; ++q) Rout[q] = R[q];
   if (r) {
     for (int q = 0; q < kMaxD * kMaxD; ++q) r->m[q] = 0.0f;
     for (int n = 0; n < D; ++n)
       for (int k = 0; k < DO; ++k)
-        r->m[transposed ? k * kMaxD + n : n * kMaxD + k] = (float)R[n * DO + k];
+        r->m[transposed ? k * kMaxD + n : n * kMaxD + k] = (float)R[(size_t)n * DO + k];
   }
   if (dout) *dout = DO;
   return CKAN_OK;
+}
+
+// Chebyshev layers whose derivative series is longer than the operator in
+// kernel arguments: the row-by-row kernels (launch_cheb_deriv_rows).
+inline bool deriv_by_rows(const ckan_basis_spec* spec, int degree, int order) {
+  return !spec && order >= 0 && degree + order >= kMaxD;
 }
 
 int check_f32_layer(const ckan_desc* desc) {
@@ -625,12 +635,19 @@ int ckan_derivative_coeffs(const ckan_desc* desc, const ckan_basis_spec* spec, i
                            const float* coeffs, float* out, void* stream) {
   int rc = check_f32_layer(desc);
   if (rc) return rc;
+  const int64_t rows = (int64_t)desc->in_dim * desc->out_dim;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (deriv_by_rows(spec, desc->degree, order)) {
+    if ((rc = derivative_xform(nullptr, desc->degree, order, false, nullptr, nullptr))) return rc;
+    if (!coeffs || !out) return fail(CKAN_ERR_INVALID_ARG, "coeffs/out is NULL");
+    ProfScope ps("deriv_coeffs", s);
+    launch_cheb_deriv_rows(coeffs, out, rows, desc->degree, order, false, 0, s);
+    return check_launch("derivative_coeffs");
+  }
   BasisXform r;
   int dout = 0;
   if ((rc = derivative_xform(spec, desc->degree, order, false, &r, &dout))) return rc;
   if (!coeffs || !out) return fail(CKAN_ERR_INVALID_ARG, "coeffs/out is NULL");
-  const int64_t rows = (int64_t)desc->in_dim * desc->out_dim;
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   ProfScope ps("deriv_coeffs", s);
   launch_coeff_xform(coeffs, out, rows, desc->degree + 1, dout, 0, r, s);
   return check_launch("derivative_coeffs");
@@ -641,12 +658,19 @@ int ckan_derivative_coeffs_backward(const ckan_desc* desc, const ckan_basis_spec
                                     void* stream) {
   int rc = check_f32_layer(desc);
   if (rc) return rc;
+  const int64_t rows = (int64_t)desc->in_dim * desc->out_dim;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (deriv_by_rows(spec, desc->degree, order)) {
+    if ((rc = derivative_xform(nullptr, desc->degree, order, true, nullptr, nullptr))) return rc;
+    if (!dout_grad || !dcoeffs) return fail(CKAN_ERR_INVALID_ARG, "dout_grad/dcoeffs is NULL");
+    ProfScope ps("deriv_coeffs_bwd", s);
+    launch_cheb_deriv_rows(dout_grad, dcoeffs, rows, desc->degree, order, true, 0, s);
+    return check_launch("derivative_coeffs_backward");
+  }
   BasisXform rt;
   int dout = 0;
   if ((rc = derivative_xform(spec, desc->degree, order, true, &rt, &dout))) return rc;
   if (!dout_grad || !dcoeffs) return fail(CKAN_ERR_INVALID_ARG, "dout_grad/dcoeffs is NULL");
-  const int64_t rows = (int64_t)desc->in_dim * desc->out_dim;
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   ProfScope ps("deriv_coeffs_bwd", s);
   launch_coeff_xform(dout_grad, dcoeffs, rows, dout, desc->degree + 1, 0, rt, s);
   return check_launch("derivative_coeffs_backward");
@@ -661,9 +685,10 @@ int ckan_jacobian(const ckan_desc* desc, const ckan_basis_spec* spec, const floa
                   const float* coeffs, float* jac, void* ws, size_t ws_bytes, void* stream) {
   int rc = check_f32_layer(desc);
   if (rc) return rc;
+  const bool by_rows = deriv_by_rows(spec, desc->degree, 1);
   BasisXform r;
   int dout = 0;
-  if ((rc = derivative_xform(spec, desc->degree, 1, false, &r, &dout))) return rc;
+  if ((rc = derivative_xform(spec, desc->degree, 1, false, by_rows ? nullptr : &r, &dout))) return rc;
   if (desc->batch == 0) return CKAN_OK;
   if (!x || !coeffs || !jac) return fail(CKAN_ERR_INVALID_ARG, "x/coeffs/jac is NULL");
   const size_t need = ckan_jacobian_workspace_bytes(desc);
@@ -673,7 +698,10 @@ int ckan_jacobian(const ckan_desc* desc, const ckan_basis_spec* spec, const floa
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   ProfScope ps("jacobian", s);
   float* c1t = reinterpret_cast<float*>(ws);
-  launch_coeff_xform(coeffs, c1t, rows, desc->degree + 1, dout, desc->out_dim, r, s);
+  if (by_rows)
+    launch_cheb_deriv_rows(coeffs, c1t, rows, desc->degree, 1, false, desc->out_dim, s);
+  else
+    launch_coeff_xform(coeffs, c1t, rows, desc->degree + 1, dout, desc->out_dim, r, s);
   launch_jacobian(x, c1t, jac, desc->batch, desc->in_dim, desc->out_dim, dout, s);
   return check_launch("jacobian");
 }

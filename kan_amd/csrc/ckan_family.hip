@@ -113,7 +113,7 @@ static void chebyshev_dx(const double* a, int deg, double* out /* deg + 2 */) {
 }
 
 bool derivative_to_chebyshev(const double* M, int degree, int order, double* R) {
-  if (degree < 0 || order < 0 || degree + order >= kMaxD) return false;
+  if (degree < 0 || order < 0) return false;
   const int D = degree + 1, DO = D + order;
   std::vector<double> cur(DO, 0.0), nxt(DO + 1, 0.0);
   for (int n = 0; n < D; ++n) {
@@ -307,6 +307,143 @@ void launch_coeff_xform(const float* in, float* out, int64_t rows, int din, int 
   hipLaunchKernelGGL(k_coeff_xform, g, dim3(256), 0, s, in, out, rows, din, dout, transposed_o, r);
 }
 
+// ---- the derivative operator row by row (Chebyshev series of any degree) ---
+// For series too long for the operator matrix in the kernel arguments, each
+// (i, o) row is transformed on the device, in place in LDS, one derivative
+// step at a time (the steps of chebyshev_dx in fp32): the Chebyshev
+// derivative recurrence b_{k-1} = b_{k+1} + 2 k a_k (b_0 halved), then the
+// product with 1 - t^2, a stencil since t^2 T_k = T_k / 2 + (T_{k+2} +
+// T_{|k-2|}) / 4:  r_j = q_j / 2 - (q_{j-2} + q_{j+2}) / 4, less q_1 / 4 at
+// j = 1 and q_0 / 4 at j = 2.  The adjoint applies the transposed steps in
+// reverse order (the coefficient gradient).
+constexpr int kDerivRows = 32;  // rows per block, one lane each
+
+// degree deg (r[0..deg]) -> degree deg + 1 (r[0..deg + 1]); r[deg + 1] is 0 on entry
+__device__ void cheb_dx_inplace(float* r, int deg) {
+  float bnext = 0.0f, bcur = 0.0f, ak = r[deg];  // b_{k+1}, b_k, a_k
+  for (int k = deg; k >= 1; --k) {
+    const float akm1 = r[k - 1];
+    const float bkm1 = fmaf(2.0f * (float)k, ak, bnext);
+    r[k - 1] = bkm1;
+    bnext = bcur;
+    bcur = bkm1;
+    ak = akm1;
+  }
+  r[deg] = 0.0f;
+  if (deg >= 1) r[0] *= 0.5f;
+  const float q0 = r[0];  // q = r[0 .. deg - 1]
+  float qm2 = 0.0f, qm1 = 0.0f;
+  for (int j = 0; j <= deg + 1; ++j) {
+    const float qj = j <= deg - 1 ? r[j] : 0.0f;
+    const float qj2 = j + 2 <= deg - 1 ? r[j + 2] : 0.0f;
+    float v = 0.5f * qj - 0.25f * (qm2 + qj2);
+    if (j == 1) v -= 0.25f * qj;
+    if (j == 2) v -= 0.25f * (deg >= 1 ? q0 : 0.0f);
+    r[j] = v;
+    qm2 = qm1;
+    qm1 = qj;
+  }
+}
+
+// the transpose of cheb_dx_inplace: r[0..deg + 1] -> r[0..deg] (r[deg + 1] zeroed)
+__device__ void cheb_dx_adjoint_inplace(float* r, int deg) {
+  float rm2 = 0.0f, rm1 = 0.0f;
+  for (int k = 0; k <= deg + 1; ++k) {
+    const float rk = r[k];
+    const float rk2 = k + 2 <= deg + 1 ? r[k + 2] : 0.0f;
+    float v = 0.5f * rk - 0.25f * (rk2 + rm2);
+    if (k == 1) v -= 0.25f * rk;
+    if (k == 0) v -= 0.25f * rk2;
+    r[k] = k < deg ? v : 0.0f;
+    rm2 = rm1;
+    rm1 = rk;
+  }
+  float se = 0.0f, so = 0.0f;  // weighted sums of the b-bar of even / odd index below k
+  for (int k = 0; k <= deg; ++k) {
+    const float qb = k < deg ? r[k] : 0.0f;
+    r[k] = 2.0f * (float)k * ((k & 1) ? se : so);
+    const float w = k == 0 ? 0.5f : 1.0f;
+    if (k & 1) so = fmaf(w, qb, so);
+    else se = fmaf(w, qb, se);
+  }
+}
+
+// in [rows][din] -> out: [rows][dout], or [o][dout][i] for rows q = i * tO + o
+// when tO > 0 (the Jacobian's layout).  ADJ: the transposed operator.
+template <bool ADJ>
+__global__ void __launch_bounds__(64)
+k_cheb_deriv_rows(const float* __restrict__ in, float* __restrict__ out, int64_t rows, int din,
+                  int dout, int deg0, int order, int pitch, int tO) {
+  extern __shared__ float sm[];
+  const int tid = threadIdx.x;
+  const int64_t q0 = (int64_t)blockIdx.x * kDerivRows;
+  const int nr = (int)(rows - q0 < kDerivRows ? rows - q0 : kDerivRows);
+  for (int idx = tid; idx < kDerivRows * pitch; idx += 64) sm[idx] = 0.0f;
+  __syncthreads();
+  for (int idx = tid; idx < nr * din; idx += 64) {  // the block's rows are contiguous
+    const int r = idx / din, k = idx - r * din;
+    sm[r * pitch + k] = in[q0 * din + idx];
+  }
+  __syncthreads();
+  if (tid < nr) {
+    float* rr = sm + tid * pitch;
+    if constexpr (!ADJ) {
+      for (int st = 0; st < order; ++st) cheb_dx_inplace(rr, deg0 + st);
+    } else {
+      for (int st = order - 1; st >= 0; --st) cheb_dx_adjoint_inplace(rr, deg0 + st);
+    }
+  }
+  __syncthreads();
+  if (tO == 0) {
+    for (int idx = tid; idx < nr * dout; idx += 64) {
+      const int r = idx / dout, k = idx - r * dout;
+      out[q0 * dout + idx] = sm[r * pitch + k];
+    }
+  } else {
+    const int64_t I = rows / tO;
+    for (int idx = tid; idx < nr * dout; idx += 64) {
+      const int r = idx / dout, k = idx - r * dout;
+      const int64_t q = q0 + r, i = q / tO, o = q - i * tO;
+      out[((size_t)o * dout + k) * I + i] = sm[r * pitch + k];
+    }
+  }
+}
+
+void launch_cheb_deriv_rows(const float* in, float* out, int64_t rows, int degree, int order,
+                            bool adjoint, int transposed_o, hipStream_t s) {
+  const int D = degree + 1, DO = D + order;
+  const int pitch = DO | 1;  // odd: the 32 row lanes hit distinct banks
+  const size_t lds = (size_t)kDerivRows * pitch * sizeof(float);
+  const dim3 g((unsigned)((rows + kDerivRows - 1) / kDerivRows));
+  if (adjoint)
+    hipLaunchKernelGGL(k_cheb_deriv_rows<true>, g, dim3(64), lds, s, in, out, rows, DO, D, degree,
+                       order, pitch, transposed_o);
+  else
+    hipLaunchKernelGGL(k_cheb_deriv_rows<false>, g, dim3(64), lds, s, in, out, rows, D, DO, degree,
+                       order, pitch, transposed_o);
+}
+
+// jac[b, o, i] for any number of terms: the recurrence runs along k for each o.
+__global__ void __launch_bounds__(256)
+k_jacobian_any(const float* __restrict__ x, const float* __restrict__ c1t, float* __restrict__ jac,
+               int64_t B, int I, int O, int dout) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  const int64_t b = blockIdx.y;
+  if (i >= I) return;
+  const float t = tanhf(x[b * I + i]), t2 = t + t;
+  for (int o = 0; o < O; ++o) {
+    const float* c = c1t + (size_t)o * dout * I + i;
+    float tp = t, tc = 1.0f, acc = 0.0f;  // T_{-1} = t, T_0
+    for (int k = 0; k < dout; ++k) {
+      acc = fmaf(c[(size_t)k * I], tc, acc);
+      const float nx = fmaf(t2, tc, -tp);
+      tp = tc;
+      tc = nx;
+    }
+    jac[((size_t)b * O + o) * I + i] = acc;
+  }
+}
+
 void launch_jacobian(const float* x, const float* c1t, float* jac, int64_t B, int I, int O,
                      int dout, hipStream_t s) {
   constexpr int64_t kMaxGridY = 65535;
@@ -319,8 +456,10 @@ void launch_jacobian(const float* x, const float* c1t, float* jac, int64_t B, in
       hipLaunchKernelGGL((k_jacobian<5>), g, dim3(256), 0, s, xb, c1t, jb, nb, I, O, dout);
     else if (dout <= 9)
       hipLaunchKernelGGL((k_jacobian<9>), g, dim3(256), 0, s, xb, c1t, jb, nb, I, O, dout);
-    else
+    else if (dout <= 17)
       hipLaunchKernelGGL((k_jacobian<17>), g, dim3(256), 0, s, xb, c1t, jb, nb, I, O, dout);
+    else
+      hipLaunchKernelGGL(k_jacobian_any, g, dim3(256), 0, s, xb, c1t, jb, nb, I, O, dout);
   }
 }
 

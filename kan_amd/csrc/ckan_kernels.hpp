@@ -94,13 +94,19 @@ void launch_basis_family_bwd(const float* t, const float* g, int64_t n, int deg,
 // f(x) = sum_k c_k T_k(tanh x) has d/dx f = (1 - t^2) f'(t): again a Chebyshev
 // series in t = tanh x, one degree higher.  R[n * (D + order) + k] (fp64,
 // exact up to rounding) maps row n of M (the family's change of basis, D x D)
-// through `order` such steps; false if degree + order > kMaxD - 1.
+// through `order` such steps (R has degree + 1 rows of degree + 1 + order).
 bool derivative_to_chebyshev(const double* M, int degree, int order, double* R);
 // out = in R over rows q of `rows`: in [rows][din], R [din][dout] (row-major,
 // r[n * kMaxD + k]).  transposed_o > 0 writes out as [o][dout][i] for rows
 // q = i * transposed_o + o (the Jacobian's layout), else [rows][dout].
 void launch_coeff_xform(const float* in, float* out, int64_t rows, int din, int dout,
                         int transposed_o, const BasisXform& r, hipStream_t s);
+// The derivative operator (adjoint: its transpose) applied row by row on the
+// device, for Chebyshev series of any degree: in [rows][D] -> out [rows][D +
+// order] (adjoint: [rows][D + order] -> [rows][D]); transposed_o > 0 writes
+// [o][dout][i] as launch_coeff_xform does.
+void launch_cheb_deriv_rows(const float* in, float* out, int64_t rows, int degree, int order,
+                            bool adjoint, int transposed_o, hipStream_t s);
 // jac[b, o, i] = sum_k C1t[o][k][i] T_k(tanh x[b, i]), k < dout.
 void launch_jacobian(const float* x, const float* c1t, float* jac, int64_t B, int I, int O,
                      int dout, hipStream_t s);

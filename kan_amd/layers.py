@@ -64,7 +64,8 @@ class KANLayer(nn.Module, ABC):
         Divergence: the reference evaluates ChebyshevBasis.derivative, whose
         coefficients are wrong from degree 3 on and which differentiates in
         tanh(x) without the chain factor; this returns the exact x-derivative
-        (a Chebyshev series of degree degree + order, so degree + order <= 16)."""
+        (a Chebyshev series of degree degree + order: degree + order <= 256,
+        or 16 for the Jacobi / Hermite layers)."""
         check = getattr(self.basis_function, "_check_input_map", None)
         if callable(check):
             check()

@@ -134,16 +134,64 @@ def test_derivatives_are_differentiable():
     assert _rel(xd.grad, xr.grad) <= FP32_TOL
 
 
+def _derivatives_graph(x, c, order):
+    """sum_i d^order y[b, o] / d x[b, i]^order in fp64 with c kept in the graph
+    (each y[b, o] is a sum of univariate functions, so the repeated gradient
+    of the column sum is the per-input derivative)."""
+    xr = x.double().requires_grad_(True)
+    y = do.chebykan_forward64(xr, c)
+    cols = []
+    for o in range(y.shape[1]):
+        g = y[:, o].sum()
+        for _ in range(order):
+            d = torch.autograd.grad(g, xr, create_graph=True)[0]
+            g = d.sum()
+        cols.append(d.sum(1))
+    return torch.stack(cols, 1)
+
+
+@pytest.mark.parametrize("B,I,O,deg,order", [
+    (64, 8, 6, 14, 3),      # degree 17 derivative layer: the row-by-row operator
+    (100, 12, 10, 20, 1),   # degree 20 layer (vector-ALU forward)
+    (50, 6, 5, 40, 2),
+])
+def test_long_derivative_series_fp32(B, I, O, deg, order):
+    """Past degree + order 16 the derivative coefficients come from the
+    row-by-row device operator and the derivative layer runs the vector-ALU
+    forward: values, coefficient and input gradients, and the Jacobian."""
+    print(f"long derivative series B={B} I={I} O={O} deg={deg} order={order}", flush=True)
+    torch.manual_seed(B + deg)
+    layer = kan_amd.ChebyKANLayer(I, O, deg).cuda()
+    x = _inputs(deg, B, I)
+    got = layer.compute_derivatives(x.cuda(), order=order)
+    c64 = layer.cheby_coeffs.detach().cpu().double()
+    ref = do.derivatives(x, c64, order)
+    assert _rel(got, ref) <= FP32_TOL
+    # coefficient gradient of sum(w * derivative): the adjoint operator
+    w = torch.randn(B, O, generator=torch.Generator().manual_seed(1))
+    layer.cheby_coeffs.grad = None
+    (layer.compute_derivatives(x.cuda(), order=order) * w.cuda()).sum().backward()
+    cr = c64.clone().requires_grad_(True)
+    (_derivatives_graph(x, cr, order) * w.double()).sum().backward()
+    assert _rel(layer.cheby_coeffs.grad, cr.grad) <= FP32_TOL
+    if order == 1 or deg + 1 > 16:
+        jac = layer.jacobian(x.cuda())
+        xr = x.double().requires_grad_(True)
+        yr = do.chebykan_forward64(xr, c64)
+        jr = torch.stack([torch.autograd.grad(yr[:, o].sum(), xr, retain_graph=True)[0]
+                          for o in range(O)], 1)
+        assert _rel(jac, jr) <= FP32_TOL
+
+
 def test_derivative_errors():
-    layer = kan_amd.ChebyKANLayer(8, 4, 14).cuda()
     x = torch.randn(10, 8, device="cuda")
-    with pytest.raises(_lib.CkanError) as e:
-        layer.compute_derivatives(x, order=3)  # degree 17 derivative layer
-    assert e.value.code == _lib.CKAN_ERR_UNSUPPORTED
     with pytest.raises(ValueError):
-        layer.compute_derivatives(x, order=-1)
-    with pytest.raises(_lib.CkanError) as e:  # the order-1 series of degree 17
-        kan_amd.ChebyKANLayer(8, 4, 16).cuda().jacobian(x)
+        kan_amd.ChebyKANLayer(8, 4, 14).cuda().compute_derivatives(x, order=-1)
+    with pytest.raises(_lib.CkanError) as e:  # degree + order above 256
+        kan_amd.ChebyKANLayer(8, 4, 250).cuda().compute_derivatives(x, order=7)
+    assert e.value.code == _lib.CKAN_ERR_UNSUPPORTED
+    with pytest.raises(_lib.CkanError) as e:  # family bases stop at degree + order 16
+        kan_amd.JacobiKANLayer(8, 4, 15).cuda().compute_derivatives(x, order=2)
     assert e.value.code == _lib.CKAN_ERR_UNSUPPORTED
     layer64 = kan_amd.ChebyKANLayer(8, 4, 3).cuda().double()
     with pytest.raises(RuntimeError):

@@ -109,6 +109,24 @@ def test_derivative_matrix_rows_follow_chebder():
     np.testing.assert_array_equal(R1[0], np.zeros(deg + 2))
 
 
+@pytest.mark.parametrize("deg,order", [(12, 5), (30, 2), (64, 3)])
+def test_derivative_matrix_long_series_follow_chebder(deg, order):
+    """Past degree + order 16 (the operator the GPU row kernels apply): row n
+    of R is (1 - t^2) d/dt applied `order` times to T_n, checked through
+    numpy's chebder / chebmulx in fp64, relative to each row's size."""
+    R = _lib.derivative_matrix(None, deg, order)
+    assert R.shape == (deg + 1, deg + 1 + order)
+    for n in range(deg + 1):
+        q = np.zeros(n + 1)
+        q[n] = 1.0
+        for _ in range(order):
+            d = npc.chebder(q) if len(q) > 1 else np.zeros(1)
+            q = npc.chebsub(d, npc.chebmulx(npc.chebmulx(d)))
+        expect = np.zeros(deg + 1 + order)
+        expect[:len(q)] = q[:deg + 1 + order]
+        np.testing.assert_allclose(R[n], expect, rtol=0, atol=1e-12 * max(1.0, np.abs(expect).max()))
+
+
 def test_derivative_matrix_order_zero_and_limits():
     deg = 4
     np.testing.assert_array_equal(_lib.derivative_matrix(None, deg, 0), np.eye(deg + 1))
@@ -118,7 +136,10 @@ def test_derivative_matrix_order_zero_and_limits():
         __import__("ctypes").POINTER(__import__("ctypes").c_double))))
     np.testing.assert_allclose(_lib.derivative_matrix(spec, deg, 0), M.reshape(deg + 1, deg + 1))
     with pytest.raises(_lib.CkanError) as e:
-        _lib.derivative_matrix(None, 12, 5)  # degree 17 > 16
+        _lib.derivative_matrix(None, 250, 7)  # degree + order above 256
+    assert e.value.code == _lib.CKAN_ERR_UNSUPPORTED
+    with pytest.raises(_lib.CkanError) as e:  # family bases stop at degree + order 16
+        _lib.derivative_matrix(_lib.make_spec(_lib.CKAN_BASIS_JACOBI, 12, 0.0, 0.0, 1.0), 12, 5)
     assert e.value.code == _lib.CKAN_ERR_UNSUPPORTED
     with pytest.raises(_lib.CkanError) as e:
         _lib.derivative_matrix(None, 4, -1)
