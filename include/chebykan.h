@@ -61,9 +61,10 @@ typedef enum ckan_input_map {
  * batch of `batch` rows (kan/layers/chebykan.py:21-22,64).
  * Degrees 0..16 run on the MFMA kernels in the compute precision.  Degrees
  * 17..256 (the reference layer takes any degree, kan/layers/chebykan.py:21-51)
- * run on vector-ALU kernels in fp32 whatever `compute` asks, with the tanh
- * input map only; their packed buffer is C widened to fp32 in its own
- * [in, out, D] layout and they need no workspace (the size queries return 0). */
+ * run on vector-ALU kernels in fp32 whatever `compute` asks, with either input
+ * map; their packed buffer is C widened to fp32 in its own [in, out, D]
+ * layout followed by the basis recurrence block, and they need no workspace
+ * (the size queries return 0). */
 typedef struct ckan_desc {
   int64_t batch;        /* B: rows of x after x.view(-1, in_dim)          */
   int32_t in_dim;       /* I                                               */
@@ -169,6 +170,12 @@ int ckan_backward_f64(const ckan_desc* desc, const double* t_cache, const double
  * and its coefficient gradient is dC = dC' M^T; the input gradient is the
  * ChebyKAN layer's with C'.  So ckan_pack_coeffs_basis + ckan_forward +
  * ckan_backward (into dC') + ckan_coeff_grad_from_chebyshev run such a layer.
+ * Above degree 16 (the vector-ALU kernels) the packed buffer carries the
+ * family's recurrence instead of C M: the kernels evaluate P_n(s u) by the
+ * recurrence and differentiate it, ckan_backward's dC is already the family
+ * coefficients' gradient and ckan_coeff_grad_from_chebyshev is the identity
+ * (a copy, an accumulation, or nothing in place), so the same four calls
+ * serve every degree.
  * Families and the reference code each replaces:
  *   JACOBI     P_n^(alpha,beta), alpha, beta > -1, s = 1: JacobiBasis
  *              (kan/basis/jacobi.py:84-117,147-188), JacobiKANLayer
@@ -187,7 +194,9 @@ typedef enum ckan_basis_family {
 
 typedef struct ckan_basis_spec {
   int32_t family;   /* ckan_basis_family                                      */
-  int32_t degree;   /* 0..16; equal to desc->degree where a desc is passed too */
+  int32_t degree;   /* 0..256 (0..16 for ckan_basis_to_chebyshev and the
+                       derivative entry points); equal to desc->degree where a
+                       desc is passed too */
   double alpha;     /* Jacobi parameters (> -1); ignored by the other families */
   double beta;
   double scale;     /* s: the basis is evaluated at s * tanh(x) (finite)       */
@@ -196,15 +205,17 @@ typedef struct ckan_basis_spec {
 /* Host only: M as (degree+1)^2 doubles, M[n * (degree+1) + k]. */
 int ckan_basis_to_chebyshev(const ckan_basis_spec* spec, double* M);
 /* ckan_pack_coeffs of C' = C M, for C in the family's basis (fp32 or bf16 per
- * desc->coeff_dtype).  M is built on the host and passed by value. */
+ * desc->coeff_dtype).  M is built on the host and passed by value.  Above
+ * degree 16: C widened to fp32 and the family's recurrence block. */
 int ckan_pack_coeffs_basis(const ckan_desc* desc, const ckan_basis_spec* spec, const void* coeffs,
                            void* packed, void* stream);
 /* dcoeffs[i, o, n] (+)= sum_k dcheb[i, o, k] M[n, k] (fp32 [in, out, D]);
- * dcheb may equal dcoeffs when accumulate == 0 (in place). */
+ * dcheb may equal dcoeffs when accumulate == 0 (in place).  Above degree 16,
+ * dcoeffs (+)= dcheb (ckan_backward's output is already in the family basis). */
 int ckan_coeff_grad_from_chebyshev(const ckan_desc* desc, const ckan_basis_spec* spec,
                                    const float* dcheb, float* dcoeffs, int accumulate, void* stream);
-/* out[q, n] = P_n(t[q]), n = 0..degree, by the family's recurrence (the
- * reference's basis_functions of an already-normalised input; s unused). */
+/* out[q, n] = P_n(t[q]), n = 0..degree (<= 256), by the family's recurrence
+ * (the reference's basis_functions of an already-normalised input; s unused). */
 int ckan_family_basis(const ckan_basis_spec* spec, const float* t, int64_t n, float* out,
                       void* stream);
 /* dt[q] = sum_n g[q, n] P_n'(t[q]): backward of ckan_family_basis. */

@@ -86,9 +86,6 @@ int validate_desc(const ckan_desc* d) {
     if (d->in_scale != 0.0f || d->in_shift != 0.0f)
       return fail(CKAN_ERR_INVALID_ARG, "in_scale/in_shift must be 0 with the tanh input map");
   } else if (d->input_map == CKAN_INPUT_AFFINE) {
-    if (d->degree > kMfmaMaxDegree)
-      return fail(CKAN_ERR_UNSUPPORTED, "the affine input map is served up to degree %d",
-                  kMfmaMaxDegree);
     if (!isfinite(d->in_scale) || !isfinite(d->in_shift) || d->in_scale == 0.0f)
       return fail(CKAN_ERR_INVALID_ARG, "affine input map needs a finite non-zero in_scale and finite in_shift");
   } else {
@@ -112,11 +109,21 @@ Plan plan_of(const ckan_desc* d) {
 }
 
 // Layers above the MFMA kernels' degree limit run on the vector-ALU kernels
-// in fp32 (whatever desc->compute asks), with C copied to fp32 in its own
-// [I, O, D] layout as the "packed" buffer and a tanh cache of row pitch I.
+// in fp32 (whatever desc->compute asks).  Their packed buffer is C copied to
+// fp32 in its own [I, O, D] layout, then (at the next 256-byte boundary) the
+// basis recurrence block; the input-map cache has row pitch I.
 inline bool valu_route(const ckan_desc* d) { return d->degree > kMfmaMaxDegree; }
 inline int64_t valu_coeffs(const ckan_desc* d) {
   return (int64_t)d->in_dim * d->out_dim * (d->degree + 1);
+}
+inline size_t valu_rec_offset(const ckan_desc* d) {
+  return align256((size_t)valu_coeffs(d) * sizeof(float));
+}
+inline float* valu_rec(const ckan_desc* d, void* packed) {
+  return reinterpret_cast<float*>(static_cast<char*>(packed) + valu_rec_offset(d));
+}
+inline const float* valu_rec(const ckan_desc* d, const void* packed) {
+  return reinterpret_cast<const float*>(static_cast<const char*>(packed) + valu_rec_offset(d));
 }
 
 // Paths that implement only the tanh input map.
@@ -184,12 +191,13 @@ int ckan::backward_impl(const ckan_desc* desc, const float* t_cache, const void*
       }
       return CKAN_OK;
     }
-    if (!t_cache || !dy || (need_dx && !packed))
-      return fail(CKAN_ERR_INVALID_ARG, "t_cache/dy/packed is NULL");
+    // packed carries the basis recurrence: required for dC as well
+    if (!t_cache || !dy || !packed) return fail(CKAN_ERR_INVALID_ARG, "t_cache/dy/packed is NULL");
     ProfScope ps("bwd_valu", s);
     launch_backward_valu<float>(t_cache, static_cast<const float*>(packed), dy, dx, dcoeffs, om,
-                                desc->batch, desc->in_dim, desc->out_dim,
-                                desc->degree, s);
+                                desc->batch, desc->in_dim, desc->out_dim, desc->degree, s,
+                                packed ? valu_rec(desc, packed) : nullptr, desc->input_map,
+                                desc->in_scale);
     return check_launch("backward (vector ALU)");
   }
   const Plan p = plan_of(desc);
@@ -257,7 +265,8 @@ const char* ckan_version(void) { return "kan_amd-chebykan 0.1.0 (gfx950)"; }
 
 size_t ckan_packed_bytes(const ckan_desc* desc) {
   if (validate_desc(desc) != CKAN_OK) return 0;
-  if (valu_route(desc)) return align256((size_t)valu_coeffs(desc) * sizeof(float));
+  if (valu_route(desc))
+    return valu_rec_offset(desc) + align256((size_t)recur_floats(desc->degree) * sizeof(float));
   return packed_bytes(plan_of(desc));
 }
 
@@ -298,10 +307,11 @@ int ckan_pack_coeffs(const ckan_desc* desc, const void* coeffs, void* packed, vo
   if (!coeffs || !packed) return fail(CKAN_ERR_INVALID_ARG, "coeffs/packed is NULL");
   if (!aligned16(packed)) return fail(CKAN_ERR_INVALID_ARG, "packed buffer must be 16-byte aligned");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  if (valu_route(desc)) {
+  if (valu_route(desc)) {  // C in fp32 and the Chebyshev recurrence block
     ProfScope ps("pack", s);
     launch_to_f32(coeffs, desc->coeff_dtype == CKAN_DTYPE_BF16, static_cast<float*>(packed),
                   valu_coeffs(desc), s);
+    launch_write_recur(valu_rec(desc, packed), CKAN_BASIS_CHEBYSHEV, 0.0, 0.0, desc->degree, 1.0f, s);
     return check_launch("pack_coeffs");
   }
   const Plan p = plan_of(desc);
@@ -323,7 +333,9 @@ int ckan_forward(const ckan_desc* desc, const float* x, const void* packed, floa
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     ProfScope ps("fwd_valu", s);
     launch_forward_valu<float>(x, static_cast<const float*>(packed), y, t_cache, desc->batch,
-                               desc->in_dim, desc->out_dim, desc->degree, s);
+                               desc->in_dim, desc->out_dim, desc->degree, s,
+                               valu_rec(desc, packed), desc->input_map, desc->in_scale,
+                               desc->in_shift);
     return check_launch("forward (vector ALU)");
   }
   const Plan p = plan_of(desc);
@@ -365,6 +377,7 @@ int ckan_forward_noalloc(const ckan_desc* desc, const float* x, const void* pack
 
 namespace {
 int family_xform(const ckan_basis_spec* spec, int degree, BasisXform* xf);
+int family_valid(const ckan_basis_spec* spec, int degree);
 }
 
 int ckan_pack_forward(const ckan_desc* desc, const ckan_basis_spec* spec, const void* coeffs,
@@ -372,14 +385,16 @@ int ckan_pack_forward(const ckan_desc* desc, const ckan_basis_spec* spec, const 
                       size_t ws_bytes, void* stream) {
   int rc = validate_desc(desc);
   if (rc) return rc;
+  if (valu_route(desc)) {
+    rc = spec ? ckan_pack_coeffs_basis(desc, spec, coeffs, packed, stream)
+              : ckan_pack_coeffs(desc, coeffs, packed, stream);
+    if (rc) return rc;
+    return ckan_forward(desc, x, packed, y, t_cache, ws, ws_bytes, stream);
+  }
   BasisXform xf;
   if (spec && (rc = family_xform(spec, desc->degree, &xf))) return rc;
   if (!coeffs || !packed) return fail(CKAN_ERR_INVALID_ARG, "coeffs/packed is NULL");
   if (!aligned16(packed)) return fail(CKAN_ERR_INVALID_ARG, "packed buffer must be 16-byte aligned");
-  if (valu_route(desc)) {  // spec is NULL here: family_xform serves degree <= 16 only
-    if ((rc = ckan_pack_coeffs(desc, coeffs, packed, stream))) return rc;
-    return ckan_forward(desc, x, packed, y, t_cache, ws, ws_bytes, stream);
-  }
   const Plan p = plan_of(desc);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const bool cbf = desc->coeff_dtype == CKAN_DTYPE_BF16;
@@ -504,6 +519,20 @@ int family_of(const ckan_basis_spec* spec, int degree, double* a, double* b, dou
   return CKAN_OK;
 }
 
+// Validates a basis spec of a layer of degree `degree` up to the vector-ALU
+// path's limit (the recurrence-block form of the basis has no matrix).
+int family_valid(const ckan_basis_spec* spec, int degree) {
+  if (!spec) return fail(CKAN_ERR_INVALID_ARG, "basis spec is NULL");
+  if (spec->degree != degree)
+    return fail(CKAN_ERR_INVALID_ARG, "basis degree %d != layer degree %d", spec->degree, degree);
+  if (!isfinite(spec->scale)) return fail(CKAN_ERR_INVALID_ARG, "basis scale must be finite");
+  double a, b, c;
+  if (!recur_coef(spec->family, 0, spec->alpha, spec->beta, &a, &b, &c))
+    return fail(CKAN_ERR_INVALID_ARG, "invalid basis family %d or parameters (alpha=%g, beta=%g; "
+                "Jacobi needs alpha, beta > -1)", spec->family, spec->alpha, spec->beta);
+  return CKAN_OK;
+}
+
 int family_xform(const ckan_basis_spec* spec, int degree, BasisXform* xf) {
   double a[kMaxD], b[kMaxD], c[kMaxD];
   int rc = family_of(spec, degree, a, b, c);
@@ -517,17 +546,6 @@ int family_xform(const ckan_basis_spec* spec, int degree, BasisXform* xf) {
   return CKAN_OK;
 }
 
-int family_recur(const ckan_basis_spec* spec, Recur3* r) {
-  double a[kMaxD], b[kMaxD], c[kMaxD];
-  int rc = family_of(spec, -1, a, b, c);
-  if (rc) return rc;
-  for (int n = 0; n < kMaxD; ++n) {
-    r->a[n] = (float)a[n];
-    r->b[n] = (float)b[n];
-    r->c[n] = (float)c[n];
-  }
-  return CKAN_OK;
-}
 }  // namespace
 
 int ckan_basis_to_chebyshev(const ckan_basis_spec* spec, double* M) {
@@ -543,12 +561,23 @@ int ckan_pack_coeffs_basis(const ckan_desc* desc, const ckan_basis_spec* spec, c
                            void* packed, void* stream) {
   int rc = validate_desc(desc);
   if (rc) return rc;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (valu_route(desc)) {  // C in fp32 and the family's recurrence block
+    if ((rc = family_valid(spec, desc->degree))) return rc;
+    if (!coeffs || !packed) return fail(CKAN_ERR_INVALID_ARG, "coeffs/packed is NULL");
+    if (!aligned16(packed)) return fail(CKAN_ERR_INVALID_ARG, "packed buffer must be 16-byte aligned");
+    ProfScope ps("pack", s);
+    launch_to_f32(coeffs, desc->coeff_dtype == CKAN_DTYPE_BF16, static_cast<float*>(packed),
+                  valu_coeffs(desc), s);
+    launch_write_recur(valu_rec(desc, packed), spec->family, spec->alpha, spec->beta, desc->degree,
+                       (float)spec->scale, s);
+    return check_launch("pack_coeffs_basis");
+  }
   BasisXform xf;
   if ((rc = family_xform(spec, desc->degree, &xf))) return rc;
   if (!coeffs || !packed) return fail(CKAN_ERR_INVALID_ARG, "coeffs/packed is NULL");
   if (!aligned16(packed)) return fail(CKAN_ERR_INVALID_ARG, "packed buffer must be 16-byte aligned");
   const Plan p = plan_of(desc);
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   ProfScope ps("pack", s);
   launch_pack(coeffs, desc->coeff_dtype == CKAN_DTYPE_BF16, packed, p, s, &xf);
   return check_launch("pack_coeffs_basis");
@@ -558,13 +587,25 @@ int ckan_coeff_grad_from_chebyshev(const ckan_desc* desc, const ckan_basis_spec*
                                    const float* dcheb, float* dcoeffs, int accumulate, void* stream) {
   int rc = validate_desc(desc);
   if (rc) return rc;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (valu_route(desc)) {
+    // the vector-ALU backward already differentiates in the family's basis:
+    // the map is the identity (a copy, an accumulation, or nothing in place)
+    if ((rc = family_valid(spec, desc->degree))) return rc;
+    if (!dcheb || !dcoeffs) return fail(CKAN_ERR_INVALID_ARG, "dcheb/dcoeffs is NULL");
+    if (dcheb == dcoeffs && accumulate)
+      return fail(CKAN_ERR_INVALID_ARG, "in-place transform (dcheb == dcoeffs) cannot accumulate");
+    if (dcheb == dcoeffs) return CKAN_OK;
+    ProfScope ps("coeff_from_cheb", s);
+    launch_to_f32(dcheb, false, dcoeffs, valu_coeffs(desc), s, accumulate != 0);
+    return check_launch("coeff_grad_from_chebyshev");
+  }
   BasisXform xf;
   if ((rc = family_xform(spec, desc->degree, &xf))) return rc;
   if (!dcheb || !dcoeffs) return fail(CKAN_ERR_INVALID_ARG, "dcheb/dcoeffs is NULL");
   if (dcheb == dcoeffs && accumulate)
     return fail(CKAN_ERR_INVALID_ARG, "in-place transform (dcheb == dcoeffs) cannot accumulate");
   const Plan p = plan_of(desc);
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   ProfScope ps("coeff_from_cheb", s);
   launch_coeff_from_cheb(dcheb, dcoeffs, p, accumulate != 0, xf, s);
   return check_launch("coeff_grad_from_chebyshev");
@@ -708,29 +749,34 @@ int ckan_jacobian(const ckan_desc* desc, const ckan_basis_spec* spec, const floa
 
 int ckan_family_basis(const ckan_basis_spec* spec, const float* t, int64_t n, float* out,
                       void* stream) {
-  Recur3 r;
-  int rc = family_recur(spec, &r);
+  int rc = family_valid(spec, spec ? spec->degree : 0);
   if (rc) return rc;
+  if (spec->degree < 0 || spec->degree > kValuMaxDegree)
+    return fail(spec->degree < 0 ? CKAN_ERR_INVALID_ARG : CKAN_ERR_UNSUPPORTED,
+                "basis degree %d outside 0..%d", spec->degree, kValuMaxDegree);
   if (n < 0) return fail(CKAN_ERR_INVALID_ARG, "n must be >= 0");
   if (n == 0) return CKAN_OK;
   if (!t || !out) return fail(CKAN_ERR_INVALID_ARG, "t/out is NULL");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   ProfScope ps("basis", s);
-  launch_basis_family(t, n, spec->degree, r, out, s);
+  launch_basis_family(t, n, spec->degree, spec->family, spec->alpha, spec->beta, out, s);
   return check_launch("family_basis");
 }
 
 int ckan_family_basis_backward(const ckan_basis_spec* spec, const float* t, const float* g,
                                int64_t n, float* dt, void* stream) {
-  Recur3 r;
-  int rc = family_recur(spec, &r);
+  int rc = family_valid(spec, spec ? spec->degree : 0);
   if (rc) return rc;
+  if (spec->degree < 0 || spec->degree > kValuMaxDegree)
+    return fail(spec->degree < 0 ? CKAN_ERR_INVALID_ARG : CKAN_ERR_UNSUPPORTED,
+                "basis degree %d outside 0..%d", spec->degree, kValuMaxDegree);
   if (n < 0) return fail(CKAN_ERR_INVALID_ARG, "n must be >= 0");
   if (n == 0) return CKAN_OK;
   if (!t || !g || !dt) return fail(CKAN_ERR_INVALID_ARG, "t/g/dt is NULL");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   ProfScope ps("basis_bwd", s);
-  launch_basis_family_bwd(t, g, n, spec->degree, r, dt, s);
+  launch_basis_family_bwd(t, g, n, spec->degree, spec->family, spec->alpha, spec->beta, dt,
+                          s);
   return check_launch("family_basis_backward");
 }
 

@@ -19,40 +19,85 @@ namespace ckan {
 // Recurrences of kan/basis/jacobi.py:147-188 (P^(alpha,beta)_n, written as
 // (a_n t + b_n) P_{n-1} - c_n P_{n-2}), kan/basis/hermite.py:158-193
 // (physicists' H_n) and :195-233 (probabilists' He_n), and T_n itself.
-bool family_recurrence(int family, int degree, double alpha, double beta, double* a, double* b,
-                       double* c) {
-  if (degree < 0 || degree >= kMaxD) return false;
-  for (int n = 0; n < kMaxD; ++n) a[n] = b[n] = c[n] = 0.0;
+// P_n = (a_n t + b_n) P_{n-1} - c_n P_{n-2} (n >= 1, c_1 = 0): the
+// coefficients of degree n of a ckan_basis_family (host and device; the
+// families' standard recurrences).  False for an unknown family or invalid
+// Jacobi parameters.
+__host__ __device__ bool recur_coef(int family, int n, double alpha, double beta, double* a,
+                                    double* b, double* c) {
+  *a = *b = *c = 0.0;
+  if (family == CKAN_BASIS_JACOBI &&
+      (!(alpha > -1.0) || !(beta > -1.0) || !isfinite(alpha) || !isfinite(beta)))
+    return false;
+  if (family != CKAN_BASIS_CHEBYSHEV && family != CKAN_BASIS_JACOBI &&
+      family != CKAN_BASIS_HERMITE && family != CKAN_BASIS_HERMITE_E)
+    return false;
+  if (n < 1) return true;
   switch (family) {
     case CKAN_BASIS_CHEBYSHEV:
-      a[1] = 1.0;
-      for (int n = 2; n <= degree; ++n) { a[n] = 2.0; c[n] = 1.0; }
+      *a = n == 1 ? 1.0 : 2.0;
+      *c = n == 1 ? 0.0 : 1.0;
       return true;
     case CKAN_BASIS_JACOBI: {
-      if (!(alpha > -1.0) || !(beta > -1.0) || !isfinite(alpha) || !isfinite(beta)) return false;
       const double ab = alpha + beta;
-      a[1] = (ab + 2.0) / 2.0;
-      b[1] = (alpha - beta) / 2.0;
-      for (int n = 2; n <= degree; ++n) {
-        const double ct = 2.0 * n + ab - 1.0;
-        const double den = 2.0 * n * (n + ab) * (2.0 * n + ab - 2.0);
-        a[n] = ct * (2.0 * n + ab) * (2.0 * n + ab - 2.0) / den;
-        b[n] = ct * (alpha * alpha - beta * beta) / den;
-        c[n] = 2.0 * (n + alpha - 1.0) * (n + beta - 1.0) * (2.0 * n + ab) / den;
+      if (n == 1) {
+        *a = (ab + 2.0) / 2.0;
+        *b = (alpha - beta) / 2.0;
+        return true;
       }
+      const double ct = 2.0 * n + ab - 1.0;
+      const double den = 2.0 * n * (n + ab) * (2.0 * n + ab - 2.0);
+      *a = ct * (2.0 * n + ab) * (2.0 * n + ab - 2.0) / den;
+      *b = ct * (alpha * alpha - beta * beta) / den;
+      *c = 2.0 * (n + alpha - 1.0) * (n + beta - 1.0) * (2.0 * n + ab) / den;
       return true;
     }
     case CKAN_BASIS_HERMITE:
-      a[1] = 2.0;
-      for (int n = 2; n <= degree; ++n) { a[n] = 2.0; c[n] = 2.0 * (n - 1); }
+      *a = 2.0;
+      *c = n == 1 ? 0.0 : 2.0 * (n - 1);
       return true;
     case CKAN_BASIS_HERMITE_E:
-      a[1] = 1.0;
-      for (int n = 2; n <= degree; ++n) { a[n] = 1.0; c[n] = (double)(n - 1); }
+      *a = 1.0;
+      *c = n == 1 ? 0.0 : (double)(n - 1);
       return true;
     default:
       return false;
   }
+}
+
+bool family_recurrence(int family, int degree, double alpha, double beta, double* a, double* b,
+                       double* c) {
+  if (degree < 0 || degree >= kMaxD) return false;
+  for (int n = 0; n < kMaxD; ++n) a[n] = b[n] = c[n] = 0.0;
+  for (int n = 1; n <= degree; ++n)
+    if (!recur_coef(family, n, alpha, beta, a + n, b + n, c + n)) return false;
+  return recur_coef(family, 0, alpha, beta, a, b, c);  // also checks the family at degree 0
+}
+
+// The recurrence block of a vector-ALU packed buffer: a[D], b[D], c[D], the
+// basis scale s (P_n is evaluated at s * t) and the kind: 0 for the Chebyshev
+// basis at scale 1 (the kernels' specialised recurrence), 1 otherwise.
+__global__ void k_write_recur(float* __restrict__ rec, int family, double alpha, double beta, int D,
+                              float scale) {
+  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  if (n < D) {
+    double a, b, c;
+    recur_coef(family, n, alpha, beta, &a, &b, &c);
+    rec[n] = (float)a;
+    rec[D + n] = (float)b;
+    rec[2 * D + n] = (float)c;
+  }
+  if (n == 0) {
+    rec[3 * D] = scale;
+    rec[3 * D + 1] = (family == CKAN_BASIS_CHEBYSHEV && scale == 1.0f) ? 0.0f : 1.0f;
+  }
+}
+
+void launch_write_recur(float* rec, int family, double alpha, double beta, int degree, float scale,
+                        hipStream_t s) {
+  const int D = degree + 1;
+  hipLaunchKernelGGL(k_write_recur, dim3((unsigned)((D + 255) / 256)), dim3(256), 0, s, rec, family,
+                     alpha, beta, D, scale);
 }
 
 // The recurrence run on Chebyshev coefficient vectors: multiplication by u is
@@ -233,19 +278,36 @@ k_coeff_from_cheb(const float* dcheb, float* dc, int64_t rows, int D, int accumu
   }
 }
 
+// The recurrence coefficients a_n, b_n, c_n (n <= deg) of a family into LDS,
+// rounded to fp32 once per block; ends with the block's barrier.
+__device__ __forceinline__ void stage_family(float* ra, float* rb, float* rc, int deg, int family,
+                                             double alpha, double beta) {
+  for (int k = threadIdx.x; k <= deg; k += blockDim.x) {
+    double a, b, c;
+    recur_coef(family, k, alpha, beta, &a, &b, &c);
+    ra[k] = (float)a;
+    rb[k] = (float)b;
+    rc[k] = (float)c;
+  }
+  __syncthreads();
+}
+
 // out[q, n] = P_n(t[q]) by the family's recurrence, n = 0..deg.
 __global__ void __launch_bounds__(256)
-k_basis_family(const float* __restrict__ t, int64_t n, int deg, Recur3 r, float* __restrict__ out) {
+k_basis_family(const float* __restrict__ t, int64_t n, int deg, int family, double alpha,
+               double beta, float* __restrict__ out) {
+  __shared__ float ra[kValuMaxDegree + 1], rb[kValuMaxDegree + 1], rc[kValuMaxDegree + 1];
+  stage_family(ra, rb, rc, deg, family, alpha, beta);
   for (int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; q < n;
        q += (int64_t)gridDim.x * blockDim.x) {
     const float tv = t[q];
     float* o = out + q * (deg + 1);
     o[0] = 1.0f;
     if (deg < 1) continue;
-    float p0 = 1.0f, p1 = fmaf(r.a[1], tv, r.b[1]);
+    float p0 = 1.0f, p1 = fmaf(ra[1], tv, rb[1]);
     o[1] = p1;
     for (int d = 2; d <= deg; ++d) {
-      const float pn = fmaf(fmaf(r.a[d], tv, r.b[d]), p1, -r.c[d] * p0);
+      const float pn = fmaf(fmaf(ra[d], tv, rb[d]), p1, -rc[d] * p0);
       o[d] = pn;
       p0 = p1;
       p1 = pn;
@@ -257,20 +319,22 @@ k_basis_family(const float* __restrict__ t, int64_t n, int deg, Recur3 r, float*
 // P_n' = a_n P_{n-1} + (a_n t + b_n) P_{n-1}' - c_n P_{n-2}'.
 __global__ void __launch_bounds__(256)
 k_basis_family_bwd(const float* __restrict__ t, const float* __restrict__ g, int64_t n, int deg,
-                   Recur3 r, float* __restrict__ dt) {
+                   int family, double alpha, double beta, float* __restrict__ dt) {
+  __shared__ float ra[kValuMaxDegree + 1], rb[kValuMaxDegree + 1], rc[kValuMaxDegree + 1];
+  stage_family(ra, rb, rc, deg, family, alpha, beta);
   for (int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; q < n;
        q += (int64_t)gridDim.x * blockDim.x) {
     const float tv = t[q];
     const float* gq = g + q * (deg + 1);
     float s = 0.0f;
     if (deg >= 1) {
-      float p0 = 1.0f, p1 = fmaf(r.a[1], tv, r.b[1]);  // P_{n-2}, P_{n-1}
-      float d0 = 0.0f, d1 = r.a[1];                     // their derivatives
+      float p0 = 1.0f, p1 = fmaf(ra[1], tv, rb[1]);  // P_{n-2}, P_{n-1}
+      float d0 = 0.0f, d1 = ra[1];                    // their derivatives
       s = gq[1] * d1;
       for (int d = 2; d <= deg; ++d) {
-        const float lin = fmaf(r.a[d], tv, r.b[d]);
-        const float pn = fmaf(lin, p1, -r.c[d] * p0);
-        const float dn = fmaf(r.a[d], p1, fmaf(lin, d1, -r.c[d] * d0));
+        const float lin = fmaf(ra[d], tv, rb[d]);
+        const float pn = fmaf(lin, p1, -rc[d] * p0);
+        const float dn = fmaf(ra[d], p1, fmaf(lin, d1, -rc[d] * d0));
         s = fmaf(gq[d], dn, s);
         p0 = p1; p1 = pn;
         d0 = d1; d1 = dn;
@@ -463,14 +527,16 @@ void launch_jacobian(const float* x, const float* c1t, float* jac, int64_t B, in
   }
 }
 
-void launch_basis_family(const float* t, int64_t n, int deg, const Recur3& r, float* out,
-                         hipStream_t s) {
-  hipLaunchKernelGGL(k_basis_family, dim3(grid_of(n)), dim3(256), 0, s, t, n, deg, r, out);
+void launch_basis_family(const float* t, int64_t n, int deg, int family, double alpha,
+                         double beta, float* out, hipStream_t s) {
+  hipLaunchKernelGGL(k_basis_family, dim3(grid_of(n)), dim3(256), 0, s, t, n, deg, family, alpha,
+                     beta, out);
 }
 
-void launch_basis_family_bwd(const float* t, const float* g, int64_t n, int deg, const Recur3& r,
-                             float* dt, hipStream_t s) {
-  hipLaunchKernelGGL(k_basis_family_bwd, dim3(grid_of(n)), dim3(256), 0, s, t, g, n, deg, r, dt);
+void launch_basis_family_bwd(const float* t, const float* g, int64_t n, int deg, int family,
+                             double alpha, double beta, float* dt, hipStream_t s) {
+  hipLaunchKernelGGL(k_basis_family_bwd, dim3(grid_of(n)), dim3(256), 0, s, t, g, n, deg, family,
+                     alpha, beta, dt);
 }
 
 }  // namespace ckan

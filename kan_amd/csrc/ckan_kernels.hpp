@@ -70,25 +70,27 @@ BwdLayout bwd_layout(const Plan& p, bool need_dx, bool need_dc);
 
 // ---- other polynomial bases expressed in the Chebyshev basis --------------
 constexpr int kMaxD = 17;  // degree <= 16
-// Three-term recurrence: P_0 = 1, P_1 = a[1] t + b[1],
-// P_n = (a[n] t + b[n]) P_{n-1} - c[n] P_{n-2}  (n >= 2).
-struct Recur3 { float a[kMaxD], b[kMaxD], c[kMaxD]; };
 // Change of basis P_n(s u) = sum_k m[n * kMaxD + k] T_k(u), zero-padded.
 struct BasisXform { float m[kMaxD * kMaxD]; };
 // Recurrence coefficients (double) of a ckan_basis_family; false if the
 // family or its parameters are invalid.
 bool family_recurrence(int family, int degree, double alpha, double beta, double* a, double* b,
                        double* c);
+// The coefficients of degree n alone (a = b = c = 0 for n = 0); false as above.
+__host__ __device__ bool recur_coef(int family, int n, double alpha, double beta, double* a,
+                                    double* b, double* c);
 // M[n * (degree + 1) + k] with P_n(scale u) = sum_k M[n, k] T_k(u) (exact, fp64).
 void family_to_chebyshev(const double* a, const double* b, const double* c, int degree,
                          double scale, double* M);
 // dc[q, n] (+)= sum_k dcheb[q, k] m[n][k] over the I*O rows q; dcheb may be dc.
 void launch_coeff_from_cheb(const float* dcheb, float* dc, const Plan& p, bool accumulate,
                             const BasisXform& xf, hipStream_t s);
-void launch_basis_family(const float* t, int64_t n, int deg, const Recur3& r, float* out,
-                         hipStream_t s);
-void launch_basis_family_bwd(const float* t, const float* g, int64_t n, int deg, const Recur3& r,
-                             float* dt, hipStream_t s);
+// out[q, n] = P_n(t[q]) (n <= deg <= kValuMaxDegree) and its backward; the
+// recurrence coefficients are formed on the device (recur_coef).
+void launch_basis_family(const float* t, int64_t n, int deg, int family, double alpha,
+                         double beta, float* out, hipStream_t s);
+void launch_basis_family_bwd(const float* t, const float* g, int64_t n, int deg, int family,
+                             double alpha, double beta, float* dt, hipStream_t s);
 
 // ---- derivatives of a layer's univariate functions w.r.t. its input ---------
 // f(x) = sum_k c_k T_k(tanh x) has d/dx f = (1 - t^2) f'(t): again a Chebyshev
@@ -113,18 +115,29 @@ void launch_jacobian(const float* x, const float* c1t, float* jac, int64_t B, in
 
 // ---- vector-ALU path (ckan_valu.hip): any degree, T = float or double ------
 // Serves fp64 layers and fp32 layers above kMfmaMaxDegree, with C in its own
-// [I, O, D] layout; t = tanh(x) is [B, I].
+// [I, O, D] layout; t = input map of x, [B, I].  rec (fp32 only): the packed
+// buffer's recurrence block (a[D], b[D], c[D], scale, kind); nullptr (and
+// kind 0) selects the Chebyshev kernels' specialised recurrence.
 constexpr int kMfmaMaxDegree = 16;   // the packed MFMA kernels' limit
 constexpr int kValuMaxDegree = 256;  // the vector-ALU path's limit
 template <typename T>
-void launch_forward_valu(const T* x, const T* C, T* y, T* t, int64_t B, int I, int O,
-                         int deg, hipStream_t s);
+void launch_forward_valu(const T* x, const T* C, T* y, T* t, int64_t B, int I, int O, int deg,
+                         hipStream_t s, const float* rec = nullptr, int imap = 0, float ima = 0.0f,
+                         float imb = 0.0f);
 // dC written by mode om.mode (for T = double: store or accumulate only).
 template <typename T>
 void launch_backward_valu(const T* t, const T* C, const T* dy, T* dx, T* dC, DcOut om, int64_t B,
-                          int I, int O, int deg, hipStream_t s);
-// dst[q] = float(src[q]) for q < n, src fp32 or bf16.
-void launch_to_f32(const void* src, bool src_bf16, float* dst, int64_t n, hipStream_t s);
+                          int I, int O, int deg, hipStream_t s, const float* rec = nullptr,
+                          int imap = 0, float ima = 0.0f);
+// The recurrence block (a[D], b[D], c[D], scale, kind) of a ckan_basis_family.
+void launch_write_recur(float* rec, int family, double alpha, double beta, int degree, float scale,
+                        hipStream_t s);
+// dst[q] = float(src[q]) (accumulate: dst[q] += float(src[q])) for q < n, src
+// fp32 or bf16.
+void launch_to_f32(const void* src, bool src_bf16, float* dst, int64_t n, hipStream_t s,
+                   bool accumulate = false);
+// Floats of the recurrence block of a layer of degree `degree`.
+inline int64_t recur_floats(int degree) { return 3 * (int64_t)(degree + 1) + 2; }
 
 // ---- launchers -------------------------------------------------------------
 void launch_tanh(const float* x, float* t, const Plan& p, hipStream_t s);

@@ -1,50 +1,91 @@
 // The ChebyKAN layer on the vector ALU, for any degree, in fp32 or fp64:
-//   forward  y[b, o]     = sum_{i, d} T_d(t[b, i]) C[i, o, d],  t = tanh(x)
-//   dx       dx[b, i]    = (1 - t^2) sum_d G[b, i, d] d U_{d-1}(t),
+//   forward  y[b, o]     = sum_{i, d} P_d(t[b, i]) C[i, o, d],  t = tanh(x)
+//   dx       dx[b, i]    = t'(x) sum_d G[b, i, d] P_d'(t),
 //                          G[b, i, d] = sum_o dy[b, o] C[i, o, d]
-//   dC       dC[i, o, d] = sum_b T_d(t[b, i]) dy[b, o]
+//   dC       dC[i, o, d] = sum_b P_d(t[b, i]) dy[b, o]
+// with P_d = T_d (the Chebyshev kernels, fp32 and fp64) or, in fp32, any
+// basis of a three-term recurrence P_d = (a_d u + b_d) P_{d-1} - c_d P_{d-2}
+// at u = s t (the Jacobi and Hermite layers, kan/basis/jacobi.py:131-188,
+// kan/basis/hermite.py:158-233), whose coefficients come from the packed
+// buffer's recurrence block.  t = tanh(x), or the affine map a x + b of a
+// finite-domain Hermite layer (kan/basis/hermite.py:102-112).
 // It serves the fp64 layer (the reference computes in fp64 when its
 // parameter is fp64: kan/layers/chebykan.py:48-51 after .double()) and fp32
-// layers above the MFMA kernels' degree 16 (the reference layer takes any
+// layers above the MFMA kernels' degree 16 (the reference layers take any
 // degree, kan/layers/chebykan.py:21-51).  Register-tiled kernels with LDS
 // staging read C in its own [I, O, D] layout.  The degree axis is taken in
 // chunks of at most DM degrees (one launch each; DM = 3, 5, 9 or 17, the
-// smallest that holds D, and 17 above): a chunk starting at d0
-// first advances the recurrence to T_{d0-1}, T_{d0} (or U_{d0-2}, U_{d0-1}),
-// so register arrays stay bounded for any degree.  t = tanh(x) is [B, I].
+// smallest that holds D, and 17 above): a chunk starting at d0 first advances
+// the recurrences to degree d0, so register arrays stay bounded for any
+// degree.  t is [B, I].
 #include "ckan_kernels.hpp"
 
 #include <math.h>
 
 namespace ckan {
 
-constexpr int kValuDM = 17;  // degrees per chunk above degree 16
+constexpr int kValuDM = 17;                               // degrees per chunk above degree 16
+constexpr int kRecFloats = 3 * (kValuMaxDegree + 1) + 2;  // a, b, c, scale, kind
 
 template <typename T> __device__ __forceinline__ T vtanh(T x);
 template <> __device__ __forceinline__ float vtanh<float>(float x) { return tanhf(x); }
 template <> __device__ __forceinline__ double vtanh<double>(double x) { return tanh(x); }
 
+// t = tanh(x), or ima x + imb with the affine map.
 template <typename T>
 __global__ void __launch_bounds__(256)
-k_tanh_v(const T* __restrict__ x, T* __restrict__ t, int64_t n) {
+k_tanh_v(const T* __restrict__ x, T* __restrict__ t, int64_t n, int imap, float ima, float imb) {
   for (int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; q < n;
        q += (int64_t)gridDim.x * blockDim.x)
-    t[q] = vtanh<T>(x[q]);
+    t[q] = imap ? fma((T)ima, x[q], (T)imb) : vtanh<T>(x[q]);
 }
 
-// T_{d0-1} and T_{d0} of t.  T_{-1} = t extends the recurrence
-// T_{d+1} = 2t T_d - T_{d-1} down to d = 0 (its first step gives
-// 2t - t = t = T_1 exactly), so every step below is the same FMA.
-template <typename T>
-__device__ __forceinline__ void cheb_seek(T t, int d0, T& tp, T& tc) {
-  tp = t;     // T_{-1}
-  tc = T(1);  // T_0
-  const T t2 = t + t;
-  for (int d = 0; d < d0; ++d) {
-    const T nx = fma(t2, tc, -tp);
-    tp = tc;
-    tc = nx;
+// Basis recurrences.  Chebyshev (GEN = false): T_{d+1} = 2t T_d - T_{d-1},
+// w = 2t, started from T_{-1} = t so that the first step gives 2t - t = t =
+// T_1 exactly and every step is the same FMA.  GEN: P_{d+1} = (a_{d+1} w +
+// b_{d+1}) P_d - c_{d+1} P_{d-1}, w = u = s t, started from P_{-1} = 0 (c_1 =
+// 0); rs holds a[D], b[D], c[D], s, kind (0: the Chebyshev recurrence, whose
+// specialised code the kernels then take).
+template <typename T, bool GEN>
+__device__ __forceinline__ void rec_init(T t, const float* rs, int D, T& w, T& pm, T& pc) {
+  if constexpr (GEN) {
+    w = (T)rs[3 * D] * t;
+    pm = T(0);
+  } else {
+    w = t + t;
+    pm = t;
   }
+  pc = T(1);
+}
+template <typename T, bool GEN>
+__device__ __forceinline__ void rec_step(T w, const float* rs, int D, int n, T& pm, T& pc) {
+  T nx;
+  if constexpr (GEN) {
+    // read the step's coefficients here: hoisted out of the unrolled degree
+    // loops they would hold 3 registers per degree for the whole kernel
+    asm volatile("" ::: "memory");
+    nx = fma(fma((T)rs[n], w, (T)rs[D + n]), pc, -(T)rs[2 * D + n] * pm);
+  } else {
+    nx = fma(w, pc, -pm);
+  }
+  pm = pc;
+  pc = nx;
+}
+
+// The recurrence block into LDS (fp32 with a block), before the block's
+// first barrier; after it, rec_generic tells whether the block asks for the
+// generic recurrence (a uniform branch around each tile's loops).
+template <typename T>
+__device__ __forceinline__ void stage_rec(float* rs, const float* __restrict__ rec, int D) {
+  if constexpr (sizeof(T) == 4) {
+    if (rec)
+      for (int k = threadIdx.x; k < 3 * D + 2; k += blockDim.x) rs[k] = rec[k];
+  }
+}
+template <typename T>
+__device__ __forceinline__ bool rec_generic(const float* rs, const float* rec, int D) {
+  if constexpr (sizeof(T) == 4) return rec != nullptr && rs[3 * D + 1] != 0.0f;
+  else return false;
 }
 
 // SEEK = false instantiations serve the first chunk (d0 = 0, stored, not
@@ -56,14 +97,40 @@ __device__ __forceinline__ void cheb_seek(T t, int d0, T& tp, T& tc) {
 // (r, c < 4).  Inputs are taken KI at a time: t [64][KI] and the chunk of C
 // as [KI][DM][64 outputs] in LDS.  accumulate: add to y (later chunks).
 constexpr int kValuKI = 4;
-template <typename T, int DM, bool SEEK>
-__global__ void __launch_bounds__(256)
-k_fwd_v(const T* __restrict__ t, const T* __restrict__ C, T* __restrict__ y, int64_t B, int I,
-        int O, int D, int d0_arg, int dn, int accumulate) {
+// One LDS tile of the forward (KI inputs): acc += P(t) C.
+template <typename T, int DM, bool GEN>
+__device__ __forceinline__ void fwd_tile(T (&acc)[4][4], const T (&ts)[64][kValuKI + 1],
+                                         const T (&cs)[kValuKI][DM][64], const float* rs, int D,
+                                         int d0, int dn, int tr, int to) {
+#pragma unroll
+  for (int ii = 0; ii < kValuKI; ++ii) {
+    T pm[4], pc[4], w[4];  // P_{d-1}, P_d, the recurrence's argument
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      rec_init<T, GEN>(ts[tr + 16 * r][ii], rs, D, w[r], pm[r], pc[r]);
+      for (int n = 1; n <= d0; ++n) rec_step<T, GEN>(w[r], rs, D, n, pm[r], pc[r]);
+    }
+    for (int d = 0; d < dn; ++d) {  // rolled: measured faster than unrolled here
+      T cv[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) cv[c] = cs[ii][d][to + 16 * c];
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[r][c] = fma(pc[r], cv[c], acc[r][c]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) rec_step<T, GEN>(w[r], rs, D, d0 + d + 1, pm[r], pc[r]);
+    }
+  }
+}
+
+// The forward kernel's body for one recurrence kind (uniform over the launch).
+template <typename T, int DM, bool SEEK, bool GEN>
+__device__ __forceinline__ void fwd_body(const T* __restrict__ t, const T* __restrict__ C,
+                                         T* __restrict__ y, int64_t B, int I, int O, int D,
+                                         int d0, int dn, int accumulate, const float* rs,
+                                         T (&ts)[64][kValuKI + 1], T (&cs)[kValuKI][DM][64]) {
   constexpr int KI = kValuKI;
-  const int d0 = SEEK ? d0_arg : 0;
-  __shared__ T ts[64][KI + 1];
-  __shared__ T cs[KI][DM][64];
   const int tid = threadIdx.x, tr = tid >> 4, to = tid & 15;
   const int64_t b0 = (int64_t)blockIdx.x * 64;
   const int o0 = blockIdx.y * 64;
@@ -85,33 +152,7 @@ k_fwd_v(const T* __restrict__ t, const T* __restrict__ C, T* __restrict__ y, int
       cs[ii][d][ol] = (i < I && o < O) ? C[((size_t)i * O + o) * D + d0 + d] : T(0);
     }
     __syncthreads();
-#pragma unroll
-    for (int ii = 0; ii < KI; ++ii) {
-      T tp[4], tc[4], tw[4];  // T_{d-1}, T_d, 2 t
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const T tv = ts[tr + 16 * r][ii];
-        tw[r] = tv + tv;
-        cheb_seek<T>(tv, d0, tp[r], tc[r]);
-      }
-      for (int d = 0; d < dn; ++d) {  // rolled: measured faster than unrolled here
-        {
-          T cv[4];
-#pragma unroll
-          for (int c = 0; c < 4; ++c) cv[c] = cs[ii][d][to + 16 * c];
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-#pragma unroll
-            for (int c = 0; c < 4; ++c) acc[r][c] = fma(tc[r], cv[c], acc[r][c]);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {  // T_{d+1} = 2t T_d - T_{d-1}
-            const T nx = fma(tw[r], tc[r], -tp[r]);
-            tp[r] = tc[r];
-            tc[r] = nx;
-          }
-        }
-      }
-    }
+    fwd_tile<T, DM, GEN>(acc, ts, cs, rs, D, d0, dn, tr, to);
   }
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
@@ -125,24 +166,115 @@ k_fwd_v(const T* __restrict__ t, const T* __restrict__ C, T* __restrict__ y, int
   }
 }
 
+template <typename T, int DM, bool SEEK>
+__global__ void __launch_bounds__(256)
+k_fwd_v(const T* __restrict__ t, const T* __restrict__ C, T* __restrict__ y, int64_t B, int I,
+        int O, int D, int d0_arg, int dn, int accumulate, const float* __restrict__ rec) {
+  const int d0 = SEEK ? d0_arg : 0;
+  __shared__ T ts[64][kValuKI + 1];
+  __shared__ T cs[kValuKI][DM][64];
+  __shared__ float rs[sizeof(T) == 4 ? kRecFloats : 1];
+  stage_rec<T>(rs, rec, D);
+  __syncthreads();
+  if (rec_generic<T>(rs, rec, D))
+    fwd_body<T, DM, SEEK, true>(t, C, y, B, I, O, D, d0, dn, accumulate, rs, ts, cs);
+  else
+    fwd_body<T, DM, SEEK, false>(t, C, y, B, I, O, D, d0, dn, accumulate, rs, ts, cs);
+}
+
 // dx, degrees [d0, d0 + dn): block tile 128 rows x 8 inputs; thread
 // (rr, ii) = (tid / 8, tid % 8) owns G[b, i, d0 .. d0+dn) of rows rr + 32 h
 // (h < 4) in registers.  Outputs are taken 16 at a time: dy [128][16] and the
 // chunk of C as [8 inputs][16 outputs][DM] in LDS, the per-input stride padded
 // to an odd number of elements so the 8 inputs of a wave read distinct banks.
-// accumulate: add to dx (later chunks).
+// accumulate: add to dx (later chunks).  The epilogue sums G_d P_d'(t)
+// (Chebyshev: d U_{d-1}(t); GEN: the differentiated recurrence, times s) and
+// applies t'(x): 1 - t^2, or ima with the affine map.
+// The dx epilogue for one recurrence kind: dx[b, i] = t'(x) sum_d G_d P_d'(t)
+// for the thread's rows rr + 32 h.
+template <typename T, int DM, bool SEEK, bool GEN>
+__device__ __forceinline__ void dx_epilogue(const T* __restrict__ t, T* __restrict__ dx,
+                                            const T (&g)[4][DM], int64_t B, int I, int D, int d0,
+                                            int dn, int accumulate, const float* rs, int imap,
+                                            float ima) {
+  const int tid = threadIdx.x, rr = tid >> 3, ii = tid & 7;
+  const int64_t b0 = (int64_t)blockIdx.x * 128;
+  const int i = blockIdx.y * 8 + ii;
+  if (i >= I) return;
+#pragma unroll
+  for (int h = 0; h < 4; ++h) {
+    const int64_t b = b0 + rr + 32 * h;
+    if (b >= B) continue;
+    const T tv = t[b * I + i];
+    T s = T(0);
+    if constexpr (GEN) {
+      // (pm, pc) = (P_{n-1}, P_n), (qm, qc) their derivatives in u, from n = 0:
+      // P_n' = a_n P_{n-1} + (a_n u + b_n) P_{n-1}' - c_n P_{n-2}'
+      const T u = (T)rs[3 * D] * tv;
+      T pm = T(0), pc = T(1), qm = T(0), qc = T(0);
+      auto step = [&](int n) {
+        asm volatile("" ::: "memory");  // coefficients read per step, not hoisted
+        const T an = (T)rs[n], fn = fma(an, u, (T)rs[D + n]), cn = (T)rs[2 * D + n];
+        const T pn = fma(fn, pc, -cn * pm);
+        const T qn = fma(an, pc, fma(fn, qc, -cn * qm));
+        pm = pc;
+        pc = pn;
+        qm = qc;
+        qc = qn;
+      };
+      for (int n = 1; n <= d0; ++n) step(n);
+#pragma unroll
+      for (int d = 0; d < DM; ++d) {
+        if (d < dn) {
+          s = fma(g[h][d], qc, s);
+          step(d0 + d + 1);
+        }
+      }
+      s *= (T)rs[3 * D];  // du/dt
+    } else {
+      const T t2 = tv + tv;
+      // (up, u) = (U_{deg-2}, U_{deg-1}) at degree deg.  The first chunk
+      // starts at degree 1 (T_0 has no derivative, so G[., ., 0] is never
+      // formed) from (U_{-1}, U_0) = (0, 1); a later chunk advances the
+      // recurrence U_{n+1} = 2t U_n - U_{n-1} from (U_{-1}, U_0) to degree d0.
+      constexpr int dfirst = SEEK ? 0 : 1;
+      T up = T(0), u = T(1);
+      for (int d = 1; d < d0; ++d) {
+        const T un = fma(t2, u, -up);
+        up = u;
+        u = un;
+      }
+      T deg = (T)(d0 + dfirst);  // counted in T (exact)
+#pragma unroll
+      for (int d = dfirst; d < DM; ++d) {
+        if (d < dn) {  // dT_deg/dt = deg U_{deg-1}
+          s = fma(g[h][d] * deg, u, s);
+          const T un = fma(t2, u, -up);
+          up = u;
+          u = un;
+          deg += T(1);
+        }
+      }
+    }
+    const T v = s * (imap ? (T)ima : T(1) - tv * tv);
+    dx[b * I + i] = SEEK && accumulate ? dx[b * I + i] + v : v;
+  }
+}
+
 template <typename T, int DM, bool SEEK>
 __global__ void __launch_bounds__(256)
 k_dx_v(const T* __restrict__ t, const T* __restrict__ C, const T* __restrict__ dy,
-       T* __restrict__ dx, int64_t B, int I, int O, int D, int d0_arg, int dn,
-       int accumulate) {
+       T* __restrict__ dx, int64_t B, int I, int O, int D, int d0_arg, int dn, int accumulate,
+       const float* __restrict__ rec, int imap, float ima) {
   constexpr int OC = 16, CST = OC * (DM + 1) + 1;
   const int d0 = SEEK ? d0_arg : 0;
   __shared__ T ys[128][OC + 1];
   __shared__ T cs[8 * CST];
+  __shared__ float rs[sizeof(T) == 4 ? kRecFloats : 1];
   const int tid = threadIdx.x, rr = tid >> 3, ii = tid & 7;
   const int64_t b0 = (int64_t)blockIdx.x * 128;
   const int i0 = blockIdx.y * 8;
+  stage_rec<T>(rs, rec, D);
   T g[4][DM];
 #pragma unroll
   for (int h = 0; h < 4; ++h)
@@ -176,39 +308,11 @@ k_dx_v(const T* __restrict__ t, const T* __restrict__ C, const T* __restrict__ d
       }
     }
   }
-  const int i = i0 + ii;
-  if (i >= I) return;
-#pragma unroll
-  for (int h = 0; h < 4; ++h) {
-    const int64_t b = b0 + rr + 32 * h;
-    if (b >= B) continue;
-    const T tv = t[b * I + i];
-    const T t2 = tv + tv;
-    // (up, u) = (U_{deg-2}, U_{deg-1}) at degree deg.  The first chunk starts
-    // at degree 1 (T_0 has no derivative, so G[., ., 0] is never formed) from
-    // (U_{-1}, U_0) = (0, 1); a later chunk advances the recurrence
-    // U_{n+1} = 2t U_n - U_{n-1} from (U_{-1}, U_0) to degree d0.
-    constexpr int dfirst = SEEK ? 0 : 1;
-    T up = T(0), u = T(1), s = T(0);
-    for (int d = 1; d < d0; ++d) {
-      const T un = fma(t2, u, -up);
-      up = u;
-      u = un;
-    }
-    T deg = (T)(d0 + dfirst);  // counted in T (exact)
-#pragma unroll
-    for (int d = dfirst; d < DM; ++d) {
-      if (d < dn) {  // dT_deg/dt = deg U_{deg-1}
-        s = fma(g[h][d] * deg, u, s);
-        const T un = fma(t2, u, -up);
-        up = u;
-        u = un;
-        deg += T(1);
-      }
-    }
-    const T v = s * (T(1) - tv * tv);
-    dx[b * I + i] = SEEK && accumulate ? dx[b * I + i] + v : v;
-  }
+  if (O == 0) __syncthreads();  // the recurrence block is staged before its first use
+  if (rec_generic<T>(rs, rec, D))
+    dx_epilogue<T, DM, SEEK, true>(t, dx, g, B, I, D, d0, dn, accumulate, rs, imap, ima);
+  else
+    dx_epilogue<T, DM, SEEK, false>(t, dx, g, B, I, D, d0, dn, accumulate, rs, imap, ima);
 }
 
 // dC, degrees [d0, d0 + dn): block tile 8 inputs x 128 outputs; thread
@@ -225,13 +329,36 @@ template <> struct DcWrite<double> {  // store or accumulate
   }
 };
 
-template <typename T, int DM, bool SEEK>
-__global__ void __launch_bounds__(256)
-k_dc_v(const T* __restrict__ t, const T* __restrict__ dy, T* __restrict__ dC, int64_t B, int I,
-       int O, int D, int d0_arg, int dn, DcOut om) {
-  const int d0 = SEEK ? d0_arg : 0;
-  __shared__ T ts[32][9];
-  __shared__ T ys[32][129];
+// One LDS tile of dC (32 rows): acc += P(t) dy.
+template <typename T, int DM, bool GEN>
+__device__ __forceinline__ void dc_tile(T (&acc)[4][DM], const T (&ts)[32][9],
+                                        const T (&ys)[32][129], const float* rs, int D, int d0,
+                                        int dn, int il, int ol) {
+  for (int r = 0; r < 32; ++r) {
+    T yv[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) yv[c] = ys[r][ol + 32 * c];
+    T w, pm, pc;
+    rec_init<T, GEN>(ts[r][il], rs, D, w, pm, pc);
+    for (int n = 1; n <= d0; ++n) rec_step<T, GEN>(w, rs, D, n, pm, pc);
+#pragma unroll
+    for (int d = 0; d < DM; ++d) {
+      if (d < dn) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[c][d] = fma(pc, yv[c], acc[c][d]);
+        rec_step<T, GEN>(w, rs, D, d0 + d + 1, pm, pc);
+      }
+    }
+  }
+}
+
+// The dC kernel's body for one recurrence kind (the kind is uniform over the
+// launch; one body per kind keeps each one's register allocation its own).
+template <typename T, int DM, bool SEEK, bool GEN>
+__device__ __forceinline__ void dc_body(const T* __restrict__ t, const T* __restrict__ dy,
+                                        T* __restrict__ dC, int64_t B, int I, int O, int D,
+                                        int d0, int dn, const DcOut& om, const float* rs,
+                                        T (&ts)[32][9], T (&ys)[32][129]) {
   const int tid = threadIdx.x, il = tid >> 5, ol = tid & 31;
   const int i0 = blockIdx.x * 8, o0 = blockIdx.y * 128;
   T acc[4][DM];
@@ -252,24 +379,7 @@ k_dc_v(const T* __restrict__ t, const T* __restrict__ dy, T* __restrict__ dC, in
       ys[r][o] = (b < B && o0 + o < O) ? dy[b * O + o0 + o] : T(0);
     }
     __syncthreads();
-    for (int r = 0; r < 32; ++r) {
-      const T tv = ts[r][il], t2 = tv + tv;
-      T yv[4];
-#pragma unroll
-      for (int c = 0; c < 4; ++c) yv[c] = ys[r][ol + 32 * c];
-      T tp, tc;
-      cheb_seek<T>(tv, d0, tp, tc);
-#pragma unroll
-      for (int d = 0; d < DM; ++d) {
-        if (d < dn) {
-#pragma unroll
-          for (int c = 0; c < 4; ++c) acc[c][d] = fma(tc, yv[c], acc[c][d]);
-          const T nx = fma(t2, tc, -tp);
-          tp = tc;
-          tc = nx;
-        }
-      }
-    }
+    dc_tile<T, DM, GEN>(acc, ts, ys, rs, D, d0, dn, il, ol);
   }
   const int i = i0 + il;
   if (i >= I) return;
@@ -284,13 +394,33 @@ k_dc_v(const T* __restrict__ t, const T* __restrict__ dy, T* __restrict__ dC, in
   }
 }
 
-// dst = float(src), src fp32 or bf16 (the coefficient copy of this path).
+template <typename T, int DM, bool SEEK>
 __global__ void __launch_bounds__(256)
-k_to_f32(const void* __restrict__ src, int src_bf16, float* __restrict__ dst, int64_t n) {
+k_dc_v(const T* __restrict__ t, const T* __restrict__ dy, T* __restrict__ dC, int64_t B, int I,
+       int O, int D, int d0_arg, int dn, DcOut om, const float* __restrict__ rec) {
+  const int d0 = SEEK ? d0_arg : 0;
+  __shared__ T ts[32][9];
+  __shared__ T ys[32][129];
+  __shared__ float rs[sizeof(T) == 4 ? kRecFloats : 1];
+  stage_rec<T>(rs, rec, D);
+  __syncthreads();
+  if (rec_generic<T>(rs, rec, D))
+    dc_body<T, DM, SEEK, true>(t, dy, dC, B, I, O, D, d0, dn, om, rs, ts, ys);
+  else
+    dc_body<T, DM, SEEK, false>(t, dy, dC, B, I, O, D, d0, dn, om, rs, ts, ys);
+}
+
+// dst = float(src) (or dst += float(src)), src fp32 or bf16: the coefficient
+// copy of this path.
+__global__ void __launch_bounds__(256)
+k_to_f32(const void* __restrict__ src, int src_bf16, float* __restrict__ dst, int64_t n,
+         int accumulate) {
   for (int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; q < n;
-       q += (int64_t)gridDim.x * blockDim.x)
-    dst[q] = src_bf16 ? __uint_as_float((uint32_t)static_cast<const uint16_t*>(src)[q] << 16)
-                      : static_cast<const float*>(src)[q];
+       q += (int64_t)gridDim.x * blockDim.x) {
+    const float v = src_bf16 ? __uint_as_float((uint32_t)static_cast<const uint16_t*>(src)[q] << 16)
+                             : static_cast<const float*>(src)[q];
+    dst[q] = accumulate ? dst[q] + v : v;
+  }
 }
 
 static unsigned vgrid(int64_t n) {
@@ -299,9 +429,11 @@ static unsigned vgrid(int64_t n) {
   return (unsigned)(g < 1 ? 1 : g);
 }
 
-void launch_to_f32(const void* src, bool src_bf16, float* dst, int64_t n, hipStream_t s) {
+void launch_to_f32(const void* src, bool src_bf16, float* dst, int64_t n, hipStream_t s,
+                   bool accumulate) {
   if (n > 0)
-    hipLaunchKernelGGL(k_to_f32, dim3(vgrid(n)), dim3(256), 0, s, src, src_bf16 ? 1 : 0, dst, n);
+    hipLaunchKernelGGL(k_to_f32, dim3(vgrid(n)), dim3(256), 0, s, src, src_bf16 ? 1 : 0, dst, n,
+                       accumulate ? 1 : 0);
 }
 
 // Chunk size: the smallest instantiated DM that holds D, 17 above.
@@ -309,78 +441,82 @@ static int valu_dm(int D) { return D <= 3 ? 3 : D <= 5 ? 5 : D <= 9 ? 9 : kValuD
 
 template <typename T, int DM>
 static void fwd_chunks(const T* t, const T* C, T* y, int64_t B, int I, int O, int D,
-                       hipStream_t s) {
+                       const float* rec, hipStream_t s) {
   const dim3 g((unsigned)((B + 63) / 64), (unsigned)((O + 63) / 64));
   for (int d0 = 0; d0 < D; d0 += DM) {
     const int dn = D - d0 < DM ? D - d0 : DM;
     if (d0 == 0)
       hipLaunchKernelGGL((k_fwd_v<T, DM, false>), g, dim3(256), 0, s, t, C, y, B, I, O, D,
-                         d0, dn, 0);
+                         d0, dn, 0, rec);
     else
       hipLaunchKernelGGL((k_fwd_v<T, DM, true>), g, dim3(256), 0, s, t, C, y, B, I, O, D,
-                         d0, dn, 1);
+                         d0, dn, 1, rec);
   }
 }
 
 template <typename T, int DM>
 static void bwd_chunks(const T* t, const T* C, const T* dy, T* dx, T* dC, DcOut om, int64_t B,
-                       int I, int O, int D, hipStream_t s) {
+                       int I, int O, int D, const float* rec, int imap, float ima, hipStream_t s) {
   for (int d0 = 0; d0 < D; d0 += DM) {
     const int dn = D - d0 < DM ? D - d0 : DM;
     if (dx && B > 0) {
       const dim3 g((unsigned)((B + 127) / 128), (unsigned)((I + 7) / 8));
       if (d0 == 0)
         hipLaunchKernelGGL((k_dx_v<T, DM, false>), g, dim3(256), 0, s, t, C, dy, dx, B, I,
-                           O, D, d0, dn, 0);
+                           O, D, d0, dn, 0, rec, imap, ima);
       else
         hipLaunchKernelGGL((k_dx_v<T, DM, true>), g, dim3(256), 0, s, t, C, dy, dx, B, I,
-                           O, D, d0, dn, 1);
+                           O, D, d0, dn, 1, rec, imap, ima);
     }
     if (dC) {
       const dim3 g((unsigned)((I + 7) / 8), (unsigned)((O + 127) / 128));
       if (d0 == 0)
         hipLaunchKernelGGL((k_dc_v<T, DM, false>), g, dim3(256), 0, s, t, dy, dC, B, I, O,
-                           D, d0, dn, om);
+                           D, d0, dn, om, rec);
       else
         hipLaunchKernelGGL((k_dc_v<T, DM, true>), g, dim3(256), 0, s, t, dy, dC, B, I, O,
-                           D, d0, dn, om);
+                           D, d0, dn, om, rec);
     }
   }
 }
 
 template <typename T>
-void launch_forward_valu(const T* x, const T* C, T* y, T* t, int64_t B, int I, int O,
-                         int deg, hipStream_t s) {
+void launch_forward_valu(const T* x, const T* C, T* y, T* t, int64_t B, int I, int O, int deg,
+                         hipStream_t s, const float* rec, int imap, float ima, float imb) {
   if (B == 0) return;
-  hipLaunchKernelGGL(k_tanh_v<T>, dim3(vgrid(B * I)), dim3(256), 0, s, x, t, B * I);
+  hipLaunchKernelGGL(k_tanh_v<T>, dim3(vgrid(B * I)), dim3(256), 0, s, x, t, B * I, imap, ima, imb);
   const int D = deg + 1;
   switch (valu_dm(D)) {
-    case 3: fwd_chunks<T, 3>(t, C, y, B, I, O, D, s); break;
-    case 5: fwd_chunks<T, 5>(t, C, y, B, I, O, D, s); break;
-    case 9: fwd_chunks<T, 9>(t, C, y, B, I, O, D, s); break;
-    default: fwd_chunks<T, kValuDM>(t, C, y, B, I, O, D, s); break;
+    case 3: fwd_chunks<T, 3>(t, C, y, B, I, O, D, rec, s); break;
+    case 5: fwd_chunks<T, 5>(t, C, y, B, I, O, D, rec, s); break;
+    case 9: fwd_chunks<T, 9>(t, C, y, B, I, O, D, rec, s); break;
+    default: fwd_chunks<T, kValuDM>(t, C, y, B, I, O, D, rec, s); break;
   }
 }
 
 template <typename T>
 void launch_backward_valu(const T* t, const T* C, const T* dy, T* dx, T* dC, DcOut om, int64_t B,
-                          int I, int O, int deg, hipStream_t s) {
+                          int I, int O, int deg, hipStream_t s, const float* rec, int imap,
+                          float ima) {
   const int D = deg + 1;
   switch (valu_dm(D)) {
-    case 3: bwd_chunks<T, 3>(t, C, dy, dx, dC, om, B, I, O, D, s); break;
-    case 5: bwd_chunks<T, 5>(t, C, dy, dx, dC, om, B, I, O, D, s); break;
-    case 9: bwd_chunks<T, 9>(t, C, dy, dx, dC, om, B, I, O, D, s); break;
-    default: bwd_chunks<T, kValuDM>(t, C, dy, dx, dC, om, B, I, O, D, s); break;
+    case 3: bwd_chunks<T, 3>(t, C, dy, dx, dC, om, B, I, O, D, rec, imap, ima, s); break;
+    case 5: bwd_chunks<T, 5>(t, C, dy, dx, dC, om, B, I, O, D, rec, imap, ima, s); break;
+    case 9: bwd_chunks<T, 9>(t, C, dy, dx, dC, om, B, I, O, D, rec, imap, ima, s); break;
+    default: bwd_chunks<T, kValuDM>(t, C, dy, dx, dC, om, B, I, O, D, rec, imap, ima, s); break;
   }
 }
 
 template void launch_forward_valu<float>(const float*, const float*, float*, float*, int64_t, int,
-                                         int, int, hipStream_t);
+                                         int, int, hipStream_t, const float*, int, float, float);
 template void launch_forward_valu<double>(const double*, const double*, double*, double*, int64_t,
-                                          int, int, int, hipStream_t);
+                                          int, int, int, hipStream_t, const float*, int, float,
+                                          float);
 template void launch_backward_valu<float>(const float*, const float*, const float*, float*, float*,
-                                          DcOut, int64_t, int, int, int, hipStream_t);
+                                          DcOut, int64_t, int, int, int, hipStream_t, const float*,
+                                          int, float);
 template void launch_backward_valu<double>(const double*, const double*, const double*, double*,
-                                           double*, DcOut, int64_t, int, int, int, hipStream_t);
+                                           double*, DcOut, int64_t, int, int, int, hipStream_t,
+                                           const float*, int, float);
 
 }  // namespace ckan

@@ -61,20 +61,56 @@ def test_descriptor_validation(field, value, code):
 
 def test_high_degree_sizes_and_limits():
     """Degrees 17..256 run on the vector-ALU kernels: the packed buffer is C
-    as fp32 [I, O, D], the tanh cache has row pitch I, no workspace."""
+    as fp32 [I, O, D] followed, at the next 256-byte boundary, by the basis
+    recurrence block (3 D + 2 floats); the input-map cache has row pitch I; no
+    workspace."""
     lib = _lib.load()
+
+    def al(n):
+        return -(-n // 256) * 256
+
     for deg, B, I, O in [(17, 8, 4, 3), (40, 33, 70, 5), (256, 1, 2, 2)]:
         for compute, cdt in [(0, 0), (1, 1)]:
             d = _lib.make_desc(B, I, O, deg, compute, cdt)
-            assert lib.ckan_packed_bytes(d) == -(-I * O * (deg + 1) * 4 // 256) * 256
+            D = deg + 1
+            assert lib.ckan_packed_bytes(d) == al(I * O * D * 4) + al((3 * D + 2) * 4)
             assert lib.ckan_tcache_elems(d) == B * I
             assert lib.ckan_fwd_workspace_bytes(d) == 0
             assert lib.ckan_bwd_workspace_bytes(d, 1, 1) == 0
-    # the affine input map (finite-domain Hermite) is served up to degree 16
-    assert lib.ckan_packed_bytes(_lib.make_desc(8, 4, 3, 16, 0, 0, (0.5, 0.1))) > 0
-    d = _lib.make_desc(8, 4, 3, 17, 0, 0, (0.5, 0.1))
-    assert lib.ckan_forward(d, 16, 16, 16, 16, None, 0, None) == _lib.CKAN_ERR_UNSUPPORTED
-    assert b"affine" in lib.ckan_last_error()
+    # the affine input map (finite-domain Hermite) is served at every degree
+    for deg in (16, 17, 256):
+        assert lib.ckan_packed_bytes(_lib.make_desc(8, 4, 3, deg, 0, 0, (0.5, 0.1))) > 0
+    assert lib.ckan_packed_bytes(_lib.make_desc(8, 4, 3, 257, 0, 0)) == 0
+
+
+def test_high_degree_family_spec_checked_before_launch():
+    """Jacobi / Hermite layers above degree 16 are packed as C plus the
+    family's recurrence block: the spec is validated (degree match, family,
+    Jacobi parameters, finite scale) before anything is launched."""
+    lib = _lib.load()
+    d = _lib.make_desc(8, 4, 3, 40, 0, 0)
+    ok = _lib.make_spec(_lib.CKAN_BASIS_JACOBI, 40, 0.5, 1.5, 1.0)
+    # valid spec: the NULL coefficient pointer is what is rejected
+    assert lib.ckan_pack_coeffs_basis(d, ok, None, 256, None) == _lib.CKAN_ERR_INVALID_ARG
+    assert b"NULL" in lib.ckan_last_error()
+    for bad in (_lib.make_spec(_lib.CKAN_BASIS_JACOBI, 39, 0.5, 1.5, 1.0),
+                _lib.make_spec(_lib.CKAN_BASIS_JACOBI, 40, -1.0, 1.5, 1.0),
+                _lib.make_spec(99, 40, 0.0, 0.0, 1.0),
+                _lib.make_spec(_lib.CKAN_BASIS_HERMITE, 40, 0.0, 0.0, float("inf"))):
+        assert lib.ckan_pack_coeffs_basis(d, bad, 256, 256, None) == _lib.CKAN_ERR_INVALID_ARG
+        assert lib.ckan_pack_forward(d, bad, 256, 256, 256, 256, 256, None, 0, None) == \
+            _lib.CKAN_ERR_INVALID_ARG
+        assert lib.ckan_coeff_grad_from_chebyshev(d, bad, 256, 512, 0, None) == \
+            _lib.CKAN_ERR_INVALID_ARG
+    # the materialised family basis: degree up to 256, validated first
+    big = _lib.make_spec(_lib.CKAN_BASIS_HERMITE, 257, 0.0, 0.0, 3.0)
+    assert lib.ckan_family_basis(big, 256, 4, 256, None) == _lib.CKAN_ERR_UNSUPPORTED
+    assert lib.ckan_family_basis(ok, None, 4, 256, None) == _lib.CKAN_ERR_INVALID_ARG
+    assert b"NULL" in lib.ckan_last_error()
+    assert lib.ckan_family_basis_backward(ok, 256, 256, 0, 256, None) == 0  # n == 0: nothing to do
+    # the identity map in place cannot accumulate; in place without it is a no-op
+    assert lib.ckan_coeff_grad_from_chebyshev(d, ok, 256, 256, 1, None) == _lib.CKAN_ERR_INVALID_ARG
+    assert lib.ckan_coeff_grad_from_chebyshev(d, ok, 256, 256, 0, None) == 0
 
 
 def test_null_pointers_rejected_before_launch():

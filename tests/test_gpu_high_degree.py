@@ -182,3 +182,143 @@ def test_high_degree_executor_matches_oracle(optimizer):
     for l in range(2):
         assert _rel(ex.get_coeffs(l), c_ref[l]) <= 1e-5
     ex.close()
+
+
+# Jacobi / Hermite layers above degree 16: the vector-ALU kernels run the
+# family's own three-term recurrence (coefficients from the packed buffer's
+# recurrence block) and differentiate it for dx, so dC comes out in the
+# family's basis directly.  Oracle: the reference's op order
+# (oracle/family_oracle.py) evaluated in fp64; the same op order in fp32
+# stays within 5.1e-6 of it on these cases (Jacobi(1.5, 0.5) at degree 40 the
+# largest).
+FAMILY_CASES = [
+    # family, alpha, beta, B, I, O, deg
+    ("jacobi", 0.0, 0.0, 200, 33, 20, 24),
+    ("jacobi", 1.5, 0.5, 129, 16, 50, 40),   # three chunks
+    ("jacobi", -0.5, 0.25, 64, 8, 8, 17),    # a chunk of 17 and one of 1
+    ("jacobi", 0.5, 0.5, 16, 4, 3, 100),
+    ("hermite", 0, 0, 70, 9, 13, 20),
+    ("hermite", 0, 0, 40, 6, 5, 32),
+    ("hermite_e", 0, 0, 150, 24, 40, 30),
+]
+
+
+def _family_spec(family, deg, alpha=0.0, beta=0.0):
+    from kan_amd import _lib
+    if family == "jacobi":
+        return _lib.make_spec(_lib.CKAN_BASIS_JACOBI, deg, alpha, beta, 1.0)
+    fam = _lib.CKAN_BASIS_HERMITE if family == "hermite" else _lib.CKAN_BASIS_HERMITE_E
+    return _lib.make_spec(fam, deg, 0.0, 0.0, 3.0)
+
+
+def _family_gpu(x, c, dy, spec, compute="fp32", affine=None):
+    from kan_amd import functional as F
+    xd = x.cuda().requires_grad_(True)
+    cd = c.cuda().requires_grad_(True)
+    y = F.family_kan(xd, cd, spec, compute, affine)
+    y.backward(dy.cuda())
+    torch.cuda.synchronize()
+    return y.detach().cpu(), xd.grad.cpu(), cd.grad.cpu()
+
+
+@pytest.mark.parametrize("family,alpha,beta,B,I,O,deg", FAMILY_CASES)
+def test_high_degree_family_parity(family, alpha, beta, B, I, O, deg):
+    from oracle import family_oracle as fo
+    print(f"high degree {family}({alpha},{beta}) B={B} I={I} O={O} deg={deg}", flush=True)
+    x, c, dy = _inputs(B, I, O, deg, seed=B + deg)
+    y, dx, dc = _family_gpu(x, c, dy, _family_spec(family, deg, alpha, beta))
+    y_ref, dx_ref, dc_ref = fo.family_forward_backward(x.double(), c.double(), dy.double(),
+                                                       family, alpha, beta)
+    assert _rel(y, y_ref) <= FP32_TOL
+    assert _rel(dx, dx_ref) <= FP32_TOL
+    assert _rel(dc, dc_ref) <= FP32_TOL
+
+
+def test_high_degree_family_bf16_request_runs_fp32():
+    print("high degree family bf16 request", flush=True)
+    x, c, dy = _inputs(90, 12, 20, 22, seed=21)
+    spec = _family_spec("jacobi", 22, 0.5, -0.5)
+    a = _family_gpu(x, c, dy, spec, "fp32")
+    b = _family_gpu(x, c, dy, spec, "bf16")
+    for u, v in zip(a, b):
+        assert torch.equal(u, v)
+
+
+@pytest.mark.parametrize("scaling,B,I,O,deg", [("physicist", 120, 20, 30, 20),
+                                                ("probabilist", 33, 7, 9, 28)])
+def test_high_degree_hermite_finite_domain(scaling, B, I, O, deg):
+    """HermiteKANLayer(domain=(lo, hi), normalize_domain=True) above degree
+    16: the affine map onto [-3, 3] (kan/basis/hermite.py:102-112) runs in the
+    vector-ALU input-map launch, dx takes its constant chain factor; the
+    coefficient gradient accumulates over two backward calls."""
+    import kan_amd
+    from oracle import family_oracle as fo
+    print(f"high degree hermite affine {scaling} B={B} I={I} O={O} deg={deg}", flush=True)
+    dom = (-2.0, 5.0)
+    torch.manual_seed(B + deg)
+    m = kan_amd.HermiteKANLayer(I, O, deg, scaling=scaling, domain=dom, normalize_domain=True)
+    c = m.hermite_coeffs.detach().clone()
+    g = torch.Generator().manual_seed(B + I)
+    x = torch.rand(B, I, generator=g) * 7.6 - 2.3  # partly outside [lo, hi]
+    dy = torch.randn(B, O, generator=g)
+    fam = "hermite" if scaling == "physicist" else "hermite_e"
+    y_ref, dx_ref, dc_ref = fo.family_forward_backward(x.double(), c.double(), dy.double(), fam,
+                                                       domain=dom)
+    m = m.cuda()
+    for _ in range(2):
+        xd = x.cuda().requires_grad_(True)
+        y = m(xd)
+        y.backward(dy.cuda())
+    torch.cuda.synchronize()
+    assert _rel(y, y_ref) <= FP32_TOL
+    assert _rel(xd.grad, dx_ref) <= FP32_TOL
+    assert _rel(m.hermite_coeffs.grad, 2 * dc_ref) <= FP32_TOL
+
+
+def test_high_degree_family_coeff_grad_map_is_identity():
+    """ckan_coeff_grad_from_chebyshev above degree 16 (where the backward
+    already differentiates in the family's basis): a copy, an accumulation,
+    and nothing in place."""
+    from kan_amd import _lib
+    print("high degree family coefficient-gradient map", flush=True)
+    lib = _lib.load()
+    I, O, deg = 9, 11, 30
+    spec = _family_spec("hermite_e", deg)
+    d = _lib.make_desc(4, I, O, deg, 0, 0)
+    st = _lib.stream_ptr(torch.device("cuda"))
+    g = torch.Generator().manual_seed(31)
+    src = torch.randn(I, O, deg + 1, generator=g).cuda()
+    base = torch.randn(I, O, deg + 1, generator=g).cuda()
+    out = torch.empty_like(src)
+    _lib.check(lib.ckan_coeff_grad_from_chebyshev(d, spec, src.data_ptr(), out.data_ptr(), 0, st))
+    acc = base.clone()
+    _lib.check(lib.ckan_coeff_grad_from_chebyshev(d, spec, src.data_ptr(), acc.data_ptr(), 1, st))
+    same = src.clone()
+    _lib.check(lib.ckan_coeff_grad_from_chebyshev(d, spec, same.data_ptr(), same.data_ptr(), 0, st))
+    torch.cuda.synchronize()
+    assert torch.equal(out, src)
+    assert torch.equal(acc, base + src)
+    assert torch.equal(same, src)
+
+
+@pytest.mark.parametrize("family,alpha,beta,deg", [("jacobi", 1.0, 0.5, 40), ("hermite", 0, 0, 24),
+                                                   ("hermite_e", 0, 0, 40)])
+def test_high_degree_family_basis_functions(family, alpha, beta, deg):
+    """The materialised family basis and its backward above degree 16
+    (kan/basis/jacobi.py:119-188, kan/basis/hermite.py:141-233), against the
+    reference's recurrence in fp64."""
+    from kan_amd import functional as F
+    from oracle import family_oracle as fo
+    print(f"high degree {family} basis deg={deg}", flush=True)
+    s = 1.0 if family == "jacobi" else 3.0
+    t = (torch.rand(300, 7, generator=torch.Generator().manual_seed(1)) * 2 - 1) * s
+    g = torch.randn(300, 7, deg + 1, generator=torch.Generator().manual_seed(2))
+    tr = t.clone().double().requires_grad_(True)
+    ref = fo.family_basis(tr, family, deg, alpha, beta)
+    (ref * g.double()).sum().backward()
+    td = t.cuda().requires_grad_(True)
+    out = F.family_basis(td, _family_spec(family, deg, alpha, beta))
+    (out * g.cuda()).sum().backward()
+    torch.cuda.synchronize()
+    assert _rel(out, ref) <= FP32_TOL
+    assert _rel(td.grad, tr.grad) <= FP32_TOL
