@@ -45,10 +45,13 @@ k_tanh_flat(const f32x4_t* __restrict__ x, f32x4_t* __restrict__ t, int64_t n4, 
             float imb) {
   const int64_t base = (int64_t)blockIdx.x * (256 * kTanhU) + threadIdx.x;
   f32x4_t v[kTanhU];
+  // x, C and dy are read once per launch: non-temporal loads keep them from
+  // displacing reused data (pack + tanh 34 -> 28 us, dy re-layout 18 -> 16 us
+  // at config 3)
 #pragma unroll
   for (int u = 0; u < kTanhU; ++u) {
     const int64_t k = base + u * 256;
-    v[u] = k < n4 ? x[k] : f32x4_t{0.f, 0.f, 0.f, 0.f};
+    v[u] = k < n4 ? __builtin_nontemporal_load(x + k) : f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
 #pragma unroll
   for (int u = 0; u < kTanhU; ++u) {
@@ -110,7 +113,7 @@ k_pack(const CT* __restrict__ C, typename Elem<BF>::type* __restrict__ Cf,
 #pragma unroll
   for (int u = 0; u < kPackTanhU; ++u) {
     const int64_t k = tj0 + tid + u * 256;
-    tx[u] = k < tj1 ? tj.x[k] : f32x4_t{0.f, 0.f, 0.f, 0.f};
+    tx[u] = k < tj1 ? __builtin_nontemporal_load(tj.x + k) : f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
   const int i0 = ib * 32, o0 = ob * 32;
   const int D = p.D;
@@ -130,7 +133,7 @@ k_pack(const CT* __restrict__ C, typename Elem<BF>::type* __restrict__ Cf,
       const int il = v / (8 * D), k4 = v - il * (8 * D);
       const int i = i0 + il;
       buf[q] = (v < nv && i < p.I)
-          ? *reinterpret_cast<const f32x4_t*>(reinterpret_cast<const float*>(C) + ((size_t)i * p.O + o0) * D + k4 * 4)
+          ? __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(reinterpret_cast<const float*>(C) + ((size_t)i * p.O + o0) * D + k4 * 4))
           : f32x4_t{0.f, 0.f, 0.f, 0.f};
     }
 #pragma unroll
@@ -239,7 +242,7 @@ k_pack(const CT* __restrict__ C, typename Elem<BF>::type* __restrict__ Cf,
 #pragma unroll
       for (int u = 0; u < kPackTanhU; ++u) {
         const int64_t k = c0 + tid + u * 256;
-        tx[u] = k < tj1 ? tj.x[k] : f32x4_t{0.f, 0.f, 0.f, 0.f};
+        tx[u] = k < tj1 ? __builtin_nontemporal_load(tj.x + k) : f32x4_t{0.f, 0.f, 0.f, 0.f};
       }
     }
 #pragma unroll
@@ -301,7 +304,7 @@ k_prep_dy(const float* __restrict__ dy, typename Elem<BF>::type* __restrict__ dY
   for (int m = 0; m < kPrepRows / 8; ++m) {
     const int64_t b = r0 + m * 8 + rs;
     if (b < p.B && vec) {
-      v[m] = *reinterpret_cast<const f32x4_t*>(dy + b * p.O + o);
+      v[m] = __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(dy + b * p.O + o));
     } else {
 #pragma unroll
       for (int j = 0; j < 4; ++j) v[m][j] = (b < p.B && o + j < p.O) ? dy[b * p.O + o + j] : 0.0f;

@@ -539,7 +539,11 @@ k_fwd_pipe(const float* __restrict__ tc, const typename Elem<BF>::type* __restri
         float* op = out + r0 * pitch + o;
         if (full_rows) {
 #pragma unroll
-          for (int v = 0; v < 16; ++v) op[(8 * (v >> 2) + (v & 3)) * pitch] = acc[mi][keep0 + j][v] + add;
+          for (int v = 0; v < 16; ++v) {
+            float* a = op + (8 * (v >> 2) + (v & 3)) * pitch;
+            if (split) *a = acc[mi][keep0 + j][v] + add;
+            else __builtin_nontemporal_store(acc[mi][keep0 + j][v] + add, a);
+          }
         } else {
 #pragma unroll
           for (int v = 0; v < 16; ++v)
@@ -649,7 +653,7 @@ k_fwd_stream(const float* __restrict__ x, float* __restrict__ tc,
 #pragma unroll
   for (int q = 0; q < KPW; ++q) {
     const int sg = min(sg0 + q / G::SGK, nsg - 1);
-    bfr[q] = load_frag<BF>(Cf + cf_elem<BF>(p.KB, nb, sg * G::SGK + q % G::SGK, lane) - (size_t)lane * 8, lane);
+    bfr[q] = load_frag_nt<BF>(Cf + cf_elem<BF>(p.KB, nb, sg * G::SGK + q % G::SGK, lane) - (size_t)lane * 8, lane);
   }
 #pragma unroll
   for (int q = 0; q < KPW; ++q)
@@ -858,7 +862,7 @@ k_fwd_cols(const float* __restrict__ x, float* __restrict__ tc, const uint16_t* 
 #pragma unroll
     for (int l = 0; l < NL; ++l) {
       const int kb = min(bb * K::KBB + 4 * l, kbmax);
-      fb[buf][l] = *reinterpret_cast<const bf16x8_t*>(stream + (size_t)kb * 128);
+      fb[buf][l] = __builtin_nontemporal_load(reinterpret_cast<const bf16x8_t*>(stream + (size_t)kb * 128));
     }
   };
 
@@ -1100,7 +1104,7 @@ k_dx_pipe(const typename Elem<BF>::type* __restrict__ dYx,
         up = u;
         u = un;
       }
-      if (icol && r < p.B) dx[r * p.I + i] = sum * input_slope(tv[v], p);
+      if (icol && r < p.B) __builtin_nontemporal_store(sum * input_slope(tv[v], p), dx + r * p.I + i);
     }
   }
 }
@@ -1310,7 +1314,7 @@ k_dx_dh(const typename Elem<BF>::type* __restrict__ dYx,
     float* dp = dx + r0 * p.I + i;
     if (icol && r0 - 4 * g + 32 <= p.B) {
 #pragma unroll
-      for (int v = 0; v < 16; ++v) dp[(int64_t)(8 * (v >> 2) + (v & 3)) * p.I] = res[v];
+      for (int v = 0; v < 16; ++v) __builtin_nontemporal_store(res[v], dp + (int64_t)(8 * (v >> 2) + (v & 3)) * p.I);
     } else if (icol) {
 #pragma unroll
       for (int v = 0; v < 16; ++v)
@@ -1434,7 +1438,7 @@ k_dx(const typename Elem<BF>::type* __restrict__ dYx, const typename Elem<BF>::t
         up = u;
         u = un;
       }
-      if (ok) dx[r * p.I + i] = s * input_slope(tv, p);
+      if (ok) __builtin_nontemporal_store(s * input_slope(tv, p), dx + r * p.I + i);
     }
   }
 }
