@@ -92,21 +92,33 @@ __device__ __forceinline__ bool rec_generic(const float* rs, const float* rec, i
 // accumulated) with no seek loops in the code, as register-lean as a
 // single-chunk kernel.
 
-// Forward, degrees [d0, d0 + dn): block tile 64 rows x 64 outputs, 256
-// threads, thread (tr, to) owns rows tr + 16 r and outputs to + 16 c
-// (r, c < 4).  Inputs are taken KI at a time: t [64][KI] and the chunk of C
+// Register tile widths: rows per thread of the forward (WF), of dx (WX) and
+// outputs per thread of dC (WC).  The fp64 forward on chunks of up to 9
+// degrees takes 8 rows: half the C values read from LDS per FMA and the basis
+// recurrence spread over twice the FMAs (config-3 shape in fp64: forward 5.9
+// -> 5.1 ms).  8 rows in dx measured slower (occupancy 3 -> 2) and 8 outputs
+// in dC no faster, so those keep 4.
+template <typename T, int DM> struct VTile {
+  static constexpr int WF = (sizeof(T) == 8 && DM <= 9) ? 8 : 4;
+  static constexpr int WX = 4;
+  static constexpr int WC = 4;
+};
+
+// Forward, degrees [d0, d0 + dn): block tile 16 RT rows x 64 outputs (RT = WF), 256
+// threads, thread (tr, to) owns rows tr + 16 r (r < RT) and outputs to + 16 c
+// (c < 4).  Inputs are taken KI at a time: t [16 RT][KI] and the chunk of C
 // as [KI][DM][64 outputs] in LDS.  accumulate: add to y (later chunks).
 constexpr int kValuKI = 4;
 // One LDS tile of the forward (KI inputs): acc += P(t) C.
-template <typename T, int DM, bool GEN>
-__device__ __forceinline__ void fwd_tile(T (&acc)[4][4], const T (&ts)[64][kValuKI + 1],
+template <typename T, int DM, bool GEN, int RT>
+__device__ __forceinline__ void fwd_tile(T (&acc)[RT][4], const T (&ts)[16 * RT][kValuKI + 1],
                                          const T (&cs)[kValuKI][DM][64], const float* rs, int D,
                                          int d0, int dn, int tr, int to) {
 #pragma unroll
   for (int ii = 0; ii < kValuKI; ++ii) {
-    T pm[4], pc[4], w[4];  // P_{d-1}, P_d, the recurrence's argument
+    T pm[RT], pc[RT], w[RT];  // P_{d-1}, P_d, the recurrence's argument
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
+    for (int r = 0; r < RT; ++r) {
       rec_init<T, GEN>(ts[tr + 16 * r][ii], rs, D, w[r], pm[r], pc[r]);
       for (int n = 1; n <= d0; ++n) rec_step<T, GEN>(w[r], rs, D, n, pm[r], pc[r]);
     }
@@ -115,11 +127,11 @@ __device__ __forceinline__ void fwd_tile(T (&acc)[4][4], const T (&ts)[64][kValu
 #pragma unroll
       for (int c = 0; c < 4; ++c) cv[c] = cs[ii][d][to + 16 * c];
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
+      for (int r = 0; r < RT; ++r)
 #pragma unroll
         for (int c = 0; c < 4; ++c) acc[r][c] = fma(pc[r], cv[c], acc[r][c]);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) rec_step<T, GEN>(w[r], rs, D, d0 + d + 1, pm[r], pc[r]);
+      for (int r = 0; r < RT; ++r) rec_step<T, GEN>(w[r], rs, D, d0 + d + 1, pm[r], pc[r]);
     }
   }
 }
@@ -129,19 +141,20 @@ template <typename T, int DM, bool SEEK, bool GEN>
 __device__ __forceinline__ void fwd_body(const T* __restrict__ t, const T* __restrict__ C,
                                          T* __restrict__ y, int64_t B, int I, int O, int D,
                                          int d0, int dn, int accumulate, const float* rs,
-                                         T (&ts)[64][kValuKI + 1], T (&cs)[kValuKI][DM][64]) {
-  constexpr int KI = kValuKI;
+                                         T (&ts)[16 * VTile<T, DM>::WF][kValuKI + 1],
+                                         T (&cs)[kValuKI][DM][64]) {
+  constexpr int KI = kValuKI, RT = VTile<T, DM>::WF, BR = 16 * RT;
   const int tid = threadIdx.x, tr = tid >> 4, to = tid & 15;
-  const int64_t b0 = (int64_t)blockIdx.x * 64;
+  const int64_t b0 = (int64_t)blockIdx.x * BR;
   const int o0 = blockIdx.y * 64;
-  T acc[4][4];
+  T acc[RT][4];
 #pragma unroll
-  for (int r = 0; r < 4; ++r)
+  for (int r = 0; r < RT; ++r)
 #pragma unroll
     for (int c = 0; c < 4; ++c) acc[r][c] = T(0);
   for (int i0 = 0; i0 < I; i0 += KI) {
     __syncthreads();
-    for (int k = tid; k < 64 * KI; k += 256) {
+    for (int k = tid; k < BR * KI; k += 256) {
       const int r = k / KI, ii = k % KI;
       const int64_t b = b0 + r;
       ts[r][ii] = (b < B && i0 + ii < I) ? t[b * I + i0 + ii] : T(0);
@@ -152,10 +165,10 @@ __device__ __forceinline__ void fwd_body(const T* __restrict__ t, const T* __res
       cs[ii][d][ol] = (i < I && o < O) ? C[((size_t)i * O + o) * D + d0 + d] : T(0);
     }
     __syncthreads();
-    fwd_tile<T, DM, GEN>(acc, ts, cs, rs, D, d0, dn, tr, to);
+    fwd_tile<T, DM, GEN, RT>(acc, ts, cs, rs, D, d0, dn, tr, to);
   }
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
+  for (int r = 0; r < RT; ++r) {
     const int64_t b = b0 + tr + 16 * r;
     if (b >= B) continue;
 #pragma unroll
@@ -171,7 +184,7 @@ __global__ void __launch_bounds__(256)
 k_fwd_v(const T* __restrict__ t, const T* __restrict__ C, T* __restrict__ y, int64_t B, int I,
         int O, int D, int d0_arg, int dn, int accumulate, const float* __restrict__ rec) {
   const int d0 = SEEK ? d0_arg : 0;
-  __shared__ T ts[64][kValuKI + 1];
+  __shared__ T ts[16 * VTile<T, DM>::WF][kValuKI + 1];
   __shared__ T cs[kValuKI][DM][64];
   __shared__ float rs[sizeof(T) == 4 ? kRecFloats : 1];
   stage_rec<T>(rs, rec, D);
@@ -182,27 +195,28 @@ k_fwd_v(const T* __restrict__ t, const T* __restrict__ C, T* __restrict__ y, int
     fwd_body<T, DM, SEEK, false>(t, C, y, B, I, O, D, d0, dn, accumulate, rs, ts, cs);
 }
 
-// dx, degrees [d0, d0 + dn): block tile 128 rows x 8 inputs; thread
-// (rr, ii) = (tid / 8, tid % 8) owns G[b, i, d0 .. d0+dn) of rows rr + 32 h
-// (h < 4) in registers.  Outputs are taken 16 at a time: dy [128][16] and the
-// chunk of C as [8 inputs][16 outputs][DM] in LDS, the per-input stride padded
-// to an odd number of elements so the 8 inputs of a wave read distinct banks.
-// accumulate: add to dx (later chunks).  The epilogue sums G_d P_d'(t)
-// (Chebyshev: d U_{d-1}(t); GEN: the differentiated recurrence, times s) and
-// applies t'(x): 1 - t^2, or ima with the affine map.
+// dx, degrees [d0, d0 + dn): block tile 32 HT rows x 8 inputs (HT = WX);
+// thread (rr, ii) = (tid / 8, tid % 8) owns G[b, i, d0 .. d0+dn) of rows
+// rr + 32 h (h < HT) in registers.  Outputs are taken 16 at a time: dy
+// [32 HT][16] and the chunk of C as [8 inputs][16 outputs][DM] in LDS, the
+// per-input stride padded to an odd number of elements so the 8 inputs of a
+// wave read distinct banks.  accumulate: add to dx (later chunks).  The
+// epilogue sums G_d P_d'(t) (Chebyshev: d U_{d-1}(t); GEN: the differentiated
+// recurrence, times s) and applies t'(x): 1 - t^2, or ima with the affine map.
+
 // The dx epilogue for one recurrence kind: dx[b, i] = t'(x) sum_d G_d P_d'(t)
 // for the thread's rows rr + 32 h.
-template <typename T, int DM, bool SEEK, bool GEN>
+template <typename T, int DM, bool SEEK, bool GEN, int HT>
 __device__ __forceinline__ void dx_epilogue(const T* __restrict__ t, T* __restrict__ dx,
-                                            const T (&g)[4][DM], int64_t B, int I, int D, int d0,
+                                            const T (&g)[HT][DM], int64_t B, int I, int D, int d0,
                                             int dn, int accumulate, const float* rs, int imap,
                                             float ima) {
   const int tid = threadIdx.x, rr = tid >> 3, ii = tid & 7;
-  const int64_t b0 = (int64_t)blockIdx.x * 128;
+  const int64_t b0 = (int64_t)blockIdx.x * (32 * HT);
   const int i = blockIdx.y * 8 + ii;
   if (i >= I) return;
 #pragma unroll
-  for (int h = 0; h < 4; ++h) {
+  for (int h = 0; h < HT; ++h) {
     const int64_t b = b0 + rr + 32 * h;
     if (b >= B) continue;
     const T tv = t[b * I + i];
@@ -261,28 +275,26 @@ __device__ __forceinline__ void dx_epilogue(const T* __restrict__ t, T* __restri
   }
 }
 
-template <typename T, int DM, bool SEEK>
-__global__ void __launch_bounds__(256)
-k_dx_v(const T* __restrict__ t, const T* __restrict__ C, const T* __restrict__ dy,
-       T* __restrict__ dx, int64_t B, int I, int O, int D, int d0_arg, int dn, int accumulate,
-       const float* __restrict__ rec, int imap, float ima) {
-  constexpr int OC = 16, CST = OC * (DM + 1) + 1;
-  const int d0 = SEEK ? d0_arg : 0;
-  __shared__ T ys[128][OC + 1];
-  __shared__ T cs[8 * CST];
-  __shared__ float rs[sizeof(T) == 4 ? kRecFloats : 1];
+// The dx kernel's body; FULL: the chunk holds DM degrees (dn == DM).
+template <typename T, int DM, bool SEEK, bool FULL, int CST, int BR>
+__device__ __forceinline__ void dx_body(const T* __restrict__ t, const T* __restrict__ C,
+                                        const T* __restrict__ dy, T* __restrict__ dx, int64_t B,
+                                        int I, int O, int D, int d0, int dn_arg, int accumulate,
+                                        const float* __restrict__ rec, int imap, float ima,
+                                        T (&ys)[BR][17], T (&cs)[8 * CST], const float* rs) {
+  constexpr int OC = 16, HT = BR / 32;
+  const int dn = FULL ? DM : dn_arg;
   const int tid = threadIdx.x, rr = tid >> 3, ii = tid & 7;
-  const int64_t b0 = (int64_t)blockIdx.x * 128;
+  const int64_t b0 = (int64_t)blockIdx.x * BR;
   const int i0 = blockIdx.y * 8;
-  stage_rec<T>(rs, rec, D);
-  T g[4][DM];
+  T g[HT][DM];
 #pragma unroll
-  for (int h = 0; h < 4; ++h)
+  for (int h = 0; h < HT; ++h)
 #pragma unroll
     for (int d = 0; d < DM; ++d) g[h][d] = T(0);
   for (int oc = 0; oc < O; oc += OC) {
     __syncthreads();
-    for (int k = tid; k < 128 * OC; k += 256) {
+    for (int k = tid; k < BR * OC; k += 256) {
       const int r = k / OC, ol = k % OC;
       const int64_t b = b0 + r;
       ys[r][ol] = (b < B && oc + ol < O) ? dy[b * O + oc + ol] : T(0);
@@ -294,31 +306,50 @@ k_dx_v(const T* __restrict__ t, const T* __restrict__ C, const T* __restrict__ d
     }
     __syncthreads();
     for (int ol = 0; ol < OC; ++ol) {
-      T a[4];
+      T a[HT];
 #pragma unroll
-      for (int h = 0; h < 4; ++h) a[h] = ys[rr + 32 * h][ol];
+      for (int h = 0; h < HT; ++h) a[h] = ys[rr + 32 * h][ol];
       const T* cr = cs + ii * CST + ol * (DM + 1);
 #pragma unroll
       for (int d = 0; d < DM; ++d) {
         if (d < dn) {
           const T cv = cr[d];
 #pragma unroll
-          for (int h = 0; h < 4; ++h) g[h][d] = fma(a[h], cv, g[h][d]);
+          for (int h = 0; h < HT; ++h) g[h][d] = fma(a[h], cv, g[h][d]);
         }
       }
     }
   }
   if (O == 0) __syncthreads();  // the recurrence block is staged before its first use
   if (rec_generic<T>(rs, rec, D))
-    dx_epilogue<T, DM, SEEK, true>(t, dx, g, B, I, D, d0, dn, accumulate, rs, imap, ima);
+    dx_epilogue<T, DM, SEEK, true, HT>(t, dx, g, B, I, D, d0, dn, accumulate, rs, imap, ima);
   else
-    dx_epilogue<T, DM, SEEK, false>(t, dx, g, B, I, D, d0, dn, accumulate, rs, imap, ima);
+    dx_epilogue<T, DM, SEEK, false, HT>(t, dx, g, B, I, D, d0, dn, accumulate, rs, imap, ima);
 }
 
-// dC, degrees [d0, d0 + dn): block tile 8 inputs x 128 outputs; thread
-// (il, ol) = (tid / 32, tid % 32) owns outputs ol + 32 c (c < 4) of input il,
-// all degrees of the chunk, so each basis recurrence serves four outputs.
-// Rows are taken 32 at a time: t [32][8] and dy [32][128] in LDS.
+template <typename T, int DM, bool SEEK>
+__global__ void __launch_bounds__(256)
+k_dx_v(const T* __restrict__ t, const T* __restrict__ C, const T* __restrict__ dy,
+       T* __restrict__ dx, int64_t B, int I, int O, int D, int d0_arg, int dn, int accumulate,
+       const float* __restrict__ rec, int imap, float ima) {
+  constexpr int OC = 16, CST = OC * (DM + 1) + 1, BR = 32 * VTile<T, DM>::WX;
+  const int d0 = SEEK ? d0_arg : 0;
+  __shared__ T ys[BR][OC + 1];
+  __shared__ T cs[8 * CST];
+  __shared__ float rs[sizeof(T) == 4 ? kRecFloats : 1];
+  stage_rec<T>(rs, rec, D);
+  if (dn == DM)
+    dx_body<T, DM, SEEK, true, CST, BR>(t, C, dy, dx, B, I, O, D, d0, dn, accumulate, rec, imap,
+                                        ima, ys, cs, rs);
+  else
+    dx_body<T, DM, SEEK, false, CST, BR>(t, C, dy, dx, B, I, O, D, d0, dn, accumulate, rec, imap,
+                                         ima, ys, cs, rs);
+}
+
+// dC, degrees [d0, d0 + dn): block tile 8 inputs x 32 CT outputs (CT = WC);
+// thread (il, ol) = (tid / 32, tid % 32) owns outputs ol + 32 c (c < CT) of
+// input il, all degrees of the chunk, so each basis recurrence serves CT
+// outputs.  Rows are taken 32 at a time: t [32][8] and dy [32][32 CT] in LDS.
 template <typename T> struct DcWrite;
 template <> struct DcWrite<float> {  // the dC write modes of the MFMA kernels
   static __device__ __forceinline__ void put(float* d, float v, const DcOut& om) { dc_write(d, v, om); }
@@ -330,14 +361,14 @@ template <> struct DcWrite<double> {  // store or accumulate
 };
 
 // One LDS tile of dC (32 rows): acc += P(t) dy.
-template <typename T, int DM, bool GEN>
-__device__ __forceinline__ void dc_tile(T (&acc)[4][DM], const T (&ts)[32][9],
-                                        const T (&ys)[32][129], const float* rs, int D, int d0,
-                                        int dn, int il, int ol) {
+template <typename T, int DM, bool GEN, int CT>
+__device__ __forceinline__ void dc_tile(T (&acc)[CT][DM], const T (&ts)[32][9],
+                                        const T (&ys)[32][32 * CT + 1], const float* rs, int D,
+                                        int d0, int dn, int il, int ol) {
   for (int r = 0; r < 32; ++r) {
-    T yv[4];
+    T yv[CT];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) yv[c] = ys[r][ol + 32 * c];
+    for (int c = 0; c < CT; ++c) yv[c] = ys[r][ol + 32 * c];
     T w, pm, pc;
     rec_init<T, GEN>(ts[r][il], rs, D, w, pm, pc);
     for (int n = 1; n <= d0; ++n) rec_step<T, GEN>(w, rs, D, n, pm, pc);
@@ -345,7 +376,7 @@ __device__ __forceinline__ void dc_tile(T (&acc)[4][DM], const T (&ts)[32][9],
     for (int d = 0; d < DM; ++d) {
       if (d < dn) {
 #pragma unroll
-        for (int c = 0; c < 4; ++c) acc[c][d] = fma(pc, yv[c], acc[c][d]);
+        for (int c = 0; c < CT; ++c) acc[c][d] = fma(pc, yv[c], acc[c][d]);
         rec_step<T, GEN>(w, rs, D, d0 + d + 1, pm, pc);
       }
     }
@@ -354,16 +385,18 @@ __device__ __forceinline__ void dc_tile(T (&acc)[4][DM], const T (&ts)[32][9],
 
 // The dC kernel's body for one recurrence kind (the kind is uniform over the
 // launch; one body per kind keeps each one's register allocation its own).
-template <typename T, int DM, bool SEEK, bool GEN>
+template <typename T, int DM, bool SEEK, bool GEN, bool FULL>
 __device__ __forceinline__ void dc_body(const T* __restrict__ t, const T* __restrict__ dy,
                                         T* __restrict__ dC, int64_t B, int I, int O, int D,
-                                        int d0, int dn, const DcOut& om, const float* rs,
-                                        T (&ts)[32][9], T (&ys)[32][129]) {
+                                        int d0, int dn_arg, const DcOut& om, const float* rs,
+                                        T (&ts)[32][9], T (&ys)[32][32 * VTile<T, DM>::WC + 1]) {
+  constexpr int CT = VTile<T, DM>::WC, BO = 32 * CT;
+  const int dn = FULL ? DM : dn_arg;
   const int tid = threadIdx.x, il = tid >> 5, ol = tid & 31;
-  const int i0 = blockIdx.x * 8, o0 = blockIdx.y * 128;
-  T acc[4][DM];
+  const int i0 = blockIdx.x * 8, o0 = blockIdx.y * BO;
+  T acc[CT][DM];
 #pragma unroll
-  for (int c = 0; c < 4; ++c)
+  for (int c = 0; c < CT; ++c)
 #pragma unroll
     for (int d = 0; d < DM; ++d) acc[c][d] = T(0);
   for (int64_t bc = 0; bc < B; bc += 32) {
@@ -373,18 +406,18 @@ __device__ __forceinline__ void dc_body(const T* __restrict__ t, const T* __rest
       const int64_t b = bc + r;
       ts[r][k] = (b < B && i0 + k < I) ? t[b * I + i0 + k] : T(0);
     }
-    for (int k = tid; k < 32 * 128; k += 256) {
-      const int r = k >> 7, o = k & 127;
+    for (int k = tid; k < 32 * BO; k += 256) {
+      const int r = k / BO, o = k % BO;
       const int64_t b = bc + r;
       ys[r][o] = (b < B && o0 + o < O) ? dy[b * O + o0 + o] : T(0);
     }
     __syncthreads();
-    dc_tile<T, DM, GEN>(acc, ts, ys, rs, D, d0, dn, il, ol);
+    dc_tile<T, DM, GEN, CT>(acc, ts, ys, rs, D, d0, dn, il, ol);
   }
   const int i = i0 + il;
   if (i >= I) return;
 #pragma unroll
-  for (int c = 0; c < 4; ++c) {
+  for (int c = 0; c < CT; ++c) {
     const int o = o0 + ol + 32 * c;
     if (o >= O) continue;
     T* dst = dC + ((size_t)i * O + o) * D + d0;
@@ -400,14 +433,15 @@ k_dc_v(const T* __restrict__ t, const T* __restrict__ dy, T* __restrict__ dC, in
        int O, int D, int d0_arg, int dn, DcOut om, const float* __restrict__ rec) {
   const int d0 = SEEK ? d0_arg : 0;
   __shared__ T ts[32][9];
-  __shared__ T ys[32][129];
+  __shared__ T ys[32][32 * VTile<T, DM>::WC + 1];
   __shared__ float rs[sizeof(T) == 4 ? kRecFloats : 1];
   stage_rec<T>(rs, rec, D);
   __syncthreads();
-  if (rec_generic<T>(rs, rec, D))
-    dc_body<T, DM, SEEK, true>(t, dy, dC, B, I, O, D, d0, dn, om, rs, ts, ys);
-  else
-    dc_body<T, DM, SEEK, false>(t, dy, dC, B, I, O, D, d0, dn, om, rs, ts, ys);
+  const bool gen = rec_generic<T>(rs, rec, D), full = dn == DM;
+  if (gen && full) dc_body<T, DM, SEEK, true, true>(t, dy, dC, B, I, O, D, d0, dn, om, rs, ts, ys);
+  else if (gen) dc_body<T, DM, SEEK, true, false>(t, dy, dC, B, I, O, D, d0, dn, om, rs, ts, ys);
+  else if (full) dc_body<T, DM, SEEK, false, true>(t, dy, dC, B, I, O, D, d0, dn, om, rs, ts, ys);
+  else dc_body<T, DM, SEEK, false, false>(t, dy, dC, B, I, O, D, d0, dn, om, rs, ts, ys);
 }
 
 // dst = float(src) (or dst += float(src)), src fp32 or bf16: the coefficient
@@ -442,7 +476,8 @@ static int valu_dm(int D) { return D <= 3 ? 3 : D <= 5 ? 5 : D <= 9 ? 9 : kValuD
 template <typename T, int DM>
 static void fwd_chunks(const T* t, const T* C, T* y, int64_t B, int I, int O, int D,
                        const float* rec, hipStream_t s) {
-  const dim3 g((unsigned)((B + 63) / 64), (unsigned)((O + 63) / 64));
+  constexpr int BR = 16 * VTile<T, DM>::WF;
+  const dim3 g((unsigned)((B + BR - 1) / BR), (unsigned)((O + 63) / 64));
   for (int d0 = 0; d0 < D; d0 += DM) {
     const int dn = D - d0 < DM ? D - d0 : DM;
     if (d0 == 0)
@@ -460,7 +495,8 @@ static void bwd_chunks(const T* t, const T* C, const T* dy, T* dx, T* dC, DcOut 
   for (int d0 = 0; d0 < D; d0 += DM) {
     const int dn = D - d0 < DM ? D - d0 : DM;
     if (dx && B > 0) {
-      const dim3 g((unsigned)((B + 127) / 128), (unsigned)((I + 7) / 8));
+      constexpr int BR = 32 * VTile<T, DM>::WX;
+      const dim3 g((unsigned)((B + BR - 1) / BR), (unsigned)((I + 7) / 8));
       if (d0 == 0)
         hipLaunchKernelGGL((k_dx_v<T, DM, false>), g, dim3(256), 0, s, t, C, dy, dx, B, I,
                            O, D, d0, dn, 0, rec, imap, ima);
@@ -469,7 +505,8 @@ static void bwd_chunks(const T* t, const T* C, const T* dy, T* dx, T* dC, DcOut 
                            O, D, d0, dn, 1, rec, imap, ima);
     }
     if (dC) {
-      const dim3 g((unsigned)((I + 7) / 8), (unsigned)((O + 127) / 128));
+      constexpr int BO = 32 * VTile<T, DM>::WC;
+      const dim3 g((unsigned)((I + 7) / 8), (unsigned)((O + BO - 1) / BO));
       if (d0 == 0)
         hipLaunchKernelGGL((k_dc_v<T, DM, false>), g, dim3(256), 0, s, t, dy, dC, B, I, O,
                            D, d0, dn, om, rec);
