@@ -104,23 +104,29 @@ template <typename T, int DM> struct VTile {
   static constexpr int WC = 4;
 };
 
-// Forward, degrees [d0, d0 + dn): block tile 16 RT rows x 64 outputs (RT = WF), 256
-// threads, thread (tr, to) owns rows tr + 16 r (r < RT) and outputs to + 16 c
-// (c < 4).  Inputs are taken KI at a time: t [16 RT][KI] and the chunk of C
-// as [KI][DM][64 outputs] in LDS.  accumulate: add to y (later chunks).
+// Forward: block tile 16 RT rows x 64 outputs (RT = WF), 256 threads, thread
+// (tr, to) owns rows tr + 16 r (r < RT) and outputs to + 16 c (c < 4).
+// Inputs are taken KI at a time (t [16 RT][KI] in LDS) and, for each input
+// tile, the degree axis DM degrees at a time ([KI][DM][64 outputs] of C in
+// LDS).  Above one chunk (MULTI) the recurrences of the thread's (row, input)
+// pairs stay in registers from chunk to chunk, so one launch covers any
+// degree without re-advancing a recurrence.
 constexpr int kValuKI = 4;
-// One LDS tile of the forward (KI inputs): acc += P(t) C.
-template <typename T, int DM, bool GEN, int RT>
-__device__ __forceinline__ void fwd_tile(T (&acc)[RT][4], const T (&ts)[16 * RT][kValuKI + 1],
+
+// Degrees [d0, d0 + dn) of one input tile: acc += P(t) C.  The recurrence of
+// (row r, input ii) is (w, pm, pc)[r][ii] at degree d0 on entry; INIT: started
+// here from t, input by input (so that only one input's recurrences are live).
+template <typename T, int DM, bool GEN, int RT, bool INIT>
+__device__ __forceinline__ void fwd_tile(T (&acc)[RT][4], T (&w)[RT][kValuKI],
+                                         T (&pm)[RT][kValuKI], T (&pc)[RT][kValuKI],
+                                         const T (&ts)[16 * RT][kValuKI + 1],
                                          const T (&cs)[kValuKI][DM][64], const float* rs, int D,
                                          int d0, int dn, int tr, int to) {
 #pragma unroll
   for (int ii = 0; ii < kValuKI; ++ii) {
-    T pm[RT], pc[RT], w[RT];  // P_{d-1}, P_d, the recurrence's argument
+    if constexpr (INIT) {
 #pragma unroll
-    for (int r = 0; r < RT; ++r) {
-      rec_init<T, GEN>(ts[tr + 16 * r][ii], rs, D, w[r], pm[r], pc[r]);
-      for (int n = 1; n <= d0; ++n) rec_step<T, GEN>(w[r], rs, D, n, pm[r], pc[r]);
+      for (int r = 0; r < RT; ++r) rec_init<T, GEN>(ts[tr + 16 * r][ii], rs, D, w[r][ii], pm[r][ii], pc[r][ii]);
     }
     for (int d = 0; d < dn; ++d) {  // rolled: measured faster than unrolled here
       T cv[4];
@@ -129,24 +135,31 @@ __device__ __forceinline__ void fwd_tile(T (&acc)[RT][4], const T (&ts)[16 * RT]
 #pragma unroll
       for (int r = 0; r < RT; ++r)
 #pragma unroll
-        for (int c = 0; c < 4; ++c) acc[r][c] = fma(pc[r], cv[c], acc[r][c]);
+        for (int c = 0; c < 4; ++c) acc[r][c] = fma(pc[r][ii], cv[c], acc[r][c]);
 #pragma unroll
-      for (int r = 0; r < RT; ++r) rec_step<T, GEN>(w[r], rs, D, d0 + d + 1, pm[r], pc[r]);
+      for (int r = 0; r < RT; ++r) rec_step<T, GEN>(w[r][ii], rs, D, d0 + d + 1, pm[r][ii], pc[r][ii]);
     }
   }
 }
 
 // The forward kernel's body for one recurrence kind (uniform over the launch).
-template <typename T, int DM, bool SEEK, bool GEN>
+template <typename T, int DM, bool GEN, bool MULTI>
 __device__ __forceinline__ void fwd_body(const T* __restrict__ t, const T* __restrict__ C,
                                          T* __restrict__ y, int64_t B, int I, int O, int D,
-                                         int d0, int dn, int accumulate, const float* rs,
+                                         const float* rs,
                                          T (&ts)[16 * VTile<T, DM>::WF][kValuKI + 1],
                                          T (&cs)[kValuKI][DM][64]) {
   constexpr int KI = kValuKI, RT = VTile<T, DM>::WF, BR = 16 * RT;
   const int tid = threadIdx.x, tr = tid >> 4, to = tid & 15;
   const int64_t b0 = (int64_t)blockIdx.x * BR;
   const int o0 = blockIdx.y * 64;
+  auto stage_c = [&](int i0, int d0, int dn) {
+    for (int k = tid; k < KI * 64 * dn; k += 256) {
+      const int ii = k / (64 * dn), rem = k % (64 * dn), ol = rem / dn, d = rem % dn;
+      const int i = i0 + ii, o = o0 + ol;
+      cs[ii][d][ol] = (i < I && o < O) ? C[((size_t)i * O + o) * D + d0 + d] : T(0);
+    }
+  };
   T acc[RT][4];
 #pragma unroll
   for (int r = 0; r < RT; ++r)
@@ -159,13 +172,25 @@ __device__ __forceinline__ void fwd_body(const T* __restrict__ t, const T* __res
       const int64_t b = b0 + r;
       ts[r][ii] = (b < B && i0 + ii < I) ? t[b * I + i0 + ii] : T(0);
     }
-    for (int k = tid; k < KI * 64 * dn; k += 256) {
-      const int ii = k / (64 * dn), rem = k % (64 * dn), ol = rem / dn, d = rem % dn;
-      const int i = i0 + ii, o = o0 + ol;
-      cs[ii][d][ol] = (i < I && o < O) ? C[((size_t)i * O + o) * D + d0 + d] : T(0);
-    }
+    if (!MULTI) stage_c(i0, 0, D);
     __syncthreads();
-    fwd_tile<T, DM, GEN, RT>(acc, ts, cs, rs, D, d0, dn, tr, to);
+    T w[RT][KI], pm[RT][KI], pc[RT][KI];
+    if constexpr (!MULTI) {
+      fwd_tile<T, DM, GEN, RT, true>(acc, w, pm, pc, ts, cs, rs, D, 0, D, tr, to);
+    } else {
+#pragma unroll
+      for (int r = 0; r < RT; ++r)
+#pragma unroll
+        for (int ii = 0; ii < KI; ++ii)
+          rec_init<T, GEN>(ts[tr + 16 * r][ii], rs, D, w[r][ii], pm[r][ii], pc[r][ii]);
+      for (int d0 = 0; d0 < D; d0 += DM) {
+        const int dn = D - d0 < DM ? D - d0 : DM;
+        __syncthreads();  // the previous chunk's reads of cs are done
+        stage_c(i0, d0, dn);
+        __syncthreads();
+        fwd_tile<T, DM, GEN, RT, false>(acc, w, pm, pc, ts, cs, rs, D, d0, dn, tr, to);
+      }
+    }
   }
 #pragma unroll
   for (int r = 0; r < RT; ++r) {
@@ -174,25 +199,25 @@ __device__ __forceinline__ void fwd_body(const T* __restrict__ t, const T* __res
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const int o = o0 + to + 16 * c;
-      if (o < O) y[b * O + o] = SEEK && accumulate ? y[b * O + o] + acc[r][c] : acc[r][c];
+      if (o < O) y[b * O + o] = acc[r][c];
     }
   }
 }
 
-template <typename T, int DM, bool SEEK>
+// MULTI: more degrees than one chunk of DM.
+template <typename T, int DM, bool MULTI>
 __global__ void __launch_bounds__(256)
 k_fwd_v(const T* __restrict__ t, const T* __restrict__ C, T* __restrict__ y, int64_t B, int I,
-        int O, int D, int d0_arg, int dn, int accumulate, const float* __restrict__ rec) {
-  const int d0 = SEEK ? d0_arg : 0;
+        int O, int D, const float* __restrict__ rec) {
   __shared__ T ts[16 * VTile<T, DM>::WF][kValuKI + 1];
   __shared__ T cs[kValuKI][DM][64];
   __shared__ float rs[sizeof(T) == 4 ? kRecFloats : 1];
   stage_rec<T>(rs, rec, D);
   __syncthreads();
   if (rec_generic<T>(rs, rec, D))
-    fwd_body<T, DM, SEEK, true>(t, C, y, B, I, O, D, d0, dn, accumulate, rs, ts, cs);
+    fwd_body<T, DM, true, MULTI>(t, C, y, B, I, O, D, rs, ts, cs);
   else
-    fwd_body<T, DM, SEEK, false>(t, C, y, B, I, O, D, d0, dn, accumulate, rs, ts, cs);
+    fwd_body<T, DM, false, MULTI>(t, C, y, B, I, O, D, rs, ts, cs);
 }
 
 // dx, degrees [d0, d0 + dn): block tile 32 HT rows x 8 inputs (HT = WX);
@@ -360,9 +385,11 @@ template <> struct DcWrite<double> {  // store or accumulate
   }
 };
 
-// One LDS tile of dC (32 rows): acc += P(t) dy.
-template <typename T, int DM, bool GEN, int CT>
-__device__ __forceinline__ void dc_tile(T (&acc)[CT][DM], const T (&ts)[32][9],
+// One LDS tile of dC (32 rows): acc += P(t) dy.  SEEK: the recurrences start
+// at degree d0 from sst, [3][32][9] (w, P_{d0-1}, P_{d0} of each (row,
+// input), advanced once per block instead of once per output thread).
+template <typename T, int DM, bool GEN, int CT, bool SEEK>
+__device__ __forceinline__ void dc_tile(T (&acc)[CT][DM], const T (&ts)[32][9], const T* sst,
                                         const T (&ys)[32][32 * CT + 1], const float* rs, int D,
                                         int d0, int dn, int il, int ol) {
   for (int r = 0; r < 32; ++r) {
@@ -370,8 +397,13 @@ __device__ __forceinline__ void dc_tile(T (&acc)[CT][DM], const T (&ts)[32][9],
 #pragma unroll
     for (int c = 0; c < CT; ++c) yv[c] = ys[r][ol + 32 * c];
     T w, pm, pc;
-    rec_init<T, GEN>(ts[r][il], rs, D, w, pm, pc);
-    for (int n = 1; n <= d0; ++n) rec_step<T, GEN>(w, rs, D, n, pm, pc);
+    if constexpr (SEEK) {
+      w = sst[r * 9 + il];
+      pm = sst[288 + r * 9 + il];
+      pc = sst[576 + r * 9 + il];
+    } else {
+      rec_init<T, GEN>(ts[r][il], rs, D, w, pm, pc);
+    }
 #pragma unroll
     for (int d = 0; d < DM; ++d) {
       if (d < dn) {
@@ -389,7 +421,8 @@ template <typename T, int DM, bool SEEK, bool GEN, bool FULL>
 __device__ __forceinline__ void dc_body(const T* __restrict__ t, const T* __restrict__ dy,
                                         T* __restrict__ dC, int64_t B, int I, int O, int D,
                                         int d0, int dn_arg, const DcOut& om, const float* rs,
-                                        T (&ts)[32][9], T (&ys)[32][32 * VTile<T, DM>::WC + 1]) {
+                                        T (&ts)[32][9], T* sst,
+                                        T (&ys)[32][32 * VTile<T, DM>::WC + 1]) {
   constexpr int CT = VTile<T, DM>::WC, BO = 32 * CT;
   const int dn = FULL ? DM : dn_arg;
   const int tid = threadIdx.x, il = tid >> 5, ol = tid & 31;
@@ -412,7 +445,17 @@ __device__ __forceinline__ void dc_body(const T* __restrict__ t, const T* __rest
       ys[r][o] = (b < B && o0 + o < O) ? dy[b * O + o0 + o] : T(0);
     }
     __syncthreads();
-    dc_tile<T, DM, GEN, CT>(acc, ts, ys, rs, D, d0, dn, il, ol);
+    if constexpr (SEEK) {  // each thread advances one (row, input) recurrence to degree d0
+      const int r = tid >> 3, k = tid & 7;
+      T w, pm, pc;
+      rec_init<T, GEN>(ts[r][k], rs, D, w, pm, pc);
+      for (int n = 1; n <= d0; ++n) rec_step<T, GEN>(w, rs, D, n, pm, pc);
+      sst[r * 9 + k] = w;
+      sst[288 + r * 9 + k] = pm;
+      sst[576 + r * 9 + k] = pc;
+      __syncthreads();
+    }
+    dc_tile<T, DM, GEN, CT, SEEK>(acc, ts, sst, ys, rs, D, d0, dn, il, ol);
   }
   const int i = i0 + il;
   if (i >= I) return;
@@ -430,18 +473,22 @@ __device__ __forceinline__ void dc_body(const T* __restrict__ t, const T* __rest
 template <typename T, int DM, bool SEEK>
 __global__ void __launch_bounds__(256)
 k_dc_v(const T* __restrict__ t, const T* __restrict__ dy, T* __restrict__ dC, int64_t B, int I,
-       int O, int D, int d0_arg, int dn, DcOut om, const float* __restrict__ rec) {
-  const int d0 = SEEK ? d0_arg : 0;
+       int O, int D, int d0_arg, int dn_arg, DcOut om, const float* __restrict__ rec) {
+  // SEEK: every chunk of the degree axis in one launch, chunk blockIdx.z (the
+  // chunks write disjoint degrees of dC, so they run side by side)
+  const int d0 = SEEK ? d0_arg + (int)blockIdx.z * DM : 0;
+  const int dn = SEEK ? min(DM, D - d0) : dn_arg;
   __shared__ T ts[32][9];
+  __shared__ T sst[SEEK ? 3 * 32 * 9 : 1];  // seek states, read only with SEEK
   __shared__ T ys[32][32 * VTile<T, DM>::WC + 1];
   __shared__ float rs[sizeof(T) == 4 ? kRecFloats : 1];
   stage_rec<T>(rs, rec, D);
   __syncthreads();
   const bool gen = rec_generic<T>(rs, rec, D), full = dn == DM;
-  if (gen && full) dc_body<T, DM, SEEK, true, true>(t, dy, dC, B, I, O, D, d0, dn, om, rs, ts, ys);
-  else if (gen) dc_body<T, DM, SEEK, true, false>(t, dy, dC, B, I, O, D, d0, dn, om, rs, ts, ys);
-  else if (full) dc_body<T, DM, SEEK, false, true>(t, dy, dC, B, I, O, D, d0, dn, om, rs, ts, ys);
-  else dc_body<T, DM, SEEK, false, false>(t, dy, dC, B, I, O, D, d0, dn, om, rs, ts, ys);
+  if (gen && full) dc_body<T, DM, SEEK, true, true>(t, dy, dC, B, I, O, D, d0, dn, om, rs, ts, sst, ys);
+  else if (gen) dc_body<T, DM, SEEK, true, false>(t, dy, dC, B, I, O, D, d0, dn, om, rs, ts, sst, ys);
+  else if (full) dc_body<T, DM, SEEK, false, true>(t, dy, dC, B, I, O, D, d0, dn, om, rs, ts, sst, ys);
+  else dc_body<T, DM, SEEK, false, false>(t, dy, dC, B, I, O, D, d0, dn, om, rs, ts, sst, ys);
 }
 
 // dst = float(src) (or dst += float(src)), src fp32 or bf16: the coefficient
@@ -474,19 +521,17 @@ void launch_to_f32(const void* src, bool src_bf16, float* dst, int64_t n, hipStr
 static int valu_dm(int D) { return D <= 3 ? 3 : D <= 5 ? 5 : D <= 9 ? 9 : kValuDM; }
 
 template <typename T, int DM>
-static void fwd_chunks(const T* t, const T* C, T* y, int64_t B, int I, int O, int D,
+static void fwd_launch(const T* t, const T* C, T* y, int64_t B, int I, int O, int D,
                        const float* rec, hipStream_t s) {
   constexpr int BR = 16 * VTile<T, DM>::WF;
   const dim3 g((unsigned)((B + BR - 1) / BR), (unsigned)((O + 63) / 64));
-  for (int d0 = 0; d0 < D; d0 += DM) {
-    const int dn = D - d0 < DM ? D - d0 : DM;
-    if (d0 == 0)
-      hipLaunchKernelGGL((k_fwd_v<T, DM, false>), g, dim3(256), 0, s, t, C, y, B, I, O, D,
-                         d0, dn, 0, rec);
-    else
-      hipLaunchKernelGGL((k_fwd_v<T, DM, true>), g, dim3(256), 0, s, t, C, y, B, I, O, D,
-                         d0, dn, 1, rec);
+  if constexpr (DM == kValuDM) {  // the only chunk size with more degrees than one chunk
+    if (D > DM) {
+      hipLaunchKernelGGL((k_fwd_v<T, DM, true>), g, dim3(256), 0, s, t, C, y, B, I, O, D, rec);
+      return;
+    }
   }
+  hipLaunchKernelGGL((k_fwd_v<T, DM, false>), g, dim3(256), 0, s, t, C, y, B, I, O, D, rec);
 }
 
 template <typename T, int DM>
@@ -504,16 +549,17 @@ static void bwd_chunks(const T* t, const T* C, const T* dy, T* dx, T* dC, DcOut 
         hipLaunchKernelGGL((k_dx_v<T, DM, true>), g, dim3(256), 0, s, t, C, dy, dx, B, I,
                            O, D, d0, dn, 1, rec, imap, ima);
     }
-    if (dC) {
-      constexpr int BO = 32 * VTile<T, DM>::WC;
-      const dim3 g((unsigned)((I + 7) / 8), (unsigned)((O + BO - 1) / BO));
-      if (d0 == 0)
-        hipLaunchKernelGGL((k_dc_v<T, DM, false>), g, dim3(256), 0, s, t, dy, dC, B, I, O,
-                           D, d0, dn, om, rec);
-      else
-        hipLaunchKernelGGL((k_dc_v<T, DM, true>), g, dim3(256), 0, s, t, dy, dC, B, I, O,
-                           D, d0, dn, om, rec);
-    }
+  }
+  if (dC) {  // one launch: the chunks of the degree axis side by side (grid z)
+    constexpr int BO = 32 * VTile<T, DM>::WC;
+    const int nch = (D + DM - 1) / DM;
+    const dim3 g((unsigned)((I + 7) / 8), (unsigned)((O + BO - 1) / BO), (unsigned)nch);
+    if (nch == 1)
+      hipLaunchKernelGGL((k_dc_v<T, DM, false>), g, dim3(256), 0, s, t, dy, dC, B, I, O, D, 0,
+                         D, om, rec);
+    else
+      hipLaunchKernelGGL((k_dc_v<T, DM, true>), g, dim3(256), 0, s, t, dy, dC, B, I, O, D, 0,
+                         DM, om, rec);
   }
 }
 
@@ -524,10 +570,10 @@ void launch_forward_valu(const T* x, const T* C, T* y, T* t, int64_t B, int I, i
   hipLaunchKernelGGL(k_tanh_v<T>, dim3(vgrid(B * I)), dim3(256), 0, s, x, t, B * I, imap, ima, imb);
   const int D = deg + 1;
   switch (valu_dm(D)) {
-    case 3: fwd_chunks<T, 3>(t, C, y, B, I, O, D, rec, s); break;
-    case 5: fwd_chunks<T, 5>(t, C, y, B, I, O, D, rec, s); break;
-    case 9: fwd_chunks<T, 9>(t, C, y, B, I, O, D, rec, s); break;
-    default: fwd_chunks<T, kValuDM>(t, C, y, B, I, O, D, rec, s); break;
+    case 3: fwd_launch<T, 3>(t, C, y, B, I, O, D, rec, s); break;
+    case 5: fwd_launch<T, 5>(t, C, y, B, I, O, D, rec, s); break;
+    case 9: fwd_launch<T, 9>(t, C, y, B, I, O, D, rec, s); break;
+    default: fwd_launch<T, kValuDM>(t, C, y, B, I, O, D, rec, s); break;
   }
 }
 
