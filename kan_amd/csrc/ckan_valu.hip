@@ -14,10 +14,12 @@
 // layers above the MFMA kernels' degree 16 (the reference layers take any
 // degree, kan/layers/chebykan.py:21-51).  Register-tiled kernels with LDS
 // staging read C in its own [I, O, D] layout.  The degree axis is taken in
-// chunks of at most DM degrees (one launch each; DM = 3, 5, 9 or 17, the
-// smallest that holds D, and 17 above): a chunk starting at d0 first advances
-// the recurrences to degree d0, so register arrays stay bounded for any
-// degree.  t is [B, I].
+// chunks of at most DM degrees (DM = 3, 5, 9 or 17, the smallest that holds
+// D, and 17 above), so register arrays stay bounded for any degree: the
+// forward walks the chunks inside one launch with its recurrences in
+// registers; dC runs the chunks side by side in one launch (grid z), each
+// block advancing its recurrences to the chunk's first degree once; dx runs
+// one launch per chunk, accumulating.  t is [B, I].
 #include "ckan_kernels.hpp"
 
 #include <math.h>

@@ -2,8 +2,8 @@
 any degree: kan/layers/chebykan.py:21-51, kan/basis/chebyshev.py:78-101).
 
 Those layers run on the vector-ALU kernels in fp32, the degree axis in
-chunks of 17 (several launches, each advancing the recurrence to its first
-degree).  The oracle runs in fp64 here: the fp32 acos/cos of the reference's
+chunks of 17 (the cases below cover one chunk and a remainder of 1, whole
+chunks, several chunks with a short last one, and degree 256).  The oracle runs in fp64 here: the fp32 acos/cos of the reference's
 default path itself drifts by about d * 6e-8 at degree d, so the fp64 form is
 the honest yardstick.
 
