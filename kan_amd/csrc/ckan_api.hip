@@ -380,9 +380,23 @@ int family_xform(const ckan_basis_spec* spec, int degree, BasisXform* xf);
 int family_valid(const ckan_basis_spec* spec, int degree);
 }
 
+namespace {
+int pack_forward_impl(const ckan_desc* desc, const ckan_basis_spec* spec, const void* coeffs,
+                      void* packed, const float* x, float* y, float* t_cache, void* ws,
+                      size_t ws_bytes, void* stream, bool t_ready, bool out_tanh);
+}
+
 int ckan_pack_forward(const ckan_desc* desc, const ckan_basis_spec* spec, const void* coeffs,
                       void* packed, const float* x, float* y, float* t_cache, void* ws,
                       size_t ws_bytes, void* stream) {
+  return pack_forward_impl(desc, spec, coeffs, packed, x, y, t_cache, ws, ws_bytes, stream, false,
+                           false);
+}
+
+namespace {
+int pack_forward_impl(const ckan_desc* desc, const ckan_basis_spec* spec, const void* coeffs,
+                      void* packed, const float* x, float* y, float* t_cache, void* ws,
+                      size_t ws_bytes, void* stream, bool t_ready, bool out_tanh) {
   int rc = validate_desc(desc);
   if (rc) return rc;
   if (valu_route(desc)) {
@@ -403,7 +417,7 @@ int ckan_pack_forward(const ckan_desc* desc, const ckan_basis_spec* spec, const 
     launch_pack(coeffs, cbf, packed, p, s, spec ? &xf : nullptr);
     return check_launch("pack_forward");
   }
-  if (!x || !y || !t_cache) return fail(CKAN_ERR_INVALID_ARG, "x/y/t_cache is NULL");
+  if ((!x && !t_ready) || !y || !t_cache) return fail(CKAN_ERR_INVALID_ARG, "x/y/t_cache is NULL");
   if (!aligned16(t_cache)) return fail(CKAN_ERR_INVALID_ARG, "t_cache must be 16-byte aligned");
   const FwdChoice c = choose_fwd(p);
   const size_t need = fwd_ws_bytes(p, c);
@@ -413,24 +427,25 @@ int ckan_pack_forward(const ckan_desc* desc, const ckan_basis_spec* spec, const 
   // the bias partials are summed by the forward GEMM where it can, and the
   // tanh of x rides in the pack launch where the layout allows: fewer launches
   const bool sum_in_gemm = fwd_sums_bias(p, c);
-  const bool fuse_tanh = fwd_reads_tcache(c) && pack_tanh_fusable(p, x);
+  const bool fuse_tanh = !t_ready && fwd_reads_tcache(c) && pack_tanh_fusable(p, x);
   {
     ProfScope ps(fuse_tanh ? "pack_tanh" : "pack", s);
     launch_pack(coeffs, cbf, packed, p, s, spec ? &xf : nullptr, !sum_in_gemm,
                 fuse_tanh ? x : nullptr, fuse_tanh ? t_cache : nullptr);
   }
   if ((rc = check_launch("pack_forward: pack"))) return rc;
-  if (fwd_reads_tcache(c) && !fuse_tanh) {
+  if (!t_ready && fwd_reads_tcache(c) && !fuse_tanh) {
     ProfScope ps("tanh", s);
     launch_tanh(x, t_cache, p, s);
   }
   if ((rc = check_launch("pack_forward: tanh"))) return rc;
   {
     ProfScope ps("fwd_gemm", s);
-    launch_fwd_gemm(x, t_cache, packed, y, ws, p, c, s, sum_in_gemm);
+    launch_fwd_gemm(x, t_cache, packed, y, ws, p, c, s, sum_in_gemm, out_tanh);
   }
   return check_launch("pack_forward: fwd_gemm");
 }
+}  // namespace
 
 int ckan_backward(const ckan_desc* desc, const float* t_cache, const void* packed,
                   const float* dy, float* dx, float* dcoeffs, int accumulate, void* ws,
@@ -857,3 +872,24 @@ size_t ckan_profile_report(char* buf, size_t len) {
 }
 
 }  // extern "C"
+
+bool ckan::layer_reads_tcache(const ckan_desc* desc) {
+  if (validate_desc(desc) != CKAN_OK || valu_route(desc)) return false;
+  const Plan p = plan_of(desc);
+  return p.I == p.I_sg && fwd_reads_tcache(choose_fwd(p));
+}
+
+bool ckan::layer_out_tanh_ok(const ckan_desc* desc) {
+  if (validate_desc(desc) != CKAN_OK || valu_route(desc)) return false;
+  return fwd_out_tanh_ok(plan_of(desc));
+}
+
+int ckan::pack_forward_ex(const ckan_desc* desc, const void* coeffs, void* packed, const float* x,
+                          float* out, float* t_cache, void* ws, size_t ws_bytes, void* stream,
+                          bool t_ready, bool out_tanh) {
+  if ((t_ready && !layer_reads_tcache(desc)) || (out_tanh && !layer_out_tanh_ok(desc)))
+    return fail(CKAN_ERR_INVALID_ARG, "pack_forward_ex: the layer's forward path does not allow "
+                "a precomputed tanh cache / a tanh output");
+  return pack_forward_impl(desc, nullptr, coeffs, packed, x, out, t_cache, ws, ws_bytes, stream,
+                           t_ready, out_tanh);
+}

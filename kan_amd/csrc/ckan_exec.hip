@@ -345,6 +345,9 @@ struct ckan_exec {
     float* y = nullptr;     // activation out [B, O]
     float* dy = nullptr;    // gradient wrt y  [B, O]
     size_t packed_bytes = 0;
+    // the training step's forward stores tanh(y) straight into the next
+    // layer's tanh cache (y itself is not needed by the step)
+    bool tanh_out = false;
   };
   ckan_exec_config cfg;
   std::vector<int32_t> widths, degrees;
@@ -447,10 +450,13 @@ int run_step(ckan_exec* ex, const float* x, const void* target, hipStream_t s,
   int rc;
   for (int l = 0; l < L; ++l) {
     auto& ly = ex->layers[l];
+    // pack and forward in one call: tanh in the pack launch (or, after a layer
+    // with tanh_out, already in ly.t), bias summed by the forward
+    const bool t_ready = l > 0 && ex->layers[l - 1].tanh_out;
     const float* in = l == 0 ? x : ex->layers[l - 1].y;
-    // pack and forward in one call: tanh in the pack launch, bias summed by the forward
-    if ((rc = ckan_pack_forward(&ly.desc, nullptr, ly.C, ly.packed, in, ly.y, ly.t, ex->fws,
-                                ex->fws_bytes, s)))
+    float* out = ly.tanh_out ? ex->layers[l + 1].t : ly.y;
+    if ((rc = pack_forward_ex(&ly.desc, ly.C, ly.packed, t_ready ? nullptr : in, out, ly.t,
+                              ex->fws, ex->fws_bytes, s, t_ready, ly.tanh_out)))
       return rc;
   }
   auto& last = ex->layers[L - 1];
@@ -550,6 +556,9 @@ int ckan_exec_create(const ckan_exec_config* cfg, ckan_exec** out, void* stream)
     if (f > ex->fws_bytes) ex->fws_bytes = f;
     if (b > ex->bws_bytes) ex->bws_bytes = b;
   }
+  for (int l = 0; rc == CKAN_OK && l + 1 < cfg->n_layers; ++l)
+    ex->layers[l].tanh_out = layer_out_tanh_ok(&ex->layers[l].desc) &&
+                             layer_reads_tcache(&ex->layers[l + 1].desc);
   if (rc == CKAN_OK) {
     ex->fws_bytes = align256(ex->fws_bytes);
     ex->bws_bytes = align256(ex->bws_bytes);

@@ -291,8 +291,9 @@ template <int CR> __device__ __forceinline__ int fwd_t_xor(int r) {
 // The bias: bias_f[o] when nib == 0; otherwise the block sums the nib
 // per-input-block partials bias_part[ib][o] itself (in the order k_col_reduce
 // adds them, so the two give the same bits), and the first row tile also
-// writes the sums to bias_out.
-template <int P, bool BF>
+// writes the sums to bias_out.  OT (unsplit launches only): store tanh(y)
+// in place of y, for the next layer of a stack.
+template <int P, bool BF, bool OT>
 __global__ void __launch_bounds__(512)
 k_fwd_pipe(const float* __restrict__ tc, const typename Elem<BF>::type* __restrict__ Cf,
            const float* __restrict__ bias_f, float* __restrict__ y, float* __restrict__ part,
@@ -541,14 +542,18 @@ k_fwd_pipe(const float* __restrict__ tc, const typename Elem<BF>::type* __restri
 #pragma unroll
           for (int v = 0; v < 16; ++v) {
             float* a = op + (8 * (v >> 2) + (v & 3)) * pitch;
-            if (split) *a = acc[mi][keep0 + j][v] + add;
-            else __builtin_nontemporal_store(acc[mi][keep0 + j][v] + add, a);
+            const float yv = acc[mi][keep0 + j][v] + add;
+            if (split) *a = yv;
+            else if constexpr (OT) *a = tanhf(yv);  // read again soon, by the next layer
+            else __builtin_nontemporal_store(yv, a);
           }
         } else {
 #pragma unroll
           for (int v = 0; v < 16; ++v)
-            if (r0 + 8 * (v >> 2) + (v & 3) < nrow)
-              op[(8 * (v >> 2) + (v & 3)) * pitch] = acc[mi][keep0 + j][v] + add;
+            if (r0 + 8 * (v >> 2) + (v & 3) < nrow) {
+              const float yv = acc[mi][keep0 + j][v] + add;
+              op[(8 * (v >> 2) + (v & 3)) * pitch] = OT && !split ? tanhf(yv) : yv;
+            }
         }
       }
     }
@@ -2067,7 +2072,8 @@ FwdChoice choose_fwd(const Plan& p) {
 
 template <int P, bool BF>
 static void fwd_dispatch(const float* x, float* t, const void* packed, float* y, void* ws,
-                         const Plan& p, const FwdChoice& c, hipStream_t s, int nib) {
+                         const Plan& p, const FwdChoice& c, hipStream_t s, int nib,
+                         bool out_tanh) {
   typedef typename Elem<BF>::type E;
   const E* Cf = reinterpret_cast<const E*>(packed);
   char* pk = const_cast<char*>(reinterpret_cast<const char*>(packed));
@@ -2121,9 +2127,20 @@ static void fwd_dispatch(const float* x, float* t, const void* packed, float* y,
           }
           const size_t lds = (size_t)K::LDS_BYTES;
           static std::atomic<uint32_t> lds_set{0};
-          ensure_lds_limit(reinterpret_cast<const void*>(&k_fwd_pipe<P, BF>), (int)lds, lds_set);
-          hipLaunchKernelGGL((k_fwd_pipe<P, BF>), grid, dim3(K::THREADS), lds, s, t, Cf, bias, y,
-                             part, p, c.sg_per_split, bpart, nib_k, nib_k > 0 ? bias_out : nullptr);
+          if (out_tanh) {
+            static std::atomic<uint32_t> lds_set_ot{0};
+            ensure_lds_limit(reinterpret_cast<const void*>(&k_fwd_pipe<P, BF, true>), (int)lds,
+                             lds_set_ot);
+            hipLaunchKernelGGL((k_fwd_pipe<P, BF, true>), grid, dim3(K::THREADS), lds, s, t, Cf,
+                               bias, y, part, p, c.sg_per_split, bpart, nib_k,
+                               nib_k > 0 ? bias_out : nullptr);
+          } else {
+            ensure_lds_limit(reinterpret_cast<const void*>(&k_fwd_pipe<P, BF, false>), (int)lds,
+                             lds_set);
+            hipLaunchKernelGGL((k_fwd_pipe<P, BF, false>), grid, dim3(K::THREADS), lds, s, t, Cf,
+                               bias, y, part, p, c.sg_per_split, bpart, nib_k,
+                               nib_k > 0 ? bias_out : nullptr);
+          }
         } else {
           hipLaunchKernelGGL((k_fwd<P, BF, 2, 4, 4, 1>), grid, dim3(256), 0, s, t, Cf, bias, y,
                              part, p, c.sg_per_split, bpart, nib_k, bias_out);
@@ -2140,6 +2157,25 @@ static void fwd_dispatch(const float* x, float* t, const void* packed, float* y,
   }
 }
 
+// The forward can store tanh(y) in place of y: the pipelined kernel, unsplit,
+// stores y itself.
+template <int P, bool BF> static bool out_tanh_ok(const Plan& p, const FwdChoice& c) {
+  if constexpr (FwdPipe<P, BF>::kOk)
+    return c.tile == kFwdBig && c.splits == 1 && fwd_pipe_offsets_fit(p);
+  else
+    return false;
+}
+bool fwd_out_tanh_ok(const Plan& p) {
+  const FwdChoice c = choose_fwd(p);
+  const bool bf = p.esz == 2;
+  switch (p.P) {
+    case 2: return bf ? out_tanh_ok<2, true>(p, c) : out_tanh_ok<2, false>(p, c);
+    case 4: return bf ? out_tanh_ok<4, true>(p, c) : out_tanh_ok<4, false>(p, c);
+    case 8: return bf ? out_tanh_ok<8, true>(p, c) : out_tanh_ok<8, false>(p, c);
+    default: return bf ? out_tanh_ok<16, true>(p, c) : out_tanh_ok<16, false>(p, c);
+  }
+}
+
 // The forward can sum the bias partials itself: every unsplit kernel does it
 // once per column; a split forward's reduce does it per output element, so
 // only for small outputs.
@@ -2151,10 +2187,11 @@ bool fwd_sums_bias(const Plan& p, const FwdChoice& c) {
 }
 
 void launch_fwd_gemm(const float* x, float* t, const void* packed, float* y, void* ws,
-                     const Plan& p, const FwdChoice& c, hipStream_t s, bool sum_bias) {
+                     const Plan& p, const FwdChoice& c, hipStream_t s, bool sum_bias,
+                     bool out_tanh) {
   const bool bf = p.esz == 2;
   const int nib = sum_bias && fwd_sums_bias(p, c) ? p.NIB : 0;
-#define CKAN_FW(PP, BB) fwd_dispatch<PP, BB>(x, t, packed, y, ws, p, c, s, nib)
+#define CKAN_FW(PP, BB) fwd_dispatch<PP, BB>(x, t, packed, y, ws, p, c, s, nib, out_tanh)
   switch (p.P) {
     case 2: bf ? CKAN_FW(2, true) : CKAN_FW(2, false); break;
     case 4: bf ? CKAN_FW(4, true) : CKAN_FW(4, false); break;

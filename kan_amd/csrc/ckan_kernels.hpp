@@ -165,9 +165,15 @@ void launch_dc_sum(const float* part, int S, float* dC, DcOut om, const Plan& p,
 // reduce_bias = false) and the forward must reduce them; the pipelined kernel
 // does so in its epilogue (and fills the bias slot) when fwd_sums_bias holds,
 // the caller launches the reduction first otherwise.
+// out_tanh: store tanh(y) in place of y (the next layer's tanh cache in a
+// stack; needs fwd_out_tanh_ok).
 void launch_fwd_gemm(const float* x, float* t, const void* packed, float* y, void* ws,
-                     const Plan& p, const FwdChoice& c, hipStream_t s, bool sum_bias = false);
+                     const Plan& p, const FwdChoice& c, hipStream_t s, bool sum_bias = false,
+                     bool out_tanh = false);
 bool fwd_sums_bias(const Plan& p, const FwdChoice& c);
+// The forward path of p can store tanh(y) in place of y (the pipelined
+// kernel, unsplit).
+bool fwd_out_tanh_ok(const Plan& p);
 // bias = sum of the per-input-block partials, into the packed buffer's bias slot
 void launch_bias_reduce(void* packed, const Plan& p, hipStream_t s);
 void launch_dx_gemm(const void* dYx, const void* packed, const float* t, float* dx,
@@ -183,6 +189,16 @@ void launch_sgd(float* p, const float* g, int64_t n, float lr, float wd, hipStre
 int backward_impl(const struct ckan_desc* desc, const float* t_cache, const void* packed,
                   const float* dy, float* dx, float* dcoeffs, DcOut om, void* ws,
                   size_t ws_bytes, void* stream);
+// ckan_pack_forward (no basis spec) for a layer inside a stack: t_ready, the
+// tanh cache already holds the layer's input map (x unused; the layer's
+// forward must read the cache); out_tanh, store tanh(y) into `out` (the next
+// layer's tanh cache) in place of y (needs fwd_out_tanh_ok).
+int pack_forward_ex(const struct ckan_desc* desc, const void* coeffs, void* packed,
+                    const float* x, float* out, float* t_cache, void* ws, size_t ws_bytes,
+                    void* stream, bool t_ready, bool out_tanh);
+// Whether the layer of desc can take t_ready / out_tanh in pack_forward_ex.
+bool layer_reads_tcache(const struct ckan_desc* desc);
+bool layer_out_tanh_ok(const struct ckan_desc* desc);
 void launch_adam(float* p, const float* g, float* m, float* v, int64_t n, float w1, float beta2,
                  float one_m_beta2, float bc2_sqrt, float eps, float neg_step, float wd,
                  hipStream_t s);

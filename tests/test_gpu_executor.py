@@ -310,3 +310,36 @@ def test_fit_equals_the_step_loop(widths, degrees, B, loss, opt):
         assert torch.equal(exs[0].get_coeffs(l), exs[1].get_coeffs(l))
     for ex in exs:
         ex.close()
+
+
+def test_hidden_layers_store_tanh_into_the_next_cache():
+    """At large batches a hidden layer's forward writes tanh(y) straight into
+    the next layer's tanh cache (no y, no separate tanh pass).  The training
+    step's loss must equal the MSE of the executor's plain forward (which
+    takes the unfused path) bit for bit up to the host-side mean, and the
+    step must follow the oracle."""
+    from kan_amd import ResidentExecutor
+    widths, degrees, B, lr = [128, 256, 256, 16], [8, 8, 8], 32768, 0.01
+    print(f"executor tanh-out widths={widths} B={B}", flush=True)
+    g = torch.Generator().manual_seed(61)
+    x = torch.rand(B, widths[0], generator=g) * 6 - 3
+    y = torch.randn(B, widths[-1], generator=g)
+    torch.manual_seed(62)
+    coeffs = [orc.init_coeffs(widths[l], widths[l + 1], degrees[l]) for l in range(3)]
+    ex = ResidentExecutor(widths, degrees, B, compute="bf16", loss="mse", optimizer="sgd", lr=lr)
+    for l, c in enumerate(coeffs):
+        ex.set_coeffs(l, c)
+    xd, yd = x.cuda(), y.cuda()
+    out0 = ex.forward(xd)
+    mse0 = torch.mean((out0.double() - yd.double()) ** 2).item()
+    l0 = ex.step(xd, yd).item()
+    assert abs(l0 - mse0) <= 1e-6 * mse0, (l0, mse0)
+    rows = torch.randperm(B, generator=torch.Generator().manual_seed(63))[:512]
+    ref = orc.mlp_forward(x[rows], coeffs, bf16_coeffs=True)
+    assert _rel(out0.cpu()[rows], ref) <= 2e-2
+    out1 = ex.forward(xd)
+    mse1 = torch.mean((out1.double() - yd.double()) ** 2).item()
+    l1 = ex.step(xd, yd).item()
+    assert abs(l1 - mse1) <= 1e-6 * mse1, (l1, mse1)
+    assert l1 < l0
+    ex.close()
