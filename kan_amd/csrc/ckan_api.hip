@@ -126,6 +126,14 @@ inline const float* valu_rec(const ckan_desc* d, const void* packed) {
   return reinterpret_cast<const float*>(static_cast<const char*>(packed) + valu_rec_offset(d));
 }
 
+// The vector-ALU dx launch puts 8 inputs per block on grid y (at most 65535).
+int valu_backward_shape_ok(const ckan_desc* d) {
+  if ((d->in_dim + 7) / 8 > 65535)
+    return fail(CKAN_ERR_UNSUPPORTED, "in_dim %d above 524280 is not supported by the vector-ALU "
+                "backward (degree above 16 or fp64)", d->in_dim);
+  return CKAN_OK;
+}
+
 // Paths that implement only the tanh input map.
 int require_tanh_map(const ckan_desc* d, const char* what) {
   if (d->input_map != CKAN_INPUT_TANH)
@@ -182,6 +190,7 @@ int ckan::backward_impl(const ckan_desc* desc, const float* t_cache, const void*
   if (!need_dx && !need_dc) return CKAN_OK;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (valu_route(desc)) {
+    if ((rc = valu_backward_shape_ok(desc))) return rc;
     if (desc->batch == 0) {
       if (need_dc && om.mode >= kDcSgd)
         return fail(CKAN_ERR_UNSUPPORTED, "backward: an optimizer-applying call needs batch >= 1");
@@ -498,6 +507,7 @@ int ckan_backward_f64(const ckan_desc* desc, const double* t_cache, const double
   if (desc->compute != CKAN_COMPUTE_FP32 || desc->coeff_dtype != CKAN_DTYPE_F32)
     return fail(CKAN_ERR_INVALID_ARG, "fp64 path: desc->compute and desc->coeff_dtype must be 0");
   if ((rc = require_tanh_map(desc, "fp64 path"))) return rc;
+  if ((rc = valu_backward_shape_ok(desc))) return rc;
   if (!dx && !dcoeffs) return CKAN_OK;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (desc->batch == 0) {

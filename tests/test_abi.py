@@ -77,6 +77,10 @@ def test_high_degree_sizes_and_limits():
             assert lib.ckan_tcache_elems(d) == B * I
             assert lib.ckan_fwd_workspace_bytes(d) == 0
             assert lib.ckan_bwd_workspace_bytes(d, 1, 1) == 0
+    # the vector-ALU backward puts 8 inputs per block on grid y: in_dim <= 524280
+    big = _lib.make_desc(4, 524288, 2, 20, 0, 0)
+    assert lib.ckan_backward(big, 256, 256, 256, 256, 256, 0, None, 0, None) == _lib.CKAN_ERR_UNSUPPORTED
+    assert b"524280" in lib.ckan_last_error()
     # the affine input map (finite-domain Hermite) is served at every degree
     for deg in (16, 17, 256):
         assert lib.ckan_packed_bytes(_lib.make_desc(8, 4, 3, deg, 0, 0, (0.5, 0.1))) > 0
