@@ -745,7 +745,7 @@ k_fwd_reduce(const float* __restrict__ part, int S, const float* __restrict__ bi
 }
 
 // ---------------------------------------------------------------------------
-// Forward, very small batch (B <= 4), one launch: column-owning blocks.
+// Forward, very small batch (B <= 16), one launch: column-owning blocks.
 // Block b owns one 8-output stream of the bf16 coefficients (cf_bf16_elem)
 // and the whole reduction, so no split-K partials and no second launch; with
 // 2048 outputs that is 256 blocks, one per CU.  Its 16 waves split the
@@ -776,6 +776,15 @@ struct FwdCols {
   static constexpr int VPR = 4 * U;                    // vectors per row per batch
   static constexpr int NV = R * VPR;                   // vectors per batch
   static constexpr int PASSES = (NV + 63) / 64;
+  // LDS slots of a wave: vector (step j, k-group gg, row r) at (4 j + gg) RP + r.
+  // The vector-building lanes of one row write 4U different (j, gg) at once;
+  // an odd pitch spreads them over the banks (pitch R >= 4: 16-byte slots a
+  // multiple of 64 bytes apart, 16 lanes on one bank group).
+  static constexpr int RP = R >= 4 ? R + 1 : R;
+  static constexpr int SLOTS = 4 * U * RP;
+  // Above 4 rows the tanh values come from the tanh cache (written by
+  // launch_tanh): tanh per vector made the kernel vector-ALU-bound.
+  static constexpr bool TPRE = R > 4;
 };
 
 __device__ __forceinline__ void mma16(f32x4_t& acc, const bf16x8_t& a, const bf16x8_t& b) {
@@ -801,7 +810,7 @@ k_fwd_cols(const float* __restrict__ x, float* __restrict__ tc, const uint16_t* 
   typedef FwdGroup<P> G;
   constexpr int U = K::U, NL = K::NL, NU = K::NU, SGK = G::SGK, PASSES = K::PASSES;
   static_assert(K::KBB % SGK == 0, "a batch holds whole super-groups");
-  __shared__ bf16x8_t vec[K::WAVES][U][4][R];
+  __shared__ bf16x8_t vec[K::WAVES][K::SLOTS];
   __shared__ float red[K::WAVES][16][8];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -862,7 +871,9 @@ k_fwd_cols(const float* __restrict__ x, float* __restrict__ tc, const uint16_t* 
       const int64_t r = jb.r < p.B ? jb.r : p.B - 1;
       const int i0 = (bb * K::SGB + jb.sgl) * G::SGI + jb.off;
 #pragma unroll
-      for (int u = 0; u < NU; ++u) xv[buf][q][u] = x[r * p.I + min(i0 + u, p.I - 1)];
+      for (int u = 0; u < NU; ++u)
+        xv[buf][q][u] = K::TPRE ? tc[r * p.I_sg + min(i0 + u, p.I_sg - 1)]
+                                : x[r * p.I + min(i0 + u, p.I - 1)];
     }
 #pragma unroll
     for (int l = 0; l < NL; ++l) {
@@ -884,8 +895,10 @@ k_fwd_cols(const float* __restrict__ x, float* __restrict__ tc, const uint16_t* 
       float tv[NU];
 #pragma unroll
       for (int u = 0; u < NU; ++u)
-        tv[u] = (sg < nsg && i0 + u < p.I) ? input_map(xv[buf][q][u], p.imap, p.ima, p.imb) : 0.0f;
-      if (writes_t && live && jb.on && jb.r < p.B && sg < nsg) {
+        tv[u] = (sg < nsg && i0 + u < p.I)
+            ? (K::TPRE ? xv[buf][q][u] : input_map(xv[buf][q][u], p.imap, p.ima, p.imb))
+            : 0.0f;
+      if (!K::TPRE && writes_t && live && jb.on && jb.r < p.B && sg < nsg) {
         if constexpr (P <= 8) {
 #pragma unroll
           for (int u = 0; u < NU; ++u) tc[(int64_t)jb.r * p.I_sg + i0 + u] = tv[u];
@@ -906,7 +919,7 @@ k_fwd_cols(const float* __restrict__ x, float* __restrict__ tc, const uint16_t* 
       }
       // batches past the wave's range, and super-groups past the last, add nothing
       const bf16x8_t a = (live && sg < nsg) ? make_frag_bf(vals).v : bf16x8_t{};
-      if (jb.on) vec[wave][jb.j][jb.gg][jb.r] = a;
+      if (jb.on) vec[wave][(4 * jb.j + jb.gg) * K::RP + jb.r] = a;
     }
     // the wave reads other lanes' writes of its own area: wait for them to
     // complete (without the wait, reads have returned stale vectors on
@@ -915,8 +928,8 @@ k_fwd_cols(const float* __restrict__ x, float* __restrict__ tc, const uint16_t* 
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
     for (int l = 0; l < NL; ++l) {
-      mma16(acc, vec[wave][2 * l][G4][rl], fb[buf][l]);
-      mma16(acc, vec[wave][2 * l + 1][G4][rl], row_rotate8(fb[buf][l]));
+      mma16(acc, vec[wave][(4 * (2 * l) + G4) * K::RP + rl], fb[buf][l]);
+      mma16(acc, vec[wave][(4 * (2 * l + 1) + G4) * K::RP + rl], row_rotate8(fb[buf][l]));
     }
   };
 
@@ -2017,11 +2030,11 @@ constexpr int kFwdColsMinBlocks = 256;
 
 FwdChoice choose_fwd(const Plan& p) {
   FwdChoice c;
-  if (p.B <= (p.P == 2 ? 2 : 4) && p.esz == 2 && p.O32 / 8 >= kFwdColsMinBlocks) {
+  if (p.B <= (p.P == 2 ? 2 : 16) && p.esz == 2 && p.O32 / 8 >= kFwdColsMinBlocks) {
     // enough 8-output streams to spread the coefficient stream over the chip
     // without a split reduction: one launch
     c.tile = kFwdCols;
-    c.bm = p.B <= 1 ? 1 : p.B <= 2 ? 2 : 4;
+    c.bm = p.B <= 1 ? 1 : p.B <= 2 ? 2 : p.B <= 4 ? 4 : p.B <= 8 ? 8 : 16;
     c.bnf = 8;
     c.tiles_m = 1;
     c.tiles_n = p.O32 / 8;
@@ -2095,7 +2108,11 @@ static void fwd_dispatch(const float* x, float* t, const void* packed, float* y,
       // degree 2 (four inputs per vector in registers) up to 2 rows
       if (c.bm == 1) CKAN_COLS(1);
       else if (c.bm == 2) CKAN_COLS(2);
-      else if constexpr (P > 2) CKAN_COLS(4);
+      else if constexpr (P > 2) {
+        if (c.bm == 4) CKAN_COLS(4);
+        else if (c.bm == 8) CKAN_COLS(8);
+        else CKAN_COLS(16);
+      }
 #undef CKAN_COLS
     }
     return;

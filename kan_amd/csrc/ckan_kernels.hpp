@@ -34,7 +34,7 @@ inline size_t packed_bytes(const Plan& p) {
 // Tile shapes (waves along M x waves along N, fragments per wave M x N):
 enum FwdTile {
   kFwdBig = 0, kFwdSmall32 = 1, kFwdSmall64 = 2, kFwdStream32 = 3, kFwdStream64 = 4,
-  kFwdCols = 5    // B <= 4, bf16: column-owning blocks, one launch, tanh computed in the kernel
+  kFwdCols = 5    // B <= 16, bf16: column-owning blocks, one launch (tanh in the kernel up to 4 rows)
 };
 struct FwdChoice {
   int tile;           // FwdTile
@@ -44,12 +44,13 @@ struct FwdChoice {
 };
 FwdChoice choose_fwd(const Plan& p);
 inline bool fwd_streaming(const FwdChoice& c) { return c.tile == kFwdStream32 || c.tile == kFwdStream64; }
-// The 32-row streaming forward and the column-owning forward compute tanh
-// themselves (each value is needed by every column block, cheap
-// at <= 32 rows); every other path reads the tanh cache written by
-// launch_tanh first.
+// The 32-row streaming forward and the column-owning forward up to 4 rows
+// compute tanh themselves (each value is needed by every column block, cheap
+// at few rows); every other path reads the tanh cache written by launch_tanh
+// first (the column-owning forward at 5..16 rows is vector-ALU-bound
+// otherwise).
 inline bool fwd_reads_tcache(const FwdChoice& c) {
-  return c.tile != kFwdStream32 && c.tile != kFwdCols;
+  return c.tile != kFwdStream32 && !(c.tile == kFwdCols && c.bm <= 4);
 }
 // split-K partials [splits][B32][O32] fp32, summed in order by k_fwd_reduce
 inline size_t fwd_ws_bytes(const Plan& p, const FwdChoice& c) {
