@@ -139,7 +139,9 @@ int ckan_forward_noalloc(const ckan_desc* desc, const float* x, const void* pack
  *   dx[b, i]    = (1 - t^2) sum_{o, d} dy[b, o] C[i, o, d] d U_{d-1}(t)   (dx may be NULL)
  *   dC[i, o, d] = sum_b T_d(t[b, i]) dy[b, o]                            (dcoeffs may be NULL)
  * With accumulate != 0, dC is added to the existing contents of dcoeffs
- * (torch AccumulateGrad semantics); otherwise it is overwritten.
+ * (torch AccumulateGrad semantics); otherwise it is overwritten.  packed may
+ * be NULL when dx is NULL, except above degree 16, where it also carries the
+ * basis recurrence that dC needs.
  * Replaces: torch autograd through kan/basis/chebyshev.py:78,101,136-145
  * (BmmBackward0 x2, CosBackward0, MulBackward0, AcosBackward0, TanhBackward0).
  * Divergence: for |x| >= 9.0108, where fp32 tanh(x) == +-1, the reference

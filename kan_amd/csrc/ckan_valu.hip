@@ -76,7 +76,8 @@ __device__ __forceinline__ void rec_step(T w, const float* rs, int D, int n, T& 
 
 // The recurrence block into LDS (fp32 with a block), before the block's
 // first barrier; after it, rec_generic tells whether the block asks for the
-// generic recurrence (a uniform branch around each tile's loops).
+// generic recurrence (a uniform branch around the kernel's body, which is
+// instantiated once per recurrence kind).
 template <typename T>
 __device__ __forceinline__ void stage_rec(float* rs, const float* __restrict__ rec, int D) {
   if constexpr (sizeof(T) == 4) {
@@ -90,9 +91,9 @@ __device__ __forceinline__ bool rec_generic(const float* rs, const float* rec, i
   else return false;
 }
 
-// SEEK = false instantiations serve the first chunk (d0 = 0, stored, not
-// accumulated) with no seek loops in the code, as register-lean as a
-// single-chunk kernel.
+// dx and dC: SEEK = false instantiations serve the first (or only) chunk (d0
+// = 0, stored, not accumulated) with no seek loops in the code, as
+// register-lean as a single-chunk kernel.
 
 // Register tile widths: rows per thread of the forward (WF), of dx (WX) and
 // outputs per thread of dC (WC).  The fp64 forward on chunks of up to 9
