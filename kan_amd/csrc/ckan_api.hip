@@ -226,15 +226,16 @@ int ckan::backward_impl(const ckan_desc* desc, const float* t_cache, const void*
   const BwdLayout L = bwd_layout(p, need_dx, need_dc);
   if (ws_bytes < L.total)
     return fail(CKAN_ERR_WORKSPACE, "backward workspace too small: %zu < %zu bytes", ws_bytes, L.total);
-  if (!ws || !aligned16(ws)) return fail(CKAN_ERR_INVALID_ARG, "workspace is NULL or misaligned");
+  if (L.total > 0 && (!ws || !aligned16(ws)))
+    return fail(CKAN_ERR_INVALID_ARG, "workspace is NULL or misaligned");
   char* w = reinterpret_cast<char*>(ws);
   void* dYx = w + L.dyx_off;
   void* dYc = w + L.dyc_off;
   float* colsum = reinterpret_cast<float*>(w + L.colsum_off);
   float* part = reinterpret_cast<float*>(w + L.part_off);
-  {
+  if (need_dx || !L.dc_small) {  // the small dC reads dy itself
     ProfScope ps("prep_dy", s);
-    launch_prep_dy(dy, dYx, dYc, colsum, p, need_dx, need_dc, s);
+    launch_prep_dy(dy, dYx, dYc, colsum, p, need_dx, need_dc && !L.dc_small, s);
   }
   if ((rc = check_launch("prep_dy"))) return rc;
   if (need_dx) {
@@ -242,6 +243,11 @@ int ckan::backward_impl(const ckan_desc* desc, const float* t_cache, const void*
     launch_dx_gemm(dYx, packed, t_cache, dx, p, s);
   }
   if ((rc = check_launch("dx_gemm"))) return rc;
+  if (need_dc && L.dc_small) {
+    ProfScope ps("dc_gemm", s);
+    launch_dc_small(dy, t_cache, dcoeffs, om, p, s);
+    return check_launch("dc_small");
+  }
   if (need_dc) {
     // the pipelined dC kernel reduces the column-sum partials itself
     const float* colsum_r = nullptr;

@@ -588,6 +588,77 @@ void launch_bias_reduce(void* packed, const Plan& p, hipStream_t s) {
                        p.O32, p.O32, reinterpret_cast<float*>(base + packed_biasf_offset(p)));
 }
 
+// Small dC: dC[i, o, d] = sum_b T_d(t[b, i]) dy[b, o] in fp32 for problems
+// whose MFMA pipeline would be all prologue (config 2: B = 256).  A block
+// takes 8 inputs x 8 outputs; its 256 threads are 64 (input, output) pairs x
+// 4 row quarters.  t [B][8] and dy [B][8] are staged in LDS, each thread
+// accumulates its pair's D sums over its quarter of the rows (Chebyshev
+// recurrence in registers), and the quarters are added in order through LDS.
+constexpr int kDcSmallRows = 512;  // rows staged at once
+template <int DMAX>
+__global__ void __launch_bounds__(256)
+k_dc_small(const float* __restrict__ dy, const float* __restrict__ t, float* __restrict__ dC,
+           DcOut om, Plan p) {
+  __shared__ float ts[kDcSmallRows][9];
+  __shared__ float ys[kDcSmallRows][9];
+  __shared__ float red[4][64][DMAX + 1];
+  const int tid = threadIdx.x, q = tid & 63, rq = tid >> 6;
+  const int il = q >> 3, ol = q & 7;
+  const int i0 = blockIdx.x * 8, o0 = blockIdx.y * 8;
+  const int D = p.D;
+  const int rows = (int)p.B;  // <= kDcSmallRows (dc_small_ok)
+  for (int k = tid; k < rows * 8; k += 256) {
+    const int r = k >> 3, c = k & 7;
+    ts[r][c] = i0 + c < p.I ? t[(int64_t)r * p.I_sg + i0 + c] : 0.0f;
+    ys[r][c] = o0 + c < p.O ? dy[(int64_t)r * p.O + o0 + c] : 0.0f;
+  }
+  __syncthreads();
+  float acc[DMAX];
+#pragma unroll
+  for (int d = 0; d < DMAX; ++d) acc[d] = 0.0f;
+  const int per = (rows + 3) / 4, r0 = rq * per, r1 = min(rows, r0 + per);
+  for (int r = r0; r < r1; ++r) {
+    const float tv = ts[r][il], yv = ys[r][ol], t2 = tv + tv;
+    float pm = tv, pc = 1.0f;  // T_{-1} = t, T_0 = 1
+#pragma unroll
+    for (int d = 0; d < DMAX; ++d) {
+      acc[d] = fmaf(pc, yv, acc[d]);
+      const float nx = fmaf(t2, pc, -pm);
+      pm = pc;
+      pc = nx;
+    }
+  }
+#pragma unroll
+  for (int d = 0; d < DMAX; ++d) red[rq][q][d] = acc[d];
+  __syncthreads();
+  const int i = i0 + il, o = o0 + ol;
+  if (rq == 0 && i < p.I && o < p.O) {
+    float* dst = dC + ((size_t)i * p.O + o) * D;
+#pragma unroll
+    for (int d = 0; d < DMAX; ++d)
+      if (d < D) dc_write(dst + d, ((red[0][q][d] + red[1][q][d]) + red[2][q][d]) + red[3][q][d], om);
+  }
+}
+
+bool dc_small_ok(const Plan& p) {
+  // fp32 work ~ pairs * rows * (2 D + 2) lane-instructions: below ~2^28 the
+  // vector ALU finishes in a few microseconds, ahead of the pipelined kernel's
+  // prologue (and its split sum)
+  const int64_t pairs = (int64_t)p.I * p.O;
+  return p.B >= 1 && p.B <= kDcSmallRows && pairs * p.B * (2 * p.D + 2) <= ((int64_t)1 << 28);
+}
+
+void launch_dc_small(const float* dy, const float* t, float* dC, DcOut om, const Plan& p,
+                     hipStream_t s) {
+  const dim3 grid((unsigned)ceil_div(p.I, 8), (unsigned)ceil_div(p.O, 8));
+  switch (p.P) {
+    case 2: hipLaunchKernelGGL((k_dc_small<3>), grid, dim3(256), 0, s, dy, t, dC, om, p); break;
+    case 4: hipLaunchKernelGGL((k_dc_small<5>), grid, dim3(256), 0, s, dy, t, dC, om, p); break;
+    case 8: hipLaunchKernelGGL((k_dc_small<9>), grid, dim3(256), 0, s, dy, t, dC, om, p); break;
+    default: hipLaunchKernelGGL((k_dc_small<17>), grid, dim3(256), 0, s, dy, t, dC, om, p); break;
+  }
+}
+
 void launch_prep_dy(const float* dy, void* dYx, void* dYc, float* colsum_part, const Plan& p,
                     bool need_dx, bool need_dc, hipStream_t s) {
   const int64_t dx_rows = need_dx ? dx_row_frags(p) * 32 : 0;  // dYx rows incl. zero padding

@@ -2299,8 +2299,10 @@ static void dc_pipe_shape(const Plan& p, int& no, int& ki) {
   }
 }
 
-BwdLayout bwd_layout(const Plan& p, bool need_dx, bool need_dc) {
+BwdLayout bwd_layout(const Plan& p, bool need_dx, bool need_dc_arg) {
   BwdLayout L;
+  L.dc_small = need_dc_arg && dc_small_ok(p);
+  const bool need_dc = need_dc_arg && !L.dc_small;  // the re-laid operands and partials
   size_t off = 0;
   L.dyx_off = off;
   if (need_dx) off += align256((size_t)dx_row_frags(p) * p.KBx * kFragElems * p.esz);

@@ -66,6 +66,7 @@ struct BwdLayout {
   size_t dyx_off, dyc_off, colsum_off, part_off, total;
   int dc_splits, dc_st_per_split;
   bool dc_pipe;
+  bool dc_small;  // dC by launch_dc_small (no dy re-layout, no partials)
 };
 BwdLayout bwd_layout(const Plan& p, bool need_dx, bool need_dc);
 
@@ -181,6 +182,11 @@ void launch_dx_gemm(const void* dYx, const void* packed, const float* t, float* 
                     const Plan& p, hipStream_t s);
 // colsum: the per-64-row column-sum partials for the pipelined kernel (which
 // reduces them itself), the reduced row otherwise.
+// Small, latency-bound dC (few rows, few (input, output) pairs): fp32 on the
+// vector ALU straight from dy and the tanh cache, one launch, written by om.
+bool dc_small_ok(const Plan& p);
+void launch_dc_small(const float* dy, const float* t, float* dC, DcOut om, const Plan& p,
+                     hipStream_t s);
 void launch_dc_gemm(const void* dYc, const float* t, const float* colsum, float* part, float* dC,
                     DcOut om, const Plan& p, const BwdLayout& L, hipStream_t s);
 void launch_sgd(float* p, const float* g, int64_t n, float lr, float wd, hipStream_t s);

@@ -135,15 +135,28 @@ def test_null_pointers_rejected_before_launch():
 
 def test_workspace_too_small_is_reported():
     lib = _lib.load()
-    d = _desc(B=16, I=2048, O=2048, deg=8, compute=1, cdt=1)
+    d = _desc(B=24, I=2048, O=2048, deg=8, compute=1, cdt=1)
     need = lib.ckan_fwd_workspace_bytes(ctypes.byref(d))
-    assert need > 0  # 16 rows take the split-K streaming forward (partials)
-    # up to 4 rows at 2048+ outputs take the one-launch forward: no workspace
-    assert lib.ckan_fwd_workspace_bytes(ctypes.byref(_desc(B=1, I=2048, O=2048, deg=8, compute=1,
-                                                           cdt=1))) == 0
+    assert need > 0  # 24 rows take the split-K streaming forward (partials)
+    # up to 16 rows at 2048+ outputs take the one-launch forward: no workspace
+    for rows in (1, 4, 16):
+        assert lib.ckan_fwd_workspace_bytes(ctypes.byref(_desc(B=rows, I=2048, O=2048, deg=8,
+                                                               compute=1, cdt=1))) == 0
     rc = lib.ckan_forward(ctypes.byref(d), 16, 16, 16, 16, 16, need - 256, None)
     assert rc == _lib.CKAN_ERR_WORKSPACE
     assert b"workspace" in lib.ckan_last_error()
+
+
+def test_small_backward_needs_no_dc_workspace():
+    """Latency-bound layers (few rows, few (input, output) pairs) take the
+    small vector-ALU dC: no dy re-layout for it, no split partials, so a
+    dC-only backward needs no workspace; with dx the dY re-layout remains."""
+    lib = _lib.load()
+    d = _desc(B=256, I=784, O=64, deg=4)
+    assert lib.ckan_bwd_workspace_bytes(ctypes.byref(d), 0, 1) == 0
+    assert lib.ckan_bwd_workspace_bytes(ctypes.byref(d), 1, 1) > 0
+    big = _desc(B=8192, I=1024, O=1024, deg=8, compute=1)
+    assert lib.ckan_bwd_workspace_bytes(ctypes.byref(big), 0, 1) > 0
 
 
 def test_empty_calls_are_noops():
