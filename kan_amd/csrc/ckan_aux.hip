@@ -607,10 +607,22 @@ k_dc_small(const float* __restrict__ dy, const float* __restrict__ t, float* __r
   const int i0 = blockIdx.x * 8, o0 = blockIdx.y * 8;
   const int D = p.D;
   const int rows = (int)p.B;  // <= kDcSmallRows (dc_small_ok)
-  for (int k = tid; k < rows * 8; k += 256) {
-    const int r = k >> 3, c = k & 7;
-    ts[r][c] = i0 + c < p.I ? t[(int64_t)r * p.I_sg + i0 + c] : 0.0f;
-    ys[r][c] = o0 + c < p.O ? dy[(int64_t)r * p.O + o0 + c] : 0.0f;
+  // every load of the staging in flight at once (a rolled loop waited for
+  // each pair of loads in turn: 8 round trips at 256 rows)
+  constexpr int NLD = kDcSmallRows * 8 / 256;
+  float tl[NLD], yl[NLD];
+#pragma unroll
+  for (int u = 0; u < NLD; ++u) {
+    const int k = tid + 256 * u, r = k >> 3, c = k & 7;
+    const bool in = r < rows;
+    tl[u] = in && i0 + c < p.I ? t[(int64_t)r * p.I_sg + i0 + c] : 0.0f;
+    yl[u] = in && o0 + c < p.O ? dy[(int64_t)r * p.O + o0 + c] : 0.0f;
+  }
+#pragma unroll
+  for (int u = 0; u < NLD; ++u) {
+    const int k = tid + 256 * u, r = k >> 3, c = k & 7;
+    ts[r][c] = tl[u];
+    ys[r][c] = yl[u];
   }
   __syncthreads();
   float acc[DMAX];
