@@ -625,30 +625,51 @@ k_dc_small(const float* __restrict__ dy, const float* __restrict__ t, float* __r
     ys[r][c] = yl[u];
   }
   __syncthreads();
-  float acc[DMAX];
+  // rows 4 at a time with 4 accumulator sets: independent recurrences and
+  // LDS reads in flight together (one row at a time was latency-bound);
+  // the sets are added in order at the end
+  constexpr int RU = 4;
+  float acc[RU][DMAX];
 #pragma unroll
-  for (int d = 0; d < DMAX; ++d) acc[d] = 0.0f;
+  for (int u = 0; u < RU; ++u)
+#pragma unroll
+    for (int d = 0; d < DMAX; ++d) acc[u][d] = 0.0f;
   const int per = (rows + 3) / 4, r0 = rq * per, r1 = min(rows, r0 + per);
-  for (int r = r0; r < r1; ++r) {
-    const float tv = ts[r][il], yv = ys[r][ol], t2 = tv + tv;
-    float pm = tv, pc = 1.0f;  // T_{-1} = t, T_0 = 1
+  for (int r = r0; r < r1; r += RU) {
+    float tv[RU], yv[RU];
 #pragma unroll
-    for (int d = 0; d < DMAX; ++d) {
-      acc[d] = fmaf(pc, yv, acc[d]);
-      const float nx = fmaf(t2, pc, -pm);
-      pm = pc;
-      pc = nx;
+    for (int u = 0; u < RU; ++u) {  // rows past r1 add zero (their dy is masked)
+      const bool in = r + u < r1;
+      tv[u] = ts[in ? r + u : r][il];
+      yv[u] = in ? ys[r + u][ol] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < RU; ++u) {
+      const float t2 = tv[u] + tv[u];
+      float pm = tv[u], pc = 1.0f;  // T_{-1} = t, T_0 = 1
+#pragma unroll
+      for (int d = 0; d < DMAX; ++d) {
+        acc[u][d] = fmaf(pc, yv[u], acc[u][d]);
+        const float nx = fmaf(t2, pc, -pm);
+        pm = pc;
+        pc = nx;
+      }
     }
   }
 #pragma unroll
-  for (int d = 0; d < DMAX; ++d) red[rq][q][d] = acc[d];
+  for (int d = 0; d < DMAX; ++d) red[rq][q][d] = ((acc[0][d] + acc[1][d]) + acc[2][d]) + acc[3][d];
   __syncthreads();
-  const int i = i0 + il, o = o0 + ol;
-  if (rq == 0 && i < p.I && o < p.O) {
-    float* dst = dC + ((size_t)i * p.O + o) * D;
-#pragma unroll
-    for (int d = 0; d < DMAX; ++d)
-      if (d < D) dc_write(dst + d, ((red[0][q][d] + red[1][q][d]) + red[2][q][d]) + red[3][q][d], om);
+  // the block's 8 x 8 x D results, spread over all threads: input il's 8
+  // outputs are one contiguous run of 8 D floats of dC (one round trip for
+  // the read-modify-write modes instead of D)
+  const int ovalid = min(8, p.O - o0);
+  for (int k = tid; k < 64 * D; k += 256) {
+    const int kil = k / (8 * D), rem = k - kil * 8 * D, kol = rem / D, d = rem - kol * D;
+    const int i = i0 + kil;
+    if (i >= p.I || kol >= ovalid) continue;
+    const int kq = kil * 8 + kol;
+    const float g = ((red[0][kq][d] + red[1][kq][d]) + red[2][kq][d]) + red[3][kq][d];
+    dc_write(dC + ((size_t)i * p.O + o0) * D + rem, g, om);
   }
 }
 
