@@ -594,7 +594,7 @@ void launch_bias_reduce(void* packed, const Plan& p, hipStream_t s) {
 // 4 row quarters.  t [B][8] and dy [B][8] are staged in LDS, each thread
 // accumulates its pair's D sums over its quarter of the rows (Chebyshev
 // recurrence in registers), and the quarters are added in order through LDS.
-constexpr int kDcSmallRows = 512;  // rows staged at once
+constexpr int kDcSmallRows = 256;  // rows staged at once (all of the batch)
 template <int DMAX>
 __global__ void __launch_bounds__(256)
 k_dc_small(const float* __restrict__ dy, const float* __restrict__ t, float* __restrict__ dC,
@@ -735,14 +735,16 @@ __global__ void __launch_bounds__(256)
 k_dc_sum(const float* __restrict__ part, int S, float* __restrict__ dC, int64_t n, DcOut om) {
   for (int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; q < n;
        q += (int64_t)gridDim.x * blockDim.x) {
+    // 16 loads in flight per round trip, added in split order
     float acc = 0.0f;
-    int z = 0;
-    for (; z + 4 <= S; z += 4) {
-      const float a = part[(size_t)z * n + q], b = part[(size_t)(z + 1) * n + q];
-      const float c = part[(size_t)(z + 2) * n + q], d = part[(size_t)(z + 3) * n + q];
-      acc = (((acc + a) + b) + c) + d;
+    for (int z0 = 0; z0 < S; z0 += 16) {
+      float v[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) v[j] = z0 + j < S ? part[(size_t)(z0 + j) * n + q] : 0.0f;
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        if (z0 + j < S) acc += v[j];
     }
-    for (; z < S; ++z) acc += part[(size_t)z * n + q];
     dc_write(dC + q, acc, om);
   }
 }
