@@ -233,14 +233,17 @@ int ckan::backward_impl(const ckan_desc* desc, const float* t_cache, const void*
   void* dYc = w + L.dyc_off;
   float* colsum = reinterpret_cast<float*>(w + L.colsum_off);
   float* part = reinterpret_cast<float*>(w + L.part_off);
-  if (need_dx || !L.dc_small) {  // the small dC reads dy itself
+  // the small kernels read dy themselves
+  const bool prep_x = need_dx && !L.dx_small, prep_c = need_dc && !L.dc_small;
+  if (prep_x || prep_c) {
     ProfScope ps("prep_dy", s);
-    launch_prep_dy(dy, dYx, dYc, colsum, p, need_dx, need_dc && !L.dc_small, s);
+    launch_prep_dy(dy, dYx, dYc, colsum, p, prep_x, prep_c, s);
   }
   if ((rc = check_launch("prep_dy"))) return rc;
   if (need_dx) {
     ProfScope ps("dx_gemm", s);
-    launch_dx_gemm(dYx, packed, t_cache, dx, p, s);
+    if (L.dx_small) launch_dx_small(dy, packed, t_cache, dx, p, s);
+    else launch_dx_gemm(dYx, packed, t_cache, dx, p, s);
   }
   if ((rc = check_launch("dx_gemm"))) return rc;
   if (need_dc && L.dc_small) {

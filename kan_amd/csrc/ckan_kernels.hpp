@@ -67,6 +67,7 @@ struct BwdLayout {
   int dc_splits, dc_st_per_split;
   bool dc_pipe;
   bool dc_small;  // dC by launch_dc_small (no dy re-layout, no partials)
+  bool dx_small;  // dx by launch_dx_small (no dy re-layout)
 };
 BwdLayout bwd_layout(const Plan& p, bool need_dx, bool need_dc);
 
@@ -185,6 +186,11 @@ void launch_dx_gemm(const void* dYx, const void* packed, const float* t, float* 
 // Small, latency-bound dC (few rows, few (input, output) pairs): fp32 on the
 // vector ALU straight from dy and the tanh cache, one launch, written by om.
 bool dc_small_ok(const Plan& p);
+// Small, latency-bound dx (few outputs to reduce over): fp32 on the vector ALU
+// from dy, the packed dX operand (degree-scaled C) and the tanh cache.
+bool dx_small_ok(const Plan& p);
+void launch_dx_small(const float* dy, const void* packed, const float* t, float* dx,
+                     const Plan& p, hipStream_t s);
 void launch_dc_small(const float* dy, const float* t, float* dC, DcOut om, const Plan& p,
                      hipStream_t s);
 void launch_dc_gemm(const void* dYc, const float* t, const float* colsum, float* part, float* dC,

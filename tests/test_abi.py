@@ -149,12 +149,16 @@ def test_workspace_too_small_is_reported():
 
 def test_small_backward_needs_no_dc_workspace():
     """Latency-bound layers (few rows, few (input, output) pairs) take the
-    small vector-ALU dC: no dy re-layout for it, no split partials, so a
-    dC-only backward needs no workspace; with dx the dY re-layout remains."""
+    small vector-ALU dC, and with at most 64 outputs the small vector-ALU dx:
+    both read dy as given, so neither needs a re-layout or split partials.
+    Past 64 outputs dx takes the GEMM and its dY re-layout again."""
     lib = _lib.load()
     d = _desc(B=256, I=784, O=64, deg=4)
     assert lib.ckan_bwd_workspace_bytes(ctypes.byref(d), 0, 1) == 0
-    assert lib.ckan_bwd_workspace_bytes(ctypes.byref(d), 1, 1) > 0
+    assert lib.ckan_bwd_workspace_bytes(ctypes.byref(d), 1, 1) == 0
+    assert lib.ckan_bwd_workspace_bytes(ctypes.byref(d), 1, 0) == 0
+    wide = _desc(B=256, I=64, O=128, deg=4)
+    assert lib.ckan_bwd_workspace_bytes(ctypes.byref(wide), 1, 0) > 0
     big = _desc(B=8192, I=1024, O=1024, deg=8, compute=1)
     assert lib.ckan_bwd_workspace_bytes(ctypes.byref(big), 0, 1) > 0
 
