@@ -11,6 +11,8 @@ reported alongside).
 Prints ONE JSON line.  Besides the driver contract fields it carries
   roofline      for the dominant kernel, from HIP events recorded by the
                 library on the launch stream over a second timed pass
+  library_gemm  torch's bf16 matmul (hipBLASLt) timed on plain operands of
+                the same three GEMM shapes, as a vendor-library reference
   cpu_baseline  the oracle's op-for-op torch restatement of the reference
                 path, timed on this host's cores on a bounded sample
 """
@@ -103,6 +105,24 @@ def _time_loop(fn, iters, warmup):
     e1.record()
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / iters
+
+
+def _library_gemms(iters=50):
+    """torch's bf16 matmul (hipBLASLt) on plain operands of the three config-3
+    contractions, for scale: the same (M, N, K) as the fused kernels, without
+    the basis generation, the degree reduction or the epilogues they fuse.
+    Operands in the (N, T) layout, the fastest of the three tried."""
+    import torch
+    shapes = {"fwd_gemm": (B, O, K), "dx_gemm": (B, I * DEG, O), "dc_gemm": (K, O, B)}
+    out = {}
+    for name, (m, n, k) in shapes.items():
+        a = torch.randn(m, k, device="cuda", dtype=torch.bfloat16)
+        bt = torch.randn(n, k, device="cuda", dtype=torch.bfloat16)
+        ms = _time_loop(lambda: a @ bt.t(), iters, 10)
+        out[name] = {"m": m, "n": n, "k": k, "us": round(ms * 1e3, 1),
+                     "tflops": round(2.0 * m * n * k / (ms * 1e-3) / 1e12, 1)}
+        del a, bt
+    return out
 
 
 SUITE = ("cfg1", "cfg2", "cfg4", "cfg5", "families", "fp64")
@@ -464,6 +484,8 @@ def main():
     ap.add_argument("--no-suite", action="store_true", help="skip configs 1, 2, 4, 5")
     ap.add_argument("--suite-only", default=",".join(SUITE),
                     help="comma list of suite entries to run (default: all of %s)" % (SUITE,))
+    ap.add_argument("--no-library", action="store_true",
+                    help="skip the hipBLASLt reference GEMMs at the same shapes")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="run a plain device copy of this many MiB first (counter calibration)")
     args = ap.parse_args()
@@ -513,6 +535,8 @@ def main():
         t32 = STEP_FLOP / (ms32 * 1e-3) / 1e12
         extra["fp32_variant"] = {"ms_per_step": ms32, "samples_per_s": B / (ms32 * 1e-3),
                                  "tflops": t32, "frac_fp32_peak": t32 / PEAK_FP32_TFLOPS}
+    if not args.no_library and args.compute == "bf16":
+        extra["library_gemm"] = _library_gemms()
 
     out = {
         "metric": "fused ChebyKAN fwd+bwd samples/s & TFLOP/s (% MFMA peak), 1 MI355X",

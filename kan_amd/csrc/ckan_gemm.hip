@@ -1346,6 +1346,241 @@ k_dx_dh(const typename Elem<BF>::type* __restrict__ dYx,
 }
 
 // ---------------------------------------------------------------------------
+// dX at degree 16, bf16: v_mfma_f32_16x16x32_bf16 on 16-input column
+// fragments.  A 32-input block carries 16 x 32 = 512 GEMM columns, so the
+// 32x32 kernel above fits only 128 rows per block and each wave reads 9 KiB
+// of fragments per 8 MFMAs, which made LDS reads its bound at degree 16 (40 %
+// MFMA busy).  Here a tile is 256 rows x 16 inputs x 16 degrees, as big as
+// degree 8's, and each wave reads 12 KiB per 32 (half-size) MFMAs.  Both
+// operands keep their 32-row / 32-input fragment layouts: a 16x16x32
+// fragment (16 rows or inputs, 32 k = two 16-k fragments) is four 256-byte
+// runs of them, gathered by one LDS-DMA copy into 1 KiB ordered by lane, so
+// every fragment read is one contiguous ds_read_b128.  Lane l of a 16x16x32
+// operand holds row (or input) l % 16 at k 8 (l / 16) .. + 7, i.e. 16-k block
+// l / 32, half (l / 16) % 2 of the stored fragments.
+//
+// Persistent: one block per CU walks tiles blockIdx.x, + gridDim.x, ... as one
+// stream of stages, so the copies of a tile's first stages are in flight
+// while the previous tile finishes (its last MFMAs and epilogue) instead of
+// after a new block's launch; with 16 stages per tile (512 outputs) or 2 (64)
+// that start-up was a large share of each tile.  Consecutive tiles of a block
+// keep their input block when the input blocks divide the grid, so each XCD
+// (blocks round-robin over 8) keeps the same few coefficient blocks in L2.
+//
+// Stage (32 k): copies 0-15 = A fragments (rows 16 q .. + 15 of the tile),
+// copies 16-31 = B fragments of degrees 0..15 (16 inputs).  Waves 0-3 issue
+// the A copies after their MFMAs, waves 4-7 the B copies after their fragment
+// reads (each wave four).  The tile's tanh values (256 rows x 16 inputs, for
+// the epilogue) come by 16 more copies, two per wave, issued just before the
+// copies of the tile's first stage, into one of two LDS buffers.  Every wait
+// is on this wave's own copies (vmcnt, in issue order): at each stage only the
+// copies issued one stage earlier may be pending.  The dx stores of a tile go out
+// after the next tile's first barrier, so no wait ever covers stores issued
+// just before it.  Wave (rg, dh) = (wave / 2, wave % 2) owns rows
+// 64 rg .. + 63 (four 16-row fragments) and degrees 8 dh .. + 7.
+// ---------------------------------------------------------------------------
+struct Dx16 {
+  static constexpr int THR = 512, NBUF = 3, ROWS = 256;
+  static constexpr int STAGE_BYTES = 32 * 1024;
+  static constexpr int RING = NBUF * STAGE_BYTES;          // 96 KiB
+  static constexpr int TBUF = ROWS * 16 * 4;               // tanh values of a tile
+  static constexpr int XCH = 8 * 2 * 4 * 64 * 4;           // the dh pairs' exchange
+  static constexpr int LDS_BYTES = RING + 2 * TBUF + XCH;  // 144 KiB
+};
+
+__global__ void __launch_bounds__(512)
+k_dx16(const uint16_t* __restrict__ dYx, const uint16_t* __restrict__ Cb,
+       const float* __restrict__ tc, float* __restrict__ dx, Plan p, int nib16, int ntiles) {
+  typedef Dx16 K;
+  constexpr int P = 16, NBUF = K::NBUF;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int dh = wave & 1, rg = wave >> 1, hw = wave >> 2;
+  const int nst = p.KBx / 2;
+  const int G = gridDim.x;
+  const int mine = (ntiles - (int)blockIdx.x + G - 1) / G;  // tiles of this block (>= 1)
+  const int c4 = lane >> 4, kbl = c4 >> 1, gq = c4 & 1, l16 = lane & 15;
+  const size_t frag_run = (size_t)p.KBx * 1024;  // bytes of one fragment row (all k)
+
+  // per-lane copy offsets, the same for every tile and stage
+  uint32_t off[4];
+#pragma unroll
+  for (int qi = 0; qi < 4; ++qi) {
+    const int q = (wave & 3) * 4 + qi;  // A: 16-row fragment q; B: degree q
+    off[qi] = hw ? (uint32_t)(((size_t)q * p.KBx + kbl) * 1024 + (l16 + 32 * gq) * 16)
+                 : (uint32_t)(((size_t)(q >> 1) * p.KBx + kbl) * 1024 + (16 * (q & 1) + l16 + 32 * gq) * 16);
+  }
+  const uint32_t lring = (uint32_t)(uintptr_t)smem + (uint32_t)(hw * 16 + (wave & 3) * 4) * 1024;
+  const uint32_t ltb = (uint32_t)(uintptr_t)smem + K::RING + (uint32_t)wave * 2048;
+  const float* tbuf = reinterpret_cast<const float*>(smem + K::RING);
+  float* xch = reinterpret_cast<float*>(smem + K::RING + 2 * K::TBUF);
+  // tanh copy j (rows 16 (2 wave + j) .. + 15 of the tile): lane -> row
+  // lane / 4, 16-byte chunk lane % 4 of the tile's 16 inputs
+  const int trow = lane >> 2, tch = lane & 3;
+
+  // issue cursor: tile ik of this block, stage ist, ring slot islot
+  int ik = 0, ist = 0, islot = 0;
+  const char* isrc = nullptr;  // copy base of tile ik (stage 0)
+  auto tile_base = [&](int k) __attribute__((always_inline)) {
+    const int tix = (int)blockIdx.x + (k < mine ? k : mine - 1) * G;
+    const int rb = tix / nib16, ib = tix - rb * nib16;
+    return hw ? reinterpret_cast<const char*>(Cb) + (size_t)(ib >> 1) * P * frag_run + (ib & 1) * 256
+              : reinterpret_cast<const char*>(dYx) + (size_t)rb * 8 * frag_run;
+  };
+  auto issue = [&]() __attribute__((always_inline)) {
+    if (ist == 0) {
+      // the tile's tanh values, ahead of its first stage; past the last tile
+      // the last tile's again, into the buffer no epilogue reads any more
+      // (always two copies, so the waits below can count them)
+      isrc = tile_base(ik);
+      const int tix = (int)blockIdx.x + (ik < mine ? ik : mine - 1) * G;
+      const int rb = tix / nib16, ib = tix - rb * nib16;
+      const int ich = ib * 16 + 4 * tch < p.I_sg ? 4 * tch : 0;  // chunks past the pitch: unused
+      const char* tb = reinterpret_cast<const char*>(tc + ib * 16);
+      const uint32_t l = ltb + (uint32_t)(ik & 1) * K::TBUF;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int64_t r = (int64_t)rb * K::ROWS + 16 * (2 * wave + j) + trow;
+        const int64_t rr = r < p.B ? r : p.B - 1;  // rows past B: unused
+        dma16s(tb, (uint32_t)((rr * p.I_sg + ich) * 4), l + j * 1024);
+      }
+    }
+    // past the last tile: its last stage again (in range, never read)
+    const char* sb = isrc + (size_t)(ik < mine ? ist : nst - 1) * 2048;
+    const uint32_t l = lring + islot * K::STAGE_BYTES;
+#pragma unroll
+    for (int qi = 0; qi < 4; ++qi) dma16s(sb, off[qi], l + qi * 1024);
+    islot = islot + 1 == NBUF ? 0 : islot + 1;
+    if (++ist == nst) {
+      ist = 0;
+      ++ik;
+    }
+  };
+
+  f32x4_t acc[4][8];
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[mi][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  // the previous tile's results, stored after the next tile's first barrier
+  float res[2][4];
+  int64_t rrow0 = 0;   // first row of the pending results (+ 16 m + v)
+  int pend = 0;        // results pending
+  int pcol = 0;        // their input column
+  auto store_pending = [&]() __attribute__((always_inline)) {
+    if (pend) {
+#pragma unroll
+      for (int m = 0; m < 2; ++m)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int64_t r = rrow0 + 16 * m + v;
+          if (pcol < p.I && r < p.B) __builtin_nontemporal_store(res[m][v], dx + r * p.I + pcol);
+        }
+      pend = 0;
+    }
+  };
+
+  pin_sgpr(dx);
+#pragma unroll
+  for (int q = 0; q < NBUF - 1; ++q) issue();
+  int k = 0, st = 0, slot = 0;
+  const int total = mine * nst;
+  for (int gs = 0; gs < total; ++gs) {
+    // this wave's copies of this stage (and everything older) landed; issued
+    // after them: the next stage's four copies, and before a tile's last stage
+    // also the next tile's two tanh copies
+    if (st == nst - 1) wait_vmcnt<4 * (NBUF - 2) + 2>();
+    else wait_vmcnt<4 * (NBUF - 2)>();
+    block_barrier();
+    store_pending();
+    const char* base = smem + slot * K::STAGE_BYTES;
+    bf16x8_t fa[4], fb[8];
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+      fa[mi] = *reinterpret_cast<const bf16x8_t*>(base + (rg * 4 + mi) * 1024 + lane * 16);
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      fb[j] = *reinterpret_cast<const bf16x8_t*>(base + (16 + dh * 8 + j) * 1024 + lane * 16);
+    __builtin_amdgcn_sched_barrier(0);
+    if (hw) issue();
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi) mma16(acc[mi][j], fa[mi], fb[j]);
+    __builtin_amdgcn_sched_barrier(0);
+    if (!hw) issue();
+    slot = slot + 1 == NBUF ? 0 : slot + 1;
+    if (++st < nst) continue;
+
+    // ---- tile k done: epilogue ----
+    const int tix = (int)blockIdx.x + k * G;
+    const int rb = tix / nib16, ib = tix - rb * nib16;
+    const float* tt = tbuf + (size_t)(k & 1) * K::ROWS * 16;
+    const int rl0 = rg * 64 + 4 * c4;  // tile row of (mi, v) = rl0 + 16 mi + v
+    // partial sums over this wave's degrees d = 8 dh + j + 1 (weights U_{d-1})
+    float part[4][4];
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const float t = tt[(rl0 + 16 * mi + v) * 16 + l16];
+        const float t2 = t + t;
+        float up = 0.0f, u = 1.0f;  // U_{-1}, U_0; advanced to U_{8 dh}
+        if (dh) {
+#pragma unroll
+          for (int q = 0; q < 8; ++q) {
+            const float un = fmaf(t2, u, -up);
+            up = u;
+            u = un;
+          }
+        }
+        float sum = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          sum = fmaf(acc[mi][j][v], u, sum);
+          const float un = fmaf(t2, u, -up);
+          up = u;
+          u = un;
+        }
+        part[mi][v] = sum;
+      }
+    // wave (rg, dh) keeps row fragments 2 dh, 2 dh + 1 and hands the other
+    // two to its pair
+    const int keep = 2 * dh, give = 2 - 2 * dh;
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) xch[(((rg * 2 + dh) * 2 + m) * 4 + v) * 64 + lane] = part[give + m][v];
+    wait_lgkmcnt<0>();
+    block_barrier();
+#pragma unroll
+    for (int m = 0; m < 2; ++m)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const float other = xch[(((rg * 2 + (dh ^ 1)) * 2 + m) * 4 + v) * 64 + lane];
+        const float mine_v = part[keep + m][v];
+        // fixed order: the lower degrees' half first
+        const float sum = dh ? other + mine_v : mine_v + other;
+        res[m][v] = sum * input_slope(tt[(rl0 + 16 * (keep + m) + v) * 16 + l16], p);
+      }
+    rrow0 = (int64_t)rb * K::ROWS + rl0 + 16 * keep;
+    pcol = ib * 16 + l16;
+    pend = 1;
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[mi][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    st = 0;
+    ++k;
+  }
+  store_pending();
+  wait_vmcnt<0>();  // the copies past the last tile
+}
+
+// ---------------------------------------------------------------------------
 // dX: one block = 4 waves along rows x one input block (32 inputs x P degrees).
 // B fragments (coefficients, all P degrees of the input block) are shared
 // through LDS; A fragments (dy) are per-wave global loads, prefetched a stage
@@ -2223,12 +2458,31 @@ void launch_fwd_gemm(const float* x, float* t, const void* packed, float* y, voi
 // dX stage depth: 4 k-blocks for bf16; fp32 halves it to bound LDS.
 template <bool BF> struct DxKI { static constexpr int v = BF ? 4 : 2; };
 
+// k_dx16's limits: 32-bit per-lane offsets into the tanh cache and a tile
+// count that fits an int
+static bool dx16_ok(const Plan& p) {
+  return (uint64_t)p.B * p.I_sg * sizeof(float) < (1ull << 32) &&
+         ceil_div(p.B32, Dx16::ROWS) * ceil_div(p.I, 16) < (1ll << 30);
+}
+
 template <int P, bool BF>
 static void dx_dispatch(const void* dYx, const void* packed, const float* t, float* dx,
                         const Plan& p, hipStream_t s) {
   typedef typename Elem<BF>::type E;
   constexpr int NM = BwdTile<P>::NM;
   const E* Cb = reinterpret_cast<const E*>(packed) + packed_cf_elems(p);
+  if constexpr (P == 16 && BF) {
+    if (dx16_ok(p)) {
+      const int nib16 = (int)ceil_div(p.I, 16);
+      const int ntiles = (int)(ceil_div(p.B32, Dx16::ROWS) * nib16);
+      static std::atomic<uint32_t> lds_set{0};
+      ensure_lds_limit(reinterpret_cast<const void*>(&k_dx16), Dx16::LDS_BYTES, lds_set);
+      hipLaunchKernelGGL(k_dx16, dim3(ntiles < kChipBlocks ? ntiles : kChipBlocks), dim3(Dx16::THR),
+                         Dx16::LDS_BYTES, s, reinterpret_cast<const uint16_t*>(dYx),
+                         reinterpret_cast<const uint16_t*>(Cb), t, dx, p, nib16, ntiles);
+      return;
+    }
+  }
   if constexpr (DxDh<P, BF>::kOk) {
     typedef DxDh<P, BF> K;
     const int n_rb = (int)ceil_div(p.B32 / 32, K::RG * K::NM);

@@ -231,6 +231,10 @@ template <int P> struct BwdTile {
 inline int bwd_nm(int P) { return (16 / P) < 4 ? (16 / P) : 4; }
 // dX row fragments (32 rows each) padded to whole tiles of 4 waves x NM
 // fragments; the padding fragments of dYx hold zeros.
-inline int64_t dx_row_frags(const Plan& p) { return round_up(p.B32 / 32, 4 * bwd_nm(p.P)); }
+// dY re-layout rows for dx, in 32-row fragments, zero-padded to whole row
+// blocks of the dx kernel (256 rows; 128 for fp32 at degree 16)
+inline int64_t dx_row_frags(const Plan& p) {
+  return round_up(p.B32 / 32, p.P == 16 && p.esz == 2 ? 8 : 4 * bwd_nm(p.P));
+}
 
 }  // namespace ckan

@@ -67,6 +67,10 @@ SHAPES = [
     (1000, 100, 150, 6),  # pipelined forward: ragged rows, padded inputs, partial tiles
     (777, 40, 300, 12),   # the same at degree 16 (P = 16)
     (50, 100, 70, 6),     # streaming forward, 33..64 rows (tanh from the cache), padded inputs
+    (300, 50, 130, 16),   # degree-16 dx on 16-input blocks: ragged rows, inputs and outputs
+    (520, 272, 96, 13),   # the same past one 256-row block, 17 input blocks
+    (4096, 600, 64, 16),  # degree-16 dx, 608 tiles over 256 persistent blocks, 2 stages each
+    (2048, 1040, 512, 15),  # the same with 16 stages per tile, 65 input blocks
 ]
 
 
