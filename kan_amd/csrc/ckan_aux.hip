@@ -279,76 +279,108 @@ k_col_reduce(const float* __restrict__ part, int nparts, int pitch, int n, float
 //   dYx: dX A operand  [B32/32][KBx][64][8]  (rows b, reduction o)
 //   dYc: dC B operand  [NBf][KBc][64][8]     (columns o, reduction b)
 // and writes colsum_part[bb][o] = sum of dy over rows [64 bb, 64 bb + 64).
-// One wave per (32 columns, 64 rows).  The wave reads its tile of dy once,
-// each load instruction covering 8 whole 128-byte row segments, writes it to a
+// A wave's unit is (32 columns, 64 rows): it reads that tile of dy once, each
+// load instruction covering 8 whole 128-byte row segments, writes it to a
 // private LDS tile and reads it back in both fragment orders: 8 consecutive
 // columns of a row per lane (dYx) and 8 consecutive rows of a column (dYc).
+// Waves stride over the units with the next unit's loads in flight while
+// they re-lay and store the current one, so reads and writes overlap instead
+// of every wave loading first and storing after.
+#ifndef CKAN_PREP_BLOCKS
+#define CKAN_PREP_BLOCKS 512
+#endif
+constexpr int kPrepBlocks = CKAN_PREP_BLOCKS;  // grid cap: 2 blocks (8 waves) per CU
 template <bool BF>
 __global__ void __launch_bounds__(256)
 k_prep_dy(const float* __restrict__ dy, typename Elem<BF>::type* __restrict__ dYx,
            typename Elem<BF>::type* __restrict__ dYc, float* __restrict__ colsum_part,
            Plan p, int need_dx, int need_dc, int nob, int nbb, int64_t dx_rows, int dyal) {
   constexpr int TP = 36;  // row pitch (floats): 16-byte aligned rows
+  constexpr int NL = kPrepRows / 8;
   __shared__ __attribute__((aligned(16))) float tile[4][kPrepRows * TP];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-  const int w = blockIdx.x * 4 + wv;
-  if (w >= nob * nbb) return;
-  const int ob = w % nob, bb = w / nob;
+  const int nw = nob * nbb, stride = (int)gridDim.x * 4;
+  int w = blockIdx.x * 4 + wv;
+  if (w >= nw) return;
   const int g = lane >> 5, c = lane & 31;
   const int rs = lane >> 3, q = lane & 7;
-  const int64_t r0 = (int64_t)bb * kPrepRows;
-  const int o = ob * 32 + 4 * q;
-  const bool vec = dyal && (p.O & 3) == 0 && o + 4 <= p.O;
-  f32x4_t v[kPrepRows / 8];
-#pragma unroll
-  for (int m = 0; m < kPrepRows / 8; ++m) {
-    const int64_t b = r0 + m * 8 + rs;
-    if (b < p.B && vec) {
-      v[m] = __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(dy + b * p.O + o));
-    } else {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) v[m][j] = (b < p.B && o + j < p.O) ? dy[b * p.O + o + j] : 0.0f;
-    }
-  }
   float* t = tile[wv];
+
+  auto load = [&](int wu, f32x4_t (&v)[NL]) __attribute__((always_inline)) {
+    const int ob = wu % nob, bb = wu / nob;
+    const int64_t r0 = (int64_t)bb * kPrepRows;
+    const int o = ob * 32 + 4 * q;
+    const bool vec = dyal && (p.O & 3) == 0 && o + 4 <= p.O;
 #pragma unroll
-  for (int m = 0; m < kPrepRows / 8; ++m) *reinterpret_cast<f32x4_t*>(t + (m * 8 + rs) * TP + 4 * q) = v[m];
-  // the tile is private to this wave, whose LDS accesses are performed in
-  // issue order; the compiler barrier keeps the reads after the writes
-  asm volatile("" ::: "memory");
-  if (need_dx) {
+    for (int m = 0; m < NL; ++m) {
+      const int64_t b = r0 + m * 8 + rs;
+      if (b < p.B && vec) {
+        v[m] = __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(dy + b * p.O + o));
+      } else {
 #pragma unroll
-    for (int mbl = 0; mbl < kPrepRows / 32; ++mbl) {
-      const int64_t b0 = r0 + mbl * 32;
-      if (b0 < dx_rows) {
+        for (int j = 0; j < 4; ++j) v[m][j] = (b < p.B && o + j < p.O) ? dy[b * p.O + o + j] : 0.0f;
+      }
+    }
+  };
+  auto process = [&](int wu, const f32x4_t (&v)[NL]) __attribute__((always_inline)) {
+    const int ob = wu % nob, bb = wu / nob;
+    const int64_t r0 = (int64_t)bb * kPrepRows;
+    // the tile is private to this wave, whose LDS accesses are performed in
+    // issue order; the compiler barriers keep the previous unit's reads
+    // before these writes and these writes before the reads below
+    asm volatile("" ::: "memory");
 #pragma unroll
-        for (int kbl = 0; kbl < 2; ++kbl) {
-          const float* src = t + (mbl * 32 + c) * TP + 16 * kbl + 8 * g;
-          const f32x4_t a = *reinterpret_cast<const f32x4_t*>(src);
-          const f32x4_t e = *reinterpret_cast<const f32x4_t*>(src + 4);
-          const float vv[8] = {a[0], a[1], a[2], a[3], e[0], e[1], e[2], e[3]};
-          store_frag<BF>(dYx + ((size_t)(b0 / 32) * p.KBx + ob * 2 + kbl) * kFragElems, lane, vv);
+    for (int m = 0; m < NL; ++m) *reinterpret_cast<f32x4_t*>(t + (m * 8 + rs) * TP + 4 * q) = v[m];
+    asm volatile("" ::: "memory");
+    if (need_dx) {
+#pragma unroll
+      for (int mbl = 0; mbl < kPrepRows / 32; ++mbl) {
+        const int64_t b0 = r0 + mbl * 32;
+        if (b0 < dx_rows) {
+#pragma unroll
+          for (int kbl = 0; kbl < 2; ++kbl) {
+            const float* src = t + (mbl * 32 + c) * TP + 16 * kbl + 8 * g;
+            const f32x4_t a = *reinterpret_cast<const f32x4_t*>(src);
+            const f32x4_t e = *reinterpret_cast<const f32x4_t*>(src + 4);
+            const float vv[8] = {a[0], a[1], a[2], a[3], e[0], e[1], e[2], e[3]};
+            store_frag<BF>(dYx + ((size_t)(b0 / 32) * p.KBx + ob * 2 + kbl) * kFragElems, lane, vv);
+          }
         }
       }
     }
-  }
-  if (need_dc && ob < p.NBf) {
-    float u[kPrepRows / 16][8];
+    if (need_dc && ob < p.NBf) {
+      float u[kPrepRows / 16][8];
 #pragma unroll
-    for (int kbl = 0; kbl < kPrepRows / 16; ++kbl)
+      for (int kbl = 0; kbl < kPrepRows / 16; ++kbl)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) u[kbl][j] = t[(kbl * 16 + 8 * g + j) * TP + c];
-    float cs = 0.0f;
+        for (int j = 0; j < 8; ++j) u[kbl][j] = t[(kbl * 16 + 8 * g + j) * TP + c];
+      float cs = 0.0f;
 #pragma unroll
-    for (int kbl = 0; kbl < kPrepRows / 16; ++kbl) {
-      const int64_t b0 = r0 + kbl * 16;
+      for (int kbl = 0; kbl < kPrepRows / 16; ++kbl) {
+        const int64_t b0 = r0 + kbl * 16;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) cs += u[kbl][j];
-      if (b0 < p.Bc) store_frag<BF>(dYc + ((size_t)ob * p.KBc + b0 / 16) * kFragElems, lane, u[kbl]);
+        for (int j = 0; j < 8; ++j) cs += u[kbl][j];
+        if (b0 < p.Bc) store_frag<BF>(dYc + ((size_t)ob * p.KBc + b0 / 16) * kFragElems, lane, u[kbl]);
+      }
+      // rows of lane halves interleave in blocks of 8; add the halves in a fixed order
+      const float other = __shfl_xor(cs, 32);
+      if (g == 0 && bb < p.NBB) colsum_part[(size_t)bb * p.O32 + ob * 32 + c] = cs + other;
     }
-    // rows of lane halves interleave in blocks of 8; add the halves in a fixed order
-    const float other = __shfl_xor(cs, 32);
-    if (g == 0 && bb < p.NBB) colsum_part[(size_t)bb * p.O32 + ob * 32 + c] = cs + other;
+  };
+
+  f32x4_t va[NL], vb[NL];
+  load(w, va);
+  for (;;) {  // two units per pass, alternating register sets
+    int wn = w + stride;
+    if (wn < nw) load(wn, vb);
+    process(w, va);
+    if (wn >= nw) break;
+    w = wn;
+    wn = w + stride;
+    if (wn < nw) load(wn, va);
+    process(w, vb);
+    if (wn >= nw) break;
+    w = wn;
   }
 }
 
@@ -699,7 +731,8 @@ void launch_prep_dy(const float* dy, void* dYx, void* dYc, float* colsum_part, c
   if (dx_rows > row_end) row_end = dx_rows;
   const int nob = p.O64 / 32;
   const int nbb = (int)ceil_div(row_end, kPrepRows);
-  dim3 grid((unsigned)ceil_div((int64_t)nob * nbb, 4));
+  const int64_t blocks = ceil_div((int64_t)nob * nbb, 4);
+  dim3 grid((unsigned)(blocks < kPrepBlocks ? blocks : kPrepBlocks));
   if (p.esz == 2)
     hipLaunchKernelGGL((k_prep_dy<true>), grid, dim3(256), 0, s, dy,
                        reinterpret_cast<uint16_t*>(dYx), reinterpret_cast<uint16_t*>(dYc),
