@@ -73,6 +73,60 @@ k_ce(const float* __restrict__ y, const int64_t* __restrict__ labels, float* __r
   }
 }
 
+// Softmax cross-entropy and its mean in one launch, for up to 1024 rows of
+// at most 16 classes (config 2's 10): thread b owns row b.  The row's max and
+// exp-sum are formed in k_ce's order (its lane butterfly, with the lanes past
+// O adding exact zeros), and the row losses are summed in k_sum_scalar's
+// order, so dy and the loss have the bits of the two-launch path.
+constexpr int kCeSmallRows = 1024, kCeSmallO = 16;
+__global__ void __launch_bounds__(1024)
+k_ce_small(const float* __restrict__ y, const int64_t* __restrict__ labels, float* __restrict__ dy,
+           int B, int O, float* __restrict__ out, float* __restrict__ out2) {
+  __shared__ float rl[kCeSmallRows];
+  __shared__ float red[256];
+  const int b = threadIdx.x;
+  if (b < B) {
+    const float* yr = y + (int64_t)b * O;
+    float yv[kCeSmallO], e[kCeSmallO];
+#pragma unroll
+    for (int o = 0; o < kCeSmallO; ++o) yv[o] = o < O ? yr[o] : 0.0f;
+    float m = -INFINITY;
+#pragma unroll
+    for (int o = 0; o < kCeSmallO; ++o)
+      if (o < O) m = fmaxf(m, yv[o]);
+#pragma unroll
+    for (int o = 0; o < kCeSmallO; ++o) e[o] = o < O ? expf(yv[o] - m) : 0.0f;
+#pragma unroll
+    for (int w = kCeSmallO / 2; w > 0; w >>= 1)
+#pragma unroll
+      for (int o = 0; o < w; ++o) e[o] = e[o] + e[o + w];
+    const float s = e[0];
+    const int64_t lab = labels[b];
+    const float inv_b = 1.0f / (float)B;
+#pragma unroll
+    for (int o = 0; o < kCeSmallO; ++o)
+      if (o < O) dy[(int64_t)b * O + o] = (expf(yv[o] - m) / s - (o == lab ? 1.0f : 0.0f)) * inv_b;
+    const float yl = (lab >= 0 && lab < O) ? yr[lab] : 0.0f;
+    rl[b] = (logf(s) + m) - yl;
+  }
+  __syncthreads();
+  if (b < 256) {
+    float acc = 0.0f;
+    for (int k = b; k < B; k += 256) acc += rl[k];
+    red[b] = acc;
+  }
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if (b < w) red[b] += red[b + w];
+    __syncthreads();
+  }
+  if (b == 0) {
+    const float scale = (float)(1.0 / (double)B);
+    *out = red[0] * scale;
+    if (out2) *out2 = red[0] * scale;
+  }
+}
+
 // loss = scale * sum_k part[k], k < n, in a fixed order (one block); also
 // into out2 when given (the caller's per-step loss slot).
 __global__ void __launch_bounds__(256)
@@ -469,6 +523,10 @@ int run_step(ckan_exec* ex, const float* x, const void* target, hipStream_t s,
                        (float)(2.0 / (double)n), ex->loss_part);
     hipLaunchKernelGGL(k_sum_scalar, dim3(1), dim3(256), 0, s, ex->loss_part,
                        (int64_t)kLossBlocks, (float)(1.0 / (double)n), ex->loss, loss_copy);
+  } else if (B <= kCeSmallRows && O <= kCeSmallO) {
+    hipLaunchKernelGGL(k_ce_small, dim3(1), dim3(kCeSmallRows), 0, s, last.y,
+                       reinterpret_cast<const int64_t*>(target), last.dy, (int)B, O, ex->loss,
+                       loss_copy);
   } else {
     hipLaunchKernelGGL(k_ce, dim3((unsigned)((B + 3) / 4)), dim3(256), 0, s, last.y,
                        reinterpret_cast<const int64_t*>(target), last.dy, B, O, ex->loss_part);

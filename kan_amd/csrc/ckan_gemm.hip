@@ -729,10 +729,11 @@ k_fwd_stream(const float* __restrict__ x, float* __restrict__ tc,
 // y[r, o] = bias[o] + sum_z part[z][r][o], z in split order.  nib > 0: the
 // bias comes from its per-input-block partials (summed per element: the host
 // chooses this only for small outputs) and the packed bias slot is filled.
+// out_tanh: tanh(y) is stored instead (the next layer's tanh cache).
 __global__ void __launch_bounds__(256)
 k_fwd_reduce(const float* __restrict__ part, int S, const float* __restrict__ bias_f,
              float* __restrict__ y, Plan p, const float* __restrict__ bias_part, int nib,
-             float* __restrict__ bias_out) {
+             float* __restrict__ bias_out, int out_tanh) {
   const int64_t n = p.B * (int64_t)p.O;
   const int64_t nn = n > p.O32 ? n : p.O32;
   for (int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; q < nn;
@@ -742,7 +743,8 @@ k_fwd_reduce(const float* __restrict__ part, int S, const float* __restrict__ bi
     const int64_t r = q / p.O;
     const int o = (int)(q - r * p.O);
     const float bias = nib > 0 ? bias_from_parts(bias_part, nib, p.O32, o) : bias_f[o];
-    y[q] = split_sum(part + (size_t)r * p.O32 + o, (size_t)p.B32 * p.O32, (unsigned)S, bias);
+    const float v = split_sum(part + (size_t)r * p.O32 + o, (size_t)p.B32 * p.O32, (unsigned)S, bias);
+    y[q] = out_tanh ? tanhf(v) : v;
   }
 }
 
@@ -2407,13 +2409,14 @@ static void fwd_dispatch(const float* x, float* t, const void* packed, float* y,
     int64_t gsz = ((n > p.O32 ? n : p.O32) + 255) / 256;
     if (gsz > 65536) gsz = 65536;
     hipLaunchKernelGGL(k_fwd_reduce, dim3((unsigned)gsz), dim3(256), 0, s, part, c.splits, bias, y,
-                       p, bpart, nib, bias_out);
+                       p, bpart, nib, bias_out, (int)out_tanh);
   }
 }
 
 // The forward can store tanh(y) in place of y: the pipelined kernel, unsplit,
-// stores y itself.
+// stores y itself; a split forward's reduce stores every y.
 template <int P, bool BF> static bool out_tanh_ok(const Plan& p, const FwdChoice& c) {
+  if (c.tile != kFwdCols && (c.splits > 1 || fwd_streaming(c))) return true;
   if constexpr (FwdPipe<P, BF>::kOk)
     return c.tile == kFwdBig && c.splits == 1 && fwd_pipe_offsets_fit(p);
   else

@@ -49,6 +49,31 @@ def test_config2_ce_sgd_matches_oracle(use_graph):
     ex.close()
 
 
+@pytest.mark.parametrize("widths,degrees,B", [
+    ([40, 32, 20], [3, 4], 300),   # 20 classes: the per-row-wave loss and a separate sum
+    ([24, 12], [5], 1500),         # past 1024 rows: the same
+])
+def test_ce_multi_block_loss_matches_oracle(widths, degrees, B):
+    """Small softmax cross-entropy (up to 1024 rows, 16 classes) runs as one
+    launch with its sum; larger ones as one wave per row plus a sum launch."""
+    from kan_amd import ResidentExecutor
+    print(f"executor ce {widths} B={B}", flush=True)
+    g = torch.Generator().manual_seed(7)
+    x = torch.rand(B, widths[0], generator=g) * 4 - 2
+    labels = torch.randint(0, widths[-1], (B,), generator=g)
+    coeffs = _make(widths, degrees, 27)
+    ex = ResidentExecutor(widths, degrees, B, compute="fp32", loss="ce", optimizer="sgd", lr=0.05)
+    for l, c in enumerate(coeffs):
+        ex.set_coeffs(l, c)
+    losses = [ex.step(x.cuda(), labels.cuda()).item() for _ in range(3)]
+    c_ref, losses_ref = orc.train_steps(x, labels, coeffs, steps=3, loss="ce", optimizer="sgd", lr=0.05)
+    for a, b in zip(losses, losses_ref):
+        assert abs(a - b) <= 1e-5 * abs(b) + 1e-6
+    for l in range(len(degrees)):
+        assert _rel(ex.get_coeffs(l), c_ref[l]) <= 1e-5
+    ex.close()
+
+
 def test_mse_stack_deg16_sgd_matches_oracle():
     from kan_amd import ResidentExecutor
     print("executor mse deg16 stack", flush=True)
