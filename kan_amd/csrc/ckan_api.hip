@@ -402,6 +402,9 @@ namespace {
 int pack_forward_impl(const ckan_desc* desc, const ckan_basis_spec* spec, const void* coeffs,
                       void* packed, const float* x, float* y, float* t_cache, void* ws,
                       size_t ws_bytes, void* stream, bool t_ready, bool out_tanh);
+int forward_packed(const Plan& p, const FwdChoice& c, const void* packed, const float* x, float* y,
+                   float* t_cache, void* ws, hipStream_t s, bool t_done, bool sum_in_gemm,
+                   bool out_tanh);
 }
 
 int ckan_pack_forward(const ckan_desc* desc, const ckan_basis_spec* spec, const void* coeffs,
@@ -452,10 +455,20 @@ int pack_forward_impl(const ckan_desc* desc, const ckan_basis_spec* spec, const 
                 fuse_tanh ? x : nullptr, fuse_tanh ? t_cache : nullptr);
   }
   if ((rc = check_launch("pack_forward: pack"))) return rc;
-  if (!t_ready && fwd_reads_tcache(c) && !fuse_tanh) {
+  return forward_packed(p, c, packed, x, y, t_cache, ws, s, t_ready || fuse_tanh, sum_in_gemm,
+                        out_tanh);
+}
+
+// The forward after the pack: the tanh of x unless the cache holds it
+// already, then the GEMM.
+int forward_packed(const Plan& p, const FwdChoice& c, const void* packed, const float* x, float* y,
+                   float* t_cache, void* ws, hipStream_t s, bool t_done, bool sum_in_gemm,
+                   bool out_tanh) {
+  if (!t_done && fwd_reads_tcache(c)) {
     ProfScope ps("tanh", s);
     launch_tanh(x, t_cache, p, s);
   }
+  int rc;
   if ((rc = check_launch("pack_forward: tanh"))) return rc;
   {
     ProfScope ps("fwd_gemm", s);
@@ -901,6 +914,46 @@ bool ckan::layer_reads_tcache(const ckan_desc* desc) {
 bool ckan::layer_out_tanh_ok(const ckan_desc* desc) {
   if (validate_desc(desc) != CKAN_OK || valu_route(desc)) return false;
   return fwd_out_tanh_ok(plan_of(desc));
+}
+
+bool ckan::pack_pair_fits(const ckan_desc* a, const ckan_desc* b) {
+  if (validate_desc(a) != CKAN_OK || validate_desc(b) != CKAN_OK || valu_route(a) || valu_route(b))
+    return false;
+  if (a->coeff_dtype != CKAN_DTYPE_F32 || b->coeff_dtype != CKAN_DTYPE_F32) return false;
+  if (a->batch != b->batch || a->out_dim != b->in_dim || a->batch < 1) return false;
+  return pack_pair_ok(plan_of(a), plan_of(b)) && layer_out_tanh_ok(a) && layer_reads_tcache(b);
+}
+
+int ckan::pack2_forward_ex(const ckan_desc* da, const void* Ca, void* pka, const float* xa,
+                           float* ta, bool ta_ready, const ckan_desc* db, const void* Cb,
+                           void* pkb, float* tb, float* outb, bool outb_tanh, void* ws,
+                           size_t ws_bytes, void* stream) {
+  if (!pack_pair_fits(da, db) || (ta_ready && !layer_reads_tcache(da)) ||
+      (outb_tanh && !layer_out_tanh_ok(db)))
+    return fail(CKAN_ERR_INVALID_ARG, "pack2_forward_ex: the layer pair does not allow one pack launch");
+  if (!Ca || !pka || !Cb || !pkb || !ta || !tb || !outb || (!xa && !ta_ready))
+    return fail(CKAN_ERR_INVALID_ARG, "pack2_forward_ex: NULL pointer");
+  if (!aligned16(pka) || !aligned16(pkb) || !aligned16(ta) || !aligned16(tb))
+    return fail(CKAN_ERR_INVALID_ARG, "pack2_forward_ex: packed buffers and caches must be 16-byte aligned");
+  const Plan pa = plan_of(da), pb = plan_of(db);
+  const FwdChoice ca = choose_fwd(pa), cb = choose_fwd(pb);
+  const size_t need = fwd_ws_bytes(pa, ca) > fwd_ws_bytes(pb, cb) ? fwd_ws_bytes(pa, ca) : fwd_ws_bytes(pb, cb);
+  if (ws_bytes < need)
+    return fail(CKAN_ERR_WORKSPACE, "forward workspace too small: %zu < %zu bytes", ws_bytes, need);
+  if (need && !ws) return fail(CKAN_ERR_INVALID_ARG, "workspace is NULL");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const bool sum_a = fwd_sums_bias(pa, ca), sum_b = fwd_sums_bias(pb, cb);
+  const bool fuse_tanh = !ta_ready && fwd_reads_tcache(ca) && pack_tanh_fusable(pa, xa);
+  {
+    ProfScope ps("pack2", s);
+    launch_pack_pair(reinterpret_cast<const float*>(Ca), pka, pa, !sum_a, fuse_tanh ? xa : nullptr,
+                     fuse_tanh ? ta : nullptr, reinterpret_cast<const float*>(Cb), pkb, pb, !sum_b, s);
+  }
+  int rc;
+  if ((rc = check_launch("pack2_forward: pack"))) return rc;
+  if ((rc = forward_packed(pa, ca, pka, xa, tb, ta, ws, s, ta_ready || fuse_tanh, sum_a, true)))
+    return rc;
+  return forward_packed(pb, cb, pkb, nullptr, outb, tb, ws, s, true, sum_b, outb_tanh);
 }
 
 int ckan::pack_forward_ex(const ckan_desc* desc, const void* coeffs, void* packed, const float* x,

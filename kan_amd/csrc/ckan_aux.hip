@@ -94,20 +94,22 @@ struct TanhJob {
 };
 constexpr int kPackTanhU = 8;  // tanh float4 per thread in flight at once
 
+// One pack block: input block ib, output block ob; `lin` numbers the block
+// for its tanh share.
 template <int P, bool BF, typename CT, bool XF>
-__global__ void __launch_bounds__(256)
-k_pack(const CT* __restrict__ C, typename Elem<BF>::type* __restrict__ Cf,
-       typename Elem<BF>::type* __restrict__ Cb, float* __restrict__ bias_part, Plan p, int cal,
-       XfArg<XF> xf, TanhJob tj) {
+__device__ __forceinline__ void pack_tile(const CT* __restrict__ C, typename Elem<BF>::type* __restrict__ Cf,
+                                          typename Elem<BF>::type* __restrict__ Cb,
+                                          float* __restrict__ bias_part, const Plan& p, int cal,
+                                          const XfArg<XF>& xf, const TanhJob& tj, int ib, int ob,
+                                          int64_t lin) {
   using G = FwdGroup<P>;
   constexpr int RPMAX = 32 * (P + 1) + 1;
   __shared__ float tile[32 * RPMAX];
   __shared__ float bsum[8][32];
   const int tid = threadIdx.x;
-  const int ib = blockIdx.x, ob = blockIdx.y;
   // tanh share: the first chunk's loads go out with the tile's, so both streams
   // are in flight together; the tanh itself runs after the re-layout
-  const int64_t tj0 = tj.per * (blockIdx.x + (int64_t)gridDim.x * blockIdx.y);
+  const int64_t tj0 = tj.per * lin;
   const int64_t tj1 = tj.x ? (tj0 + tj.per < tj.n4 ? tj0 + tj.per : tj.n4) : 0;
   f32x4_t tx[kPackTanhU];
 #pragma unroll
@@ -254,6 +256,39 @@ k_pack(const CT* __restrict__ C, typename Elem<BF>::type* __restrict__ Cf,
       if (k < tj1) tj.t[k] = r;
     }
   }
+}
+
+template <int P, bool BF, typename CT, bool XF>
+__global__ void __launch_bounds__(256)
+k_pack(const CT* __restrict__ C, typename Elem<BF>::type* __restrict__ Cf,
+       typename Elem<BF>::type* __restrict__ Cb, float* __restrict__ bias_part, Plan p, int cal,
+       XfArg<XF> xf, TanhJob tj) {
+  pack_tile<P, BF, CT, XF>(C, Cf, Cb, bias_part, p, cal, xf, tj, blockIdx.x, blockIdx.y,
+                           blockIdx.x + (int64_t)gridDim.x * blockIdx.y);
+}
+
+// Two layers' packs in one launch (fp32 coefficients, the Chebyshev basis):
+// blocks [0, a.nblocks) pack layer a, the rest layer b.  For stacks of small
+// layers, where each pack is a latency-bound launch of a few blocks.
+template <bool BF> struct PackJob {
+  const float* C;
+  typename Elem<BF>::type* Cf;
+  typename Elem<BF>::type* Cb;
+  float* bias;
+  Plan p;
+  int cal, nx, nblocks;
+  TanhJob tj;
+};
+template <int P, bool BF>
+__global__ void __launch_bounds__(256)
+k_pack2(PackJob<BF> a, PackJob<BF> b) {
+  const int bid = blockIdx.x;
+  if (bid < a.nblocks)
+    pack_tile<P, BF, float, false>(a.C, a.Cf, a.Cb, a.bias, a.p, a.cal, XfArg<false>{}, a.tj,
+                                   bid % a.nx, bid / a.nx, bid);
+  else
+    pack_tile<P, BF, float, false>(b.C, b.Cf, b.Cb, b.bias, b.p, b.cal, XfArg<false>{}, b.tj,
+                                   (bid - a.nblocks) % b.nx, (bid - a.nblocks) / b.nx, bid - a.nblocks);
 }
 
 // out[o] = sum_k part[k][o] for k < nparts (row pitch `pitch`): 4 interleaved
@@ -610,6 +645,56 @@ void launch_pack(const void* C, bool c_bf16, void* packed, const Plan& p, hipStr
     hipLaunchKernelGGL(k_col_reduce, dim3((unsigned)ceil_div(p.O32, 64)), dim3(256), 0, s,
                        reinterpret_cast<const float*>(base + packed_bias_offset(p)), p.NIB,
                        p.O32, p.O32, reinterpret_cast<float*>(base + packed_biasf_offset(p)));
+}
+
+template <int P, bool BF>
+static void launch_pack2_t(const float* Ca, void* pa, const Plan& qa, const TanhJob& tja,
+                           const float* Cb_, void* pb, const Plan& qb, hipStream_t s) {
+  typedef typename Elem<BF>::type E;
+  auto job = [](const float* C, void* packed, const Plan& q, const TanhJob& tj) {
+    PackJob<BF> j;
+    j.C = C;
+    j.Cf = reinterpret_cast<E*>(packed);
+    j.Cb = j.Cf + packed_cf_elems(q);
+    j.bias = reinterpret_cast<float*>(reinterpret_cast<char*>(packed) +
+                                      (q.NIB == 1 ? packed_biasf_offset(q) : packed_bias_offset(q)));
+    j.p = q;
+    j.cal = (int)is_al16(C);
+    j.nx = q.NIB;
+    j.nblocks = q.NIB * (q.O64 / 32);
+    j.tj = tj;
+    return j;
+  };
+  const PackJob<BF> a = job(Ca, pa, qa, tja);
+  const PackJob<BF> b = job(Cb_, pb, qb, TanhJob{nullptr, nullptr, 0, 0, qb.imap, qb.ima, qb.imb});
+  hipLaunchKernelGGL((k_pack2<P, BF>), dim3((unsigned)(a.nblocks + b.nblocks)), dim3(256), 0, s, a, b);
+}
+
+bool pack_pair_ok(const Plan& a, const Plan& b) {
+  return a.P == b.P && a.esz == b.esz && (int64_t)a.NIB * (a.O64 / 32) + (int64_t)b.NIB * (b.O64 / 32) < (1 << 30);
+}
+
+void launch_pack_pair(const float* Ca, void* pa, const Plan& qa, bool reduce_a, const float* xa,
+                      float* ta, const float* Cb_, void* pb, const Plan& qb, bool reduce_b,
+                      hipStream_t s) {
+  TanhJob tj{nullptr, nullptr, 0, 0, qa.imap, qa.ima, qa.imb};
+  if (xa && ta) {  // pack_tanh_fusable(qa, xa) holds: the caller checked
+    tj.x = reinterpret_cast<const f32x4_t*>(xa);
+    tj.t = reinterpret_cast<f32x4_t*>(ta);
+    tj.n4 = qa.B * qa.I / 4;
+    tj.per = round_up(ceil_div(tj.n4, (int64_t)qa.NIB * (qa.O64 / 32)), 256);
+  }
+  const bool bf = qa.esz == 2;
+#define CKAN_PK2(PP, BB) launch_pack2_t<PP, BB>(Ca, pa, qa, tj, Cb_, pb, qb, s)
+  switch (qa.P) {
+    case 2: bf ? CKAN_PK2(2, true) : CKAN_PK2(2, false); break;
+    case 4: bf ? CKAN_PK2(4, true) : CKAN_PK2(4, false); break;
+    case 8: bf ? CKAN_PK2(8, true) : CKAN_PK2(8, false); break;
+    default: bf ? CKAN_PK2(16, true) : CKAN_PK2(16, false); break;
+  }
+#undef CKAN_PK2
+  if (qa.NIB > 1 && reduce_a) launch_bias_reduce(pa, qa, s);
+  if (qb.NIB > 1 && reduce_b) launch_bias_reduce(pb, qb, s);
 }
 
 void launch_bias_reduce(void* packed, const Plan& p, hipStream_t s) {

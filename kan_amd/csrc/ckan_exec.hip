@@ -402,6 +402,9 @@ struct ckan_exec {
     // the training step's forward stores tanh(y) straight into the next
     // layer's tanh cache (y itself is not needed by the step)
     bool tanh_out = false;
+    // this layer's pack and the next layer's run as one launch (the next
+    // layer's input comes from this one's tanh output)
+    bool pack_pair = false;
   };
   ckan_exec_config cfg;
   std::vector<int32_t> widths, degrees;
@@ -507,6 +510,16 @@ int run_step(ckan_exec* ex, const float* x, const void* target, hipStream_t s,
     // pack and forward in one call: tanh in the pack launch (or, after a layer
     // with tanh_out, already in ly.t), bias summed by the forward
     const bool t_ready = l > 0 && ex->layers[l - 1].tanh_out;
+    if (ly.pack_pair) {  // layers l and l + 1: both packs in one launch
+      auto& nx = ex->layers[l + 1];
+      float* outb = nx.tanh_out ? ex->layers[l + 2].t : nx.y;
+      if ((rc = pack2_forward_ex(&ly.desc, ly.C, ly.packed, l == 0 ? x : ex->layers[l - 1].y, ly.t,
+                                 t_ready, &nx.desc, nx.C, nx.packed, nx.t, outb, nx.tanh_out,
+                                 ex->fws, ex->fws_bytes, s)))
+        return rc;
+      ++l;
+      continue;
+    }
     const float* in = l == 0 ? x : ex->layers[l - 1].y;
     float* out = ly.tanh_out ? ex->layers[l + 1].t : ly.y;
     if ((rc = pack_forward_ex(&ly.desc, ly.C, ly.packed, t_ready ? nullptr : in, out, ly.t,
@@ -617,6 +630,11 @@ int ckan_exec_create(const ckan_exec_config* cfg, ckan_exec** out, void* stream)
   for (int l = 0; rc == CKAN_OK && l + 1 < cfg->n_layers; ++l)
     ex->layers[l].tanh_out = layer_out_tanh_ok(&ex->layers[l].desc) &&
                              layer_reads_tcache(&ex->layers[l + 1].desc);
+  for (int l = 0; rc == CKAN_OK && l + 1 < cfg->n_layers; ++l) {
+    auto& ly = ex->layers[l];
+    ly.pack_pair = ly.tanh_out && pack_pair_fits(&ly.desc, &ex->layers[l + 1].desc);
+    if (ly.pack_pair) ++l;  // the next layer's pack is taken
+  }
   if (rc == CKAN_OK) {
     ex->fws_bytes = align256(ex->fws_bytes);
     ex->bws_bytes = align256(ex->bws_bytes);

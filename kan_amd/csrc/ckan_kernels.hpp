@@ -212,6 +212,21 @@ int pack_forward_ex(const struct ckan_desc* desc, const void* coeffs, void* pack
 // Whether the layer of desc can take t_ready / out_tanh in pack_forward_ex.
 bool layer_reads_tcache(const struct ckan_desc* desc);
 bool layer_out_tanh_ok(const struct ckan_desc* desc);
+// Two consecutive layers a, b of a stack whose forward a stores tanh(y) into
+// b's tanh cache tb: both packs in one launch (b's pack needs nothing of a),
+// then a's forward, then b's (t_ready; out_tanh into outb when outb_tanh).
+// pack_pair_fits: the pair allows it (fp32 coefficients, Chebyshev kernels on
+// both, same padded degree and compute type, a's tanh output, b's cache read).
+bool pack_pair_fits(const struct ckan_desc* a, const struct ckan_desc* b);
+int pack2_forward_ex(const struct ckan_desc* da, const void* Ca, void* pka, const float* xa,
+                     float* ta, bool ta_ready, const struct ckan_desc* db, const void* Cb,
+                     void* pkb, float* tb, float* outb, bool outb_tanh, void* ws, size_t ws_bytes,
+                     void* stream);
+// the Plan-level launch behind pack2_forward_ex (xa, ta: a's fused tanh, or null)
+bool pack_pair_ok(const Plan& a, const Plan& b);
+void launch_pack_pair(const float* Ca, void* pa, const Plan& qa, bool reduce_a, const float* xa,
+                      float* ta, const float* Cb, void* pb, const Plan& qb, bool reduce_b,
+                      hipStream_t s);
 void launch_adam(float* p, const float* g, float* m, float* v, int64_t n, float w1, float beta2,
                  float one_m_beta2, float bc2_sqrt, float eps, float neg_step, float wd,
                  hipStream_t s);
