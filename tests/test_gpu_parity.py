@@ -71,6 +71,7 @@ SHAPES = [
     (520, 272, 96, 13),   # the same past one 256-row block, 17 input blocks
     (4096, 600, 64, 16),  # degree-16 dx, 608 tiles over 256 persistent blocks, 2 stages each
     (2048, 1040, 512, 15),  # the same with 16 stages per tile, 65 input blocks
+    (5, 40, 100, 16),     # degree-16 dx with 5 rows: one partial tile per input block
 ]
 
 
