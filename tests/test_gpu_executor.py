@@ -95,6 +95,33 @@ def test_mse_stack_deg16_sgd_matches_oracle():
     ex.close()
 
 
+@pytest.mark.parametrize("compute,tol", [("fp32", 1e-5), ("bf16", 2e-2)])
+def test_paired_pack_with_bias_reduce_matches_oracle(compute, tol):
+    """A 1024 -> 2048 layer at 512 rows forwards split-K, stores tanh(y) into
+    the next layer's cache from its reduce and leaves the bias sum to a
+    separate reduce launch: its pack and the next layer's run as one launch,
+    followed by both bias reduces."""
+    from kan_amd import ResidentExecutor
+    print(f"executor paired pack + bias reduce {compute}", flush=True)
+    widths, degrees, B, lr = [1024, 2048, 16], [3, 3], 512, 0.01
+    g = torch.Generator().manual_seed(9)
+    x = torch.rand(B, widths[0], generator=g) * 4 - 2
+    y = torch.randn(B, widths[-1], generator=g)
+    coeffs = _make(widths, degrees, 41)
+    if compute == "bf16":
+        coeffs = [c.bfloat16().float() for c in coeffs]
+    ex = ResidentExecutor(widths, degrees, B, compute=compute, loss="mse", optimizer="sgd", lr=lr)
+    for l, c in enumerate(coeffs):
+        ex.set_coeffs(l, c)
+    loss = ex.step(x.cuda(), y.cuda()).item()
+    c_ref, losses_ref = orc.train_steps(x, y, coeffs, steps=1, loss="mse", optimizer="sgd", lr=lr)
+    assert abs(loss - losses_ref[0]) <= tol * abs(losses_ref[0])
+    for l in range(2):
+        # the step itself (C1 - C0 = -lr * dC) against the oracle's
+        assert _rel(ex.get_coeffs(l).cpu() - coeffs[l], c_ref[l] - coeffs[l]) <= tol
+    ex.close()
+
+
 @pytest.mark.parametrize("widths,degrees,B,compute", [
     ([96, 64, 10], [4, 4], 128, "fp32"),    # dC written in place by the pipelined kernel
     ([96, 64, 10], [4, 4], 512, "fp32"),    # split dC: the split-sum kernel applies the step
