@@ -1132,9 +1132,11 @@ k_dx_pipe(const typename Elem<BF>::type* __restrict__ dYx,
 }
 
 // ---------------------------------------------------------------------------
-// dX for degrees up to 8.  One block = 2*RG waves (dh, rg): wave rg takes
-// NM = 2 fragments of 32 rows, wave dh half of the P degrees, for one input
-// block (32 inputs); acc = NM x P/2 fragments, two waves per SIMD.  RG = 4
+// dX for degrees up to 8 (and fp32 at degree 16, with NM = 1: 128-row
+// blocks; bf16 at degree 16 takes k_dx16 below).  One block = 2*RG waves
+// (dh, rg): wave rg takes NM = 2 fragments of 32 rows, wave dh half of the P
+// degrees, for one input block (32 inputs); acc = NM x P/2 fragments, two
+// waves per SIMD.  RG = 4
 // (256 rows per block, one block per CU) streams a third less operand data
 // per MFMA than RG = 2 (two 128-row blocks per CU, whose epilogues overlap
 // each other's MFMAs) and measures faster.  Both operands (dy rows and the
