@@ -25,14 +25,42 @@ constexpr int kLossBlocks = 256;  // fixed partial count: deterministic loss sum
 // block writes one partial sum.
 __global__ void __launch_bounds__(256)
 k_mse(const float* __restrict__ y, const float* __restrict__ tgt, float* __restrict__ dy,
-      int64_t n, float scale_grad, float* __restrict__ part) {
+      int64_t n, float scale_grad, float* __restrict__ part, int vec) {
   __shared__ float red[256];
   float s = 0.0f;
-  for (int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; q < n;
-       q += (int64_t)gridDim.x * blockDim.x) {
-    const float d = y[q] - tgt[q];
-    s = fmaf(d, d, s);
-    dy[q] = scale_grad * d;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const int64_t t0 = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (vec) {
+    // float4 strides, four of them loaded before any is used (one element
+    // per round trip made config 4's 4 M-element loss latency-bound: 31 us)
+    constexpr int U = 4;
+    const int64_t n4 = n / 4;
+    const f32x4_t* y4 = reinterpret_cast<const f32x4_t*>(y);
+    const f32x4_t* t4 = reinterpret_cast<const f32x4_t*>(tgt);
+    f32x4_t* d4 = reinterpret_cast<f32x4_t*>(dy);
+    for (int64_t q0 = t0; q0 < n4; q0 += U * stride) {
+      f32x4_t a[U], b[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t q = q0 + u * stride;
+        a[u] = q < n4 ? __builtin_nontemporal_load(y4 + q) : f32x4_t{0.f, 0.f, 0.f, 0.f};
+        b[u] = q < n4 ? __builtin_nontemporal_load(t4 + q) : f32x4_t{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t q = q0 + u * stride;
+        const f32x4_t d = a[u] - b[u];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) s = fmaf(d[j], d[j], s);
+        if (q < n4) d4[q] = scale_grad * d;
+      }
+    }
+  } else {
+    for (int64_t q = t0; q < n; q += stride) {
+      const float d = y[q] - tgt[q];
+      s = fmaf(d, d, s);
+      dy[q] = scale_grad * d;
+    }
   }
   red[threadIdx.x] = s;
   __syncthreads();
@@ -531,9 +559,12 @@ int run_step(ckan_exec* ex, const float* x, const void* target, hipStream_t s,
   const int O = last.desc.out_dim;
   if (ex->cfg.loss == CKAN_LOSS_MSE) {
     const int64_t n = B * O;
+    const int vec = n % 4 == 0 && (reinterpret_cast<uintptr_t>(target) & 15) == 0 &&
+                    (reinterpret_cast<uintptr_t>(last.y) & 15) == 0 &&
+                    (reinterpret_cast<uintptr_t>(last.dy) & 15) == 0;
     hipLaunchKernelGGL(k_mse, dim3(kLossBlocks), dim3(256), 0, s, last.y,
                        reinterpret_cast<const float*>(target), last.dy, n,
-                       (float)(2.0 / (double)n), ex->loss_part);
+                       (float)(2.0 / (double)n), ex->loss_part, vec);
     hipLaunchKernelGGL(k_sum_scalar, dim3(1), dim3(256), 0, s, ex->loss_part,
                        (int64_t)kLossBlocks, (float)(1.0 / (double)n), ex->loss, loss_copy);
   } else if (B <= kCeSmallRows && O <= kCeSmallO) {
