@@ -867,8 +867,49 @@ k_dc_sum(const float* __restrict__ part, int S, float* __restrict__ dC, int64_t 
   }
 }
 
+// The same four elements per thread (float4), with the destination's read
+// (SGD / accumulate modes) issued together with the partials' loads: config
+// 4's 4.5 M-element layers 27 -> 18 us.
+__global__ void __launch_bounds__(256)
+k_dc_sum4(const f32x4_t* __restrict__ part, int S, f32x4_t* __restrict__ dC, int64_t n4, DcOut om) {
+  for (int64_t q = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; q < n4;
+       q += (int64_t)gridDim.x * blockDim.x) {
+    const bool rmw = om.mode == kDcSgd || om.mode == kDcAccumulate;
+    const f32x4_t c = rmw ? dC[q] : f32x4_t{0.f, 0.f, 0.f, 0.f};
+    f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int z0 = 0; z0 < S; z0 += 8) {
+      f32x4_t v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        v[j] = z0 + j < S ? __builtin_nontemporal_load(part + (size_t)(z0 + j) * n4 + q)
+                          : f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (z0 + j < S) acc += v[j];
+    }
+    if (om.mode == kDcAccumulate) {
+      dC[q] = c + acc;
+    } else if (om.mode == kDcSgd) {
+      f32x4_t r;
+      r.x = sgd_update(c.x, acc.x, om.lr, om.wd);
+      r.y = sgd_update(c.y, acc.y, om.lr, om.wd);
+      r.z = sgd_update(c.z, acc.z, om.lr, om.wd);
+      r.w = sgd_update(c.w, acc.w, om.lr, om.wd);
+      dC[q] = r;
+    } else {
+      dc_write4(dC + q, acc, om);
+    }
+  }
+}
+
 void launch_dc_sum(const float* part, int S, float* dC, DcOut om, const Plan& p, hipStream_t s) {
   const int64_t n = (int64_t)p.I * p.O * p.D;
+  if (n % 4 == 0 && is_al16(part) && is_al16(dC)) {
+    hipLaunchKernelGGL(k_dc_sum4, dim3(grid_for(n / 4)), dim3(256), 0, s,
+                       reinterpret_cast<const f32x4_t*>(part), S, reinterpret_cast<f32x4_t*>(dC),
+                       n / 4, om);
+    return;
+  }
   hipLaunchKernelGGL(k_dc_sum, dim3(grid_for(n)), dim3(256), 0, s, part, S, dC, n, om);
 }
 
