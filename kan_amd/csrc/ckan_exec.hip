@@ -211,6 +211,7 @@ k_copy_f32(const float* __restrict__ src, float* __restrict__ dst, int64_t n) {
 constexpr int kTinyMaxLayers = 8;
 constexpr int kTinyMaxD = 17;
 constexpr int64_t kTinyMaxMacs = (int64_t)1 << 18;  // multiply-adds per step
+constexpr int kTinyStepsPerLaunch = 1024;  // fit's steps per launch (bounds a launch's duration)
 
 struct TinyLayerArg {
   float* C;
@@ -220,6 +221,8 @@ struct TinyLayerArg {
   float* y;   // layer output [B, O]
   float* dy;  // gradient wrt y [B, O]
   int I, O, D;
+  // float offsets of the same arrays in the launch's LDS (TinyArgs::lds)
+  int sC, sm, sv, st, sy, sdy;
 };
 
 struct TinyArgs {
@@ -231,7 +234,26 @@ struct TinyArgs {
   int64_t B;
   float lr, wd, w1, beta2, one_m_beta2, eps;
   double lr_d, b1_d, b2_d;
+  // the whole state (coefficients, moments, activations) fits in LDS: the
+  // launch copies the coefficients and moments in, runs its steps there and
+  // copies them back, so a step's phases pass no data through memory
+  int lds, lds_floats;
 };
+constexpr int kTinyLdsFloats = 12 * 1024;  // 48 KiB of dynamic LDS
+
+// Layer l with its arrays in LDS when the launch keeps the state there.
+__device__ __forceinline__ TinyLayerArg tiny_layer(const TinyArgs& a, float* st, int l) {
+  TinyLayerArg ly = a.L[l];
+  if (a.lds) {
+    ly.C = st + ly.sC;
+    ly.m = st + ly.sm;
+    ly.v = st + ly.sv;
+    ly.t = st + ly.st;
+    ly.y = st + ly.sy;
+    ly.dy = st + ly.sdy;
+  }
+  return ly;
+}
 
 __device__ __forceinline__ float tiny_round(float v, int bf) { return bf ? (float)(__bf16)v : v; }
 
@@ -250,25 +272,64 @@ __device__ float tiny_block_sum(float* red, float v) {
   return r;
 }
 
+// nsteps steps on the same x / target (the executor's fit), one after the
+// other in this one workgroup: step k's loss also goes to losses[k] when given.
+// A barrier ends each layer's update, so the next step reads the new
+// coefficients.
 __global__ void __launch_bounds__(1024)
 k_tiny_step(TinyArgs a, const float* __restrict__ x, const void* __restrict__ target,
-            int64_t* __restrict__ step, float* __restrict__ loss, float* __restrict__ loss_copy) {
+            int64_t* __restrict__ step, float* __restrict__ loss, float* __restrict__ losses,
+            int nsteps) {
   __shared__ float red[1024];
-  __shared__ float sc[2];
+  __shared__ float scs[kTinyStepsPerLaunch][2];
+  extern __shared__ float st_lds[];
   const int tid = threadIdx.x, nt = blockDim.x;
   const int64_t B = a.B;
   const int bf = a.bf16;
-  if (a.opt == CKAN_OPT_ADAM && tid == 0) {  // the device step count, as k_adam_scalars
-    const int64_t s1 = *step + 1;
-    *step = s1;
-    sc[0] = (float)(-(a.lr_d / (1.0 - pow(a.b1_d, (double)s1))));
-    sc[1] = (float)sqrt(1.0 - pow(a.b2_d, (double)s1));
+  auto move_state = [&](bool in) {  // coefficients and moments, global <-> LDS
+    for (int l = 0; l < a.nl; ++l) {
+      const TinyLayerArg g = a.L[l];
+      const int64_t n = (int64_t)g.I * g.O * g.D;
+      const bool adam = a.opt == CKAN_OPT_ADAM;
+      for (int64_t q = tid; q < n; q += nt) {
+        if (in) {
+          st_lds[g.sC + q] = g.C[q];
+          if (adam) {
+            st_lds[g.sm + q] = g.m[q];
+            st_lds[g.sv + q] = g.v[q];
+          }
+        } else {
+          g.C[q] = st_lds[g.sC + q];
+          if (adam) {
+            g.m[q] = st_lds[g.sm + q];
+            g.v[q] = st_lds[g.sv + q];
+          }
+        }
+      }
+    }
+    __syncthreads();
+  };
+  if (a.lds) move_state(true);
+  if (a.opt == CKAN_OPT_ADAM) {
+    // every step's Adam scalars up front, one step per thread (as
+    // k_adam_scalars, in double from the device step count): a pow per step
+    // on one thread would hold every step's barrier
+    const int64_t s0 = *step;
+    for (int k = tid; k < nsteps; k += nt) {
+      const double s1 = (double)(s0 + k + 1);
+      scs[k][0] = (float)(-(a.lr_d / (1.0 - pow(a.b1_d, s1))));
+      scs[k][1] = (float)sqrt(1.0 - pow(a.b2_d, s1));
+    }
+    __syncthreads();  // every thread has read the count
+    if (tid == 0) *step = s0 + nsteps;
   }
+  for (int ks = 0; ks < nsteps; ++ks) {
+  const float* sc = scs[ks];
 
   // ---- forward: t = tanh(in); y = sum_i C[i,o,0] + sum_{i,d>=1} T_d(t) C[i,o,d]
   const float* in = x;
   for (int l = 0; l < a.nl; ++l) {
-    const TinyLayerArg ly = a.L[l];
+    const TinyLayerArg ly = tiny_layer(a, st_lds, l);
     const int I = ly.I, O = ly.O, D = ly.D;
     for (int64_t q = tid; q < B * I; q += nt) ly.t[q] = tanhf(in[q]);
     __syncthreads();
@@ -296,7 +357,7 @@ k_tiny_step(TinyArgs a, const float* __restrict__ x, const void* __restrict__ ta
   }
 
   // ---- loss and its gradient (mean reduction)
-  const TinyLayerArg last = a.L[a.nl - 1];
+  const TinyLayerArg last = tiny_layer(a, st_lds, a.nl - 1);
   const int O = last.O;
   float part = 0.0f;
   if (a.loss == CKAN_LOSS_MSE) {
@@ -327,17 +388,17 @@ k_tiny_step(TinyArgs a, const float* __restrict__ x, const void* __restrict__ ta
   }
   if (tid == 0) {
     *loss = part;
-    if (loss_copy) *loss_copy = part;
+    if (losses) losses[ks] = part;
   }
   __syncthreads();
 
   // ---- backward and the optimizer, last layer first
   for (int l = a.nl - 1; l >= 0; --l) {
-    const TinyLayerArg ly = a.L[l];
+    const TinyLayerArg ly = tiny_layer(a, st_lds, l);
     const int I = ly.I, Ol = ly.O, D = ly.D;
     if (l > 0) {
       // dx[b,i] = (1 - t^2) sum_d U_{d-1}(t) sum_o dy[b,o] d C[i,o,d]
-      float* dx = a.L[l - 1].dy;
+      float* dx = tiny_layer(a, st_lds, l - 1).dy;
       for (int64_t q = tid; q < B * I; q += nt) {
         const int64_t b = q / I;
         const int i = (int)(q - b * I);
@@ -406,6 +467,8 @@ k_tiny_step(TinyArgs a, const float* __restrict__ x, const void* __restrict__ ta
     }
     __syncthreads();
   }
+  }  // steps
+  if (a.lds) move_state(false);
 }
 
 int grid_of(int64_t n) {
@@ -499,15 +562,28 @@ bool tiny_eligible(const ckan_exec* ex) {
   return macs <= kTinyMaxMacs;
 }
 
-int run_tiny(ckan_exec* ex, const float* x, const void* target, float* loss_copy, hipStream_t s) {
+int run_tiny(ckan_exec* ex, const float* x, const void* target, float* losses, hipStream_t s,
+             int nsteps = 1) {
   const auto& c = ex->cfg;
   TinyArgs a{};
   a.nl = c.n_layers;
+  int64_t off = 0;
+  const bool adam = c.optimizer == CKAN_OPT_ADAM;
   for (int l = 0; l < a.nl; ++l) {
     const auto& ly = ex->layers[l];
-    a.L[l] = TinyLayerArg{ly.C, ly.m, ly.v, ly.t, ly.y, ly.dy, ly.desc.in_dim, ly.desc.out_dim,
-                          ly.desc.degree + 1};
+    TinyLayerArg& t = a.L[l];
+    t = TinyLayerArg{ly.C, ly.m, ly.v, ly.t, ly.y, ly.dy, ly.desc.in_dim, ly.desc.out_dim,
+                     ly.desc.degree + 1};
+    const int64_t nc = (int64_t)t.I * t.O * t.D, bi = c.batch * t.I, bo = c.batch * t.O;
+    t.sC = (int)off; off += nc;
+    t.sm = (int)off; off += adam ? nc : 0;
+    t.sv = (int)off; off += adam ? nc : 0;
+    t.st = (int)off; off += bi;
+    t.sy = (int)off; off += bo;
+    t.sdy = (int)off; off += bo;
   }
+  a.lds = off <= kTinyLdsFloats;
+  a.lds_floats = a.lds ? (int)off : 0;
   a.loss = c.loss;
   a.opt = c.optimizer;
   a.bf16 = c.compute == CKAN_COMPUTE_BF16;
@@ -521,8 +597,17 @@ int run_tiny(ckan_exec* ex, const float* x, const void* target, float* loss_copy
   a.lr_d = (double)c.lr;
   a.b1_d = (double)c.beta1;
   a.b2_d = (double)c.beta2;
-  hipLaunchKernelGGL(k_tiny_step, dim3(1), dim3(1024), 0, s, a, x, target, ex->step, ex->loss,
-                     loss_copy);
+  // threads: the widest elementwise phase (B x width), as a power of two
+  // from 64 to 1024: idle waves only lengthen every barrier of the step
+  int64_t widest = 1;
+  for (int l = 0; l < a.nl; ++l) {
+    const int64_t w = c.batch * (a.L[l].I > a.L[l].O ? a.L[l].I : a.L[l].O);
+    if (w > widest) widest = w;
+  }
+  int threads = 64;
+  while (threads < 1024 && threads < widest) threads *= 2;
+  hipLaunchKernelGGL(k_tiny_step, dim3(1), dim3(threads), (size_t)a.lds_floats * sizeof(float), s,
+                     a, x, target, ex->step, ex->loss, losses, nsteps);
   return hipGetLastError() == hipSuccess ? CKAN_OK : efail(CKAN_ERR_HIP, "executor: step launch failed");
 }
 
@@ -864,6 +949,13 @@ int ckan_exec_steps(ckan_exec* ex, const float* x, const void* target, int64_t n
     hipStreamWaitEvent(s, ex->ev_out, 0);
   }
   int rc;
+  if (ex->tiny) {  // the steps in one launch per chunk: no launch gap between steps
+    for (int64_t k = 0; k < nsteps; k += kTinyStepsPerLaunch) {
+      const int n = (int)(nsteps - k < kTinyStepsPerLaunch ? nsteps - k : kTinyStepsPerLaunch);
+      if ((rc = run_tiny(ex, x, target, losses ? losses + k : nullptr, s, n))) return rc;
+    }
+    return CKAN_OK;
+  }
   for (int64_t k = 0; k < nsteps; ++k) {
     float* lk = losses ? losses + k : nullptr;
     if ((rc = run_step(ex, x, target, s, lk))) return rc;
