@@ -165,7 +165,8 @@ def _suite(only=SUITE, cpu=True):
         out["cfg1"] = {"workload": "ChebyKANLayer(1,1,8) sin(2 pi x), 100 pts, MSE+Adam, resident",
                        "us_per_step": ms_fit * 1e3, "steps": 1000,
                        "timing": "1000 steps issued by one ResidentExecutor.fit call "
-                                 "(ckan_exec_steps), each step one single-workgroup launch",
+                                 "(ckan_exec_steps): one single-workgroup launch runs them "
+                                 "one after another, the state in LDS",
                        "final_loss": float(fit_losses[-1][-1].item()),
                        "us_per_step_python_step_loop": res1["eager"][0] * 1e3,
                        "us_per_step_hip_graph": res1["graph"][0] * 1e3}
