@@ -717,7 +717,7 @@ __global__ void __launch_bounds__(256)
 k_dc_small(const float* __restrict__ dy, const float* __restrict__ t, float* __restrict__ dC,
            DcOut om, Plan p) {
   __shared__ float ts[kDcSmallRows][9];
-  __shared__ float ys[kDcSmallRows][9];
+  __shared__ __attribute__((aligned(16))) float ys[kDcSmallRows][8];
   __shared__ float red[4][64][DMAX + 1];
   const int tid = threadIdx.x, q = tid & 63, rq = tid >> 6;
   const int il = q >> 3, ol = q & 7;
@@ -742,39 +742,80 @@ k_dc_small(const float* __restrict__ dy, const float* __restrict__ t, float* __r
     ys[r][c] = yl[u];
   }
   __syncthreads();
-  // rows 4 at a time with 4 accumulator sets: independent recurrences and
-  // LDS reads in flight together (one row at a time was latency-bound);
-  // the sets are added in order at the end
-  constexpr int RU = 4;
-  float acc[RU][DMAX];
+  if constexpr (DMAX <= 9) {
+    // thread = (input il2, output half og, row slice rs of 16): the
+    // recurrence of (row, input) serves 4 outputs (one per (input, output)
+    // pair and row made it vector-ALU-bound: config 2's 784 -> 64 layer
+    // 11.8 us); the wave's 4 row slices (lane bits 4-5) are added by a fixed
+    // butterfly, the 4 waves' in order below
+    const int lane = tid & 63;
+    const int il2 = lane & 7, og = (lane >> 3) & 1, rs = rq * 4 + (lane >> 4);
+    float acc[4][DMAX];
 #pragma unroll
-  for (int u = 0; u < RU; ++u)
+    for (int c = 0; c < 4; ++c)
 #pragma unroll
-    for (int d = 0; d < DMAX; ++d) acc[u][d] = 0.0f;
-  const int per = (rows + 3) / 4, r0 = rq * per, r1 = min(rows, r0 + per);
-  for (int r = r0; r < r1; r += RU) {
-    float tv[RU], yv[RU];
-#pragma unroll
-    for (int u = 0; u < RU; ++u) {  // rows past r1 add zero (their dy is masked)
-      const bool in = r + u < r1;
-      tv[u] = ts[in ? r + u : r][il];
-      yv[u] = in ? ys[r + u][ol] : 0.0f;
-    }
-#pragma unroll
-    for (int u = 0; u < RU; ++u) {
-      const float t2 = tv[u] + tv[u];
-      float pm = tv[u], pc = 1.0f;  // T_{-1} = t, T_0 = 1
+      for (int d = 0; d < DMAX; ++d) acc[c][d] = 0.0f;
+    for (int r = rs; r < rows; r += 16) {
+      const float tv = ts[r][il2], t2 = tv + tv;
+      const f32x4_t yv = *reinterpret_cast<const f32x4_t*>(&ys[r][og * 4]);
+      float pm = tv, pc = 1.0f;  // T_{-1} = t, T_0 = 1
 #pragma unroll
       for (int d = 0; d < DMAX; ++d) {
-        acc[u][d] = fmaf(pc, yv[u], acc[u][d]);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[c][d] = fmaf(pc, yv[c], acc[c][d]);
         const float nx = fmaf(t2, pc, -pm);
         pm = pc;
         pc = nx;
       }
     }
-  }
 #pragma unroll
-  for (int d = 0; d < DMAX; ++d) red[rq][q][d] = ((acc[0][d] + acc[1][d]) + acc[2][d]) + acc[3][d];
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int d = 0; d < DMAX; ++d) {
+        acc[c][d] += __shfl_xor(acc[c][d], 16);
+        acc[c][d] += __shfl_xor(acc[c][d], 32);
+      }
+    if ((lane >> 4) == 0) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int d = 0; d < DMAX; ++d) red[rq][il2 * 8 + og * 4 + c][d] = acc[c][d];
+    }
+  } else {
+    // rows 4 at a time with 4 accumulator sets: independent recurrences and
+    // LDS reads in flight together (one row at a time was latency-bound);
+    // the sets are added in order at the end
+    constexpr int RU = 4;
+    float acc[RU][DMAX];
+#pragma unroll
+    for (int u = 0; u < RU; ++u)
+#pragma unroll
+      for (int d = 0; d < DMAX; ++d) acc[u][d] = 0.0f;
+    const int per = (rows + 3) / 4, r0 = rq * per, r1 = min(rows, r0 + per);
+    for (int r = r0; r < r1; r += RU) {
+      float tv[RU], yv[RU];
+#pragma unroll
+      for (int u = 0; u < RU; ++u) {  // rows past r1 add zero (their dy is masked)
+        const bool in = r + u < r1;
+        tv[u] = ts[in ? r + u : r][il];
+        yv[u] = in ? ys[r + u][ol] : 0.0f;
+      }
+#pragma unroll
+      for (int u = 0; u < RU; ++u) {
+        const float t2 = tv[u] + tv[u];
+        float pm = tv[u], pc = 1.0f;  // T_{-1} = t, T_0 = 1
+#pragma unroll
+        for (int d = 0; d < DMAX; ++d) {
+          acc[u][d] = fmaf(pc, yv[u], acc[u][d]);
+          const float nx = fmaf(t2, pc, -pm);
+          pm = pc;
+          pc = nx;
+        }
+      }
+    }
+#pragma unroll
+    for (int d = 0; d < DMAX; ++d) red[rq][q][d] = ((acc[0][d] + acc[1][d]) + acc[2][d]) + acc[3][d];
+  }
   __syncthreads();
   // the block's 8 x 8 x D results, spread over all threads: input il's 8
   // outputs are one contiguous run of 8 D floats of dC (one round trip for

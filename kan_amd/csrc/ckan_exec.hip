@@ -653,7 +653,9 @@ int run_step(ckan_exec* ex, const float* x, const void* target, hipStream_t s,
     hipLaunchKernelGGL(k_sum_scalar, dim3(1), dim3(256), 0, s, ex->loss_part,
                        (int64_t)kLossBlocks, (float)(1.0 / (double)n), ex->loss, loss_copy);
   } else if (B <= kCeSmallRows && O <= kCeSmallO) {
-    hipLaunchKernelGGL(k_ce_small, dim3(1), dim3(kCeSmallRows), 0, s, last.y,
+    // one thread per row, at least the 256 of the fixed-order sum
+    const int threads = B <= 256 ? 256 : B <= 512 ? 512 : kCeSmallRows;
+    hipLaunchKernelGGL(k_ce_small, dim3(1), dim3(threads), 0, s, last.y,
                        reinterpret_cast<const int64_t*>(target), last.dy, (int)B, O, ex->loss,
                        loss_copy);
   } else {
