@@ -240,6 +240,11 @@ int ckan::backward_impl(const ckan_desc* desc, const float* t_cache, const void*
     launch_prep_dy(dy, dYx, dYc, colsum, p, prep_x, prep_c, s);
   }
   if ((rc = check_launch("prep_dy"))) return rc;
+  if (need_dx && L.dx_small && need_dc && L.dc_small && bwd_small_one_launch(p)) {
+    ProfScope ps("bwd_small", s);
+    launch_bwd_small(dy, packed, t_cache, dx, dcoeffs, om, p, s);
+    return check_launch("bwd_small");
+  }
   if (need_dx) {
     ProfScope ps("dx_gemm", s);
     if (L.dx_small) launch_dx_small(dy, packed, t_cache, dx, p, s);

@@ -713,15 +713,15 @@ void launch_bias_reduce(void* packed, const Plan& p, hipStream_t s) {
 // recurrence in registers), and the quarters are added in order through LDS.
 constexpr int kDcSmallRows = 256;  // rows staged at once (all of the batch)
 template <int DMAX>
-__global__ void __launch_bounds__(256)
-k_dc_small(const float* __restrict__ dy, const float* __restrict__ t, float* __restrict__ dC,
-           DcOut om, Plan p) {
+__device__ __forceinline__ void dc_small_body(const float* __restrict__ dy, const float* __restrict__ t,
+                                              float* __restrict__ dC, const DcOut& om,
+                                              const Plan& p, int bx, int by) {
   __shared__ float ts[kDcSmallRows][9];
   __shared__ __attribute__((aligned(16))) float ys[kDcSmallRows][8];
   __shared__ float red[4][64][DMAX + 1];
   const int tid = threadIdx.x, q = tid & 63, rq = tid >> 6;
   const int il = q >> 3, ol = q & 7;
-  const int i0 = blockIdx.x * 8, o0 = blockIdx.y * 8;
+  const int i0 = bx * 8, o0 = by * 8;
   const int D = p.D;
   const int rows = (int)p.B;  // <= kDcSmallRows (dc_small_ok)
   // every load of the staging in flight at once (a rolled loop waited for
@@ -829,6 +829,155 @@ k_dc_small(const float* __restrict__ dy, const float* __restrict__ t, float* __r
     const float g = ((red[0][kq][d] + red[1][kq][d]) + red[2][kq][d]) + red[3][kq][d];
     dc_write(dC + ((size_t)i * p.O + o0) * D + rem, g, om);
   }
+}
+
+template <int DMAX>
+__global__ void __launch_bounds__(256)
+k_dc_small(const float* __restrict__ dy, const float* __restrict__ t, float* __restrict__ dC,
+           DcOut om, Plan p) {
+  dc_small_body<DMAX>(dy, t, dC, om, p, blockIdx.x, blockIdx.y);
+}
+
+// Small dx: dx[b, i] = t'(x) sum_e U_e(t) sum_o dy[b, o] Cb(i, o, e) for
+// layers whose reduction over outputs is short (config 2's 64 -> 10 layer),
+// where the pipelined kernel would be all prologue.  Cb is the packed dX
+// operand, (e + 1) C[i, o, e + 1] in the compute precision, read here in its
+// fragment layout.  Block: 32 rows x 8 inputs, one (row, input) per thread;
+// dy rows and the block's coefficients are staged in LDS with every load in
+// flight at once.
+constexpr int kDxSmallO = 64;  // outputs staged at once (all of them)
+template <int P, bool BF>
+__device__ __forceinline__ void dx_small_body(const float* __restrict__ dy,
+                                              const typename Elem<BF>::type* __restrict__ Cb,
+                                              const float* __restrict__ t, float* __restrict__ dx,
+                                              const Plan& p, int bx, int by) {
+  typedef typename Elem<BF>::type E;
+  __shared__ float cs[8][kDxSmallO][P + 1];
+  __shared__ float ys[32][kDxSmallO + 1];
+  const int tid = threadIdx.x;
+  const int64_t b0 = (int64_t)bx * 32;
+  const int i0 = by * 8;
+  constexpr int NC = 8 * kDxSmallO * P / 256, NY = 32 * kDxSmallO / 256;
+  float cv[NC], yv[NY];
+#pragma unroll
+  for (int u = 0; u < NC; ++u) {  // k = (il, o, e): Cb fragment element of (i, o, e)
+    const int k = tid + 256 * u, il = k / (kDxSmallO * P), rem = k - il * kDxSmallO * P;
+    const int o = rem / P, e = rem - o * P, i = i0 + il;
+    float v = 0.0f;
+    if (i < p.I && o < p.O) {
+      const size_t q = ((size_t)((i >> 5) * P + e) * p.KBx + (o >> 4)) * kFragElems +
+                       ((i & 31) + 32 * ((o & 15) >> 3)) * 8 + (o & 7);
+      if constexpr (BF) v = __uint_as_float((uint32_t)Cb[q] << 16);
+      else v = Cb[q];
+    }
+    cv[u] = v;
+  }
+#pragma unroll
+  for (int u = 0; u < NY; ++u) {
+    const int k = tid + 256 * u, r = k / kDxSmallO, o = k - r * kDxSmallO;
+    yv[u] = (b0 + r < p.B && o < p.O) ? dy[(b0 + r) * p.O + o] : 0.0f;
+  }
+#pragma unroll
+  for (int u = 0; u < NC; ++u) {
+    const int k = tid + 256 * u, il = k / (kDxSmallO * P), rem = k - il * kDxSmallO * P;
+    cs[il][rem / P][rem % P] = cv[u];
+  }
+#pragma unroll
+  for (int u = 0; u < NY; ++u) {
+    const int k = tid + 256 * u;
+    ys[k / kDxSmallO][k % kDxSmallO] = yv[u];
+  }
+  __syncthreads();
+  const int r = tid >> 3, il = tid & 7;
+  const int64_t b = b0 + r;
+  const int i = i0 + il;
+  if (b >= p.B || i >= p.I) return;
+  float g[P];
+#pragma unroll
+  for (int e = 0; e < P; ++e) g[e] = 0.0f;
+  for (int o = 0; o < p.O; ++o) {
+    const float a = ys[r][o];
+#pragma unroll
+    for (int e = 0; e < P; ++e) g[e] = fmaf(a, cs[il][o][e], g[e]);
+  }
+  const float tv = t[b * p.I_sg + i], t2 = tv + tv;
+  float up = 0.0f, u = 1.0f, s = 0.0f;  // U_{e-1}, U_e
+#pragma unroll
+  for (int e = 0; e < P; ++e) {
+    s = fmaf(g[e], u, s);
+    const float un = fmaf(t2, u, -up);
+    up = u;
+    u = un;
+  }
+  __builtin_nontemporal_store(s * input_slope(tv, p), dx + b * p.I + i);
+}
+
+template <int P, bool BF>
+__global__ void __launch_bounds__(256)
+k_dx_small(const float* __restrict__ dy, const typename Elem<BF>::type* __restrict__ Cb,
+           const float* __restrict__ t, float* __restrict__ dx, Plan p) {
+  dx_small_body<P, BF>(dy, Cb, t, dx, p, blockIdx.x, blockIdx.y);
+}
+
+bool dx_small_ok(const Plan& p) {
+  return p.O <= kDxSmallO && (int64_t)p.B * p.I * p.O * p.P <= ((int64_t)1 << 27);
+}
+
+void launch_dx_small(const float* dy, const void* packed, const float* t, float* dx,
+                     const Plan& p, hipStream_t s) {
+  const dim3 grid((unsigned)ceil_div(p.B, 32), (unsigned)ceil_div(p.I, 8));
+#define CKAN_DXS(PP, BB)                                                                       \
+  hipLaunchKernelGGL((k_dx_small<PP, BB>), grid, dim3(256), 0, s, dy,                          \
+                     reinterpret_cast<const typename Elem<BB>::type*>(packed) + packed_cf_elems(p), \
+                     t, dx, p)
+  const bool bf = p.esz == 2;
+  switch (p.P) {
+    case 2: if (bf) CKAN_DXS(2, true); else CKAN_DXS(2, false); break;
+    case 4: if (bf) CKAN_DXS(4, true); else CKAN_DXS(4, false); break;
+    case 8: if (bf) CKAN_DXS(8, true); else CKAN_DXS(8, false); break;
+    default: if (bf) CKAN_DXS(16, true); else CKAN_DXS(16, false); break;
+  }
+#undef CKAN_DXS
+}
+
+
+// Both small backward kernels of one layer in one launch (they read the same
+// dy and tanh cache and write different outputs: dx, and dC or the layer's
+// coefficients): blocks [0, ndx) take dx, the rest dC.
+template <int P, bool BF>
+__global__ void __launch_bounds__(256)
+k_bwd_small(const float* __restrict__ dy, const typename Elem<BF>::type* __restrict__ Cb,
+            const float* __restrict__ t, float* __restrict__ dx, float* __restrict__ dC, DcOut om,
+            Plan p, int nx_dx, int ndx, int nx_dc) {
+  const int bid = blockIdx.x;
+  if (bid < ndx) dx_small_body<P, BF>(dy, Cb, t, dx, p, bid % nx_dx, bid / nx_dx);
+  else dc_small_body<P + 1>(dy, t, dC, om, p, (bid - ndx) % nx_dc, (bid - ndx) / nx_dc);
+}
+
+// One round of the fused launch (its LDS, both kernels' arrays, fits 3 blocks
+// per CU): larger layers keep the two launches, each at its own occupancy.
+bool bwd_small_one_launch(const Plan& p) {
+  const int64_t ndx = ceil_div(p.B, 32) * ceil_div(p.I, 8), ndc = ceil_div(p.I, 8) * ceil_div(p.O, 8);
+  return ndx + ndc <= 3 * 256;
+}
+
+void launch_bwd_small(const float* dy, const void* packed, const float* t, float* dx, float* dC,
+                      DcOut om, const Plan& p, hipStream_t s) {
+  const int nx_dx = (int)ceil_div(p.B, 32), nx_dc = (int)ceil_div(p.I, 8);
+  const int ndx = nx_dx * (int)ceil_div(p.I, 8), ndc = nx_dc * (int)ceil_div(p.O, 8);
+  const dim3 grid((unsigned)(ndx + ndc));
+#define CKAN_BWS(PP, BB)                                                                        \
+  hipLaunchKernelGGL((k_bwd_small<PP, BB>), grid, dim3(256), 0, s, dy,                          \
+                     reinterpret_cast<const typename Elem<BB>::type*>(packed) + packed_cf_elems(p), \
+                     t, dx, dC, om, p, nx_dx, ndx, nx_dc)
+  const bool bf = p.esz == 2;
+  switch (p.P) {
+    case 2: if (bf) CKAN_BWS(2, true); else CKAN_BWS(2, false); break;
+    case 4: if (bf) CKAN_BWS(4, true); else CKAN_BWS(4, false); break;
+    case 8: if (bf) CKAN_BWS(8, true); else CKAN_BWS(8, false); break;
+    default: if (bf) CKAN_BWS(16, true); else CKAN_BWS(16, false); break;
+  }
+#undef CKAN_BWS
 }
 
 bool dc_small_ok(const Plan& p) {

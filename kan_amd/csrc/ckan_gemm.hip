@@ -2524,100 +2524,6 @@ void launch_dx_gemm(const void* dYx, const void* packed, const float* t, float* 
   }
 }
 
-// Small dx: dx[b, i] = t'(x) sum_e U_e(t) sum_o dy[b, o] Cb(i, o, e) for
-// layers whose reduction over outputs is short (config 2's 64 -> 10 layer),
-// where the pipelined kernel would be all prologue.  Cb is the packed dX
-// operand, (e + 1) C[i, o, e + 1] in the compute precision, read here in its
-// fragment layout.  Block: 32 rows x 8 inputs, one (row, input) per thread;
-// dy rows and the block's coefficients are staged in LDS with every load in
-// flight at once.
-constexpr int kDxSmallO = 64;  // outputs staged at once (all of them)
-template <int P, bool BF>
-__global__ void __launch_bounds__(256)
-k_dx_small(const float* __restrict__ dy, const typename Elem<BF>::type* __restrict__ Cb,
-           const float* __restrict__ t, float* __restrict__ dx, Plan p) {
-  typedef typename Elem<BF>::type E;
-  __shared__ float cs[8][kDxSmallO][P + 1];
-  __shared__ float ys[32][kDxSmallO + 1];
-  const int tid = threadIdx.x;
-  const int64_t b0 = (int64_t)blockIdx.x * 32;
-  const int i0 = blockIdx.y * 8;
-  constexpr int NC = 8 * kDxSmallO * P / 256, NY = 32 * kDxSmallO / 256;
-  float cv[NC], yv[NY];
-#pragma unroll
-  for (int u = 0; u < NC; ++u) {  // k = (il, o, e): Cb fragment element of (i, o, e)
-    const int k = tid + 256 * u, il = k / (kDxSmallO * P), rem = k - il * kDxSmallO * P;
-    const int o = rem / P, e = rem - o * P, i = i0 + il;
-    float v = 0.0f;
-    if (i < p.I && o < p.O) {
-      const size_t q = ((size_t)((i >> 5) * P + e) * p.KBx + (o >> 4)) * kFragElems +
-                       ((i & 31) + 32 * ((o & 15) >> 3)) * 8 + (o & 7);
-      if constexpr (BF) v = __uint_as_float((uint32_t)Cb[q] << 16);
-      else v = Cb[q];
-    }
-    cv[u] = v;
-  }
-#pragma unroll
-  for (int u = 0; u < NY; ++u) {
-    const int k = tid + 256 * u, r = k / kDxSmallO, o = k - r * kDxSmallO;
-    yv[u] = (b0 + r < p.B && o < p.O) ? dy[(b0 + r) * p.O + o] : 0.0f;
-  }
-#pragma unroll
-  for (int u = 0; u < NC; ++u) {
-    const int k = tid + 256 * u, il = k / (kDxSmallO * P), rem = k - il * kDxSmallO * P;
-    cs[il][rem / P][rem % P] = cv[u];
-  }
-#pragma unroll
-  for (int u = 0; u < NY; ++u) {
-    const int k = tid + 256 * u;
-    ys[k / kDxSmallO][k % kDxSmallO] = yv[u];
-  }
-  __syncthreads();
-  const int r = tid >> 3, il = tid & 7;
-  const int64_t b = b0 + r;
-  const int i = i0 + il;
-  if (b >= p.B || i >= p.I) return;
-  float g[P];
-#pragma unroll
-  for (int e = 0; e < P; ++e) g[e] = 0.0f;
-  for (int o = 0; o < p.O; ++o) {
-    const float a = ys[r][o];
-#pragma unroll
-    for (int e = 0; e < P; ++e) g[e] = fmaf(a, cs[il][o][e], g[e]);
-  }
-  const float tv = t[b * p.I_sg + i], t2 = tv + tv;
-  float up = 0.0f, u = 1.0f, s = 0.0f;  // U_{e-1}, U_e
-#pragma unroll
-  for (int e = 0; e < P; ++e) {
-    s = fmaf(g[e], u, s);
-    const float un = fmaf(t2, u, -up);
-    up = u;
-    u = un;
-  }
-  __builtin_nontemporal_store(s * input_slope(tv, p), dx + b * p.I + i);
-}
-
-bool dx_small_ok(const Plan& p) {
-  return p.O <= kDxSmallO && (int64_t)p.B * p.I * p.O * p.P <= ((int64_t)1 << 27);
-}
-
-void launch_dx_small(const float* dy, const void* packed, const float* t, float* dx,
-                     const Plan& p, hipStream_t s) {
-  const dim3 grid((unsigned)ceil_div(p.B, 32), (unsigned)ceil_div(p.I, 8));
-#define CKAN_DXS(PP, BB)                                                                       \
-  hipLaunchKernelGGL((k_dx_small<PP, BB>), grid, dim3(256), 0, s, dy,                          \
-                     reinterpret_cast<const typename Elem<BB>::type*>(packed) + packed_cf_elems(p), \
-                     t, dx, p)
-  const bool bf = p.esz == 2;
-  switch (p.P) {
-    case 2: if (bf) CKAN_DXS(2, true); else CKAN_DXS(2, false); break;
-    case 4: if (bf) CKAN_DXS(4, true); else CKAN_DXS(4, false); break;
-    case 8: if (bf) CKAN_DXS(8, true); else CKAN_DXS(8, false); break;
-    default: if (bf) CKAN_DXS(16, true); else CKAN_DXS(16, false); break;
-  }
-#undef CKAN_DXS
-}
-
 // dC stage depth in k-blocks: 4 for bf16, 2 for fp32 (LDS bound).
 template <bool BF> struct DcKI { static constexpr int v = BF ? 4 : 2; };
 

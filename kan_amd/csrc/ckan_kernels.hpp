@@ -193,6 +193,11 @@ void launch_dx_small(const float* dy, const void* packed, const float* t, float*
                      const Plan& p, hipStream_t s);
 void launch_dc_small(const float* dy, const float* t, float* dC, DcOut om, const Plan& p,
                      hipStream_t s);
+// launch_dx_small and launch_dc_small of one layer as one launch, for layers
+// where that is one round of blocks (bwd_small_one_launch)
+bool bwd_small_one_launch(const Plan& p);
+void launch_bwd_small(const float* dy, const void* packed, const float* t, float* dx, float* dC,
+                      DcOut om, const Plan& p, hipStream_t s);
 void launch_dc_gemm(const void* dYc, const float* t, const float* colsum, float* part, float* dC,
                     DcOut om, const Plan& p, const BwdLayout& L, hipStream_t s);
 void launch_sgd(float* p, const float* g, int64_t n, float lr, float wd, hipStream_t s);
