@@ -409,7 +409,7 @@ int pack_forward_impl(const ckan_desc* desc, const ckan_basis_spec* spec, const 
                       size_t ws_bytes, void* stream, bool t_ready, bool out_tanh);
 int forward_packed(const Plan& p, const FwdChoice& c, const void* packed, const float* x, float* y,
                    float* t_cache, void* ws, hipStream_t s, bool t_done, bool sum_in_gemm,
-                   bool out_tanh);
+                   bool out_tanh, bool reduce = true);
 }
 
 int ckan_pack_forward(const ckan_desc* desc, const ckan_basis_spec* spec, const void* coeffs,
@@ -468,7 +468,7 @@ int pack_forward_impl(const ckan_desc* desc, const ckan_basis_spec* spec, const 
 // already, then the GEMM.
 int forward_packed(const Plan& p, const FwdChoice& c, const void* packed, const float* x, float* y,
                    float* t_cache, void* ws, hipStream_t s, bool t_done, bool sum_in_gemm,
-                   bool out_tanh) {
+                   bool out_tanh, bool reduce) {
   if (!t_done && fwd_reads_tcache(c)) {
     ProfScope ps("tanh", s);
     launch_tanh(x, t_cache, p, s);
@@ -477,7 +477,7 @@ int forward_packed(const Plan& p, const FwdChoice& c, const void* packed, const 
   if ((rc = check_launch("pack_forward: tanh"))) return rc;
   {
     ProfScope ps("fwd_gemm", s);
-    launch_fwd_gemm(x, t_cache, packed, y, ws, p, c, s, sum_in_gemm, out_tanh);
+    launch_fwd_gemm(x, t_cache, packed, y, ws, p, c, s, sum_in_gemm, out_tanh, reduce);
   }
   return check_launch("pack_forward: fwd_gemm");
 }
@@ -959,6 +959,54 @@ int ckan::pack2_forward_ex(const ckan_desc* da, const void* Ca, void* pka, const
   if ((rc = forward_packed(pa, ca, pka, xa, tb, ta, ws, s, ta_ready || fuse_tanh, sum_a, true)))
     return rc;
   return forward_packed(pb, cb, pkb, nullptr, outb, tb, ws, s, true, sum_b, outb_tanh);
+}
+
+bool ckan::pack2_tail_ce_fits(const ckan_desc* a, const ckan_desc* b) {
+  if (!pack_pair_fits(a, b) || a->compute != CKAN_COMPUTE_FP32 || b->compute != CKAN_COMPUTE_FP32 ||
+      b->input_map != CKAN_INPUT_TANH)
+    return false;
+  const Plan pa = plan_of(a);
+  return fwd_tail_ce_ok(pa, choose_fwd(pa), b->out_dim, b->degree + 1);
+}
+
+int ckan::pack2_forward_tail_ce(const ckan_desc* da, const void* Ca, void* pka, const float* xa,
+                                float* ta, bool ta_ready, const ckan_desc* db, const void* Cb,
+                                void* pkb, float* tb, float* yb, const int64_t* labels, float* dyb,
+                                float* loss_part, void* ws, size_t ws_bytes, void* stream) {
+  if (!pack2_tail_ce_fits(da, db) || (ta_ready && !layer_reads_tcache(da)))
+    return fail(CKAN_ERR_INVALID_ARG, "pack2_forward_tail_ce: the layer pair does not allow the fused tail");
+  if (!Ca || !pka || !Cb || !pkb || !ta || !tb || !yb || !labels || !dyb || !loss_part ||
+      (!xa && !ta_ready))
+    return fail(CKAN_ERR_INVALID_ARG, "pack2_forward_tail_ce: NULL pointer");
+  if (!aligned16(pka) || !aligned16(pkb) || !aligned16(ta) || !aligned16(tb))
+    return fail(CKAN_ERR_INVALID_ARG, "pack2_forward_tail_ce: packed buffers and caches must be 16-byte aligned");
+  const Plan pa = plan_of(da), pb = plan_of(db);
+  const FwdChoice ca = choose_fwd(pa);
+  const size_t need = fwd_ws_bytes(pa, ca);
+  if (ws_bytes < need)
+    return fail(CKAN_ERR_WORKSPACE, "forward workspace too small: %zu < %zu bytes", ws_bytes, need);
+  if (need && !ws) return fail(CKAN_ERR_INVALID_ARG, "workspace is NULL");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  // b's forward runs in the tail from its fp32 coefficients: b's packed
+  // bias slot is not filled (the step's backward reads only b's dX operand,
+  // and a later forward packs again)
+  const bool sum_a = fwd_sums_bias(pa, ca);
+  const bool fuse_tanh = !ta_ready && fwd_reads_tcache(ca) && pack_tanh_fusable(pa, xa);
+  {
+    ProfScope ps("pack2", s);
+    launch_pack_pair(reinterpret_cast<const float*>(Ca), pka, pa, !sum_a, fuse_tanh ? xa : nullptr,
+                     fuse_tanh ? ta : nullptr, reinterpret_cast<const float*>(Cb), pkb, pb, false, s);
+  }
+  int rc;
+  if ((rc = check_launch("pack2_forward_tail_ce: pack"))) return rc;
+  if ((rc = forward_packed(pa, ca, pka, xa, tb, ta, ws, s, ta_ready || fuse_tanh, sum_a, true, false)))
+    return rc;
+  {
+    ProfScope ps("fwd_tail", s);
+    launch_fwd_tail_ce(pka, ws, pa, ca, sum_a, tb, reinterpret_cast<const float*>(Cb), db->out_dim,
+                       db->degree + 1, yb, labels, dyb, loss_part, s);
+  }
+  return check_launch("pack2_forward_tail_ce: tail");
 }
 
 int ckan::pack_forward_ex(const ckan_desc* desc, const void* coeffs, void* packed, const float* x,

@@ -496,6 +496,9 @@ struct ckan_exec {
     // this layer's pack and the next layer's run as one launch (the next
     // layer's input comes from this one's tanh output)
     bool pack_pair = false;
+    // with pack_pair on the last two layers of a cross-entropy stack: the
+    // second layer's forward and the loss gradient run in one tail launch
+    bool tail_ce = false;
   };
   ckan_exec_config cfg;
   std::vector<int32_t> widths, degrees;
@@ -623,6 +626,16 @@ int run_step(ckan_exec* ex, const float* x, const void* target, hipStream_t s,
     // pack and forward in one call: tanh in the pack launch (or, after a layer
     // with tanh_out, already in ly.t), bias summed by the forward
     const bool t_ready = l > 0 && ex->layers[l - 1].tanh_out;
+    if (ly.tail_ce) {  // the last two layers, their packs, forwards and the loss gradient
+      auto& nx = ex->layers[l + 1];
+      if ((rc = pack2_forward_tail_ce(&ly.desc, ly.C, ly.packed, l == 0 ? x : ex->layers[l - 1].y,
+                                      ly.t, t_ready, &nx.desc, nx.C, nx.packed, nx.t, nx.y,
+                                      reinterpret_cast<const int64_t*>(target), nx.dy,
+                                      ex->loss_part, ex->fws, ex->fws_bytes, s)))
+        return rc;
+      ++l;
+      continue;
+    }
     if (ly.pack_pair) {  // layers l and l + 1: both packs in one launch
       auto& nx = ex->layers[l + 1];
       float* outb = nx.tanh_out ? ex->layers[l + 2].t : nx.y;
@@ -642,7 +655,11 @@ int run_step(ckan_exec* ex, const float* x, const void* target, hipStream_t s,
   auto& last = ex->layers[L - 1];
   const int64_t B = ex->cfg.batch;
   const int O = last.desc.out_dim;
-  if (ex->cfg.loss == CKAN_LOSS_MSE) {
+  const bool tail = L >= 2 && ex->layers[L - 2].tail_ce;
+  if (tail) {  // the rows' losses came from the tail launch: their mean
+    hipLaunchKernelGGL(k_sum_scalar, dim3(1), dim3(256), 0, s, ex->loss_part, B,
+                       (float)(1.0 / (double)B), ex->loss, loss_copy);
+  } else if (ex->cfg.loss == CKAN_LOSS_MSE) {
     const int64_t n = B * O;
     const int vec = n % 4 == 0 && (reinterpret_cast<uintptr_t>(target) & 15) == 0 &&
                     (reinterpret_cast<uintptr_t>(last.y) & 15) == 0 &&
@@ -751,6 +768,8 @@ int ckan_exec_create(const ckan_exec_config* cfg, ckan_exec** out, void* stream)
   for (int l = 0; rc == CKAN_OK && l + 1 < cfg->n_layers; ++l) {
     auto& ly = ex->layers[l];
     ly.pack_pair = ly.tanh_out && pack_pair_fits(&ly.desc, &ex->layers[l + 1].desc);
+    ly.tail_ce = ly.pack_pair && l + 2 == cfg->n_layers && cfg->loss == CKAN_LOSS_CE &&
+                 pack2_tail_ce_fits(&ly.desc, &ex->layers[l + 1].desc);
     if (ly.pack_pair) ++l;  // the next layer's pack is taken
   }
   if (rc == CKAN_OK) {

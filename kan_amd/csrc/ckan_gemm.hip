@@ -748,6 +748,85 @@ k_fwd_reduce(const float* __restrict__ part, int S, const float* __restrict__ bi
   }
 }
 
+// The end of a stack's training forward, one row per wave: layer a's split
+// sum (the bits of k_fwd_reduce with out_tanh: tanh(y_a) into layer b's
+// tanh cache tb, pitch a.O = b's inputs), then the last layer b on the vector
+// ALU from its fp32 coefficients Cb [Ib, Ob, Db] (lane i takes input i: its
+// T_d(t_i) by the three-term recurrence, times Cb[i, k, d]; the 64 lanes are
+// added by an xor butterfly, which leaves the same bits in every lane), then
+// the row's softmax cross-entropy as k_ce_small computes it: yb, dyb =
+// (softmax - onehot) / B and the row's loss into loss_part[r], whose mean
+// k_sum_scalar takes in k_ce_small's order.  Ib <= 64, Ob <= kTailO.
+constexpr int kTailO = 16, kTailRows = 4;
+__global__ void __launch_bounds__(256)
+k_fwd_tail_ce(const float* __restrict__ part, int S, const float* __restrict__ bias_f, Plan pa,
+              const float* __restrict__ bias_part, int nib, float* __restrict__ bias_out,
+              float* __restrict__ tb, const float* __restrict__ Cb, int Ob, int Db,
+              float* __restrict__ yb, const int64_t* __restrict__ labels, float* __restrict__ dyb,
+              float* __restrict__ loss_part) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * kTailRows + (threadIdx.x >> 6);
+  if (nib > 0 && blockIdx.x == 0)
+    for (int q = threadIdx.x; q < pa.O32; q += blockDim.x) bias_out[q] = bias_from_parts(bias_part, nib, pa.O32, q);
+  if (r >= pa.B) return;
+  const int Ib = pa.O;
+  float t = 0.0f;
+  if (lane < Ib) {
+    const float bias = nib > 0 ? bias_from_parts(bias_part, nib, pa.O32, lane) : bias_f[lane];
+    t = tanhf(split_sum(part + (size_t)r * pa.O32 + lane, (size_t)pa.B32 * pa.O32, (unsigned)S, bias));
+    tb[r * Ib + lane] = t;
+  }
+  float acc[kTailO];
+#pragma unroll
+  for (int k = 0; k < kTailO; ++k) acc[k] = 0.0f;
+  if (lane < Ib) {
+    const float* c = Cb + (size_t)lane * Ob * Db;
+    const float t2 = t + t;
+    float tm = 1.0f, tc = t;  // T_{d-1}, T_d from d = 0
+    for (int d = 0; d < Db; ++d) {
+      const float td = d == 0 ? 1.0f : tc;
+#pragma unroll
+      for (int k = 0; k < kTailO; ++k)
+        if (k < Ob) acc[k] = fmaf(c[k * Db + d], td, acc[k]);
+      if (d > 0) {
+        const float tn = fmaf(t2, tc, -tm);
+        tm = tc;
+        tc = tn;
+      }
+    }
+  }
+#pragma unroll
+  for (int w = 32; w >= 1; w >>= 1)
+#pragma unroll
+    for (int k = 0; k < kTailO; ++k) acc[k] += __shfl_xor(acc[k], w);
+  // the cross-entropy of row r (every lane holds the same y)
+  float m = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < kTailO; ++k)
+    if (k < Ob) m = fmaxf(m, acc[k]);
+  float e[kTailO];
+#pragma unroll
+  for (int k = 0; k < kTailO; ++k) e[k] = k < Ob ? expf(acc[k] - m) : 0.0f;
+#pragma unroll
+  for (int w = kTailO / 2; w > 0; w >>= 1)
+#pragma unroll
+    for (int k = 0; k < w; ++k) e[k] = e[k] + e[k + w];
+  const float sm = e[0];
+  const int64_t lab = labels[r];
+  const float inv_b = 1.0f / (float)pa.B;
+  float yl = 0.0f, mine = 0.0f;
+#pragma unroll
+  for (int k = 0; k < kTailO; ++k) {
+    if (k == lab) yl = acc[k];
+    if (k == lane) mine = acc[k];
+  }
+  if (lane < Ob) {
+    yb[r * Ob + lane] = mine;
+    dyb[r * Ob + lane] = (expf(mine - m) / sm - (lane == lab ? 1.0f : 0.0f)) * inv_b;
+  }
+  if (lane == 0) loss_part[r] = (logf(sm) + m) - ((lab >= 0 && lab < Ob) ? yl : 0.0f);
+}
+
 // ---------------------------------------------------------------------------
 // Forward, very small batch (B <= 16), one launch: column-owning blocks.
 // Block b owns one 8-output stream of the bf16 coefficients (cf_bf16_elem)
@@ -2327,7 +2406,7 @@ FwdChoice choose_fwd(const Plan& p) {
 template <int P, bool BF>
 static void fwd_dispatch(const float* x, float* t, const void* packed, float* y, void* ws,
                          const Plan& p, const FwdChoice& c, hipStream_t s, int nib,
-                         bool out_tanh) {
+                         bool out_tanh, bool reduce) {
   typedef typename Elem<BF>::type E;
   const E* Cf = reinterpret_cast<const E*>(packed);
   char* pk = const_cast<char*>(reinterpret_cast<const char*>(packed));
@@ -2406,7 +2485,7 @@ static void fwd_dispatch(const float* x, float* t, const void* packed, float* y,
         break;
     }
   }
-  if (split) {
+  if (split && reduce) {
     const int64_t n = p.B * (int64_t)p.O;
     int64_t gsz = ((n > p.O32 ? n : p.O32) + 255) / 256;
     if (gsz > 65536) gsz = 65536;
@@ -2447,10 +2526,10 @@ bool fwd_sums_bias(const Plan& p, const FwdChoice& c) {
 
 void launch_fwd_gemm(const float* x, float* t, const void* packed, float* y, void* ws,
                      const Plan& p, const FwdChoice& c, hipStream_t s, bool sum_bias,
-                     bool out_tanh) {
+                     bool out_tanh, bool reduce) {
   const bool bf = p.esz == 2;
   const int nib = sum_bias && fwd_sums_bias(p, c) ? p.NIB : 0;
-#define CKAN_FW(PP, BB) fwd_dispatch<PP, BB>(x, t, packed, y, ws, p, c, s, nib, out_tanh)
+#define CKAN_FW(PP, BB) fwd_dispatch<PP, BB>(x, t, packed, y, ws, p, c, s, nib, out_tanh, reduce)
   switch (p.P) {
     case 2: bf ? CKAN_FW(2, true) : CKAN_FW(2, false); break;
     case 4: bf ? CKAN_FW(4, true) : CKAN_FW(4, false); break;
@@ -2661,6 +2740,25 @@ void launch_dc_gemm(const void* dYc, const float* t, const float* colsum, float*
     default: bf ? CKAN_DC(16, true) : CKAN_DC(16, false); break;
   }
 #undef CKAN_DC
+}
+
+bool fwd_tail_ce_ok(const Plan& pa, const FwdChoice& ca, int Ob, int Db) {
+  return (ca.splits > 1 && !fwd_streaming(ca) && ca.tile != kFwdCols) && pa.O <= 64 && Ob >= 1 &&
+         Ob <= kTailO && Db >= 1 && Db <= 17 && pa.B <= 4096;
+}
+
+void launch_fwd_tail_ce(const void* packed_a, void* ws, const Plan& pa, const FwdChoice& ca,
+                        bool sum_bias, float* tb, const float* Cb, int Ob, int Db, float* yb,
+                        const int64_t* labels, float* dyb, float* loss_part, hipStream_t s) {
+  char* pk = const_cast<char*>(reinterpret_cast<const char*>(packed_a));
+  const float* bias = reinterpret_cast<const float*>(pk + packed_biasf_offset(pa));
+  const float* bpart = reinterpret_cast<const float*>(pk + packed_bias_offset(pa));
+  const int nib = sum_bias && fwd_sums_bias(pa, ca) ? pa.NIB : 0;
+  float* bias_out = nib > 0 ? reinterpret_cast<float*>(pk + packed_biasf_offset(pa)) : nullptr;
+  const unsigned grid = (unsigned)ceil_div(pa.B, kTailRows);
+  hipLaunchKernelGGL(k_fwd_tail_ce, dim3(grid), dim3(64 * kTailRows), 0, s,
+                     reinterpret_cast<const float*>(ws), ca.splits, bias, pa, bpart, nib, bias_out,
+                     tb, Cb, Ob, Db, yb, labels, dyb, loss_part);
 }
 
 }  // namespace ckan

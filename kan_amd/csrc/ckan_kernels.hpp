@@ -172,7 +172,17 @@ void launch_dc_sum(const float* part, int S, float* dC, DcOut om, const Plan& p,
 // stack; needs fwd_out_tanh_ok).
 void launch_fwd_gemm(const float* x, float* t, const void* packed, float* y, void* ws,
                      const Plan& p, const FwdChoice& c, hipStream_t s, bool sum_bias = false,
-                     bool out_tanh = false);
+                     bool out_tanh = false, bool reduce = true);
+// reduce = false above leaves a split forward's partials in ws for
+// launch_fwd_tail_ce, which sums them (the last two layers of a stack
+// trained with cross-entropy, when fwd_tail_ce_ok holds): layer a's split
+// sum into b's tanh cache tb, layer b's forward from its fp32 coefficients
+// Cb [Ib = a.O, Ob, Db] into yb, and the rows' cross-entropy gradient dyb and
+// losses loss_part (their mean: k_sum_scalar).
+bool fwd_tail_ce_ok(const Plan& pa, const FwdChoice& ca, int Ob, int Db);
+void launch_fwd_tail_ce(const void* packed_a, void* ws, const Plan& pa, const FwdChoice& ca,
+                        bool sum_bias, float* tb, const float* Cb, int Ob, int Db, float* yb,
+                        const int64_t* labels, float* dyb, float* loss_part, hipStream_t s);
 bool fwd_sums_bias(const Plan& p, const FwdChoice& c);
 // The forward path of p can store tanh(y) in place of y (the pipelined
 // kernel, unsplit).
@@ -227,6 +237,18 @@ int pack2_forward_ex(const struct ckan_desc* da, const void* Ca, void* pka, cons
                      float* ta, bool ta_ready, const struct ckan_desc* db, const void* Cb,
                      void* pkb, float* tb, float* outb, bool outb_tanh, void* ws, size_t ws_bytes,
                      void* stream);
+// pack2_forward_ex for the last two layers of a stack trained with
+// cross-entropy (labels: int64 class per row): a's forward leaves its split
+// partials, and one launch sums them into tb, runs b's forward into yb on the
+// vector ALU and writes the rows' CE gradient dyb and losses loss_part (their
+// mean is the caller's k_sum_scalar).  pack2_tail_ce_fits: the pair allows it
+// (pack_pair_fits, fp32 compute, a split forward for a, a.O <= 64, b.O <= 16,
+// b.degree <= 16, B <= 4096).
+bool pack2_tail_ce_fits(const struct ckan_desc* a, const struct ckan_desc* b);
+int pack2_forward_tail_ce(const struct ckan_desc* da, const void* Ca, void* pka, const float* xa,
+                          float* ta, bool ta_ready, const struct ckan_desc* db, const void* Cb,
+                          void* pkb, float* tb, float* yb, const int64_t* labels, float* dyb,
+                          float* loss_part, void* ws, size_t ws_bytes, void* stream);
 // the Plan-level launch behind pack2_forward_ex (xa, ta: a's fused tanh, or null)
 bool pack_pair_ok(const Plan& a, const Plan& b);
 void launch_pack_pair(const float* Ca, void* pa, const Plan& qa, bool reduce_a, const float* xa,

@@ -74,6 +74,42 @@ def test_ce_multi_block_loss_matches_oracle(widths, degrees, B):
     ex.close()
 
 
+@pytest.mark.parametrize("widths,degrees,B", [
+    ([200, 48, 7], [4, 3], 123),   # rows not a multiple of the tail's 4 per block, 7 classes
+    ([130, 64, 16], [2, 2], 77),   # 64 inputs (one per lane) and 16 classes, degree 2
+    ([300, 64, 5], [8, 8], 200),   # degree 8: 9 coefficients per (input, class)
+])
+def test_fused_ce_tail_matches_oracle(widths, degrees, B):
+    """The last two layers of a cross-entropy stack end in one launch: the
+    first layer's split sum, the second layer's forward on the vector ALU from
+    its fp32 coefficients, and each row's softmax gradient and loss (mean by a
+    sum launch).  Losses and trained coefficients against the oracle; the
+    library's launch record shows the tail ran."""
+    from kan_amd import ResidentExecutor, _lib
+    print(f"executor fused ce tail {widths} {degrees} B={B}", flush=True)
+    g = torch.Generator().manual_seed(11)
+    x = torch.rand(B, widths[0], generator=g) * 4 - 2
+    labels = torch.randint(0, widths[-1], (B,), generator=g)
+    coeffs = _make(widths, degrees, 31)
+    ex = ResidentExecutor(widths, degrees, B, compute="fp32", loss="ce", optimizer="sgd", lr=0.05)
+    for l, c in enumerate(coeffs):
+        ex.set_coeffs(l, c)
+    xd, ld = x.cuda(), labels.cuda()
+    _lib.profile_enable(True)
+    try:
+        losses = [ex.step(xd, ld).item() for _ in range(3)]
+        rep = _lib.profile_report()
+    finally:
+        _lib.profile_enable(False)
+    assert rep.get("fwd_tail", (0,))[0] == 3, rep
+    c_ref, losses_ref = orc.train_steps(x, labels, coeffs, steps=3, loss="ce", optimizer="sgd", lr=0.05)
+    for a, b in zip(losses, losses_ref):
+        assert abs(a - b) <= 1e-5 * abs(b) + 1e-6
+    for l in range(len(degrees)):
+        assert _rel(ex.get_coeffs(l), c_ref[l]) <= 1e-5
+    ex.close()
+
+
 def test_mse_stack_deg16_sgd_matches_oracle():
     from kan_amd import ResidentExecutor
     print("executor mse deg16 stack", flush=True)
