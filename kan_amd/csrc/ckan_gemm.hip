@@ -756,31 +756,60 @@ k_fwd_reduce(const float* __restrict__ part, int S, const float* __restrict__ bi
 // added by an xor butterfly, which leaves the same bits in every lane), then
 // the row's softmax cross-entropy as k_ce_small computes it: yb, dyb =
 // (softmax - onehot) / B and the row's loss into loss_part[r], whose mean
-// k_sum_scalar takes in k_ce_small's order.  Ib <= 64, Ob <= kTailO.
-constexpr int kTailO = 16, kTailRows = 4;
+// k_sum_scalar takes in k_ce_small's order.  Ib <= 64, Ob <= kTailO; the
+// block stages Cb in LDS (Ib Ob Db <= kTailC floats), its coalesced loads
+// issued ahead of the split sums so that both latencies overlap.
+constexpr int kTailO = 16, kTailRows = 4, kTailC = 8192, kTailCL = 16;
+
 __global__ void __launch_bounds__(256)
 k_fwd_tail_ce(const float* __restrict__ part, int S, const float* __restrict__ bias_f, Plan pa,
               const float* __restrict__ bias_part, int nib, float* __restrict__ bias_out,
               float* __restrict__ tb, const float* __restrict__ Cb, int Ob, int Db,
               float* __restrict__ yb, const int64_t* __restrict__ labels, float* __restrict__ dyb,
               float* __restrict__ loss_part) {
-  const int lane = threadIdx.x & 63;
-  const int64_t r = (int64_t)blockIdx.x * kTailRows + (threadIdx.x >> 6);
+  extern __shared__ float csh[];  // Cb [Ib][Ob][Db]
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int64_t r = (int64_t)blockIdx.x * kTailRows + (tid >> 6);
+  const bool active = r < pa.B;
+  const int Ib = pa.O, nC = Ib * Ob * Db;
+  float cv[kTailCL];
+#pragma unroll
+  for (int u = 0; u < kTailCL; ++u) {
+    const int q = tid + u * 256;
+    cv[u] = q < nC ? Cb[q] : 0.0f;
+  }
   if (nib > 0 && blockIdx.x == 0)
-    for (int q = threadIdx.x; q < pa.O32; q += blockDim.x) bias_out[q] = bias_from_parts(bias_part, nib, pa.O32, q);
-  if (r >= pa.B) return;
-  const int Ib = pa.O;
+    for (int q = tid; q < pa.O32; q += blockDim.x) bias_out[q] = bias_from_parts(bias_part, nib, pa.O32, q);
   float t = 0.0f;
-  if (lane < Ib) {
+  if (active && lane < Ib) {
     const float bias = nib > 0 ? bias_from_parts(bias_part, nib, pa.O32, lane) : bias_f[lane];
     t = tanhf(split_sum(part + (size_t)r * pa.O32 + lane, (size_t)pa.B32 * pa.O32, (unsigned)S, bias));
     tb[r * Ib + lane] = t;
   }
+#pragma unroll
+  for (int u = 0; u < kTailCL; ++u) {
+    const int q = tid + u * 256;
+    if (q < nC) csh[q] = cv[u];
+  }
+  for (int q0 = kTailCL * 256; q0 < nC; q0 += kTailCL * 256) {
+#pragma unroll
+    for (int u = 0; u < kTailCL; ++u) {
+      const int q = q0 + tid + u * 256;
+      cv[u] = q < nC ? Cb[q] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < kTailCL; ++u) {
+      const int q = q0 + tid + u * 256;
+      if (q < nC) csh[q] = cv[u];
+    }
+  }
+  __syncthreads();
+  if (!active) return;
   float acc[kTailO];
 #pragma unroll
   for (int k = 0; k < kTailO; ++k) acc[k] = 0.0f;
   if (lane < Ib) {
-    const float* c = Cb + (size_t)lane * Ob * Db;
+    const float* c = csh + lane * Ob * Db;
     const float t2 = t + t;
     float tm = 1.0f, tc = t;  // T_{d-1}, T_d from d = 0
     for (int d = 0; d < Db; ++d) {
@@ -2744,7 +2773,7 @@ void launch_dc_gemm(const void* dYc, const float* t, const float* colsum, float*
 
 bool fwd_tail_ce_ok(const Plan& pa, const FwdChoice& ca, int Ob, int Db) {
   return (ca.splits > 1 && !fwd_streaming(ca) && ca.tile != kFwdCols) && pa.O <= 64 && Ob >= 1 &&
-         Ob <= kTailO && Db >= 1 && Db <= 17 && pa.B <= 4096;
+         Ob <= kTailO && Db >= 1 && Db <= 17 && pa.O * Ob * Db <= kTailC && pa.B <= 4096;
 }
 
 void launch_fwd_tail_ce(const void* packed_a, void* ws, const Plan& pa, const FwdChoice& ca,
@@ -2756,7 +2785,8 @@ void launch_fwd_tail_ce(const void* packed_a, void* ws, const Plan& pa, const Fw
   const int nib = sum_bias && fwd_sums_bias(pa, ca) ? pa.NIB : 0;
   float* bias_out = nib > 0 ? reinterpret_cast<float*>(pk + packed_biasf_offset(pa)) : nullptr;
   const unsigned grid = (unsigned)ceil_div(pa.B, kTailRows);
-  hipLaunchKernelGGL(k_fwd_tail_ce, dim3(grid), dim3(64 * kTailRows), 0, s,
+  const size_t lds = (size_t)pa.O * Ob * Db * sizeof(float);
+  hipLaunchKernelGGL(k_fwd_tail_ce, dim3(grid), dim3(64 * kTailRows), lds, s,
                      reinterpret_cast<const float*>(ws), ca.splits, bias, pa, bpart, nib, bias_out,
                      tb, Cb, Ob, Db, yb, labels, dyb, loss_part);
 }

@@ -243,7 +243,7 @@ int pack2_forward_ex(const struct ckan_desc* da, const void* Ca, void* pka, cons
 // vector ALU and writes the rows' CE gradient dyb and losses loss_part (their
 // mean is the caller's k_sum_scalar).  pack2_tail_ce_fits: the pair allows it
 // (pack_pair_fits, fp32 compute, a split forward for a, a.O <= 64, b.O <= 16,
-// b.degree <= 16, B <= 4096).
+// b.degree <= 16, a.O * b.O * (b.degree + 1) <= 8192, B <= 4096).
 bool pack2_tail_ce_fits(const struct ckan_desc* a, const struct ckan_desc* b);
 int pack2_forward_tail_ce(const struct ckan_desc* da, const void* Ca, void* pka, const float* xa,
                           float* ta, bool ta_ready, const struct ckan_desc* db, const void* Cb,
