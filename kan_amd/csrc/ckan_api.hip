@@ -181,9 +181,27 @@ int scratch_ptr(void** out) {
 
 void ckan::set_last_error(const char* msg) { g_err = msg; }
 
+namespace {
+int backward_core(const ckan_desc* desc, const float* t_cache, const void* packed, const float* dy,
+                  float* dx, float* dcoeffs, DcOut om, void* ws, size_t ws_bytes, void* stream,
+                  const LossMean* lm, bool* lm_used);
+}
+
 int ckan::backward_impl(const ckan_desc* desc, const float* t_cache, const void* packed,
                         const float* dy, float* dx, float* dcoeffs, DcOut om, void* ws,
-                        size_t ws_bytes, void* stream) {
+                        size_t ws_bytes, void* stream, const LossMean* lm) {
+  bool used = false;
+  const int rc = backward_core(desc, t_cache, packed, dy, dx, dcoeffs, om, ws, ws_bytes, stream,
+                               lm && lm->part ? lm : nullptr, &used);
+  if (rc || !lm || !lm->part || used) return rc;
+  launch_loss_mean(*lm, reinterpret_cast<hipStream_t>(stream));
+  return check_launch("loss mean");
+}
+
+namespace {
+int backward_core(const ckan_desc* desc, const float* t_cache, const void* packed, const float* dy,
+                  float* dx, float* dcoeffs, DcOut om, void* ws, size_t ws_bytes, void* stream,
+                  const LossMean* lm, bool* lm_used) {
   int rc = validate_desc(desc);
   if (rc) return rc;
   const bool need_dx = dx != nullptr, need_dc = dcoeffs != nullptr;
@@ -242,7 +260,8 @@ int ckan::backward_impl(const ckan_desc* desc, const float* t_cache, const void*
   if ((rc = check_launch("prep_dy"))) return rc;
   if (need_dx && L.dx_small && need_dc && L.dc_small && bwd_small_one_launch(p)) {
     ProfScope ps("bwd_small", s);
-    launch_bwd_small(dy, packed, t_cache, dx, dcoeffs, om, p, s);
+    launch_bwd_small(dy, packed, t_cache, dx, dcoeffs, om, p, s, lm ? *lm : LossMean{});
+    *lm_used = lm != nullptr;
     return check_launch("bwd_small");
   }
   if (need_dx) {
@@ -279,6 +298,8 @@ int ckan::backward_impl(const ckan_desc* desc, const float* t_cache, const void*
   }
   return CKAN_OK;
 }
+
+}  // namespace
 
 extern "C" {
 

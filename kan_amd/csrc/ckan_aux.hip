@@ -943,33 +943,42 @@ void launch_dx_small(const float* dy, const void* packed, const float* t, float*
 
 // Both small backward kernels of one layer in one launch (they read the same
 // dy and tanh cache and write different outputs: dx, and dC or the layer's
-// coefficients): blocks [0, ndx) take dx, the rest dC.
+// coefficients): blocks [0, ndx) take dx, the next ndc dC, and with lm.part
+// one more block takes the step's loss mean.
 template <int P, bool BF>
 __global__ void __launch_bounds__(256)
 k_bwd_small(const float* __restrict__ dy, const typename Elem<BF>::type* __restrict__ Cb,
             const float* __restrict__ t, float* __restrict__ dx, float* __restrict__ dC, DcOut om,
-            Plan p, int nx_dx, int ndx, int nx_dc) {
+            Plan p, int nx_dx, int ndx, int nx_dc, int ndc, LossMean lm) {
   const int bid = blockIdx.x;
   if (bid < ndx) dx_small_body<P, BF>(dy, Cb, t, dx, p, bid % nx_dx, bid / nx_dx);
-  else dc_small_body<P + 1>(dy, t, dC, om, p, (bid - ndx) % nx_dc, (bid - ndx) / nx_dc);
+  else if (bid < ndx + ndc) dc_small_body<P + 1>(dy, t, dC, om, p, (bid - ndx) % nx_dc, (bid - ndx) / nx_dc);
+  else loss_mean_block(lm);
 }
 
 // One round of the fused launch (its LDS, both kernels' arrays, fits 3 blocks
 // per CU): larger layers keep the two launches, each at its own occupancy.
+// The loss mean alone, where the backward takes no small one-launch path.
+__global__ void __launch_bounds__(256) k_loss_mean(LossMean lm) { loss_mean_block(lm); }
+
+void launch_loss_mean(const LossMean& lm, hipStream_t s) {
+  hipLaunchKernelGGL(k_loss_mean, dim3(1), dim3(256), 0, s, lm);
+}
+
 bool bwd_small_one_launch(const Plan& p) {
   const int64_t ndx = ceil_div(p.B, 32) * ceil_div(p.I, 8), ndc = ceil_div(p.I, 8) * ceil_div(p.O, 8);
   return ndx + ndc <= 3 * 256;
 }
 
 void launch_bwd_small(const float* dy, const void* packed, const float* t, float* dx, float* dC,
-                      DcOut om, const Plan& p, hipStream_t s) {
+                      DcOut om, const Plan& p, hipStream_t s, LossMean lm) {
   const int nx_dx = (int)ceil_div(p.B, 32), nx_dc = (int)ceil_div(p.I, 8);
   const int ndx = nx_dx * (int)ceil_div(p.I, 8), ndc = nx_dc * (int)ceil_div(p.O, 8);
-  const dim3 grid((unsigned)(ndx + ndc));
+  const dim3 grid((unsigned)(ndx + ndc + (lm.part ? 1 : 0)));
 #define CKAN_BWS(PP, BB)                                                                        \
   hipLaunchKernelGGL((k_bwd_small<PP, BB>), grid, dim3(256), 0, s, dy,                          \
                      reinterpret_cast<const typename Elem<BB>::type*>(packed) + packed_cf_elems(p), \
-                     t, dx, dC, om, p, nx_dx, ndx, nx_dc)
+                     t, dx, dC, om, p, nx_dx, ndx, nx_dc, ndc, lm)
   const bool bf = p.esz == 2;
   switch (p.P) {
     case 2: if (bf) CKAN_BWS(2, true); else CKAN_BWS(2, false); break;

@@ -104,6 +104,35 @@ struct DcOut {
   const float* sc;
 };
 
+// A loss mean for a kernel that also takes it (the last launch of an executor
+// step's loss, folded into the next launch): out = scale * sum_k part[k],
+// k < n; also into out2 when given.  part == nullptr: none.
+struct LossMean {
+  const float* part;
+  int64_t n;
+  float scale;
+  float* out;
+  float* out2;
+};
+
+// The sum of LossMean by one 256-thread block in a fixed order: strided
+// per-thread sums, then a tree (k_sum_scalar's order, so the same bits).
+__device__ __forceinline__ void loss_mean_block(const LossMean& lm) {
+  __shared__ float red[256];
+  float s = 0.0f;
+  for (int64_t k = threadIdx.x; k < lm.n; k += 256) s += lm.part[k];
+  red[threadIdx.x] = s;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if (threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    *lm.out = red[0] * lm.scale;
+    if (lm.out2) *lm.out2 = red[0] * lm.scale;
+  }
+}
+
 // The SGD update of one parameter: the arithmetic of every SGD path here.
 __device__ __forceinline__ float sgd_update(float p, float g, float lr, float wd) {
   float gv = g;

@@ -160,19 +160,7 @@ k_ce_small(const float* __restrict__ y, const int64_t* __restrict__ labels, floa
 __global__ void __launch_bounds__(256)
 k_sum_scalar(const float* __restrict__ part, int64_t n, float scale, float* __restrict__ out,
              float* __restrict__ out2) {
-  __shared__ float red[256];
-  float s = 0.0f;
-  for (int64_t k = threadIdx.x; k < n; k += 256) s += part[k];
-  red[threadIdx.x] = s;
-  __syncthreads();
-  for (int w = 128; w > 0; w >>= 1) {
-    if (threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
-    __syncthreads();
-  }
-  if (threadIdx.x == 0) {
-    *out = red[0] * scale;
-    if (out2) *out2 = red[0] * scale;
-  }
+  loss_mean_block(LossMean{part, n, scale, out, out2});
 }
 
 // Adam scalars for the next step from the device step counter (one thread):
@@ -655,10 +643,12 @@ int run_step(ckan_exec* ex, const float* x, const void* target, hipStream_t s,
   auto& last = ex->layers[L - 1];
   const int64_t B = ex->cfg.batch;
   const int O = last.desc.out_dim;
+  // with the fused tail the rows' losses are in loss_part; the last layer's
+  // backward takes their mean along
   const bool tail = L >= 2 && ex->layers[L - 2].tail_ce;
-  if (tail) {  // the rows' losses came from the tail launch: their mean
-    hipLaunchKernelGGL(k_sum_scalar, dim3(1), dim3(256), 0, s, ex->loss_part, B,
-                       (float)(1.0 / (double)B), ex->loss, loss_copy);
+  const LossMean lm_tail{ex->loss_part, B, (float)(1.0 / (double)B), ex->loss, loss_copy};
+  if (tail) {
+    // no loss launch: the tail wrote dy and the rows' losses
   } else if (ex->cfg.loss == CKAN_LOSS_MSE) {
     const int64_t n = B * O;
     const int vec = n % 4 == 0 && (reinterpret_cast<uintptr_t>(target) & 15) == 0 &&
@@ -700,7 +690,7 @@ int run_step(ckan_exec* ex, const float* x, const void* target, hipStream_t s,
                  (float)(1.0 - (double)c.beta2), c.eps, ly.C, ly.m, ly.v, ex->adam_sc};
     }
     if ((rc = backward_impl(&ly.desc, ly.t, ly.packed, ly.dy, dx, ly.C, om, ex->bws,
-                            ex->bws_bytes, s)))
+                            ex->bws_bytes, s, tail && l == L - 1 ? &lm_tail : nullptr)))
       return rc;
   }
   return CKAN_OK;

@@ -207,16 +207,20 @@ void launch_dc_small(const float* dy, const float* t, float* dC, DcOut om, const
 // where that is one round of blocks (bwd_small_one_launch)
 bool bwd_small_one_launch(const Plan& p);
 void launch_bwd_small(const float* dy, const void* packed, const float* t, float* dx, float* dC,
-                      DcOut om, const Plan& p, hipStream_t s);
+                      DcOut om, const Plan& p, hipStream_t s,
+                      LossMean lm = LossMean{});
+void launch_loss_mean(const LossMean& lm, hipStream_t s);
 void launch_dc_gemm(const void* dYc, const float* t, const float* colsum, float* part, float* dC,
                     DcOut om, const Plan& p, const BwdLayout& L, hipStream_t s);
 void launch_sgd(float* p, const float* g, int64_t n, float lr, float wd, hipStream_t s);
 // ckan_backward with the dC write mode given by om; with om.mode kDcSgd or
 // kDcAdam, dcoeffs is the parameter and receives its optimizer step (batch
-// >= 1 only).
+// >= 1 only).  lm (optional): a loss mean taken along, by one more block of
+// the small one-launch backward where that path runs, else by one launch
+// after the backward.
 int backward_impl(const struct ckan_desc* desc, const float* t_cache, const void* packed,
                   const float* dy, float* dx, float* dcoeffs, DcOut om, void* ws,
-                  size_t ws_bytes, void* stream);
+                  size_t ws_bytes, void* stream, const LossMean* lm = nullptr);
 // ckan_pack_forward (no basis spec) for a layer inside a stack: t_ready, the
 // tanh cache already holds the layer's input map (x unused; the layer's
 // forward must read the cache); out_tanh, store tanh(y) into `out` (the next
