@@ -335,7 +335,12 @@ int ckan_exec_set_adam_state(ckan_exec* ex, int32_t layer, const float* m, const
                              int64_t step, void* stream);
 /* One training step on x [batch, widths[0]] (fp32, device) and target:
  * fp32 [batch, widths[n]] for MSE or int64 [batch] class indices for CE.
- * Writes the step's loss (fp32 scalar, device) to loss_out when non-NULL. */
+ * Writes the step's loss (fp32 scalar, device) to loss_out when non-NULL.
+ * CE labels must lie in [0, widths[n]): there is no ignore_index, every row
+ * counts in the mean, and the kernels do not check the labels (an
+ * out-of-range label reads nothing out of bounds but leaves the loss and its
+ * gradient without that row's target term).  The Python wrapper rejects such
+ * labels before the launch, as torch.nn.CrossEntropyLoss would. */
 int ckan_exec_step(ckan_exec* ex, const float* x, const void* target, float* loss_out,
                    void* stream);
 /* `nsteps` training steps on the same x and target (the reference loop's

@@ -920,7 +920,9 @@ k_dx_small(const float* __restrict__ dy, const typename Elem<BF>::type* __restri
 }
 
 bool dx_small_ok(const Plan& p) {
-  return p.O <= kDxSmallO && (int64_t)p.B * p.I * p.O * p.P <= ((int64_t)1 << 27);
+  // grid y = input blocks of 8 (launch_dx_small): at most 65535
+  return p.O <= kDxSmallO && ceil_div(p.I, 8) <= 65535 &&
+         (int64_t)p.B * p.I * p.O * p.P <= ((int64_t)1 << 27);
 }
 
 void launch_dx_small(const float* dy, const void* packed, const float* t, float* dx,
@@ -956,8 +958,11 @@ k_bwd_small(const float* __restrict__ dy, const typename Elem<BF>::type* __restr
   else loss_mean_block(lm);
 }
 
-// One round of the fused launch (its LDS, both kernels' arrays, fits 3 blocks
-// per CU): larger layers keep the two launches, each at its own occupancy.
+// One round of the fused launch: larger layers keep the two launches, each at
+// its own occupancy.  A k_bwd_small block holds the static LDS of all three
+// bodies at once (about 55 KB at P = 8, 80 KB at P = 16), so the blocks one CU
+// holds are read from the runtime's occupancy calculation for the
+// instantiation, not assumed.
 // The loss mean alone, where the backward takes no small one-launch path.
 __global__ void __launch_bounds__(256) k_loss_mean(LossMean lm) { loss_mean_block(lm); }
 
@@ -965,9 +970,29 @@ void launch_loss_mean(const LossMean& lm, hipStream_t s) {
   hipLaunchKernelGGL(k_loss_mean, dim3(1), dim3(256), 0, s, lm);
 }
 
+template <int P, bool BF>
+static int bwd_small_blocks_per_cu() {
+  static const int n = [] {
+    int v = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, k_bwd_small<P, BF>, 256, 0) != hipSuccess ||
+        v < 1)
+      v = 1;
+    return v;
+  }();
+  return n;
+}
+
 bool bwd_small_one_launch(const Plan& p) {
   const int64_t ndx = ceil_div(p.B, 32) * ceil_div(p.I, 8), ndc = ceil_div(p.I, 8) * ceil_div(p.O, 8);
-  return ndx + ndc <= 3 * 256;
+  const bool bf = p.esz == 2;
+  int per_cu;
+  switch (p.P) {
+    case 2: per_cu = bf ? bwd_small_blocks_per_cu<2, true>() : bwd_small_blocks_per_cu<2, false>(); break;
+    case 4: per_cu = bf ? bwd_small_blocks_per_cu<4, true>() : bwd_small_blocks_per_cu<4, false>(); break;
+    case 8: per_cu = bf ? bwd_small_blocks_per_cu<8, true>() : bwd_small_blocks_per_cu<8, false>(); break;
+    default: per_cu = bf ? bwd_small_blocks_per_cu<16, true>() : bwd_small_blocks_per_cu<16, false>(); break;
+  }
+  return ndx + ndc <= (int64_t)per_cu * kNumCUs;
 }
 
 void launch_bwd_small(const float* dy, const void* packed, const float* t, float* dx, float* dC,
@@ -994,7 +1019,9 @@ bool dc_small_ok(const Plan& p) {
   // vector ALU finishes in a few microseconds, ahead of the pipelined kernel's
   // prologue (and its split sum)
   const int64_t pairs = (int64_t)p.I * p.O;
-  return p.B >= 1 && p.B <= kDcSmallRows && pairs * p.B * (2 * p.D + 2) <= ((int64_t)1 << 28);
+  // grid y = output blocks of 8 (launch_dc_small): at most 65535
+  return p.B >= 1 && p.B <= kDcSmallRows && ceil_div(p.O, 8) <= 65535 &&
+         pairs * p.B * (2 * p.D + 2) <= ((int64_t)1 << 28);
 }
 
 void launch_dc_small(const float* dy, const float* t, float* dC, DcOut om, const Plan& p,

@@ -33,6 +33,7 @@ typedef __attribute__((ext_vector_type(4))) float f32x4_t;
 typedef __attribute__((ext_vector_type(4))) unsigned u32x4_t;
 
 constexpr int kFragElems = 512;  // 64 lanes x 8 values
+constexpr int kNumCUs = 256;      // MI355X: 8 XCDs x 32 compute units
 
 __host__ __device__ constexpr int padded_degree(int deg) {
   return deg <= 2 ? 2 : deg <= 4 ? 4 : deg <= 8 ? 8 : deg <= 16 ? 16 : -1;

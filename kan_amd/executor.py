@@ -9,6 +9,7 @@ layer -- one iteration of the reference training loop (README.md:61-69).
 from __future__ import annotations
 
 import ctypes
+import weakref
 from typing import List, Optional, Sequence
 
 import torch
@@ -19,6 +20,50 @@ from .layers import ChebyKANLayer, KANSequential
 
 _LOSS = {"mse": _lib.CKAN_LOSS_MSE, "ce": _lib.CKAN_LOSS_CE, "cross_entropy": _lib.CKAN_LOSS_CE}
 _OPT = {"sgd": _lib.CKAN_OPT_SGD, "adam": _lib.CKAN_OPT_ADAM}
+
+
+def check_sequential(model: KANSequential) -> List[ChebyKANLayer]:
+    """The ChebyKAN layers of ``model`` in order; ValueError when a module is
+    not a ChebyKANLayer (an activation, a Jacobi or Hermite layer) or when the
+    widths do not chain (layer l's input_dim != layer l-1's output_dim)."""
+    layers = list(model)
+    if not layers:
+        raise ValueError("the model has no layers")
+    for l, m in enumerate(layers):
+        if type(m) is not ChebyKANLayer:
+            raise ValueError(f"module {l} ({type(m).__name__}) is not a ChebyKANLayer: the "
+                             "resident executor runs stacks of ChebyKAN layers only")
+        if l and m.input_dim != layers[l - 1].output_dim:
+            raise ValueError(f"layer {l} takes {m.input_dim} inputs but layer {l - 1} "
+                             f"produces {layers[l - 1].output_dim}")
+    return layers
+
+
+def check_rows(t: torch.Tensor, rows: int, cols: int, name: str) -> None:
+    """The executor reads exactly rows x cols elements of ``t``."""
+    if tuple(t.shape) != (rows, cols):
+        raise RuntimeError(f"{name} must be [{rows}, {cols}], got {list(t.shape)}")
+
+
+def check_labels(labels: torch.Tensor, n_classes: int) -> None:
+    """Class indices for the cross-entropy loss.
+
+    torch.nn.CrossEntropyLoss raises on a label outside [0, C) and leaves rows
+    labelled with its ignore_index (-100 by default) out of the loss and its
+    mean.  The executor's loss kernels average over every row, so both cases
+    are rejected here, before any launch, instead of training on a wrong
+    loss.  Reads the labels' range (one device synchronisation when they live
+    on the GPU)."""
+    if labels.dtype.is_floating_point or labels.dtype == torch.bool:
+        raise ValueError(f"labels must be an integer tensor, got {labels.dtype}")
+    if labels.numel() == 0:
+        return
+    lo, hi = int(labels.min()), int(labels.max())
+    if lo == -100:
+        raise ValueError("labels hold -100 (CrossEntropyLoss's ignore_index): the executor's "
+                         "cross-entropy has no ignored rows; drop those rows from the batch")
+    if lo < 0 or hi >= n_classes:
+        raise ValueError(f"labels must lie in [0, {n_classes}), found values in [{lo}, {hi}]")
 
 
 class ResidentExecutor:
@@ -57,6 +102,7 @@ class ResidentExecutor:
                                                   self._stream()))
         self._h = handle
         self._loss = torch.empty((), dtype=torch.float32, device=self.device)
+        self._labels_checked = None  # (weakref to the last labels checked, their _version)
 
     def _stream(self) -> int:
         return _lib.stream_ptr(self.device)
@@ -66,7 +112,14 @@ class ResidentExecutor:
 
     @classmethod
     def from_sequential(cls, model: KANSequential, batch: int, **kw) -> "ResidentExecutor":
-        layers: List[ChebyKANLayer] = [m for m in model if isinstance(m, ChebyKANLayer)]
+        """An executor over ``model``'s layers with their current coefficients.
+
+        The executor's kernels run ChebyKAN layers back to back, each layer's
+        output feeding the next (kan/layers/base.py:144-166), so every module
+        of ``model`` must be a ChebyKANLayer and each layer's input_dim must
+        equal the previous layer's output_dim; anything else raises ValueError
+        before any device work."""
+        layers = check_sequential(model)
         widths = [layers[0].input_dim] + [m.output_dim for m in layers]
         ex = cls(widths, [m.degree for m in layers], batch, **kw)
         for l, m in enumerate(layers):
@@ -87,35 +140,33 @@ class ResidentExecutor:
 
     def step(self, x: torch.Tensor, target: torch.Tensor) -> torch.Tensor:
         """One training step; returns the step's loss as a new device scalar."""
-        x = x.to(self.device, torch.float32).contiguous()
-        if tuple(x.shape) != (self.batch, self.widths[0]):
-            raise RuntimeError(f"x must be [{self.batch}, {self.widths[0]}]")
-        if self.loss_name == "mse":
-            target = target.to(self.device, torch.float32).contiguous()
-            if tuple(target.shape) != (self.batch, self.widths[-1]):
-                raise RuntimeError(f"target must be [{self.batch}, {self.widths[-1]}]")
-        else:
-            target = target.to(self.device, torch.int64).contiguous()
-            if tuple(target.shape) != (self.batch,):
-                raise RuntimeError(f"labels must be [{self.batch}]")
+        x, target = self._inputs(x, target)
         _lib.check(self._lib.ckan_exec_step(self._h, x.data_ptr(), target.data_ptr(),
                                             self._loss.data_ptr(), self._stream()))
         # the library writes every step's loss into the same 4 bytes: hand the
         # caller its own copy, as a torch loss tensor would be
         return self._loss.clone()
 
+    def _x(self, x: torch.Tensor) -> torch.Tensor:
+        check_rows(x, self.batch, self.widths[0], "x")
+        return x.to(self.device, torch.float32).contiguous()
+
     def _inputs(self, x: torch.Tensor, target: torch.Tensor):
-        x = x.to(self.device, torch.float32).contiguous()
-        if tuple(x.shape) != (self.batch, self.widths[0]):
-            raise RuntimeError(f"x must be [{self.batch}, {self.widths[0]}]")
+        x = self._x(x)
         if self.loss_name == "mse":
+            check_rows(target, self.batch, self.widths[-1], "target")
             target = target.to(self.device, torch.float32).contiguous()
-            if tuple(target.shape) != (self.batch, self.widths[-1]):
-                raise RuntimeError(f"target must be [{self.batch}, {self.widths[-1]}]")
         else:
-            target = target.to(self.device, torch.int64).contiguous()
             if tuple(target.shape) != (self.batch,):
-                raise RuntimeError(f"labels must be [{self.batch}]")
+                raise RuntimeError(f"labels must be [{self.batch}], got {list(target.shape)}")
+            # checked once per labels tensor and version (full-batch loops pass
+            # the same tensor every step); the weak reference cannot outlive
+            # the tensor, so a new tensor at a reused address is checked again
+            seen = self._labels_checked
+            if seen is None or seen[0]() is not target or seen[1] != target._version:
+                check_labels(target, self.widths[-1])
+                self._labels_checked = (weakref.ref(target), target._version)
+            target = target.to(self.device, torch.int64).contiguous()
         return x, target
 
     def fit(self, x: torch.Tensor, target: torch.Tensor, steps: int) -> torch.Tensor:
@@ -129,7 +180,7 @@ class ResidentExecutor:
         return losses
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        x = x.to(self.device, torch.float32).contiguous()
+        x = self._x(x)
         y = torch.empty(self.batch, self.widths[-1], dtype=torch.float32, device=self.device)
         _lib.check(self._lib.ckan_exec_forward(self._h, x.data_ptr(), y.data_ptr(), self._stream()))
         return y

@@ -163,6 +163,21 @@ def test_small_backward_needs_no_dc_workspace():
     assert lib.ckan_bwd_workspace_bytes(ctypes.byref(big), 0, 1) > 0
 
 
+def test_small_backward_grid_limit_routes_to_gemm():
+    """The small vector-ALU dx puts 8 inputs per block on grid y, the small dC
+    8 outputs: past 65535 blocks (524280 inputs / outputs) a layer leaves
+    those kernels for the GEMM path, which re-lays dy out in a workspace."""
+    lib = _lib.load()
+
+    def ws(B, I, O, need_dx, need_dc):
+        return lib.ckan_bwd_workspace_bytes(ctypes.byref(_desc(B=B, I=I, O=O, deg=4)), need_dx, need_dc)
+
+    assert ws(1, 524280, 2, 1, 0) == 0
+    assert ws(1, 524288, 2, 1, 0) > 0
+    assert ws(1, 1, 524280, 0, 1) == 0
+    assert ws(1, 1, 524288, 0, 1) > 0
+
+
 def test_empty_calls_are_noops():
     lib = _lib.load()
     d = _desc(B=0)
