@@ -418,6 +418,22 @@ __device__ __forceinline__ void dma16s_salu(const void* sbase, uint32_t voff, ui
                :: "v"(voff), "s"(s), "s"(l) : "memory", "m0");
 }
 
+// Word 3 of a raw buffer descriptor on gfx9 parts (32-bit data format, no
+// swizzle); the descriptor's size field bounds-checks each access, and
+// stores past it are dropped.
+constexpr int kBufferWord3 = 0x00020000;
+// Cache-policy bits of a buffer access marked non-temporal (gfx940+ "nt").
+constexpr int kBufferNonTemporal = 2;
+// A raw buffer descriptor for `bytes` bytes from `base`.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, kBufferWord3);
+}
+// Non-temporal store of one float at byte offset voff + soff of a buffer
+// (the builtin takes the data as an unsigned int: the bits, not the value).
+__device__ __forceinline__ void buffer_store_f32_nt(float v, __amdgpu_buffer_rsrc_t rs, int voff, int soff) {
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), rs, voff, soff, kBufferNonTemporal);
+}
+
 // Makes a wave-uniform value (a kernel argument) live in SGPRs from here on.
 // Without it the compiler may issue the scalar load of an argument that is
 // only used after a pipelined loop right before that loop; a scalar load in

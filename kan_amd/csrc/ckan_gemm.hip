@@ -1458,6 +1458,283 @@ k_dx_dh(const typename Elem<BF>::type* __restrict__ dYx,
 }
 
 // ---------------------------------------------------------------------------
+// dX, bf16, degrees 3..8, persistent, with copy waves.  The tiles, MFMAs and
+// accumulation order of k_dx_dh: waves 0-7 only read fragments and run
+// MFMAs (wave (rg, dh) = (wave / 2, wave % 2): fragment rows 2 rg, 2 rg + 1,
+// degrees dh PH .. + PH - 1) and waves 8-11 (one per SIMD) only issue the
+// global -> LDS copies.  12 waves make three per SIMD, so every wave fits 168
+// registers: the MFMA waves hold one k-block's fragments at a time and read
+// the tile's tanh values from LDS in the epilogue.
+//
+// Persistent: block b walks tiles b, b + G, ... (tile = (row block rb, input
+// block ib), rb fastest) as one stream of stages of KI = 2 k-blocks; the
+// copies run three stages ahead in a ring of four.  Barrier B_s starts stage
+// s; before it the copy waves have waited for stage s + 1 and every MFMA wave
+// has finished reading stage s - 1, so after it the copy waves fill slot
+// (s + 3) % 4 = (s - 1) % 4, and an MFMA wave reads the first k-block of
+// stage s + 1 before B_{s+1}, overlapping the barrier.  A tile's epilogue:
+// its tanh values (copied into a 32 KiB buffer after the previous tile's
+// epilogue) are read and each wave's degree sums formed and scaled by their
+// rows' input slope; the next stage barrier frees the buffer, which then
+// carries the dh pairs' exchange (one more barrier, X).  The next tile's tanh
+// copies follow the barrier after that.  A tile needs at least 4 stages
+// (tanh copies waited two stages after their issue, before the tile's last).
+//
+// Measured at config 3 (cuts of a scratch copy): the MFMA loop alone takes
+// 84 us of the kernel's ~115; the copies and fragment reads ~18 us; the
+// epilogue ~14 us when it held the kept row's tanh values across the
+// exchange (register spills whose reloads waited behind the tile's stores),
+// about half that with the sums scaled before the exchange.  A 16x16x32
+// version whose waves own every degree (no exchange) ran its MFMA loop 27 %
+// slower, and one with the copies issued between the MFMA waves' MFMAs ran
+// 20 % slower than k_dx_dh.
+// ---------------------------------------------------------------------------
+template <int P>
+struct DxWs {
+  static constexpr int PH = P / 2, KI = 2, FB = 1024;
+  static constexpr int NMW = 8, NDW = 4, THR = (NMW + NDW) * 64;
+  static constexpr int A_FR = 8 * KI, B_FR = P * KI, STAGE_FR = A_FR + B_FR;
+  static constexpr int STAGE_BYTES = STAGE_FR * FB;
+  static constexpr int CPW = STAGE_FR / NDW;   // stage copies per copy wave
+  static constexpr int NBUF = 4;
+  static constexpr int RING = NBUF * STAGE_BYTES;
+  static constexpr int TBUF = 256 * 32 * 4;    // tanh tile [256 rows][32 inputs] fp32
+  static constexpr int TCPW = TBUF / FB / NDW;  // tanh copies per copy wave
+  static constexpr int XCH = NMW * 16 * 64 * 4;  // the dh pairs' exchange (in the tanh buffer)
+  static constexpr int LDS_BYTES = RING + TBUF;
+  static constexpr int MIN_STAGES = 4;
+  static constexpr bool kOk = (P == 4 || P == 8) && STAGE_FR % NDW == 0 && XCH <= TBUF &&
+                              CPW + TCPW < 64 && LDS_BYTES <= 160 * 1024;
+};
+
+template <int P>
+__global__ void __launch_bounds__(768)
+k_dx_ws(const uint16_t* __restrict__ dYx, const uint16_t* __restrict__ Cb,
+        const float* __restrict__ tc, float* __restrict__ dx, Plan p, int n_rb, int ntiles) {
+  typedef DxWs<P> K;
+  constexpr int PH = K::PH, KI = K::KI, FB = K::FB, NBUF = K::NBUF, CPW = K::CPW, TCPW = K::TCPW;
+  static_assert(K::kOk, "shape");
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nst = p.KBx / KI;  // stages per tile (>= MIN_STAGES, checked on the host)
+  const int G = gridDim.x;
+  const int mine = (ntiles - (int)blockIdx.x + G - 1) / G;  // tiles of this block (>= 1)
+  const int total = mine * nst;
+  float* tbuf = reinterpret_cast<float*>(smem + K::RING);
+
+  if (wave >= K::NMW) {
+    // ---- copy waves ----
+    const int dw = wave - K::NMW;
+    const uint32_t ring = (uint32_t)(uintptr_t)smem, tb = ring + K::RING;
+    const uint32_t voff = (uint32_t)lane * 16;
+    const char* const a0 = reinterpret_cast<const char*>(dYx);
+    const char* const b0 = reinterpret_cast<const char*>(Cb);
+    const size_t run = (size_t)p.KBx * FB;  // one fragment row / degree, all k-blocks
+    // stage cursor of the next issue: tile ik, stage ist (clamped at the end)
+    int ik = 0, ist = 0, islot = 0;
+    auto issue = [&]() __attribute__((always_inline)) {
+      const int tix = (int)blockIdx.x + (ik < mine ? ik : mine - 1) * G;
+      const int st = ik < mine ? ist : nst - 1;  // past the end: in-range data, never read
+      const int rb = tix % n_rb, ib = tix / n_rb;
+      const char* a = a0 + (size_t)rb * 8 * run + (size_t)st * KI * FB;
+      const char* b = b0 + (size_t)ib * P * run + (size_t)st * KI * FB;
+      const uint32_t l = ring + (uint32_t)islot * K::STAGE_BYTES;
+#pragma unroll
+      for (int q = 0; q < CPW; ++q) {
+        const int f = dw * CPW + q;  // wave-uniform
+        const char* src = f < K::A_FR ? a + (size_t)(f / KI) * run + (f % KI) * FB
+                                      : b + (size_t)((f - K::A_FR) / KI) * run + ((f - K::A_FR) % KI) * FB;
+        dma16s(src, voff, l + (uint32_t)f * FB);
+      }
+      if (++ist == nst) { ist = 0; ++ik; }
+      islot = islot == NBUF - 1 ? 0 : islot + 1;
+    };
+    // the tanh values of tile k: copy (dw, j) = tile rows 8 (dw TCPW + j) ..
+    // + 7, lane -> row lane / 8, 16-byte chunk lane % 8 (32 inputs per row)
+    auto issue_t = [&](int k) __attribute__((always_inline)) {
+      const int tix = (int)blockIdx.x + k * G;
+      const int rb = tix % n_rb, ib = tix / n_rb;
+      const int ch = ib * 32 + 4 * (lane & 7) < p.I_sg ? 4 * (lane & 7) : 0;  // past the pitch: unused
+#pragma unroll
+      for (int j = 0; j < TCPW; ++j) {
+        const int64_t r = (int64_t)rb * 256 + 8 * (dw * TCPW + j) + (lane >> 3);
+        const int64_t rr = r < p.B ? r : p.B - 1;  // rows past B: unused
+        dma16s(tc, (uint32_t)((rr * p.I_sg + ib * 32 + ch) * 4), tb + (uint32_t)(dw * TCPW + j) * FB);
+      }
+    };
+    issue_t(0);
+    issue();
+    issue();
+    issue();
+    wait_vmcnt<2 * CPW>();  // tanh tile 0 and stage 0
+    block_barrier();        // P
+    wait_vmcnt<CPW>();      // stage 1
+    block_barrier();        // B_0
+    int st = 0, k = 0;      // the stage just started
+    for (int s = 0; s < total; ++s) {
+      // the next tile's tanh values, after the barrier that follows its
+      // predecessor's exchange (B_{S+1}, S = the tile's first stage)
+      const bool tcopy = st == 1 && k > 0;
+      if (tcopy) issue_t(k);
+      issue();  // stage s + 3
+      if (tcopy) wait_vmcnt<CPW + TCPW>();  // stage s + 2
+      else wait_vmcnt<CPW>();
+      block_barrier();  // B_{s+1}
+      if (++st == nst) {
+        st = 0;
+        ++k;
+        block_barrier();  // X: the exchange of tile k - 1
+      }
+    }
+    wait_vmcnt<0>();
+    return;
+  }
+
+  // ---- MFMA waves ----
+  const int dh = wave & 1, rg = wave >> 1, g = lane >> 5;
+  const char* const ring = smem;
+  auto read = [&](int slot, int kk, Frag<true>* fa, Frag<true>* fb) __attribute__((always_inline)) {
+    const char* base = ring + slot * K::STAGE_BYTES;
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+      fa[mi] = load_frag<true>(reinterpret_cast<const uint16_t*>(base + ((rg * 2 + mi) * KI + kk) * FB), lane);
+#pragma unroll
+    for (int e = 0; e < PH; ++e)
+      fb[e] = load_frag<true>(reinterpret_cast<const uint16_t*>(base + (K::A_FR + (dh * PH + e) * KI + kk) * FB), lane);
+  };
+
+  f32x16_t acc[2][PH];
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+    for (int e = 0; e < PH; ++e)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[mi][e][v] = 0.0f;
+
+  pin_sgpr(dx);
+  Frag<true> fa[2], fb[PH];
+  block_barrier();  // P: stage 0 landed
+  read(0, 0, fa, fb);
+  block_barrier();  // B_0
+  int slot = 0;
+  for (int k = 0; k < mine; ++k) {
+    for (int st = 0; st < nst; ++st) {
+#pragma unroll
+      for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int e = 0; e < PH; ++e) mma(acc[mi][e], fa[mi], fb[e]);
+      read(slot, 1, fa, fb);
+#pragma unroll
+      for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int e = 0; e < PH; ++e) mma(acc[mi][e], fa[mi], fb[e]);
+      slot = slot == NBUF - 1 ? 0 : slot + 1;
+      if (st + 1 < nst) {
+        read(slot, 0, fa, fb);  // stage s + 1 landed before B_s
+        block_barrier();        // B_{s+1}
+      }
+    }
+
+    // epilogue of tile k: degree sums with U_{d-1}(t) over this wave's
+    // degrees d = dh PH + e + 1 (k_dx_dh's arithmetic), one fragment row at a
+    // time; dh is made a constant so that no register array is indexed at run
+    // time
+    const int tix = (int)blockIdx.x + k * G;
+    const int rb = tix % n_rb, ib = tix / n_rb;
+    auto epilogue = [&](auto DH) __attribute__((always_inline)) {
+      constexpr int d = decltype(DH)::value, keep = d, give = 1 - d;
+      // the row handed to the pair first (its accumulators die before the
+      // kept row's are read), each sum scaled by its row's input slope here,
+      // so no tanh value is held across the exchange
+      float part[2][16];  // [0]: the row handed over, [1]: the row kept
+      int toff = (rg * 64 + 4 * g) * 32 + (lane & 31);
+      asm volatile("" : "+v"(toff));
+      const float* tl = tbuf + toff;
+#pragma unroll
+      for (int step = 0; step < 2; ++step) {
+        const int mi = step == 0 ? give : keep;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const float tv = tl[(mi * 32 + 8 * (v >> 2) + (v & 3)) * 32];
+          const float t2 = tv + tv;
+          float up = 0.0f, u = 1.0f;  // U_{-1}, U_0; advanced to U_{d*PH}
+#pragma unroll
+          for (int j = 0; j < PH; ++j) {
+            const float un = fmaf(t2, u, -up);
+            up = d ? u : up;
+            u = d ? un : u;
+          }
+          float sum = 0.0f;
+#pragma unroll
+          for (int e = 0; e < PH; ++e) {
+            sum = fmaf(acc[mi][e][v], u, sum);
+            const float un = fmaf(t2, u, -up);
+            up = u;
+            u = un;
+          }
+          part[step][v] = sum * input_slope(tv, p);
+          if ((v & 3) == 3) __builtin_amdgcn_sched_barrier(0);  // 168-register budget
+        }
+      }
+      // the sums are formed here, before the barriers
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) asm volatile("" ::"v"(part[q][v]));
+      wait_lgkmcnt<0>();
+      block_barrier();  // B_S: every wave has read its tanh values; the buffer is free
+      // wave (rg, d) keeps fragment row d and hands row 1 - d to its pair
+      int xoff = rg * 2 * 16 * 64 + lane;
+      asm volatile("" : "+v"(xoff));
+      float* xw = tbuf + xoff + d * 16 * 64;
+      const float* xr = tbuf + xoff + (d ^ 1) * 16 * 64;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) xw[v * 64] = part[0][v];
+      wait_lgkmcnt<0>();
+      block_barrier();  // X
+      float res[16];
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const float other = xr[v * 64];
+        // fixed order: the lower degrees' half first
+        res[v] = d ? other + part[1][v] : part[1][v] + other;
+      }
+      // row r0u + 4 g + 8 (v / 4) + v % 4, input i, by buffer stores: the
+      // descriptor's base is row r0u and its size ends at row B (the unit
+      // drops stores past it, the rows of a partial tile), a wave-uniform
+      // row offset and a per-lane 32-bit offset (no 64-bit address registers)
+      const int i = ib * 32 + (lane & 31);
+      const int64_t r0u = ((int64_t)rb * 8 + rg * 2 + d) * 32;
+      const int64_t rows_left = p.B - r0u;
+      if (rows_left > 0) {
+        const __amdgpu_buffer_rsrc_t rs =
+            buffer_rsrc(dx + r0u * p.I, (int)((rows_left < 32 ? rows_left : 32) * p.I * 4));
+        const int loff = (4 * g * p.I + i) * (int)sizeof(float);
+        if (i < p.I) {
+#pragma unroll
+          for (int v = 0; v < 16; ++v)
+            buffer_store_f32_nt(res[v], rs, loff, (8 * (v >> 2) + (v & 3)) * p.I * 4);
+        }
+      }
+    };
+    if (dh) epilogue(std::integral_constant<int, 1>{});
+    else epilogue(std::integral_constant<int, 0>{});
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+      for (int e = 0; e < PH; ++e)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[mi][e][v] = 0.0f;
+    // the next tile's first stage (landed before B_S); after the last tile a
+    // read of in-range LDS whose values are never used (unconditional, so the
+    // last stage's fragments are not kept live through the epilogue)
+    read(slot, 0, fa, fb);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // dX at degree 16, bf16: v_mfma_f32_16x16x32_bf16 on 16-input column
 // fragments.  A 32-input block carries 16 x 32 = 512 GEMM columns, so the
 // 32x32 kernel above fits only 128 rows per block and each wave reads 9 KiB
@@ -2578,6 +2855,15 @@ static bool dx16_ok(const Plan& p) {
          ceil_div(p.B32, Dx16::ROWS) * ceil_div(p.I, 16) < (1ll << 30);
 }
 
+// k_dx_ws's limits: at least four stages per tile (the tanh copies of a tile
+// are waited two stages after their issue), 32-bit per-lane offsets into the
+// tanh cache, a tile count that fits an int
+static bool dx_ws_ok(const Plan& p) {
+  return p.KBx / DxWs<8>::KI >= DxWs<8>::MIN_STAGES &&
+         (uint64_t)p.B * p.I_sg * sizeof(float) < (1ull << 32) &&
+         ceil_div(p.B32, 256) * p.NIB < (1ll << 30);
+}
+
 template <int P, bool BF>
 static void dx_dispatch(const void* dYx, const void* packed, const float* t, float* dx,
                         const Plan& p, hipStream_t s) {
@@ -2593,6 +2879,19 @@ static void dx_dispatch(const void* dYx, const void* packed, const float* t, flo
       hipLaunchKernelGGL(k_dx16, dim3(ntiles < kChipBlocks ? ntiles : kChipBlocks), dim3(Dx16::THR),
                          Dx16::LDS_BYTES, s, reinterpret_cast<const uint16_t*>(dYx),
                          reinterpret_cast<const uint16_t*>(Cb), t, dx, p, nib16, ntiles);
+      return;
+    }
+  }
+  if constexpr (BF && (P == 4 || P == 8)) {
+    if (dx_ws_ok(p)) {
+      typedef DxWs<P> K;
+      const int n_rb = (int)ceil_div(p.B32, 256);
+      const int ntiles = n_rb * p.NIB;
+      static std::atomic<uint32_t> lds_set{0};
+      ensure_lds_limit(reinterpret_cast<const void*>(&k_dx_ws<P>), K::LDS_BYTES, lds_set);
+      hipLaunchKernelGGL((k_dx_ws<P>), dim3(ntiles < kChipBlocks ? ntiles : kChipBlocks),
+                         dim3(K::THR), K::LDS_BYTES, s, reinterpret_cast<const uint16_t*>(dYx),
+                         reinterpret_cast<const uint16_t*>(Cb), t, dx, p, n_rb, ntiles);
       return;
     }
   }

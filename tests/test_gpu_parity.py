@@ -72,6 +72,9 @@ SHAPES = [
     (4096, 600, 64, 16),  # degree-16 dx, 608 tiles over 256 persistent blocks, 2 stages each
     (2048, 1040, 512, 15),  # the same with 16 stages per tile, 65 input blocks
     (5, 40, 100, 16),     # degree-16 dx with 5 rows: one partial tile per input block
+    (2100, 1000, 136, 7),  # bf16 dx with copy waves: 288 tiles over 256 persistent blocks
+                           # (two tiles for some), ragged rows / inputs / outputs, 6 stages
+    (2600, 900, 130, 4),   # the same at degree 4: 319 tiles, 4 stages per tile
 ]
 
 
