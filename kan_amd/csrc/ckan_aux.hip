@@ -117,6 +117,18 @@ __device__ __forceinline__ void pack_tile(const CT* __restrict__ C, typename Ele
     const int64_t k = tj0 + tid + u * 256;
     tx[u] = k < tj1 ? __builtin_nontemporal_load(tj.x + k) : f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
+  // tanh of the chunk at c0 held in tx, stored to t
+  auto tanh_chunk = [&](int64_t c0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < kPackTanhU; ++u) {
+      const int64_t k = c0 + tid + u * 256;
+      f32x4_t r;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) r[j] = input_map(tx[u][j], tj.imap, tj.ima, tj.imb);
+      if (k < tj1) tj.t[k] = r;  // read again by the GEMMs: cached store
+    }
+  };
+  bool first_done = false;  // the first chunk is done while the tile loads (float4 path)
   const int i0 = ib * 32, o0 = ob * 32;
   const int D = p.D;
   const int RP = 32 * D + 1;
@@ -138,6 +150,10 @@ __device__ __forceinline__ void pack_tile(const CT* __restrict__ C, typename Ele
           ? __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(reinterpret_cast<const float*>(C) + ((size_t)i * p.O + o0) * D + k4 * 4))
           : f32x4_t{0.f, 0.f, 0.f, 0.f};
     }
+    // the tanh share's first chunk (its loads went out before the tile's)
+    // while the tile's loads are in flight
+    tanh_chunk(tj0);
+    first_done = true;
 #pragma unroll
     for (int q = 0; q < MAXV; ++q) {
       const int v = tid + q * 256;
@@ -239,7 +255,7 @@ __device__ __forceinline__ void pack_tile(const CT* __restrict__ C, typename Ele
     store_frag<BF>(Cb + ((size_t)(ib * P + e) * p.KBx + kbx) * kFragElems, lane, v);
   }
 
-  for (int64_t c0 = tj0; c0 < tj1; c0 += 256 * kPackTanhU) {
+  for (int64_t c0 = first_done ? tj0 + 256 * kPackTanhU : tj0; c0 < tj1; c0 += 256 * kPackTanhU) {
     if (c0 > tj0) {
 #pragma unroll
       for (int u = 0; u < kPackTanhU; ++u) {
@@ -247,14 +263,7 @@ __device__ __forceinline__ void pack_tile(const CT* __restrict__ C, typename Ele
         tx[u] = k < tj1 ? __builtin_nontemporal_load(tj.x + k) : f32x4_t{0.f, 0.f, 0.f, 0.f};
       }
     }
-#pragma unroll
-    for (int u = 0; u < kPackTanhU; ++u) {
-      const int64_t k = c0 + tid + u * 256;
-      f32x4_t r;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) r[j] = input_map(tx[u][j], tj.imap, tj.ima, tj.imb);
-      if (k < tj1) tj.t[k] = r;
-    }
+    tanh_chunk(c0);
   }
 }
 
