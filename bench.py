@@ -314,6 +314,31 @@ def _suite(only=SUITE, cpu=True):
                              "gemm_GBps": alg_bytes / (gemm_ms * 1e-3) / 1e9,
                              "frac_hbm_peak": alg_bytes / (gemm_ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
                              "forward_GBps": alg_bytes / (ms * 1e-3) / 1e9}
+            # the drop-in layer: ChebyKANLayer(2048, 2048, 8) with bf16 coefficients,
+            # called under no_grad; its packed operands are cached per coefficient
+            # version, so each call runs the forward alone (cold: NROT layers rotated)
+            layers = []
+            for _ in range(NROT):
+                m = kan_amd.ChebyKANLayer(I5, O5, 8, compute="bf16").to(dev)
+                m.cheby_coeffs.data = c5.to(dev)
+                layers.append(m)
+            kk = [0]
+
+            def lfwd():
+                m = layers[kk[0] % NROT]
+                kk[0] += 1
+                return m(x5)
+            with torch.no_grad():
+                for m in layers:
+                    m(x5)  # packs once
+                torch.cuda.synchronize()
+                ms_layer = _time_loop(lfwd, 300, 30)
+                y_layer = layers[0](x5)
+                torch.cuda.synchronize()
+            assert torch.equal(y_layer, y5), "layer and raw forward disagree"
+            ent["cold"]["us_layer_forward"] = ms_layer * 1e3
+            ent["cold"]["layer_over_raw"] = ms_layer * 1e3 / ent["cold"]["us_forward"]
+            del layers
             if cpu:
                 from oracle import chebykan_oracle as orc
                 cores = _cpu_threads()
@@ -329,7 +354,9 @@ def _suite(only=SUITE, cpu=True):
         del packs
         out["cfg5"] = {"workload": "ChebyKANLayer(2048,2048,8) inference, bf16 coefficients (packed once); "
                                    f"warm = one packed copy, cold = {NROT} copies rotated (forward "
-                                   "operands above the 256 MB Infinity Cache)",
+                                   "operands above the 256 MB Infinity Cache); us_layer_forward = "
+                                   "the drop-in module called under no_grad (its packed operands "
+                                   f"cached per coefficient version), {NROT} modules rotated",
                        **res5}
 
     if "families" in only:
@@ -430,7 +457,7 @@ def _cpu_baseline(sample_rows: int, reps: int):
         "kind": "port",
         "host": _cpu_info(),
         "sample": (f"config-3 layer (1024->1024, deg 8) fwd+bwd(dx,dC) on {sample_rows} of the "
-                   f"8192 rows, fp32 torch CPU op-for-op restatement of "
+                   f"{B} rows, fp32 torch CPU op-for-op restatement of "
                    f"kan/basis/chebyshev.py:78,92-101,130-145 + autograd; median of {n} "
                    f"steps after 1 warm-up ({t * 1e3:.1f} ms/step, {spent:.1f} s of CPU work)"),
     }
@@ -478,7 +505,8 @@ def main():
                     help="untimed steps for this many seconds before the warm-up (0: none); "
                          "reported in the JSON line")
     ap.add_argument("--compute", default="bf16", choices=["bf16", "fp32"])
-    ap.add_argument("--cpu-rows", type=int, default=1024)
+    ap.add_argument("--cpu-rows", type=int, default=B,
+                    help="config-3 rows in the CPU baseline's step (default: all of them)")
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-fp32", action="store_true")

@@ -6,6 +6,7 @@ from __future__ import annotations
 
 import ctypes
 import threading
+import weakref
 
 import torch
 
@@ -31,6 +32,64 @@ def _forward_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     return ws
 
 
+# Packed-operand cache.  The reference re-lays C out inside the einsum on every
+# call (kan/basis/chebyshev.py:101); here the packed operands depend only on
+# the coefficients' values and the layer's shape, precision and basis, so the
+# last packing of each coefficient tensor is kept and reused while the tensor
+# is unchanged: same object, same storage and the same version counter (every
+# in-place update, an optimizer step included, advances it).  A changed tensor
+# is packed into a new buffer, so a graph recorded before the change keeps its
+# own operands for its backward.  Code that writes the coefficients through a
+# raw pointer (a C-ABI call) must advance the version itself, as kan_amd.optim
+# does (torch.autograd.graph.increment_version).  Entries die with their tensor; one packed
+# buffer per live coefficient tensor stays allocated (2 I O P bytes in bf16,
+# about 4 I O P in fp32).  clear_pack_cache() drops them all.
+# Entries are keyed by id(tensor) and hold a weak reference to the tensor
+# (checked by identity on lookup; a tensor's == is elementwise, so weak-keyed
+# dictionaries cannot hold tensors) whose callback drops the entry.
+_pack_cache = {}  # id(coeffs) -> (weakref to coeffs, key, packed)
+_pack_lock = threading.Lock()
+
+
+def clear_pack_cache() -> None:
+    """Release every cached packed-coefficient buffer."""
+    with _pack_lock:
+        _pack_cache.clear()
+
+
+def cached_pack(coeffs: torch.Tensor):
+    """The packed buffer cached for ``coeffs`` (whatever its version), or None."""
+    with _pack_lock:
+        ent = _pack_cache.get(id(coeffs))
+    return ent[2] if ent is not None and ent[0]() is coeffs else None
+
+
+def _cache_get(coeffs: torch.Tensor, key):
+    with _pack_lock:
+        ent = _pack_cache.get(id(coeffs))
+    if ent is not None and ent[0]() is coeffs and ent[1] == key:
+        return ent[2]
+    return None
+
+
+def _cache_put(coeffs: torch.Tensor, key, packed: torch.Tensor) -> None:
+    i = id(coeffs)
+
+    def drop(ref, i=i):  # the tensor died: its entry goes (unless already replaced)
+        ent = _pack_cache.get(i)
+        if ent is not None and ent[0] is ref:
+            _pack_cache.pop(i, None)
+
+    with _pack_lock:
+        _pack_cache[i] = (weakref.ref(coeffs, drop), key, packed)
+
+
+def _pack_key(coeffs: torch.Tensor, compute: str, spec, affine):
+    spec_key = None if spec is None else bytes(spec)
+    return (coeffs._version, coeffs.data_ptr(), coeffs.dtype, tuple(coeffs.shape), coeffs.device,
+            compute, spec_key, None if affine is None else tuple(affine))
+
+
 def _require_device(*tensors) -> None:
     for t in tensors:
         if t is not None and not t.is_cuda:
@@ -54,6 +113,73 @@ def coeff_code(dtype: torch.dtype) -> int:
     raise RuntimeError(f"kan_amd ChebyKAN supports float32 or bfloat16 coefficients, got {dtype}")
 
 
+# Descriptors by (batch, in, out, degree, compute, coefficient dtype, affine).
+_descs = {}
+# tanh caches of forwards that keep no graph (nothing reads them afterwards),
+# one per (device, stream), grown as needed: calls sharing one must not overlap.
+_t_scratch = {}
+
+
+def _desc_for(batch, in_dim, out_dim, degree, compute, dtype, affine):
+    key = (batch, in_dim, out_dim, degree, compute, dtype, affine)
+    d = _descs.get(key)
+    if d is None:
+        d = _lib.make_desc(batch, in_dim, out_dim, degree, compute_code(compute), coeff_code(dtype),
+                           affine)
+        if len(_descs) > 4096:
+            _descs.clear()
+        _descs[key] = d
+    return d
+
+
+def _layer_forward(x, coeffs, compute, spec, affine, keep_t):
+    """The layer's forward through the C-ABI: returns (y, t, packed, desc).
+    With keep_t the tanh cache is a new tensor (saved for the backward);
+    otherwise a per-stream scratch buffer."""
+    _require_device(x, coeffs)
+    if coeffs.dim() != 3:
+        raise RuntimeError(f"coefficients must be [in, out, degree+1], got {tuple(coeffs.shape)}")
+    in_dim, out_dim, dd = coeffs.shape
+    if x.dim() != 2 or x.shape[1] != in_dim:
+        raise RuntimeError(f"x must be [batch, {in_dim}], got {tuple(x.shape)}")
+    lib = _lib.load()
+    dev = x.device
+    x32 = x.contiguous() if x.dtype == torch.float32 else x.float().contiguous()
+    desc = _desc_for(x32.shape[0], in_dim, out_dim, dd - 1, compute, coeffs.dtype,
+                     None if affine is None else tuple(affine))
+    stream = _lib.stream_ptr(dev)
+    t_elems = lib.ckan_tcache_elems(desc)
+    if keep_t:
+        t = torch.empty(t_elems, dtype=torch.float32, device=dev)
+    else:
+        tkey = (dev.index, stream)
+        t = _t_scratch.get(tkey)
+        if t is None or t.numel() < t_elems:
+            t = torch.empty(max(t_elems, 64), dtype=torch.float32, device=dev)
+            _t_scratch[tkey] = t
+    y = torch.empty(x32.shape[0], out_dim, dtype=torch.float32, device=dev)
+    ws_bytes = lib.ckan_fwd_workspace_bytes(desc)
+    ws = _forward_workspace(dev, ws_bytes) if ws_bytes else None
+    key = _pack_key(coeffs, compute, spec, affine)
+    packed = _cache_get(coeffs, key)
+    if packed is not None:
+        _lib.check(lib.ckan_forward(desc, x32.data_ptr(), packed.data_ptr(), y.data_ptr(),
+                                    t.data_ptr(), _lib.ptr(ws), ws_bytes, stream))
+    else:
+        c = coeffs.detach().contiguous()
+        packed = torch.empty(lib.ckan_packed_bytes(desc), dtype=torch.uint8, device=dev)
+        # pack (in the family's basis when a spec is given) and forward in one call
+        _lib.check(lib.ckan_pack_forward(desc, spec, c.data_ptr(), packed.data_ptr(),
+                                         x32.data_ptr(), y.data_ptr(), t.data_ptr(),
+                                         _lib.ptr(ws), ws_bytes, stream))
+        _cache_put(coeffs, key, packed)
+    return y, t, packed, desc
+
+
+def _needs_graph(x: torch.Tensor, coeffs: torch.Tensor) -> bool:
+    return torch.is_grad_enabled() and (x.requires_grad or coeffs.requires_grad)
+
+
 class ChebyKANFunction(torch.autograd.Function):
     """y = einsum('bid,iod->bo', T(tanh x), C) with hand-written HIP backward.
 
@@ -66,28 +192,7 @@ class ChebyKANFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x: torch.Tensor, coeffs: torch.Tensor, compute: str = "fp32", spec=None,
                 affine=None):
-        _require_device(x, coeffs)
-        if coeffs.dim() != 3:
-            raise RuntimeError(f"coefficients must be [in, out, degree+1], got {tuple(coeffs.shape)}")
-        in_dim, out_dim, dd = coeffs.shape
-        if x.dim() != 2 or x.shape[1] != in_dim:
-            raise RuntimeError(f"x must be [batch, {in_dim}], got {tuple(x.shape)}")
-        lib = _lib.load()
-        dev = x.device
-        x32 = x.contiguous() if x.dtype == torch.float32 else x.float().contiguous()
-        c = coeffs.detach().contiguous()
-        desc = _lib.make_desc(x32.shape[0], in_dim, out_dim, dd - 1, compute_code(compute),
-                              coeff_code(c.dtype), affine)
-        stream = _lib.stream_ptr(dev)
-        packed = torch.empty(lib.ckan_packed_bytes(desc), dtype=torch.uint8, device=dev)
-        t = torch.empty(lib.ckan_tcache_elems(desc), dtype=torch.float32, device=dev)
-        y = torch.empty(x32.shape[0], out_dim, dtype=torch.float32, device=dev)
-        ws_bytes = lib.ckan_fwd_workspace_bytes(desc)
-        ws = _forward_workspace(dev, ws_bytes) if ws_bytes else None
-        # pack (in the family's basis when a spec is given) and forward in one call
-        _lib.check(lib.ckan_pack_forward(desc, spec,
-                                         c.data_ptr(), packed.data_ptr(), x32.data_ptr(),
-                                         y.data_ptr(), t.data_ptr(), _lib.ptr(ws), ws_bytes, stream))
+        y, t, packed, desc = _layer_forward(x, coeffs, compute, spec, affine, keep_t=True)
         ctx.save_for_backward(t, packed)
         ctx.desc = desc
         ctx.spec = spec
@@ -236,6 +341,8 @@ def chebykan(x: torch.Tensor, coeffs: torch.Tensor, compute: str = "fp32") -> to
     fp64 coefficients select the fp64 path (``compute`` does not apply there)."""
     if coeffs.dtype == torch.float64:
         return ChebyKANFunction64.apply(x, coeffs)
+    if not _needs_graph(x, coeffs):  # inference: no autograd node, no tanh cache kept
+        return _layer_forward(x, coeffs, compute, None, None, keep_t=False)[0]
     return ChebyKANFunction.apply(x, coeffs, compute, None)
 
 
@@ -246,6 +353,8 @@ def family_kan(x: torch.Tensor, coeffs: torch.Tensor, spec, compute: str = "fp32
     if coeffs.dtype == torch.float64:
         raise RuntimeError("kan_amd: the fp64 path serves the Chebyshev layer; Jacobi / Hermite "
                            "layers take float32 or bfloat16 coefficients")
+    if not _needs_graph(x, coeffs):
+        return _layer_forward(x, coeffs, compute, spec, affine, keep_t=False)[0]
     return ChebyKANFunction.apply(x, coeffs, compute, spec, affine)
 
 

@@ -10,6 +10,7 @@ from __future__ import annotations
 from typing import Iterable, Tuple
 
 import torch
+from torch.autograd.graph import increment_version
 
 from . import _lib
 
@@ -43,6 +44,9 @@ class SGD(torch.optim.Optimizer):
                 _lib.check(lib.ckan_sgd_step(p.data_ptr(), g.data_ptr(), p.numel(),
                                              float(group["lr"]), float(group["weight_decay"]),
                                              _lib.stream_ptr(p.device)))
+                # the kernel wrote p through its pointer: advance its version as a
+                # torch in-place op would (the layers' packed-operand caches key on it)
+                increment_version(p)
         return loss
 
 
@@ -92,4 +96,5 @@ class Adam(torch.optim.Optimizer):
                     st["exp_avg_sq"].data_ptr(), p.numel(), step, float(group["lr"]),
                     float(b1), float(b2), float(group["eps"]), float(group["weight_decay"]),
                     _lib.stream_ptr(p.device)))
+                increment_version(p)  # written through its pointer (see SGD.step)
         return loss

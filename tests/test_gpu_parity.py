@@ -560,3 +560,62 @@ def test_pack_forward_equals_pack_then_forward(B, I, O, deg, compute, family):
     assert torch.equal(p0, p1)
     if family is None and B * I <= 4096 * 1024:
         assert _rel(y1.cpu(), orc.layer_forward(x.cpu(), c.cpu())) <= (FP32_TOL if compute == 0 else BF16_TOL)
+
+
+@pytest.mark.parametrize("compute,tol", [("fp32", FP32_TOL), ("bf16", BF16_TOL)])
+def test_packed_operand_cache_reuse_and_invalidation(compute, tol):
+    """The drop-in layer packs its coefficients once per version of the
+    parameter: a second call with C unchanged reuses the packed buffer and
+    gives the bits of an uncached call; an in-place update (under no_grad, or
+    an optimizer step) is packed again and matches the oracle on the new C."""
+    import kan_amd
+    from kan_amd import functional as F
+    print(f"pack cache {compute}", flush=True)
+    torch.manual_seed(5)
+    layer = kan_amd.ChebyKANLayer(96, 80, 8, compute=compute).cuda()
+    x = torch.randn(300, 96).cuda()
+    p = layer.cheby_coeffs
+
+    def ref(xc):
+        c = p.detach().cpu()
+        if compute == "bf16":
+            c = c.bfloat16().float()
+        return orc.layer_forward(xc.cpu(), c)
+
+    with torch.no_grad():
+        y1 = layer(x)
+        e1 = F.cached_pack(p)
+        y2 = layer(x)
+        assert F.cached_pack(p) is e1  # reused, no re-pack
+        y_fresh = F.chebykan(x, p.detach().clone(), compute)  # another tensor: packed anew
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2) and torch.equal(y2, y_fresh)
+    assert _rel(y2, ref(x)) <= tol
+    with torch.no_grad():
+        p.add_(0.01 * torch.randn_like(p))
+        y3 = layer(x)
+    assert F.cached_pack(p) is not e1
+    assert _rel(y3, ref(x)) <= tol
+    # an optimizer step through autograd invalidates it as well
+    opt = torch.optim.SGD(layer.parameters(), lr=0.5)
+    layer(x).pow(2).sum().backward()
+    e3 = F.cached_pack(p)
+    opt.step()
+    with torch.no_grad():
+        y4 = layer(x)
+    assert F.cached_pack(p) is not e3
+    assert _rel(y4, ref(x)) <= tol
+    # and so does a step of this package's own optimizers, which write the
+    # parameter through the C-ABI (they advance its version themselves)
+    from kan_amd import optim
+    opt2 = optim.Adam(layer.parameters(), lr=0.05)
+    layer.cheby_coeffs.grad = None
+    layer(x).pow(2).sum().backward()
+    e4 = F.cached_pack(p)
+    opt2.step()
+    with torch.no_grad():
+        y5 = layer(x)
+    assert F.cached_pack(p) is not e4
+    assert _rel(y5, ref(x)) <= tol
+    F.clear_pack_cache()
+    assert F.cached_pack(p) is None
