@@ -165,6 +165,25 @@ int ckan_forward_f64(const ckan_desc* desc, const double* x, const double* coeff
 int ckan_backward_f64(const ckan_desc* desc, const double* t_cache, const double* coeffs,
                       const double* dy, double* dx, double* dcoeffs, int accumulate, void* stream);
 
+/* The fp64 path for a layer of another polynomial family (ckan_basis_spec,
+ * below): the Jacobi and Hermite layers after .double(), whose reference
+ * computes their bases in fp64 (kan/basis/jacobi.py:96-117,159-188,
+ * kan/basis/hermite.py:118-139,158-233).  The basis P_n(s tanh x) is evaluated
+ * by the family's three-term recurrence in fp64 (no change of basis, whose
+ * matrix entries reach 1e10 for Hermite), from a recurrence block that
+ * ckan_write_recurrence_f64 writes into a caller-owned device buffer of
+ * ckan_recurrence_bytes_f64(spec) bytes (8-byte aligned) once per spec;
+ * the forward and backward then read it (spec->degree must equal
+ * desc->degree: the library cannot check the buffer's contents).  dcoeffs is
+ * the family coefficients' gradient.  The tanh input map only. */
+size_t ckan_recurrence_bytes_f64(const struct ckan_basis_spec* spec);
+int ckan_write_recurrence_f64(const struct ckan_basis_spec* spec, double* rec, void* stream);
+int ckan_forward_f64_basis(const ckan_desc* desc, const double* rec, const double* x,
+                           const double* coeffs, double* y, double* t_cache, void* stream);
+int ckan_backward_f64_basis(const ckan_desc* desc, const double* rec, const double* t_cache,
+                            const double* coeffs, const double* dy, double* dx, double* dcoeffs,
+                            int accumulate, void* stream);
+
 /* ---- other polynomial bases through the same kernels ---------------------
  * A layer whose basis is a three-term-recurrence family P_0..P_deg evaluated
  * at s * tanh(x) is the ChebyKAN layer with coefficients C' = C M, where

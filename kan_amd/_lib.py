@@ -101,6 +101,11 @@ SIGNATURES = {
     "ckan_backward": (ctypes.c_int, [_pdesc, _vp, _vp, _vp, _vp, _vp, ctypes.c_int, _vp, _sz, _vp]),
     "ckan_forward_f64": (ctypes.c_int, [_pdesc, _vp, _vp, _vp, _vp, _vp]),
     "ckan_backward_f64": (ctypes.c_int, [_pdesc, _vp, _vp, _vp, _vp, _vp, ctypes.c_int, _vp]),
+    "ckan_recurrence_bytes_f64": (_sz, [_pspec]),
+    "ckan_write_recurrence_f64": (ctypes.c_int, [_pspec, _vp, _vp]),
+    "ckan_forward_f64_basis": (ctypes.c_int, [_pdesc, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "ckan_backward_f64_basis": (ctypes.c_int, [_pdesc, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_int,
+                                               _vp]),
     "ckan_basis_to_chebyshev": (ctypes.c_int, [_pspec, ctypes.POINTER(_f64)]),
     "ckan_pack_coeffs_basis": (ctypes.c_int, [_pdesc, _pspec, _vp, _vp, _vp]),
     "ckan_coeff_grad_from_chebyshev": (ctypes.c_int, [_pdesc, _pspec, _vp, _vp, ctypes.c_int, _vp]),

@@ -532,8 +532,10 @@ int ckan_basis_backward(const float* t, const float* g, int64_t n, int32_t degre
   return check_launch("basis_backward");
 }
 
-int ckan_forward_f64(const ckan_desc* desc, const double* x, const double* coeffs, double* y,
-                     double* t_cache, void* stream) {
+namespace {
+// The fp64 layer; rec: the family's fp64 recurrence block (nullptr: Chebyshev).
+int forward_f64_impl(const ckan_desc* desc, const double* rec, const double* x,
+                     const double* coeffs, double* y, double* t_cache, void* stream) {
   int rc = validate_desc(desc);
   if (rc) return rc;
   if (desc->compute != CKAN_COMPUTE_FP32 || desc->coeff_dtype != CKAN_DTYPE_F32)
@@ -544,12 +546,13 @@ int ckan_forward_f64(const ckan_desc* desc, const double* x, const double* coeff
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   ProfScope ps("fwd_f64", s);
   launch_forward_valu<double>(x, coeffs, y, t_cache, desc->batch, desc->in_dim,
-                              desc->out_dim, desc->degree, s);
+                              desc->out_dim, desc->degree, s, rec);
   return check_launch("forward_f64");
 }
 
-int ckan_backward_f64(const ckan_desc* desc, const double* t_cache, const double* coeffs,
-                      const double* dy, double* dx, double* dcoeffs, int accumulate, void* stream) {
+int backward_f64_impl(const ckan_desc* desc, const double* rec, const double* t_cache,
+                      const double* coeffs, const double* dy, double* dx, double* dcoeffs,
+                      int accumulate, void* stream) {
   int rc = validate_desc(desc);
   if (rc) return rc;
   if (desc->compute != CKAN_COMPUTE_FP32 || desc->coeff_dtype != CKAN_DTYPE_F32)
@@ -571,8 +574,19 @@ int ckan_backward_f64(const ckan_desc* desc, const double* t_cache, const double
   ProfScope ps("bwd_f64", s);
   const DcOut om{accumulate ? kDcAccumulate : kDcStore};
   launch_backward_valu<double>(t_cache, coeffs, dy, dx, dcoeffs, om, desc->batch, desc->in_dim,
-                               desc->out_dim, desc->degree, s);
+                               desc->out_dim, desc->degree, s, rec);
   return check_launch("backward_f64");
+}
+}  // namespace
+
+int ckan_forward_f64(const ckan_desc* desc, const double* x, const double* coeffs, double* y,
+                     double* t_cache, void* stream) {
+  return forward_f64_impl(desc, nullptr, x, coeffs, y, t_cache, stream);
+}
+
+int ckan_backward_f64(const ckan_desc* desc, const double* t_cache, const double* coeffs,
+                      const double* dy, double* dx, double* dcoeffs, int accumulate, void* stream) {
+  return backward_f64_impl(desc, nullptr, t_cache, coeffs, dy, dx, dcoeffs, accumulate, stream);
 }
 
 namespace {
@@ -620,6 +634,38 @@ int family_xform(const ckan_basis_spec* spec, int degree, BasisXform* xf) {
 }
 
 }  // namespace
+
+size_t ckan_recurrence_bytes_f64(const ckan_basis_spec* spec) {
+  if (!spec || spec->degree < 0 || spec->degree > kValuMaxDegree) return 0;
+  return (size_t)(3 * (spec->degree + 1) + 2) * sizeof(double);
+}
+
+int ckan_write_recurrence_f64(const ckan_basis_spec* spec, double* rec, void* stream) {
+  if (!spec) return fail(CKAN_ERR_INVALID_ARG, "basis spec is NULL");
+  if (spec->degree < 0 || spec->degree > kValuMaxDegree)
+    return fail(spec->degree < 0 ? CKAN_ERR_INVALID_ARG : CKAN_ERR_UNSUPPORTED,
+                "basis degree %d outside 0..%d", spec->degree, kValuMaxDegree);
+  int rc = family_valid(spec, spec->degree);
+  if (rc) return rc;
+  if (!rec) return fail(CKAN_ERR_INVALID_ARG, "rec is NULL");
+  if (reinterpret_cast<uintptr_t>(rec) & 7) return fail(CKAN_ERR_INVALID_ARG, "rec must be 8-byte aligned");
+  launch_write_recur_f64(rec, spec->family, spec->alpha, spec->beta, spec->degree, spec->scale,
+                         reinterpret_cast<hipStream_t>(stream));
+  return check_launch("write_recurrence_f64");
+}
+
+int ckan_forward_f64_basis(const ckan_desc* desc, const double* rec, const double* x,
+                           const double* coeffs, double* y, double* t_cache, void* stream) {
+  if (!rec) return fail(CKAN_ERR_INVALID_ARG, "rec is NULL");
+  return forward_f64_impl(desc, rec, x, coeffs, y, t_cache, stream);
+}
+
+int ckan_backward_f64_basis(const ckan_desc* desc, const double* rec, const double* t_cache,
+                            const double* coeffs, const double* dy, double* dx, double* dcoeffs,
+                            int accumulate, void* stream) {
+  if (!rec) return fail(CKAN_ERR_INVALID_ARG, "rec is NULL");
+  return backward_f64_impl(desc, rec, t_cache, coeffs, dy, dx, dcoeffs, accumulate, stream);
+}
 
 int ckan_basis_to_chebyshev(const ckan_basis_spec* spec, double* M) {
   double a[kMaxD], b[kMaxD], c[kMaxD];

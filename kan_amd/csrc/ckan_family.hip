@@ -100,6 +100,30 @@ void launch_write_recur(float* rec, int family, double alpha, double beta, int d
                      alpha, beta, D, scale);
 }
 
+// The same block in fp64, for the fp64 family layers.
+__global__ void k_write_recur_f64(double* __restrict__ rec, int family, double alpha, double beta,
+                                  int D, double scale) {
+  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  if (n < D) {
+    double a, b, c;
+    recur_coef(family, n, alpha, beta, &a, &b, &c);
+    rec[n] = a;
+    rec[D + n] = b;
+    rec[2 * D + n] = c;
+  }
+  if (n == 0) {
+    rec[3 * D] = scale;
+    rec[3 * D + 1] = (family == CKAN_BASIS_CHEBYSHEV && scale == 1.0) ? 0.0 : 1.0;
+  }
+}
+
+void launch_write_recur_f64(double* rec, int family, double alpha, double beta, int degree,
+                            double scale, hipStream_t s) {
+  const int D = degree + 1;
+  hipLaunchKernelGGL(k_write_recur_f64, dim3((unsigned)((D + 255) / 256)), dim3(256), 0, s, rec,
+                     family, alpha, beta, D, scale);
+}
+
 // The recurrence run on Chebyshev coefficient vectors: multiplication by u is
 // u T_0 = T_1 and u T_k = (T_{k+1} + T_{k-1}) / 2 for k >= 1.
 void family_to_chebyshev(const double* a, const double* b, const double* c, int degree,

@@ -118,23 +118,26 @@ void launch_jacobian(const float* x, const float* c1t, float* jac, int64_t B, in
 
 // ---- vector-ALU path (ckan_valu.hip): any degree, T = float or double ------
 // Serves fp64 layers and fp32 layers above kMfmaMaxDegree, with C in its own
-// [I, O, D] layout; t = input map of x, [B, I].  rec (fp32 only): the packed
-// buffer's recurrence block (a[D], b[D], c[D], scale, kind); nullptr (and
-// kind 0) selects the Chebyshev kernels' specialised recurrence.
+// [I, O, D] layout; t = input map of x, [B, I].  rec: the recurrence block
+// (a[D], b[D], c[D], scale, kind) in the element type (fp32: the packed
+// buffer's; fp64: written by launch_write_recur_f64); nullptr (and kind 0)
+// selects the Chebyshev kernels' specialised recurrence.
 constexpr int kMfmaMaxDegree = 16;   // the packed MFMA kernels' limit
 constexpr int kValuMaxDegree = 256;  // the vector-ALU path's limit
 template <typename T>
 void launch_forward_valu(const T* x, const T* C, T* y, T* t, int64_t B, int I, int O, int deg,
-                         hipStream_t s, const float* rec = nullptr, int imap = 0, float ima = 0.0f,
+                         hipStream_t s, const T* rec = nullptr, int imap = 0, float ima = 0.0f,
                          float imb = 0.0f);
 // dC written by mode om.mode (for T = double: store or accumulate only).
 template <typename T>
 void launch_backward_valu(const T* t, const T* C, const T* dy, T* dx, T* dC, DcOut om, int64_t B,
-                          int I, int O, int deg, hipStream_t s, const float* rec = nullptr,
+                          int I, int O, int deg, hipStream_t s, const T* rec = nullptr,
                           int imap = 0, float ima = 0.0f);
 // The recurrence block (a[D], b[D], c[D], scale, kind) of a ckan_basis_family.
 void launch_write_recur(float* rec, int family, double alpha, double beta, int degree, float scale,
                         hipStream_t s);
+void launch_write_recur_f64(double* rec, int family, double alpha, double beta, int degree,
+                            double scale, hipStream_t s);
 // dst[q] = float(src[q]) (accumulate: dst[q] += float(src[q])) for q < n, src
 // fp32 or bf16.
 void launch_to_f32(const void* src, bool src_bf16, float* dst, int64_t n, hipStream_t s,

@@ -49,7 +49,7 @@ k_tanh_v(const T* __restrict__ x, T* __restrict__ t, int64_t n, int imap, float 
 // 0); rs holds a[D], b[D], c[D], s, kind (0: the Chebyshev recurrence, whose
 // specialised code the kernels then take).
 template <typename T, bool GEN>
-__device__ __forceinline__ void rec_init(T t, const float* rs, int D, T& w, T& pm, T& pc) {
+__device__ __forceinline__ void rec_init(T t, const T* rs, int D, T& w, T& pm, T& pc) {
   if constexpr (GEN) {
     w = (T)rs[3 * D] * t;
     pm = T(0);
@@ -60,7 +60,7 @@ __device__ __forceinline__ void rec_init(T t, const float* rs, int D, T& w, T& p
   pc = T(1);
 }
 template <typename T, bool GEN>
-__device__ __forceinline__ void rec_step(T w, const float* rs, int D, int n, T& pm, T& pc) {
+__device__ __forceinline__ void rec_step(T w, const T* rs, int D, int n, T& pm, T& pc) {
   T nx;
   if constexpr (GEN) {
     // read the step's coefficients here: hoisted out of the unrolled degree
@@ -74,21 +74,27 @@ __device__ __forceinline__ void rec_step(T w, const float* rs, int D, int n, T& 
   pc = nx;
 }
 
-// The recurrence block into LDS (fp32 with a block), before the block's
-// first barrier; after it, rec_generic tells whether the block asks for the
-// generic recurrence (a uniform branch around the kernel's body, which is
-// instantiated once per recurrence kind).
+// The recurrence block: an fp32 block is copied into LDS before the block's
+// first barrier; an fp64 block (the fp64 family layers) is read where it is,
+// by wave-uniform loads, which keeps the fp64 kernels' LDS (and occupancy) as
+// it is.  rec_src gives the copy to read; after the barrier, rec_generic
+// tells whether the block asks for the generic recurrence (a uniform branch
+// around the kernel's body, which is instantiated once per recurrence kind).
 template <typename T>
-__device__ __forceinline__ void stage_rec(float* rs, const float* __restrict__ rec, int D) {
+__device__ __forceinline__ void stage_rec(float* rs, const T* __restrict__ rec, int D) {
   if constexpr (sizeof(T) == 4) {
     if (rec)
       for (int k = threadIdx.x; k < 3 * D + 2; k += blockDim.x) rs[k] = rec[k];
   }
 }
 template <typename T>
-__device__ __forceinline__ bool rec_generic(const float* rs, const float* rec, int D) {
-  if constexpr (sizeof(T) == 4) return rec != nullptr && rs[3 * D + 1] != 0.0f;
-  else return false;
+__device__ __forceinline__ const T* rec_src(const float* lds, const T* rec) {
+  if constexpr (sizeof(T) == 4) return lds;
+  else return rec;
+}
+template <typename T>
+__device__ __forceinline__ bool rec_generic(const T* rs, const T* rec, int D) {
+  return rec != nullptr && rs[3 * D + 1] != T(0);
 }
 
 // dx and dC: SEEK = false instantiations serve the first (or only) chunk (d0
@@ -123,7 +129,7 @@ template <typename T, int DM, bool GEN, int RT, bool INIT>
 __device__ __forceinline__ void fwd_tile(T (&acc)[RT][4], T (&w)[RT][kValuKI],
                                          T (&pm)[RT][kValuKI], T (&pc)[RT][kValuKI],
                                          const T (&ts)[16 * RT][kValuKI + 1],
-                                         const T (&cs)[kValuKI][DM][64], const float* rs, int D,
+                                         const T (&cs)[kValuKI][DM][64], const T* rs, int D,
                                          int d0, int dn, int tr, int to) {
 #pragma unroll
   for (int ii = 0; ii < kValuKI; ++ii) {
@@ -149,7 +155,7 @@ __device__ __forceinline__ void fwd_tile(T (&acc)[RT][4], T (&w)[RT][kValuKI],
 template <typename T, int DM, bool GEN, bool MULTI>
 __device__ __forceinline__ void fwd_body(const T* __restrict__ t, const T* __restrict__ C,
                                          T* __restrict__ y, int64_t B, int I, int O, int D,
-                                         const float* rs,
+                                         const T* rs,
                                          T (&ts)[16 * VTile<T, DM>::WF][kValuKI + 1],
                                          T (&cs)[kValuKI][DM][64]) {
   constexpr int KI = kValuKI, RT = VTile<T, DM>::WF, BR = 16 * RT;
@@ -211,11 +217,12 @@ __device__ __forceinline__ void fwd_body(const T* __restrict__ t, const T* __res
 template <typename T, int DM, bool MULTI>
 __global__ void __launch_bounds__(256)
 k_fwd_v(const T* __restrict__ t, const T* __restrict__ C, T* __restrict__ y, int64_t B, int I,
-        int O, int D, const float* __restrict__ rec) {
+        int O, int D, const T* __restrict__ rec) {
   __shared__ T ts[16 * VTile<T, DM>::WF][kValuKI + 1];
   __shared__ T cs[kValuKI][DM][64];
-  __shared__ float rs[sizeof(T) == 4 ? kRecFloats : 1];
-  stage_rec<T>(rs, rec, D);
+  __shared__ float rs_l[sizeof(T) == 4 ? kRecFloats : 1];
+  stage_rec<T>(rs_l, rec, D);
+  const T* rs = rec_src<T>(rs_l, rec);
   __syncthreads();
   if (rec_generic<T>(rs, rec, D))
     fwd_body<T, DM, true, MULTI>(t, C, y, B, I, O, D, rs, ts, cs);
@@ -237,7 +244,7 @@ k_fwd_v(const T* __restrict__ t, const T* __restrict__ C, T* __restrict__ y, int
 template <typename T, int DM, bool SEEK, bool GEN, int HT>
 __device__ __forceinline__ void dx_epilogue(const T* __restrict__ t, T* __restrict__ dx,
                                             const T (&g)[HT][DM], int64_t B, int I, int D, int d0,
-                                            int dn, int accumulate, const float* rs, int imap,
+                                            int dn, int accumulate, const T* rs, int imap,
                                             float ima) {
   const int tid = threadIdx.x, rr = tid >> 3, ii = tid & 7;
   const int64_t b0 = (int64_t)blockIdx.x * (32 * HT);
@@ -308,8 +315,8 @@ template <typename T, int DM, bool SEEK, bool FULL, int CST, int BR>
 __device__ __forceinline__ void dx_body(const T* __restrict__ t, const T* __restrict__ C,
                                         const T* __restrict__ dy, T* __restrict__ dx, int64_t B,
                                         int I, int O, int D, int d0, int dn_arg, int accumulate,
-                                        const float* __restrict__ rec, int imap, float ima,
-                                        T (&ys)[BR][17], T (&cs)[8 * CST], const float* rs) {
+                                        const T* __restrict__ rec, int imap, float ima,
+                                        T (&ys)[BR][17], T (&cs)[8 * CST], const T* rs) {
   constexpr int OC = 16, HT = BR / 32;
   const int dn = FULL ? DM : dn_arg;
   const int tid = threadIdx.x, rr = tid >> 3, ii = tid & 7;
@@ -359,13 +366,14 @@ template <typename T, int DM, bool SEEK>
 __global__ void __launch_bounds__(256)
 k_dx_v(const T* __restrict__ t, const T* __restrict__ C, const T* __restrict__ dy,
        T* __restrict__ dx, int64_t B, int I, int O, int D, int d0_arg, int dn, int accumulate,
-       const float* __restrict__ rec, int imap, float ima) {
+       const T* __restrict__ rec, int imap, float ima) {
   constexpr int OC = 16, CST = OC * (DM + 1) + 1, BR = 32 * VTile<T, DM>::WX;
   const int d0 = SEEK ? d0_arg : 0;
   __shared__ T ys[BR][OC + 1];
   __shared__ T cs[8 * CST];
-  __shared__ float rs[sizeof(T) == 4 ? kRecFloats : 1];
-  stage_rec<T>(rs, rec, D);
+  __shared__ float rs_l[sizeof(T) == 4 ? kRecFloats : 1];
+  stage_rec<T>(rs_l, rec, D);
+  const T* rs = rec_src<T>(rs_l, rec);
   if (dn == DM)
     dx_body<T, DM, SEEK, true, CST, BR>(t, C, dy, dx, B, I, O, D, d0, dn, accumulate, rec, imap,
                                         ima, ys, cs, rs);
@@ -393,7 +401,7 @@ template <> struct DcWrite<double> {  // store or accumulate
 // input), advanced once per block instead of once per output thread).
 template <typename T, int DM, bool GEN, int CT, bool SEEK>
 __device__ __forceinline__ void dc_tile(T (&acc)[CT][DM], const T (&ts)[32][9], const T* sst,
-                                        const T (&ys)[32][32 * CT + 1], const float* rs, int D,
+                                        const T (&ys)[32][32 * CT + 1], const T* rs, int D,
                                         int d0, int dn, int il, int ol) {
   for (int r = 0; r < 32; ++r) {
     T yv[CT];
@@ -423,7 +431,7 @@ __device__ __forceinline__ void dc_tile(T (&acc)[CT][DM], const T (&ts)[32][9], 
 template <typename T, int DM, bool SEEK, bool GEN, bool FULL>
 __device__ __forceinline__ void dc_body(const T* __restrict__ t, const T* __restrict__ dy,
                                         T* __restrict__ dC, int64_t B, int I, int O, int D,
-                                        int d0, int dn_arg, const DcOut& om, const float* rs,
+                                        int d0, int dn_arg, const DcOut& om, const T* rs,
                                         T (&ts)[32][9], T* sst,
                                         T (&ys)[32][32 * VTile<T, DM>::WC + 1]) {
   constexpr int CT = VTile<T, DM>::WC, BO = 32 * CT;
@@ -476,7 +484,7 @@ __device__ __forceinline__ void dc_body(const T* __restrict__ t, const T* __rest
 template <typename T, int DM, bool SEEK>
 __global__ void __launch_bounds__(256)
 k_dc_v(const T* __restrict__ t, const T* __restrict__ dy, T* __restrict__ dC, int64_t B, int I,
-       int O, int D, int d0_arg, int dn_arg, DcOut om, const float* __restrict__ rec) {
+       int O, int D, int d0_arg, int dn_arg, DcOut om, const T* __restrict__ rec) {
   // SEEK: every chunk of the degree axis in one launch, chunk blockIdx.z (the
   // chunks write disjoint degrees of dC, so they run side by side)
   const int d0 = SEEK ? d0_arg + (int)blockIdx.z * DM : 0;
@@ -484,8 +492,9 @@ k_dc_v(const T* __restrict__ t, const T* __restrict__ dy, T* __restrict__ dC, in
   __shared__ T ts[32][9];
   __shared__ T sst[SEEK ? 3 * 32 * 9 : 1];  // seek states, read only with SEEK
   __shared__ T ys[32][32 * VTile<T, DM>::WC + 1];
-  __shared__ float rs[sizeof(T) == 4 ? kRecFloats : 1];
-  stage_rec<T>(rs, rec, D);
+  __shared__ float rs_l[sizeof(T) == 4 ? kRecFloats : 1];
+  stage_rec<T>(rs_l, rec, D);
+  const T* rs = rec_src<T>(rs_l, rec);
   __syncthreads();
   const bool gen = rec_generic<T>(rs, rec, D), full = dn == DM;
   if (gen && full) dc_body<T, DM, SEEK, true, true>(t, dy, dC, B, I, O, D, d0, dn, om, rs, ts, sst, ys);
@@ -525,7 +534,7 @@ static int valu_dm(int D) { return D <= 3 ? 3 : D <= 5 ? 5 : D <= 9 ? 9 : kValuD
 
 template <typename T, int DM>
 static void fwd_launch(const T* t, const T* C, T* y, int64_t B, int I, int O, int D,
-                       const float* rec, hipStream_t s) {
+                       const T* rec, hipStream_t s) {
   constexpr int BR = 16 * VTile<T, DM>::WF;
   const dim3 g((unsigned)((B + BR - 1) / BR), (unsigned)((O + 63) / 64));
   if constexpr (DM == kValuDM) {  // the only chunk size with more degrees than one chunk
@@ -539,7 +548,7 @@ static void fwd_launch(const T* t, const T* C, T* y, int64_t B, int I, int O, in
 
 template <typename T, int DM>
 static void bwd_chunks(const T* t, const T* C, const T* dy, T* dx, T* dC, DcOut om, int64_t B,
-                       int I, int O, int D, const float* rec, int imap, float ima, hipStream_t s) {
+                       int I, int O, int D, const T* rec, int imap, float ima, hipStream_t s) {
   for (int d0 = 0; d0 < D; d0 += DM) {
     const int dn = D - d0 < DM ? D - d0 : DM;
     if (dx && B > 0) {
@@ -568,7 +577,7 @@ static void bwd_chunks(const T* t, const T* C, const T* dy, T* dx, T* dC, DcOut 
 
 template <typename T>
 void launch_forward_valu(const T* x, const T* C, T* y, T* t, int64_t B, int I, int O, int deg,
-                         hipStream_t s, const float* rec, int imap, float ima, float imb) {
+                         hipStream_t s, const T* rec, int imap, float ima, float imb) {
   if (B == 0) return;
   hipLaunchKernelGGL(k_tanh_v<T>, dim3(vgrid(B * I)), dim3(256), 0, s, x, t, B * I, imap, ima, imb);
   const int D = deg + 1;
@@ -582,7 +591,7 @@ void launch_forward_valu(const T* x, const T* C, T* y, T* t, int64_t B, int I, i
 
 template <typename T>
 void launch_backward_valu(const T* t, const T* C, const T* dy, T* dx, T* dC, DcOut om, int64_t B,
-                          int I, int O, int deg, hipStream_t s, const float* rec, int imap,
+                          int I, int O, int deg, hipStream_t s, const T* rec, int imap,
                           float ima) {
   const int D = deg + 1;
   switch (valu_dm(D)) {
@@ -596,13 +605,13 @@ void launch_backward_valu(const T* t, const T* C, const T* dy, T* dx, T* dC, DcO
 template void launch_forward_valu<float>(const float*, const float*, float*, float*, int64_t, int,
                                          int, int, hipStream_t, const float*, int, float, float);
 template void launch_forward_valu<double>(const double*, const double*, double*, double*, int64_t,
-                                          int, int, int, hipStream_t, const float*, int, float,
+                                          int, int, int, hipStream_t, const double*, int, float,
                                           float);
 template void launch_backward_valu<float>(const float*, const float*, const float*, float*, float*,
                                           DcOut, int64_t, int, int, int, hipStream_t, const float*,
                                           int, float);
 template void launch_backward_valu<double>(const double*, const double*, const double*, double*,
                                            double*, DcOut, int64_t, int, int, int, hipStream_t,
-                                           const float*, int, float);
+                                           const double*, int, float);
 
 }  // namespace ckan

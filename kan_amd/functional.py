@@ -289,12 +289,36 @@ class FamilyBasisFunction(torch.autograd.Function):
         return dt.to(ctx.t_dtype), None
 
 
+# fp64 recurrence blocks of basis families, by (device, spec bytes): a few
+# hundred bytes each, written once (ckan_write_recurrence_f64).
+_rec64 = {}
+_rec64_lock = threading.Lock()
+
+
+def _recurrence_f64(spec, device: torch.device) -> torch.Tensor:
+    key = (device, bytes(spec))
+    with _rec64_lock:
+        rec = _rec64.get(key)
+    if rec is None:
+        lib = _lib.load()
+        nbytes = lib.ckan_recurrence_bytes_f64(spec)
+        if nbytes == 0:
+            raise RuntimeError(f"kan_amd: basis degree {spec.degree} is outside the fp64 path's 0..256")
+        rec = torch.empty(nbytes // 8, dtype=torch.float64, device=device)
+        _lib.check(lib.ckan_write_recurrence_f64(spec, rec.data_ptr(), _lib.stream_ptr(device)))
+        with _rec64_lock:
+            _rec64[key] = rec
+    return rec
+
+
 class ChebyKANFunction64(torch.autograd.Function):
     """The layer in fp64 end to end (the reference's behaviour for fp64
-    parameters): x is taken as fp64, y, dx and dC are fp64."""
+    parameters): x is taken as fp64, y, dx and dC are fp64.  With a basis
+    ``spec`` the basis is that family's P_n(s tanh x), by its recurrence in
+    fp64 (the Jacobi and Hermite layers after .double())."""
 
     @staticmethod
-    def forward(ctx, x: torch.Tensor, coeffs: torch.Tensor):
+    def forward(ctx, x: torch.Tensor, coeffs: torch.Tensor, spec=None):
         _require_device(x, coeffs)
         if coeffs.dim() != 3:
             raise RuntimeError(f"coefficients must be [in, out, degree+1], got {tuple(coeffs.shape)}")
@@ -308,31 +332,41 @@ class ChebyKANFunction64(torch.autograd.Function):
         desc = _lib.make_desc(x64.shape[0], in_dim, out_dim, dd - 1, 0, 0)
         t = torch.empty(x64.shape[0], in_dim, dtype=torch.float64, device=dev)
         y = torch.empty(x64.shape[0], out_dim, dtype=torch.float64, device=dev)
-        _lib.check(lib.ckan_forward_f64(desc, x64.data_ptr(), c.data_ptr(), y.data_ptr(),
-                                        t.data_ptr(), _lib.stream_ptr(dev)))
-        ctx.save_for_backward(t, c)
+        rec = _recurrence_f64(spec, dev) if spec is not None else None
+        if rec is None:
+            _lib.check(lib.ckan_forward_f64(desc, x64.data_ptr(), c.data_ptr(), y.data_ptr(),
+                                            t.data_ptr(), _lib.stream_ptr(dev)))
+        else:
+            _lib.check(lib.ckan_forward_f64_basis(desc, rec.data_ptr(), x64.data_ptr(), c.data_ptr(),
+                                                  y.data_ptr(), t.data_ptr(), _lib.stream_ptr(dev)))
+        ctx.save_for_backward(t, c, rec)
         ctx.desc = desc
         ctx.x_dtype = x.dtype
         return y
 
     @staticmethod
     def backward(ctx, dy: torch.Tensor):
-        t, c = ctx.saved_tensors
+        t, c, rec = ctx.saved_tensors
         desc = ctx.desc
         need_dx, need_dc = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
         if not (need_dx or need_dc):
-            return None, None
+            return None, None, None
         lib = _lib.load()
         dev = dy.device
         dy64 = dy.contiguous() if dy.dtype == torch.float64 else dy.double().contiguous()
         dx = torch.empty(desc.batch, desc.in_dim, dtype=torch.float64, device=dev) if need_dx else None
         dc = (torch.empty(desc.in_dim, desc.out_dim, desc.degree + 1, dtype=torch.float64, device=dev)
               if need_dc else None)
-        _lib.check(lib.ckan_backward_f64(desc, t.data_ptr(), c.data_ptr(), dy64.data_ptr(),
-                                         _lib.ptr(dx), _lib.ptr(dc), 0, _lib.stream_ptr(dev)))
+        if rec is None:
+            _lib.check(lib.ckan_backward_f64(desc, t.data_ptr(), c.data_ptr(), dy64.data_ptr(),
+                                             _lib.ptr(dx), _lib.ptr(dc), 0, _lib.stream_ptr(dev)))
+        else:
+            _lib.check(lib.ckan_backward_f64_basis(desc, rec.data_ptr(), t.data_ptr(), c.data_ptr(),
+                                                   dy64.data_ptr(), _lib.ptr(dx), _lib.ptr(dc), 0,
+                                                   _lib.stream_ptr(dev)))
         if dx is not None and ctx.x_dtype != torch.float64:
             dx = dx.to(ctx.x_dtype)
-        return dx, dc
+        return dx, dc, None
 
 
 def chebykan(x: torch.Tensor, coeffs: torch.Tensor, compute: str = "fp32") -> torch.Tensor:
@@ -351,8 +385,10 @@ def family_kan(x: torch.Tensor, coeffs: torch.Tensor, spec, compute: str = "fp32
     """y = einsum('bid,iod->bo', P(s u), C) for the family of ``spec``, with
     u = tanh x, or u = affine[0] x + affine[1] when ``affine`` is given."""
     if coeffs.dtype == torch.float64:
-        raise RuntimeError("kan_amd: the fp64 path serves the Chebyshev layer; Jacobi / Hermite "
-                           "layers take float32 or bfloat16 coefficients")
+        if affine is not None:
+            raise RuntimeError("kan_amd: a Hermite layer with a finite domain (an affine input map) "
+                               "runs in float32 or bfloat16; its fp64 path takes the tanh map only")
+        return ChebyKANFunction64.apply(x, coeffs, spec)
     if not _needs_graph(x, coeffs):
         return _layer_forward(x, coeffs, compute, spec, affine, keep_t=False)[0]
     return ChebyKANFunction.apply(x, coeffs, compute, spec, affine)

@@ -262,3 +262,20 @@ def test_basis_helpers_and_network_stubs_mirror_reference():
         seq.visualize_network()
     with pytest.raises(NotImplementedError, match="Jacobian"):
         seq.jacobian(torch.zeros(1, 2))
+
+
+def test_f64_basis_entry_points_validate_before_launch():
+    """The fp64 family entry points: the recurrence block's size, NULL and
+    alignment checks, and the degree limit, all on the host."""
+    lib = _lib.load()
+    spec = _lib.make_spec(_lib.CKAN_BASIS_HERMITE, 8, 0.0, 0.0, 3.0)
+    assert lib.ckan_recurrence_bytes_f64(spec) == (3 * 9 + 2) * 8
+    assert lib.ckan_recurrence_bytes_f64(_lib.make_spec(_lib.CKAN_BASIS_HERMITE, 257, 0, 0, 3.0)) == 0
+    assert lib.ckan_write_recurrence_f64(spec, None, None) == _lib.CKAN_ERR_INVALID_ARG
+    assert lib.ckan_write_recurrence_f64(spec, 12, None) == _lib.CKAN_ERR_INVALID_ARG  # misaligned
+    bad = _lib.make_spec(_lib.CKAN_BASIS_JACOBI, 8, -1.5, 0.0, 1.0)
+    assert lib.ckan_write_recurrence_f64(bad, 256, None) == _lib.CKAN_ERR_INVALID_ARG
+    d = _lib.make_desc(8, 4, 3, 8, 0, 0)
+    assert lib.ckan_forward_f64_basis(d, None, 256, 256, 256, 256, None) == _lib.CKAN_ERR_INVALID_ARG
+    assert lib.ckan_backward_f64_basis(d, None, 256, 256, 256, 256, 256, 0, None) == \
+        _lib.CKAN_ERR_INVALID_ARG

@@ -74,3 +74,55 @@ def test_fp64_empty_batch_zeroes_grad():
     assert torch.count_nonzero(dc).item() == 0
     bad = _lib.make_desc(4, I, O, deg, 1, 0)  # bf16 compute makes no sense for fp64
     assert lib.ckan_forward_f64(bad, 16, 16, 16, 16, st) == _lib.CKAN_ERR_INVALID_ARG
+
+
+@pytest.mark.parametrize("family,deg,alpha,beta", [
+    ("jacobi", 8, 0.5, 0.5), ("jacobi", 12, -0.3, 1.2), ("jacobi", 20, 0.0, 0.0),
+    ("hermite", 8, 0.0, 0.0), ("hermite", 12, 0.0, 0.0), ("hermite_e", 10, 0.0, 0.0),
+])
+def test_fp64_family_layers_match_oracle(family, deg, alpha, beta):
+    """JacobiKANLayer / HermiteKANLayer after .double(): the reference computes
+    their bases in fp64 (kan/basis/jacobi.py:96-117, kan/basis/hermite.py:118-139).
+    y, dx and dC against the oracle's op-for-op restatement run in fp64 (the
+    reference's recurrences), and against the closed forms (power sums, whose
+    cancellation at these degrees costs a few more bits: 1e-10)."""
+    import kan_amd
+    from oracle import family_oracle as fo
+    print(f"fp64 family {family} deg={deg}", flush=True)
+    torch.manual_seed(11 + deg)
+    I, O, B = 40, 24, 90
+    if family == "jacobi":
+        layer = kan_amd.JacobiKANLayer(I, O, deg, alpha=alpha, beta=beta)
+    else:
+        layer = kan_amd.HermiteKANLayer(I, O, deg, scaling="physicist" if family == "hermite"
+                                        else "probabilist")
+    layer = layer.double()
+    c = layer.get_coefficients().detach().clone()
+    layer = layer.cuda()
+    g = torch.Generator().manual_seed(deg)
+    x = torch.randn(B, I, generator=g, dtype=torch.float64)
+    dy = torch.randn(B, O, generator=g, dtype=torch.float64)
+    xd = x.cuda().requires_grad_(True)
+    y = layer(xd)
+    assert y.dtype == torch.float64
+    y.backward(dy.cuda())
+    torch.cuda.synchronize()
+    dc = layer.get_coefficients().grad
+    y_ref, dx_ref, dc_ref = fo.family_forward_backward(x, c, dy, family, alpha, beta)
+    assert _rel(y, y_ref) <= FP64_TOL
+    assert _rel(xd.grad, dx_ref) <= FP64_TOL
+    assert _rel(dc, dc_ref) <= FP64_TOL
+    y_cf = fo.family_forward_fp64(x.numpy(), c.numpy(), family, alpha, beta)
+    dx_cf, dc_cf = fo.family_backward_fp64(x.numpy(), c.numpy(), dy.numpy(), family, alpha, beta)
+    assert _rel(y, torch.from_numpy(y_cf)) <= 1e-10
+    assert _rel(xd.grad, torch.from_numpy(dx_cf)) <= 1e-10
+    assert _rel(dc, torch.from_numpy(dc_cf)) <= 1e-10
+
+
+def test_fp64_finite_domain_hermite_raises():
+    """The affine input map of a finite-domain Hermite layer carries its scale
+    and shift in fp32 (ckan_desc), so the fp64 path refuses it clearly."""
+    import kan_amd
+    layer = kan_amd.HermiteKANLayer(6, 4, 5, domain=(-2.0, 3.0)).double().cuda()
+    with pytest.raises(RuntimeError, match="finite domain"):
+        layer(torch.randn(3, 6, dtype=torch.float64).cuda())
