@@ -342,6 +342,20 @@ typedef enum ckan_exec_flags {
 /* Allocates every device buffer; coefficients start at zero (set them with
  * ckan_exec_set_coeffs).  `stream` orders the initialisation. */
 int ckan_exec_create(const ckan_exec_config* cfg, ckan_exec** out, void* stream);
+/* ckan_exec_create for a KANSequential whose layers may be JacobiKANLayer
+ * (kan/layers/jacobikan.py:64-78) or HermiteKANLayer
+ * (kan/layers/hermitekan.py:68-82).  `bases` holds n_layers basis specs (host
+ * array; spec.degree must equal degrees[l]; a Chebyshev spec of scale 1 is the
+ * plain ChebyKAN layer), NULL for a stack of ChebyKAN layers.  `affine` (host
+ * array of 2 * n_layers floats, or NULL) gives layer l the input map
+ * t = affine[2l] * x + affine[2l+1] (CKAN_INPUT_AFFINE: the Hermite layer's
+ * finite domain) in place of tanh; (0, 0) keeps tanh.  A layer's
+ * coefficients (ckan_exec_set/get_coeffs, Adam state) are those of its own
+ * basis.  Family layers up to degree 16 train through the change of basis
+ * into Chebyshev coefficients (gradient mapped back by the transpose before
+ * the optimizer step); above it, on the vector-ALU recurrence. */
+int ckan_exec_create_basis(const ckan_exec_config* cfg, const struct ckan_basis_spec* bases,
+                           const float* affine, ckan_exec** out, void* stream);
 int ckan_exec_destroy(ckan_exec* ex);
 /* Device-to-device copy of one layer's fp32 master coefficients [in, out, D]. */
 int ckan_exec_set_coeffs(ckan_exec* ex, int32_t layer, const float* src, void* stream);

@@ -156,6 +156,8 @@ CKAN_OPT_ADAM = 1
 _pcfg = ctypes.POINTER(CkanExecConfig)
 SIGNATURES.update({
     "ckan_exec_create": (ctypes.c_int, [_pcfg, ctypes.POINTER(_vp), _vp]),
+    "ckan_exec_create_basis": (ctypes.c_int, [_pcfg, _pspec, ctypes.POINTER(_f32),
+                                              ctypes.POINTER(_vp), _vp]),
     "ckan_exec_destroy": (ctypes.c_int, [_vp]),
     "ckan_exec_set_coeffs": (ctypes.c_int, [_vp, _i32, _vp, _vp]),
     "ckan_exec_get_coeffs": (ctypes.c_int, [_vp, _i32, _vp, _vp]),

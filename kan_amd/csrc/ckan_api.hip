@@ -726,7 +726,7 @@ int ckan_coeff_grad_from_chebyshev(const ckan_desc* desc, const ckan_basis_spec*
     return fail(CKAN_ERR_INVALID_ARG, "in-place transform (dcheb == dcoeffs) cannot accumulate");
   const Plan p = plan_of(desc);
   ProfScope ps("coeff_from_cheb", s);
-  launch_coeff_from_cheb(dcheb, dcoeffs, p, accumulate != 0, xf, s);
+  launch_coeff_from_cheb(dcheb, dcoeffs, p, DcOut{accumulate ? kDcAccumulate : kDcStore}, xf, s);
   return check_launch("coeff_grad_from_chebyshev");
 }
 
@@ -1078,10 +1078,18 @@ int ckan::pack2_forward_tail_ce(const ckan_desc* da, const void* Ca, void* pka, 
 
 int ckan::pack_forward_ex(const ckan_desc* desc, const void* coeffs, void* packed, const float* x,
                           float* out, float* t_cache, void* ws, size_t ws_bytes, void* stream,
-                          bool t_ready, bool out_tanh) {
+                          bool t_ready, bool out_tanh, const ckan_basis_spec* spec) {
   if ((t_ready && !layer_reads_tcache(desc)) || (out_tanh && !layer_out_tanh_ok(desc)))
     return fail(CKAN_ERR_INVALID_ARG, "pack_forward_ex: the layer's forward path does not allow "
                 "a precomputed tanh cache / a tanh output");
-  return pack_forward_impl(desc, nullptr, coeffs, packed, x, out, t_cache, ws, ws_bytes, stream,
+  return pack_forward_impl(desc, spec, coeffs, packed, x, out, t_cache, ws, ws_bytes, stream,
                            t_ready, out_tanh);
+}
+
+bool ckan::layer_on_valu(const ckan_desc* desc) { return valu_route(desc); }
+
+int ckan::basis_check(const ckan_basis_spec* spec, int degree, BasisXform* xf) {
+  if (degree > kMfmaMaxDegree) return family_valid(spec, degree);
+  BasisXform tmp;
+  return family_xform(spec, degree, xf ? xf : &tmp);
 }

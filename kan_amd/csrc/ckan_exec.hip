@@ -487,6 +487,15 @@ struct ckan_exec {
     // with pack_pair on the last two layers of a cross-entropy stack: the
     // second layer's forward and the loss gradient run in one tail launch
     bool tail_ce = false;
+    // A Jacobi / Hermite layer (P_n(scale t) in place of T_n(t)).  Up to
+    // kMfmaMaxDegree its pack multiplies C by the change of basis M into
+    // Chebyshev coefficients C' = C M; its dC kernels then produce dC', and one
+    // more launch forms dC = dC' M^T and applies the optimizer step to C.
+    // Above it the vector-ALU backward differentiates in the family's basis
+    // and applies the step itself, as for a Chebyshev layer.
+    bool family = false;
+    ckan_basis_spec spec{};
+    BasisXform xf{};
   };
   ckan_exec_config cfg;
   std::vector<int32_t> widths, degrees;
@@ -496,6 +505,7 @@ struct ckan_exec {
   void* bws = nullptr;
   size_t bws_bytes = 0;
   float* loss_part = nullptr;  // max(kLossBlocks, B) partials
+  float* gcheb = nullptr;      // dC' of the family layers on the MFMA path
   float* loss = nullptr;
   int64_t* step = nullptr;     // Adam step count (device)
   float* adam_sc = nullptr;    // Adam scalars (device)
@@ -544,6 +554,8 @@ bool tiny_eligible(const ckan_exec* ex) {
   const auto& c = ex->cfg;
   if (c.flags & CKAN_EXEC_NO_FUSED_SMALL) return false;
   if (c.n_layers > kTinyMaxLayers) return false;
+  for (const auto& ly : ex->layers)  // the one-launch step: Chebyshev series of tanh(x) only
+    if (ly.family || ly.desc.input_map != CKAN_INPUT_TANH) return false;
   int64_t macs = 0;
   for (int l = 0; l < c.n_layers; ++l) {
     const int64_t io = (int64_t)ex->widths[l] * ex->widths[l + 1];
@@ -637,7 +649,8 @@ int run_step(ckan_exec* ex, const float* x, const void* target, hipStream_t s,
     const float* in = l == 0 ? x : ex->layers[l - 1].y;
     float* out = ly.tanh_out ? ex->layers[l + 1].t : ly.y;
     if ((rc = pack_forward_ex(&ly.desc, ly.C, ly.packed, t_ready ? nullptr : in, out, ly.t,
-                              ex->fws, ex->fws_bytes, s, t_ready, ly.tanh_out)))
+                              ex->fws, ex->fws_bytes, s, t_ready, ly.tanh_out,
+                              ly.family ? &ly.spec : nullptr)))
       return rc;
   }
   auto& last = ex->layers[L - 1];
@@ -689,8 +702,21 @@ int run_step(ckan_exec* ex, const float* x, const void* target, hipStream_t s,
       om = DcOut{kDcAdam, 0.0f, c.weight_decay, (float)(1.0 - (double)c.beta1), c.beta2,
                  (float)(1.0 - (double)c.beta2), c.eps, ly.C, ly.m, ly.v, ex->adam_sc};
     }
+    const LossMean* lm = tail && l == L - 1 ? &lm_tail : nullptr;
+    if (ly.family && !layer_on_valu(&ly.desc)) {
+      // dC' into gcheb, then dC = dC' M^T and the optimizer step into C
+      if ((rc = backward_impl(&ly.desc, ly.t, ly.packed, ly.dy, dx, ex->gcheb, DcOut{kDcStore},
+                              ex->bws, ex->bws_bytes, s, lm)))
+        return rc;
+      const Plan p = make_plan(c.batch, ly.desc.in_dim, ly.desc.out_dim, ly.desc.degree,
+                               c.compute == CKAN_COMPUTE_BF16);
+      launch_coeff_from_cheb(ex->gcheb, ly.C, p, om, ly.xf, s);
+      if (hipGetLastError() != hipSuccess)
+        return efail(CKAN_ERR_HIP, "executor: basis gradient launch failed");
+      continue;
+    }
     if ((rc = backward_impl(&ly.desc, ly.t, ly.packed, ly.dy, dx, ly.C, om, ex->bws,
-                            ex->bws_bytes, s, tail && l == L - 1 ? &lm_tail : nullptr)))
+                            ex->bws_bytes, s, lm)))
       return rc;
   }
   return CKAN_OK;
@@ -701,6 +727,11 @@ int run_step(ckan_exec* ex, const float* x, const void* target, hipStream_t s,
 extern "C" {
 
 int ckan_exec_create(const ckan_exec_config* cfg, ckan_exec** out, void* stream) {
+  return ckan_exec_create_basis(cfg, nullptr, nullptr, out, stream);
+}
+
+int ckan_exec_create_basis(const ckan_exec_config* cfg, const ckan_basis_spec* bases,
+                           const float* affine, ckan_exec** out, void* stream) {
   if (!cfg || !out) return efail(CKAN_ERR_INVALID_ARG, "executor: cfg/out is NULL");
   *out = nullptr;
   if (cfg->n_layers < 1 || !cfg->widths || !cfg->degrees)
@@ -722,16 +753,36 @@ int ckan_exec_create(const ckan_exec_config* cfg, ckan_exec** out, void* stream)
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   int rc = CKAN_OK;
   ex->layers.resize(cfg->n_layers);
+  int64_t gcheb_elems = 0;
   for (int l = 0; l < cfg->n_layers && rc == CKAN_OK; ++l) {
     auto& ly = ex->layers[l];
     ly.desc = ckan_desc{cfg->batch, ex->widths[l], ex->widths[l + 1], ex->degrees[l],
-                        cfg->compute, CKAN_DTYPE_F32, 0};
+                        cfg->compute, CKAN_DTYPE_F32, CKAN_INPUT_TANH};
+    if (affine && (affine[2 * l] != 0.0f || affine[2 * l + 1] != 0.0f)) {
+      ly.desc.input_map = CKAN_INPUT_AFFINE;
+      ly.desc.in_scale = affine[2 * l];
+      ly.desc.in_shift = affine[2 * l + 1];
+    }
     ly.packed_bytes = ckan_packed_bytes(&ly.desc);
     if (ly.packed_bytes == 0) {
-      rc = efail(CKAN_ERR_INVALID_ARG, "executor: invalid layer shape or degree");
+      rc = efail(CKAN_ERR_INVALID_ARG, "executor: invalid layer shape, degree or input map");
       break;
     }
+    if (bases) {
+      ly.spec = bases[l];
+      if (ly.spec.degree != ly.desc.degree) {
+        char msg[96];
+        snprintf(msg, sizeof msg, "executor: layer %d basis degree %d != layer degree %d", l,
+                 ly.spec.degree, ly.desc.degree);
+        rc = efail(CKAN_ERR_INVALID_ARG, msg);
+        break;
+      }
+      // a Chebyshev spec of scale 1 is the plain layer
+      ly.family = !(ly.spec.family == CKAN_BASIS_CHEBYSHEV && ly.spec.scale == 1.0);
+      if (ly.family && (rc = basis_check(&ly.spec, ly.desc.degree, &ly.xf))) break;
+    }
     ly.ncoef = (int64_t)ly.desc.in_dim * ly.desc.out_dim * (ly.desc.degree + 1);
+    if (ly.family && !layer_on_valu(&ly.desc) && ly.ncoef > gcheb_elems) gcheb_elems = ly.ncoef;
     const int64_t ny = cfg->batch * ly.desc.out_dim;
     if ((rc = dev_alloc(ex, (void**)&ly.C, ly.ncoef * 4)) ||
         (rc = dev_alloc(ex, &ly.packed, ly.packed_bytes)) ||
@@ -754,10 +805,14 @@ int ckan_exec_create(const ckan_exec_config* cfg, ckan_exec** out, void* stream)
   }
   for (int l = 0; rc == CKAN_OK && l + 1 < cfg->n_layers; ++l)
     ex->layers[l].tanh_out = layer_out_tanh_ok(&ex->layers[l].desc) &&
+                             ex->layers[l + 1].desc.input_map == CKAN_INPUT_TANH &&
                              layer_reads_tcache(&ex->layers[l + 1].desc);
   for (int l = 0; rc == CKAN_OK && l + 1 < cfg->n_layers; ++l) {
     auto& ly = ex->layers[l];
-    ly.pack_pair = ly.tanh_out && pack_pair_fits(&ly.desc, &ex->layers[l + 1].desc);
+    // the paired launch packs Chebyshev coefficients and maps x by tanh
+    ly.pack_pair = ly.tanh_out && !ly.family && !ex->layers[l + 1].family &&
+                   ly.desc.input_map == CKAN_INPUT_TANH &&
+                   pack_pair_fits(&ly.desc, &ex->layers[l + 1].desc);
     ly.tail_ce = ly.pack_pair && l + 2 == cfg->n_layers && cfg->loss == CKAN_LOSS_CE &&
                  pack2_tail_ce_fits(&ly.desc, &ex->layers[l + 1].desc);
     if (ly.pack_pair) ++l;  // the next layer's pack is taken
@@ -771,7 +826,8 @@ int ckan_exec_create(const ckan_exec_config* cfg, ckan_exec** out, void* stream)
         !(rc = dev_alloc(ex, (void**)&ex->loss_part, nloss * 4)) &&
         !(rc = dev_alloc(ex, (void**)&ex->loss, 256)) &&
         !(rc = dev_alloc(ex, (void**)&ex->step, 256)) &&
-        !(rc = dev_alloc(ex, (void**)&ex->adam_sc, 256))) {
+        !(rc = dev_alloc(ex, (void**)&ex->adam_sc, 256)) &&
+        !(rc = gcheb_elems ? dev_alloc(ex, (void**)&ex->gcheb, gcheb_elems * 4) : CKAN_OK)) {
       if (ex->fws_bytes) launch_zero(ex->fws, ex->fws_bytes, s);
       launch_zero(ex->step, 256, s);
     }
@@ -988,8 +1044,8 @@ int ckan_exec_forward(ckan_exec* ex, const float* x, float* y, void* stream) {
     auto& ly = ex->layers[l];
     const float* in = l == 0 ? x : ex->layers[l - 1].y;
     float* out = l == L - 1 ? y : ly.y;
-    if ((rc = ckan_pack_forward(&ly.desc, nullptr, ly.C, ly.packed, in, out, ly.t, ex->fws,
-                                ex->fws_bytes, s)))
+    if ((rc = ckan_pack_forward(&ly.desc, ly.family ? &ly.spec : nullptr, ly.C, ly.packed, in,
+                                out, ly.t, ex->fws, ex->fws_bytes, s)))
       return rc;
   }
   return CKAN_OK;

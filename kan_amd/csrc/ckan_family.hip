@@ -251,14 +251,16 @@ k_jacobian(const float* __restrict__ x, const float* __restrict__ c1t, float* __
   }
 }
 
-// dc[q, n] (+)= sum_{k <= n} dcheb[q, k] m[n][k] over rows q of D values.
-// A block takes 256 consecutive rows: one contiguous run of 256 * D floats,
-// moved with float4 accesses when aligned and staged in LDS (odd D: the
-// per-row reads hit distinct banks).  Every load of a block precedes its
-// stores and blocks own disjoint rows, so dcheb may alias dc.
+// g[q, n] = sum_{k <= n} dcheb[q, k] m[n][k] over rows q of D values, written
+// into dc by om (stored, accumulated, or applied as an SGD / Adam step with dc
+// the parameter and om.base == dc).  A block takes 256 consecutive rows: one
+// contiguous run of 256 * D floats, moved with float4 accesses when aligned
+// and staged in LDS (odd D: the per-row reads hit distinct banks).  Every
+// load of a block precedes its stores and blocks own disjoint rows, so dcheb
+// may alias dc.
 template <int DM>
 __global__ void __launch_bounds__(256)
-k_coeff_from_cheb(const float* dcheb, float* dc, int64_t rows, int D, int accumulate, int vec,
+k_coeff_from_cheb(const float* dcheb, float* dc, int64_t rows, int D, DcOut om, int vec,
                   BasisXform xf) {
   __shared__ __attribute__((aligned(16))) float tile[256 * DM];
   const int tid = threadIdx.x;
@@ -289,16 +291,10 @@ k_coeff_from_cheb(const float* dcheb, float* dc, int64_t rows, int D, int accumu
   }
   __syncthreads();
   if (v4) {
-    for (int k = tid; k < n / 4; k += 256) {
-      f32x4_t r = reinterpret_cast<const f32x4_t*>(tile)[k];
-      if (accumulate) {
-        const f32x4_t o = reinterpret_cast<const f32x4_t*>(dst)[k];
-        r = f32x4_t{o[0] + r[0], o[1] + r[1], o[2] + r[2], o[3] + r[3]};
-      }
-      reinterpret_cast<f32x4_t*>(dst)[k] = r;
-    }
+    for (int k = tid; k < n / 4; k += 256)
+      dc_write4(reinterpret_cast<f32x4_t*>(dst) + k, reinterpret_cast<const f32x4_t*>(tile)[k], om);
   } else {
-    for (int k = tid; k < n; k += 256) dst[k] = accumulate ? dst[k] + tile[k] : tile[k];
+    for (int k = tid; k < n; k += 256) dc_write(dst + k, tile[k], om);
   }
 }
 
@@ -375,17 +371,16 @@ static unsigned grid_of(int64_t work) {
   return (unsigned)g;
 }
 
-void launch_coeff_from_cheb(const float* dcheb, float* dc, const Plan& p, bool accumulate,
+void launch_coeff_from_cheb(const float* dcheb, float* dc, const Plan& p, const DcOut& om,
                             const BasisXform& xf, hipStream_t s) {
   const int64_t rows = (int64_t)p.I * p.O;
   const dim3 g((unsigned)((rows + 255) / 256));
   const int vec = is_al16(dcheb) && is_al16(dc);
-  const int acc = accumulate ? 1 : 0;
   switch (p.P) {
-    case 2: hipLaunchKernelGGL((k_coeff_from_cheb<3>), g, dim3(256), 0, s, dcheb, dc, rows, p.D, acc, vec, xf); break;
-    case 4: hipLaunchKernelGGL((k_coeff_from_cheb<5>), g, dim3(256), 0, s, dcheb, dc, rows, p.D, acc, vec, xf); break;
-    case 8: hipLaunchKernelGGL((k_coeff_from_cheb<9>), g, dim3(256), 0, s, dcheb, dc, rows, p.D, acc, vec, xf); break;
-    default: hipLaunchKernelGGL((k_coeff_from_cheb<17>), g, dim3(256), 0, s, dcheb, dc, rows, p.D, acc, vec, xf); break;
+    case 2: hipLaunchKernelGGL((k_coeff_from_cheb<3>), g, dim3(256), 0, s, dcheb, dc, rows, p.D, om, vec, xf); break;
+    case 4: hipLaunchKernelGGL((k_coeff_from_cheb<5>), g, dim3(256), 0, s, dcheb, dc, rows, p.D, om, vec, xf); break;
+    case 8: hipLaunchKernelGGL((k_coeff_from_cheb<9>), g, dim3(256), 0, s, dcheb, dc, rows, p.D, om, vec, xf); break;
+    default: hipLaunchKernelGGL((k_coeff_from_cheb<17>), g, dim3(256), 0, s, dcheb, dc, rows, p.D, om, vec, xf); break;
   }
 }
 

@@ -85,8 +85,10 @@ __host__ __device__ bool recur_coef(int family, int n, double alpha, double beta
 // M[n * (degree + 1) + k] with P_n(scale u) = sum_k M[n, k] T_k(u) (exact, fp64).
 void family_to_chebyshev(const double* a, const double* b, const double* c, int degree,
                          double scale, double* M);
-// dc[q, n] (+)= sum_k dcheb[q, k] m[n][k] over the I*O rows q; dcheb may be dc.
-void launch_coeff_from_cheb(const float* dcheb, float* dc, const Plan& p, bool accumulate,
+// g[q, n] = sum_k dcheb[q, k] m[n][k] over the I*O rows q, written into dc
+// by om (store, accumulate, or an SGD / Adam step on the parameter dc with
+// om.base == dc); dcheb may be dc.
+void launch_coeff_from_cheb(const float* dcheb, float* dc, const Plan& p, const DcOut& om,
                             const BasisXform& xf, hipStream_t s);
 // out[q, n] = P_n(t[q]) (n <= deg <= kValuMaxDegree) and its backward; the
 // recurrence coefficients are formed on the device (recur_coef).
@@ -228,9 +230,18 @@ int backward_impl(const struct ckan_desc* desc, const float* t_cache, const void
 // tanh cache already holds the layer's input map (x unused; the layer's
 // forward must read the cache); out_tanh, store tanh(y) into `out` (the next
 // layer's tanh cache) in place of y (needs fwd_out_tanh_ok).
+// spec: the layer's basis (nullptr: Chebyshev), as in ckan_pack_forward.
 int pack_forward_ex(const struct ckan_desc* desc, const void* coeffs, void* packed,
                     const float* x, float* out, float* t_cache, void* ws, size_t ws_bytes,
-                    void* stream, bool t_ready, bool out_tanh);
+                    void* stream, bool t_ready, bool out_tanh,
+                    const struct ckan_basis_spec* spec = nullptr);
+// Whether the layer runs on the vector-ALU path (degree > kMfmaMaxDegree),
+// whose backward differentiates in the layer's own basis.
+bool layer_on_valu(const struct ckan_desc* desc);
+// Validates a basis spec for a layer of degree `degree`; on the MFMA path
+// (degree <= kMfmaMaxDegree) also forms its change of basis into *xf (when
+// xf is given).  Sets the last error on failure.
+int basis_check(const struct ckan_basis_spec* spec, int degree, BasisXform* xf);
 // Whether the layer of desc can take t_ready / out_tanh in pack_forward_ex.
 bool layer_reads_tcache(const struct ckan_desc* desc);
 bool layer_out_tanh_ok(const struct ckan_desc* desc);

@@ -1,7 +1,7 @@
 """Resident multi-layer executor over the C-ABI (ckan_exec_*).
 
-Trains a KANSequential of ChebyKAN layers (kan/layers/base.py:144-166) in place
-on one GPU: the library owns fp32 master coefficients, packed operands,
+Trains a KANSequential of ChebyKAN, Jacobi and Hermite layers
+(kan/layers/base.py:144-166) in place on one GPU: the library owns fp32 master coefficients, packed operands,
 activations, tanh caches, gradients and optimizer state, and one ``step`` runs
 forward, the loss and its gradient, backward and the optimizer for every
 layer -- one iteration of the reference training loop (README.md:61-69).
@@ -10,29 +10,33 @@ from __future__ import annotations
 
 import ctypes
 import weakref
-from typing import List, Optional, Sequence
+from typing import Optional, Sequence
 
 import torch
 
 from . import _lib
 from .functional import compute_code
-from .layers import ChebyKANLayer, KANSequential
+from .layers import ChebyKANLayer, HermiteKANLayer, JacobiKANLayer, KANSequential
 
 _LOSS = {"mse": _lib.CKAN_LOSS_MSE, "ce": _lib.CKAN_LOSS_CE, "cross_entropy": _lib.CKAN_LOSS_CE}
 _OPT = {"sgd": _lib.CKAN_OPT_SGD, "adam": _lib.CKAN_OPT_ADAM}
 
 
-def check_sequential(model: KANSequential) -> List[ChebyKANLayer]:
-    """The ChebyKAN layers of ``model`` in order; ValueError when a module is
-    not a ChebyKANLayer (an activation, a Jacobi or Hermite layer) or when the
-    widths do not chain (layer l's input_dim != layer l-1's output_dim)."""
+_LAYER_TYPES = (ChebyKANLayer, JacobiKANLayer, HermiteKANLayer)
+
+
+def check_sequential(model: KANSequential) -> list:
+    """The KAN layers of ``model`` in order; ValueError when a module is not a
+    ChebyKANLayer, JacobiKANLayer or HermiteKANLayer (an activation, a spline
+    layer) or when the widths do not chain (layer l's input_dim != layer
+    l-1's output_dim)."""
     layers = list(model)
     if not layers:
         raise ValueError("the model has no layers")
     for l, m in enumerate(layers):
-        if type(m) is not ChebyKANLayer:
-            raise ValueError(f"module {l} ({type(m).__name__}) is not a ChebyKANLayer: the "
-                             "resident executor runs stacks of ChebyKAN layers only")
+        if type(m) not in _LAYER_TYPES:
+            raise ValueError(f"module {l} ({type(m).__name__}) is not a ChebyKAN, Jacobi or "
+                             "Hermite layer: the resident executor runs stacks of those only")
         if l and m.input_dim != layers[l - 1].output_dim:
             raise ValueError(f"layer {l} takes {m.input_dim} inputs but layer {l - 1} "
                              f"produces {layers[l - 1].output_dim}")
@@ -66,14 +70,31 @@ def check_labels(labels: torch.Tensor, n_classes: int) -> None:
         raise ValueError(f"labels must lie in [0, {n_classes}), found values in [{lo}, {hi}]")
 
 
+def layer_basis(m):
+    """(basis spec or None, affine (scale, shift) or None) of a KAN layer: the
+    spec of a Jacobi / Hermite layer's basis, and the finite-domain map of a
+    Hermite layer that has one (None: the tanh map)."""
+    if type(m) is ChebyKANLayer:
+        return None, None
+    b = m.basis_function
+    affine = b._affine() if hasattr(b, "_affine") else None
+    return b.spec(), affine
+
+
 class ResidentExecutor:
-    """A resident ChebyKAN stack: ``widths`` has n_layers + 1 entries."""
+    """A resident KAN stack: ``widths`` has n_layers + 1 entries.
+
+    ``bases``: per layer, a basis spec (``_lib.make_spec``; None for a
+    ChebyKAN layer), or None for an all-ChebyKAN stack.  ``affine``: per
+    layer, (scale, shift) of the input map t = scale * x + shift, or None for
+    tanh (the Hermite layer's finite domain)."""
 
     def __init__(self, widths: Sequence[int], degrees: Sequence[int], batch: int,
                  compute: str = "bf16", loss: str = "mse", optimizer: str = "sgd",
                  lr: float = 0.01, betas=(0.9, 0.999), eps: float = 1e-8,
                  weight_decay: float = 0.0, use_graph: bool = False, fused_small: bool = True,
-                 device="cuda"):
+                 device="cuda", bases: Optional[Sequence] = None,
+                 affine: Optional[Sequence] = None):
         self.device = torch.device(device)
         if self.device.type != "cuda":
             raise RuntimeError("ResidentExecutor runs only on a ROCm device")
@@ -96,10 +117,26 @@ class ResidentExecutor:
             _LOSS[loss], _OPT[optimizer], 1 if use_graph else 0, float(lr), float(betas[0]),
             float(betas[1]), float(eps), float(weight_decay),
             0 if fused_small else _lib.CKAN_EXEC_NO_FUSED_SMALL)
+        n = len(self.degrees)
+        specs = aff = None
+        if bases is not None:
+            if len(bases) != n:
+                raise ValueError("bases must have one entry per layer")
+            specs = (_lib.CkanBasisSpec * n)(*[
+                b if b is not None else _lib.make_spec(_lib.CKAN_BASIS_CHEBYSHEV, d)
+                for b, d in zip(bases, self.degrees)])
+        if affine is not None:
+            if len(affine) != n:
+                raise ValueError("affine must have one entry per layer")
+            flat = []
+            for a in affine:
+                flat += [0.0, 0.0] if a is None else [float(a[0]), float(a[1])]
+            aff = (ctypes.c_float * (2 * n))(*flat)
+        self._specs, self._aff = specs, aff
         handle = ctypes.c_void_p()
         with torch.cuda.device(self.device):
-            _lib.check(self._lib.ckan_exec_create(ctypes.byref(cfg), ctypes.byref(handle),
-                                                  self._stream()))
+            _lib.check(self._lib.ckan_exec_create_basis(ctypes.byref(cfg), specs, aff,
+                                                        ctypes.byref(handle), self._stream()))
         self._h = handle
         self._loss = torch.empty((), dtype=torch.float32, device=self.device)
         self._labels_checked = None  # (weakref to the last labels checked, their _version)
@@ -114,16 +151,21 @@ class ResidentExecutor:
     def from_sequential(cls, model: KANSequential, batch: int, **kw) -> "ResidentExecutor":
         """An executor over ``model``'s layers with their current coefficients.
 
-        The executor's kernels run ChebyKAN layers back to back, each layer's
+        The executor's kernels run KAN layers back to back, each layer's
         output feeding the next (kan/layers/base.py:144-166), so every module
-        of ``model`` must be a ChebyKANLayer and each layer's input_dim must
-        equal the previous layer's output_dim; anything else raises ValueError
-        before any device work."""
+        of ``model`` must be a ChebyKANLayer, JacobiKANLayer or
+        HermiteKANLayer and each layer's input_dim must equal the previous
+        layer's output_dim; anything else raises ValueError before any device
+        work."""
         layers = check_sequential(model)
         widths = [layers[0].input_dim] + [m.output_dim for m in layers]
+        per = [layer_basis(m) for m in layers]
+        if any(b is not None or a is not None for b, a in per):
+            kw.setdefault("bases", [b for b, _ in per])
+            kw.setdefault("affine", [a for _, a in per])
         ex = cls(widths, [m.degree for m in layers], batch, **kw)
         for l, m in enumerate(layers):
-            ex.set_coeffs(l, m.cheby_coeffs.detach())
+            ex.set_coeffs(l, m.get_coefficients().detach())
         return ex
 
     def set_coeffs(self, layer: int, coeffs: torch.Tensor) -> None:

@@ -160,29 +160,36 @@ def round_bf16_ste(c: torch.Tensor) -> torch.Tensor:
 
 
 def mlp_forward(x: torch.Tensor, coeff_list, use_recurrence: bool = False,
-                bf16_coeffs: bool = False) -> torch.Tensor:
+                bf16_coeffs: bool = False, layer_fns=None) -> torch.Tensor:
     """A stack of ChebyKAN layers as in KANSequential (kan/layers/base.py:144-153).
 
     ``bf16_coeffs`` evaluates each layer with its coefficients rounded to
     bf16 (the bf16-compute case; the reference itself cannot run bf16
-    coefficients, so its fp32 math on the rounded operands is the check)."""
+    coefficients, so its fp32 math on the rounded operands is the check).
+    ``layer_fns``: per layer, a function (h, coeffs) -> output standing in
+    for another layer type (a Jacobi / Hermite layer of family_oracle), or
+    None for the ChebyKAN layer."""
     h = x
-    for c in coeff_list:
-        h = layer_forward(h, round_bf16_ste(c) if bf16_coeffs else c, use_recurrence)
+    for l, c in enumerate(coeff_list):
+        fn = layer_fns[l] if layer_fns is not None else None
+        if fn is not None:
+            h = fn(h, c)
+        else:
+            h = layer_forward(h, round_bf16_ste(c) if bf16_coeffs else c, use_recurrence)
     return h
 
 
 def train_steps(x: torch.Tensor, target: torch.Tensor, coeff_list, steps: int,
                 loss: str = "mse", optimizer: str = "adam", lr: float = 0.01,
                 weight_decay: float = 0.0, eps: float = 1e-8, bf16_coeffs: bool = False,
-                return_state: bool = False):
+                return_state: bool = False, layer_fns=None):
     """The reference training loop (README.md:55-69) on the restatement.
 
     zero_grad -> forward -> loss (MSELoss / CrossEntropyLoss, mean reduction)
     -> backward -> torch.optim.Adam / SGD step, ``steps`` times.
     Returns (final coefficient list, list of per-step losses), plus the
     optimizer's per-parameter state list (exp_avg, exp_avg_sq, step for
-    Adam) when ``return_state``.
+    Adam) when ``return_state``.  ``layer_fns`` as in mlp_forward.
     """
     params = [c.detach().clone().requires_grad_(True) for c in coeff_list]
     if optimizer == "adam":
@@ -192,7 +199,7 @@ def train_steps(x: torch.Tensor, target: torch.Tensor, coeff_list, steps: int,
     losses = []
     for _ in range(steps):
         opt.zero_grad()
-        out = mlp_forward(x, params, bf16_coeffs=bf16_coeffs)
+        out = mlp_forward(x, params, bf16_coeffs=bf16_coeffs, layer_fns=layer_fns)
         if loss == "mse":
             l = F.mse_loss(out, target)
         else:

@@ -279,3 +279,30 @@ def test_f64_basis_entry_points_validate_before_launch():
     assert lib.ckan_forward_f64_basis(d, None, 256, 256, 256, 256, None) == _lib.CKAN_ERR_INVALID_ARG
     assert lib.ckan_backward_f64_basis(d, None, 256, 256, 256, 256, 256, 0, None) == \
         _lib.CKAN_ERR_INVALID_ARG
+
+
+def test_exec_create_basis_validates_before_allocating():
+    """ckan_exec_create_basis: a spec whose degree differs from the layer's,
+    an invalid family parameter or an invalid affine map on the first layer
+    returns before the first device allocation."""
+    lib = _lib.load()
+    w = (ctypes.c_int32 * 3)(6, 5, 3)
+    d = (ctypes.c_int32 * 2)(4, 3)
+    cfg = _lib.CkanExecConfig(2, w, d, 16, 0, _lib.CKAN_LOSS_MSE, _lib.CKAN_OPT_SGD, 0, 0.01,
+                              0.9, 0.999, 1e-8, 0.0, 0)
+    h = ctypes.c_void_p()
+
+    def create(specs, aff=None):
+        arr = (_lib.CkanBasisSpec * 2)(*specs)
+        return lib.ckan_exec_create_basis(ctypes.byref(cfg), arr, aff, ctypes.byref(h), None)
+
+    cheb3 = _lib.make_spec(_lib.CKAN_BASIS_CHEBYSHEV, 3)
+    assert create([_lib.make_spec(_lib.CKAN_BASIS_JACOBI, 5), cheb3]) == _lib.CKAN_ERR_INVALID_ARG
+    assert b"basis degree 5 != layer degree 4" in lib.ckan_last_error()
+    assert create([_lib.make_spec(_lib.CKAN_BASIS_JACOBI, 4, -1.5, 0.0), cheb3]) == \
+        _lib.CKAN_ERR_INVALID_ARG
+    assert b"alpha" in lib.ckan_last_error()
+    aff = (ctypes.c_float * 4)(0.0, 0.5, 0.0, 0.0)  # scale 0 with a shift: no input map
+    assert create([_lib.make_spec(_lib.CKAN_BASIS_HERMITE, 4, 0, 0, 3.0), cheb3], aff) == \
+        _lib.CKAN_ERR_INVALID_ARG
+    assert not h.value

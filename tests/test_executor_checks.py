@@ -9,7 +9,8 @@ import pytest
 import torch
 import torch.nn as nn
 
-from kan_amd import ChebyKANLayer, JacobiKANLayer, KANSequential
+from kan_amd import ChebyKANLayer, HermiteKANLayer, JacobiKANLayer, KANSequential
+from kan_amd import _lib
 from kan_amd import executor as exm
 
 
@@ -113,11 +114,37 @@ def test_from_sequential_rejects_other_modules():
     with pytest.raises(ValueError, match="Tanh"):
         exm.ResidentExecutor.from_sequential(
             KANSequential(ChebyKANLayer(6, 5, 2), nn.Tanh(), ChebyKANLayer(5, 3, 2)), batch=4)
-    with pytest.raises(ValueError, match="JacobiKANLayer"):
+    with pytest.raises(ValueError, match="Linear"):
         exm.ResidentExecutor.from_sequential(
-            KANSequential(ChebyKANLayer(6, 5, 2), JacobiKANLayer(5, 3, 2)), batch=4)
+            KANSequential(ChebyKANLayer(6, 5, 2), nn.Linear(5, 3)), batch=4)
+    mixed = KANSequential(ChebyKANLayer(6, 5, 2), JacobiKANLayer(5, 4, 3),
+                          HermiteKANLayer(4, 3, 2))
+    assert [m.output_dim for m in exm.check_sequential(mixed)] == [5, 4, 3]
     with pytest.raises(ValueError, match="takes 4 inputs"):
         exm.ResidentExecutor.from_sequential(
             KANSequential(ChebyKANLayer(6, 5, 2), ChebyKANLayer(4, 3, 2)), batch=4)
     with pytest.raises(ValueError, match="no layers"):
         exm.ResidentExecutor.from_sequential(KANSequential(), batch=4)
+
+
+def test_layer_basis_specs_and_input_maps():
+    """The per-layer basis handed to ckan_exec_create_basis: None for
+    ChebyKAN; the family, parameters and scale of a Jacobi / Hermite layer;
+    the finite-domain affine map (scale, shift) of a Hermite layer that has
+    one, u = 2 (x - lo) / (hi - lo) - 1 (the basis then runs at scale 3)."""
+    assert exm.layer_basis(ChebyKANLayer(3, 2, 4)) == (None, None)
+    spec, aff = exm.layer_basis(JacobiKANLayer(3, 2, 5, alpha=0.5, beta=-0.25))
+    assert (spec.family, spec.degree, spec.alpha, spec.beta, spec.scale) == (
+        _lib.CKAN_BASIS_JACOBI, 5, 0.5, -0.25, 1.0)
+    assert aff is None
+    spec, aff = exm.layer_basis(HermiteKANLayer(3, 2, 6, scaling="probabilist"))
+    assert (spec.family, spec.degree, spec.scale) == (_lib.CKAN_BASIS_HERMITE_E, 6, 3.0)
+    assert aff is None
+    spec, aff = exm.layer_basis(HermiteKANLayer(3, 2, 6, domain=(-2.0, 6.0)))
+    assert spec.family == _lib.CKAN_BASIS_HERMITE
+    a, b = aff
+    for x in (-2.0, 6.0, 1.0):  # 3 (a x + b) is the reference's 6 (x - lo) / (hi - lo) - 3
+        assert abs(3 * (a * x + b) - (6.0 / 8.0 * (x + 2.0) - 3.0)) < 1e-12
+    # an infinite domain (or normalize_domain=False) keeps 3 tanh(x)
+    assert exm.layer_basis(HermiteKANLayer(3, 2, 6, domain=(-2.0, 6.0),
+                                           normalize_domain=False))[1] is None

@@ -431,3 +431,123 @@ def test_hidden_layers_store_tanh_into_the_next_cache():
     assert abs(l1 - mse1) <= 1e-6 * mse1, (l1, mse1)
     assert l1 < l0
     ex.close()
+
+
+# ---- Jacobi / Hermite layers in the executor ---------------------------------
+
+def _family_stack(kinds, widths, seed):
+    """The package modules of a mixed stack, their coefficients (the oracle's
+    init, times the kind's scale) and the oracle's per-layer forward
+    functions.  kinds: ("cheb", deg) | ("jacobi", deg, alpha, beta) |
+    ("hermite", deg, scaling, domain, init_mult)."""
+    from oracle import family_oracle as fam
+    from kan_amd import ChebyKANLayer, HermiteKANLayer, JacobiKANLayer, KANSequential
+    torch.manual_seed(seed)
+    mods, fns = [], []
+    for l, k in enumerate(kinds):
+        i, o, d = widths[l], widths[l + 1], k[1]
+        mult = 1.0
+        if k[0] == "cheb":
+            m, fn = ChebyKANLayer(i, o, d), None
+        elif k[0] == "jacobi":
+            a, b = k[2], k[3]
+            m = JacobiKANLayer(i, o, d, alpha=a, beta=b)
+            fn = (lambda a, b: lambda h, c: fam.family_forward(h, c, "jacobi", a, b))(a, b)
+        else:
+            scaling, dom, mult = k[2], k[3], k[4]
+            m = HermiteKANLayer(i, o, d, scaling=scaling, domain=dom)
+            name = "hermite" if scaling == "physicist" else "hermite_e"
+            fn = (lambda name, dom: lambda h, c: fam.family_forward(h, c, name, domain=dom))(name, dom)
+        with torch.no_grad():
+            m.get_coefficients().copy_(orc.init_coeffs(i, o, d) * mult)
+        mods.append(m)
+        fns.append(fn)
+    return KANSequential(*mods), fns
+
+
+# Stacks whose fp32 oracle trajectory agrees with its fp64 run to 1e-5 over
+# the steps taken, so that the bound below tests the kernels and not the
+# conditioning: the Hermite layers' H_n(3 t) reach thousands, which (at the
+# reference's init scale) saturates the next tanh, where the reference's
+# closed-form Chebyshev backward is 0 * inf in fp32.  Inputs lie inside the
+# finite domain of a Hermite layer that has one.
+FAMILY_STACKS = [
+    # MFMA path: Jacobi and Hermite (3 tanh) through the change of basis
+    ([20, 16, 12, 6], [("jacobi", 4, 0.5, -0.3), ("hermite", 5, "physicist", None, 0.01),
+                       ("cheb", 3)], None),
+    # a finite-domain Hermite first layer (affine map), He_n, and a Jacobi
+    # layer above degree 16 (vector-ALU recurrence, optimizer fused)
+    ([10, 14, 8, 5], [("hermite", 4, "physicist", (-2.0, 2.0), 0.02),
+                      ("hermite", 3, "probabilist", None, 0.2), ("jacobi", 20, 1.0, 1.0)],
+     (-2.0, 2.0)),
+]
+
+
+def _family_inputs(widths, x_range, loss, B, seed):
+    g = torch.Generator().manual_seed(seed)
+    if x_range is None:
+        x = torch.randn(B, widths[0], generator=g)
+    else:
+        x = x_range[0] + (x_range[1] - x_range[0]) * torch.rand(B, widths[0], generator=g)
+    if loss == "mse":
+        tgt = torch.randn(B, widths[-1], generator=g) * 0.2
+    else:
+        tgt = torch.randint(0, widths[-1], (B,), generator=g)
+    return x, tgt
+
+
+@pytest.mark.parametrize("widths,kinds,x_range", FAMILY_STACKS)
+@pytest.mark.parametrize("loss,opt", [("mse", "sgd"), ("ce", "adam")])
+def test_family_stack_training_matches_oracle(widths, kinds, x_range, loss, opt):
+    from kan_amd import ResidentExecutor
+    print(f"executor family stack {kinds} loss={loss} opt={opt}", flush=True)
+    B, steps, lr = 200, 4, (0.02 if opt == "sgd" else 0.002)
+    model, fns = _family_stack(kinds, widths, 31)
+    x, tgt = _family_inputs(widths, x_range, loss, B, 32)
+    coeffs = [m.get_coefficients().detach().clone() for m in model]
+    ex = ResidentExecutor.from_sequential(model, B, compute="fp32", loss=loss, optimizer=opt, lr=lr)
+    xd, td = x.cuda(), tgt.cuda()
+    losses = [ex.step(xd, td).item() for _ in range(steps)]
+    c_ref, l_ref = orc.train_steps(x, tgt, coeffs, steps=steps, loss=loss, optimizer=opt, lr=lr,
+                                   layer_fns=fns)
+    for a, b in zip(losses, l_ref):
+        assert abs(a - b) <= 1e-4 * abs(b) + 1e-6, (losses, l_ref)
+    for l in range(len(kinds)):
+        assert _rel(ex.get_coeffs(l), c_ref[l]) <= 1e-4, l
+    # the trained stack's forward is the modules' forward on the trained coefficients
+    y = ex.forward(xd)
+    y_ref = orc.mlp_forward(x, c_ref, layer_fns=fns)
+    assert _rel(y, y_ref) <= 1e-4
+    ex.close()
+
+
+def test_family_stack_bf16_and_graph_replay():
+    """bf16 compute (C' = C M rounded to bf16) against the fp32 oracle at the
+    bf16 bound, and graph replays bit-identical to the plain step sequence
+    (SGD: Adam's first steps move every coefficient by about lr whatever the
+    gradient's size, which turns bf16 rounding of near-zero gradients into
+    sign flips that no bound on relative error covers)."""
+    from kan_amd import ResidentExecutor
+    widths, kinds, x_range = FAMILY_STACKS[0]
+    print("executor family stack bf16 + graph", flush=True)
+    B, steps, lr = 256, 3, 0.02
+    model, fns = _family_stack(kinds, widths, 41)
+    x, tgt = _family_inputs(widths, x_range, "mse", B, 42)
+    coeffs = [m.get_coefficients().detach().clone() for m in model]
+    runs = []
+    for use_graph in (False, True):
+        ex = ResidentExecutor.from_sequential(model, B, compute="bf16", loss="mse",
+                                              optimizer="sgd", lr=lr, use_graph=use_graph)
+        xd, td = x.cuda(), tgt.cuda()
+        ls = [ex.step(xd, td).item() for _ in range(steps)]
+        runs.append((ls, [ex.get_coeffs(l).cpu() for l in range(len(kinds))]))
+        ex.close()
+    assert runs[0][0] == runs[1][0]
+    for a, b in zip(runs[0][1], runs[1][1]):
+        assert torch.equal(a, b)
+    c_ref, l_ref = orc.train_steps(x, tgt, coeffs, steps=steps, loss="mse", optimizer="sgd",
+                                   lr=lr, layer_fns=fns)
+    for a, b in zip(runs[0][0], l_ref):
+        assert abs(a - b) <= 3e-2 * abs(b)
+    for l in range(len(kinds)):
+        assert _rel(runs[0][1][l], c_ref[l]) <= 3e-2
