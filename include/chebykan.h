@@ -249,15 +249,18 @@ int ckan_family_basis_backward(const ckan_basis_spec* spec, const float* t, cons
  * x that is again a Chebyshev series in t = tanh x, of degree degree + k:
  *   d^k f / dx^k = sum_j Ck[i, o, j] T_j(t),   Ck = C R,   R = M L^k,
  * with M the family's change of basis and L : p -> (1 - t^2) p'(t) (exact in
- * the T basis).  Requires fp32 coefficients and degree + k <= 16 for a
- * family basis, degree + k <= 256 for the Chebyshev one (above 16 the device
+ * the T basis).  Under the affine input map of desc (t = a x + b, the Hermite
+ * layer's finite domain) L : p -> a p'(t) instead, the series one degree
+ * lower (Ck keeps degree + 1 + k columns, the last 2k zero).  Requires fp32
+ * coefficients and degree + k <= 16 for a family basis or the affine map,
+ * degree + k <= 256 for the Chebyshev one under tanh (above 16 the device
  * applies L row by row in place of the matrix R).
  * Replaces KANLayer.compute_derivatives / jacobian (kan/layers/base.py:102-141)
  * and ChebyshevBasis.derivative (kan/basis/chebyshev.py:174-267).  Divergence:
  * the reference's derivative coefficients are wrong for n >= 3, omit the
  * tanh chain factor and its jacobian adds the other inputs' derivatives at 0;
  * these return the exact derivatives with respect to x. */
-/* R (fp64, row-major [degree + 1][degree + 1 + order]); host only. */
+/* R (fp64, row-major [degree + 1][degree + 1 + order]) of the tanh map; host only. */
 int ckan_derivative_matrix(const ckan_basis_spec* spec, int32_t degree, int32_t order, double* R);
 /* out [in, out, degree + 1 + order] = coeffs [in, out, degree + 1] R; a
  * ChebyKAN forward of degree desc->degree + order with `out` then gives

@@ -66,13 +66,12 @@ class BasisFunction(ABC):
         Divergence: the reference's Chebyshev derivative coefficients are wrong
         from degree 3 on and leave out the input map's chain factor; this is the
         exact derivative in x, the same quantity KANLayer.compute_derivatives
-        returns (degree + order <= 256; 16 for the Jacobi / Hermite bases)."""
-        check = getattr(self, "_check_input_map", None)
-        if callable(check):
-            check()
+        returns (degree + order <= 256; 16 for the Jacobi / Hermite bases and
+        under a Hermite basis' finite-domain affine map)."""
         x = x.reshape(-1, coefficients.shape[0])
+        aff = getattr(self, "_affine", None)
         return F.derivatives(x, coefficients, self._spec_or_none(), order,
-                             getattr(self, "compute", "fp32"))
+                             getattr(self, "compute", "fp32"), aff() if callable(aff) else None)
 
     def numerical_derivative(self, x: torch.Tensor, coefficients: torch.Tensor, order: int = 1,
                              eps: float = 1e-6) -> torch.Tensor:
@@ -232,13 +231,6 @@ class HermiteBasis(BasisFunction):
             return None
         lo, hi = self._domain
         return 2.0 / (hi - lo), -(hi + lo) / (hi - lo)
-
-    def _check_input_map(self) -> None:
-        """compute_derivatives / jacobian serve the tanh input map only."""
-        if self._affine_map():
-            raise RuntimeError(
-                "kan_amd HermiteBasis: derivatives and the Jacobian are computed for the "
-                "3*tanh(x) input map only; this layer maps a finite domain linearly.")
 
     def forward(self, x: torch.Tensor, coefficients: torch.Tensor) -> torch.Tensor:
         x = x.view(-1, coefficients.shape[0])

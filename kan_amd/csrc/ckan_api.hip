@@ -733,8 +733,9 @@ int ckan_coeff_grad_from_chebyshev(const ckan_desc* desc, const ckan_basis_spec*
 namespace {
 // R = M L^order for a layer of degree `degree` (spec NULL: Chebyshev, M = I),
 // as floats in r->m[n * kMaxD + k] (transposed: r->m[k * kMaxD + n]); *dout = D + order.
+// affine_a != 0: L is the derivative under the affine input map t = a x + b.
 int derivative_xform(const ckan_basis_spec* spec, int degree, int order, bool transposed,
-                     BasisXform* r, int* dout, double* Rout = nullptr) {
+                     BasisXform* r, int* dout, double* Rout = nullptr, double affine_a = 0.0) {
   if (degree < 0) return fail(CKAN_ERR_INVALID_ARG, "degree must be >= 0");
   if (order < 0) return fail(CKAN_ERR_INVALID_ARG, "derivative order must be >= 0");
   if (degree + order > kValuMaxDegree)
@@ -756,8 +757,10 @@ int derivative_xform(const ckan_basis_spec* spec, int degree, int order, bool tr
     for (int n = 0; n < D; ++n) M[(size_t)n * D + n] = 1.0;
   }
   std::vector<double> R((size_t)D * DO);
-  if (!derivative_to_chebyshev(M.data(), degree, order, R.data()))
-    return fail(CKAN_ERR_UNSUPPORTED, "derivative of order %d at degree %d", order, degree);
+  const bool ok = affine_a != 0.0
+                      ? affine_derivative_to_chebyshev(M.data(), degree, order, affine_a, R.data())
+                      : derivative_to_chebyshev(M.data(), degree, order, R.data());
+  if (!ok) return fail(CKAN_ERR_UNSUPPORTED, "derivative of order %d at degree %d", order, degree);
   if (Rout)
     for (size_t q = 0; q < (size_t)D * DO; ++q) Rout[q] = R[q];
   if (r) {
@@ -776,13 +779,22 @@ inline bool deriv_by_rows(const ckan_basis_spec* spec, int degree, int order) {
   return !spec && order >= 0 && degree + order >= kMaxD;
 }
 
-int check_f32_layer(const ckan_desc* desc) {
+// Derivative calls: fp32 coefficients; the affine input map only where the
+// operator fits in kernel arguments (the row-by-row kernels serve tanh).
+int check_f32_layer(const ckan_desc* desc, const ckan_basis_spec* spec, int order) {
   int rc = validate_desc(desc);
   if (rc) return rc;
-  if ((rc = require_tanh_map(desc, "derivatives"))) return rc;
+  if (desc->input_map == CKAN_INPUT_AFFINE && deriv_by_rows(spec, desc->degree, order))
+    return fail(CKAN_ERR_UNSUPPORTED, "derivatives under the affine input map: degree %d + order "
+                "%d exceeds %d", desc->degree, order, kMaxD - 1);
   if (desc->coeff_dtype != CKAN_DTYPE_F32)
     return fail(CKAN_ERR_UNSUPPORTED, "derivatives take fp32 coefficients");
   return CKAN_OK;
+}
+
+// The chain factor of the input map in derivative_xform (0: tanh).
+inline double map_slope(const ckan_desc* desc) {
+  return desc->input_map == CKAN_INPUT_AFFINE ? (double)desc->in_scale : 0.0;
 }
 }  // namespace
 
@@ -793,7 +805,7 @@ int ckan_derivative_matrix(const ckan_basis_spec* spec, int32_t degree, int32_t 
 
 int ckan_derivative_coeffs(const ckan_desc* desc, const ckan_basis_spec* spec, int32_t order,
                            const float* coeffs, float* out, void* stream) {
-  int rc = check_f32_layer(desc);
+  int rc = check_f32_layer(desc, spec, order);
   if (rc) return rc;
   const int64_t rows = (int64_t)desc->in_dim * desc->out_dim;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
@@ -806,7 +818,9 @@ int ckan_derivative_coeffs(const ckan_desc* desc, const ckan_basis_spec* spec, i
   }
   BasisXform r;
   int dout = 0;
-  if ((rc = derivative_xform(spec, desc->degree, order, false, &r, &dout))) return rc;
+  if ((rc = derivative_xform(spec, desc->degree, order, false, &r, &dout, nullptr,
+                             map_slope(desc))))
+    return rc;
   if (!coeffs || !out) return fail(CKAN_ERR_INVALID_ARG, "coeffs/out is NULL");
   ProfScope ps("deriv_coeffs", s);
   launch_coeff_xform(coeffs, out, rows, desc->degree + 1, dout, 0, r, s);
@@ -816,7 +830,7 @@ int ckan_derivative_coeffs(const ckan_desc* desc, const ckan_basis_spec* spec, i
 int ckan_derivative_coeffs_backward(const ckan_desc* desc, const ckan_basis_spec* spec,
                                     int32_t order, const float* dout_grad, float* dcoeffs,
                                     void* stream) {
-  int rc = check_f32_layer(desc);
+  int rc = check_f32_layer(desc, spec, order);
   if (rc) return rc;
   const int64_t rows = (int64_t)desc->in_dim * desc->out_dim;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
@@ -829,7 +843,9 @@ int ckan_derivative_coeffs_backward(const ckan_desc* desc, const ckan_basis_spec
   }
   BasisXform rt;
   int dout = 0;
-  if ((rc = derivative_xform(spec, desc->degree, order, true, &rt, &dout))) return rc;
+  if ((rc = derivative_xform(spec, desc->degree, order, true, &rt, &dout, nullptr,
+                             map_slope(desc))))
+    return rc;
   if (!dout_grad || !dcoeffs) return fail(CKAN_ERR_INVALID_ARG, "dout_grad/dcoeffs is NULL");
   ProfScope ps("deriv_coeffs_bwd", s);
   launch_coeff_xform(dout_grad, dcoeffs, rows, dout, desc->degree + 1, 0, rt, s);
@@ -843,12 +859,14 @@ size_t ckan_jacobian_workspace_bytes(const ckan_desc* desc) {
 
 int ckan_jacobian(const ckan_desc* desc, const ckan_basis_spec* spec, const float* x,
                   const float* coeffs, float* jac, void* ws, size_t ws_bytes, void* stream) {
-  int rc = check_f32_layer(desc);
+  int rc = check_f32_layer(desc, spec, 1);
   if (rc) return rc;
   const bool by_rows = deriv_by_rows(spec, desc->degree, 1);
   BasisXform r;
   int dout = 0;
-  if ((rc = derivative_xform(spec, desc->degree, 1, false, by_rows ? nullptr : &r, &dout))) return rc;
+  if ((rc = derivative_xform(spec, desc->degree, 1, false, by_rows ? nullptr : &r, &dout, nullptr,
+                             map_slope(desc))))
+    return rc;
   if (desc->batch == 0) return CKAN_OK;
   if (!x || !coeffs || !jac) return fail(CKAN_ERR_INVALID_ARG, "x/coeffs/jac is NULL");
   const size_t need = ckan_jacobian_workspace_bytes(desc);
@@ -862,7 +880,8 @@ int ckan_jacobian(const ckan_desc* desc, const ckan_basis_spec* spec, const floa
     launch_cheb_deriv_rows(coeffs, c1t, rows, desc->degree, 1, false, desc->out_dim, s);
   else
     launch_coeff_xform(coeffs, c1t, rows, desc->degree + 1, dout, desc->out_dim, r, s);
-  launch_jacobian(x, c1t, jac, desc->batch, desc->in_dim, desc->out_dim, dout, s);
+  launch_jacobian(x, c1t, jac, desc->batch, desc->in_dim, desc->out_dim, dout, desc->input_map,
+                  desc->in_scale, desc->in_shift, s);
   return check_launch("jacobian");
 }
 

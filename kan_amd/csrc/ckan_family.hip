@@ -181,6 +181,27 @@ static void chebyshev_dx(const double* a, int deg, double* out /* deg + 2 */) {
   for (int k = 0; k <= deg + 1; ++k) out[k] = (k <= dq ? b[k] : 0.0) - u2[k];
 }
 
+bool affine_derivative_to_chebyshev(const double* M, int degree, int order, double a,
+                                    double* R) {
+  if (degree < 0 || order < 0) return false;
+  const int D = degree + 1, DO = D + order;
+  double am = 1.0;
+  for (int s = 0; s < order; ++s) am *= a;
+  std::vector<double> cur(D + 2, 0.0), nxt(D + 2, 0.0);
+  for (int n = 0; n < D; ++n) {
+    for (int k = 0; k < D + 2; ++k) cur[k] = k < D ? M[n * D + k] : 0.0;
+    for (int s = 0; s < order; ++s) {
+      // d/du of sum_k c_k T_k(u): e_{k-1} = e_{k+1} + 2 k c_k (k = deg..1), e_0 halved
+      for (int k = 0; k < D + 2; ++k) nxt[k] = 0.0;
+      for (int k = degree; k >= 1; --k) nxt[k - 1] = nxt[k + 1] + 2.0 * k * cur[k];
+      nxt[0] *= 0.5;
+      cur.swap(nxt);
+    }
+    for (int k = 0; k < DO; ++k) R[(size_t)n * DO + k] = k < D ? am * cur[k] : 0.0;
+  }
+  return true;
+}
+
 bool derivative_to_chebyshev(const double* M, int degree, int order, double* R) {
   if (degree < 0 || order < 0) return false;
   const int D = degree + 1, DO = D + order;
@@ -226,16 +247,17 @@ k_coeff_xform(const float* __restrict__ in, float* __restrict__ out, int64_t row
   }
 }
 
-// jac[b, o, i] = sum_k c1t[o][k][i] T_k(tanh x[b, i]): block (i-block, b),
-// one input per thread, the T_k in registers, a loop over outputs.
+// jac[b, o, i] = sum_k c1t[o][k][i] T_k(t[b, i]), t the layer's input map of
+// x (tanh, or the affine map): block (i-block, b), one input per thread, the
+// T_k in registers, a loop over outputs.
 template <int DM>
 __global__ void __launch_bounds__(256)
 k_jacobian(const float* __restrict__ x, const float* __restrict__ c1t, float* __restrict__ jac,
-           int64_t B, int I, int O, int dout) {
+           int64_t B, int I, int O, int dout, int imap, float ima, float imb) {
   const int i = blockIdx.x * 256 + threadIdx.x;
   const int64_t b = blockIdx.y;
   if (i >= I) return;
-  const float t = tanhf(x[b * I + i]);
+  const float t = input_map(x[b * I + i], imap, ima, imb);
   float T[DM];
   T[0] = 1.0f;
   if (DM > 1) T[1] = t;
@@ -509,11 +531,11 @@ void launch_cheb_deriv_rows(const float* in, float* out, int64_t rows, int degre
 // jac[b, o, i] for any number of terms: the recurrence runs along k for each o.
 __global__ void __launch_bounds__(256)
 k_jacobian_any(const float* __restrict__ x, const float* __restrict__ c1t, float* __restrict__ jac,
-               int64_t B, int I, int O, int dout) {
+               int64_t B, int I, int O, int dout, int imap, float ima, float imb) {
   const int i = blockIdx.x * 256 + threadIdx.x;
   const int64_t b = blockIdx.y;
   if (i >= I) return;
-  const float t = tanhf(x[b * I + i]), t2 = t + t;
+  const float t = input_map(x[b * I + i], imap, ima, imb), t2 = t + t;
   for (int o = 0; o < O; ++o) {
     const float* c = c1t + (size_t)o * dout * I + i;
     float tp = t, tc = 1.0f, acc = 0.0f;  // T_{-1} = t, T_0
@@ -528,7 +550,7 @@ k_jacobian_any(const float* __restrict__ x, const float* __restrict__ c1t, float
 }
 
 void launch_jacobian(const float* x, const float* c1t, float* jac, int64_t B, int I, int O,
-                     int dout, hipStream_t s) {
+                     int dout, int imap, float ima, float imb, hipStream_t s) {
   constexpr int64_t kMaxGridY = 65535;
   for (int64_t b0 = 0; b0 < B; b0 += kMaxGridY) {  // rows in chunks of the grid's y limit
     const int64_t nb = B - b0 < kMaxGridY ? B - b0 : kMaxGridY;
@@ -536,13 +558,17 @@ void launch_jacobian(const float* x, const float* c1t, float* jac, int64_t B, in
     const float* xb = x + b0 * I;
     float* jb = jac + b0 * O * I;
     if (dout <= 5)
-      hipLaunchKernelGGL((k_jacobian<5>), g, dim3(256), 0, s, xb, c1t, jb, nb, I, O, dout);
+      hipLaunchKernelGGL((k_jacobian<5>), g, dim3(256), 0, s, xb, c1t, jb, nb, I, O, dout,
+                         imap, ima, imb);
     else if (dout <= 9)
-      hipLaunchKernelGGL((k_jacobian<9>), g, dim3(256), 0, s, xb, c1t, jb, nb, I, O, dout);
+      hipLaunchKernelGGL((k_jacobian<9>), g, dim3(256), 0, s, xb, c1t, jb, nb, I, O, dout,
+                         imap, ima, imb);
     else if (dout <= 17)
-      hipLaunchKernelGGL((k_jacobian<17>), g, dim3(256), 0, s, xb, c1t, jb, nb, I, O, dout);
+      hipLaunchKernelGGL((k_jacobian<17>), g, dim3(256), 0, s, xb, c1t, jb, nb, I, O, dout,
+                         imap, ima, imb);
     else
-      hipLaunchKernelGGL(k_jacobian_any, g, dim3(256), 0, s, xb, c1t, jb, nb, I, O, dout);
+      hipLaunchKernelGGL(k_jacobian_any, g, dim3(256), 0, s, xb, c1t, jb, nb, I, O, dout, imap,
+                         ima, imb);
   }
 }
 

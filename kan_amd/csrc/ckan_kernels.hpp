@@ -103,6 +103,12 @@ void launch_basis_family_bwd(const float* t, const float* g, int64_t n, int deg,
 // exact up to rounding) maps row n of M (the family's change of basis, D x D)
 // through `order` such steps (R has degree + 1 rows of degree + 1 + order).
 bool derivative_to_chebyshev(const double* M, int degree, int order, double* R);
+// The same for the affine input map t = a x + b: d/dx f = a f'(t), the plain
+// Chebyshev derivative (one degree lower), so R (same shape, D + order
+// columns) holds a^order times row n of M differentiated `order` times, its
+// last 2 * order columns zero.
+bool affine_derivative_to_chebyshev(const double* M, int degree, int order, double a,
+                                    double* R);
 // out = in R over rows q of `rows`: in [rows][din], R [din][dout] (row-major,
 // r[n * kMaxD + k]).  transposed_o > 0 writes out as [o][dout][i] for rows
 // q = i * transposed_o + o (the Jacobian's layout), else [rows][dout].
@@ -114,9 +120,10 @@ void launch_coeff_xform(const float* in, float* out, int64_t rows, int din, int 
 // [o][dout][i] as launch_coeff_xform does.
 void launch_cheb_deriv_rows(const float* in, float* out, int64_t rows, int degree, int order,
                             bool adjoint, int transposed_o, hipStream_t s);
-// jac[b, o, i] = sum_k C1t[o][k][i] T_k(tanh x[b, i]), k < dout.
+// jac[b, o, i] = sum_k C1t[o][k][i] T_k(t[b, i]), k < dout, t the input map
+// (imap, ima, imb as in input_map) of x.
 void launch_jacobian(const float* x, const float* c1t, float* jac, int64_t B, int I, int O,
-                     int dout, hipStream_t s);
+                     int dout, int imap, float ima, float imb, hipStream_t s);
 
 // ---- vector-ALU path (ckan_valu.hip): any degree, T = float or double ------
 // Serves fp64 layers and fp32 layers above kMfmaMaxDegree, with C in its own

@@ -408,9 +408,10 @@ def _spec_ref(spec):
     return None if spec is None else ctypes.byref(spec)
 
 
-def _derivative_desc(coeffs: torch.Tensor, batch: int = 0) -> "_lib.CkanDesc":
+def _derivative_desc(coeffs: torch.Tensor, batch: int = 0, affine=None) -> "_lib.CkanDesc":
     in_dim, out_dim, dd = coeffs.shape
-    return _lib.make_desc(batch, in_dim, out_dim, dd - 1, _lib.CKAN_COMPUTE_FP32, _lib.CKAN_DTYPE_F32)
+    return _lib.make_desc(batch, in_dim, out_dim, dd - 1, _lib.CKAN_COMPUTE_FP32, _lib.CKAN_DTYPE_F32,
+                          None if affine is None else tuple(affine))
 
 
 def _f32_coeffs(coeffs: torch.Tensor) -> torch.Tensor:
@@ -424,16 +425,17 @@ def _f32_coeffs(coeffs: torch.Tensor) -> torch.Tensor:
 
 
 class DerivativeCoeffsFunction(torch.autograd.Function):
-    """Ck = C R [in, out, D + order]: the Chebyshev coefficients in tanh x of
-    the order-k x-derivative of each univariate function (R from the library,
-    exact in fp64, applied in fp32); backward dC = dCk R^T."""
+    """Ck = C R [in, out, D + order]: the Chebyshev coefficients in tanh x (in
+    u = affine[0] x + affine[1] under an affine input map) of the order-k
+    x-derivative of each univariate function (R from the library, exact in
+    fp64, applied in fp32); backward dC = dCk R^T."""
 
     @staticmethod
-    def forward(ctx, coeffs: torch.Tensor, spec, order: int):
+    def forward(ctx, coeffs: torch.Tensor, spec, order: int, affine=None):
         c = _f32_coeffs(coeffs.detach())
         in_dim, out_dim, dd = c.shape
         out = torch.empty(in_dim, out_dim, dd + order, dtype=torch.float32, device=c.device)
-        desc = _derivative_desc(c)
+        desc = _derivative_desc(c, 0, affine)
         lib = _lib.load()
         _lib.check(lib.ckan_derivative_coeffs(desc, _spec_ref(spec), int(order), c.data_ptr(),
                                               out.data_ptr(), _lib.stream_ptr(c.device)))
@@ -451,33 +453,40 @@ class DerivativeCoeffsFunction(torch.autograd.Function):
                                                        _lib.stream_ptr(g.device)))
         if ctx.c_dtype != torch.float32:
             dc = dc.to(ctx.c_dtype)
-        return dc, None, None
+        return dc, None, None, None
 
 
-def derivative_coeffs(coeffs: torch.Tensor, spec, order: int) -> torch.Tensor:
-    return DerivativeCoeffsFunction.apply(coeffs, spec, int(order))
+def derivative_coeffs(coeffs: torch.Tensor, spec, order: int, affine=None) -> torch.Tensor:
+    return DerivativeCoeffsFunction.apply(coeffs, spec, int(order), affine)
 
 
 def derivatives(x: torch.Tensor, coeffs: torch.Tensor, spec, order: int = 1,
-                compute: str = "fp32") -> torch.Tensor:
+                compute: str = "fp32", affine=None) -> torch.Tensor:
     """[B, out]: sum_i d^order f_{i,o} / dx^order (x[b, i]), the sum over inputs of
-    each univariate function's order-th x-derivative (differentiable in x and C)."""
+    each univariate function's order-th x-derivative (differentiable in x and C).
+    ``affine`` = (a, b): the layer maps x by u = a x + b instead of tanh."""
     if order < 0:
         raise ValueError(f"order must be >= 0, got {order}")
     if order == 0:
-        return chebykan(x, coeffs, compute) if spec is None else family_kan(x, coeffs, spec, compute)
-    return ChebyKANFunction.apply(x, derivative_coeffs(coeffs, spec, order), compute, None)
+        if spec is None and affine is None:
+            return chebykan(x, coeffs, compute)
+        if spec is None:
+            return ChebyKANFunction.apply(x, coeffs, compute, None, affine)
+        return family_kan(x, coeffs, spec, compute, affine)
+    return ChebyKANFunction.apply(x, derivative_coeffs(coeffs, spec, order, affine), compute, None,
+                                  affine)
 
 
-def jacobian(x: torch.Tensor, coeffs: torch.Tensor, spec) -> torch.Tensor:
-    """[B, out, in]: d y[b, o] / d x[b, i] (fp32; not differentiable)."""
+def jacobian(x: torch.Tensor, coeffs: torch.Tensor, spec, affine=None) -> torch.Tensor:
+    """[B, out, in]: d y[b, o] / d x[b, i] (fp32; not differentiable); ``affine``
+    as in derivatives."""
     c = _f32_coeffs(coeffs.detach())
     _require_device(x)
     in_dim, out_dim, _ = c.shape
     if x.dim() != 2 or x.shape[1] != in_dim:
         raise RuntimeError(f"x must be [batch, {in_dim}], got {tuple(x.shape)}")
     x32 = x.detach().float().contiguous()
-    desc = _derivative_desc(c, x32.shape[0])
+    desc = _derivative_desc(c, x32.shape[0], affine)
     lib = _lib.load()
     jac = torch.empty(x32.shape[0], out_dim, in_dim, dtype=torch.float32, device=x.device)
     ws_bytes = lib.ckan_jacobian_workspace_bytes(desc)

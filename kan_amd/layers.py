@@ -57,6 +57,11 @@ class KANLayer(nn.Module, ABC):
     def _compute_mode(self) -> str:
         return getattr(self.basis_function, "compute", "fp32")
 
+    def _input_affine(self):
+        """(a, b) of the basis' affine input map u = a x + b, or None for tanh."""
+        aff = getattr(self.basis_function, "_affine", None)
+        return aff() if callable(aff) else None
+
     def compute_derivatives(self, x: torch.Tensor, order: int = 1) -> torch.Tensor:
         """[batch, output_dim]: sum over inputs i of the order-th derivative in
         x_i of each univariate function f_{i,o} (kan/layers/base.py:102-114).
@@ -65,13 +70,11 @@ class KANLayer(nn.Module, ABC):
         coefficients are wrong from degree 3 on and which differentiates in
         tanh(x) without the chain factor; this returns the exact x-derivative
         (a Chebyshev series of degree degree + order: degree + order <= 256,
-        or 16 for the Jacobi / Hermite layers)."""
-        check = getattr(self.basis_function, "_check_input_map", None)
-        if callable(check):
-            check()
+        or 16 for the Jacobi / Hermite layers; a Hermite layer with a finite
+        domain differentiates through its affine map, chain factor included)."""
         x = x.reshape(-1, self.input_dim)
         return F.derivatives(x, self.get_coefficients(), self._basis_spec(), order,
-                             self._compute_mode())
+                             self._compute_mode(), self._input_affine())
 
     def jacobian(self, x: torch.Tensor) -> torch.Tensor:
         """[batch, output_dim, input_dim]: d y[b, o] / d x[b, i] (kan/layers/base.py:116-141).
@@ -80,11 +83,8 @@ class KANLayer(nn.Module, ABC):
         with the other inputs zeroed, which adds their derivatives at 0 (and
         the reference's derivative is itself inexact); this is the exact
         Jacobian.  Computed in fp32; not differentiable."""
-        check = getattr(self.basis_function, "_check_input_map", None)
-        if callable(check):
-            check()
         x = x.reshape(-1, self.input_dim)
-        return F.jacobian(x, self.get_coefficients(), self._basis_spec())
+        return F.jacobian(x, self.get_coefficients(), self._basis_spec(), self._input_affine())
 
 
 class ChebyKANLayer(KANLayer):

@@ -10,6 +10,7 @@ Tolerances (norm-wise, ||a - b|| / ||b||):
 Divergence from the reference (documented in kan_amd/layers.py): these are
 the exact x-derivatives; the reference's are not (see the oracle's header).
 """
+import numpy as np
 import pytest
 import torch
 
@@ -112,6 +113,43 @@ def test_family_derivatives_and_jacobian(family, kw, order):
     got = layer.compute_derivatives(x.cuda(), order=order)
     assert _rel(got, do.derivatives(x, c, order, fwd)) <= FP32_TOL
     assert _rel(layer.jacobian(x.cuda()), do.jacobian(x, c, fwd)) <= FP32_TOL
+
+
+AFFINE_CASES = [
+    ("hermite", dict(scaling="physicist", domain=(-1.5, 2.5)), 1),
+    ("hermite", dict(scaling="physicist", domain=(-1.5, 2.5)), 3),
+    ("hermite_e", dict(scaling="probabilist", domain=(-3.0, 1.0)), 2),
+]
+
+
+@pytest.mark.parametrize("family,kw,order", AFFINE_CASES)
+def test_hermite_finite_domain_derivatives_and_jacobian(family, kw, order):
+    """A Hermite layer with a finite domain maps x by z = 6 (x - lo) / (hi -
+    lo) - 3 (kan/basis/hermite.py:102-112): its x-derivatives carry the
+    constant chain factor (6 / (hi - lo))^order and lower the degree, against
+    fp64 autograd through the oracle's forward with that map, and the
+    derivative of H_n(z) = 2n H_{n-1}(z) (He_n: n He_{n-1}) at order 1."""
+    B, I, O, deg = 300, 24, 20, 6
+    print(f"hermite affine derivatives {family} {kw} order={order}", flush=True)
+    torch.manual_seed(21 + order)
+    layer = kan_amd.HermiteKANLayer(I, O, deg, **kw).cuda()
+    fwd = lambda xx, cc: fo.family_forward(xx, cc, family, domain=kw["domain"])
+    c = layer.get_coefficients().detach().cpu()
+    lo, hi = kw["domain"]
+    x = lo + (hi - lo) * torch.rand(B, I, generator=torch.Generator().manual_seed(5 + order))
+    got = layer.compute_derivatives(x.cuda(), order=order)
+    assert _rel(got, do.derivatives(x, c, order, fwd)) <= FP32_TOL
+    J = layer.jacobian(x.cuda())
+    assert _rel(J, do.jacobian(x, c, fwd)) <= FP32_TOL
+    if order == 1:  # the closed form: dx of the fp64 backward with dy = e_o, summed over i
+        dx, _ = fo.family_backward_fp64(x.numpy(), c.double().numpy(), np.ones((B, O)), family,
+                                        domain=kw["domain"])
+        assert _rel(got.sum(dim=1), torch.from_numpy(dx.sum(axis=1))) <= FP32_TOL
+    # outside the operator's reach: degree + order above 16
+    with pytest.raises(_lib.CkanError) as e:
+        kan_amd.HermiteKANLayer(8, 4, 15, domain=(-1.0, 1.0)).cuda().compute_derivatives(
+            x[:, :8].cuda(), order=2)
+    assert e.value.code == _lib.CKAN_ERR_UNSUPPORTED
 
 
 def test_derivatives_are_differentiable():
