@@ -40,7 +40,14 @@ STEP_FLOP = 3.0 * GEMM_FLOP          # x requires grad: fwd + dX + dC
 
 
 def _step(layer, x, dy):
-    layer.get_coefficients().grad = None
+    import torch
+    c = layer.get_coefficients()
+    # a training step's optimizer updates the coefficients in place, which
+    # advances their version; the layer keeps its packed operand per version,
+    # so this makes every timed step re-pack as training does (with unchanged
+    # coefficients the pack would be skipped: work left out of the step)
+    torch.autograd.graph.increment_version(c)
+    c.grad = None
     x.grad = None
     y = layer(x)
     y.backward(dy)
