@@ -339,7 +339,12 @@ typedef enum ckan_exec_flags {
    * ChebyKANLayer(1, 1, 8) on 100 points) runs each step as one launch of a
    * single-workgroup kernel instead of the per-layer kernel sequence; this
    * flag keeps the kernel sequence for such stacks too. */
-  CKAN_EXEC_NO_FUSED_SMALL = 1
+  CKAN_EXEC_NO_FUSED_SMALL = 1,
+  /* A two-layer cross-entropy stack of small layers (e.g. 784 -> 64 -> 10)
+   * keeps its packed operands current from the step's dC launch, which
+   * writes them from the updated coefficients, so its steps run no pack
+   * launch; this flag packs at every step instead (the same bits). */
+  CKAN_EXEC_PACK_EACH_STEP = 2
 } ckan_exec_flags;
 
 /* Allocates every device buffer; coefficients start at zero (set them with

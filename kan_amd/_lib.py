@@ -146,6 +146,7 @@ class CkanExecConfig(ctypes.Structure):
 
 
 CKAN_EXEC_NO_FUSED_SMALL = 1
+CKAN_EXEC_PACK_EACH_STEP = 2
 
 
 CKAN_LOSS_MSE = 0

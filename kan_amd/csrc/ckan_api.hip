@@ -1095,6 +1095,81 @@ int ckan::pack2_forward_tail_ce(const ckan_desc* da, const void* Ca, void* pka, 
   return check_launch("pack2_forward_tail_ce: tail");
 }
 
+bool ckan::self_pack_pair_fits(const ckan_desc* a, const ckan_desc* b) {
+  if (!pack2_tail_ce_fits(a, b)) return false;
+  const Plan pa = plan_of(a), pb = plan_of(b);
+  const FwdChoice ca = choose_fwd(pa);
+  // a's bias as per-input-block partials, summed by the tail
+  return pa.P == pb.P && pa.esz == pb.esz && dc_pack_ok(pa) && dc_pack_ok(pb) && dx_small_ok(pb) &&
+         (pa.NIB == 1 || fwd_sums_bias(pa, ca));
+}
+
+int ckan::self_pack_layer(const ckan_desc* desc, const void* C, void* packed, void* stream) {
+  if (validate_desc(desc) != CKAN_OK || valu_route(desc))
+    return fail(CKAN_ERR_INVALID_ARG, "self_pack_layer: not a packed-kernel layer");
+  if (!C || !packed || !aligned16(packed))
+    return fail(CKAN_ERR_INVALID_ARG, "self_pack_layer: NULL or misaligned buffer");
+  const Plan p = plan_of(desc);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  {
+    ProfScope ps("pack", s);
+    launch_pack(C, false, packed, p, s, nullptr, !fwd_sums_bias(p, choose_fwd(p)));
+  }
+  return check_launch("self_pack_layer");
+}
+
+int ckan::forward_tail_ce_packed(const ckan_desc* da, const void* pka, const float* xa, float* ta,
+                                 const ckan_desc* db, const void* Cb, float* tb, float* yb,
+                                 const int64_t* labels, float* dyb, float* loss_part, float* dya,
+                                 void* ws, size_t ws_bytes, void* stream) {
+  if (!self_pack_pair_fits(da, db))
+    return fail(CKAN_ERR_INVALID_ARG, "forward_tail_ce_packed: the layer pair does not allow it");
+  if (!pka || !xa || !ta || !Cb || !tb || !yb || !labels || !dyb || !loss_part || !dya)
+    return fail(CKAN_ERR_INVALID_ARG, "forward_tail_ce_packed: NULL pointer");
+  if (!aligned16(pka) || !aligned16(ta) || !aligned16(tb))
+    return fail(CKAN_ERR_INVALID_ARG, "forward_tail_ce_packed: packed buffer and caches must be 16-byte aligned");
+  const Plan pa = plan_of(da);
+  const FwdChoice ca = choose_fwd(pa);
+  const size_t need = fwd_ws_bytes(pa, ca);
+  if (ws_bytes < need)
+    return fail(CKAN_ERR_WORKSPACE, "forward workspace too small: %zu < %zu bytes", ws_bytes, need);
+  if (need && !ws) return fail(CKAN_ERR_INVALID_ARG, "workspace is NULL");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const bool sum_a = fwd_sums_bias(pa, ca);
+  int rc;
+  if (fwd_maps_x_ok(pa, ca, xa)) {  // the GEMM maps x and writes a's tanh cache
+    ProfScope ps("fwd_gemm", s);
+    launch_fwd_gemm(xa, ta, pka, tb, ws, pa, ca, s, sum_a, true, false, true);
+  } else if ((rc = forward_packed(pa, ca, pka, xa, tb, ta, ws, s, false, sum_a, true, false))) {
+    return rc;
+  }
+  if ((rc = check_launch("forward_tail_ce_packed: forward"))) return rc;
+  {
+    ProfScope ps("fwd_tail", s);
+    launch_fwd_tail_ce(pka, ws, pa, ca, sum_a, tb, reinterpret_cast<const float*>(Cb), db->out_dim,
+                       db->degree + 1, yb, labels, dyb, loss_part, s, dya);
+  }
+  return check_launch("forward_tail_ce_packed: tail");
+}
+
+int ckan::backward_self_packed(const ckan_desc* da, const float* ta, const float* dya, float* Ca,
+                               const DcOut& oma, void* pka, const ckan_desc* db, const float* tb,
+                               const float* dyb, float* Cb, const DcOut& omb, void* pkb,
+                               const LossMean& lm, void* stream) {
+  if (!self_pack_pair_fits(da, db))
+    return fail(CKAN_ERR_INVALID_ARG, "backward_self_packed: the layer pair does not allow it");
+  if (oma.mode < kDcSgd || omb.mode < kDcSgd)
+    return fail(CKAN_ERR_INVALID_ARG, "backward_self_packed: needs an optimizer step");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  {
+    ProfScope ps("dc_pack", s);
+    const DcPackArgs a{dya, ta, Ca, oma, plan_of(da), pka, true, false};
+    const DcPackArgs b{dyb, tb, Cb, omb, plan_of(db), pkb, false, true};
+    launch_dc_pack(a, &b, s, lm);
+  }
+  return check_launch("backward_self_packed");
+}
+
 int ckan::pack_forward_ex(const ckan_desc* desc, const void* coeffs, void* packed, const float* x,
                           float* out, float* t_cache, void* ws, size_t ws_bytes, void* stream,
                           bool t_ready, bool out_tanh, const ckan_basis_spec* spec) {

@@ -721,6 +721,55 @@ void launch_bias_reduce(void* packed, const Plan& p, hipStream_t s) {
 // accumulates its pair's D sums over its quarter of the rows (Chebyshev
 // recurrence in registers), and the quarters are added in order through LDS.
 constexpr int kDcSmallRows = 256;  // rows staged at once (all of the batch)
+
+// One 256-thread group's sums for 8 inputs x 8 outputs (DMAX <= 9), from t
+// staged as ts[r * TP + input] and dy as ys[r * 8 + output]: thread (lane,
+// wave rq) takes input il2 = lane % 8, outputs 4 og .. 4 og + 3 (og = lane /
+// 8 % 2) and rows r = rs (mod 16), rs = 4 rq + lane / 16, so the recurrence of
+// a (row, input) serves 4 outputs (one per (input, output) pair and row made
+// it vector-ALU-bound: config 2's 784 -> 64 layer 11.8 us); the wave's 4 row
+// slices are added by a fixed butterfly into red[(rq * 64 + il2 * 8 + 4 og +
+// c) * (DMAX + 1) + d], and the caller adds the 4 waves' rows in rq order.
+// SYNC: a block barrier before red is written (red may overlay ts).
+template <int DMAX, int TP, bool SYNC = false>
+__device__ __forceinline__ void dc_small_sums(const float* ts, const float* ys, float* red, int rows,
+                                              int gt) {
+  const int lane = gt & 63, rq = gt >> 6;
+  const int il2 = lane & 7, og = (lane >> 3) & 1, rs = rq * 4 + (lane >> 4);
+  float acc[4][DMAX];
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int d = 0; d < DMAX; ++d) acc[c][d] = 0.0f;
+  for (int r = rs; r < rows; r += 16) {
+    const float tv = ts[r * TP + il2], t2 = tv + tv;
+    const f32x4_t yv = *reinterpret_cast<const f32x4_t*>(ys + r * 8 + og * 4);
+    float pm = tv, pc = 1.0f;  // T_{-1} = t, T_0 = 1
+#pragma unroll
+    for (int d = 0; d < DMAX; ++d) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) acc[c][d] = fmaf(pc, yv[c], acc[c][d]);
+      const float nx = fmaf(t2, pc, -pm);
+      pm = pc;
+      pc = nx;
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int d = 0; d < DMAX; ++d) {
+      acc[c][d] += __shfl_xor(acc[c][d], 16);
+      acc[c][d] += __shfl_xor(acc[c][d], 32);
+    }
+  if constexpr (SYNC) __syncthreads();
+  if ((lane >> 4) == 0) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int d = 0; d < DMAX; ++d) red[(rq * 64 + il2 * 8 + og * 4 + c) * (DMAX + 1) + d] = acc[c][d];
+  }
+}
+
 template <int DMAX>
 __device__ __forceinline__ void dc_small_body(const float* __restrict__ dy, const float* __restrict__ t,
                                               float* __restrict__ dC, const DcOut& om,
@@ -752,44 +801,7 @@ __device__ __forceinline__ void dc_small_body(const float* __restrict__ dy, cons
   }
   __syncthreads();
   if constexpr (DMAX <= 9) {
-    // thread = (input il2, output half og, row slice rs of 16): the
-    // recurrence of (row, input) serves 4 outputs (one per (input, output)
-    // pair and row made it vector-ALU-bound: config 2's 784 -> 64 layer
-    // 11.8 us); the wave's 4 row slices (lane bits 4-5) are added by a fixed
-    // butterfly, the 4 waves' in order below
-    const int lane = tid & 63;
-    const int il2 = lane & 7, og = (lane >> 3) & 1, rs = rq * 4 + (lane >> 4);
-    float acc[4][DMAX];
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-#pragma unroll
-      for (int d = 0; d < DMAX; ++d) acc[c][d] = 0.0f;
-    for (int r = rs; r < rows; r += 16) {
-      const float tv = ts[r][il2], t2 = tv + tv;
-      const f32x4_t yv = *reinterpret_cast<const f32x4_t*>(&ys[r][og * 4]);
-      float pm = tv, pc = 1.0f;  // T_{-1} = t, T_0 = 1
-#pragma unroll
-      for (int d = 0; d < DMAX; ++d) {
-#pragma unroll
-        for (int c = 0; c < 4; ++c) acc[c][d] = fmaf(pc, yv[c], acc[c][d]);
-        const float nx = fmaf(t2, pc, -pm);
-        pm = pc;
-        pc = nx;
-      }
-    }
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-#pragma unroll
-      for (int d = 0; d < DMAX; ++d) {
-        acc[c][d] += __shfl_xor(acc[c][d], 16);
-        acc[c][d] += __shfl_xor(acc[c][d], 32);
-      }
-    if ((lane >> 4) == 0) {
-#pragma unroll
-      for (int c = 0; c < 4; ++c)
-#pragma unroll
-        for (int d = 0; d < DMAX; ++d) red[rq][il2 * 8 + og * 4 + c][d] = acc[c][d];
-    }
+    dc_small_sums<DMAX, 9>(&ts[0][0], &ys[0][0], &red[0][0][0], rows, tid);
   } else {
     // rows 4 at a time with 4 accumulator sets: independent recurrences and
     // LDS reads in flight together (one row at a time was latency-bound);
@@ -845,6 +857,155 @@ __global__ void __launch_bounds__(256)
 k_dc_small(const float* __restrict__ dy, const float* __restrict__ t, float* __restrict__ dC,
            DcOut om, Plan p) {
   dc_small_body<DMAX>(dy, t, dC, om, p, blockIdx.x, blockIdx.y);
+}
+
+// The small dC with its optimizer step applied, which also writes the layer's
+// packed operands for the next step from the updated coefficients, so that a
+// resident training step runs no pack launch.  A block takes 32 inputs (one
+// input block of the pack) x 8 outputs with four 256-thread groups; group q
+// computes inputs 8q .. 8q + 7 as a k_dc_small block does (dc_small_sums, the
+// waves added in the same order, so the same bits).  The updated 32 x 8 x D
+// coefficients stay in LDS (zero for inputs and outputs past the layer, as in
+// the pack's tile), and from them the block writes the pack's entries for its
+// inputs and outputs, each formed as the pack forms it: the forward operand
+// Cf (degrees 1..P), the input block's bias partial (groups of 4 inputs
+// summed in order, then the 8 groups in order) and the dX operand Cb
+// ((e + 1) C[i, o, e + 1]).  A null pointer skips that part.
+template <bool BF> struct DcPackJob {
+  const float* dy;                   // [B, O]
+  const float* t;                    // tanh cache, row pitch I_sg
+  float* C;                          // [I, O, D], receives the step by om
+  DcOut om;
+  Plan p;
+  typename Elem<BF>::type* Cf;       // forward operand, or nullptr
+  float* bias;                       // bias partials [NIB][O32] (the bias for NIB == 1), or nullptr
+  typename Elem<BF>::type* Cb;       // dX operand, or nullptr
+  int nx, nblocks;                   // input blocks of 32; blocks of the job
+};
+constexpr int kDcPackThreads = 1024;
+constexpr int kDcPackTP = 40;  // t staging row pitch: a wave's 4 rows x 8 inputs hit distinct banks
+
+template <int DMAX, int P, bool BF>
+__device__ __forceinline__ void dc_pack_body(const DcPackJob<BF>& j, int bx, int by) {
+  static_assert(DMAX <= 9, "the small dC sums take DMAX <= 9");
+  using G = FwdGroup<P>;
+  constexpr int TSF = kDcSmallRows * kDcPackTP;  // t [rows][32 inputs], pitch kDcPackTP
+  constexpr int RDG = 4 * 64 * (DMAX + 1);       // one group's wave sums [4][64][DMAX + 1]
+  static_assert(4 * RDG <= TSF, "the wave sums overlay the t staging");
+  constexpr int CNP = 8 * DMAX + 1;              // updated-C row pitch
+  __shared__ __attribute__((aligned(16))) float stage[TSF];
+  __shared__ __attribute__((aligned(16))) float ys[kDcSmallRows * 8];
+  __shared__ float cn[32 * CNP];
+  const Plan& p = j.p;
+  const int tid = threadIdx.x, grp = tid >> 8;
+  const int i0 = bx * 32, o0 = by * 8;
+  const int D = p.D;
+  const int rows = (int)p.B;  // <= kDcSmallRows (dc_small_ok)
+  // staging with every load in flight at once: t of the 32 inputs (one
+  // 128-byte run per row), dy of the 8 outputs, and the coefficients the
+  // step updates (element k of the tile's 32 x 8D run: input k / 8D)
+  constexpr int NT = kDcSmallRows * 32 / kDcPackThreads, NY = kDcSmallRows * 8 / kDcPackThreads;
+  constexpr int NE = (32 * 8 * DMAX + kDcPackThreads - 1) / kDcPackThreads;
+  const int ne = 32 * 8 * D, ovalid = min(8, p.O - o0);
+  float tl[NT], yl[NY], cold[NE];
+#pragma unroll
+  for (int m = 0; m < NE; ++m) {
+    const int k = tid + kDcPackThreads * m;
+    const int kil = k / (8 * D), rem = k - kil * 8 * D;
+    const bool ok = k < ne && i0 + kil < p.I && rem / D < ovalid && j.om.mode != kDcStore;
+    cold[m] = ok ? j.C[((size_t)(i0 + kil) * p.O + o0) * D + rem] : 0.0f;
+  }
+#pragma unroll
+  for (int u = 0; u < NT; ++u) {
+    const int k = tid + kDcPackThreads * u, r = k >> 5, c = k & 31;
+    tl[u] = r < rows && i0 + c < p.I ? j.t[(int64_t)r * p.I_sg + i0 + c] : 0.0f;
+  }
+#pragma unroll
+  for (int u = 0; u < NY; ++u) {
+    const int k = tid + kDcPackThreads * u, r = k >> 3, c = k & 7;
+    yl[u] = r < rows && o0 + c < p.O ? j.dy[(int64_t)r * p.O + o0 + c] : 0.0f;
+  }
+#pragma unroll
+  for (int u = 0; u < NT; ++u) {
+    const int k = tid + kDcPackThreads * u;
+    stage[(k >> 5) * kDcPackTP + (k & 31)] = tl[u];
+  }
+#pragma unroll
+  for (int u = 0; u < NY; ++u) ys[tid + kDcPackThreads * u] = yl[u];
+  __syncthreads();
+  // group grp: inputs 8 grp .. 8 grp + 7; its wave sums overlay the staging
+  // once every group has read it (the barrier inside)
+  dc_small_sums<DMAX, kDcPackTP, true>(stage + grp * 8, ys, stage + grp * RDG, rows, tid & 255);
+  __syncthreads();
+#pragma unroll
+  for (int m = 0; m < NE; ++m) {
+    const int k = tid + kDcPackThreads * m;
+    if (k >= ne) break;
+    const int kil = k / (8 * D), rem = k - kil * 8 * D, kol = rem / D, d = rem - kol * D;
+    const int i = i0 + kil;
+    float v = 0.0f;
+    if (i < p.I && kol < ovalid) {
+      const float* rd = stage + (kil >> 3) * RDG + ((kil & 7) * 8 + kol) * (DMAX + 1) + d;
+      const float g = ((rd[0] + rd[64 * (DMAX + 1)]) + rd[128 * (DMAX + 1)]) + rd[192 * (DMAX + 1)];
+      v = dc_apply_from(j.C + ((size_t)i * p.O + o0) * D + rem, cold[m], g, j.om);
+    }
+    cn[kil * CNP + rem] = v;
+  }
+  __syncthreads();
+  if (j.bias && tid < 8) {
+    float s = 0.0f;
+    for (int g8 = 0; g8 < 8; ++g8) {
+      float sg = 0.0f;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) sg += cn[(g8 * 4 + q) * CNP + tid * D];
+      s += sg;
+    }
+    j.bias[(size_t)bx * p.O32 + o0 + tid] = s;
+  }
+  if (j.Cf) {  // the pack's k-blocks of input block bx, lanes of these 8 outputs
+    const int ob = o0 >> 5, olo = o0 & 31;
+    for (int item = tid; item < 2 * P * 16; item += kDcPackThreads) {
+      const int kbl = item >> 4, g = (item >> 3) & 1, oj = item & 7;
+      const int kb = bx * 2 * P + kbl;
+      if (kb >= p.KB) continue;
+      const int lane = olo + oj + 32 * g;
+      const int r = kb / G::SGK, q = kb - r * G::SGK;
+      const int s = q / G::KBG, h = q - s * G::KBG;
+      float v[8];
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) {
+        const int vv = 8 * h + jj;
+        const int u = vv / P, d = vv % P + 1;
+        const int i = r * G::SGI + g * 2 * G::IPG + s * (G::IPG / 2) + u;
+        v[jj] = d <= p.deg ? cn[(i - i0) * CNP + oj * D + d] : 0.0f;
+      }
+      store_frag<BF>(j.Cf + cf_elem<BF>(p.KB, ob, kb, lane) - (size_t)lane * 8, lane, v);
+    }
+  }
+  if (j.Cb) {  // output k-block o0 / 16, half (o0 / 8) % 2
+    const int kbx = o0 >> 4, g = (o0 >> 3) & 1;
+    for (int item = tid; item < P * 32; item += kDcPackThreads) {
+      const int e = item >> 5, il = item & 31;
+      float v[8];
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj)
+        v[jj] = (e + 1 <= p.deg) ? cn[il * CNP + jj * D + e + 1] * (float)(e + 1) : 0.0f;
+      store_frag<BF>(j.Cb + ((size_t)(bx * P + e) * p.KBx + kbx) * kFragElems, il + 32 * g, v);
+    }
+  }
+}
+
+// Two layers' dC-and-pack in one launch: blocks [0, a.nblocks) take a, the
+// next b.nblocks (may be 0) b, and with lm.part one more block the step's
+// loss mean.
+template <int DMAX, int P, bool BF>
+__global__ void __launch_bounds__(kDcPackThreads)
+k_dc_pack2(DcPackJob<BF> a, DcPackJob<BF> b, LossMean lm) {
+  const int bid = blockIdx.x;
+  if (bid < a.nblocks) dc_pack_body<DMAX, P, BF>(a, bid % a.nx, bid / a.nx);
+  else if (bid < a.nblocks + b.nblocks)
+    dc_pack_body<DMAX, P, BF>(b, (bid - a.nblocks) % b.nx, (bid - a.nblocks) / b.nx);
+  else loss_mean_block(lm);
 }
 
 // Small dx: dx[b, i] = t'(x) sum_e U_e(t) sum_o dy[b, o] Cb(i, o, e) for
@@ -1042,6 +1203,51 @@ void launch_dc_small(const float* dy, const float* t, float* dC, DcOut om, const
     case 8: hipLaunchKernelGGL((k_dc_small<9>), grid, dim3(256), 0, s, dy, t, dC, om, p); break;
     default: hipLaunchKernelGGL((k_dc_small<17>), grid, dim3(256), 0, s, dy, t, dC, om, p); break;
   }
+}
+
+bool dc_pack_ok(const Plan& p) {
+  return dc_small_ok(p) && p.P <= 8 && ceil_div(p.I, 32) * ceil_div(p.O, 8) < (1 << 29);
+}
+
+template <int P, bool BF>
+static void launch_dc_pack_t(const DcPackArgs& a, const DcPackArgs* b, const LossMean& lm,
+                             hipStream_t s) {
+  typedef typename Elem<BF>::type E;
+  auto job = [](const DcPackArgs& x) {
+    DcPackJob<BF> j;
+    const Plan& q = x.p;
+    char* base = reinterpret_cast<char*>(x.packed);
+    j.dy = x.dy;
+    j.t = x.t;
+    j.C = x.C;
+    j.om = x.om;
+    j.p = q;
+    j.Cf = x.cf ? reinterpret_cast<E*>(base) : nullptr;
+    // the pack's bias pointer: the bias itself when there is one input block
+    j.bias = x.cf ? reinterpret_cast<float*>(base + (q.NIB == 1 ? packed_biasf_offset(q)
+                                                                 : packed_bias_offset(q)))
+                  : nullptr;
+    j.Cb = x.cb ? reinterpret_cast<E*>(base) + packed_cf_elems(q) : nullptr;
+    j.nx = (int)ceil_div(q.I, 32);
+    j.nblocks = j.nx * (int)ceil_div(q.O, 8);
+    return j;
+  };
+  const DcPackJob<BF> ja = job(a);
+  DcPackJob<BF> jb{};
+  if (b) jb = job(*b);
+  const dim3 grid((unsigned)(ja.nblocks + jb.nblocks + (lm.part ? 1 : 0)));
+  hipLaunchKernelGGL((k_dc_pack2<P + 1, P, BF>), grid, dim3(kDcPackThreads), 0, s, ja, jb, lm);
+}
+
+void launch_dc_pack(const DcPackArgs& a, const DcPackArgs* b, hipStream_t s, LossMean lm) {
+  const bool bf = a.p.esz == 2;
+#define CKAN_DCP(PP) bf ? launch_dc_pack_t<PP, true>(a, b, lm, s) : launch_dc_pack_t<PP, false>(a, b, lm, s)
+  switch (a.p.P) {
+    case 2: CKAN_DCP(2); break;
+    case 4: CKAN_DCP(4); break;
+    default: CKAN_DCP(8); break;
+  }
+#undef CKAN_DCP
 }
 
 void launch_prep_dy(const float* dy, void* dYx, void* dYc, float* colsum_part, const Plan& p,

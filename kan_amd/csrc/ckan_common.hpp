@@ -116,13 +116,16 @@ struct LossMean {
   float* out2;
 };
 
-// The sum of LossMean by one 256-thread block in a fixed order: strided
-// per-thread sums, then a tree (k_sum_scalar's order, so the same bits).
+// The sum of LossMean by one block (256 threads or more; the first 256 do
+// the work) in a fixed order: strided per-thread sums, then a tree
+// (k_sum_scalar's order, so the same bits).
 __device__ __forceinline__ void loss_mean_block(const LossMean& lm) {
   __shared__ float red[256];
-  float s = 0.0f;
-  for (int64_t k = threadIdx.x; k < lm.n; k += 256) s += lm.part[k];
-  red[threadIdx.x] = s;
+  if (threadIdx.x < 256) {
+    float s = 0.0f;
+    for (int64_t k = threadIdx.x; k < lm.n; k += 256) s += lm.part[k];
+    red[threadIdx.x] = s;
+  }
   __syncthreads();
   for (int w = 128; w > 0; w >>= 1) {
     if (threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
@@ -157,6 +160,25 @@ __device__ __forceinline__ float adam_update(float pv, float g, float* m, float*
   *m = mv;
   *v = vv;
   return pv + neg_step * (mv / denom);
+}
+
+// Writes g into d as the mode says, with old the value d holds (read ahead
+// by the caller), and returns the value stored.
+__device__ __forceinline__ float dc_apply_from(float* d, float old, float g, const DcOut& o) {
+  float v;
+  if (o.mode == kDcStore) {
+    v = g;
+  } else if (o.mode == kDcAccumulate) {
+    v = old + g;
+  } else if (o.mode == kDcSgd) {
+    v = sgd_update(old, g, o.lr, o.wd);
+  } else {
+    const size_t q = (size_t)(d - o.base);
+    v = adam_update(old, g, o.m + q, o.v + q, o.w1, o.beta2, o.one_m_beta2, o.eps, o.wd, o.sc[0],
+                    o.sc[1]);
+  }
+  *d = v;
+  return v;
 }
 
 __device__ __forceinline__ void dc_write(float* d, float g, const DcOut& o) {

@@ -510,6 +510,11 @@ struct ckan_exec {
   int64_t* step = nullptr;     // Adam step count (device)
   float* adam_sc = nullptr;    // Adam scalars (device)
   bool tiny = false;           // the whole step runs as one k_tiny_step launch
+  // A two-layer cross-entropy stack whose packed operands are kept current by
+  // the step's dC launch (self_pack_pair_fits): the step runs no pack, and
+  // every other change of C (creation, ckan_exec_set_coeffs) packs at once.
+  // Layer 0's dX operand is not kept (the first layer has no dX).
+  bool self_pack = false;
   // graph mode
   hipStream_t es = nullptr;
   hipEvent_t ev_in = nullptr, ev_out = nullptr;
@@ -614,11 +619,45 @@ int run_tiny(ckan_exec* ex, const float* x, const void* target, float* losses, h
   return hipGetLastError() == hipSuccess ? CKAN_OK : efail(CKAN_ERR_HIP, "executor: step launch failed");
 }
 
+// The optimizer write mode of layer ly's dC.
+DcOut step_mode(const ckan_exec* ex, ckan_exec::Layer& ly) {
+  const auto& c = ex->cfg;
+  if (c.optimizer == CKAN_OPT_SGD) return DcOut{kDcSgd, c.lr, c.weight_decay};
+  return DcOut{kDcAdam, 0.0f, c.weight_decay, (float)(1.0 - (double)c.beta1), c.beta2,
+               (float)(1.0 - (double)c.beta2), c.eps, ly.C, ly.m, ly.v, ex->adam_sc};
+}
+
+// The step of a self_pack stack, three launches: layer 0's forward (its GEMM
+// maps x itself) leaving split partials; the fused tail (layer 1's forward,
+// the loss gradient and layer 1's dX into layer 0's dy); both layers' dC with
+// the optimizer step, writing the packed operands the next step reads, and
+// the loss mean.
+int run_step_self_packed(ckan_exec* ex, const float* x, const void* target, hipStream_t s,
+                         float* loss_copy) {
+  auto& a = ex->layers[0];
+  auto& b = ex->layers[1];
+  const auto& c = ex->cfg;
+  int rc;
+  if ((rc = forward_tail_ce_packed(&a.desc, a.packed, x, a.t, &b.desc, b.C, b.t, b.y,
+                                   reinterpret_cast<const int64_t*>(target), b.dy, ex->loss_part,
+                                   a.dy, ex->fws, ex->fws_bytes, s)))
+    return rc;
+  if (c.optimizer != CKAN_OPT_SGD) {
+    hipLaunchKernelGGL(k_adam_scalars, dim3(1), dim3(64), 0, s, ex->step, (double)c.lr,
+                       (double)c.beta1, (double)c.beta2, ex->adam_sc);
+    if (hipGetLastError() != hipSuccess) return efail(CKAN_ERR_HIP, "executor: adam launch failed");
+  }
+  const LossMean lm{ex->loss_part, c.batch, (float)(1.0 / (double)c.batch), ex->loss, loss_copy};
+  return backward_self_packed(&a.desc, a.t, a.dy, a.C, step_mode(ex, a), a.packed, &b.desc, b.t,
+                              b.dy, b.C, step_mode(ex, b), b.packed, lm, s);
+}
+
 // The step body on stream s with inputs x / target; the loss also goes to
 // loss_copy when given.
 int run_step(ckan_exec* ex, const float* x, const void* target, hipStream_t s,
              float* loss_copy = nullptr) {
   if (ex->tiny) return run_tiny(ex, x, target, loss_copy, s);
+  if (ex->self_pack) return run_step_self_packed(ex, x, target, s, loss_copy);
   const int L = (int)ex->layers.size();
   int rc;
   for (int l = 0; l < L; ++l) {
@@ -697,11 +736,7 @@ int run_step(ckan_exec* ex, const float* x, const void* target, hipStream_t s,
   for (int l = L - 1; l >= 0; --l) {
     auto& ly = ex->layers[l];
     float* dx = l > 0 ? ex->layers[l - 1].dy : nullptr;
-    DcOut om{kDcSgd, c.lr, c.weight_decay};
-    if (!sgd) {
-      om = DcOut{kDcAdam, 0.0f, c.weight_decay, (float)(1.0 - (double)c.beta1), c.beta2,
-                 (float)(1.0 - (double)c.beta2), c.eps, ly.C, ly.m, ly.v, ex->adam_sc};
-    }
+    const DcOut om = step_mode(ex, ly);
     const LossMean* lm = tail && l == L - 1 ? &lm_tail : nullptr;
     if (ly.family && !layer_on_valu(&ly.desc)) {
       // dC' into gcheb, then dC = dC' M^T and the optimizer step into C
@@ -833,6 +868,13 @@ int ckan_exec_create_basis(const ckan_exec_config* cfg, const ckan_basis_spec* b
     }
   }
   if (rc == CKAN_OK) ex->tiny = tiny_eligible(ex);
+  if (rc == CKAN_OK && !ex->tiny && cfg->n_layers == 2 && ex->layers[0].tail_ce &&
+      !(cfg->flags & CKAN_EXEC_PACK_EACH_STEP) &&
+      self_pack_pair_fits(&ex->layers[0].desc, &ex->layers[1].desc)) {
+    ex->self_pack = true;
+    for (int l = 0; l < 2 && rc == CKAN_OK; ++l)
+      rc = self_pack_layer(&ex->layers[l].desc, ex->layers[l].C, ex->layers[l].packed, s);
+  }
   if (rc == CKAN_OK && cfg->use_graph) {
     const int O = ex->widths[cfg->n_layers];
     ex->tgt_bytes = cfg->loss == CKAN_LOSS_MSE ? (size_t)cfg->batch * O * 4 : (size_t)cfg->batch * 8;
@@ -878,7 +920,9 @@ int ckan_exec_set_coeffs(ckan_exec* ex, int32_t layer, const float* src, void* s
   auto& ly = ex->layers[layer];
   hipLaunchKernelGGL(k_copy_f32, dim3(grid_of(ly.ncoef)), dim3(256), 0,
                      reinterpret_cast<hipStream_t>(stream), src, ly.C, ly.ncoef);
-  return hipGetLastError() == hipSuccess ? CKAN_OK : efail(CKAN_ERR_HIP, "executor: copy failed");
+  if (hipGetLastError() != hipSuccess) return efail(CKAN_ERR_HIP, "executor: copy failed");
+  // the packed operands follow C (the step itself does not pack)
+  return ex->self_pack ? self_pack_layer(&ly.desc, ly.C, ly.packed, stream) : CKAN_OK;
 }
 
 int ckan_exec_get_coeffs(ckan_exec* ex, int32_t layer, float* dst, void* stream) {

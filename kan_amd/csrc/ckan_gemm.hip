@@ -19,19 +19,35 @@
 
 namespace ckan {
 
-// s0 + sum_{z < n} src[z * stride], added in z order; loads are issued 8 at a
-// time so a long split count does not serialise on memory latency.
+// s0 + sum_{z < n} src[z * stride] (n >= 1), added in z order.  Every load of
+// a round is issued before its first addition, so a long split count does not
+// serialise on memory latency: up to 16 terms one round of 16, else rounds of
+// 64 (the fused cross-entropy tail sums 49 splits per output).  The loads are
+// unconditional, past n from the last term's address (a load under a branch
+// is waited for inside that branch, one round trip per term), and a
+// scheduling barrier keeps them ahead of the additions (left to itself the
+// compiler issued them 8 at a time, each batch waited for).
 __device__ __forceinline__ float split_sum(const float* __restrict__ src, size_t stride,
                                            unsigned n, float s0) {
-  // 16 loads in flight per round trip (small-batch forwards split up to 64
-  // ways); the additions stay in split order
   float s = s0;
-  for (unsigned z0 = 0; z0 < n; z0 += 16) {
+  if (n <= 16) {
     float v[16];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) v[j] = (z0 + j < n) ? src[(size_t)(z0 + j) * stride] : 0.0f;
+    for (int j = 0; j < 16; ++j) v[j] = src[(size_t)((unsigned)j < n ? j : n - 1) * stride];
+    __builtin_amdgcn_sched_barrier(0);  // every load issued before the first use
 #pragma unroll
-    for (int j = 0; j < 16; ++j) s += v[j];
+    for (int j = 0; j < 16; ++j)
+      if ((unsigned)j < n) s += v[j];
+    return s;
+  }
+  for (unsigned z0 = 0; z0 < n; z0 += 64) {
+    float v[64];
+#pragma unroll
+    for (int j = 0; j < 64; ++j) v[j] = src[(size_t)(z0 + j < n ? z0 + j : n - 1) * stride];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < 64; ++j)
+      if (z0 + j < n) s += v[j];
   }
   return s;
 }
@@ -44,12 +60,16 @@ __device__ __forceinline__ float split_sum(const float* __restrict__ src, size_t
 // With gridDim.z > 1 the SGs are split over blocks; each block writes its
 // partial tile to the workspace and k_fwd_reduce, a separate launch, adds the
 // partials in fixed split order.
-template <int P, bool BF, int NM, int NN, int WGM, int WGN>
+// XT: tc is x itself (rows unpadded, I == I_sg, 16-byte aligned); the block
+// maps each value by the input map as it loads it (the arithmetic of
+// launch_tanh), and the first column block's first wave column stores the
+// mapped values into the tanh cache tout for the backward (each value once).
+template <int P, bool BF, int NM, int NN, int WGM, int WGN, bool XT = false>
 __global__ void __launch_bounds__(256)
 k_fwd(const float* __restrict__ tc, const typename Elem<BF>::type* __restrict__ Cf,
       const float* __restrict__ bias_f, float* __restrict__ y, float* __restrict__ part,
       Plan p, int sg_per_split, const float* __restrict__ bias_part, int nib,
-      float* __restrict__ bias_out) {
+      float* __restrict__ bias_out, float* __restrict__ tout) {
   typedef typename Elem<BF>::type E;
   typedef FwdGroup<P> G;
   static_assert(WGM * WGN == 4, "4 waves per block");
@@ -151,8 +171,22 @@ k_fwd(const float* __restrict__ tc, const typename Elem<BF>::type* __restrict__ 
       float tv[G::LANE_T];
 #pragma unroll
       for (int q = 0; q < G::LANE_T / 4; ++q) {
+        if constexpr (XT) {
+          f32x4_t m;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) m[e] = input_map(tcur[mi][q][e], p.imap, p.ima, p.imb);
+          tcur[mi][q] = m;
+        }
         tv[4 * q + 0] = tcur[mi][q][0]; tv[4 * q + 1] = tcur[mi][q][1];
         tv[4 * q + 2] = tcur[mi][q][2]; tv[4 * q + 3] = tcur[mi][q][3];
+      }
+      if constexpr (XT) {  // the waves along N map the same rows: the first stores them
+        if (blockIdx.y == 0 && wn == 0 && rvalid[mi]) {
+          const int64_t r = m_blk + (wm * NM + mi) * 32 + (lane & 31);
+          f32x4_t* dst = reinterpret_cast<f32x4_t*>(tout + r * p.I_sg + (size_t)sg * G::SGI + g * G::LANE_T);
+#pragma unroll
+          for (int q = 0; q < G::LANE_T / 4; ++q) dst[q] = tcur[mi][q];
+        }
       }
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
@@ -759,14 +793,52 @@ k_fwd_reduce(const float* __restrict__ part, int S, const float* __restrict__ bi
 // k_sum_scalar takes in k_ce_small's order.  Ib <= 64, Ob <= kTailO; the
 // block stages Cb in LDS (Ib Ob Db <= kTailC floats), its coalesced loads
 // issued ahead of the split sums so that both latencies overlap.
+// With dxa, lane i also writes layer b's dX for the row, dL/dy_a[r, i] =
+// (1 - t_i^2) sum_e U_e(t_i) sum_k dy[k] (e + 1) Cb[i, k, e + 1] over e < Pb
+// (b's padded degree), in k_dx_small's arithmetic (the same bits): the row's
+// gradient dy[k] is broadcast from lane k, and the operand (e + 1) Cb is
+// formed as the pack forms it.
 constexpr int kTailO = 16, kTailRows = 4, kTailC = 8192, kTailCL = 16;
+
+// Lane i's dX of the row for b's padded degree PB: c = Cb[i] staged [Ob][Db],
+// dmine the row's dy of this lane's class (read from lane k for class k), t
+// its input.  Reads are unconditional from in-range addresses and classes
+// past Ob leave g unchanged, so g[e] takes k_dx_small's additions in its
+// order.  b's input map is tanh (the tail's precondition): dt/dy_a = 1 - t^2.
+template <int PB>
+__device__ __forceinline__ float tail_dx(const float* c, int Ob, int Db, float dmine, float t) {
+  float g[PB];
+#pragma unroll
+  for (int e = 0; e < PB; ++e) g[e] = 0.0f;
+#pragma unroll
+  for (int k = 0; k < kTailO; ++k) {
+    const int kk = k < Ob ? k : 0;
+    const float a = __shfl(dmine, kk);
+#pragma unroll
+    for (int e = 0; e < PB; ++e) {
+      const float cc = c[kk * Db + (e + 1 < Db ? e + 1 : 0)];
+      const float w = e + 1 < Db ? cc * (float)(e + 1) : 0.0f;  // the packed dX operand's value
+      g[e] = k < Ob ? fmaf(a, w, g[e]) : g[e];
+    }
+  }
+  const float t2 = t + t;
+  float up = 0.0f, u = 1.0f, sd = 0.0f;  // U_{e-1}, U_e
+#pragma unroll
+  for (int e = 0; e < PB; ++e) {
+    sd = fmaf(g[e], u, sd);
+    const float un = fmaf(t2, u, -up);
+    up = u;
+    u = un;
+  }
+  return sd * (1.0f - t * t);
+}
 
 __global__ void __launch_bounds__(256)
 k_fwd_tail_ce(const float* __restrict__ part, int S, const float* __restrict__ bias_f, Plan pa,
               const float* __restrict__ bias_part, int nib, float* __restrict__ bias_out,
               float* __restrict__ tb, const float* __restrict__ Cb, int Ob, int Db,
               float* __restrict__ yb, const int64_t* __restrict__ labels, float* __restrict__ dyb,
-              float* __restrict__ loss_part) {
+              float* __restrict__ loss_part, float* __restrict__ dxa, int Pb) {
   extern __shared__ float csh[];  // Cb [Ib][Ob][Db]
   const int tid = threadIdx.x, lane = tid & 63;
   const int64_t r = (int64_t)blockIdx.x * kTailRows + (tid >> 6);
@@ -814,9 +886,13 @@ k_fwd_tail_ce(const float* __restrict__ part, int S, const float* __restrict__ b
     float tm = 1.0f, tc = t;  // T_{d-1}, T_d from d = 0
     for (int d = 0; d < Db; ++d) {
       const float td = d == 0 ? 1.0f : tc;
+      // reads from in-range addresses, unconditional: an LDS read under a
+      // branch is waited for inside it (one round trip per read)
+      float cv[kTailO];
 #pragma unroll
-      for (int k = 0; k < kTailO; ++k)
-        if (k < Ob) acc[k] = fmaf(c[k * Db + d], td, acc[k]);
+      for (int k = 0; k < kTailO; ++k) cv[k] = c[(k < Ob ? k : 0) * Db + d];
+#pragma unroll
+      for (int k = 0; k < kTailO; ++k) acc[k] = k < Ob ? fmaf(cv[k], td, acc[k]) : acc[k];
       if (d > 0) {
         const float tn = fmaf(t2, tc, -tm);
         tm = tc;
@@ -849,11 +925,23 @@ k_fwd_tail_ce(const float* __restrict__ part, int S, const float* __restrict__ b
     if (k == lab) yl = acc[k];
     if (k == lane) mine = acc[k];
   }
+  const float dmine = (expf(mine - m) / sm - (lane == lab ? 1.0f : 0.0f)) * inv_b;
   if (lane < Ob) {
     yb[r * Ob + lane] = mine;
-    dyb[r * Ob + lane] = (expf(mine - m) / sm - (lane == lab ? 1.0f : 0.0f)) * inv_b;
+    dyb[r * Ob + lane] = dmine;
   }
   if (lane == 0) loss_part[r] = (logf(sm) + m) - ((lab >= 0 && lab < Ob) ? yl : 0.0f);
+  if (dxa) {
+    const float* c = csh + (lane < Ib ? lane : 0) * Ob * Db;
+    float dx;
+    switch (Pb) {
+      case 2: dx = tail_dx<2>(c, Ob, Db, dmine, t); break;
+      case 4: dx = tail_dx<4>(c, Ob, Db, dmine, t); break;
+      case 8: dx = tail_dx<8>(c, Ob, Db, dmine, t); break;
+      default: dx = tail_dx<16>(c, Ob, Db, dmine, t); break;
+    }
+    if (lane < Ib) __builtin_nontemporal_store(dx, dxa + r * Ib + lane);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -2684,7 +2772,13 @@ FwdChoice choose_fwd(const Plan& p) {
   if (p.B <= 32) {
     c.tile = kFwdSmall32; c.bm = 32; c.bnf = 4;
   } else if (p.B <= 64 || (p.B <= 512 && ceil_div(p.B, 256) * ceil_div(p.NBf, 4) < 64)) {
-    c.tile = kFwdSmall64; c.bm = 64; c.bnf = 4;
+    // at most 2 output fragments: 2 x 2 waves, none idle (config 2's 784 -> 64
+    // forward 13.4 -> 10.6 us with the tanh in the kernel)
+    if (p.NBf <= 2) {
+      c.tile = kFwdSmall64N2; c.bm = 64; c.bnf = 2;
+    } else {
+      c.tile = kFwdSmall64; c.bm = 64; c.bnf = 4;
+    }
   } else {
     c.tile = kFwdBig; c.bm = 256; c.bnf = 4;
   }
@@ -2712,7 +2806,7 @@ FwdChoice choose_fwd(const Plan& p) {
 template <int P, bool BF>
 static void fwd_dispatch(const float* x, float* t, const void* packed, float* y, void* ws,
                          const Plan& p, const FwdChoice& c, hipStream_t s, int nib,
-                         bool out_tanh, bool reduce) {
+                         bool out_tanh, bool reduce, bool xt) {
   typedef typename Elem<BF>::type E;
   const E* Cf = reinterpret_cast<const E*>(packed);
   char* pk = const_cast<char*>(reinterpret_cast<const char*>(packed));
@@ -2752,20 +2846,37 @@ static void fwd_dispatch(const float* x, float* t, const void* packed, float* y,
   } else {
     dim3 grid(c.tiles_m, c.tiles_n, c.splits);
     switch (c.tile) {
+      // xt: the kernel maps x itself and stores the tanh cache t
       case kFwdSmall32:
-        hipLaunchKernelGGL((k_fwd<P, BF, 1, 1, 1, 4>), grid, dim3(256), 0, s, t, Cf, bias, y, part,
-                           p, c.sg_per_split, bpart, nib_k, bias_out);
+        if (xt)
+          hipLaunchKernelGGL((k_fwd<P, BF, 1, 1, 1, 4, true>), grid, dim3(256), 0, s, x, Cf, bias, y,
+                             part, p, c.sg_per_split, bpart, nib_k, bias_out, t);
+        else
+          hipLaunchKernelGGL((k_fwd<P, BF, 1, 1, 1, 4>), grid, dim3(256), 0, s, t, Cf, bias, y, part,
+                             p, c.sg_per_split, bpart, nib_k, bias_out, nullptr);
+        break;
+      case kFwdSmall64N2:
+        if (xt)
+          hipLaunchKernelGGL((k_fwd<P, BF, 1, 1, 2, 2, true>), grid, dim3(256), 0, s, x, Cf, bias, y,
+                             part, p, c.sg_per_split, bpart, nib_k, bias_out, t);
+        else
+          hipLaunchKernelGGL((k_fwd<P, BF, 1, 1, 2, 2>), grid, dim3(256), 0, s, t, Cf, bias, y, part,
+                             p, c.sg_per_split, bpart, nib_k, bias_out, nullptr);
         break;
       case kFwdSmall64:
-        hipLaunchKernelGGL((k_fwd<P, BF, 2, 1, 1, 4>), grid, dim3(256), 0, s, t, Cf, bias, y, part,
-                           p, c.sg_per_split, bpart, nib_k, bias_out);
+        if (xt)
+          hipLaunchKernelGGL((k_fwd<P, BF, 2, 1, 1, 4, true>), grid, dim3(256), 0, s, x, Cf, bias, y,
+                             part, p, c.sg_per_split, bpart, nib_k, bias_out, t);
+        else
+          hipLaunchKernelGGL((k_fwd<P, BF, 2, 1, 1, 4>), grid, dim3(256), 0, s, t, Cf, bias, y, part,
+                             p, c.sg_per_split, bpart, nib_k, bias_out, nullptr);
         break;
       default:
         if constexpr (FwdPipe<P, BF>::kOk) {
           typedef FwdPipe<P, BF> K;
           if (!fwd_pipe_offsets_fit(p)) {  // per-lane copy offsets are 32-bit
             hipLaunchKernelGGL((k_fwd<P, BF, 2, 4, 4, 1>), grid, dim3(256), 0, s, t, Cf, bias, y,
-                               part, p, c.sg_per_split, bpart, nib_k, bias_out);
+                               part, p, c.sg_per_split, bpart, nib_k, bias_out, nullptr);
             break;
           }
           const size_t lds = (size_t)K::LDS_BYTES;
@@ -2786,7 +2897,7 @@ static void fwd_dispatch(const float* x, float* t, const void* packed, float* y,
           }
         } else {
           hipLaunchKernelGGL((k_fwd<P, BF, 2, 4, 4, 1>), grid, dim3(256), 0, s, t, Cf, bias, y,
-                             part, p, c.sg_per_split, bpart, nib_k, bias_out);
+                             part, p, c.sg_per_split, bpart, nib_k, bias_out, nullptr);
         }
         break;
     }
@@ -2830,12 +2941,18 @@ bool fwd_sums_bias(const Plan& p, const FwdChoice& c) {
   return true;
 }
 
+bool fwd_maps_x_ok(const Plan& p, const FwdChoice& c, const float* x) {
+  return (c.tile == kFwdSmall32 || c.tile == kFwdSmall64 || c.tile == kFwdSmall64N2) &&
+         p.I == p.I_sg && p.I % 4 == 0 &&
+         is_al16(x);
+}
+
 void launch_fwd_gemm(const float* x, float* t, const void* packed, float* y, void* ws,
                      const Plan& p, const FwdChoice& c, hipStream_t s, bool sum_bias,
-                     bool out_tanh, bool reduce) {
+                     bool out_tanh, bool reduce, bool xt) {
   const bool bf = p.esz == 2;
   const int nib = sum_bias && fwd_sums_bias(p, c) ? p.NIB : 0;
-#define CKAN_FW(PP, BB) fwd_dispatch<PP, BB>(x, t, packed, y, ws, p, c, s, nib, out_tanh, reduce)
+#define CKAN_FW(PP, BB) fwd_dispatch<PP, BB>(x, t, packed, y, ws, p, c, s, nib, out_tanh, reduce, xt)
   switch (p.P) {
     case 2: bf ? CKAN_FW(2, true) : CKAN_FW(2, false); break;
     case 4: bf ? CKAN_FW(4, true) : CKAN_FW(4, false); break;
@@ -3077,7 +3194,8 @@ bool fwd_tail_ce_ok(const Plan& pa, const FwdChoice& ca, int Ob, int Db) {
 
 void launch_fwd_tail_ce(const void* packed_a, void* ws, const Plan& pa, const FwdChoice& ca,
                         bool sum_bias, float* tb, const float* Cb, int Ob, int Db, float* yb,
-                        const int64_t* labels, float* dyb, float* loss_part, hipStream_t s) {
+                        const int64_t* labels, float* dyb, float* loss_part, hipStream_t s,
+                        float* dxa) {
   char* pk = const_cast<char*>(reinterpret_cast<const char*>(packed_a));
   const float* bias = reinterpret_cast<const float*>(pk + packed_biasf_offset(pa));
   const float* bpart = reinterpret_cast<const float*>(pk + packed_bias_offset(pa));
@@ -3087,7 +3205,7 @@ void launch_fwd_tail_ce(const void* packed_a, void* ws, const Plan& pa, const Fw
   const size_t lds = (size_t)pa.O * Ob * Db * sizeof(float);
   hipLaunchKernelGGL(k_fwd_tail_ce, dim3(grid), dim3(64 * kTailRows), lds, s,
                      reinterpret_cast<const float*>(ws), ca.splits, bias, pa, bpart, nib, bias_out,
-                     tb, Cb, Ob, Db, yb, labels, dyb, loss_part);
+                     tb, Cb, Ob, Db, yb, labels, dyb, loss_part, dxa, padded_degree(Db - 1));
 }
 
 }  // namespace ckan

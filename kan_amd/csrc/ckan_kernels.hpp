@@ -34,7 +34,8 @@ inline size_t packed_bytes(const Plan& p) {
 // Tile shapes (waves along M x waves along N, fragments per wave M x N):
 enum FwdTile {
   kFwdBig = 0, kFwdSmall32 = 1, kFwdSmall64 = 2, kFwdStream32 = 3, kFwdStream64 = 4,
-  kFwdCols = 5    // B <= 16, bf16: column-owning blocks, one launch (tanh in the kernel up to 4 rows)
+  kFwdCols = 5,   // B <= 16, bf16: column-owning blocks, one launch (tanh in the kernel up to 4 rows)
+  kFwdSmall64N2 = 6  // 64 rows x 2 output fragments, 2 x 2 waves (outputs <= 64: no idle wave column)
 };
 struct FwdChoice {
   int tile;           // FwdTile
@@ -182,19 +183,25 @@ void launch_dc_sum(const float* part, int S, float* dC, DcOut om, const Plan& p,
 // the caller launches the reduction first otherwise.
 // out_tanh: store tanh(y) in place of y (the next layer's tanh cache in a
 // stack; needs fwd_out_tanh_ok).
+// xt (needs fwd_maps_x_ok): the GEMM reads x, maps it itself and writes the
+// tanh cache t (no launch_tanh before it).
 void launch_fwd_gemm(const float* x, float* t, const void* packed, float* y, void* ws,
                      const Plan& p, const FwdChoice& c, hipStream_t s, bool sum_bias = false,
-                     bool out_tanh = false, bool reduce = true);
+                     bool out_tanh = false, bool reduce = true, bool xt = false);
+bool fwd_maps_x_ok(const Plan& p, const FwdChoice& c, const float* x);
 // reduce = false above leaves a split forward's partials in ws for
 // launch_fwd_tail_ce, which sums them (the last two layers of a stack
 // trained with cross-entropy, when fwd_tail_ce_ok holds): layer a's split
 // sum into b's tanh cache tb, layer b's forward from its fp32 coefficients
 // Cb [Ib = a.O, Ob, Db] into yb, and the rows' cross-entropy gradient dyb and
 // losses loss_part (their mean: k_sum_scalar).
+// dxa (optional): also layer b's dX into dxa [B, a.O] (dL/dy_a; b's input
+// map tanh), the bits of launch_dx_small on b's packed dX operand.
 bool fwd_tail_ce_ok(const Plan& pa, const FwdChoice& ca, int Ob, int Db);
 void launch_fwd_tail_ce(const void* packed_a, void* ws, const Plan& pa, const FwdChoice& ca,
                         bool sum_bias, float* tb, const float* Cb, int Ob, int Db, float* yb,
-                        const int64_t* labels, float* dyb, float* loss_part, hipStream_t s);
+                        const int64_t* labels, float* dyb, float* loss_part, hipStream_t s,
+                        float* dxa = nullptr);
 bool fwd_sums_bias(const Plan& p, const FwdChoice& c);
 // The forward path of p can store tanh(y) in place of y (the pipelined
 // kernel, unsplit).
@@ -221,6 +228,27 @@ bool bwd_small_one_launch(const Plan& p);
 void launch_bwd_small(const float* dy, const void* packed, const float* t, float* dx, float* dC,
                       DcOut om, const Plan& p, hipStream_t s,
                       LossMean lm = LossMean{});
+// The small dC with an optimizer step (om: kDcSgd or kDcAdam on C) that also
+// writes the layer's packed operands from the updated coefficients, bit for
+// bit as launch_pack would write them from C after the step: the forward
+// operand and bias partials (cf; the bias partials are those of a forward
+// that sums them, reduce_bias = false) and the dX operand (cb).  Other
+// entries of `packed` (padding, and the parts not requested) keep what the
+// last pack wrote.  dc_pack_ok: dc_small_ok and P <= 8.
+struct DcPackArgs {
+  const float* dy;
+  const float* t;
+  float* C;
+  DcOut om;
+  Plan p;
+  void* packed;
+  bool cf, cb;
+};
+bool dc_pack_ok(const Plan& p);
+// a and b (optional, same P and compute type) in one launch, with the loss
+// mean lm (optional) by one more block.
+void launch_dc_pack(const DcPackArgs& a, const DcPackArgs* b, hipStream_t s,
+                    LossMean lm = LossMean{});
 void launch_loss_mean(const LossMean& lm, hipStream_t s);
 void launch_dc_gemm(const void* dYc, const float* t, const float* colsum, float* part, float* dC,
                     DcOut om, const Plan& p, const BwdLayout& L, hipStream_t s);
@@ -274,6 +302,31 @@ int pack2_forward_tail_ce(const struct ckan_desc* da, const void* Ca, void* pka,
                           float* ta, bool ta_ready, const struct ckan_desc* db, const void* Cb,
                           void* pkb, float* tb, float* yb, const int64_t* labels, float* dyb,
                           float* loss_part, void* ws, size_t ws_bytes, void* stream);
+// A two-layer stack trained with cross-entropy whose packed operands the
+// step's dC launch keeps current, so that the step runs no pack:
+// self_pack_pair_fits: pack2_tail_ce_fits, both layers on the small dC path
+// with the packing epilogue (dc_pack_ok), b's dX on the small path, same P and
+// compute type, a's bias summed from its partials by the tail.
+// self_pack_layer: the pack that makes `packed` current after C changes other
+// than by a step (creation, a copy into C); the packs of the per-step path
+// without the tanh, so the same bytes.
+// forward_tail_ce_packed: pack2_forward_tail_ce without the pack (a's GEMM
+// maps x itself where fwd_maps_x_ok holds, else launch_tanh first); the tail
+// also writes b's dX into dya (a's dy).
+// backward_self_packed: one launch of both layers' dC with the optimizer step
+// (oma, omb: kDcSgd or kDcAdam) that writes a's forward operand and bias
+// partials and b's dX operand from the updated coefficients (a, the first
+// layer, has no dX), and takes the loss mean lm along.
+bool self_pack_pair_fits(const struct ckan_desc* a, const struct ckan_desc* b);
+int self_pack_layer(const struct ckan_desc* desc, const void* C, void* packed, void* stream);
+int forward_tail_ce_packed(const struct ckan_desc* da, const void* pka, const float* xa, float* ta,
+                           const struct ckan_desc* db, const void* Cb, float* tb, float* yb,
+                           const int64_t* labels, float* dyb, float* loss_part, float* dya,
+                           void* ws, size_t ws_bytes, void* stream);
+int backward_self_packed(const struct ckan_desc* da, const float* ta, const float* dya, float* Ca,
+                         const DcOut& oma, void* pka, const struct ckan_desc* db, const float* tb,
+                         const float* dyb, float* Cb, const DcOut& omb, void* pkb,
+                         const LossMean& lm, void* stream);
 // the Plan-level launch behind pack2_forward_ex (xa, ta: a's fused tanh, or null)
 bool pack_pair_ok(const Plan& a, const Plan& b);
 void launch_pack_pair(const float* Ca, void* pa, const Plan& qa, bool reduce_a, const float* xa,

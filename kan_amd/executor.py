@@ -87,14 +87,17 @@ class ResidentExecutor:
     ``bases``: per layer, a basis spec (``_lib.make_spec``; None for a
     ChebyKAN layer), or None for an all-ChebyKAN stack.  ``affine``: per
     layer, (scale, shift) of the input map t = scale * x + shift, or None for
-    tanh (the Hermite layer's finite domain)."""
+    tanh (the Hermite layer's finite domain).  ``pack_each_step``: re-pack the
+    coefficients at every step even where the step's dC launch keeps the
+    packed operands current (two-layer cross-entropy stacks of small layers);
+    the same results, for checking that path."""
 
     def __init__(self, widths: Sequence[int], degrees: Sequence[int], batch: int,
                  compute: str = "bf16", loss: str = "mse", optimizer: str = "sgd",
                  lr: float = 0.01, betas=(0.9, 0.999), eps: float = 1e-8,
                  weight_decay: float = 0.0, use_graph: bool = False, fused_small: bool = True,
                  device="cuda", bases: Optional[Sequence] = None,
-                 affine: Optional[Sequence] = None):
+                 affine: Optional[Sequence] = None, pack_each_step: bool = False):
         self.device = torch.device(device)
         if self.device.type != "cuda":
             raise RuntimeError("ResidentExecutor runs only on a ROCm device")
@@ -116,7 +119,8 @@ class ResidentExecutor:
             len(self.degrees), self._w, self._d, self.batch, compute_code(compute),
             _LOSS[loss], _OPT[optimizer], 1 if use_graph else 0, float(lr), float(betas[0]),
             float(betas[1]), float(eps), float(weight_decay),
-            0 if fused_small else _lib.CKAN_EXEC_NO_FUSED_SMALL)
+            (0 if fused_small else _lib.CKAN_EXEC_NO_FUSED_SMALL)
+            | (_lib.CKAN_EXEC_PACK_EACH_STEP if pack_each_step else 0))
         n = len(self.degrees)
         specs = aff = None
         if bases is not None:

@@ -400,6 +400,104 @@ def test_fit_equals_the_step_loop(widths, degrees, B, loss, opt):
         ex.close()
 
 
+# (the pair needs layer 2's inputs in whole forward super-groups: 16 at
+# padded degree 4, 8 at 8, 32 at 2; classes may leave an 8-output group short)
+SELF_PACK_CASES = [
+    ([784, 64, 10], [4, 4], 256, "sgd", 0.0),     # config 2
+    ([48, 48, 7], [3, 4], 77, "adam", 0.01),      # ragged input block, degree 3 < P, Adam + decay
+    ([64, 32, 5], [8, 6], 128, "sgd", 0.02),      # padded degree 8
+    ([40, 32, 3], [2, 1], 100, "sgd", 0.0),       # padded degree 2; rows padded (x mapped by launch_tanh)
+]
+
+
+@pytest.mark.parametrize("widths,degrees,B,opt,wd", SELF_PACK_CASES)
+def test_self_packed_steps_equal_the_per_step_pack(widths, degrees, B, opt, wd):
+    """Two-layer cross-entropy stacks of small layers keep their packed
+    operands current from the step's dC launch (no pack launch in the step);
+    the losses and coefficients must equal, bit for bit, those of the same
+    executor packing at every step, eager and graph-replayed, and follow the
+    oracle's loop."""
+    from kan_amd import ResidentExecutor, _lib
+    print(f"self-packed steps {widths} {degrees} B={B} {opt}", flush=True)
+    g = torch.Generator().manual_seed(31)
+    x = (torch.rand(B, widths[0], generator=g) * 4 - 2).cuda()
+    lab = torch.randint(0, widths[-1], (B,), generator=g).cuda()
+    coeffs = _make(widths, degrees, 32)
+    lr = 0.01 if opt == "adam" else 0.05
+    steps = 5
+    runs = {}
+    for each, ug in ((True, False), (False, False), (False, True)):
+        ex = ResidentExecutor(widths, degrees, B, compute="fp32", loss="ce", optimizer=opt, lr=lr,
+                              weight_decay=wd, use_graph=ug, pack_each_step=each)
+        for l, c in enumerate(coeffs):
+            ex.set_coeffs(l, c)
+        if not ug:
+            torch.cuda.synchronize()
+            _lib.profile_report()
+            _lib.profile_enable(True)
+        losses = [ex.step(x, lab).item() for _ in range(steps)]
+        if not ug:
+            torch.cuda.synchronize()
+            _lib.profile_enable(False)
+            names = set(_lib.profile_report())
+            if each:
+                assert "pack2" in names, names
+            else:
+                assert "dc_pack" in names and not any(n.startswith("pack") for n in names), names
+        runs[(each, ug)] = (losses, [ex.get_coeffs(l).cpu() for l in range(2)])
+        ex.close()
+    ref = runs[(True, False)]
+    for key in ((False, False), (False, True)):
+        assert runs[key][0] == ref[0], (key, runs[key][0], ref[0])
+        for a, b in zip(runs[key][1], ref[1]):
+            assert torch.equal(a, b), key
+    c_ref, l_ref = orc.train_steps(x.cpu(), lab.cpu(), coeffs, steps=steps, loss="ce", optimizer=opt,
+                                   lr=lr, weight_decay=wd)
+    for a, b in zip(ref[0], l_ref):
+        assert abs(a - b) <= 1e-5 * abs(b) + 1e-6
+    for l in range(2):
+        d_got = ref[1][l].double() - coeffs[l].double()
+        d_want = c_ref[l].double() - coeffs[l].double()
+        assert _rel(d_got, d_want) <= 1e-4
+
+
+def test_self_packed_operands_follow_coefficient_writes():
+    """With the per-step pack gone, set_coeffs and the executor's forward must
+    leave the packed operands matching C: steps after set_coeffs (and after a
+    forward call) equal those of a fresh executor given the same coefficients
+    (SGD has no other state)."""
+    from kan_amd import ResidentExecutor
+    widths, degrees, B = [784, 64, 10], [4, 4], 256
+    print("self-packed executor: set_coeffs and forward between steps", flush=True)
+    g = torch.Generator().manual_seed(33)
+    x = (torch.rand(B, 784, generator=g) * 2 - 1).cuda()
+    lab = torch.randint(0, 10, (B,), generator=g).cuda()
+    c0, c1 = _make(widths, degrees, 34), _make(widths, degrees, 35)
+
+    def make():
+        return ResidentExecutor(widths, degrees, B, compute="fp32", loss="ce", optimizer="sgd",
+                                lr=0.05)
+    ex = make()
+    for l, c in enumerate(c0):
+        ex.set_coeffs(l, c)
+    for _ in range(2):
+        ex.step(x, lab)
+    for l, c in enumerate(c1):
+        ex.set_coeffs(l, c)
+    la = [ex.step(x, lab).item()]
+    ex.forward(x)
+    la.append(ex.step(x, lab).item())
+    fresh = make()
+    for l, c in enumerate(c1):
+        fresh.set_coeffs(l, c)
+    lb = [fresh.step(x, lab).item() for _ in range(2)]
+    assert la == lb, (la, lb)
+    for l in range(2):
+        assert torch.equal(ex.get_coeffs(l), fresh.get_coeffs(l))
+    ex.close()
+    fresh.close()
+
+
 def test_hidden_layers_store_tanh_into_the_next_cache():
     """At large batches a hidden layer's forward writes tanh(y) straight into
     the next layer's tanh cache (no y, no separate tanh pass).  The training
