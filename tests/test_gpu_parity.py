@@ -113,6 +113,45 @@ def test_fp32_config3_scaled_parity():
 
 
 @pytest.mark.parametrize("compute,tol", [("fp32", FP32_TOL), ("bf16", BF16_TOL)])
+def test_config3_full_size_unrounded_parity(compute, tol):
+    """Full config 3 (B=8192, 1024->1024, deg 8) on fp32 coefficients that are
+    not bf16 values, every row: y, dx and dC against the oracle.  For bf16
+    the oracle takes C rounded to bf16, so the pack's own fp32 -> bf16
+    rounding is what is pinned at this size (the oracle's full step takes
+    about half a second on 16 host cores)."""
+    print(f"cfg3 full-size unrounded parity {compute}", flush=True)
+    x, c, dy = _inputs(8192, 1024, 1024, 8, seed=41, x_scale=1.5)
+    assert not torch.equal(c, c.bfloat16().float())
+    y, dx, dc = _gpu_fwd_bwd(x, c, dy, compute)
+    c_ref = c.bfloat16().float() if compute == "bf16" else c
+    y_ref, dx_ref, dc_ref = orc.layer_forward_backward(x, c_ref, dy)
+    assert _rel(y, y_ref) <= tol
+    assert _rel(dx, dx_ref) <= tol
+    assert _rel(dc, dc_ref) <= tol
+    if compute == "bf16":
+        # the forward operand (the first region of the packed buffer: 32
+        # column fragments x 512 k-blocks x 512 bf16 at this shape) holds
+        # C[i, o, d >= 1] rounded to bf16: the same bytes whether the pack
+        # rounds C itself or C arrives rounded by torch (round to nearest even)
+        import ctypes
+        from kan_amd import _lib
+        lib = _lib.load()
+        d = _lib.make_desc(8192, 1024, 1024, 8, _lib.CKAN_COMPUTE_BF16, _lib.CKAN_DTYPE_F32)
+        s = _lib.stream_ptr(torch.device("cuda"))
+        nb = lib.ckan_packed_bytes(ctypes.byref(d))
+        cf_bytes = 32 * 512 * 512 * 2
+        packs = []
+        for cc in (c, c_ref):
+            pk = torch.zeros(nb, dtype=torch.uint8, device="cuda")
+            cd = cc.cuda()
+            _lib.check(lib.ckan_pack_coeffs(ctypes.byref(d), cd.data_ptr(), pk.data_ptr(), s))
+            packs.append(pk)
+        torch.cuda.synchronize()
+        assert torch.equal(packs[0][:cf_bytes], packs[1][:cf_bytes])
+        assert not torch.equal(packs[0][cf_bytes:], packs[1][cf_bytes:])  # dX operand and fp32 bias differ
+
+
+@pytest.mark.parametrize("compute,tol", [("fp32", FP32_TOL), ("bf16", BF16_TOL)])
 def test_config3_full_size_properties(compute, tol):
     """Full config 3 (B=8192, 1024->1024, deg 8): row-local parity on sampled
     rows, and the size-independent identity <dC, C> = <dy, y>."""
