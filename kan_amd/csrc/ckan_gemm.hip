@@ -982,9 +982,10 @@ struct FwdCols {
   // multiple of 64 bytes apart, 16 lanes on one bank group).
   static constexpr int RP = R >= 4 ? R + 1 : R;
   static constexpr int SLOTS = 4 * U * RP;
-  // Above 4 rows the tanh values come from the tanh cache (written by
-  // launch_tanh): tanh per vector made the kernel vector-ALU-bound.
-  static constexpr bool TPRE = R > 4;
+  // Above kColsTanhRows rows the tanh values come from the tanh cache
+  // (written by launch_tanh): tanh per vector makes the kernel
+  // vector-ALU-bound at 16 rows.
+  static constexpr bool TPRE = R > kColsTanhRows;
 };
 
 __device__ __forceinline__ void mma16(f32x4_t& acc, const bf16x8_t& a, const bf16x8_t& b) {

@@ -34,7 +34,7 @@ inline size_t packed_bytes(const Plan& p) {
 // Tile shapes (waves along M x waves along N, fragments per wave M x N):
 enum FwdTile {
   kFwdBig = 0, kFwdSmall32 = 1, kFwdSmall64 = 2, kFwdStream32 = 3, kFwdStream64 = 4,
-  kFwdCols = 5,   // B <= 16, bf16: column-owning blocks, one launch (tanh in the kernel up to 4 rows)
+  kFwdCols = 5,   // B <= 16, bf16: column-owning blocks, one launch (tanh in the kernel up to 8 rows)
   kFwdSmall64N2 = 6  // 64 rows x 2 output fragments, 2 x 2 waves (outputs <= 64: no idle wave column)
 };
 struct FwdChoice {
@@ -45,13 +45,16 @@ struct FwdChoice {
 };
 FwdChoice choose_fwd(const Plan& p);
 inline bool fwd_streaming(const FwdChoice& c) { return c.tile == kFwdStream32 || c.tile == kFwdStream64; }
-// The 32-row streaming forward and the column-owning forward up to 4 rows
-// compute tanh themselves (each value is needed by every column block, cheap
-// at few rows); every other path reads the tanh cache written by launch_tanh
-// first (the column-owning forward at 5..16 rows is vector-ALU-bound
-// otherwise).
+// The 32-row streaming forward and the column-owning forward up to
+// kColsTanhRows rows compute tanh themselves (each value is needed by every
+// column block, cheap at few rows); every other path reads the tanh cache
+// written by launch_tanh first.  At the config-5 shape (2048 -> 2048, degree
+// 8) the column-owning forward at 8 rows takes 15.6 us cold with its own tanh
+// against 17.0 us with the cache and its launch; at 16 rows 19.4 against 17.9
+// (the tanh per basis vector makes it vector-ALU-bound there).
+constexpr int kColsTanhRows = 8;
 inline bool fwd_reads_tcache(const FwdChoice& c) {
-  return c.tile != kFwdStream32 && !(c.tile == kFwdCols && c.bm <= 4);
+  return c.tile != kFwdStream32 && !(c.tile == kFwdCols && c.bm <= kColsTanhRows);
 }
 // split-K partials [splits][B32][O32] fp32, summed in order by k_fwd_reduce
 inline size_t fwd_ws_bytes(const Plan& p, const FwdChoice& c) {

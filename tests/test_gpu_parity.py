@@ -209,17 +209,18 @@ def test_config5_small_batch_bf16_coeffs(B):
     (4, 130, 2048, 16),    # degree 16 (vectors take degree halves), 4 rows
     (3, 8, 2048, 8),       # one super-group: the rest of the batch is masked
     (4, 2048, 4096, 8),
-    (5, 300, 2048, 4),     # 5..16 rows: the column-owning forward reading the tanh cache
+    (5, 300, 2048, 4),     # 5..8 rows: the column-owning forward still computes tanh itself
     (8, 1000, 2048, 8),
-    (13, 130, 2050, 16),   # ragged rows and columns at degree 16
+    (7, 130, 2048, 16),    # degree 16 at 8 padded rows
+    (13, 130, 2050, 16),   # 9..16 rows (reading the tanh cache): ragged rows and columns at degree 16
     (16, 2048, 2048, 8),   # config 5 at batch 16
     (17, 300, 2048, 8),    # past 16 rows: the split-K streaming forward
     (64, 130, 2048, 16),
 ])
 def test_small_batch_wide_forward(B, I, O, deg):
     """Small batches at 2048 or more outputs (bf16), where up to 16 rows take
-    the one-launch column-owning forward (up to 4 computing tanh themselves and
-    writing the tanh cache, 5..16 reading the cache): y against the oracle, and
+    the one-launch column-owning forward (up to 8 computing tanh themselves and
+    writing the tanh cache, 9..16 reading the cache): y against the oracle, and
     dx / dC through the tanh cache, at shapes that exercise ragged edges."""
     print(f"small-batch wide forward B={B} I={I} O={O} deg={deg}", flush=True)
     x, c, dy = _inputs(B, I, O, deg, seed=7 * B + I + deg)
