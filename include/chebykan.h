@@ -60,7 +60,7 @@ typedef enum ckan_input_map {
 /* Problem descriptor: one ChebyKANLayer(in_dim, out_dim, degree) applied to a
  * batch of `batch` rows (kan/layers/chebykan.py:21-22,64).
  * Degrees 0..16 run on the MFMA kernels in the compute precision.  Degrees
- * 17..256 (the reference layer takes any degree, kan/layers/chebykan.py:21-51)
+ * 17..1024 (the reference layer takes any degree, kan/layers/chebykan.py:21-51)
  * run on vector-ALU kernels in fp32 whatever `compute` asks, with either input
  * map; their packed buffer is C widened to fp32 in its own [in, out, D]
  * layout followed by the basis recurrence block, and they need no workspace
@@ -69,7 +69,7 @@ typedef struct ckan_desc {
   int64_t batch;        /* B: rows of x after x.view(-1, in_dim)          */
   int32_t in_dim;       /* I                                               */
   int32_t out_dim;      /* O                                               */
-  int32_t degree;       /* deg (0..256); D = deg + 1 coefficients per (i, o) */
+  int32_t degree;       /* deg (0..1024); D = deg + 1 coefficients per (i, o) */
   int32_t compute;      /* ckan_compute                                    */
   int32_t coeff_dtype;  /* ckan_dtype of C passed to ckan_pack_coeffs      */
   int32_t input_map;    /* ckan_input_map (0: tanh)                        */
@@ -215,7 +215,7 @@ typedef enum ckan_basis_family {
 
 typedef struct ckan_basis_spec {
   int32_t family;   /* ckan_basis_family                                      */
-  int32_t degree;   /* 0..256 (0..16 for ckan_basis_to_chebyshev and the
+  int32_t degree;   /* 0..1024 (0..16 for ckan_basis_to_chebyshev and the
                        derivative entry points); equal to desc->degree where a
                        desc is passed too */
   double alpha;     /* Jacobi parameters (> -1); ignored by the other families */
@@ -235,7 +235,7 @@ int ckan_pack_coeffs_basis(const ckan_desc* desc, const ckan_basis_spec* spec, c
  * dcoeffs (+)= dcheb (ckan_backward's output is already in the family basis). */
 int ckan_coeff_grad_from_chebyshev(const ckan_desc* desc, const ckan_basis_spec* spec,
                                    const float* dcheb, float* dcoeffs, int accumulate, void* stream);
-/* out[q, n] = P_n(t[q]), n = 0..degree (<= 256), by the family's recurrence
+/* out[q, n] = P_n(t[q]), n = 0..degree (<= 1024), by the family's recurrence
  * (the reference's basis_functions of an already-normalised input; s unused). */
 int ckan_family_basis(const ckan_basis_spec* spec, const float* t, int64_t n, float* out,
                       void* stream);

@@ -738,9 +738,9 @@ int derivative_xform(const ckan_basis_spec* spec, int degree, int order, bool tr
                      BasisXform* r, int* dout, double* Rout = nullptr, double affine_a = 0.0) {
   if (degree < 0) return fail(CKAN_ERR_INVALID_ARG, "degree must be >= 0");
   if (order < 0) return fail(CKAN_ERR_INVALID_ARG, "derivative order must be >= 0");
-  if (degree + order > kValuMaxDegree)
+  if (degree + order > kDerivMaxDegree)
     return fail(CKAN_ERR_UNSUPPORTED, "degree %d + derivative order %d exceeds %d", degree, order,
-                kValuMaxDegree);
+                kDerivMaxDegree);
   // the operator in kernel arguments (and every family basis) stops at
   // degree + order = kMaxD - 1; longer Chebyshev series go row by row
   if (degree + order >= kMaxD && (spec || r))

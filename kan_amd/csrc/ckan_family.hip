@@ -421,7 +421,8 @@ void launch_coeff_xform(const float* in, float* out, int64_t rows, int din, int 
 // T_{|k-2|}) / 4:  r_j = q_j / 2 - (q_{j-2} + q_{j+2}) / 4, less q_1 / 4 at
 // j = 1 and q_0 / 4 at j = 2.  The adjoint applies the transposed steps in
 // reverse order (the coefficient gradient).
-constexpr int kDerivRows = 32;  // rows per block, one lane each
+constexpr int kDerivRows = 32;  // rows per block at most, one lane each
+constexpr size_t kDerivLds = 48 * 1024;  // a block's LDS at most (high degrees take fewer rows)
 
 // degree deg (r[0..deg]) -> degree deg + 1 (r[0..deg + 1]); r[deg + 1] is 0 on entry
 __device__ void cheb_dx_inplace(float* r, int deg) {
@@ -478,12 +479,12 @@ __device__ void cheb_dx_adjoint_inplace(float* r, int deg) {
 template <bool ADJ>
 __global__ void __launch_bounds__(64)
 k_cheb_deriv_rows(const float* __restrict__ in, float* __restrict__ out, int64_t rows, int din,
-                  int dout, int deg0, int order, int pitch, int tO) {
+                  int dout, int deg0, int order, int pitch, int tO, int rpb) {
   extern __shared__ float sm[];
   const int tid = threadIdx.x;
-  const int64_t q0 = (int64_t)blockIdx.x * kDerivRows;
-  const int nr = (int)(rows - q0 < kDerivRows ? rows - q0 : kDerivRows);
-  for (int idx = tid; idx < kDerivRows * pitch; idx += 64) sm[idx] = 0.0f;
+  const int64_t q0 = (int64_t)blockIdx.x * rpb;
+  const int nr = (int)(rows - q0 < rpb ? rows - q0 : rpb);
+  for (int idx = tid; idx < rpb * pitch; idx += 64) sm[idx] = 0.0f;
   __syncthreads();
   for (int idx = tid; idx < nr * din; idx += 64) {  // the block's rows are contiguous
     const int r = idx / din, k = idx - r * din;
@@ -517,15 +518,18 @@ k_cheb_deriv_rows(const float* __restrict__ in, float* __restrict__ out, int64_t
 void launch_cheb_deriv_rows(const float* in, float* out, int64_t rows, int degree, int order,
                             bool adjoint, int transposed_o, hipStream_t s) {
   const int D = degree + 1, DO = D + order;
-  const int pitch = DO | 1;  // odd: the 32 row lanes hit distinct banks
-  const size_t lds = (size_t)kDerivRows * pitch * sizeof(float);
-  const dim3 g((unsigned)((rows + kDerivRows - 1) / kDerivRows));
+  const int pitch = DO | 1;  // odd: the row lanes hit distinct banks
+  int rpb = (int)(kDerivLds / ((size_t)pitch * sizeof(float)));
+  if (rpb > kDerivRows) rpb = kDerivRows;
+  if (rpb < 1) rpb = 1;
+  const size_t lds = (size_t)rpb * pitch * sizeof(float);
+  const dim3 g((unsigned)((rows + rpb - 1) / rpb));
   if (adjoint)
     hipLaunchKernelGGL(k_cheb_deriv_rows<true>, g, dim3(64), lds, s, in, out, rows, DO, D, degree,
-                       order, pitch, transposed_o);
+                       order, pitch, transposed_o, rpb);
   else
     hipLaunchKernelGGL(k_cheb_deriv_rows<false>, g, dim3(64), lds, s, in, out, rows, D, DO, degree,
-                       order, pitch, transposed_o);
+                       order, pitch, transposed_o, rpb);
 }
 
 // jac[b, o, i] for any number of terms: the recurrence runs along k for each o.

@@ -136,7 +136,10 @@ void launch_jacobian(const float* x, const float* c1t, float* jac, int64_t B, in
 // buffer's; fp64: written by launch_write_recur_f64); nullptr (and kind 0)
 // selects the Chebyshev kernels' specialised recurrence.
 constexpr int kMfmaMaxDegree = 16;   // the packed MFMA kernels' limit
-constexpr int kValuMaxDegree = 256;  // the vector-ALU path's limit
+constexpr int kValuMaxDegree = 1024;  // the vector-ALU path's limit
+// Input derivatives: degree + order at most this (the series' coefficients
+// grow like n^(2 order), past fp32's useful range well before 1024).
+constexpr int kDerivMaxDegree = 256;
 template <typename T>
 void launch_forward_valu(const T* x, const T* C, T* y, T* t, int64_t B, int I, int O, int deg,
                          hipStream_t s, const T* rec = nullptr, int imap = 0, float ima = 0.0f,

@@ -26,8 +26,7 @@
 
 namespace ckan {
 
-constexpr int kValuDM = 17;                               // degrees per chunk above degree 16
-constexpr int kRecFloats = 3 * (kValuMaxDegree + 1) + 2;  // a, b, c, scale, kind
+constexpr int kValuDM = 17;  // degrees per chunk above degree 16
 
 template <typename T> __device__ __forceinline__ T vtanh(T x);
 template <> __device__ __forceinline__ float vtanh<float>(float x) { return tanhf(x); }
@@ -74,8 +73,9 @@ __device__ __forceinline__ void rec_step(T w, const T* rs, int D, int n, T& pm, 
   pc = nx;
 }
 
-// The recurrence block: an fp32 block is copied into LDS before the block's
-// first barrier; an fp64 block (the fp64 family layers) is read where it is,
+// The recurrence block: an fp32 block is copied into the kernel's dynamic
+// LDS (rec_lds_bytes, sized by the layer's degree) before the block's first
+// barrier; an fp64 block (the fp64 family layers) is read where it is,
 // by wave-uniform loads, which keeps the fp64 kernels' LDS (and occupancy) as
 // it is.  rec_src gives the copy to read; after the barrier, rec_generic
 // tells whether the block asks for the generic recurrence (a uniform branch
@@ -86,6 +86,11 @@ __device__ __forceinline__ void stage_rec(float* rs, const T* __restrict__ rec, 
     if (rec)
       for (int k = threadIdx.x; k < 3 * D + 2; k += blockDim.x) rs[k] = rec[k];
   }
+}
+// Dynamic LDS of a vector-ALU kernel: the fp32 recurrence block a, b, c
+// (D each), scale, kind, when there is one.
+template <typename T> static size_t rec_lds_bytes(const T* rec, int D) {
+  return sizeof(T) == 4 && rec ? (size_t)recur_floats(D - 1) * sizeof(float) : 0;
 }
 template <typename T>
 __device__ __forceinline__ const T* rec_src(const float* lds, const T* rec) {
@@ -220,7 +225,7 @@ k_fwd_v(const T* __restrict__ t, const T* __restrict__ C, T* __restrict__ y, int
         int O, int D, const T* __restrict__ rec) {
   __shared__ T ts[16 * VTile<T, DM>::WF][kValuKI + 1];
   __shared__ T cs[kValuKI][DM][64];
-  __shared__ float rs_l[sizeof(T) == 4 ? kRecFloats : 1];
+  extern __shared__ float rs_l[];  // the fp32 recurrence block (rec_lds_bytes)
   stage_rec<T>(rs_l, rec, D);
   const T* rs = rec_src<T>(rs_l, rec);
   __syncthreads();
@@ -371,7 +376,7 @@ k_dx_v(const T* __restrict__ t, const T* __restrict__ C, const T* __restrict__ d
   const int d0 = SEEK ? d0_arg : 0;
   __shared__ T ys[BR][OC + 1];
   __shared__ T cs[8 * CST];
-  __shared__ float rs_l[sizeof(T) == 4 ? kRecFloats : 1];
+  extern __shared__ float rs_l[];  // the fp32 recurrence block (rec_lds_bytes)
   stage_rec<T>(rs_l, rec, D);
   const T* rs = rec_src<T>(rs_l, rec);
   if (dn == DM)
@@ -492,7 +497,7 @@ k_dc_v(const T* __restrict__ t, const T* __restrict__ dy, T* __restrict__ dC, in
   __shared__ T ts[32][9];
   __shared__ T sst[SEEK ? 3 * 32 * 9 : 1];  // seek states, read only with SEEK
   __shared__ T ys[32][32 * VTile<T, DM>::WC + 1];
-  __shared__ float rs_l[sizeof(T) == 4 ? kRecFloats : 1];
+  extern __shared__ float rs_l[];  // the fp32 recurrence block (rec_lds_bytes)
   stage_rec<T>(rs_l, rec, D);
   const T* rs = rec_src<T>(rs_l, rec);
   __syncthreads();
@@ -539,11 +544,13 @@ static void fwd_launch(const T* t, const T* C, T* y, int64_t B, int I, int O, in
   const dim3 g((unsigned)((B + BR - 1) / BR), (unsigned)((O + 63) / 64));
   if constexpr (DM == kValuDM) {  // the only chunk size with more degrees than one chunk
     if (D > DM) {
-      hipLaunchKernelGGL((k_fwd_v<T, DM, true>), g, dim3(256), 0, s, t, C, y, B, I, O, D, rec);
+      hipLaunchKernelGGL((k_fwd_v<T, DM, true>), g, dim3(256), rec_lds_bytes(rec, D), s, t, C, y,
+                         B, I, O, D, rec);
       return;
     }
   }
-  hipLaunchKernelGGL((k_fwd_v<T, DM, false>), g, dim3(256), 0, s, t, C, y, B, I, O, D, rec);
+  hipLaunchKernelGGL((k_fwd_v<T, DM, false>), g, dim3(256), rec_lds_bytes(rec, D), s, t, C, y, B,
+                     I, O, D, rec);
 }
 
 template <typename T, int DM>
@@ -555,11 +562,11 @@ static void bwd_chunks(const T* t, const T* C, const T* dy, T* dx, T* dC, DcOut 
       constexpr int BR = 32 * VTile<T, DM>::WX;
       const dim3 g((unsigned)((B + BR - 1) / BR), (unsigned)((I + 7) / 8));
       if (d0 == 0)
-        hipLaunchKernelGGL((k_dx_v<T, DM, false>), g, dim3(256), 0, s, t, C, dy, dx, B, I,
-                           O, D, d0, dn, 0, rec, imap, ima);
+        hipLaunchKernelGGL((k_dx_v<T, DM, false>), g, dim3(256), rec_lds_bytes(rec, D), s, t, C,
+                           dy, dx, B, I, O, D, d0, dn, 0, rec, imap, ima);
       else
-        hipLaunchKernelGGL((k_dx_v<T, DM, true>), g, dim3(256), 0, s, t, C, dy, dx, B, I,
-                           O, D, d0, dn, 1, rec, imap, ima);
+        hipLaunchKernelGGL((k_dx_v<T, DM, true>), g, dim3(256), rec_lds_bytes(rec, D), s, t, C,
+                           dy, dx, B, I, O, D, d0, dn, 1, rec, imap, ima);
     }
   }
   if (dC) {  // one launch: the chunks of the degree axis side by side (grid z)
@@ -567,11 +574,11 @@ static void bwd_chunks(const T* t, const T* C, const T* dy, T* dx, T* dC, DcOut 
     const int nch = (D + DM - 1) / DM;
     const dim3 g((unsigned)((I + 7) / 8), (unsigned)((O + BO - 1) / BO), (unsigned)nch);
     if (nch == 1)
-      hipLaunchKernelGGL((k_dc_v<T, DM, false>), g, dim3(256), 0, s, t, dy, dC, B, I, O, D, 0,
-                         D, om, rec);
+      hipLaunchKernelGGL((k_dc_v<T, DM, false>), g, dim3(256), rec_lds_bytes(rec, D), s, t, dy,
+                         dC, B, I, O, D, 0, D, om, rec);
     else
-      hipLaunchKernelGGL((k_dc_v<T, DM, true>), g, dim3(256), 0, s, t, dy, dC, B, I, O, D, 0,
-                         DM, om, rec);
+      hipLaunchKernelGGL((k_dc_v<T, DM, true>), g, dim3(256), rec_lds_bytes(rec, D), s, t, dy,
+                         dC, B, I, O, D, 0, DM, om, rec);
   }
 }
 

@@ -303,7 +303,7 @@ def _recurrence_f64(spec, device: torch.device) -> torch.Tensor:
         lib = _lib.load()
         nbytes = lib.ckan_recurrence_bytes_f64(spec)
         if nbytes == 0:
-            raise RuntimeError(f"kan_amd: basis degree {spec.degree} is outside the fp64 path's 0..256")
+            raise RuntimeError(f"kan_amd: basis degree {spec.degree} is outside the fp64 path's 0..1024")
         rec = torch.empty(nbytes // 8, dtype=torch.float64, device=device)
         _lib.check(lib.ckan_write_recurrence_f64(spec, rec.data_ptr(), _lib.stream_ptr(device)))
         with _rec64_lock:

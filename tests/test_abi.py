@@ -43,7 +43,7 @@ def _desc(B=8, I=4, O=3, deg=8, compute=0, cdt=0):
     ("in_dim", 0, _lib.CKAN_ERR_INVALID_ARG),
     ("out_dim", 0, _lib.CKAN_ERR_INVALID_ARG),
     ("degree", -1, _lib.CKAN_ERR_INVALID_ARG),
-    ("degree", 257, _lib.CKAN_ERR_UNSUPPORTED),
+    ("degree", 1025, _lib.CKAN_ERR_UNSUPPORTED),
     ("compute", 7, _lib.CKAN_ERR_INVALID_ARG),
     ("coeff_dtype", 5, _lib.CKAN_ERR_INVALID_ARG),
     ("input_map", 1, _lib.CKAN_ERR_INVALID_ARG),   # affine with in_scale 0
@@ -60,7 +60,7 @@ def test_descriptor_validation(field, value, code):
 
 
 def test_high_degree_sizes_and_limits():
-    """Degrees 17..256 run on the vector-ALU kernels: the packed buffer is C
+    """Degrees 17..1024 run on the vector-ALU kernels: the packed buffer is C
     as fp32 [I, O, D] followed, at the next 256-byte boundary, by the basis
     recurrence block (3 D + 2 floats); the input-map cache has row pitch I; no
     workspace."""
@@ -69,7 +69,7 @@ def test_high_degree_sizes_and_limits():
     def al(n):
         return -(-n // 256) * 256
 
-    for deg, B, I, O in [(17, 8, 4, 3), (40, 33, 70, 5), (256, 1, 2, 2)]:
+    for deg, B, I, O in [(17, 8, 4, 3), (40, 33, 70, 5), (256, 1, 2, 2), (1024, 1, 2, 2)]:
         for compute, cdt in [(0, 0), (1, 1)]:
             d = _lib.make_desc(B, I, O, deg, compute, cdt)
             D = deg + 1
@@ -84,7 +84,7 @@ def test_high_degree_sizes_and_limits():
     # the affine input map (finite-domain Hermite) is served at every degree
     for deg in (16, 17, 256):
         assert lib.ckan_packed_bytes(_lib.make_desc(8, 4, 3, deg, 0, 0, (0.5, 0.1))) > 0
-    assert lib.ckan_packed_bytes(_lib.make_desc(8, 4, 3, 257, 0, 0)) == 0
+    assert lib.ckan_packed_bytes(_lib.make_desc(8, 4, 3, 1025, 0, 0)) == 0
 
 
 def test_high_degree_family_spec_checked_before_launch():
@@ -106,8 +106,8 @@ def test_high_degree_family_spec_checked_before_launch():
             _lib.CKAN_ERR_INVALID_ARG
         assert lib.ckan_coeff_grad_from_chebyshev(d, bad, 256, 512, 0, None) == \
             _lib.CKAN_ERR_INVALID_ARG
-    # the materialised family basis: degree up to 256, validated first
-    big = _lib.make_spec(_lib.CKAN_BASIS_HERMITE, 257, 0.0, 0.0, 3.0)
+    # the materialised family basis: degree up to 1024, validated first
+    big = _lib.make_spec(_lib.CKAN_BASIS_HERMITE, 1025, 0.0, 0.0, 3.0)
     assert lib.ckan_family_basis(big, 256, 4, 256, None) == _lib.CKAN_ERR_UNSUPPORTED
     assert lib.ckan_family_basis(ok, None, 4, 256, None) == _lib.CKAN_ERR_INVALID_ARG
     assert b"NULL" in lib.ckan_last_error()
@@ -270,7 +270,7 @@ def test_f64_basis_entry_points_validate_before_launch():
     lib = _lib.load()
     spec = _lib.make_spec(_lib.CKAN_BASIS_HERMITE, 8, 0.0, 0.0, 3.0)
     assert lib.ckan_recurrence_bytes_f64(spec) == (3 * 9 + 2) * 8
-    assert lib.ckan_recurrence_bytes_f64(_lib.make_spec(_lib.CKAN_BASIS_HERMITE, 257, 0, 0, 3.0)) == 0
+    assert lib.ckan_recurrence_bytes_f64(_lib.make_spec(_lib.CKAN_BASIS_HERMITE, 1025, 0, 0, 3.0)) == 0
     assert lib.ckan_write_recurrence_f64(spec, None, None) == _lib.CKAN_ERR_INVALID_ARG
     assert lib.ckan_write_recurrence_f64(spec, 12, None) == _lib.CKAN_ERR_INVALID_ARG  # misaligned
     bad = _lib.make_spec(_lib.CKAN_BASIS_JACOBI, 8, -1.5, 0.0, 1.0)

@@ -3,13 +3,15 @@ any degree: kan/layers/chebykan.py:21-51, kan/basis/chebyshev.py:78-101).
 
 Those layers run on the vector-ALU kernels in fp32, the degree axis in
 chunks of 17 (the cases below cover one chunk and a remainder of 1, whole
-chunks, several chunks with a short last one, and degree 256).  The oracle runs in fp64 here: the fp32 acos/cos of the reference's
+chunks, several chunks with a short last one, degree 256, and up to 1024, the largest served).  The oracle runs in fp64 here: the fp32 acos/cos of the reference's
 default path itself drifts by about d * 6e-8 at degree d, so the fp64 form is
 the honest yardstick.
 
 Tolerances (norm-wise, ||a - b|| / ||b||):
   fp32:  1e-5 for y, dx and dC (an fp32 recurrence against the exact fp64
-         value stays below 6e-6 up to degree 256 on these inputs)
+         value stays below 6e-6 up to degree 256 on these inputs); above
+         256, 1.2e-7 per degree (the recurrence's rounding grows linearly
+         with the degree: 1.2e-4 at 1024)
   fp64:  1e-11
 A bf16 compute request runs the same fp32 kernels (asserted bit-identical);
 bf16 coefficients are widened to fp32 and compared against the oracle on the
@@ -59,7 +61,9 @@ def _gpu(x, c, dy, compute="fp32"):
     (70, 9, 13, 35),      # three chunks, the last of 2 degrees
     (33, 5, 7, 64),
     (300, 70, 130, 20),   # several output and input tiles, ragged
-    (16, 4, 3, 256),      # the largest degree served
+    (16, 4, 3, 256),
+    (24, 5, 4, 600),      # 36 chunks, the last of 6 degrees
+    (16, 3, 3, 1024),     # the largest degree served (12 KiB recurrence block in LDS)
     (1, 3, 2, 40),
 ])
 def test_high_degree_fp32_parity(B, I, O, deg):
@@ -67,9 +71,10 @@ def test_high_degree_fp32_parity(B, I, O, deg):
     x, c, dy = _inputs(B, I, O, deg, seed=B + 7 * deg)
     y, dx, dc = _gpu(x, c, dy)
     y_ref, dx_ref, dc_ref = orc.layer_forward_backward(x.double(), c.double(), dy.double())
-    assert _rel(y, y_ref) <= FP32_TOL
-    assert _rel(dx, dx_ref) <= FP32_TOL
-    assert _rel(dc, dc_ref) <= FP32_TOL
+    tol = max(FP32_TOL, 1.2e-7 * deg)
+    assert _rel(y, y_ref) <= tol
+    assert _rel(dx, dx_ref) <= tol
+    assert _rel(dc, dc_ref) <= tol
 
 
 def test_high_degree_bf16_request_runs_fp32():
@@ -92,7 +97,7 @@ def test_high_degree_bf16_coefficients():
     assert _rel(dc.float(), dc_ref) <= 1e-2  # dC is returned in the coefficients' dtype (bf16)
 
 
-@pytest.mark.parametrize("B,I,O,deg", [(90, 20, 30, 40), (17, 5, 6, 17), (40, 8, 9, 100)])
+@pytest.mark.parametrize("B,I,O,deg", [(90, 20, 30, 40), (17, 5, 6, 17), (40, 8, 9, 100), (9, 3, 4, 1024)])
 def test_high_degree_fp64_parity(B, I, O, deg):
     print(f"high degree fp64 B={B} I={I} O={O} deg={deg}", flush=True)
     x, c, dy = _inputs(B, I, O, deg, seed=3 * B + deg, dtype=torch.float64)
@@ -197,6 +202,7 @@ FAMILY_CASES = [
     ("jacobi", 1.5, 0.5, 129, 16, 50, 40),   # three chunks
     ("jacobi", -0.5, 0.25, 64, 8, 8, 17),    # a chunk of 17 and one of 1
     ("jacobi", 0.5, 0.5, 16, 4, 3, 100),
+    ("jacobi", 0.5, 0.5, 12, 3, 4, 500),     # the recurrence block of 501 degrees in LDS
     ("hermite", 0, 0, 70, 9, 13, 20),
     ("hermite", 0, 0, 40, 6, 5, 32),
     ("hermite_e", 0, 0, 150, 24, 40, 30),
@@ -229,9 +235,10 @@ def test_high_degree_family_parity(family, alpha, beta, B, I, O, deg):
     y, dx, dc = _family_gpu(x, c, dy, _family_spec(family, deg, alpha, beta))
     y_ref, dx_ref, dc_ref = fo.family_forward_backward(x.double(), c.double(), dy.double(),
                                                        family, alpha, beta)
-    assert _rel(y, y_ref) <= FP32_TOL
-    assert _rel(dx, dx_ref) <= FP32_TOL
-    assert _rel(dc, dc_ref) <= FP32_TOL
+    tol = max(FP32_TOL, 1.2e-7 * deg)
+    assert _rel(y, y_ref) <= tol
+    assert _rel(dx, dx_ref) <= tol
+    assert _rel(dc, dc_ref) <= tol
 
 
 def test_high_degree_family_bf16_request_runs_fp32():
