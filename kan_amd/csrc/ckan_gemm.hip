@@ -786,11 +786,11 @@ k_fwd_reduce(const float* __restrict__ part, int S, const float* __restrict__ bi
 // sum (the bits of k_fwd_reduce with out_tanh: tanh(y_a) into layer b's
 // tanh cache tb, pitch a.O = b's inputs), then the last layer b on the vector
 // ALU from its fp32 coefficients Cb [Ib, Ob, Db] (lane i takes input i: its
-// T_d(t_i) by the three-term recurrence, times Cb[i, k, d]; the 64 lanes are
-// added by an xor butterfly, which leaves the same bits in every lane), then
-// the row's softmax cross-entropy as k_ce_small computes it: yb, dyb =
-// (softmax - onehot) / B and the row's loss into loss_part[r], whose mean
-// k_sum_scalar takes in k_ce_small's order.  Ib <= 64, Ob <= kTailO; the
+// T_d(t_i) by the three-term recurrence, times Cb[i, k, d]; the lanes'
+// partials are summed per class through LDS), then the row's softmax
+// cross-entropy: yb, dyb = (softmax - onehot) / B and the row's loss into
+// loss_part[r], whose mean is taken in k_sum_scalar's order by the caller's
+// next launch.  Ib <= 64, Ob <= kTailO; the
 // block stages Cb in LDS (Ib Ob Db <= kTailC floats), its coalesced loads
 // issued ahead of the split sums so that both latencies overlap.
 // With dxa, lane i also writes layer b's dX for the row, dL/dy_a[r, i] =
@@ -840,6 +840,7 @@ k_fwd_tail_ce(const float* __restrict__ part, int S, const float* __restrict__ b
               float* __restrict__ yb, const int64_t* __restrict__ labels, float* __restrict__ dyb,
               float* __restrict__ loss_part, float* __restrict__ dxa, int Pb) {
   extern __shared__ float csh[];  // Cb [Ib][Ob][Db]
+  __shared__ float red[kTailRows][64 * (kTailO + 1)];  // each wave's [input][class] partials
   const int tid = threadIdx.x, lane = tid & 63;
   const int64_t r = (int64_t)blockIdx.x * kTailRows + (tid >> 6);
   const bool active = r < pa.B;
@@ -900,37 +901,43 @@ k_fwd_tail_ce(const float* __restrict__ part, int S, const float* __restrict__ b
       }
     }
   }
+  // the sums over the 64 inputs: the lanes' class partials go through the
+  // wave's LDS area (odd pitch: writes and reads hit 64 distinct banks), lane
+  // (k, q) = (lane % 16, lane / 16) adds inputs 16q .. 16q + 15 of class k in
+  // order, and two exchanges add the quarters, so lanes k, k + 16, k + 32 and
+  // k + 48 hold y_k (a 64-lane butterfly per class was 96 dependent exchanges)
+  float* rw = red[tid >> 6];
 #pragma unroll
-  for (int w = 32; w >= 1; w >>= 1)
+  for (int k = 0; k < kTailO; ++k) rw[lane * (kTailO + 1) + k] = acc[k];
+  wait_lgkmcnt<0>();  // the wave reads other lanes' writes of its own area
+  __builtin_amdgcn_wave_barrier();
+  const int kc = lane & 15, qq = lane >> 4;
+  float yk = 0.0f;
 #pragma unroll
-    for (int k = 0; k < kTailO; ++k) acc[k] += __shfl_xor(acc[k], w);
-  // the cross-entropy of row r (every lane holds the same y)
-  float m = -INFINITY;
+  for (int u = 0; u < 16; ++u) yk += rw[(qq * 16 + u) * (kTailO + 1) + kc];
+  yk += __shfl_xor(yk, 16);
+  yk += __shfl_xor(yk, 32);
+  // the cross-entropy of row r: max and sum of the exponentials over the
+  // classes by butterflies within each 16-lane row (every row the same)
+  const bool valid = kc < Ob;
+  float m = valid ? yk : -INFINITY;
 #pragma unroll
-  for (int k = 0; k < kTailO; ++k)
-    if (k < Ob) m = fmaxf(m, acc[k]);
-  float e[kTailO];
+  for (int w = 8; w >= 1; w >>= 1) m = fmaxf(m, __shfl_xor(m, w));
+  const float ek = valid ? expf(yk - m) : 0.0f;
+  float sm = ek;
 #pragma unroll
-  for (int k = 0; k < kTailO; ++k) e[k] = k < Ob ? expf(acc[k] - m) : 0.0f;
-#pragma unroll
-  for (int w = kTailO / 2; w > 0; w >>= 1)
-#pragma unroll
-    for (int k = 0; k < w; ++k) e[k] = e[k] + e[k + w];
-  const float sm = e[0];
+  for (int w = 8; w >= 1; w >>= 1) sm += __shfl_xor(sm, w);
   const int64_t lab = labels[r];
   const float inv_b = 1.0f / (float)pa.B;
-  float yl = 0.0f, mine = 0.0f;
-#pragma unroll
-  for (int k = 0; k < kTailO; ++k) {
-    if (k == lab) yl = acc[k];
-    if (k == lane) mine = acc[k];
-  }
-  const float dmine = (expf(mine - m) / sm - (lane == lab ? 1.0f : 0.0f)) * inv_b;
+  const bool lab_ok = lab >= 0 && lab < Ob;
+  const float yl = __shfl(yk, lab_ok ? (int)lab : 0);
+  // lane k < 16: class k's gradient (read by the dX below from lane k)
+  const float dmine = (ek / sm - (kc == lab ? 1.0f : 0.0f)) * inv_b;
   if (lane < Ob) {
-    yb[r * Ob + lane] = mine;
+    yb[r * Ob + lane] = yk;
     dyb[r * Ob + lane] = dmine;
   }
-  if (lane == 0) loss_part[r] = (logf(sm) + m) - ((lab >= 0 && lab < Ob) ? yl : 0.0f);
+  if (lane == 0) loss_part[r] = (logf(sm) + m) - (lab_ok ? yl : 0.0f);
   if (dxa) {
     const float* c = csh + (lane < Ib ? lane : 0) * Ob * Db;
     float dx;
