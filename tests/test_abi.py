@@ -30,6 +30,22 @@ def test_library_exports_every_header_symbol():
     assert set(_lib.SIGNATURES) == set(names)
 
 
+def test_python_constants_match_header_enums():
+    """Every enum constant of include/chebykan.h that the ctypes layer mirrors
+    (same name in kan_amd._lib) has the header's value."""
+    txt = open(os.path.join(ROOT, "include", "chebykan.h")).read()
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+    consts = {}
+    for body in re.findall(r"typedef enum \w+ \{(.*?)\}", txt, flags=re.S):
+        for name, value in re.findall(r"\b(CKAN_[A-Z0-9_]+)\s*=\s*(\d+)", body):
+            consts[name] = int(value)
+    assert {"CKAN_EXEC_NO_FUSED_SMALL", "CKAN_EXEC_PACK_EACH_STEP", "CKAN_LOSS_CE"} <= set(consts)
+    mirrored = [n for n in consts if hasattr(_lib, n)]
+    assert len(mirrored) >= 10
+    for n in mirrored:
+        assert getattr(_lib, n) == consts[n], n
+
+
 def test_version_string():
     assert b"gfx950" in _lib.load().ckan_version()
 
