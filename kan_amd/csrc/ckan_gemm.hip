@@ -289,11 +289,13 @@ __device__ __forceinline__ void xcd_patch(int& bx, int& by) {
   }
 }
 
-template <int P, bool BF>
+// BNF_: output fragments (32 columns each) per block; 2 for layers of at most
+// 64 outputs, whose 4-fragment tile would run half its MFMAs on padding.
+template <int P, bool BF, int BNF_ = 4>
 struct FwdPipe {
   typedef typename Elem<BF>::type E;
   typedef FwdGroup<P> G;
-  static constexpr int NM = 2, NN = 4, BM = 256, BNF = 4, THREADS = 512;
+  static constexpr int NM = 2, NN = BNF_, BM = 256, BNF = BNF_, THREADS = 512;
   static constexpr int B_BYTES = BNF * G::SGK * kFragElems * (int)sizeof(E);
   static constexpr int T_BYTES = BM * G::SGI * 4;
   static constexpr int STAGE_BYTES = B_BYTES + T_BYTES;
@@ -329,13 +331,13 @@ template <int CR> __device__ __forceinline__ int fwd_t_xor(int r) {
 // adds them, so the two give the same bits), and the first row tile also
 // writes the sums to bias_out.  OT (unsplit launches only): store tanh(y)
 // in place of y, for the next layer of a stack.
-template <int P, bool BF, bool OT>
+template <int P, bool BF, bool OT, int BNF_ = 4>
 __global__ void __launch_bounds__(512)
 k_fwd_pipe(const float* __restrict__ tc, const typename Elem<BF>::type* __restrict__ Cf,
            const float* __restrict__ bias_f, float* __restrict__ y, float* __restrict__ part,
            Plan p, int sg_per_split, const float* __restrict__ bias_part, int nib,
            float* __restrict__ bias_out) {
-  typedef FwdPipe<P, BF> K;
+  typedef FwdPipe<P, BF, BNF_> K;
   typedef typename K::E E;
   typedef typename K::G G;
   constexpr int NM = K::NM, NN = K::NN, BM = K::BM, BNF = K::BNF, NPB = K::NPB;
@@ -518,10 +520,12 @@ k_fwd_pipe(const float* __restrict__ tc, const typename Elem<BF>::type* __restri
   // all 8 waves.
   constexpr int NH = NN / 2;
   // bias from the partials: thread t sums partials k = t % 4, t % 4 + 4, ... of
-  // output nb0 * 32 + t / 4 (loads issued here, ahead of the LDS hand-over)
+  // output nb0 * 32 + t / 4 (loads issued here, ahead of the LDS hand-over);
+  // the block's outputs are the first BNF * 32 of them
   float bsum = 0.0f;
   const int bo = nb0 * 32 + (tid >> 2);
-  if (nib > 0 && bo < p.O32)
+  const bool bown = (tid >> 2) < BNF * 32 && bo < p.O32;
+  if (nib > 0 && bown)
     for (int k = tid & 3; k < nib; k += 4) bsum += bias_part[(size_t)k * p.O32 + bo];
   wait_lgkmcnt<0>();
   block_barrier();
@@ -531,9 +535,9 @@ k_fwd_pipe(const float* __restrict__ tc, const typename Elem<BF>::type* __restri
     const float s0 = __shfl(bsum, q0), s1 = __shfl(bsum, q0 + 1);
     const float s2 = __shfl(bsum, q0 + 2), s3 = __shfl(bsum, q0 + 3);
     const float tot = ((s0 + s1) + s2) + s3;
-    if ((tid & 3) == 0) {
+    if ((tid & 3) == 0 && (tid >> 2) < BNF * 32) {
       bias_l[tid >> 2] = tot;
-      if (bias_out && bx == 0 && blockIdx.z == 0 && bo < p.O32) bias_out[bo] = tot;
+      if (bias_out && bx == 0 && blockIdx.z == 0 && bown) bias_out[bo] = tot;
     }
   }
   float* red = reinterpret_cast<float*>(smem);
@@ -2788,7 +2792,8 @@ FwdChoice choose_fwd(const Plan& p) {
       c.tile = kFwdSmall64; c.bm = 64; c.bnf = 4;
     }
   } else {
-    c.tile = kFwdBig; c.bm = 256; c.bnf = 4;
+    // at most 64 outputs: a 64-column tile (the pipelined kernel's BNF = 2)
+    c.tile = kFwdBig; c.bm = 256; c.bnf = p.NBf <= 2 ? 2 : 4;
   }
   c.tiles_m = (int)ceil_div(p.B, c.bm);
   c.tiles_n = (int)ceil_div(p.NBf, c.bnf);
@@ -2881,27 +2886,31 @@ static void fwd_dispatch(const float* x, float* t, const void* packed, float* y,
         break;
       default:
         if constexpr (FwdPipe<P, BF>::kOk) {
-          typedef FwdPipe<P, BF> K;
           if (!fwd_pipe_offsets_fit(p)) {  // per-lane copy offsets are 32-bit
             hipLaunchKernelGGL((k_fwd<P, BF, 2, 4, 4, 1>), grid, dim3(256), 0, s, t, Cf, bias, y,
                                part, p, c.sg_per_split, bpart, nib_k, bias_out, nullptr);
             break;
           }
-          const size_t lds = (size_t)K::LDS_BYTES;
-          static std::atomic<uint32_t> lds_set{0};
-          if (out_tanh) {
-            static std::atomic<uint32_t> lds_set_ot{0};
-            ensure_lds_limit(reinterpret_cast<const void*>(&k_fwd_pipe<P, BF, true>), (int)lds,
-                             lds_set_ot);
-            hipLaunchKernelGGL((k_fwd_pipe<P, BF, true>), grid, dim3(K::THREADS), lds, s, t, Cf,
-                               bias, y, part, p, c.sg_per_split, bpart, nib_k,
-                               nib_k > 0 ? bias_out : nullptr);
+          // one LDS-limit flag per instantiation
+          auto launch = [&](auto OTc, auto BNFc, std::atomic<uint32_t>& flag) {
+            constexpr bool OTv = decltype(OTc)::value;
+            constexpr int BNFv = decltype(BNFc)::value;
+            typedef FwdPipe<P, BF, BNFv> KV;
+            const void* fn = reinterpret_cast<const void*>(&k_fwd_pipe<P, BF, OTv, BNFv>);
+            ensure_lds_limit(fn, KV::LDS_BYTES, flag);
+            hipLaunchKernelGGL((k_fwd_pipe<P, BF, OTv, BNFv>), grid, dim3(KV::THREADS),
+                               (size_t)KV::LDS_BYTES, s, t, Cf, bias, y, part, p, c.sg_per_split,
+                               bpart, nib_k, nib_k > 0 ? bias_out : nullptr);
+          };
+          typedef std::integral_constant<bool, true> OT1;
+          typedef std::integral_constant<bool, false> OT0;
+          static std::atomic<uint32_t> lds_set[4];
+          if (c.bnf == 2) {
+            if (out_tanh) launch(OT1{}, std::integral_constant<int, 2>{}, lds_set[0]);
+            else launch(OT0{}, std::integral_constant<int, 2>{}, lds_set[1]);
           } else {
-            ensure_lds_limit(reinterpret_cast<const void*>(&k_fwd_pipe<P, BF, false>), (int)lds,
-                             lds_set);
-            hipLaunchKernelGGL((k_fwd_pipe<P, BF, false>), grid, dim3(K::THREADS), lds, s, t, Cf,
-                               bias, y, part, p, c.sg_per_split, bpart, nib_k,
-                               nib_k > 0 ? bias_out : nullptr);
+            if (out_tanh) launch(OT1{}, std::integral_constant<int, 4>{}, lds_set[2]);
+            else launch(OT0{}, std::integral_constant<int, 4>{}, lds_set[3]);
           }
         } else {
           hipLaunchKernelGGL((k_fwd<P, BF, 2, 4, 4, 1>), grid, dim3(256), 0, s, t, Cf, bias, y,

@@ -158,6 +158,43 @@ def test_paired_pack_with_bias_reduce_matches_oracle(compute, tol):
     ex.close()
 
 
+@pytest.mark.parametrize("compute,tol", [("fp32", 1e-5), ("bf16", 2e-2)])
+def test_narrow_layer_stores_tanh_for_the_next(compute, tol):
+    """A 128 -> 64 layer at 65536 rows runs the pipelined forward unsplit on its
+    64-column tile and stores tanh(y) straight into the next layer's cache:
+    two steps against the oracle's loop (the coefficient update after the
+    first step, where one gradient is the whole change, and both losses).  The
+    fp32 run is checked against the oracle evaluated in fp64: at 65536 rows
+    the fp32 oracle's own rounding of the gradient sums is near 1e-5."""
+    from kan_amd import ResidentExecutor
+    print(f"executor narrow middle layer, 64-column tile {compute}", flush=True)
+    widths, degrees, B, lr = [128, 64, 24], [8, 16], 65536, 0.05
+    g = torch.Generator().manual_seed(12)
+    x = torch.rand(B, widths[0], generator=g) * 4 - 2
+    y = torch.randn(B, widths[-1], generator=g)
+    coeffs = _make(widths, degrees, 43)
+    if compute == "bf16":
+        coeffs = [c.bfloat16().float() for c in coeffs]
+    ex = ResidentExecutor(widths, degrees, B, compute=compute, loss="mse", optimizer="sgd", lr=lr)
+    for l, c in enumerate(coeffs):
+        ex.set_coeffs(l, c)
+    xd, yd = x.cuda(), y.cuda()
+    bf = compute == "bf16"
+    # the oracle's precision: fp32 on bf16-rounded coefficients, or fp64
+    xo, yo, co = (x, y, coeffs) if bf else (x.double(), y.double(), [c.double() for c in coeffs])
+    losses = [ex.step(xd, yd).item()]
+    c_ref, _ = orc.train_steps(xo, yo, co, steps=1, loss="mse", optimizer="sgd", lr=lr,
+                               bf16_coeffs=bf)
+    for l in range(2):
+        assert _rel(ex.get_coeffs(l).cpu() - coeffs[l], c_ref[l] - co[l]) <= tol, l
+    losses.append(ex.step(xd, yd).item())
+    _, losses_ref = orc.train_steps(xo, yo, co, steps=2, loss="mse", optimizer="sgd", lr=lr,
+                                    bf16_coeffs=bf)
+    for k in range(2):
+        assert abs(losses[k] - losses_ref[k]) <= tol * abs(losses_ref[k]), (k, losses[k], losses_ref[k])
+    ex.close()
+
+
 @pytest.mark.parametrize("widths,degrees,B,compute", [
     ([96, 64, 10], [4, 4], 128, "fp32"),    # dC written in place by the pipelined kernel
     ([96, 64, 10], [4, 4], 512, "fp32"),    # split dC: the split-sum kernel applies the step

@@ -75,6 +75,9 @@ SHAPES = [
     (2100, 1000, 136, 7),  # bf16 dx with copy waves: 288 tiles over 256 persistent blocks
                            # (two tiles for some), ragged rows / inputs / outputs, 6 stages
     (2600, 900, 130, 4),   # the same at degree 4: 319 tiles, 4 stages per tile
+    (1500, 200, 40, 8),    # pipelined forward, 64-column tile (<= 64 outputs): ragged second fragment
+    (1024, 96, 20, 3),     # the same with one output fragment, degree 3
+    (3000, 130, 64, 12),   # the same at degree 16 (P = 16), ragged rows and inputs
 ]
 
 
