@@ -379,6 +379,9 @@ def _suite(only=SUITE, cpu=True):
                             lambda: kan_amd.HermiteKANLayer(I, O, DEG, compute="bf16"))):
             torch.manual_seed(6)
             layer = make().to(dev)
+            # untimed steps first, as for the headline: the figure is the steady
+            # state, not the clock ramp after the previous entry's idle gaps
+            _settle(layer, xf, dyf, 0.5)
             ms = _time_gpu(layer, xf, dyf, 30, 10)
             kern = _kernel_breakdown(layer, xf, dyf, 10)
             fam[name] = {"ms_per_step": ms, "samples_per_s": B / (ms * 1e-3),

@@ -293,8 +293,20 @@ k_coeff_from_cheb(const float* dcheb, float* dc, int64_t rows, int D, DcOut om, 
   const float* src = dcheb + r0 * D;
   float* dst = dc + r0 * D;
   if (v4) {
-    for (int k = tid; k < n / 4; k += 256)
-      reinterpret_cast<f32x4_t*>(tile)[k] = reinterpret_cast<const f32x4_t*>(src)[k];
+    // every load of the thread in flight before the first LDS store
+    constexpr int U = (256 * DM / 4 + 255) / 256;
+    f32x4_t v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int k = tid + u * 256;
+      v[u] = k < n / 4 ? __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(src) + k)
+                       : f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int k = tid + u * 256;
+      if (k < n / 4) reinterpret_cast<f32x4_t*>(tile)[k] = v[u];
+    }
   } else {
     for (int k = tid; k < n; k += 256) tile[k] = src[k];
   }
