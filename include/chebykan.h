@@ -190,7 +190,8 @@ int ckan_backward_f64_basis(const ckan_desc* desc, const double* rec, const doub
  *   P_n(s u) = sum_k M[n, k] T_k(u)      (M lower triangular, exact),
  * and its coefficient gradient is dC = dC' M^T; the input gradient is the
  * ChebyKAN layer's with C'.  So ckan_pack_coeffs_basis + ckan_forward +
- * ckan_backward (into dC') + ckan_coeff_grad_from_chebyshev run such a layer.
+ * ckan_backward (into dC') + ckan_coeff_grad_from_chebyshev run such a layer
+ * (ckan_backward_basis: the last two in one call).
  * Above degree 16 (the vector-ALU kernels) the packed buffer carries the
  * family's recurrence instead of C M: the kernels evaluate P_n(s u) by the
  * recurrence and differentiate it, ckan_backward's dC is already the family
@@ -235,6 +236,17 @@ int ckan_pack_coeffs_basis(const ckan_desc* desc, const ckan_basis_spec* spec, c
  * dcoeffs (+)= dcheb (ckan_backward's output is already in the family basis). */
 int ckan_coeff_grad_from_chebyshev(const ckan_desc* desc, const ckan_basis_spec* spec,
                                    const float* dcheb, float* dcoeffs, int accumulate, void* stream);
+/* ckan_backward (accumulate = 0) followed by ckan_coeff_grad_from_chebyshev
+ * in place, in one call: dcoeffs receives the family coefficients' gradient
+ * (stored), dx the input gradient, the workspace as for ckan_backward.  Where
+ * one pipelined dC launch writes the whole gradient, it applies M^T to each
+ * row before its stores (no second pass over dC); otherwise the map runs as
+ * its own launch.  The results are the same bits either way.
+ * Replaces: torch autograd through kan/basis/jacobi.py:95-116 and
+ * kan/basis/hermite.py:118-139 (the einsum's backward in the family basis). */
+int ckan_backward_basis(const ckan_desc* desc, const ckan_basis_spec* spec, const float* t_cache,
+                        const void* packed, const float* dy, float* dx, float* dcoeffs, void* ws,
+                        size_t ws_bytes, void* stream);
 /* out[q, n] = P_n(t[q]), n = 0..degree (<= 1024), by the family's recurrence
  * (the reference's basis_functions of an already-normalised input; s unused). */
 int ckan_family_basis(const ckan_basis_spec* spec, const float* t, int64_t n, float* out,

@@ -109,6 +109,7 @@ SIGNATURES = {
     "ckan_basis_to_chebyshev": (ctypes.c_int, [_pspec, ctypes.POINTER(_f64)]),
     "ckan_pack_coeffs_basis": (ctypes.c_int, [_pdesc, _pspec, _vp, _vp, _vp]),
     "ckan_coeff_grad_from_chebyshev": (ctypes.c_int, [_pdesc, _pspec, _vp, _vp, ctypes.c_int, _vp]),
+    "ckan_backward_basis": (ctypes.c_int, [_pdesc, _pspec, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "ckan_family_basis": (ctypes.c_int, [_pspec, _vp, _i64, _vp, _vp]),
     "ckan_family_basis_backward": (ctypes.c_int, [_pspec, _vp, _vp, _i64, _vp, _vp]),
     "ckan_derivative_matrix": (ctypes.c_int, [_pspec, _i32, _i32, ctypes.POINTER(_f64)]),

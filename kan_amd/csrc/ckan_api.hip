@@ -184,7 +184,8 @@ void ckan::set_last_error(const char* msg) { g_err = msg; }
 namespace {
 int backward_core(const ckan_desc* desc, const float* t_cache, const void* packed, const float* dy,
                   float* dx, float* dcoeffs, DcOut om, void* ws, size_t ws_bytes, void* stream,
-                  const LossMean* lm, bool* lm_used);
+                  const LossMean* lm, bool* lm_used, const BasisXform* xf = nullptr,
+                  bool* xf_done = nullptr);
 }
 
 int ckan::backward_impl(const ckan_desc* desc, const float* t_cache, const void* packed,
@@ -201,7 +202,7 @@ int ckan::backward_impl(const ckan_desc* desc, const float* t_cache, const void*
 namespace {
 int backward_core(const ckan_desc* desc, const float* t_cache, const void* packed, const float* dy,
                   float* dx, float* dcoeffs, DcOut om, void* ws, size_t ws_bytes, void* stream,
-                  const LossMean* lm, bool* lm_used) {
+                  const LossMean* lm, bool* lm_used, const BasisXform* xf, bool* xf_done) {
   int rc = validate_desc(desc);
   if (rc) return rc;
   const bool need_dx = dx != nullptr, need_dc = dcoeffs != nullptr;
@@ -284,7 +285,10 @@ int backward_core(const ckan_desc* desc, const float* t_cache, const void* packe
     }
     {
       ProfScope ps("dc_gemm", s);
-      launch_dc_gemm(dYc, t_cache, L.dc_pipe ? colsum : colsum_r, part, dcoeffs, om, p, L, s);
+      const bool map = xf && dc_gemm_maps_basis(p, L);
+      launch_dc_gemm(dYc, t_cache, L.dc_pipe ? colsum : colsum_r, part, dcoeffs, om, p, L, s,
+                     map ? xf : nullptr);
+      if (map && xf_done) *xf_done = true;
     }
     if ((rc = check_launch("dc_gemm"))) return rc;
     if (!L.dc_pipe) {
@@ -728,6 +732,30 @@ int ckan_coeff_grad_from_chebyshev(const ckan_desc* desc, const ckan_basis_spec*
   ProfScope ps("coeff_from_cheb", s);
   launch_coeff_from_cheb(dcheb, dcoeffs, p, DcOut{accumulate ? kDcAccumulate : kDcStore}, xf, s);
   return check_launch("coeff_grad_from_chebyshev");
+}
+
+int ckan_backward_basis(const ckan_desc* desc, const ckan_basis_spec* spec, const float* t_cache,
+                        const void* packed, const float* dy, float* dx, float* dcoeffs, void* ws,
+                        size_t ws_bytes, void* stream) {
+  int rc = validate_desc(desc);
+  if (rc) return rc;
+  const DcOut om{kDcStore};
+  if (valu_route(desc)) {
+    // the vector-ALU backward differentiates in the family's basis already
+    if ((rc = family_valid(spec, desc->degree))) return rc;
+    return backward_impl(desc, t_cache, packed, dy, dx, dcoeffs, om, ws, ws_bytes, stream);
+  }
+  BasisXform xf;
+  if ((rc = family_xform(spec, desc->degree, &xf))) return rc;
+  bool used = false, mapped = false;
+  if ((rc = backward_core(desc, t_cache, packed, dy, dx, dcoeffs, om, ws, ws_bytes, stream, nullptr,
+                          &used, &xf, &mapped)))
+    return rc;
+  if (!dcoeffs || mapped || desc->batch == 0) return CKAN_OK;  // an empty batch's dC is zero
+  const Plan p = plan_of(desc);
+  ProfScope ps("coeff_from_cheb", reinterpret_cast<hipStream_t>(stream));
+  launch_coeff_from_cheb(dcoeffs, dcoeffs, p, om, xf, reinterpret_cast<hipStream_t>(stream));
+  return check_launch("backward_basis: coefficient map");
 }
 
 namespace {

@@ -2371,11 +2371,16 @@ struct DcPipe {
   static constexpr bool kOk = LDS_BYTES <= 160 * 1024 && T_CHUNKS <= 512 && NF % 2 == 0;
 };
 
-template <int P, bool BF, int H_>
+// The change of basis a dC launch applies before its stores (XF = true):
+// g[n] = sum_{k <= n} g'[k] m[n][k] per (input, output) row of D values.
+template <bool XF> struct DcXf { BasisXform x; };
+template <> struct DcXf<false> {};
+
+template <int P, bool BF, int H_, bool XF = false>
 __global__ void __launch_bounds__(512)
 k_dc_pipe(const typename Elem<BF>::type* __restrict__ dYc, const float* __restrict__ tc,
           const float* __restrict__ colsum_part, float* __restrict__ out, Plan p, int st_per_split,
-          DcOut om) {
+          DcOut om, DcXf<XF> xf) {
   typedef DcPipe<P, BF, H_> K;
   typedef typename K::E E;
   constexpr int PH = K::PH, DQ = K::DQ, OG = K::OG, NN = K::NN, NO = K::NO, NF = K::NF;
@@ -2699,6 +2704,25 @@ k_dc_pipe(const typename Elem<BF>::type* __restrict__ dYc, const float* __restri
     }
     wait_lgkmcnt<0>();
     block_barrier();
+    if constexpr (XF) {
+      // the staged rows in the family's basis, in the arithmetic of
+      // k_coeff_from_cheb (the same bits as that separate pass)
+      for (int q = tid; q < 32 * OW; q += 512) {
+        float* r = stg + q * p.D;
+        float gv[P + 1];
+#pragma unroll
+        for (int k = 0; k <= P; ++k) gv[k] = k < p.D ? r[k] : 0.0f;
+#pragma unroll
+        for (int n = 0; n <= P; ++n) {
+          float acc = 0.0f;
+#pragma unroll
+          for (int k = 0; k <= n; ++k) acc = fmaf(gv[k], xf.x.m[n * kMaxD + k], acc);
+          if (n < p.D) r[n] = acc;
+        }
+      }
+      wait_lgkmcnt<0>();
+      block_barrier();
+    }
     if (ovalid > 0) {
       // ivalid runs of ovalid * D contiguous floats (one per input row), as
       // float4 when every run starts 16-byte aligned
@@ -3156,17 +3180,25 @@ BwdLayout bwd_layout(const Plan& p, bool need_dx_arg, bool need_dc_arg) {
 template <int P, bool BF, int H>
 static bool dc_pipe_launch(const void* dYc, const float* t, const float* colsum, float* part,
                            float* dC, DcOut om, const Plan& p, const BwdLayout& L,
-                           hipStream_t s) {
+                           hipStream_t s, const BasisXform* xf) {
   typedef typename Elem<BF>::type E;
   if constexpr (DcPipe<P, BF, H>::kOk) {
     typedef DcPipe<P, BF, H> K;
-    static std::atomic<uint32_t> lds_set{0};
-    ensure_lds_limit(reinterpret_cast<const void*>(&k_dc_pipe<P, BF, H>), K::LDS_BYTES, lds_set);
     const bool split = L.dc_splits > 1;
     dim3 grid(p.NIB, (unsigned)ceil_div(p.NBf, K::NO), L.dc_splits);
+    if (xf && !split) {  // the unsplit launch writes the whole gradient: it maps it
+      static std::atomic<uint32_t> lds_xf{0};
+      ensure_lds_limit(reinterpret_cast<const void*>(&k_dc_pipe<P, BF, H, true>), K::LDS_BYTES, lds_xf);
+      hipLaunchKernelGGL((k_dc_pipe<P, BF, H, true>), grid, dim3(512), K::LDS_BYTES, s,
+                         reinterpret_cast<const E*>(dYc), t, colsum, dC, p, L.dc_st_per_split, om,
+                         DcXf<true>{*xf});
+      return true;
+    }
+    static std::atomic<uint32_t> lds_set{0};
+    ensure_lds_limit(reinterpret_cast<const void*>(&k_dc_pipe<P, BF, H>), K::LDS_BYTES, lds_set);
     hipLaunchKernelGGL((k_dc_pipe<P, BF, H>), grid, dim3(512), K::LDS_BYTES, s,
                        reinterpret_cast<const E*>(dYc), t, colsum, split ? part : dC, p,
-                       L.dc_st_per_split, split ? DcOut{kDcStore} : om);
+                       L.dc_st_per_split, split ? DcOut{kDcStore} : om, DcXf<false>{});
     return true;
   }
   return false;
@@ -3175,14 +3207,14 @@ static bool dc_pipe_launch(const void* dYc, const float* t, const float* colsum,
 template <int P, bool BF>
 static void dc_dispatch(const void* dYc, const float* t, const float* colsum, float* part,
                         float* dC, DcOut om, const Plan& p, const BwdLayout& L,
-                        hipStream_t s) {
+                        hipStream_t s, const BasisXform* xf) {
   typedef typename Elem<BF>::type E;
   if (L.dc_pipe) {
     bool done = false;
     if constexpr (P == 16) {  // dc_h(p) is 1 only for degree 16
-      if (dc_h(p) == 1) done = dc_pipe_launch<P, BF, 1>(dYc, t, colsum, part, dC, om, p, L, s);
+      if (dc_h(p) == 1) done = dc_pipe_launch<P, BF, 1>(dYc, t, colsum, part, dC, om, p, L, s, xf);
     }
-    if (!done) done = dc_pipe_launch<P, BF, 2>(dYc, t, colsum, part, dC, om, p, L, s);
+    if (!done) done = dc_pipe_launch<P, BF, 2>(dYc, t, colsum, part, dC, om, p, L, s, xf);
     if (done) return;
   }
   constexpr int NM = BwdTile<P>::NM;
@@ -3191,10 +3223,25 @@ static void dc_dispatch(const void* dYc, const float* t, const float* colsum, fl
                      reinterpret_cast<const E*>(dYc), t, part, p, L.dc_st_per_split);
 }
 
-void launch_dc_gemm(const void* dYc, const float* t, const float* colsum, float* part, float* dC,
-                    DcOut om, const Plan& p, const BwdLayout& L, hipStream_t s) {
+bool dc_gemm_maps_basis(const Plan& p, const BwdLayout& L) {
+  if (!L.dc_pipe || L.dc_splits > 1) return false;
   const bool bf = p.esz == 2;
-#define CKAN_DC(PP, BB) dc_dispatch<PP, BB>(dYc, t, colsum, part, dC, om, p, L, s)
+  switch (p.P) {
+    case 2: return bf ? DcPipe<2, true, 2>::kOk : DcPipe<2, false, 2>::kOk;
+    case 4: return bf ? DcPipe<4, true, 2>::kOk : DcPipe<4, false, 2>::kOk;
+    case 8: return bf ? DcPipe<8, true, 2>::kOk : DcPipe<8, false, 2>::kOk;
+    default: {  // dc_dispatch's order: H = 1 where dc_h says so and it fits, else H = 2
+      const bool h1 = dc_h(p) == 1 && (bf ? DcPipe<16, true, 1>::kOk : DcPipe<16, false, 1>::kOk);
+      return h1 || (bf ? DcPipe<16, true, 2>::kOk : DcPipe<16, false, 2>::kOk);
+    }
+  }
+}
+
+void launch_dc_gemm(const void* dYc, const float* t, const float* colsum, float* part, float* dC,
+                    DcOut om, const Plan& p, const BwdLayout& L, hipStream_t s,
+                    const BasisXform* xf) {
+  const bool bf = p.esz == 2;
+#define CKAN_DC(PP, BB) dc_dispatch<PP, BB>(dYc, t, colsum, part, dC, om, p, L, s, xf)
   switch (p.P) {
     case 2: bf ? CKAN_DC(2, true) : CKAN_DC(2, false); break;
     case 4: bf ? CKAN_DC(4, true) : CKAN_DC(4, false); break;

@@ -256,8 +256,13 @@ bool dc_pack_ok(const Plan& p);
 void launch_dc_pack(const DcPackArgs& a, const DcPackArgs* b, hipStream_t s,
                     LossMean lm = LossMean{});
 void launch_loss_mean(const LossMean& lm, hipStream_t s);
+// xf: the gradient is wanted in another family's basis; the pipelined dC
+// applies it before its stores where dc_gemm_maps_basis says so (one unsplit
+// launch writes the whole gradient) and ignores it otherwise.
 void launch_dc_gemm(const void* dYc, const float* t, const float* colsum, float* part, float* dC,
-                    DcOut om, const Plan& p, const BwdLayout& L, hipStream_t s);
+                    DcOut om, const Plan& p, const BwdLayout& L, hipStream_t s,
+                    const BasisXform* xf = nullptr);
+bool dc_gemm_maps_basis(const Plan& p, const BwdLayout& L);
 void launch_sgd(float* p, const float* g, int64_t n, float lr, float wd, hipStream_t s);
 // ckan_backward with the dC write mode given by om; with om.mode kDcSgd or
 // kDcAdam, dcoeffs is the parameter and receives its optimizer step (batch

@@ -216,12 +216,14 @@ class ChebyKANFunction(torch.autograd.Function):
         ws_bytes = lib.ckan_bwd_workspace_bytes(desc, int(need_dx), int(need_dc))
         ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
         stream = _lib.stream_ptr(dev)
-        _lib.check(lib.ckan_backward(desc, t.data_ptr(), packed.data_ptr(), dy32.data_ptr(),
-                                     _lib.ptr(dx), _lib.ptr(dc), 0, ws.data_ptr(), ws_bytes,
-                                     stream))
-        if dc is not None and ctx.spec is not None:  # dC = dC' M^T, in place
-            _lib.check(lib.ckan_coeff_grad_from_chebyshev(desc, ctx.spec, dc.data_ptr(),
-                                                          dc.data_ptr(), 0, stream))
+        if ctx.spec is None:
+            _lib.check(lib.ckan_backward(desc, t.data_ptr(), packed.data_ptr(), dy32.data_ptr(),
+                                         _lib.ptr(dx), _lib.ptr(dc), 0, ws.data_ptr(), ws_bytes,
+                                         stream))
+        else:  # dC = dC' M^T, applied by the dC launch where it can
+            _lib.check(lib.ckan_backward_basis(desc, ctx.spec, t.data_ptr(), packed.data_ptr(),
+                                               dy32.data_ptr(), _lib.ptr(dx), _lib.ptr(dc),
+                                               ws.data_ptr(), ws_bytes, stream))
         if dx is not None and ctx.x_dtype != torch.float32:
             dx = dx.to(ctx.x_dtype)
         if dc is not None and ctx.c_dtype != torch.float32:

@@ -122,6 +122,14 @@ def test_high_degree_family_spec_checked_before_launch():
             _lib.CKAN_ERR_INVALID_ARG
         assert lib.ckan_coeff_grad_from_chebyshev(d, bad, 256, 512, 0, None) == \
             _lib.CKAN_ERR_INVALID_ARG
+        assert lib.ckan_backward_basis(d, bad, 256, 256, 256, 256, 512, None, 0, None) == \
+            _lib.CKAN_ERR_INVALID_ARG
+    # the same at a degree the MFMA kernels serve (the map is built first)
+    d8 = _lib.make_desc(8, 4, 3, 8, 0, 0)
+    for bad in (_lib.make_spec(_lib.CKAN_BASIS_JACOBI, 7, 0.5, 1.5, 1.0),
+                _lib.make_spec(_lib.CKAN_BASIS_JACOBI, 8, -1.5, 0.0, 1.0)):
+        assert lib.ckan_backward_basis(d8, bad, 256, 256, 256, 256, 512, None, 0, None) == \
+            _lib.CKAN_ERR_INVALID_ARG
     # the materialised family basis: degree up to 1024, validated first
     big = _lib.make_spec(_lib.CKAN_BASIS_HERMITE, 1025, 0.0, 0.0, 3.0)
     assert lib.ckan_family_basis(big, 256, 4, 256, None) == _lib.CKAN_ERR_UNSUPPORTED

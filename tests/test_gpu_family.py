@@ -174,3 +174,54 @@ def test_hermite_finite_domain_affine_map(scaling, B, I, O, deg, compute, tol):
     # the tanh map would give a different function
     y_tanh = fo.family_forward(x, c_ref, fam)
     assert _rel(y, y_tanh) > 10 * tol
+
+
+@pytest.mark.parametrize("family,compute,B,I,O,deg,fused", [
+    ("jacobi", "bf16", 512, 1024, 1024, 8, True),     # one unsplit pipelined dC launch maps dC
+    ("hermite", "fp32", 256, 2048, 1024, 4, True),     # degree 4: 256 outputs per block
+    ("hermite_e", "bf16", 256, 1024, 1024, 12, True),  # degree 16, one stage group
+    ("jacobi", "bf16", 2048, 256, 128, 8, False),     # split dC: the map is its own launch
+    ("hermite", "fp32", 64, 64, 48, 5, False),        # small dC on the vector ALU
+])
+def test_backward_basis_equals_backward_then_map(family, compute, B, I, O, deg, fused):
+    """ckan_backward_basis gives the bits of ckan_backward followed by the
+    in-place ckan_coeff_grad_from_chebyshev, for dx and dC, and launches no
+    separate map where one dC launch writes the whole gradient."""
+    print(f"backward_basis {family} {compute} B={B} I={I} O={O} deg={deg}", flush=True)
+    lib = _lib.load()
+    spec = _spec(family, deg, 0.5, -0.25)
+    cc = _lib.CKAN_COMPUTE_BF16 if compute == "bf16" else _lib.CKAN_COMPUTE_FP32
+    d = _lib.make_desc(B, I, O, deg, cc, _lib.CKAN_DTYPE_F32)
+    g = torch.Generator().manual_seed(B + I + deg)
+    x = (torch.rand(B, I, generator=g) * 4 - 2).cuda()
+    C = (torch.randn(I, O, deg + 1, generator=g) / (I * (deg + 1))).cuda()
+    dy = torch.randn(B, O, generator=g).cuda()
+    st = _lib.stream_ptr(x.device)
+    packed = torch.empty(lib.ckan_packed_bytes(d), dtype=torch.uint8, device=x.device)
+    t = torch.empty(lib.ckan_tcache_elems(d), device=x.device)
+    y = torch.empty(B, O, device=x.device)
+    fwb = lib.ckan_fwd_workspace_bytes(d)
+    fws = torch.empty(max(fwb, 256), dtype=torch.uint8, device=x.device)
+    _lib.check(lib.ckan_pack_coeffs_basis(d, spec, C.data_ptr(), packed.data_ptr(), st))
+    _lib.check(lib.ckan_forward(d, x.data_ptr(), packed.data_ptr(), y.data_ptr(), t.data_ptr(),
+                                fws.data_ptr(), fwb, st))
+    bwb = lib.ckan_bwd_workspace_bytes(d, 1, 1)
+    ws = torch.empty(max(bwb, 256), dtype=torch.uint8, device=x.device)
+    dx1, dc1 = torch.empty(B, I, device=x.device), torch.empty(I, O, deg + 1, device=x.device)
+    _lib.check(lib.ckan_backward(d, t.data_ptr(), packed.data_ptr(), dy.data_ptr(), dx1.data_ptr(),
+                                 dc1.data_ptr(), 0, ws.data_ptr(), bwb, st))
+    _lib.check(lib.ckan_coeff_grad_from_chebyshev(d, spec, dc1.data_ptr(), dc1.data_ptr(), 0, st))
+    dx2, dc2 = torch.full_like(dx1, float("nan")), torch.full_like(dc1, float("nan"))
+    torch.cuda.synchronize()
+    _lib.profile_enable(True)
+    try:
+        _lib.check(lib.ckan_backward_basis(d, spec, t.data_ptr(), packed.data_ptr(), dy.data_ptr(),
+                                           dx2.data_ptr(), dc2.data_ptr(), ws.data_ptr(), bwb, st))
+        torch.cuda.synchronize()
+        rep = _lib.profile_report()
+    finally:
+        _lib.profile_enable(False)
+    assert ("coeff_from_cheb" not in rep) == fused, rep
+    assert torch.equal(dx1, dx2)
+    assert torch.equal(dc1, dc2)
+    assert dc1.abs().sum() > 0
