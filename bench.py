@@ -388,7 +388,10 @@ def _suite(only=SUITE, cpu=True):
                          "tflops": STEP_FLOP / (ms * 1e-3) / 1e12,
                          # the pack launch also computes tanh(x) where the layout allows
                          "pack_ms": kern.get("pack_tanh", kern.get("pack", {})).get("avg_ms"),
-                         "coeff_from_cheb_ms": kern["coeff_from_cheb"]["avg_ms"]}
+                         # dC' M^T: in the dC launch's epilogue where one launch writes
+                         # the whole gradient (no separate map launch, None here)
+                         "dc_gemm_ms": kern["dc_gemm"]["avg_ms"],
+                         "coeff_from_cheb_ms": kern.get("coeff_from_cheb", {}).get("avg_ms")}
         out["families_cfg3_shape"] = {"workload": "1024->1024 deg 8, B=8192, bf16 MFMA, pack+fwd+bwd",
                                       **fam}
 
