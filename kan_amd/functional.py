@@ -21,8 +21,7 @@ _fwd_ws = {}
 _fwd_ws_lock = threading.Lock()
 
 
-def _forward_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    stream = _lib.stream_ptr(device)
+def _forward_workspace(device: torch.device, nbytes: int, stream: int) -> torch.Tensor:
     key = (device.index, stream)
     with _fwd_ws_lock:
         ws = _fwd_ws.get(key)
@@ -113,23 +112,28 @@ def coeff_code(dtype: torch.dtype) -> int:
     raise RuntimeError(f"kan_amd ChebyKAN supports float32 or bfloat16 coefficients, got {dtype}")
 
 
-# Descriptors by (batch, in, out, degree, compute, coefficient dtype, affine).
+# Descriptors and their tanh-cache and forward-workspace sizes by (batch, in,
+# out, degree, compute, coefficient dtype, affine).
 _descs = {}
 # tanh caches of forwards that keep no graph (nothing reads them afterwards),
 # one per (device, stream), grown as needed: calls sharing one must not overlap.
 _t_scratch = {}
 
 
-def _desc_for(batch, in_dim, out_dim, degree, compute, dtype, affine):
+def _desc_sizes(batch, in_dim, out_dim, degree, compute, dtype, affine):
+    """(desc, tanh-cache elements, forward workspace bytes), cached per shape:
+    the two sizes are host-side functions of the descriptor alone."""
     key = (batch, in_dim, out_dim, degree, compute, dtype, affine)
-    d = _descs.get(key)
-    if d is None:
+    ent = _descs.get(key)
+    if ent is None:
         d = _lib.make_desc(batch, in_dim, out_dim, degree, compute_code(compute), coeff_code(dtype),
                            affine)
+        lib = _lib.load()
+        ent = (d, lib.ckan_tcache_elems(d), lib.ckan_fwd_workspace_bytes(d))
         if len(_descs) > 4096:
             _descs.clear()
-        _descs[key] = d
-    return d
+        _descs[key] = ent
+    return ent
 
 
 def _layer_forward(x, coeffs, compute, spec, affine, keep_t):
@@ -145,10 +149,9 @@ def _layer_forward(x, coeffs, compute, spec, affine, keep_t):
     lib = _lib.load()
     dev = x.device
     x32 = x.contiguous() if x.dtype == torch.float32 else x.float().contiguous()
-    desc = _desc_for(x32.shape[0], in_dim, out_dim, dd - 1, compute, coeffs.dtype,
-                     None if affine is None else tuple(affine))
+    desc, t_elems, ws_bytes = _desc_sizes(x32.shape[0], in_dim, out_dim, dd - 1, compute,
+                                          coeffs.dtype, None if affine is None else tuple(affine))
     stream = _lib.stream_ptr(dev)
-    t_elems = lib.ckan_tcache_elems(desc)
     if keep_t:
         t = torch.empty(t_elems, dtype=torch.float32, device=dev)
     else:
@@ -158,8 +161,7 @@ def _layer_forward(x, coeffs, compute, spec, affine, keep_t):
             t = torch.empty(max(t_elems, 64), dtype=torch.float32, device=dev)
             _t_scratch[tkey] = t
     y = torch.empty(x32.shape[0], out_dim, dtype=torch.float32, device=dev)
-    ws_bytes = lib.ckan_fwd_workspace_bytes(desc)
-    ws = _forward_workspace(dev, ws_bytes) if ws_bytes else None
+    ws = _forward_workspace(dev, ws_bytes, stream) if ws_bytes else None
     key = _pack_key(coeffs, compute, spec, affine)
     packed = _cache_get(coeffs, key)
     if packed is not None:
