@@ -31,6 +31,34 @@ def _forward_workspace(device: torch.device, nbytes: int, stream: int) -> torch.
     return ws
 
 
+# Backward workspaces (the dy re-layouts, column-sum and split-K partials, all
+# written before they are read) and their sizes: likewise one per (device,
+# stream), and the size per (descriptor object, dx wanted, dC wanted).
+_bwd_ws = {}
+_bwd_sizes = {}
+
+
+def _backward_workspace(device: torch.device, desc, need_dx: bool, need_dc: bool,
+                        stream: int):
+    # keyed by the descriptor object's id; the entry holds the object, so the
+    # id cannot be reused while the entry lives
+    skey = (id(desc), need_dx, need_dc)
+    ent = _bwd_sizes.get(skey)
+    if ent is None or ent[0] is not desc:
+        ent = (desc, _lib.load().ckan_bwd_workspace_bytes(desc, int(need_dx), int(need_dc)))
+        if len(_bwd_sizes) > 4096:
+            _bwd_sizes.clear()
+        _bwd_sizes[skey] = ent
+    nbytes = ent[1]
+    key = (device.index, stream)
+    with _fwd_ws_lock:
+        ws = _bwd_ws.get(key)
+        if ws is None or ws.numel() < nbytes:
+            ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+            _bwd_ws[key] = ws
+    return ws, nbytes
+
+
 # Packed-operand cache.  The reference re-lays C out inside the einsum on every
 # call (kan/basis/chebyshev.py:101); here the packed operands depend only on
 # the coefficients' values and the layer's shape, precision and basis, so the
@@ -215,9 +243,8 @@ class ChebyKANFunction(torch.autograd.Function):
         dx = torch.empty(desc.batch, desc.in_dim, dtype=torch.float32, device=dev) if need_dx else None
         dc = (torch.empty(desc.in_dim, desc.out_dim, desc.degree + 1, dtype=torch.float32, device=dev)
               if need_dc else None)
-        ws_bytes = lib.ckan_bwd_workspace_bytes(desc, int(need_dx), int(need_dc))
-        ws = torch.empty(max(ws_bytes, 256), dtype=torch.uint8, device=dev)
         stream = _lib.stream_ptr(dev)
+        ws, ws_bytes = _backward_workspace(dev, desc, need_dx, need_dc, stream)
         if ctx.spec is None:
             _lib.check(lib.ckan_backward(desc, t.data_ptr(), packed.data_ptr(), dy32.data_ptr(),
                                          _lib.ptr(dx), _lib.ptr(dc), 0, ws.data_ptr(), ws_bytes,
