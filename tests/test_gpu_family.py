@@ -43,6 +43,8 @@ CASES = [
     ("hermite", 0, 0, 7, 5, 3, 1),
     ("hermite_e", 0, 0, 200, 72, 50, 12),
     ("hermite_e", 0, 0, 1024, 128, 256, 4),
+    ("jacobi", 0.5, -0.25, 256, 1024, 1024, 8),  # one unsplit dC launch maps dC' M^T itself
+    ("hermite", 0, 0, 128, 2048, 1024, 4),       # the same at degree 4 (256 outputs per block)
 ]
 
 
