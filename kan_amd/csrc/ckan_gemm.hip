@@ -2375,6 +2375,10 @@ struct DcPipe {
 // g[n] = sum_{k <= n} g'[k] m[n][k] per (input, output) row of D values.
 template <bool XF> struct DcXf { BasisXform x; };
 template <> struct DcXf<false> {};
+// LDS for M's rows n <= P, after the pipelined dC's own
+template <int P> constexpr int kDcXfBytes = (P + 1) * kMaxD * (int)sizeof(float);
+template <int P, bool BF, int H>
+constexpr bool dc_xf_fits() { return DcPipe<P, BF, H>::kOk && DcPipe<P, BF, H>::LDS_BYTES + kDcXfBytes<P> <= 160 * 1024; }
 
 template <int P, bool BF, int H_, bool XF = false>
 __global__ void __launch_bounds__(512)
@@ -2390,6 +2394,13 @@ k_dc_pipe(const typename Elem<BF>::type* __restrict__ dYc, const float* __restri
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int half = wave / WG, wq = wave % WG, dh = wq % DQ, og = wq / DQ;
+  if constexpr (XF) {
+    // M (rows n <= P of kMaxD floats) past the kernel's own LDS: read by the
+    // epilogue, after the loop's barriers have published it
+    static_assert((P + 1) * kMaxD <= 512, "one element per thread");
+    if (tid < (P + 1) * kMaxD)
+      reinterpret_cast<float*>(smem + K::LDS_BYTES)[tid] = xf.x.m[tid];
+  }
   const int g = lane >> 5;
   int ib, obk;
   xcd_patch(ib, obk);
@@ -2706,7 +2717,19 @@ k_dc_pipe(const typename Elem<BF>::type* __restrict__ dYc, const float* __restri
     block_barrier();
     if constexpr (XF) {
       // the staged rows in the family's basis, in the arithmetic of
-      // k_coeff_from_cheb (the same bits as that separate pass)
+      // k_coeff_from_cheb (the same bits as that separate pass); M from its
+      // LDS copy
+      const float* xm = reinterpret_cast<const float*>(smem + K::LDS_BYTES);
+      // up to degree 8 the lower triangle of M (45 values) stays in registers
+      // for all of the thread's rows; above, each use reads it from LDS
+      constexpr bool MREG = P <= 8;
+      float mr[MREG ? (P + 1) * (P + 2) / 2 : 1];
+      if constexpr (MREG) {
+#pragma unroll
+        for (int n = 0, i = 0; n <= P; ++n)
+#pragma unroll
+          for (int k = 0; k <= n; ++k, ++i) mr[i] = xm[n * kMaxD + k];
+      }
       for (int q = tid; q < 32 * OW; q += 512) {
         float* r = stg + q * p.D;
         float gv[P + 1];
@@ -2716,7 +2739,8 @@ k_dc_pipe(const typename Elem<BF>::type* __restrict__ dYc, const float* __restri
         for (int n = 0; n <= P; ++n) {
           float acc = 0.0f;
 #pragma unroll
-          for (int k = 0; k <= n; ++k) acc = fmaf(gv[k], xf.x.m[n * kMaxD + k], acc);
+          for (int k = 0; k <= n; ++k)
+            acc = fmaf(gv[k], MREG ? mr[n * (n + 1) / 2 + k] : xm[n * kMaxD + k], acc);
           if (n < p.D) r[n] = acc;
         }
       }
@@ -3186,13 +3210,16 @@ static bool dc_pipe_launch(const void* dYc, const float* t, const float* colsum,
     typedef DcPipe<P, BF, H> K;
     const bool split = L.dc_splits > 1;
     dim3 grid(p.NIB, (unsigned)ceil_div(p.NBf, K::NO), L.dc_splits);
-    if (xf && !split) {  // the unsplit launch writes the whole gradient: it maps it
-      static std::atomic<uint32_t> lds_xf{0};
-      ensure_lds_limit(reinterpret_cast<const void*>(&k_dc_pipe<P, BF, H, true>), K::LDS_BYTES, lds_xf);
-      hipLaunchKernelGGL((k_dc_pipe<P, BF, H, true>), grid, dim3(512), K::LDS_BYTES, s,
-                         reinterpret_cast<const E*>(dYc), t, colsum, dC, p, L.dc_st_per_split, om,
-                         DcXf<true>{*xf});
-      return true;
+    if constexpr (dc_xf_fits<P, BF, H>()) {
+      if (xf && !split) {  // the unsplit launch writes the whole gradient: it maps it
+        static std::atomic<uint32_t> lds_xf{0};
+        const int lds = K::LDS_BYTES + kDcXfBytes<P>;
+        ensure_lds_limit(reinterpret_cast<const void*>(&k_dc_pipe<P, BF, H, true>), lds, lds_xf);
+        hipLaunchKernelGGL((k_dc_pipe<P, BF, H, true>), grid, dim3(512), (size_t)lds, s,
+                           reinterpret_cast<const E*>(dYc), t, colsum, dC, p, L.dc_st_per_split,
+                           om, DcXf<true>{*xf});
+        return true;
+      }
     }
     static std::atomic<uint32_t> lds_set{0};
     ensure_lds_limit(reinterpret_cast<const void*>(&k_dc_pipe<P, BF, H>), K::LDS_BYTES, lds_set);
@@ -3226,13 +3253,15 @@ static void dc_dispatch(const void* dYc, const float* t, const float* colsum, fl
 bool dc_gemm_maps_basis(const Plan& p, const BwdLayout& L) {
   if (!L.dc_pipe || L.dc_splits > 1) return false;
   const bool bf = p.esz == 2;
+  // the instantiation dc_dispatch launches, and whether it has LDS left for M
   switch (p.P) {
-    case 2: return bf ? DcPipe<2, true, 2>::kOk : DcPipe<2, false, 2>::kOk;
-    case 4: return bf ? DcPipe<4, true, 2>::kOk : DcPipe<4, false, 2>::kOk;
-    case 8: return bf ? DcPipe<8, true, 2>::kOk : DcPipe<8, false, 2>::kOk;
-    default: {  // dc_dispatch's order: H = 1 where dc_h says so and it fits, else H = 2
+    case 2: return bf ? dc_xf_fits<2, true, 2>() : dc_xf_fits<2, false, 2>();
+    case 4: return bf ? dc_xf_fits<4, true, 2>() : dc_xf_fits<4, false, 2>();
+    case 8: return bf ? dc_xf_fits<8, true, 2>() : dc_xf_fits<8, false, 2>();
+    default: {  // H = 1 where dc_h says so and that kernel fits, else H = 2
       const bool h1 = dc_h(p) == 1 && (bf ? DcPipe<16, true, 1>::kOk : DcPipe<16, false, 1>::kOk);
-      return h1 || (bf ? DcPipe<16, true, 2>::kOk : DcPipe<16, false, 2>::kOk);
+      if (h1) return bf ? dc_xf_fits<16, true, 1>() : dc_xf_fits<16, false, 1>();
+      return bf ? dc_xf_fits<16, true, 2>() : dc_xf_fits<16, false, 2>();
     }
   }
 }
